@@ -1,0 +1,199 @@
+// Internal runtime shared by the HIP translation units: error reporting,
+// stream-ordered allocation of packed result blocks and scratch, and wave64
+// primitives for gfx950.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+
+#include "cu_roaring_abi.h"
+
+namespace crimpl {
+
+// ---- errors -------------------------------------------------------------
+void set_error(const char* fmt, ...);
+
+#define CR_HIP_RET(expr)                                                                    \
+    do {                                                                                    \
+        hipError_t e__ = (expr);                                                            \
+        if (e__ != hipSuccess) {                                                            \
+            ::crimpl::set_error("%s:%d: %s: %s", __FILE__, __LINE__, #expr, hipGetErrorString(e__)); \
+            return CR_ERR_HIP;                                                              \
+        }                                                                                   \
+    } while (0)
+
+#define CR_RET(expr)                  \
+    do {                              \
+        int rc__ = (expr);            \
+        if (rc__ != CR_OK) return rc__; \
+    } while (0)
+
+#define CR_LAUNCH_CHECK() CR_HIP_RET(hipGetLastError())
+
+inline hipStream_t as_stream(cr_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---- stream-ordered device memory ---------------------------------------
+int dev_alloc(void** p, size_t bytes, hipStream_t s);
+int dev_free(void* p, hipStream_t s);
+
+// Scratch that is released (stream-ordered) when the guard leaves scope.
+struct Scratch {
+    void* ptr = nullptr;
+    hipStream_t stream = nullptr;
+    Scratch() = default;
+    Scratch(const Scratch&) = delete;
+    Scratch& operator=(const Scratch&) = delete;
+    ~Scratch() { release(); }
+    int alloc(size_t bytes, hipStream_t s)
+    {
+        stream = s;
+        return dev_alloc(&ptr, bytes, s);
+    }
+    void release()
+    {
+        if (ptr) dev_free(ptr, stream);
+        ptr = nullptr;
+    }
+    template <class T>
+    T* at(size_t byte_offset) const
+    {
+        return reinterpret_cast<T*>(static_cast<char*>(ptr) + byte_offset);
+    }
+};
+
+// Carves one allocation into 256-byte aligned sections.
+struct Carver {
+    size_t total = 0;
+    size_t add(size_t bytes)
+    {
+        size_t off = total;
+        total += (bytes + 255) & ~size_t(255);
+        return off;
+    }
+};
+
+// Packed output block of a result GpuRoaring (one allocation, _alloc_base set).
+struct OutLayout {
+    size_t keys = 0, types = 0, offsets = 0, cards = 0, kidx = 0, bmp = 0, arr = 0, run = 0;
+    size_t total = 0;
+};
+OutLayout plan_out(uint64_t n_meta, uint64_t kidx_len, uint64_t bmp_words, uint64_t arr_elems, uint64_t run_u16);
+// Allocates the block and points the struct's arrays into it (sections of size
+// 0 leave the pointer null).
+int alloc_out(cr_gpu_roaring* out, const OutLayout& L, uint64_t n_meta, uint64_t kidx_len, uint64_t bmp_words,
+              uint64_t arr_elems, uint64_t run_u16, hipStream_t s);
+
+void reset(cr_gpu_roaring* r);
+int free_async(cr_gpu_roaring* r, hipStream_t s);
+
+// ---- device helpers -------------------------------------------------------
+__device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v)
+{
+    const uint32_t lane = __lane_id();
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        uint32_t t = __shfl_up(v, o, 64);
+        if (lane >= static_cast<uint32_t>(o)) v += t;
+    }
+    return v;
+}
+
+// Block-wide sum; `lds` holds one slot per wave.  All threads get the total.
+template <int NT>
+__device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t* lds)
+{
+    constexpr int NW = NT / 64;
+    v = wave_sum(v);
+    const uint32_t w = threadIdx.x >> 6;
+    if (__lane_id() == 0) lds[w] = v;
+    __syncthreads();
+    uint32_t t = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) t += lds[i];
+    __syncthreads();
+    return t;
+}
+
+// Block-wide exclusive scan of one value; returns the prefix, writes the total.
+template <int NT>
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* lds, uint32_t& total)
+{
+    constexpr int NW = NT / 64;
+    const uint32_t incl = wave_incl_scan(v);
+    const uint32_t w = threadIdx.x >> 6;
+    if (__lane_id() == 63) lds[w] = incl;
+    __syncthreads();
+    uint32_t base = 0, t = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        const uint32_t x = lds[i];
+        base += (static_cast<uint32_t>(i) < w) ? x : 0u;
+        t += x;
+    }
+    __syncthreads();
+    total = t;
+    return base + incl - v;
+}
+
+// Ordered compaction helper: exclusive rank of `flag` among the block's lanes
+// (ballot per wave, wave counts through LDS).  `lds` needs NT/64 slots.
+template <int NT>
+__device__ __forceinline__ uint32_t block_flag_rank(bool flag, uint32_t* lds, uint32_t& total)
+{
+    constexpr int NW = NT / 64;
+    const unsigned long long m = __ballot(flag);
+    const uint32_t lane = __lane_id();
+    const unsigned long long below = lane ? (m & (~0ull >> (64 - lane))) : 0ull;
+    const uint32_t w = threadIdx.x >> 6;
+    if (lane == 0) lds[w] = static_cast<uint32_t>(__popcll(m));
+    __syncthreads();
+    uint32_t base = 0, t = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        const uint32_t x = lds[i];
+        base += (static_cast<uint32_t>(i) < w) ? x : 0u;
+        t += x;
+    }
+    __syncthreads();
+    total = t;
+    return base + static_cast<uint32_t>(__popcll(below));
+}
+
+// lower_bound over a sorted u16 array in global memory.
+__device__ __forceinline__ uint32_t lower_bound_u16(const uint16_t* a, uint32_t n, uint32_t key)
+{
+    uint32_t lo = 0, hi = n;
+    while (lo < hi) {
+        uint32_t mid = (lo + hi) >> 1;
+        if (a[mid] < key)
+            lo = mid + 1;
+        else
+            hi = mid;
+    }
+    return lo;
+}
+
+// Fill kernels (used instead of hipMemsetAsync so the work stays capturable).
+__global__ void fill_u16_kernel(uint16_t* p, uint16_t v, uint64_t n);
+__global__ void fill_u32_kernel(uint32_t* p, uint32_t v, uint64_t n);
+int fill_u16(uint16_t* p, uint16_t v, uint64_t n, hipStream_t s);
+int fill_u32(uint32_t* p, uint32_t v, uint64_t n, hipStream_t s);
+
+uint64_t device_l2_bytes(int device);
+// Compute units of the current device (cached per device).
+uint32_t num_cus();
+uint32_t resolve_auto_threshold(uint32_t universe_size, int device);
+
+}  // namespace crimpl

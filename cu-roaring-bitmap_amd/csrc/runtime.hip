@@ -1,0 +1,263 @@
+// Runtime pieces shared by every entry point: error state, allocation of
+// packed result blocks, free, AUTO threshold, and small utility entry points.
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "internal.hpp"
+
+namespace crimpl {
+
+static thread_local std::string g_last_error;
+
+void set_error(const char* fmt, ...)
+{
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+}
+
+int dev_alloc(void** p, size_t bytes, hipStream_t s)
+{
+    *p = nullptr;
+    if (bytes == 0) bytes = 256;
+    hipError_t e = hipMallocAsync(p, bytes, s);
+    if (e != hipSuccess) {
+        set_error("hipMallocAsync(%zu bytes) failed: %s", bytes, hipGetErrorString(e));
+        *p = nullptr;
+        return e == hipErrorOutOfMemory ? CR_ERR_ALLOC : CR_ERR_HIP;
+    }
+    return CR_OK;
+}
+
+int dev_free(void* p, hipStream_t s)
+{
+    if (!p) return CR_OK;
+    CR_HIP_RET(hipFreeAsync(p, s));
+    return CR_OK;
+}
+
+OutLayout plan_out(uint64_t n_meta, uint64_t kidx_len, uint64_t bmp_words, uint64_t arr_elems, uint64_t run_u16)
+{
+    Carver c;
+    OutLayout L;
+    L.bmp = c.add(bmp_words * 8);  // bitmap pool first: 256-byte aligned 8 KiB containers
+    L.keys = c.add(n_meta * 2);
+    L.types = c.add(n_meta);
+    L.offsets = c.add(n_meta * 4);
+    L.cards = c.add(n_meta * 2);
+    L.kidx = c.add(kidx_len * 2);
+    L.arr = c.add(arr_elems * 2);
+    L.run = c.add(run_u16 * 2);
+    L.total = c.total;
+    return L;
+}
+
+int alloc_out(cr_gpu_roaring* out, const OutLayout& L, uint64_t n_meta, uint64_t kidx_len, uint64_t bmp_words,
+              uint64_t arr_elems, uint64_t run_u16, hipStream_t s)
+{
+    void* base = nullptr;
+    CR_RET(dev_alloc(&base, L.total, s));
+    char* b = static_cast<char*>(base);
+    out->_alloc_base = base;
+    out->keys = n_meta ? reinterpret_cast<uint16_t*>(b + L.keys) : nullptr;
+    out->types = n_meta ? reinterpret_cast<uint8_t*>(b + L.types) : nullptr;
+    out->offsets = n_meta ? reinterpret_cast<uint32_t*>(b + L.offsets) : nullptr;
+    out->cardinalities = n_meta ? reinterpret_cast<uint16_t*>(b + L.cards) : nullptr;
+    out->key_index = kidx_len ? reinterpret_cast<uint16_t*>(b + L.kidx) : nullptr;
+    out->bitmap_data = bmp_words ? reinterpret_cast<uint64_t*>(b + L.bmp) : nullptr;
+    out->array_data = arr_elems ? reinterpret_cast<uint16_t*>(b + L.arr) : nullptr;
+    out->run_data = run_u16 ? reinterpret_cast<uint16_t*>(b + L.run) : nullptr;
+    return CR_OK;
+}
+
+void reset(cr_gpu_roaring* r) { std::memset(r, 0, sizeof(*r)); }
+
+int free_async(cr_gpu_roaring* r, hipStream_t s)
+{
+    int rc = CR_OK;
+    auto f = [&](void* p) {
+        if (p && rc == CR_OK) rc = dev_free(p, s);
+    };
+    if (r->_alloc_base) {
+        f(r->_alloc_base);
+    } else {
+        f(r->keys);
+        f(r->types);
+        f(r->offsets);
+        f(r->cardinalities);
+        f(r->bitmap_data);
+        f(r->array_data);
+        f(r->run_data);
+        f(r->key_index);
+    }
+    reset(r);
+    return rc;
+}
+
+__global__ void fill_u16_kernel(uint16_t* p, uint16_t v, uint64_t n)
+{
+    for (uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x)
+        p[i] = v;
+}
+
+__global__ void fill_u32_kernel(uint32_t* p, uint32_t v, uint64_t n)
+{
+    for (uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x)
+        p[i] = v;
+}
+
+static unsigned grid_for(uint64_t n, unsigned per_block, unsigned cap)
+{
+    uint64_t g = (n + per_block - 1) / per_block;
+    if (g == 0) g = 1;
+    return static_cast<unsigned>(g < cap ? g : cap);
+}
+
+int fill_u16(uint16_t* p, uint16_t v, uint64_t n, hipStream_t s)
+{
+    if (n == 0) return CR_OK;
+    fill_u16_kernel<<<grid_for(n, 256, 4096), 256, 0, s>>>(p, v, n);
+    CR_LAUNCH_CHECK();
+    return CR_OK;
+}
+
+int fill_u32(uint32_t* p, uint32_t v, uint64_t n, hipStream_t s)
+{
+    if (n == 0) return CR_OK;
+    fill_u32_kernel<<<grid_for(n, 256, 4096), 256, 0, s>>>(p, v, n);
+    CR_LAUNCH_CHECK();
+    return CR_OK;
+}
+
+uint32_t num_cus()
+{
+    static int cache[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cache[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        cache[dev] = cus;
+    }
+    return static_cast<uint32_t>(cache[dev]);
+}
+
+uint64_t device_l2_bytes(int device)
+{
+    int dev = device;
+    if (dev < 0 && hipGetDevice(&dev) != hipSuccess) dev = 0;
+    int l2 = 0;
+    if (hipDeviceGetAttribute(&l2, hipDeviceAttributeL2CacheSize, dev) != hipSuccess || l2 <= 0)
+        l2 = 4 * 1024 * 1024;  // the reference's fallback (src/promote.cu:348-352)
+    return static_cast<uint64_t>(l2);
+}
+
+// PROMOTE_AUTO (src/promote.cu:334-367).  hipDeviceAttributeL2CacheSize
+// reports one XCD's L2 on gfx950 (4 MiB).  Point queries from every XCD hit
+// their own L2 copy of a flat bitset, so the per-XCD L2 -- not the 256 MB
+// Infinity Cache shared by all XCDs -- is the capacity that decides whether
+// a flat bitset "fits"; the rule stays `2 * ceil(U/8) > L2`.
+uint32_t resolve_auto_threshold(uint32_t universe_size, int device)
+{
+    if (universe_size == 0) return CR_PROMOTE_KEEP_DEFAULT;
+    const uint64_t flat = (static_cast<uint64_t>(universe_size) + 7u) / 8u;
+    return flat * 2u > device_l2_bytes(device) ? CR_PROMOTE_ALL : CR_PROMOTE_KEEP_DEFAULT;
+}
+
+}  // namespace crimpl
+
+using namespace crimpl;
+
+extern "C" {
+
+const char* cr_last_error(void) { return g_last_error.c_str(); }
+
+int cr_free(cr_gpu_roaring* bm)
+{
+    if (!bm) return CR_OK;
+    int rc = free_async(bm, nullptr);
+    if (rc == CR_OK) CR_HIP_RET(hipStreamSynchronize(nullptr));
+    return rc;
+}
+
+int cr_free_async(cr_gpu_roaring* bm, cr_stream_t stream)
+{
+    if (!bm) return CR_OK;
+    return free_async(bm, as_stream(stream));
+}
+
+int cr_resolve_auto_threshold(uint32_t universe_size, int device_id, uint32_t* out_threshold)
+{
+    if (!out_threshold) {
+        set_error("cr_resolve_auto_threshold: null output");
+        return CR_ERR_INVALID;
+    }
+    *out_threshold = resolve_auto_threshold(universe_size, device_id);
+    return CR_OK;
+}
+
+int cr_device_l2_bytes(int device_id, uint64_t* out_bytes)
+{
+    if (!out_bytes) return CR_ERR_INVALID;
+    *out_bytes = device_l2_bytes(device_id);
+    return CR_OK;
+}
+
+int cr_make_view(const cr_gpu_roaring* b, cr_gpu_roaring_view* v)
+{
+    if (!b || !v) {
+        set_error("cr_make_view: null argument");
+        return CR_ERR_INVALID;
+    }
+    v->keys = b->keys;
+    v->types = b->types;
+    v->offsets = b->offsets;
+    v->cardinalities = b->cardinalities;
+    v->n_containers = b->n_containers;
+    v->bitmap_data = b->bitmap_data;
+    v->array_data = b->array_data;
+    v->run_data = b->run_data;
+    v->key_index = b->key_index;
+    v->max_key = b->max_key;
+    v->all_bitmap = b->n_array_containers == 0 && b->n_run_containers == 0 && b->key_index != nullptr;
+    v->negated = b->negated;
+    return CR_OK;
+}
+
+int cr_device_malloc(void** ptr, size_t bytes)
+{
+    CR_HIP_RET(hipMalloc(ptr, bytes ? bytes : 1));
+    return CR_OK;
+}
+
+int cr_device_free(void* ptr)
+{
+    CR_HIP_RET(hipFree(ptr));
+    return CR_OK;
+}
+
+int cr_memcpy_h2d(void* dst, const void* src, size_t bytes)
+{
+    if (bytes) CR_HIP_RET(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return CR_OK;
+}
+
+int cr_memcpy_d2h(void* dst, const void* src, size_t bytes)
+{
+    if (bytes) CR_HIP_RET(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return CR_OK;
+}
+
+int cr_stream_synchronize(cr_stream_t stream)
+{
+    CR_HIP_RET(hipStreamSynchronize(as_stream(stream)));
+    return CR_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,246 @@
+// upload_from_device_bitset / upload_from_bitset on gfx950.
+//
+// Semantics follow src/upload_ids.cu:606-893 (reference): 65536-bit chunks,
+// every non-empty chunk becomes a BITMAP container (cards clamp 65536->0),
+// complement when the popcount exceeds U/2 (strict), the inverted copy is
+// masked only in the tail word U/32, max_key = last non-empty chunk,
+// total_cardinality = the input's popcount.
+//
+// One read pass computes both the plain and the inverted popcount of every
+// chunk, so the complement decision, the chunk->container map and all
+// metadata are produced on the device and the call needs a single host sync.
+#include <algorithm>
+
+#include "internal.hpp"
+
+namespace crimpl {
+
+constexpr int BS_NT = 256;
+
+struct BsTotals {
+    uint32_t n_containers;
+    uint32_t negated;
+    uint32_t max_key;
+    uint32_t pad;
+    unsigned long long total;  // popcount of the input
+};
+
+struct BsGeom {
+    uint32_t n_words;
+    uint32_t n_chunks;
+    uint32_t tail_idx;   // word masked after inversion, or 0xFFFFFFFF
+    uint32_t tail_mask;
+    uint32_t universe;
+};
+
+__device__ __forceinline__ uint32_t load_word(const uint32_t* w, uint32_t i, uint32_t n) { return i < n ? w[i] : 0u; }
+
+// Per chunk: popcount of the words and of their inversion (tail word masked,
+// words past n_words are zero in both).
+__global__ __launch_bounds__(BS_NT) void bs_count(const uint32_t* __restrict__ words, BsGeom g, uint32_t* pc,
+                                                  uint32_t* pci)
+{
+    __shared__ uint32_t red[BS_NT / 64];
+    for (uint32_t c = blockIdx.x; c < g.n_chunks; c += gridDim.x) {
+        const uint32_t base = c * 2048u;
+        uint32_t a = 0, b = 0;
+        for (uint32_t k = threadIdx.x; k < 2048u; k += BS_NT) {
+            const uint32_t i = base + k;
+            if (i < g.n_words) {
+                const uint32_t w = words[i];
+                a += __popc(w);
+                b += (i == g.tail_idx) ? __popc(~w & g.tail_mask) : 32u - __popc(w);
+            }
+        }
+        a = block_sum<BS_NT>(a, red);
+        b = block_sum<BS_NT>(b, red);
+        if (threadIdx.x == 0) {
+            pc[c] = a;
+            pci[c] = b;
+        }
+    }
+}
+
+// One workgroup: complement decision, ranks of non-empty chunks, metadata.
+__global__ __launch_bounds__(1024) void bs_plan(BsGeom g, const uint32_t* pc, const uint32_t* pci, uint32_t* cmap,
+                                                uint16_t* keys, uint8_t* types, uint32_t* offsets, uint16_t* cards,
+                                                uint16_t* key_index, BsTotals* tot)
+{
+    __shared__ uint32_t lds[16];
+    __shared__ unsigned long long s_total;
+    __shared__ uint32_t s_last;
+    const uint32_t t = threadIdx.x;
+    const uint32_t per = (g.n_chunks + 1023) / 1024;
+    const uint32_t c0 = t * per;
+    unsigned long long part = 0;
+    for (uint32_t k = 0; k < per; ++k)
+        if (c0 + k < g.n_chunks) part += pc[c0 + k];
+    if (t == 0) {
+        s_total = 0;
+        s_last = 0;
+    }
+    __syncthreads();
+    atomicAdd(&s_total, part);
+    __syncthreads();
+    const unsigned long long total = s_total;
+    const bool negate = total > static_cast<unsigned long long>(g.universe / 2u);  // :837
+    uint32_t cnt = 0;
+    for (uint32_t k = 0; k < per; ++k) {
+        const uint32_t c = c0 + k;
+        if (c < g.n_chunks && (negate ? pci[c] : pc[c]) > 0) ++cnt;
+    }
+    uint32_t n_c;
+    uint32_t rank = block_excl_scan<1024>(cnt, lds, n_c);
+    uint32_t last = 0;
+    for (uint32_t k = 0; k < per; ++k) {
+        const uint32_t c = c0 + k;
+        if (c >= g.n_chunks) break;
+        const uint32_t p = negate ? pci[c] : pc[c];
+        if (p > 0) {
+            cmap[c] = rank;
+            keys[rank] = static_cast<uint16_t>(c);
+            types[rank] = CR_BITMAP;
+            offsets[rank] = rank * 8192u;
+            cards[rank] = static_cast<uint16_t>(p > 65535u ? 0u : p);
+            key_index[c] = static_cast<uint16_t>(rank);
+            last = c;
+            ++rank;
+        } else {
+            cmap[c] = 0xFFFFFFFFu;
+            key_index[c] = 0xFFFFu;
+        }
+    }
+    if (cnt) atomicMax(&s_last, last);
+    __syncthreads();
+    if (t == 0) {
+        tot->n_containers = n_c;
+        tot->negated = negate ? 1u : 0u;
+        tot->max_key = s_last;
+        tot->total = total;
+    }
+}
+
+__global__ __launch_bounds__(BS_NT) void bs_compact(const uint32_t* __restrict__ words, BsGeom g, const uint32_t* cmap,
+                                                    const BsTotals* tot, uint64_t* __restrict__ pool)
+{
+    const bool negate = tot->negated != 0;
+    for (uint32_t c = blockIdx.x; c < g.n_chunks; c += gridDim.x) {
+        const uint32_t r = cmap[c];
+        if (r == 0xFFFFFFFFu) continue;
+        uint32_t* dst = reinterpret_cast<uint32_t*>(pool) + static_cast<uint64_t>(r) * 2048u;
+        const uint32_t base = c * 2048u;
+        const bool full = base + 2048u <= g.n_words;
+        if (full && ((reinterpret_cast<uintptr_t>(words + base) & 15u) == 0) && !negate) {
+            const uint4* s4 = reinterpret_cast<const uint4*>(words + base);
+            uint4* d4 = reinterpret_cast<uint4*>(dst);
+            d4[threadIdx.x] = s4[threadIdx.x];
+            d4[threadIdx.x + BS_NT] = s4[threadIdx.x + BS_NT];
+        } else {
+            for (uint32_t k = threadIdx.x; k < 2048u; k += BS_NT) {
+                const uint32_t i = base + k;
+                uint32_t w = 0;
+                if (i < g.n_words) {
+                    w = words[i];
+                    if (negate) {
+                        w = ~w;
+                        if (i == g.tail_idx) w &= g.tail_mask;
+                    }
+                }
+                dst[k] = w;
+            }
+        }
+    }
+}
+
+static unsigned grid_cap(uint32_t n)
+{
+    const uint32_t cus = num_cus();
+    return std::max(1u, std::min(n, static_cast<uint32_t>(cus) * 8u));
+}
+
+int upload_from_device_bitset_impl(const uint32_t* d_words, uint32_t n_words, uint32_t universe, hipStream_t s,
+                                   cr_gpu_roaring* out)
+{
+    reset(out);
+    out->universe_size = universe;
+    if (n_words == 0) return CR_OK;  // src/upload_ids.cu:811-815
+    BsGeom g{};
+    g.n_words = n_words;
+    g.n_chunks = static_cast<uint32_t>((static_cast<uint64_t>(n_words) + 2047u) / 2048u);
+    if (g.n_chunks > 65536u) {
+        set_error("upload_from_device_bitset: %u words exceed the 2^32-id key space", n_words);
+        return CR_ERR_UNSUPPORTED;
+    }
+    g.universe = universe;
+    const uint32_t tail_bits = universe % 32u;  // :851-858
+    g.tail_idx = (tail_bits > 0 && universe / 32u < n_words) ? universe / 32u : 0xFFFFFFFFu;
+    g.tail_mask = tail_bits ? ((1u << tail_bits) - 1u) : ~0u;
+
+    Carver c;
+    const size_t o_pc = c.add(4ull * g.n_chunks);
+    const size_t o_pci = c.add(4ull * g.n_chunks);
+    const size_t o_map = c.add(4ull * g.n_chunks);
+    const size_t o_tot = c.add(sizeof(BsTotals));
+    Scratch sc;
+    CR_RET(sc.alloc(c.total, s));
+    uint32_t* pc = sc.at<uint32_t>(o_pc);
+    uint32_t* pci = sc.at<uint32_t>(o_pci);
+    uint32_t* cmap = sc.at<uint32_t>(o_map);
+    BsTotals* tot = sc.at<BsTotals>(o_tot);
+
+    const OutLayout L = plan_out(g.n_chunks, g.n_chunks, static_cast<uint64_t>(g.n_chunks) * 1024u, 0, 0);
+    CR_RET(alloc_out(out, L, g.n_chunks, g.n_chunks, static_cast<uint64_t>(g.n_chunks) * 1024u, 0, 0, s));
+
+    bs_count<<<grid_cap(g.n_chunks), BS_NT, 0, s>>>(d_words, g, pc, pci);
+    CR_LAUNCH_CHECK();
+    bs_plan<<<1, 1024, 0, s>>>(g, pc, pci, cmap, out->keys, out->types, out->offsets, out->cardinalities,
+                               out->key_index, tot);
+    CR_LAUNCH_CHECK();
+    bs_compact<<<grid_cap(g.n_chunks), BS_NT, 0, s>>>(d_words, g, cmap, tot, out->bitmap_data);
+    CR_LAUNCH_CHECK();
+    BsTotals h{};
+    CR_HIP_RET(hipMemcpyAsync(&h, tot, sizeof(h), hipMemcpyDeviceToHost, s));
+    CR_HIP_RET(hipStreamSynchronize(s));
+    out->negated = h.negated != 0;
+    out->total_cardinality = h.total;  // logical count either way (:740)
+    out->n_containers = h.n_containers;
+    out->n_bitmap_containers = h.n_containers;
+    if (h.n_containers == 0) {  // no key_index on an empty result (:747-750)
+        free_async(out, s);
+        out->universe_size = universe;
+        out->negated = h.negated != 0;
+        out->total_cardinality = h.total;
+        return CR_OK;
+    }
+    out->max_key = h.max_key;
+    return CR_OK;
+}
+
+}  // namespace crimpl
+
+using namespace crimpl;
+
+extern "C" int cr_upload_from_device_bitset(const uint32_t* d_words, uint32_t n_words, uint32_t universe_size,
+                                            cr_stream_t stream, cr_gpu_roaring* out)
+{
+    if (!out || (n_words && !d_words)) {
+        set_error("cr_upload_from_device_bitset: invalid argument");
+        return CR_ERR_INVALID;
+    }
+    return upload_from_device_bitset_impl(d_words, n_words, universe_size, as_stream(stream), out);
+}
+
+extern "C" int cr_upload_from_bitset(const uint32_t* host_words, uint32_t n_words, uint32_t universe_size,
+                                     cr_stream_t stream, cr_gpu_roaring* out)
+{
+    if (!out || (n_words && !host_words)) {
+        set_error("cr_upload_from_bitset: invalid argument");
+        return CR_ERR_INVALID;
+    }
+    hipStream_t s = as_stream(stream);
+    if (n_words == 0) return upload_from_device_bitset_impl(nullptr, 0, universe_size, s, out);
+    Scratch sc;
+    CR_RET(sc.alloc(static_cast<size_t>(n_words) * 4u, s));
+    CR_HIP_RET(hipMemcpyAsync(sc.ptr, host_words, static_cast<size_t>(n_words) * 4u, hipMemcpyHostToDevice, s));
+    return upload_from_device_bitset_impl(sc.at<uint32_t>(0), n_words, universe_size, s, out);
+}

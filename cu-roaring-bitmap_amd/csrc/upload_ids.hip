@@ -1,0 +1,668 @@
+// upload_from_ids on gfx950.
+//
+// Output semantics follow src/upload_ids.cu (reference): more than 1024 ids
+// give an all-BITMAP result with keys sorted, offsets i*8192, cards clamped
+// 65536->0, key_index sized from the universe (:171-295, :567-591); the
+// complement is stored when the distinct count exceeds U/2 (:356-410); up to
+// 1024 ids follow the threshold-aware small path (:421-561).
+//
+// The large path needs no sort.  Ids are partitioned by 16-key bucket
+// (1 MiB of id space), each bucket's 16 containers are built as 128 KiB of LDS
+// bitmaps (the bit-set dedupes), and each container is written once:
+//   hist      per-workgroup bucket histogram + key presence (read ids once)
+//   colscan   per-bucket prefix over workgroups, presence OR-reduce
+//   keyscan   bucket bases, key ranks -> keys/types/offsets/key_index
+//   partition scatter ids into their bucket's range (read ids again)
+//   build     one workgroup per bucket: LDS bit-set, popcount, write containers
+#include <algorithm>
+#include <vector>
+
+#include "internal.hpp"
+
+namespace crimpl {
+
+constexpr uint32_t BK_SHIFT = 4;               // 16 keys per bucket
+constexpr uint32_t BK_KEYS = 1u << BK_SHIFT;
+constexpr int HP_NT = 1024;                    // hist / partition workgroup
+constexpr uint32_t MAX_BUCKETS = 65536 / BK_KEYS;
+constexpr uint32_t MAX_PWORDS = 65536 / 32;
+
+struct IdsTotals {
+    uint32_t n_containers;
+    uint32_t err;  // an id's key exceeded max_key
+    uint32_t max_id;
+    uint32_t pad;
+    unsigned long long total;  // distinct ids (or complement count)
+};
+
+struct IdsGeom {
+    uint64_t n;
+    uint32_t chunk;  // ids per hist/partition workgroup
+    uint32_t G;      // hist/partition workgroups
+    uint32_t K;      // keys in the universe (max_key + 1)
+    uint32_t NB;     // buckets
+    uint32_t NW;     // presence words
+};
+
+__global__ __launch_bounds__(HP_NT) void ids_hist(const uint32_t* __restrict__ ids, IdsGeom g, uint32_t* ghist,
+                                                  uint32_t* gpres, IdsTotals* tot)
+{
+    __shared__ uint32_t hist[MAX_BUCKETS];
+    __shared__ uint32_t pres[MAX_PWORDS];
+    __shared__ uint32_t s_err, s_max;
+    const uint32_t t = threadIdx.x;
+    for (uint32_t i = t; i < g.NB; i += HP_NT) hist[i] = 0;
+    for (uint32_t i = t; i < g.NW; i += HP_NT) pres[i] = 0;
+    if (t == 0) {
+        s_err = 0;
+        s_max = 0;
+    }
+    __syncthreads();
+    const uint64_t lo = static_cast<uint64_t>(blockIdx.x) * g.chunk;
+    const uint64_t hi = min(g.n, lo + g.chunk);
+    const uint32_t max_key = g.K - 1;
+    uint32_t err = 0, mx = 0;
+    for (uint64_t i = lo + t; i < hi; i += HP_NT) {
+        const uint32_t id = ids[i];
+        const uint32_t key = id >> 16;
+        mx = max(mx, id);
+        if (key > max_key) {
+            err = 1;
+            continue;
+        }
+        atomicAdd(&hist[key >> BK_SHIFT], 1u);
+        const uint32_t bit = 1u << (key & 31u);
+        if (!(pres[key >> 5] & bit)) atomicOr(&pres[key >> 5], bit);
+    }
+    if (err) atomicOr(&s_err, 1u);
+    atomicMax(&s_max, mx);
+    __syncthreads();
+    uint32_t* oh = ghist + static_cast<uint64_t>(blockIdx.x) * g.NB;
+    for (uint32_t i = t; i < g.NB; i += HP_NT) oh[i] = hist[i];
+    uint32_t* op = gpres + static_cast<uint64_t>(blockIdx.x) * g.NW;
+    for (uint32_t i = t; i < g.NW; i += HP_NT) op[i] = pres[i];
+    if (t == 0) {
+        if (s_err) atomicOr(&tot->err, 1u);
+        atomicMax(&tot->max_id, s_max);
+    }
+}
+
+// One wave per column.  Columns [0, NB) are buckets: exclusive prefix over the
+// G workgroups (in place) and the bucket total.  Columns [NB, NB+NW) are
+// presence words: OR over workgroups.
+__global__ __launch_bounds__(1024) void ids_colscan(IdsGeom g, uint32_t* ghist, const uint32_t* gpres,
+                                                    uint32_t* btotal, uint32_t* pres)
+{
+    const uint32_t wave = (blockIdx.x * 1024u + threadIdx.x) >> 6;
+    const uint32_t lane = __lane_id();
+    if (wave >= g.NB + g.NW) return;
+    const uint32_t per = (g.G + 63) / 64;  // workgroups per lane, contiguous
+    const uint32_t w0 = lane * per;
+    if (wave < g.NB) {
+        const uint32_t b = wave;
+        uint32_t s = 0;
+        for (uint32_t k = 0; k < per; ++k) {
+            const uint32_t w = w0 + k;
+            if (w < g.G) s += ghist[static_cast<uint64_t>(w) * g.NB + b];
+        }
+        const uint32_t incl = wave_incl_scan(s);
+        uint32_t run = incl - s;
+        for (uint32_t k = 0; k < per; ++k) {
+            const uint32_t w = w0 + k;
+            if (w < g.G) {
+                uint32_t* p = ghist + static_cast<uint64_t>(w) * g.NB + b;
+                const uint32_t v = *p;
+                *p = run;
+                run += v;
+            }
+        }
+        if (lane == 63) btotal[b] = incl;
+    } else {
+        const uint32_t j = wave - g.NB;
+        uint32_t acc = 0;
+        for (uint32_t k = 0; k < per; ++k) {
+            const uint32_t w = w0 + k;
+            if (w < g.G) acc |= gpres[static_cast<uint64_t>(w) * g.NW + j];
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) acc |= __shfl_xor(acc, o, 64);
+        if (lane == 0) pres[j] = acc;
+    }
+}
+
+// Bucket bases and key ranks (one workgroup).  Writes keys/types/offsets and the
+// full key_index (0xFFFF for absent keys).
+__global__ __launch_bounds__(1024) void ids_keyscan(IdsGeom g, const uint32_t* btotal, const uint32_t* pres,
+                                                    uint32_t* bbase, uint16_t* keys, uint8_t* types, uint32_t* offsets,
+                                                    uint16_t* key_index, IdsTotals* tot)
+{
+    __shared__ uint32_t lds[16];
+    const uint32_t t = threadIdx.x;
+    {  // bucket bases: 4 buckets per thread
+        uint32_t v[4], s = 0;
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t b = t * 4 + q;
+            v[q] = b < g.NB ? btotal[b] : 0u;
+            s += v[q];
+        }
+        uint32_t total;
+        uint32_t run = block_excl_scan<1024>(s, lds, total);
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t b = t * 4 + q;
+            if (b < g.NB) bbase[b] = run;
+            run += v[q];
+        }
+    }
+    {  // key ranks: 2 presence words (64 keys) per thread
+        const uint32_t j0 = 2 * t, j1 = 2 * t + 1;
+        const uint32_t p0 = j0 < g.NW ? pres[j0] : 0u, p1 = j1 < g.NW ? pres[j1] : 0u;
+        uint32_t total;
+        uint32_t rank = block_excl_scan<1024>(__popc(p0) + __popc(p1), lds, total);
+        for (uint32_t kk = 0; kk < 64; ++kk) {
+            const uint32_t key = 64 * t + kk;
+            if (key >= g.K) break;
+            const uint32_t word = kk < 32 ? p0 : p1;
+            if ((word >> (kk & 31u)) & 1u) {
+                keys[rank] = static_cast<uint16_t>(key);
+                types[rank] = CR_BITMAP;
+                offsets[rank] = rank * 8192u;
+                key_index[key] = static_cast<uint16_t>(rank);
+                ++rank;
+            } else {
+                key_index[key] = 0xFFFFu;
+            }
+        }
+        if (t == 0) tot->n_containers = total;
+    }
+}
+
+__global__ __launch_bounds__(HP_NT) void ids_partition(const uint32_t* __restrict__ ids, IdsGeom g,
+                                                       const uint32_t* ghist_off, const uint32_t* bbase,
+                                                       uint32_t* __restrict__ part)
+{
+    __shared__ uint32_t cur[MAX_BUCKETS];
+    const uint32_t t = threadIdx.x;
+    const uint32_t* off = ghist_off + static_cast<uint64_t>(blockIdx.x) * g.NB;
+    for (uint32_t i = t; i < g.NB; i += HP_NT) cur[i] = bbase[i] + off[i];
+    __syncthreads();
+    const uint64_t lo = static_cast<uint64_t>(blockIdx.x) * g.chunk;
+    const uint64_t hi = min(g.n, lo + g.chunk);
+    const uint32_t max_key = g.K - 1;
+    for (uint64_t i = lo + t; i < hi; i += HP_NT) {
+        const uint32_t id = ids[i];
+        const uint32_t key = id >> 16;
+        if (key > max_key) continue;
+        const uint32_t pos = atomicAdd(&cur[key >> BK_SHIFT], 1u);
+        part[pos] = id;
+    }
+}
+
+// One workgroup per bucket: 16 containers as 16 x 2048 u32 LDS words (128 KiB).
+// Normal mode writes the stored containers of present keys and each key's
+// distinct count; complement mode writes ~bits masked to [0, U) for keys whose
+// complement is non-empty.
+constexpr int BUILD_NT = 1024;
+
+__global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict__ part, const uint32_t* bbase,
+                                                      const uint32_t* btotal, IdsGeom g, uint32_t universe,
+                                                      bool complement, const uint16_t* key_index,
+                                                      uint64_t* __restrict__ pool, uint16_t* cards,
+                                                      uint32_t* key_count, IdsTotals* tot)
+{
+    __shared__ uint32_t bits[BK_KEYS * 2048u];  // 128 KiB of the CU's 160 KiB LDS
+    const uint32_t t = threadIdx.x;
+    const uint32_t b = blockIdx.x;
+    for (uint32_t i = t; i < BK_KEYS * 2048u; i += BUILD_NT) bits[i] = 0;
+    __syncthreads();
+    const uint32_t start = bbase[b], cnt = btotal[b];
+    for (uint32_t i = t; i < cnt; i += BUILD_NT) {
+        const uint32_t id = part[start + i];
+        const uint32_t local = (((id >> 16) & (BK_KEYS - 1)) << 11) | ((id & 0xFFFFu) >> 5);
+        atomicOr(&bits[local], 1u << (id & 31u));
+    }
+    __syncthreads();
+    const uint32_t c = t >> 6;  // wave c owns container c of the bucket
+    const uint32_t lane = __lane_id();
+    const uint32_t key = b * BK_KEYS + c;
+    if (key >= g.K) return;
+    uint32_t* cb = bits + c * 2048u;
+    uint32_t valid_words = 2048, tail_mask = ~0u;
+    if (complement) {
+        const uint64_t valid = min<uint64_t>(65536u, static_cast<uint64_t>(universe) - static_cast<uint64_t>(key) * 65536u);
+        valid_words = static_cast<uint32_t>(valid >> 5);
+        tail_mask = (valid & 31u) ? ((1u << (valid & 31u)) - 1u) : 0u;
+    }
+    uint32_t pc = 0;
+    for (uint32_t i = lane; i < 2048u; i += 64) {
+        uint32_t w = cb[i];
+        if (complement) {
+            w = ~w;
+            if (i >= valid_words) w = (i == valid_words) ? (w & tail_mask) : 0u;
+            cb[i] = w;
+        }
+        pc += __popc(w);
+    }
+    pc = wave_sum(pc);
+    if (!complement && key_count) {
+        if (lane == 0) key_count[key] = pc;
+    }
+    if (pc == 0) return;
+    const uint32_t rank = key_index[key];
+    uint32_t* dst = reinterpret_cast<uint32_t*>(pool) + static_cast<uint64_t>(rank) * 2048u;
+    for (uint32_t i = lane; i < 2048u; i += 64) dst[i] = cb[i];
+    if (lane == 0) {
+        cards[rank] = static_cast<uint16_t>(pc > 65535u ? 0u : pc);
+        atomicAdd(&tot->total, static_cast<unsigned long long>(pc));
+    }
+}
+
+// Complement key plan: key k is stored iff its complement within [0, U) is
+// non-empty.  Writes keys/types/offsets/key_index and the container count.
+__global__ __launch_bounds__(1024) void ids_keyscan_complement(IdsGeom g, uint32_t universe, const uint32_t* key_count,
+                                                               uint16_t* keys, uint8_t* types, uint32_t* offsets,
+                                                               uint16_t* key_index, IdsTotals* tot)
+{
+    __shared__ uint32_t lds[16];
+    const uint32_t t = threadIdx.x;
+    uint64_t present = 0;
+    for (uint32_t kk = 0; kk < 64; ++kk) {
+        const uint32_t key = 64 * t + kk;
+        if (key >= g.K) break;
+        const uint64_t valid = min<uint64_t>(65536u, static_cast<uint64_t>(universe) - static_cast<uint64_t>(key) * 65536u);
+        if (valid > key_count[key]) present |= 1ull << kk;
+    }
+    uint32_t total;
+    uint32_t rank = block_excl_scan<1024>(static_cast<uint32_t>(__popcll(present)), lds, total);
+    for (uint32_t kk = 0; kk < 64; ++kk) {
+        const uint32_t key = 64 * t + kk;
+        if (key >= g.K) break;
+        if ((present >> kk) & 1u) {
+            keys[rank] = static_cast<uint16_t>(key);
+            types[rank] = CR_BITMAP;
+            offsets[rank] = rank * 8192u;
+            key_index[key] = static_cast<uint16_t>(rank);
+            ++rank;
+        } else {
+            key_index[key] = 0xFFFFu;
+        }
+    }
+    if (t == 0) {
+        tot->n_containers = total;
+        tot->total = 0;
+    }
+}
+
+// ---- small path (n <= 1024), src/upload_ids.cu:421-561 --------------------
+constexpr uint32_t SMALL_MAX = 1024;
+
+struct SmallPlan {
+    uint32_t n_vals;        // stored values (complement when negated)
+    uint32_t n_containers;
+    uint32_t n_bitmap, n_array, arr_elems;
+    uint32_t total;         // distinct ids
+    uint32_t negated;
+    uint32_t max_key;       // last stored key
+    uint32_t vals[2 * SMALL_MAX];
+    uint32_t cstart[2 * SMALL_MAX + 1];
+};
+
+__global__ __launch_bounds__(1024) void ids_small_plan(const uint32_t* ids, uint32_t n, uint32_t universe, uint32_t thr,
+                                                       SmallPlan* plan)
+{
+    __shared__ uint32_t v[SMALL_MAX];
+    __shared__ uint32_t u[2 * SMALL_MAX];
+    __shared__ uint32_t lds[16];
+    __shared__ uint32_t s_m, s_nv;
+    const uint32_t t = threadIdx.x;
+    v[t] = t < n ? ids[t] : 0xFFFFFFFFu;
+    __syncthreads();
+    for (uint32_t k = 2; k <= SMALL_MAX; k <<= 1) {  // bitonic sort
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            const uint32_t p = t ^ j;
+            if (p > t) {
+                const uint32_t a = v[t], b = v[p];
+                const bool up = (t & k) == 0;
+                if ((a > b) == up) {
+                    v[t] = b;
+                    v[p] = a;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    const bool first = t < n && (t == 0 || v[t] != v[t - 1]);
+    uint32_t m;
+    const uint32_t r = block_flag_rank<1024>(first, lds, m);
+    if (first) u[r] = v[t];
+    if (t == 0) s_m = m;
+    __syncthreads();
+    const bool negate = static_cast<uint64_t>(m) > static_cast<uint64_t>(universe) / 2u;  // :437
+    uint32_t nv = m;
+    if (negate) {
+        // universe < 2*m <= 2048: complement over [0, U) by binary search in u[0, m).
+        uint32_t cand[2];
+        bool keepc[2];
+        for (int q = 0; q < 2; ++q) {
+            const uint32_t x = 2 * t + q;
+            cand[q] = x;
+            bool in = false;
+            if (x < universe) {
+                uint32_t lo = 0, hi = m;
+                while (lo < hi) {
+                    const uint32_t mid = (lo + hi) >> 1;
+                    if (u[mid] < x)
+                        lo = mid + 1;
+                    else
+                        hi = mid;
+                }
+                in = lo < m && u[lo] == x;
+            }
+            keepc[q] = x < universe && !in;
+        }
+        uint32_t tot;
+        uint32_t pos = block_excl_scan<1024>(static_cast<uint32_t>(keepc[0]) + keepc[1], lds, tot);
+        __syncthreads();  // every lane has read u[] before it is overwritten
+        for (int q = 0; q < 2; ++q)
+            if (keepc[q]) u[pos++] = cand[q];
+        nv = tot;
+        __syncthreads();
+    }
+    if (t == 0) s_nv = nv;
+    __syncthreads();
+    nv = s_nv;
+    for (uint32_t i = t; i < nv; i += 1024) plan->vals[i] = u[i];
+    // container boundaries: value i starts a container if its key differs
+    uint32_t nstart = 0;
+    bool st[2];
+    for (int q = 0; q < 2; ++q) {
+        const uint32_t i = 2 * t + q;
+        st[q] = i < nv && (i == 0 || (u[i] >> 16) != (u[i - 1] >> 16));
+        nstart += st[q];
+    }
+    uint32_t nc;
+    uint32_t cpos = block_excl_scan<1024>(nstart, lds, nc);
+    for (int q = 0; q < 2; ++q)
+        if (st[q]) plan->cstart[cpos++] = 2 * t + q;
+    __syncthreads();
+    if (t == 0) {
+        plan->cstart[nc] = nv;
+        plan->n_vals = nv;
+        plan->n_containers = nc;
+        plan->total = s_m;
+        plan->negated = negate ? 1u : 0u;
+        plan->max_key = nv ? (u[nv - 1] >> 16) : 0u;
+    }
+    __threadfence_block();
+    __syncthreads();
+    // types and pool sizes (threshold rule :493)
+    uint32_t nb = 0, na = 0, ae = 0;
+    for (uint32_t c = t; c < nc; c += 1024) {
+        const uint32_t card = plan->cstart[c + 1] - plan->cstart[c];
+        if (card > thr)
+            ++nb;
+        else {
+            ++na;
+            ae += card;
+        }
+    }
+    uint32_t s0, s1, s2;
+    block_excl_scan<1024>(nb, lds, s0);
+    block_excl_scan<1024>(na, lds, s1);
+    block_excl_scan<1024>(ae, lds, s2);
+    if (t == 0) {
+        plan->n_bitmap = s0;
+        plan->n_array = s1;
+        plan->arr_elems = s2;
+    }
+}
+
+// Single workgroup: containers are laid out in key order; bitmap containers
+// take consecutive 8 KiB slots, array containers consecutive ranges.
+__global__ __launch_bounds__(1024) void ids_small_write(const SmallPlan* plan, uint32_t thr, uint16_t* keys,
+                                                        uint8_t* types, uint32_t* offsets, uint16_t* cards,
+                                                        uint64_t* bmp, uint16_t* arr, uint16_t* key_index,
+                                                        uint32_t kidx_len)
+{
+    __shared__ uint32_t s_bslot[2 * SMALL_MAX + 1], s_aoff[2 * SMALL_MAX + 1];
+    __shared__ uint32_t lds[16];
+    const uint32_t t = threadIdx.x;
+    const uint32_t nc = plan->n_containers;
+    {  // slot prefixes: containers 2t and 2t+1
+        uint32_t card[2], nb = 0, ae = 0;
+        for (int q = 0; q < 2; ++q) {
+            const uint32_t c = 2 * t + q;
+            card[q] = c < nc ? plan->cstart[c + 1] - plan->cstart[c] : 0u;
+            if (c < nc) {
+                if (card[q] > thr)
+                    ++nb;
+                else
+                    ae += card[q];
+            }
+        }
+        uint32_t tb, ta;
+        uint32_t bs = block_excl_scan<1024>(nb, lds, tb);
+        uint32_t ao = block_excl_scan<1024>(ae, lds, ta);
+        for (int q = 0; q < 2; ++q) {
+            const uint32_t c = 2 * t + q;
+            if (c >= nc) continue;
+            s_bslot[c] = bs;
+            s_aoff[c] = ao;
+            if (card[q] > thr)
+                ++bs;
+            else
+                ao += card[q];
+        }
+    }
+    for (uint32_t i = t; i < kidx_len; i += 1024) key_index[i] = 0xFFFFu;
+    const uint64_t bmp_words = static_cast<uint64_t>(plan->n_bitmap) * 1024u;
+    for (uint64_t i = t; i < bmp_words; i += 1024) bmp[i] = 0;
+    __syncthreads();
+    for (uint32_t c = t; c < nc; c += 1024) {
+        const uint32_t s = plan->cstart[c], e = plan->cstart[c + 1], card = e - s;
+        const uint32_t key = plan->vals[s] >> 16;
+        keys[c] = static_cast<uint16_t>(key);
+        cards[c] = static_cast<uint16_t>(card > 65535u ? 0u : card);
+        key_index[key] = static_cast<uint16_t>(c);
+        if (card > thr) {
+            types[c] = CR_BITMAP;
+            offsets[c] = s_bslot[c] * 8192u;
+        } else {
+            types[c] = CR_ARRAY;
+            offsets[c] = s_aoff[c] * 2u;
+            for (uint32_t i = s; i < e; ++i) arr[s_aoff[c] + (i - s)] = static_cast<uint16_t>(plan->vals[i]);
+        }
+    }
+    __syncthreads();
+    // bitmap bits: one lane per value (atomicOr: values of one container share words)
+    for (uint32_t c = 0; c < nc; ++c) {
+        const uint32_t s = plan->cstart[c], e = plan->cstart[c + 1];
+        if (e - s <= thr) continue;
+        uint64_t* dst = bmp + static_cast<uint64_t>(s_bslot[c]) * 1024u;
+        for (uint32_t i = s + t; i < e; i += 1024) {
+            const uint32_t low = plan->vals[i] & 0xFFFFu;
+            atomicOr(reinterpret_cast<unsigned long long*>(&dst[low >> 6]), 1ull << (low & 63u));
+        }
+    }
+}
+
+static int small_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, uint32_t thr, hipStream_t s,
+                        cr_gpu_roaring* out)
+{
+    Scratch sc;
+    CR_RET(sc.alloc(sizeof(SmallPlan), s));
+    SmallPlan* plan = sc.at<SmallPlan>(0);
+    ids_small_plan<<<1, 1024, 0, s>>>(d_ids, n, universe, thr, plan);
+    CR_LAUNCH_CHECK();
+    uint32_t hdr[8];
+    CR_HIP_RET(hipMemcpyAsync(hdr, plan, sizeof(hdr), hipMemcpyDeviceToHost, s));
+    CR_HIP_RET(hipStreamSynchronize(s));
+    const uint32_t nc = hdr[1], n_bitmap = hdr[2], n_array = hdr[3], arr_elems = hdr[4];
+    out->total_cardinality = hdr[5];
+    out->negated = hdr[6] != 0;
+    if (nc == 0) return CR_OK;  // src/upload_ids.cu:454-456
+    const uint32_t max_key = hdr[7];
+    const uint64_t kidx_len = static_cast<uint64_t>(max_key) + 1u;  // last key (:547)
+    const uint64_t bmp_words = static_cast<uint64_t>(n_bitmap) * 1024u;
+    const OutLayout L = plan_out(nc, kidx_len, bmp_words, arr_elems, 0);
+    CR_RET(alloc_out(out, L, nc, kidx_len, bmp_words, arr_elems, 0, s));
+    out->n_containers = nc;
+    out->n_bitmap_containers = n_bitmap;
+    out->n_array_containers = n_array;
+    out->array_pool_bytes = arr_elems ? arr_elems * 2u : 0u;
+    out->max_key = max_key;
+    ids_small_write<<<1, 1024, 0, s>>>(plan, thr, out->keys, out->types, out->offsets, out->cardinalities,
+                                       out->bitmap_data, out->array_data, out->key_index,
+                                       static_cast<uint32_t>(kidx_len));
+    CR_LAUNCH_CHECK();
+    CR_HIP_RET(hipStreamSynchronize(s));
+    return CR_OK;
+}
+
+static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hipStream_t s, cr_gpu_roaring* out)
+{
+    if (universe == 0) {
+        set_error("upload_from_ids: universe_size 0 with %u ids (the reference's complement underflows)", n);
+        return CR_ERR_INVALID;
+    }
+    uint32_t max_key32 = (universe - 1u) >> 16;  // src/upload_ids.cu:274-278
+    if (max_key32 > 0xFFFFu) max_key32 = 0xFFFFu;
+    IdsGeom g{};
+    g.n = n;
+    g.K = max_key32 + 1u;
+    g.NB = (g.K + BK_KEYS - 1) / BK_KEYS;
+    g.NW = (g.K + 31) / 32;
+    const uint32_t cus = num_cus();
+    const uint64_t min_chunk = 16u * HP_NT;
+    uint64_t G = std::min<uint64_t>(static_cast<uint64_t>(cus), (static_cast<uint64_t>(n) + min_chunk - 1) / min_chunk);
+    if (G == 0) G = 1;
+    g.chunk = static_cast<uint32_t>((static_cast<uint64_t>(n) + G - 1) / G);
+    g.G = static_cast<uint32_t>((static_cast<uint64_t>(n) + g.chunk - 1) / g.chunk);
+
+    Carver c;
+    const size_t o_hist = c.add(sizeof(uint32_t) * static_cast<uint64_t>(g.G) * g.NB);
+    const size_t o_gpres = c.add(sizeof(uint32_t) * static_cast<uint64_t>(g.G) * g.NW);
+    const size_t o_bt = c.add(sizeof(uint32_t) * g.NB);
+    const size_t o_bb = c.add(sizeof(uint32_t) * g.NB);
+    const size_t o_pres = c.add(sizeof(uint32_t) * g.NW);
+    const size_t o_kc = c.add(sizeof(uint32_t) * g.K);
+    const size_t o_tot = c.add(sizeof(IdsTotals));
+    const size_t o_part = c.add(sizeof(uint32_t) * static_cast<uint64_t>(n));
+    Scratch sc;
+    CR_RET(sc.alloc(c.total, s));
+    uint32_t* ghist = sc.at<uint32_t>(o_hist);
+    uint32_t* gpres = sc.at<uint32_t>(o_gpres);
+    uint32_t* btotal = sc.at<uint32_t>(o_bt);
+    uint32_t* bbase = sc.at<uint32_t>(o_bb);
+    uint32_t* pres = sc.at<uint32_t>(o_pres);
+    uint32_t* key_count = sc.at<uint32_t>(o_kc);
+    IdsTotals* tot = sc.at<IdsTotals>(o_tot);
+    uint32_t* part = sc.at<uint32_t>(o_part);
+
+    // Containers <= min(keys, ids): the pool is sized by that bound.
+    const uint64_t bound = std::min<uint64_t>(g.K, n);
+    const OutLayout L = plan_out(bound, g.K, bound * 1024u, 0, 0);
+    CR_RET(alloc_out(out, L, bound, g.K, bound * 1024u, 0, 0, s));
+    out->max_key = max_key32;
+
+    CR_RET(fill_u32(reinterpret_cast<uint32_t*>(tot), 0u, sizeof(IdsTotals) / 4, s));
+    ids_hist<<<g.G, HP_NT, 0, s>>>(d_ids, g, ghist, gpres, tot);
+    CR_LAUNCH_CHECK();
+    const uint32_t cols = g.NB + g.NW;
+    ids_colscan<<<(cols + 15) / 16, 1024, 0, s>>>(g, ghist, gpres, btotal, pres);
+    CR_LAUNCH_CHECK();
+    ids_keyscan<<<1, 1024, 0, s>>>(g, btotal, pres, bbase, out->keys, out->types, out->offsets, out->key_index, tot);
+    CR_LAUNCH_CHECK();
+    ids_partition<<<g.G, HP_NT, 0, s>>>(d_ids, g, ghist, bbase, part);
+    CR_LAUNCH_CHECK();
+    ids_build<<<g.NB, BUILD_NT, 0, s>>>(part, bbase, btotal, g, universe, false, out->key_index,
+                                                out->bitmap_data, out->cardinalities, key_count, tot);
+    CR_LAUNCH_CHECK();
+    IdsTotals h{};
+    CR_HIP_RET(hipMemcpyAsync(&h, tot, sizeof(h), hipMemcpyDeviceToHost, s));
+    CR_HIP_RET(hipStreamSynchronize(s));
+    if (h.err) {
+        free_async(out, s);
+        set_error("upload_from_ids: an id's key exceeds max_key = (universe_size-1)>>16 = %u", max_key32);
+        return CR_ERR_INVALID;
+    }
+    out->universe_size = universe;
+    out->total_cardinality = h.total;
+    out->n_containers = h.n_containers;
+    out->n_bitmap_containers = h.n_containers;
+    if (h.total <= static_cast<uint64_t>(universe) / 2u) return CR_OK;  // strict (:359)
+
+    // Complement path (:361-410): ids must lie in [0, U).
+    if (h.max_id >= universe) {
+        free_async(out, s);
+        set_error("upload_from_ids: complement needs every id < universe_size (max id %u)", h.max_id);
+        return CR_ERR_INVALID;
+    }
+    const uint64_t logical = h.total;
+    cr_gpu_roaring comp;
+    reset(&comp);
+    const OutLayout L2 = plan_out(g.K, g.K, static_cast<uint64_t>(g.K) * 1024u, 0, 0);
+    CR_RET(alloc_out(&comp, L2, g.K, g.K, static_cast<uint64_t>(g.K) * 1024u, 0, 0, s));
+    ids_keyscan_complement<<<1, 1024, 0, s>>>(g, universe, key_count, comp.keys, comp.types, comp.offsets,
+                                              comp.key_index, tot);
+    CR_LAUNCH_CHECK();
+    ids_build<<<g.NB, BUILD_NT, 0, s>>>(part, bbase, btotal, g, universe, true, comp.key_index,
+                                                comp.bitmap_data, comp.cardinalities, nullptr, tot);
+    CR_LAUNCH_CHECK();
+    CR_HIP_RET(hipMemcpyAsync(&h, tot, sizeof(h), hipMemcpyDeviceToHost, s));
+    CR_HIP_RET(hipStreamSynchronize(s));
+    free_async(out, s);
+    *out = comp;
+    out->universe_size = universe;
+    out->max_key = max_key32;
+    out->negated = true;
+    out->total_cardinality = logical;  // logical count (:408)
+    out->n_containers = h.n_containers;
+    out->n_bitmap_containers = h.n_containers;
+    if (h.n_containers == 0) {  // build_from_device_ids returns early on an empty set (:180-183)
+        free_async(out, s);
+        out->universe_size = universe;
+        out->negated = true;
+        out->total_cardinality = logical;
+    }
+    return CR_OK;
+}
+
+int upload_from_device_ids_impl(const uint32_t* d_ids, uint32_t n, uint32_t universe, uint32_t thr, hipStream_t s,
+                                cr_gpu_roaring* out)
+{
+    reset(out);
+    out->universe_size = universe;
+    if (n == 0) return CR_OK;  // src/upload_ids.cu:578-582
+    if (n > SMALL_MAX) return large_upload(d_ids, n, universe, s, out);
+    const uint32_t eff = thr == CR_PROMOTE_AUTO ? resolve_auto_threshold(universe, -1) : thr;
+    return small_upload(d_ids, n, universe, eff, s, out);
+}
+
+}  // namespace crimpl
+
+using namespace crimpl;
+
+extern "C" int cr_upload_from_device_ids(const uint32_t* d_ids, uint32_t n_ids, uint32_t universe_size,
+                                         cr_stream_t stream, uint32_t bitmap_threshold, cr_gpu_roaring* out)
+{
+    if (!out || (n_ids && !d_ids)) {
+        set_error("cr_upload_from_device_ids: invalid argument");
+        return CR_ERR_INVALID;
+    }
+    return upload_from_device_ids_impl(d_ids, n_ids, universe_size, bitmap_threshold, as_stream(stream), out);
+}
+
+extern "C" int cr_upload_from_ids(const uint32_t* ids, uint32_t n_ids, uint32_t universe_size, cr_stream_t stream,
+                                  uint32_t bitmap_threshold, cr_gpu_roaring* out)
+{
+    if (!out || (n_ids && !ids)) {
+        set_error("cr_upload_from_ids: invalid argument");
+        return CR_ERR_INVALID;
+    }
+    hipStream_t s = as_stream(stream);
+    if (n_ids == 0) return upload_from_device_ids_impl(nullptr, 0, universe_size, bitmap_threshold, s, out);
+    Scratch sc;
+    CR_RET(sc.alloc(static_cast<size_t>(n_ids) * 4u, s));
+    CR_HIP_RET(hipMemcpyAsync(sc.ptr, ids, static_cast<size_t>(n_ids) * 4u, hipMemcpyHostToDevice, s));
+    return upload_from_device_ids_impl(sc.at<uint32_t>(0), n_ids, universe_size, bitmap_threshold, s, out);
+}

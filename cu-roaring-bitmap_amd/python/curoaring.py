@@ -1,0 +1,317 @@
+"""ctypes binding of libcuroaring_amd.so (the C-ABI in include/cu_roaring_abi.h).
+
+Used by the tests and bench.py.  Every call goes through the C-ABI into the HIP
+library; there is no CPU fallback: load() raises when the built library is
+missing.  Device buffers come from torch (plumbing only).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from types import SimpleNamespace
+from typing import Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.dirname(_HERE)
+LIB_PATH = os.path.join(PKG_DIR, "lib", "libcuroaring_amd.so")
+
+CR_OK = 0
+ARRAY, BITMAP, RUN = 0, 1, 2
+AND, OR, ANDNOT, XOR = 0, 1, 2, 3
+PROMOTE_KEEP_DEFAULT = 4096
+PROMOTE_ALL = 0
+PROMOTE_AUTO = 0xFFFFFFFF
+TC_BITSET, TC_ARRAY, TC_RUN = 1, 2, 3
+QUERY_CONTAINS, QUERY_WAVEFRONT = 0, 1
+
+EXPORTS = [
+    "cr_last_error", "cr_upload_from_ids", "cr_upload_from_device_ids", "cr_upload_from_bitset",
+    "cr_upload_from_device_bitset", "cr_upload_containers", "cr_get_meta", "cr_set_operation", "cr_multi_and",
+    "cr_free", "cr_free_async", "cr_resolve_auto_threshold", "cr_make_view", "cr_contains_batch",
+    "cr_topk_filtered", "cr_device_l2_bytes", "cr_device_malloc", "cr_device_free", "cr_memcpy_h2d",
+    "cr_memcpy_d2h", "cr_stream_synchronize",
+]
+
+
+class GpuRoaring(C.Structure):
+    """cr_gpu_roaring == cu_roaring::GpuRoaring (include/cu_roaring/types.cuh:15-54)."""
+    _fields_ = [
+        ("keys", C.c_void_p),
+        ("types", C.c_void_p),
+        ("offsets", C.c_void_p),
+        ("cardinalities", C.c_void_p),
+        ("n_containers", C.c_uint32),
+        ("universe_size", C.c_uint32),
+        ("total_cardinality", C.c_uint64),
+        ("bitmap_data", C.c_void_p),
+        ("n_bitmap_containers", C.c_uint32),
+        ("array_data", C.c_void_p),
+        ("n_array_containers", C.c_uint32),
+        ("array_pool_bytes", C.c_uint32),
+        ("run_data", C.c_void_p),
+        ("n_run_containers", C.c_uint32),
+        ("run_pool_bytes", C.c_uint32),
+        ("key_index", C.c_void_p),
+        ("max_key", C.c_uint32),
+        ("negated", C.c_bool),
+        ("_alloc_base", C.c_void_p),
+    ]
+
+
+class GpuRoaringView(C.Structure):
+    _fields_ = [
+        ("keys", C.c_void_p),
+        ("types", C.c_void_p),
+        ("offsets", C.c_void_p),
+        ("cardinalities", C.c_void_p),
+        ("n_containers", C.c_uint32),
+        ("bitmap_data", C.c_void_p),
+        ("array_data", C.c_void_p),
+        ("run_data", C.c_void_p),
+        ("key_index", C.c_void_p),
+        ("max_key", C.c_uint32),
+        ("all_bitmap", C.c_bool),
+        ("negated", C.c_bool),
+    ]
+
+
+class HostContainer(C.Structure):
+    _fields_ = [("key", C.c_uint16), ("typecode", C.c_uint8), ("cardinality", C.c_int32), ("data", C.c_void_p)]
+
+
+class Meta(C.Structure):
+    _fields_ = [("n_containers", C.c_uint32), ("n_bitmap_containers", C.c_uint32),
+                ("n_array_containers", C.c_uint32), ("n_run_containers", C.c_uint32),
+                ("universe_size", C.c_uint32), ("total_bytes", C.c_size_t)]
+
+
+assert C.sizeof(GpuRoaring) == 120 and C.sizeof(GpuRoaringView) == 80
+
+_lib = None
+
+
+class CrError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+def load(path: Optional[str] = None):
+    """Load the HIP library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    p = path or LIB_PATH
+    if not os.path.exists(p):
+        raise RuntimeError(f"libcuroaring_amd.so not built at {p}: run `make -C cu-roaring-bitmap_amd` "
+                           f"(or __graft_entry__.build())")
+    L = C.CDLL(p)
+    P = C.POINTER
+    L.cr_last_error.restype = C.c_char_p
+    sigs = {
+        "cr_upload_from_ids": [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, C.c_uint32, P(GpuRoaring)],
+        "cr_upload_from_device_ids": [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, C.c_uint32, P(GpuRoaring)],
+        "cr_upload_from_bitset": [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, P(GpuRoaring)],
+        "cr_upload_from_device_bitset": [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, P(GpuRoaring)],
+        "cr_upload_containers": [C.c_void_p, C.c_uint32, C.c_uint32, C.c_bool, C.c_uint64, C.c_void_p, C.c_uint32,
+                                 P(GpuRoaring)],
+        "cr_get_meta": [C.c_void_p, C.c_uint32, P(Meta)],
+        "cr_set_operation": [P(GpuRoaring), P(GpuRoaring), C.c_uint32, C.c_void_p, P(GpuRoaring)],
+        "cr_multi_and": [C.c_void_p, C.c_uint32, C.c_void_p, P(GpuRoaring)],
+        "cr_free": [P(GpuRoaring)],
+        "cr_free_async": [P(GpuRoaring), C.c_void_p],
+        "cr_resolve_auto_threshold": [C.c_uint32, C.c_int, P(C.c_uint32)],
+        "cr_make_view": [P(GpuRoaring), P(GpuRoaringView)],
+        "cr_contains_batch": [P(GpuRoaringView), C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint32, C.c_void_p],
+        "cr_topk_filtered": [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint32, C.c_uint32, P(GpuRoaring), C.c_uint32,
+                             C.c_void_p, C.c_void_p, C.c_void_p],
+        "cr_device_l2_bytes": [C.c_int, P(C.c_uint64)],
+        "cr_device_malloc": [P(C.c_void_p), C.c_size_t],
+        "cr_device_free": [C.c_void_p],
+        "cr_memcpy_h2d": [C.c_void_p, C.c_void_p, C.c_size_t],
+        "cr_memcpy_d2h": [C.c_void_p, C.c_void_p, C.c_size_t],
+        "cr_stream_synchronize": [C.c_void_p],
+    }
+    for name, args in sigs.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = C.c_int
+    _lib = L
+    return L
+
+
+def _check(rc: int, what: str):
+    if rc != CR_OK:
+        raise CrError(rc, f"{what}: {_lib.cr_last_error().decode(errors='replace')}")
+
+
+def _stream(stream) -> Optional[int]:
+    if stream is None:
+        return None
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream  # torch.cuda.Stream
+
+
+def _dptr(t) -> int:
+    return t.data_ptr()
+
+
+# ---- uploads ---------------------------------------------------------------
+def upload_from_ids(ids, universe: int, threshold: int = PROMOTE_AUTO, stream=None) -> GpuRoaring:
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    out = GpuRoaring()
+    _check(load().cr_upload_from_ids(ids.ctypes.data if ids.size else None, ids.size, universe, _stream(stream),
+                                     threshold, C.byref(out)), "upload_from_ids")
+    return out
+
+
+def upload_from_device_ids(d_ids, universe: int, threshold: int = PROMOTE_AUTO, stream=None) -> GpuRoaring:
+    """d_ids: a torch int32/uint32 CUDA tensor (read as uint32)."""
+    out = GpuRoaring()
+    n = d_ids.numel()
+    _check(load().cr_upload_from_device_ids(_dptr(d_ids) if n else None, n, universe, _stream(stream), threshold,
+                                            C.byref(out)), "upload_from_device_ids")
+    return out
+
+
+def upload_from_bitset(words, universe: int, stream=None) -> GpuRoaring:
+    words = np.ascontiguousarray(words, dtype=np.uint32)
+    out = GpuRoaring()
+    _check(load().cr_upload_from_bitset(words.ctypes.data if words.size else None, words.size, universe,
+                                        _stream(stream), C.byref(out)), "upload_from_bitset")
+    return out
+
+
+def upload_from_device_bitset(d_words, universe: int, stream=None) -> GpuRoaring:
+    out = GpuRoaring()
+    n = d_words.numel()
+    _check(load().cr_upload_from_device_bitset(_dptr(d_words) if n else None, n, universe, _stream(stream),
+                                               C.byref(out)), "upload_from_device_bitset")
+    return out
+
+
+def _container_array(containers):
+    arr = (HostContainer * max(1, len(containers)))()
+    keep = []
+    for i, (key, tc, card, payload) in enumerate(containers):
+        p = np.ascontiguousarray(payload)
+        keep.append(p)
+        arr[i] = HostContainer(key, tc, card, p.ctypes.data if p.size else None)
+    return arr, keep
+
+
+def upload_containers(containers, universe: int = 0, complemented: bool = False, logical_cardinality: int = 0,
+                      threshold: int = PROMOTE_AUTO, stream=None) -> GpuRoaring:
+    """containers: [(key, typecode, cardinality|n_runs, payload ndarray)] sorted by key."""
+    arr, keep = _container_array(containers)
+    out = GpuRoaring()
+    _check(load().cr_upload_containers(arr, len(containers), universe, complemented, logical_cardinality,
+                                       _stream(stream), threshold, C.byref(out)), "upload_containers")
+    del keep
+    return out
+
+
+def get_meta(containers) -> Meta:
+    arr, keep = _container_array(containers)
+    m = Meta()
+    _check(load().cr_get_meta(arr, len(containers), C.byref(m)), "get_meta")
+    return m
+
+
+# ---- set operations ----------------------------------------------------------
+def set_operation(a: GpuRoaring, b: GpuRoaring, op: int, stream=None) -> GpuRoaring:
+    out = GpuRoaring()
+    _check(load().cr_set_operation(C.byref(a), C.byref(b), op, _stream(stream), C.byref(out)), "set_operation")
+    return out
+
+
+def multi_and(bitmaps: Sequence[GpuRoaring], stream=None) -> GpuRoaring:
+    arr = (GpuRoaring * max(1, len(bitmaps)))()
+    for i, b in enumerate(bitmaps):
+        arr[i] = b
+    out = GpuRoaring()
+    _check(load().cr_multi_and(arr, len(bitmaps), _stream(stream), C.byref(out)), "multi_and")
+    return out
+
+
+def free(g: GpuRoaring):
+    _check(load().cr_free(C.byref(g)), "free")
+
+
+def free_async(g: GpuRoaring, stream=None):
+    _check(load().cr_free_async(C.byref(g), _stream(stream)), "free_async")
+
+
+def resolve_auto_threshold(universe: int, device: int = -1) -> int:
+    t = C.c_uint32()
+    _check(load().cr_resolve_auto_threshold(universe, device, C.byref(t)), "resolve_auto_threshold")
+    return t.value
+
+
+def device_l2_bytes(device: int = -1) -> int:
+    v = C.c_uint64()
+    _check(load().cr_device_l2_bytes(device, C.byref(v)), "device_l2_bytes")
+    return v.value
+
+
+def make_view(g: GpuRoaring) -> GpuRoaringView:
+    v = GpuRoaringView()
+    _check(load().cr_make_view(C.byref(g), C.byref(v)), "make_view")
+    return v
+
+
+def contains_batch(g: GpuRoaring, d_ids, d_out, mode: int = QUERY_CONTAINS, stream=None):
+    """d_ids / d_out: CUDA tensors of n uint32 (int32 storage); asynchronous."""
+    v = make_view(g)
+    n = d_ids.numel()
+    _check(load().cr_contains_batch(C.byref(v), _dptr(d_ids), n, _dptr(d_out), mode, _stream(stream)),
+           "contains_batch")
+
+
+def topk_filtered(d_base, d_queries, k: int, filt: Optional[GpuRoaring], d_dist, d_ids, stream=None):
+    n_base, dim = d_base.shape
+    nq = d_queries.shape[0]
+    _check(load().cr_topk_filtered(_dptr(d_base), n_base, _dptr(d_queries), nq, dim,
+                                   C.byref(filt) if filt is not None else None, k, _dptr(d_dist), _dptr(d_ids),
+                                   _stream(stream)), "topk_filtered")
+
+
+def synchronize(stream=None):
+    _check(load().cr_stream_synchronize(_stream(stream)), "stream_synchronize")
+
+
+# ---- download to host (canonical comparison) -----------------------------------
+def _d2h(ptr, n, dtype):
+    a = np.zeros(n, dtype=dtype)
+    if n and ptr:
+        _check(load().cr_memcpy_d2h(a.ctypes.data, ptr, a.nbytes), "memcpy_d2h")
+    return a
+
+
+def download(g: GpuRoaring) -> SimpleNamespace:
+    """Host copy of every field and pool (same shape as the oracle's HostRoaring)."""
+    n = g.n_containers
+    kidx = _d2h(g.key_index, g.max_key + 1, np.uint16) if g.key_index else None
+    return SimpleNamespace(
+        keys=_d2h(g.keys, n, np.uint16),
+        types=_d2h(g.types, n, np.uint8),
+        offsets=_d2h(g.offsets, n, np.uint32),
+        cards=_d2h(g.cardinalities, n, np.uint16),
+        n_containers=n,
+        universe_size=g.universe_size,
+        total_cardinality=g.total_cardinality,
+        bitmap_data=_d2h(g.bitmap_data, g.n_bitmap_containers * 1024, np.uint64),
+        n_bitmap_containers=g.n_bitmap_containers,
+        array_data=_d2h(g.array_data, g.array_pool_bytes // 2, np.uint16),
+        n_array_containers=g.n_array_containers,
+        array_pool_bytes=g.array_pool_bytes,
+        run_data=_d2h(g.run_data, g.run_pool_bytes // 2, np.uint16),
+        n_run_containers=g.n_run_containers,
+        run_pool_bytes=g.run_pool_bytes,
+        key_index=kidx,
+        max_key=g.max_key,
+        negated=bool(g.negated),
+    )

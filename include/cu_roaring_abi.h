@@ -1,0 +1,190 @@
+/*
+ * cu_roaring_abi.h -- the C-ABI boundary of the MI355X Roaring library.
+ *
+ * Plain C: pointers, sizes and status codes only.  Every entry point returns
+ * CR_OK (0) on success or a CR_ERR_* code; cr_last_error() returns a
+ * thread-local message for the last failure on the calling thread.  Device
+ * pointers are HIP device pointers; `stream` is a hipStream_t (NULL = the
+ * default stream).  Producing calls are stream-ordered and synchronise
+ * `stream` once before returning, so every host-side field of the returned
+ * struct is valid on return (the reference's contract).
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths relative to the reference checkout).
+ */
+#ifndef CU_ROARING_ABI_H
+#define CU_ROARING_ABI_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CR_OK 0
+#define CR_ERR_HIP 1          /* a HIP runtime call failed */
+#define CR_ERR_INVALID 2      /* invalid argument (e.g. an id whose key exceeds the universe) */
+#define CR_ERR_ALLOC 3        /* device or pinned host allocation failed */
+#define CR_ERR_UNSUPPORTED 4  /* request outside what this build implements */
+
+/* ContainerType (include/cu_roaring/types.cuh:7-11). */
+#define CR_ARRAY 0
+#define CR_BITMAP 1
+#define CR_RUN 2
+/* SetOp (include/cu_roaring/detail/set_ops.cuh:7-12). */
+#define CR_AND 0
+#define CR_OR 1
+#define CR_ANDNOT 2
+#define CR_XOR 3
+/* PROMOTE_* (include/cu_roaring/detail/promote.cuh:38-40). */
+#define CR_PROMOTE_KEEP_DEFAULT 4096u
+#define CR_PROMOTE_ALL 0u
+#define CR_PROMOTE_AUTO 0xFFFFFFFFu
+/* CRoaring container type codes accepted by cr_upload_containers (src/upload.cpp:21-23). */
+#define CR_TC_BITSET 1
+#define CR_TC_ARRAY 2
+#define CR_TC_RUN 3
+/* cr_contains_batch modes. */
+#define CR_QUERY_CONTAINS 0   /* GpuRoaringView::contains per lane */
+#define CR_QUERY_WAVEFRONT 1  /* wavefront_contains (== warp_contains) */
+
+/*
+ * Byte-identical to cu_roaring::GpuRoaring (include/cu_roaring/types.cuh:15-54):
+ * same field order and types, 120 bytes on LP64.
+ */
+typedef struct cr_gpu_roaring {
+    uint16_t* keys;
+    uint8_t* types;
+    uint32_t* offsets;
+    uint16_t* cardinalities;
+    uint32_t n_containers;
+    uint32_t universe_size;
+    uint64_t total_cardinality;
+    uint64_t* bitmap_data;
+    uint32_t n_bitmap_containers;
+    uint16_t* array_data;
+    uint32_t n_array_containers;
+    uint32_t array_pool_bytes;
+    uint16_t* run_data;
+    uint32_t n_run_containers;
+    uint32_t run_pool_bytes;
+    uint16_t* key_index;
+    uint32_t max_key;
+    bool negated;
+    void* _alloc_base;
+} cr_gpu_roaring;
+
+/* Byte-identical to cu_roaring::GpuRoaringView (include/cu_roaring/device/roaring_view.cuh:14-37). */
+typedef struct cr_gpu_roaring_view {
+    const uint16_t* keys;
+    const uint8_t* types;
+    const uint32_t* offsets;
+    const uint16_t* cardinalities;
+    uint32_t n_containers;
+    const uint64_t* bitmap_data;
+    const uint16_t* array_data;
+    const uint16_t* run_data;
+    const uint16_t* key_index;
+    uint32_t max_key;
+    bool all_bitmap;
+    bool negated;
+} cr_gpu_roaring_view;
+
+/* GpuRoaringMeta (include/cu_roaring/types.cuh:56-63). */
+typedef struct cr_meta {
+    uint32_t n_containers;
+    uint32_t n_bitmap_containers;
+    uint32_t n_array_containers;
+    uint32_t n_run_containers;
+    uint32_t universe_size;
+    size_t total_bytes;
+} cr_meta;
+
+/*
+ * One host container as upload() reads it from a CRoaring roaring_bitmap_t
+ * (src/upload.cpp:31-71, 155-225): typecode CR_TC_*, `cardinality` is the
+ * element count for bitset/array containers and n_runs for run containers,
+ * `data` points to 1024 u64 words, `cardinality` u16 values, or n_runs
+ * (start, length) u16 pairs.  Containers are sorted by key.
+ */
+typedef struct cr_host_container {
+    uint16_t key;
+    uint8_t typecode;
+    int32_t cardinality;
+    const void* data;
+} cr_host_container;
+
+typedef void* cr_stream_t;
+
+const char* cr_last_error(void);
+
+/* upload_from_ids (include/cu_roaring/detail/upload_ids.cuh:19-23; src/upload_ids.cu:567-591).
+ * `ids` are host ids; they are copied to the device and processed there. */
+int cr_upload_from_ids(const uint32_t* ids, uint32_t n_ids, uint32_t universe_size, cr_stream_t stream,
+                       uint32_t bitmap_threshold, cr_gpu_roaring* out);
+/* Same semantics with device-resident ids (no reference counterpart; the
+ * reference always copies host ids, src/upload_ids.cu:310-313). */
+int cr_upload_from_device_ids(const uint32_t* d_ids, uint32_t n_ids, uint32_t universe_size, cr_stream_t stream,
+                              uint32_t bitmap_threshold, cr_gpu_roaring* out);
+/* upload_from_bitset (upload_ids.cuh:48-51; src/upload_ids.cu:872-893). */
+int cr_upload_from_bitset(const uint32_t* host_words, uint32_t n_words, uint32_t universe_size, cr_stream_t stream,
+                          cr_gpu_roaring* out);
+/* upload_from_device_bitset (upload_ids.cuh:53-56; src/upload_ids.cu:806-867). */
+int cr_upload_from_device_bitset(const uint32_t* d_words, uint32_t n_words, uint32_t universe_size,
+                                 cr_stream_t stream, cr_gpu_roaring* out);
+/* upload_impl, the packed single-allocation upload of a host Roaring
+ * (include/cu_roaring/detail/upload.cuh:19-32; src/upload.cpp:89-287).
+ * `universe_size` 0 means "infer from the last key" (the overload without U).
+ * The complement of upload(bm, U) is applied by the caller, which then passes
+ * complemented=true and the logical cardinality (src/upload.cpp:296-316). */
+int cr_upload_containers(const cr_host_container* containers, uint32_t n, uint32_t universe_size, bool complemented,
+                         uint64_t logical_cardinality, cr_stream_t stream, uint32_t bitmap_threshold,
+                         cr_gpu_roaring* out);
+/* get_meta (upload.cuh:41; src/upload.cpp:31-71), over the same container list. */
+int cr_get_meta(const cr_host_container* containers, uint32_t n, cr_meta* out);
+/* set_operation (include/cu_roaring/detail/set_ops.cuh:16-19; src/set_ops.cu:567-1207). */
+int cr_set_operation(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_t op, cr_stream_t stream,
+                     cr_gpu_roaring* out);
+/* multi_and (set_ops.cuh:22-24; src/set_ops.cu:1715-1745). */
+int cr_multi_and(const cr_gpu_roaring* bitmaps, uint32_t count, cr_stream_t stream, cr_gpu_roaring* out);
+/* gpu_roaring_free / gpu_roaring_free_async (upload.cuh:34,39; src/upload.cpp:318-350).
+ * Both reset *bm to the empty struct. */
+int cr_free(cr_gpu_roaring* bm);
+int cr_free_async(cr_gpu_roaring* bm, cr_stream_t stream);
+/* resolve_auto_threshold (include/cu_roaring/detail/promote.cuh:75; src/promote.cu:334-367). */
+int cr_resolve_auto_threshold(uint32_t universe_size, int device_id, uint32_t* out_threshold);
+/* make_view (include/cu_roaring/device/make_view.cuh:9-27). */
+int cr_make_view(const cr_gpu_roaring* bm, cr_gpu_roaring_view* out);
+/* Batched point queries: out[i] = view.contains(ids[i]) (mode CR_QUERY_CONTAINS)
+ * or wavefront_contains(view, ids[i]) (CR_QUERY_WAVEFRONT), as uint32 0/1.
+ * The reference exposes contains()/warp_contains() only as device functions
+ * (roaring_view.cuh:39, roaring_warp_query.cuh:16); this is the launcher its
+ * benches and tests write around them (bench/bench_point_query.cu:123-144). */
+int cr_contains_batch(const cr_gpu_roaring_view* view, const uint32_t* d_ids, uint64_t n, uint32_t* d_out,
+                      uint32_t mode, cr_stream_t stream);
+/* Filtered brute-force top-k (no reference implementation; BASELINE.json's
+ * fused filtered top-k).  base: n_base x dim fp32 row-major (device),
+ * queries: n_q x dim fp32 (device), filter: a GpuRoaring over [0, n_base)
+ * (NULL = no filter).  Writes, per query, the k smallest squared L2 distances
+ * ascending (ties: smaller id first) and their ids; slots beyond the number of
+ * passing vectors hold +inf and -1. */
+int cr_topk_filtered(const float* d_base, uint64_t n_base, const float* d_queries, uint32_t n_q, uint32_t dim,
+                     const cr_gpu_roaring* filter, uint32_t k, float* d_out_dist, int64_t* d_out_ids,
+                     cr_stream_t stream);
+
+/* ---- utilities (no reference counterpart) -------------------------------- */
+/* L2 size the AUTO rule uses for `device_id` (hipDeviceAttributeL2CacheSize). */
+int cr_device_l2_bytes(int device_id, uint64_t* out_bytes);
+/* Plain device memory helpers for bindings that have no HIP runtime of their own. */
+int cr_device_malloc(void** ptr, size_t bytes);
+int cr_device_free(void* ptr);
+int cr_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int cr_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int cr_stream_synchronize(cr_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CU_ROARING_ABI_H */

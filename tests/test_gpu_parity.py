@@ -1,0 +1,343 @@
+"""GPU parity: the HIP library through the C-ABI vs the CPU oracle, bit-exact.
+
+Every case prints what it runs before touching the GPU.  Sizes are chosen so
+the oracle finishes in seconds; full-size configurations are covered by the
+property tests in test_gpu_scale.py.
+"""
+import numpy as np
+import pytest
+
+import orc
+from helpers import assert_same, flat_from_ids, mt_bernoulli, mt_mod_filter, words_mask
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print("CASE", *a, flush=True)
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _dev_u32(a):
+    torch = _torch()
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).cuda()
+
+
+# ---- upload_from_ids --------------------------------------------------------
+ID_CASES = [
+    # (n, universe, threshold, seed)
+    (1, 1000, orc.PROMOTE_KEEP_DEFAULT, 1),
+    (8, 200000, orc.PROMOTE_KEEP_DEFAULT, 2),
+    (500, 5 * 65536, orc.PROMOTE_ALL, 3),
+    (1000, 1 << 20, orc.PROMOTE_AUTO, 4),
+    (1024, 70000, 100, 5),
+    (1025, 70000, orc.PROMOTE_AUTO, 6),
+    (5000, 1 << 22, orc.PROMOTE_AUTO, 7),
+    (200000, 1 << 24, orc.PROMOTE_KEEP_DEFAULT, 8),
+    (300000, 1 << 30, orc.PROMOTE_AUTO, 9),
+    (50000, 0xFFFFFFFF, orc.PROMOTE_AUTO, 10),
+]
+
+
+@pytest.mark.parametrize("n,universe,thr,seed", ID_CASES)
+def test_upload_from_ids_parity(gpu, n, universe, thr, seed):
+    _say("upload_from_ids", n, universe, thr, seed)
+    rng = np.random.default_rng(seed)
+    ids = rng.integers(0, universe, n, dtype=np.uint64).astype(np.uint32)
+    if n > 10:
+        ids[: n // 10] = ids[n // 10: 2 * (n // 10)]  # ~10% duplicates
+    want = orc.upload_from_ids(ids, universe, thr, gpu.device_l2_bytes())
+    g = gpu.upload_from_ids(ids, universe, thr)
+    got = gpu.download(g)
+    assert_same(got, want, strict=True, what="upload_from_ids")
+    gpu.free(g)
+    g = gpu.upload_from_device_ids(_dev_u32(ids), universe, thr)
+    assert_same(gpu.download(g), want, strict=True, what="upload_from_device_ids")
+    gpu.free(g)
+
+
+@pytest.mark.parametrize("case", ["small_negated", "absent_key", "large_gpu_path", "reversed_all", "half",
+                                  "dense_clustered", "full_containers"])
+def test_upload_from_ids_complement_cases(gpu, case):
+    _say("upload_from_ids complement", case)
+    if case == "small_negated":  # test/test_complement.cu:129-149
+        ids, U = np.array([0, 1, 2, 3, 4, 5, 6, 8, 9], np.uint32), 10
+    elif case == "absent_key":  # :151-182
+        ids, U = mt_mod_filter(42, 200000, 10, keep_zero=False), 200000
+    elif case == "large_gpu_path":  # :184-210
+        ids, U = mt_mod_filter(123, 100000, 5, keep_zero=False), 100000
+    elif case == "reversed_all":  # test/test_promote.cu:431-449
+        ids, U = np.arange(999, -1, -1, dtype=np.uint32), 1000
+    elif case == "half":  # :227-237 (not negated)
+        ids, U = np.arange(50, dtype=np.uint32), 100
+    elif case == "dense_clustered":
+        ids, U = np.concatenate([np.arange(0, 300000), np.arange(400000, 1000000)]).astype(np.uint32), 1048576
+    else:
+        ids, U = np.arange(3 * 65536 + 5, dtype=np.uint32), 4 * 65536 + 17
+    want = orc.upload_from_ids(ids, U)
+    g = gpu.upload_from_ids(ids, U)
+    assert_same(gpu.download(g), want, strict=True, what=case)
+    gpu.free(g)
+
+
+def test_upload_from_ids_rejects_out_of_universe_keys(gpu):
+    _say("upload_from_ids invalid")
+    ids = np.arange(2000, dtype=np.uint32) + (5 << 16)
+    with pytest.raises(gpu.CrError) as e:
+        gpu.upload_from_ids(ids, 65536)
+    assert e.value.code == 2
+
+
+# ---- bitset uploads ----------------------------------------------------------
+BITSET_CASES = [(100000, 0.1, 1), (100000, 0.9, 2), (200000, 1 / 3, 3), (5 * 65536 + 123, 0.001, 4),
+                (5 * 65536 + 123, 0.95, 5), (1 << 22, 0.5, 6), (1 << 22, 0.55, 7), (64, 1.0, 8), (96, 0.0, 9)]
+
+
+@pytest.mark.parametrize("universe,density,seed", BITSET_CASES)
+def test_upload_from_bitset_parity(gpu, universe, density, seed):
+    _say("upload_from_bitset", universe, density, seed)
+    rng = np.random.default_rng(seed)
+    ids = np.nonzero(rng.random(universe) < density)[0].astype(np.uint32)
+    words = flat_from_ids(ids, universe)
+    want = orc.upload_from_bitset(words, universe)
+    g = gpu.upload_from_bitset(words, universe)
+    assert_same(gpu.download(g), want, strict=True, what="upload_from_bitset")
+    gpu.free(g)
+    g = gpu.upload_from_device_bitset(_dev_u32(words), universe)
+    assert_same(gpu.download(g), want, strict=True, what="upload_from_device_bitset")
+    gpu.free(g)
+
+
+def test_upload_from_bitset_extra_words_and_tail(gpu):
+    # n_words beyond ceil(U/32): inverted words past the tail stay all-ones (reference quirk)
+    _say("upload_from_bitset extra words")
+    U = 70000
+    words = np.full(2200 + 2048, 0xFFFFFFFF, dtype=np.uint32)
+    words[100] = 0
+    want = orc.upload_from_bitset(words, U)
+    g = gpu.upload_from_bitset(words, U)
+    assert_same(gpu.download(g), want, strict=True, what="extra words")
+    gpu.free(g)
+
+
+# ---- packed upload ------------------------------------------------------------
+def _lite_sets():
+    rng = np.random.default_rng(11)
+    U = 8 * 65536
+    sparse = np.unique(rng.integers(0, U, 2000, dtype=np.uint32))
+    dense = np.nonzero(rng.random(U) < 0.6)[0].astype(np.uint32)
+    runs = np.unique(np.concatenate([np.arange(s, s + l) for s, l in ((1000, 5000), (70000, 65000), (300000, 9))]))
+    mixed = np.unique(np.concatenate([sparse[:500], dense[dense < 2 * 65536], runs]).astype(np.uint32))
+    return U, {"sparse": sparse, "dense": dense, "runs": runs.astype(np.uint32), "mixed": mixed}
+
+
+@pytest.mark.parametrize("name", ["sparse", "dense", "runs", "mixed"])
+@pytest.mark.parametrize("thr", [orc.PROMOTE_KEEP_DEFAULT, orc.PROMOTE_ALL, orc.PROMOTE_AUTO, 100])
+@pytest.mark.parametrize("with_u", [False, True])
+def test_upload_containers_parity(gpu, name, thr, with_u):
+    _say("upload_containers", name, thr, with_u)
+    U, sets = _lite_sets()
+    lite = orc.Lite.from_sorted_ids(sets[name]).run_optimize()
+    want = orc.upload_packed(lite, U if with_u else None, thr, gpu.device_l2_bytes())
+    if with_u and lite.cardinality() > U // 2:
+        src, comp = lite.flip(0, U), True
+    else:
+        src, comp = lite, False
+    g = gpu.upload_containers(src.containers(), U if with_u else 0, comp, lite.cardinality(), thr)
+    assert_same(gpu.download(g), want, strict=True, what="upload_containers")
+    gpu.free(g)
+
+
+# ---- set operations -----------------------------------------------------------
+def _build_operands(seed):
+    """A mix of array / bitmap / run containers with shared and one-sided keys."""
+    rng = np.random.default_rng(seed)
+    U = 12 * 65536
+    parts_a, parts_b = [], []
+    for key in range(12):
+        base = key * 65536
+        kind_a, kind_b = rng.integers(0, 5, 2)
+        for kind, parts in ((kind_a, parts_a), (kind_b, parts_b)):
+            if kind == 0:
+                continue  # key absent
+            if kind == 1:
+                parts.append(base + np.unique(rng.integers(0, 65536, int(rng.integers(1, 3000)))))
+            elif kind == 2:
+                parts.append(base + np.nonzero(rng.random(65536) < rng.uniform(0.1, 0.9))[0])
+            elif kind == 3:
+                s = int(rng.integers(0, 30000))
+                parts.append(base + np.arange(s, s + int(rng.integers(100, 35000))))
+            else:
+                parts.append(base + np.arange(65536))  # full container
+    a = np.unique(np.concatenate(parts_a)).astype(np.uint32) if parts_a else np.zeros(0, np.uint32)
+    b = np.unique(np.concatenate(parts_b)).astype(np.uint32) if parts_b else np.zeros(0, np.uint32)
+    la = orc.Lite.from_sorted_ids(a).run_optimize()
+    lb = orc.Lite.from_sorted_ids(b).run_optimize()
+    return U, la, lb
+
+
+def _upload_pair(gpu, lite, U, thr, negate=False):
+    if negate:
+        comp = lite.flip(0, U)
+        want = orc.upload_packed(comp, None, thr, gpu.device_l2_bytes())
+        want.negated, want.universe_size, want.total_cardinality, want._c = True, U, lite.cardinality(), None
+        g = gpu.upload_containers(comp.containers(), 0, False, 0, thr)
+        g.negated, g.universe_size, g.total_cardinality = True, U, lite.cardinality()
+        return g, want
+    want = orc.upload_packed(lite, None, thr, gpu.device_l2_bytes())
+    return gpu.upload_containers(lite.containers(), 0, False, 0, thr), want
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3, 4, 5, 6])
+@pytest.mark.parametrize("op", [orc.AND, orc.OR, orc.ANDNOT, orc.XOR])
+def test_set_operation_mixed_parity(gpu, seed, op):
+    _say("set_operation mixed", seed, op)
+    U, la, lb = _build_operands(seed)
+    ga, oa = _upload_pair(gpu, la, U, orc.PROMOTE_KEEP_DEFAULT)
+    gb, ob = _upload_pair(gpu, lb, U, orc.PROMOTE_KEEP_DEFAULT)
+    want = orc.set_operation(oa, ob, op)
+    g = gpu.set_operation(ga, gb, op)
+    assert_same(gpu.download(g), want, strict=True, what=f"setop {op}")
+    for x in (g, ga, gb):
+        gpu.free(x)
+
+
+@pytest.mark.parametrize("op", [orc.AND, orc.OR, orc.ANDNOT, orc.XOR])
+@pytest.mark.parametrize("na", [False, True])
+@pytest.mark.parametrize("nb", [False, True])
+def test_set_operation_demorgan_parity(gpu, op, na, nb):  # test/test_complement.cu:367-462
+    _say("set_operation demorgan", op, na, nb)
+    U = 100000
+    la = orc.Lite.from_sorted_ids(mt_bernoulli(42, 0.3, U))
+    lb = orc.Lite.from_sorted_ids(mt_bernoulli(99, 0.4, U))
+    ga, oa = _upload_pair(gpu, la, U, orc.PROMOTE_AUTO, negate=na)
+    gb, ob = _upload_pair(gpu, lb, U, orc.PROMOTE_AUTO, negate=nb)
+    want = orc.set_operation(oa, ob, op)
+    g = gpu.set_operation(ga, gb, op)
+    got = gpu.download(g)
+    assert_same(got, want, strict=True, what="demorgan")
+    logical = {orc.AND: np.intersect1d, orc.OR: np.union1d, orc.ANDNOT: np.setdiff1d,
+               orc.XOR: np.setxor1d}[op](la.to_ids(), lb.to_ids())
+    assert np.array_equal(words_mask(orc.decompress(got, (U + 31) // 32), U), words_mask(flat_from_ids(logical, U), U))
+    for x in (g, ga, gb):
+        gpu.free(x)
+
+
+@pytest.mark.parametrize("op", [orc.AND, orc.OR, orc.ANDNOT, orc.XOR])
+def test_set_operation_all_bitmap_large(gpu, op):
+    _say("set_operation all-bitmap", op)
+    U = 1 << 26
+    rng = np.random.default_rng(77 + op)
+    a = rng.integers(0, U, 3_000_000, dtype=np.uint32)
+    b = rng.integers(0, U // 2, 2_000_000, dtype=np.uint32)
+    oa, ob = orc.upload_from_ids(a, U), orc.upload_from_ids(b, U)
+    ga, gb = gpu.upload_from_ids(a, U), gpu.upload_from_ids(b, U)
+    want = orc.set_operation(oa, ob, op)
+    g = gpu.set_operation(ga, gb, op)
+    assert_same(gpu.download(g), want, strict=True, what="bb large")
+    for x in (g, ga, gb):
+        gpu.free(x)
+
+
+def test_set_operation_empty_and_identical(gpu):
+    _say("set_operation empty/identical")
+    a = orc.Lite.from_sorted_ids(np.arange(1000, dtype=np.uint32))
+    b = orc.Lite.from_sorted_ids(np.arange(65536, 66536, dtype=np.uint32))
+    ga, _ = _upload_pair(gpu, a, 0, orc.PROMOTE_AUTO)
+    gb, _ = _upload_pair(gpu, b, 0, orc.PROMOTE_AUTO)
+    r = gpu.set_operation(ga, gb, orc.AND)
+    assert r.n_containers == 0
+    x = gpu.set_operation(ga, ga, orc.XOR)
+    assert x.n_containers == 0 and x.n_bitmap_containers == 1  # array x array XOR -> mixed -> BITMAP slot
+    e = gpu.upload_from_ids(np.zeros(0, np.uint32), 1000)
+    r2 = gpu.set_operation(e, e, orc.OR)
+    assert r2.n_containers == 0 and r2.universe_size == 1000
+    for g in (r, x, r2, ga, gb, e):
+        gpu.free(g)
+
+
+# ---- multi_and ----------------------------------------------------------------
+@pytest.mark.parametrize("case", ["fused_plain", "fused_negated", "fused_all_negated", "pairwise_arrays",
+                                  "fused_absent_negated_key", "single", "fused_8"])
+def test_multi_and_parity(gpu, case):
+    _say("multi_and", case)
+    rng = np.random.default_rng(hash(case) & 0xFFFF)
+    if case == "fused_absent_negated_key":  # test/test_complement.cu:604-679
+        U = 3 * 65536
+        la = np.nonzero(rng.random(U) < 0.2)[0]
+        lb = np.setdiff1d(np.arange(U), [70000, 70001, 70005, 70100, 70200])
+        lc = np.concatenate([np.nonzero(rng.random(65536) < 1 / 7)[0], 131072 + np.nonzero(rng.random(65536) < 1 / 7)[0]])
+        logicals, thr = [la, lb, lc], orc.PROMOTE_ALL
+    elif case == "fused_8":
+        U = 8 * 65536
+        logicals = [np.nonzero(rng.random(U) < (0.2 if i % 2 == 0 else 0.85))[0] for i in range(8)]
+        thr = orc.PROMOTE_ALL
+    else:
+        U = 200000
+        dens = {"fused_plain": [0.6, 0.5, 0.4], "fused_negated": [0.33, 0.5, 0.75],
+                "fused_all_negated": [0.75, 0.67, 0.8], "pairwise_arrays": [0.6, 0.01, 0.5],
+                "single": [0.3]}[case]
+        logicals = [np.nonzero(rng.random(U) < d)[0] for d in dens]
+        thr = orc.PROMOTE_ALL if case in ("fused_negated", "fused_all_negated") else orc.PROMOTE_AUTO
+    lites = [orc.Lite.from_sorted_ids(np.asarray(l, dtype=np.uint32)) for l in logicals]
+    gs, os_ = [], []
+    for lt in lites:
+        want = orc.upload_packed(lt, U, thr, gpu.device_l2_bytes())
+        src, comp = (lt.flip(0, U), True) if lt.cardinality() > U // 2 else (lt, False)
+        gs.append(gpu.upload_containers(src.containers(), U, comp, lt.cardinality(), thr))
+        os_.append(want)
+        assert_same(gpu.download(gs[-1]), want, strict=True, what="multi_and input")
+    want = orc.multi_and(os_)
+    g = gpu.multi_and(gs)
+    assert_same(gpu.download(g), want, strict=True, what=f"multi_and {case}")
+    for x in gs + [g]:
+        gpu.free(x)
+
+
+# ---- point queries ------------------------------------------------------------
+QUERY_CASES = [("ids", 1 << 24, 0.01), ("ids", 1 << 24, 0.6), ("keep", 1 << 22, 0.001), ("keep", 1 << 22, 0.3),
+               ("runs", 1 << 20, 0.0), ("bitset_neg", 1 << 21, 0.8), ("empty", 1 << 20, 0.0),
+               ("small", 5000, 0.1)]
+
+
+@pytest.mark.parametrize("layout,universe,density", QUERY_CASES)
+@pytest.mark.parametrize("mode", [0, 1])
+def test_contains_parity(gpu, layout, universe, density, mode):
+    _say("contains", layout, universe, density, mode)
+    torch = _torch()
+    rng = np.random.default_rng(int(universe * 7 + density * 1000))
+    ids = np.nonzero(rng.random(universe) < density)[0].astype(np.uint32)
+    if layout == "ids":
+        g, want = gpu.upload_from_ids(ids, universe), orc.upload_from_ids(ids, universe)
+    elif layout == "keep":
+        lt = orc.Lite.from_sorted_ids(ids)
+        g = gpu.upload_containers(lt.containers(), universe, False, lt.cardinality(), orc.PROMOTE_KEEP_DEFAULT)
+        want = orc.upload_packed(lt, universe, orc.PROMOTE_KEEP_DEFAULT)
+    elif layout == "runs":
+        ids = np.concatenate([np.arange(1000, 5000), np.arange(70000, 80000), np.arange(200000, 262144)]).astype(np.uint32)
+        lt = orc.Lite.from_sorted_ids(ids).run_optimize()
+        g = gpu.upload_containers(lt.containers(), 0, False, 0, orc.PROMOTE_KEEP_DEFAULT)
+        want = orc.upload_packed(lt, None, orc.PROMOTE_KEEP_DEFAULT)
+    elif layout == "bitset_neg":
+        w = flat_from_ids(ids, universe)
+        g, want = gpu.upload_from_bitset(w, universe), orc.upload_from_bitset(w, universe)
+    elif layout == "empty":
+        lt = orc.Lite.from_sorted_ids(np.zeros(0, np.uint32))
+        g = gpu.upload_containers([], 0, False, 0, orc.PROMOTE_AUTO)
+        want = orc.upload_packed(lt, None)
+    else:
+        g, want = gpu.upload_from_ids(ids, universe, orc.PROMOTE_KEEP_DEFAULT), orc.upload_from_ids(ids, universe, orc.PROMOTE_KEEP_DEFAULT)
+    # uniform queries over 2x the universe, plus a clustered sorted block
+    q = np.concatenate([rng.integers(0, 2 * max(universe, 1), 200000, dtype=np.uint64).astype(np.uint32),
+                        np.sort(rng.integers(0, 65536, 8192, dtype=np.uint32)) + (universe // 2 & ~0xFFFF)])
+    dq = _dev_u32(q)
+    out = torch.empty_like(dq)
+    gpu.contains_batch(g, dq, out, mode)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint32)
+    assert np.array_equal(got, orc.contains_many(want, q))
+    gpu.free(g)
