@@ -1,0 +1,303 @@
+#!/usr/bin/env python3
+"""Benchmark: upload_from_ids of 100M unsorted uint32 ids over U = 2^30 on one MI355X.
+
+BASELINE.json configs[1] (the metric "upload ms @100M IDs"): 90M distinct
+uniform ids plus 10M duplicates drawn from them, shuffled, already resident in
+HBM; one step = one upload_from_device_ids() call (all kernels, its host
+sync(s) and the allocation of the result) plus the stream-ordered free.
+
+Also reported (extra fields, measured in the same run):
+  roofline      the dominant kernel of the step: algorithmic bytes per launch /
+                its mean launch time from HIP events recorded inside the library
+                on the library's stream during the timed steps;
+  pipeline      the whole device-resident upload against the path's algorithmic
+                bytes B = 4N + 8192 n_c + 9 n_c + 2 (max_key + 1);
+  cpu_baseline  the CPU port (oracle/ orc_upload_from_ids: sort, unique, build)
+                on a 10M-id sample, scaled x10, 1 thread;
+  secondary     set_operation AND of two 50% all-bitmap 2^30 bitmaps (GB/s of
+                algorithmic bytes) and point queries (Gq/s) on a 10% 2^30 bitmap,
+                cold (512 MiB flush before each timed call).
+
+--gpus N with N > 1 exits: this build measures one GPU only.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "cu-roaring-bitmap_amd", "python"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+HBM_PEAK_GBS = 8000.0
+U = 1 << 30
+N_IDS = 100_000_000
+N_DISTINCT = 90_000_000
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def bijective30(i, seed):
+    """A permutation of [0, 2^30): xorshift-multiply rounds on 30-bit values (each step is invertible)."""
+    import torch
+    m = (1 << 30) - 1
+    x = (i + seed) & m
+    x = x ^ (x >> 15)
+    x = (x * 0x2C1B3C6D) & m
+    x = x ^ (x >> 13)
+    x = (x * 0x297A2D39) & m
+    x = x ^ (x >> 16)
+    return x
+
+
+def make_ids(torch, seed=10):
+    dev = "cuda"
+    i = torch.arange(N_DISTINCT, device=dev, dtype=torch.int64)
+    distinct = bijective30(i, seed)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 1)
+    dup = distinct[torch.randint(0, N_DISTINCT, (N_IDS - N_DISTINCT,), device=dev, generator=g)]
+    ids = torch.cat([distinct, dup])
+    g.manual_seed(seed + 2)
+    ids = ids[torch.randperm(N_IDS, device=dev, generator=g)]
+    return ids.to(torch.int32).contiguous()
+
+
+def upload_kernel_bytes(name, n, n_c, max_key):
+    """Algorithmic bytes per launch of each upload kernel."""
+    return {
+        "ids_hist": 4 * n,                          # read every id once
+        "ids_partition": 8 * n,                     # read every id, write it once into its bucket
+        "ids_build": 4 * n + 8192 * n_c + 2 * n_c,  # read partitioned ids, write containers + cards
+    }.get(name)
+
+
+def median(xs):
+    xs = sorted(xs)
+    return xs[len(xs) // 2]
+
+
+def cold_time(torch, fn, iters, flush):
+    """Median ms of fn() with the 256 MB Infinity Cache flushed before each call."""
+    ts = []
+    for _ in range(iters):
+        flush.add_(1)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    return median(ts)
+
+
+def secondary(torch, cr, flush):
+    out = {}
+    # ---- set_operation AND, two 50% all-bitmap bitmaps over 2^30 (config 3, B x B') ----
+    import numpy as np
+    conts = []
+    for seed in (32, 33):
+        r = np.random.default_rng(seed)
+        words = r.integers(0, np.iinfo(np.uint64).max, size=(16384, 1024), dtype=np.uint64, endpoint=True)
+        cards = np.bitwise_count(words).sum(axis=1, dtype=np.int64)
+        conts.append([(k, cr.TC_BITSET, int(cards[k]), words[k]) for k in range(16384)])
+    a = cr.upload_containers(conts[0], 0, False, 0, cr.PROMOTE_KEEP_DEFAULT)
+    b = cr.upload_containers(conts[1], 0, False, 0, cr.PROMOTE_KEEP_DEFAULT)
+    del conts
+    n_c = 16384
+    setop_bytes = 3 * 8192 * n_c + 9 * 3 * n_c  # 2 inputs + 1 output container each, 9 B metadata in and out
+    for _ in range(3):
+        r = cr.set_operation(a, b, cr.AND)
+        cr.free(r)
+    cr.timing_enable(True)
+    ms = []
+
+    def one():
+        r = cr.set_operation(a, b, cr.AND)
+        ms.append(r)
+    t_api = cold_time(torch, one, 10, flush)
+    rep = cr.timing_report()
+    cr.timing_enable(False)
+    assert ms[0].n_containers == n_c and ms[0].n_bitmap_containers == n_c
+    for r in ms:
+        cr.free(r)
+    kn, kms = rep.get("so_exec", (1, float("nan")))
+    k_avg = kms / kn
+    out["set_op_and_50pct_2^30"] = {
+        "algorithmic_bytes": setop_bytes,
+        "api_ms": round(t_api, 4), "api_GBps": round(setop_bytes / t_api / 1e6, 1),
+        "so_exec_ms": round(k_avg, 4), "so_exec_GBps": round(setop_bytes / k_avg / 1e6, 1),
+        "so_exec_frac_of_hbm_peak": round(setop_bytes / k_avg / 1e6 / HBM_PEAK_GBS, 4),
+        "kernels_ms": {k: round(v[1] / v[0], 4) for k, v in rep.items()},
+        "cold": True,
+    }
+    cr.free(a)
+    cr.free(b)
+    log("set op done", out["set_op_and_50pct_2^30"]["so_exec_GBps"], "GB/s kernel")
+
+    # ---- point queries on a 10% all-bitmap 2^30 bitmap (config 4) ----
+    n_set = int(0.1 * U)
+    ids = bijective30(torch.arange(n_set, device="cuda", dtype=torch.int64), 40).to(torch.int32)
+    bm = cr.upload_from_device_ids(ids, U)
+    del ids
+    nq = 100_000_000
+    g = torch.Generator(device="cuda")
+    g.manual_seed(44)
+    q_uni = torch.randint(0, U, (nq,), device="cuda", generator=g, dtype=torch.int64).to(torch.int32)
+    win = torch.randint(0, U >> 16, (nq // 4096,), device="cuda", generator=g, dtype=torch.int64)
+    off = torch.randint(0, 65536, (nq // 4096, 4096), device="cuda", generator=g, dtype=torch.int64)
+    q_clu = ((win[:, None] << 16) + off.sort(dim=1).values).reshape(-1).to(torch.int32)
+    res = torch.empty(nq, device="cuda", dtype=torch.int32)
+    q = {}
+    for qname, qq in (("uniform", q_uni), ("clustered", q_clu)):
+        for mname, mode in (("contains", cr.QUERY_CONTAINS), ("wavefront_contains", cr.QUERY_WAVEFRONT)):
+            cr.contains_batch(bm, qq, res, mode)
+            torch.cuda.synchronize()
+            t = cold_time(torch, lambda: cr.contains_batch(bm, qq, res, mode), 5, flush)
+            nqq = qq.numel()
+            q[f"{mname}_{qname}_Gqps"] = round(nqq / t / 1e6, 2)
+            q[f"{mname}_{qname}_frac_hbm_18B"] = round(18 * nqq / t / 1e6 / HBM_PEAK_GBS, 4)
+    # correctness at full size: every set id answers 1 (sample)
+    chk = bijective30(torch.arange(0, n_set, 997, device="cuda", dtype=torch.int64), 40).to(torch.int32)
+    cres = torch.empty_like(chk)
+    cr.contains_batch(bm, chk, cres, cr.QUERY_WAVEFRONT)
+    torch.cuda.synchronize()
+    assert bool((cres == 1).all()), "point query property check failed"
+    q["bitmap"] = "10% of 2^30 ids (all-bitmap, 16384 containers)"
+    q["queries"] = nq
+    out["contains_10pct_2^30"] = q
+    cr.free(bm)
+    log("queries done", q)
+    return out
+
+
+def cpu_baseline(ids_host_sample):
+    import ctypes as C
+
+    import numpy as np
+    import orc
+    lib = orc.lib()
+    c = orc._OrcRoaring()
+    s = np.ascontiguousarray(ids_host_sample, dtype=np.uint32)
+    t0 = time.perf_counter()
+    rc = lib.orc_upload_from_ids(s.ctypes.data, s.size, U, orc.PROMOTE_AUTO, orc.DEFAULT_L2, C.byref(c))
+    dt = time.perf_counter() - t0
+    assert rc == 0
+    lib.orc_free(C.byref(c))
+    return dt * 1e3 * (N_IDS / s.size)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the sharded design is "
+              f"described, not run, in this build.", file=sys.stderr)
+        sys.exit(2)
+    rank = int(os.environ.get("RANK", "0"))
+
+    import torch
+
+    import curoaring as cr
+    cr.load()
+    torch.cuda.set_device(0)
+    log("generating ids")
+    d_ids = make_ids(torch)
+    torch.cuda.synchronize()
+    flush = torch.zeros(512 << 20, dtype=torch.uint8, device="cuda")
+
+    for _ in range(args.warmup):
+        g = cr.upload_from_device_ids(d_ids, U)
+        cr.free_async(g)
+    torch.cuda.synchronize()
+    log("warmup done")
+
+    cr.timing_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    last = None
+    for k in range(args.steps):
+        g = cr.upload_from_device_ids(d_ids, U)
+        if k == args.steps - 1:
+            last = g
+        else:
+            cr.free_async(g)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    rep = cr.timing_report()
+    cr.timing_enable(False)
+    ms_per_step = elapsed * 1e3 / args.steps
+    n_c = last.n_containers
+    total = last.total_cardinality
+    ok = (n_c == 16384 and total == N_DISTINCT and not last.negated and last.max_key == 16383)
+    cr.free(last)
+    if not ok:
+        log("PROPERTY CHECK FAILED", n_c, total)
+        sys.exit(1)
+    log("timed steps done", round(ms_per_step, 4), "ms/step")
+
+    per_kernel = {k: v[1] / v[0] for k, v in rep.items()}
+    dev_ms = sum(v[1] for v in rep.values()) / args.steps
+    dom = max(("ids_hist", "ids_partition", "ids_build"), key=lambda k: per_kernel.get(k, 0.0))
+    dom_bytes = upload_kernel_bytes(dom, N_IDS, n_c, 16383)
+    dom_ms = per_kernel[dom]
+    achieved = dom_bytes / dom_ms / 1e6
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_upload_ids.json")
+    if os.path.exists(tpath):
+        try:
+            traffic = json.load(open(tpath)).get(dom)
+        except Exception:
+            traffic = None
+    path_bytes = 4 * N_IDS + 8192 * n_c + 9 * n_c + 2 * (16383 + 1)
+
+    result = {
+        "metric": "upload ms @100M IDs",
+        "value": round(ms_per_step, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u32",
+        "data": "synthetic: 90M distinct pseudo-random ids (bijective 30-bit hash) + 10M duplicates, shuffled, "
+                "device-resident",
+        "config": {"workload": "upload_from_ids, 100M unsorted u32 ids (~10% duplicates), universe 2^30, "
+                               "PROMOTE_AUTO (BASELINE configs[1], uniform variant)",
+                   "universe": U, "n_ids": N_IDS, "distinct": N_DISTINCT, "parallelism": "single GPU"},
+        "ids_per_s": round(N_IDS / (ms_per_step / 1e3), 1),
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": dom_bytes, "mean_launch_ms": round(dom_ms, 5)},
+        "pipeline": {"algorithmic_bytes": path_bytes, "device_ms": round(dev_ms, 4),
+                     "achieved_GBps": round(path_bytes / dev_ms / 1e6, 1),
+                     "frac": round(path_bytes / dev_ms / 1e6 / HBM_PEAK_GBS, 4),
+                     "kernels_ms": {k: round(v, 5) for k, v in per_kernel.items()}},
+    }
+    if rank == 0 and not args.no_cpu:
+        log("cpu baseline (10M-id sample)")
+        sample = d_ids[:10_000_000].cpu().numpy().view("uint32")
+        cms = cpu_baseline(sample)
+        result["cpu_baseline"] = {"value": round(cms, 1), "unit": "ms", "cores": 1, "kind": "port",
+                                  "sample": "orc_upload_from_ids (qsort + unique + bitmap build, the reference's "
+                                            "sort/unique/build pipeline on the CPU) on the first 10M of the 100M "
+                                            "ids, scaled x10"}
+    if not args.no_secondary:
+        del d_ids
+        torch.cuda.empty_cache()
+        result["secondary"] = secondary(torch, cr, flush)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

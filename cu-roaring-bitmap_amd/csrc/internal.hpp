@@ -191,6 +191,19 @@ __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, uint64_t n);
 int fill_u16(uint16_t* p, uint16_t v, uint64_t n, hipStream_t s);
 int fill_u32(uint32_t* p, uint32_t v, uint64_t n, hipStream_t s);
 
+// ---- per-kernel timing (off unless cr_timing_enable(1)) ---------------------
+// Each timed launch records a hipEvent pair on its own stream; cr_timing_report
+// synchronises the events and returns per-kernel launch counts and milliseconds.
+extern bool g_timing_on;
+struct TimedLaunch {
+    const char* name;
+    hipStream_t stream;
+    hipEvent_t start = nullptr;
+    TimedLaunch(const char* n, hipStream_t s);
+    ~TimedLaunch();
+};
+#define CR_TIMED(name, stream) ::crimpl::TimedLaunch cr_timed_launch__(name, stream)
+
 uint64_t device_l2_bytes(int device);
 // Compute units of the current device (cached per device).
 uint32_t num_cus();

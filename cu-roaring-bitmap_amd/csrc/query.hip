@@ -92,12 +92,15 @@ extern "C" int cr_contains_batch(const cr_gpu_roaring_view* view, const uint32_t
     const uint64_t per_block = static_cast<uint64_t>(Q_NT) * QPT;
     const unsigned grid = static_cast<unsigned>(
         std::max<uint64_t>(1, std::min<uint64_t>((n + per_block - 1) / per_block, static_cast<uint64_t>(cus) * 16u)));
-    if (v.all_bitmap && mode == CR_QUERY_CONTAINS) {
-        contains_allbitmap<<<grid, Q_NT, 0, s>>>(v, d_ids, n, d_out);
-    } else if (mode == CR_QUERY_WAVEFRONT) {
-        contains_general<CR_QUERY_WAVEFRONT><<<grid, Q_NT, 0, s>>>(v, d_ids, n, d_out);
-    } else {
-        contains_general<CR_QUERY_CONTAINS><<<grid, Q_NT, 0, s>>>(v, d_ids, n, d_out);
+    {
+        CR_TIMED("contains", s);
+        if (v.all_bitmap && mode == CR_QUERY_CONTAINS) {
+            contains_allbitmap<<<grid, Q_NT, 0, s>>>(v, d_ids, n, d_out);
+        } else if (mode == CR_QUERY_WAVEFRONT) {
+            contains_general<CR_QUERY_WAVEFRONT><<<grid, Q_NT, 0, s>>>(v, d_ids, n, d_out);
+        } else {
+            contains_general<CR_QUERY_CONTAINS><<<grid, Q_NT, 0, s>>>(v, d_ids, n, d_out);
+        }
     }
     CR_LAUNCH_CHECK();
     return CR_OK;

@@ -1,8 +1,10 @@
 // Runtime pieces shared by every entry point: error state, allocation of
 // packed result blocks, free, AUTO threshold, and small utility entry points.
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "internal.hpp"
 
@@ -135,6 +137,38 @@ int fill_u32(uint32_t* p, uint32_t v, uint64_t n, hipStream_t s)
     return CR_OK;
 }
 
+bool g_timing_on = false;
+
+struct TimingRec {
+    std::string name;
+    hipEvent_t start, stop;
+};
+static std::mutex g_timing_mu;
+static std::vector<TimingRec> g_timing_recs;
+
+TimedLaunch::TimedLaunch(const char* n, hipStream_t s) : name(n), stream(s)
+{
+    if (!g_timing_on) return;
+    if (hipEventCreate(&start) != hipSuccess) {
+        start = nullptr;
+        return;
+    }
+    (void)hipEventRecord(start, s);
+}
+
+TimedLaunch::~TimedLaunch()
+{
+    if (!start) return;
+    hipEvent_t stop = nullptr;
+    if (hipEventCreate(&stop) != hipSuccess) {
+        (void)hipEventDestroy(start);
+        return;
+    }
+    (void)hipEventRecord(stop, stream);
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    g_timing_recs.push_back(TimingRec{name, start, stop});
+}
+
 uint32_t num_cus()
 {
     static int cache[64] = {};
@@ -257,6 +291,46 @@ int cr_memcpy_d2h(void* dst, const void* src, size_t bytes)
 int cr_stream_synchronize(cr_stream_t stream)
 {
     CR_HIP_RET(hipStreamSynchronize(as_stream(stream)));
+    return CR_OK;
+}
+
+int cr_timing_enable(int on)
+{
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    for (auto& r : g_timing_recs) {
+        (void)hipEventDestroy(r.start);
+        (void)hipEventDestroy(r.stop);
+    }
+    g_timing_recs.clear();
+    g_timing_on = on != 0;
+    return CR_OK;
+}
+
+int cr_timing_report(char* buf, size_t cap)
+{
+    if (!buf || cap == 0) return CR_ERR_INVALID;
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    std::vector<std::pair<std::string, std::pair<uint64_t, double>>> agg;
+    for (auto& r : g_timing_recs) {
+        CR_HIP_RET(hipEventSynchronize(r.stop));
+        float ms = 0.f;
+        CR_HIP_RET(hipEventElapsedTime(&ms, r.start, r.stop));
+        auto it = std::find_if(agg.begin(), agg.end(), [&](auto& a) { return a.first == r.name; });
+        if (it == agg.end()) {
+            agg.push_back({r.name, {1, ms}});
+        } else {
+            it->second.first += 1;
+            it->second.second += ms;
+        }
+    }
+    std::string out;
+    char line[256];
+    for (auto& a : agg) {
+        snprintf(line, sizeof(line), "%s %llu %.6f\n", a.first.c_str(), static_cast<unsigned long long>(a.second.first),
+                 a.second.second);
+        out += line;
+    }
+    snprintf(buf, cap, "%s", out.c_str());
     return CR_OK;
 }
 

@@ -588,9 +588,15 @@ int set_operation_impl(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_
     uint32_t* tile_keep = sc.at<uint32_t>(o_tile);
 
     const Side A = side_of(a), B = side_of(b);
-    so_plan_classify<<<PLAN_GROUPS, PLAN_NT, 0, s>>>(A, B, op, recs, gc);
+    {
+        CR_TIMED("so_plan_classify", s);
+        so_plan_classify<<<PLAN_GROUPS, PLAN_NT, 0, s>>>(A, B, op, recs, gc);
+    }
     CR_LAUNCH_CHECK();
-    so_plan_assign<<<PLAN_GROUPS, PLAN_NT, 0, s>>>(recs, gc, items, tot, tile_keep, n_tiles);
+    {
+        CR_TIMED("so_plan_assign", s);
+        so_plan_assign<<<PLAN_GROUPS, PLAN_NT, 0, s>>>(recs, gc, items, tot, tile_keep, n_tiles);
+    }
     CR_LAUNCH_CHECK();
     Totals h{};
     CR_HIP_RET(hipMemcpyAsync(&h, tot, sizeof(Totals), hipMemcpyDeviceToHost, s));
@@ -610,27 +616,33 @@ int set_operation_impl(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_
     out->run_pool_bytes = static_cast<uint32_t>(run_u16 * 2);
 
     const unsigned g = exec_grid(n_items);
-    switch (op) {
-    case CR_AND:
-        so_exec<CR_AND><<<g, EXEC_NT, 0, s>>>(A, B, items, tot, out->bitmap_data, out->array_data, out->run_data,
-                                              icard, tile_keep);
-        break;
-    case CR_OR:
-        so_exec<CR_OR><<<g, EXEC_NT, 0, s>>>(A, B, items, tot, out->bitmap_data, out->array_data, out->run_data,
-                                             icard, tile_keep);
-        break;
-    case CR_ANDNOT:
-        so_exec<CR_ANDNOT><<<g, EXEC_NT, 0, s>>>(A, B, items, tot, out->bitmap_data, out->array_data,
-                                                 out->run_data, icard, tile_keep);
-        break;
-    default:
-        so_exec<CR_XOR><<<g, EXEC_NT, 0, s>>>(A, B, items, tot, out->bitmap_data, out->array_data, out->run_data,
-                                              icard, tile_keep);
-        break;
+    {
+        CR_TIMED("so_exec", s);
+        switch (op) {
+        case CR_AND:
+            so_exec<CR_AND><<<g, EXEC_NT, 0, s>>>(A, B, items, tot, out->bitmap_data, out->array_data, out->run_data,
+                                                  icard, tile_keep);
+            break;
+        case CR_OR:
+            so_exec<CR_OR><<<g, EXEC_NT, 0, s>>>(A, B, items, tot, out->bitmap_data, out->array_data, out->run_data,
+                                                 icard, tile_keep);
+            break;
+        case CR_ANDNOT:
+            so_exec<CR_ANDNOT><<<g, EXEC_NT, 0, s>>>(A, B, items, tot, out->bitmap_data, out->array_data,
+                                                     out->run_data, icard, tile_keep);
+            break;
+        default:
+            so_exec<CR_XOR><<<g, EXEC_NT, 0, s>>>(A, B, items, tot, out->bitmap_data, out->array_data, out->run_data,
+                                                  icard, tile_keep);
+            break;
+        }
     }
     CR_LAUNCH_CHECK();
-    so_compact<<<(n_items + PLAN_NT - 1) / PLAN_NT, PLAN_NT, 0, s>>>(items, icard, tile_keep, tot, out->keys,
-                                                                     out->types, out->offsets, out->cardinalities);
+    {
+        CR_TIMED("so_compact", s);
+        so_compact<<<(n_items + PLAN_NT - 1) / PLAN_NT, PLAN_NT, 0, s>>>(items, icard, tile_keep, tot, out->keys,
+                                                                         out->types, out->offsets, out->cardinalities);
+    }
     CR_LAUNCH_CHECK();
     uint32_t n_out = 0;
     CR_HIP_RET(hipMemcpyAsync(&n_out, &tot->n_out, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
@@ -808,7 +820,10 @@ static int fused_multi_and(const cr_gpu_roaring* in, uint32_t count, hipStream_t
     CR_RET(sc.alloc(c.total, s));
     uint16_t* common = sc.at<uint16_t>(o_common);
     uint32_t* cnt = sc.at<uint32_t>(o_cnt);  // [0] n_common, [1] total cardinality
-    mand_keys<<<1, 1024, 0, s>>>(args, mkp1, common, cnt);
+    {
+        CR_TIMED("mand_keys", s);
+        mand_keys<<<1, 1024, 0, s>>>(args, mkp1, common, cnt);
+    }
     CR_LAUNCH_CHECK();
     CR_RET(fill_u32(cnt + 1, 0u, 1, s));
     uint32_t n_common = 0;
@@ -824,9 +839,12 @@ static int fused_multi_and(const cr_gpu_roaring* in, uint32_t count, hipStream_t
     CR_RET(alloc_out(out, L, n_common, kidx_len, static_cast<uint64_t>(n_common) * 1024u, 0, 0, s));
     out->max_key = max_key;
     CR_RET(fill_u16(out->key_index, 0xFFFFu, kidx_len, s));
-    mand_and<<<exec_grid(n_common), EXEC_NT, 0, s>>>(args, common, cnt, out->bitmap_data, out->keys, out->types,
-                                                     out->offsets, out->cardinalities, out->key_index,
-                                                     static_cast<uint32_t>(kidx_len), cnt + 1);
+    {
+        CR_TIMED("mand_and", s);
+        mand_and<<<exec_grid(n_common), EXEC_NT, 0, s>>>(args, common, cnt, out->bitmap_data, out->keys, out->types,
+                                                         out->offsets, out->cardinalities, out->key_index,
+                                                         static_cast<uint32_t>(kidx_len), cnt + 1);
+    }
     CR_LAUNCH_CHECK();
     uint32_t total = 0;
     CR_HIP_RET(hipMemcpyAsync(&total, cnt + 1, sizeof(uint32_t), hipMemcpyDeviceToHost, s));

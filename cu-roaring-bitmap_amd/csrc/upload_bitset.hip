@@ -191,12 +191,21 @@ int upload_from_device_bitset_impl(const uint32_t* d_words, uint32_t n_words, ui
     const OutLayout L = plan_out(g.n_chunks, g.n_chunks, static_cast<uint64_t>(g.n_chunks) * 1024u, 0, 0);
     CR_RET(alloc_out(out, L, g.n_chunks, g.n_chunks, static_cast<uint64_t>(g.n_chunks) * 1024u, 0, 0, s));
 
-    bs_count<<<grid_cap(g.n_chunks), BS_NT, 0, s>>>(d_words, g, pc, pci);
+    {
+        CR_TIMED("bs_count", s);
+        bs_count<<<grid_cap(g.n_chunks), BS_NT, 0, s>>>(d_words, g, pc, pci);
+    }
     CR_LAUNCH_CHECK();
-    bs_plan<<<1, 1024, 0, s>>>(g, pc, pci, cmap, out->keys, out->types, out->offsets, out->cardinalities,
-                               out->key_index, tot);
+    {
+        CR_TIMED("bs_plan", s);
+        bs_plan<<<1, 1024, 0, s>>>(g, pc, pci, cmap, out->keys, out->types, out->offsets, out->cardinalities,
+                                   out->key_index, tot);
+    }
     CR_LAUNCH_CHECK();
-    bs_compact<<<grid_cap(g.n_chunks), BS_NT, 0, s>>>(d_words, g, cmap, tot, out->bitmap_data);
+    {
+        CR_TIMED("bs_compact", s);
+        bs_compact<<<grid_cap(g.n_chunks), BS_NT, 0, s>>>(d_words, g, cmap, tot, out->bitmap_data);
+    }
     CR_LAUNCH_CHECK();
     BsTotals h{};
     CR_HIP_RET(hipMemcpyAsync(&h, tot, sizeof(h), hipMemcpyDeviceToHost, s));

@@ -491,7 +491,10 @@ static int small_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, ui
     Scratch sc;
     CR_RET(sc.alloc(sizeof(SmallPlan), s));
     SmallPlan* plan = sc.at<SmallPlan>(0);
-    ids_small_plan<<<1, 1024, 0, s>>>(d_ids, n, universe, thr, plan);
+    {
+        CR_TIMED("ids_small_plan", s);
+        ids_small_plan<<<1, 1024, 0, s>>>(d_ids, n, universe, thr, plan);
+    }
     CR_LAUNCH_CHECK();
     uint32_t hdr[8];
     CR_HIP_RET(hipMemcpyAsync(hdr, plan, sizeof(hdr), hipMemcpyDeviceToHost, s));
@@ -510,9 +513,12 @@ static int small_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, ui
     out->n_array_containers = n_array;
     out->array_pool_bytes = arr_elems ? arr_elems * 2u : 0u;
     out->max_key = max_key;
-    ids_small_write<<<1, 1024, 0, s>>>(plan, thr, out->keys, out->types, out->offsets, out->cardinalities,
-                                       out->bitmap_data, out->array_data, out->key_index,
-                                       static_cast<uint32_t>(kidx_len));
+    {
+        CR_TIMED("ids_small_write", s);
+        ids_small_write<<<1, 1024, 0, s>>>(plan, thr, out->keys, out->types, out->offsets, out->cardinalities,
+                                           out->bitmap_data, out->array_data, out->key_index,
+                                           static_cast<uint32_t>(kidx_len));
+    }
     CR_LAUNCH_CHECK();
     CR_HIP_RET(hipStreamSynchronize(s));
     return CR_OK;
@@ -565,17 +571,32 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     out->max_key = max_key32;
 
     CR_RET(fill_u32(reinterpret_cast<uint32_t*>(tot), 0u, sizeof(IdsTotals) / 4, s));
-    ids_hist<<<g.G, HP_NT, 0, s>>>(d_ids, g, ghist, gpres, tot);
+    {
+        CR_TIMED("ids_hist", s);
+        ids_hist<<<g.G, HP_NT, 0, s>>>(d_ids, g, ghist, gpres, tot);
+    }
     CR_LAUNCH_CHECK();
     const uint32_t cols = g.NB + g.NW;
-    ids_colscan<<<(cols + 15) / 16, 1024, 0, s>>>(g, ghist, gpres, btotal, pres);
+    {
+        CR_TIMED("ids_colscan", s);
+        ids_colscan<<<(cols + 15) / 16, 1024, 0, s>>>(g, ghist, gpres, btotal, pres);
+    }
     CR_LAUNCH_CHECK();
-    ids_keyscan<<<1, 1024, 0, s>>>(g, btotal, pres, bbase, out->keys, out->types, out->offsets, out->key_index, tot);
+    {
+        CR_TIMED("ids_keyscan", s);
+        ids_keyscan<<<1, 1024, 0, s>>>(g, btotal, pres, bbase, out->keys, out->types, out->offsets, out->key_index, tot);
+    }
     CR_LAUNCH_CHECK();
-    ids_partition<<<g.G, HP_NT, 0, s>>>(d_ids, g, ghist, bbase, part);
+    {
+        CR_TIMED("ids_partition", s);
+        ids_partition<<<g.G, HP_NT, 0, s>>>(d_ids, g, ghist, bbase, part);
+    }
     CR_LAUNCH_CHECK();
-    ids_build<<<g.NB, BUILD_NT, 0, s>>>(part, bbase, btotal, g, universe, false, out->key_index,
-                                                out->bitmap_data, out->cardinalities, key_count, tot);
+    {
+        CR_TIMED("ids_build", s);
+        ids_build<<<g.NB, BUILD_NT, 0, s>>>(part, bbase, btotal, g, universe, false, out->key_index,
+                                                    out->bitmap_data, out->cardinalities, key_count, tot);
+    }
     CR_LAUNCH_CHECK();
     IdsTotals h{};
     CR_HIP_RET(hipMemcpyAsync(&h, tot, sizeof(h), hipMemcpyDeviceToHost, s));
@@ -602,11 +623,17 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     reset(&comp);
     const OutLayout L2 = plan_out(g.K, g.K, static_cast<uint64_t>(g.K) * 1024u, 0, 0);
     CR_RET(alloc_out(&comp, L2, g.K, g.K, static_cast<uint64_t>(g.K) * 1024u, 0, 0, s));
-    ids_keyscan_complement<<<1, 1024, 0, s>>>(g, universe, key_count, comp.keys, comp.types, comp.offsets,
-                                              comp.key_index, tot);
+    {
+        CR_TIMED("ids_keyscan_complement", s);
+        ids_keyscan_complement<<<1, 1024, 0, s>>>(g, universe, key_count, comp.keys, comp.types, comp.offsets,
+                                                  comp.key_index, tot);
+    }
     CR_LAUNCH_CHECK();
-    ids_build<<<g.NB, BUILD_NT, 0, s>>>(part, bbase, btotal, g, universe, true, comp.key_index,
-                                                comp.bitmap_data, comp.cardinalities, nullptr, tot);
+    {
+        CR_TIMED("ids_build", s);
+        ids_build<<<g.NB, BUILD_NT, 0, s>>>(part, bbase, btotal, g, universe, true, comp.key_index,
+                                                    comp.bitmap_data, comp.cardinalities, nullptr, tot);
+    }
     CR_LAUNCH_CHECK();
     CR_HIP_RET(hipMemcpyAsync(&h, tot, sizeof(h), hipMemcpyDeviceToHost, s));
     CR_HIP_RET(hipStreamSynchronize(s));

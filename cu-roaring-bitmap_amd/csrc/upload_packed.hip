@@ -218,8 +218,11 @@ int upload_containers_impl(const cr_host_container* conts, uint32_t n, uint32_t 
         CR_RET(raw.alloc(stage_bytes - raw_off0, s));
         CR_HIP_RET(hipMemcpyAsync(raw.ptr, h + raw_off0, stage_bytes - raw_off0, hipMemcpyHostToDevice, s));
         const ExpandDesc* ddesc = raw.at<ExpandDesc>(desc_off - raw_off0);
-        expand_containers<<<std::min<uint32_t>(n, 4096u), 256, 0, s>>>(ddesc, n, raw.at<uint8_t>(0),
-                                                                        out->bitmap_data);
+        {
+            CR_TIMED("expand_containers", s);
+            expand_containers<<<std::min<uint32_t>(n, 4096u), 256, 0, s>>>(ddesc, n, raw.at<uint8_t>(0),
+                                                                            out->bitmap_data);
+        }
         CR_LAUNCH_CHECK();
         CR_HIP_RET(hipStreamSynchronize(s));
     }

@@ -31,7 +31,7 @@ EXPORTS = [
     "cr_upload_from_device_bitset", "cr_upload_containers", "cr_get_meta", "cr_set_operation", "cr_multi_and",
     "cr_free", "cr_free_async", "cr_resolve_auto_threshold", "cr_make_view", "cr_contains_batch",
     "cr_topk_filtered", "cr_device_l2_bytes", "cr_device_malloc", "cr_device_free", "cr_memcpy_h2d",
-    "cr_memcpy_d2h", "cr_stream_synchronize",
+    "cr_memcpy_d2h", "cr_stream_synchronize", "cr_timing_enable", "cr_timing_report",
 ]
 
 
@@ -133,6 +133,8 @@ def load(path: Optional[str] = None):
         "cr_memcpy_h2d": [C.c_void_p, C.c_void_p, C.c_size_t],
         "cr_memcpy_d2h": [C.c_void_p, C.c_void_p, C.c_size_t],
         "cr_stream_synchronize": [C.c_void_p],
+        "cr_timing_enable": [C.c_int],
+        "cr_timing_report": [C.c_char_p, C.c_size_t],
     }
     for name, args in sigs.items():
         f = getattr(L, name)
@@ -281,6 +283,22 @@ def topk_filtered(d_base, d_queries, k: int, filt: Optional[GpuRoaring], d_dist,
 
 def synchronize(stream=None):
     _check(load().cr_stream_synchronize(_stream(stream)), "stream_synchronize")
+
+
+def timing_enable(on: bool = True):
+    """Start (or stop) per-kernel HIP-event timing inside the library; clears records."""
+    _check(load().cr_timing_enable(1 if on else 0), "timing_enable")
+
+
+def timing_report() -> dict:
+    """{kernel_name: (launches, total_ms)} for the launches since timing_enable()."""
+    buf = C.create_string_buffer(1 << 16)
+    _check(load().cr_timing_report(buf, len(buf)), "timing_report")
+    out = {}
+    for line in buf.value.decode().splitlines():
+        name, n, ms = line.split()
+        out[name] = (int(n), float(ms))
+    return out
 
 
 # ---- download to host (canonical comparison) -----------------------------------

@@ -183,6 +183,10 @@ int cr_device_free(void* ptr);
 int cr_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int cr_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int cr_stream_synchronize(cr_stream_t stream);
+/* Per-kernel HIP-event timing: enable (1) / disable (0) and clear the records;
+ * the report is one "kernel_name launches total_ms" line per kernel. */
+int cr_timing_enable(int on);
+int cr_timing_report(char* buf, size_t cap);
 
 #ifdef __cplusplus
 }

@@ -221,6 +221,19 @@ def _from_c(c: _OrcRoaring) -> HostRoaring:
     return r
 
 
+def as_host(r) -> HostRoaring:
+    """Wrap any object with the GpuRoaring host fields (e.g. a downloaded GPU result)."""
+    if isinstance(r, HostRoaring):
+        return r
+    return HostRoaring(keys=r.keys, types=r.types, offsets=r.offsets, cards=r.cards, n_containers=r.n_containers,
+                       universe_size=r.universe_size, total_cardinality=r.total_cardinality,
+                       bitmap_data=r.bitmap_data, n_bitmap_containers=r.n_bitmap_containers,
+                       array_data=r.array_data, n_array_containers=r.n_array_containers,
+                       array_pool_bytes=r.array_pool_bytes, run_data=r.run_data,
+                       n_run_containers=r.n_run_containers, run_pool_bytes=r.run_pool_bytes,
+                       key_index=r.key_index, max_key=r.max_key, negated=bool(r.negated))
+
+
 def _check(rc: int, what: str):
     if rc != 0:
         raise RuntimeError(f"oracle {what} failed with code {rc}")
@@ -264,7 +277,7 @@ def multi_and(inputs) -> HostRoaring:
 def contains_many(r: HostRoaring, ids) -> np.ndarray:
     ids = np.ascontiguousarray(ids, dtype=np.uint32)
     out = np.zeros(ids.size, dtype=np.uint32)
-    lib().orc_contains_many(C.byref(r.as_c()), _ptr(ids), ids.size, _ptr(out))
+    lib().orc_contains_many(C.byref(as_host(r).as_c()), _ptr(ids), ids.size, _ptr(out))
     return out
 
 
@@ -272,12 +285,12 @@ def decompress(r: HostRoaring, n_words: Optional[int] = None) -> np.ndarray:
     if n_words is None:
         n_words = (r.universe_size + 31) // 32
     out = np.zeros(max(n_words, 1), dtype=np.uint32)
-    lib().orc_decompress(C.byref(r.as_c()), _ptr(out), n_words)
+    lib().orc_decompress(C.byref(as_host(r).as_c()), _ptr(out), n_words)
     return out[:n_words]
 
 
 def true_cardinality(r: HostRoaring) -> int:
-    return lib().orc_true_cardinality(C.byref(r.as_c()))
+    return lib().orc_true_cardinality(C.byref(as_host(r).as_c()))
 
 
 # ---- roaring-lite -------------------------------------------------------
