@@ -21,6 +21,10 @@ using cu_roaring::GpuRoaringView;
 constexpr int Q_NT = 256;
 constexpr int QPT = 8;
 
+// WAVE: when every lane of the wave queries the same key, the key_index entry
+// is read once with a wave-uniform (scalar) load -- wavefront_contains'
+// amortisation -- while the QPT queries of a lane stay independent.
+template <bool WAVE>
 __global__ __launch_bounds__(Q_NT) void contains_allbitmap(GpuRoaringView v, const uint32_t* __restrict__ ids,
                                                            uint64_t n, uint32_t* __restrict__ out)
 {
@@ -36,6 +40,14 @@ __global__ __launch_bounds__(Q_NT) void contains_allbitmap(GpuRoaringView v, con
 #pragma unroll
         for (int q = 0; q < QPT; ++q) {
             const uint32_t key = id[q] >> 16;
+            if (WAVE) {
+                const uint32_t k0 = __builtin_amdgcn_readfirstlane(key);
+                if (__ballot(key != k0) == 0ull) {  // wave-uniform key
+                    const uint32_t x = v.key_index[min(k0, v.max_key)];
+                    idx[q] = k0 > v.max_key ? 0xFFFFu : x;
+                    continue;
+                }
+            }
             const uint32_t k = min(key, v.max_key);
             const uint32_t x = v.key_index[k];
             idx[q] = key > v.max_key ? 0xFFFFu : x;
@@ -79,7 +91,7 @@ using namespace crimpl;
 extern "C" int cr_contains_batch(const cr_gpu_roaring_view* view, const uint32_t* d_ids, uint64_t n, uint32_t* d_out,
                                  uint32_t mode, cr_stream_t stream)
 {
-    if (!view || (n && (!d_ids || !d_out)) || mode > CR_QUERY_WAVEFRONT) {
+    if (!view || (n && (!d_ids || !d_out)) || mode > CR_QUERY_CONTAINS_API) {
         set_error("cr_contains_batch: invalid argument");
         return CR_ERR_INVALID;
     }
@@ -95,8 +107,10 @@ extern "C" int cr_contains_batch(const cr_gpu_roaring_view* view, const uint32_t
     {
         CR_TIMED("contains", s);
         if (v.all_bitmap && mode == CR_QUERY_CONTAINS) {
-            contains_allbitmap<<<grid, Q_NT, 0, s>>>(v, d_ids, n, d_out);
-        } else if (mode == CR_QUERY_WAVEFRONT) {
+            contains_allbitmap<false><<<grid, Q_NT, 0, s>>>(v, d_ids, n, d_out);
+        } else if (v.all_bitmap) {
+            contains_allbitmap<true><<<grid, Q_NT, 0, s>>>(v, d_ids, n, d_out);
+        } else if (mode == CR_QUERY_WAVEFRONT || mode == CR_QUERY_WAVEFRONT_API) {
             contains_general<CR_QUERY_WAVEFRONT><<<grid, Q_NT, 0, s>>>(v, d_ids, n, d_out);
         } else {
             contains_general<CR_QUERY_CONTAINS><<<grid, Q_NT, 0, s>>>(v, d_ids, n, d_out);

@@ -22,7 +22,8 @@ struct KeyRec {
     uint8_t cat;
     uint8_t pad[3];
     int32_t ai, bi;
-    uint32_t size;  // array elements or run pairs reserved in the output pool
+    uint32_t size;        // array elements or run pairs reserved in the output pool
+    uint32_t aoff, boff;  // byte offsets of the source containers
 };
 
 // One output container candidate, in key order (plan pass 2).
@@ -31,7 +32,8 @@ struct Item {
     uint8_t cat;
     uint8_t pad;
     int32_t ai, bi;
-    uint32_t slot;  // bitmap slot, or u16 element offset into the array / run pool
+    uint32_t slot;        // bitmap slot, or u16 element offset into the array / run pool
+    uint32_t aoff, boff;  // byte offsets of the source containers (0 when absent)
 };
 
 // Counters accumulated per 1024-key group and totalled over all groups.
@@ -93,6 +95,8 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_classify(Side A, Side B, uint
     KeyRec rec{};
     rec.ai = ai;
     rec.bi = bi;
+    rec.aoff = ai >= 0 ? A.offsets[ai] : 0u;
+    rec.boff = bi >= 0 ? B.offsets[bi] : 0u;
     uint32_t cnt[C_N] = {};
     const bool keep_a_only = op != CR_AND;                 // OR, XOR, ANDNOT copy A-only keys
     const bool keep_b_only = op == CR_OR || op == CR_XOR;  // OR, XOR copy B-only keys
@@ -198,6 +202,8 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_assign(const KeyRec* recs, co
     it.pad = 0;
     it.ai = rec.ai;
     it.bi = rec.bi;
+    it.aoff = rec.aoff;
+    it.boff = rec.boff;
     it.slot = slot;
     items[item_pos] = it;
 }
@@ -311,8 +317,8 @@ __global__ __launch_bounds__(EXEC_NT) void so_exec(Side A, Side B, const Item* i
         bool keep = true;
         switch (it.cat) {
         case CAT_BB: {
-            const uint64_t* pa = A.bmp + (A.offsets[it.ai] >> 3);
-            const uint64_t* pb = B.bmp + (B.offsets[it.bi] >> 3);
+            const uint64_t* pa = A.bmp + (it.aoff >> 3);
+            const uint64_t* pb = B.bmp + (it.boff >> 3);
             const uint32_t pc = block_sum<EXEC_NT>(bitmap_op_stream<OP>(pa, pb, out_bmp + it.slot * 1024ull), red);
             card = pc > 65535u ? 0u : pc;  // 65536 stored as 0 (src/set_ops.cu:179-180)
             keep = card != 0 || OP == CR_OR;
@@ -337,8 +343,8 @@ __global__ __launch_bounds__(EXEC_NT) void so_exec(Side A, Side B, const Item* i
         }
         case CAT_BA: {
             const bool bmp_is_a = A.types[it.ai] == CR_BITMAP;
-            const uint64_t* bm = bmp_is_a ? A.bmp + (A.offsets[it.ai] >> 3) : B.bmp + (B.offsets[it.bi] >> 3);
-            const uint16_t* arr = bmp_is_a ? B.arr + (B.offsets[it.bi] >> 1) : A.arr + (A.offsets[it.ai] >> 1);
+            const uint64_t* bm = bmp_is_a ? A.bmp + (it.aoff >> 3) : B.bmp + (it.boff >> 3);
+            const uint16_t* arr = bmp_is_a ? B.arr + (it.boff >> 1) : A.arr + (it.aoff >> 1);
             const uint32_t n = bmp_is_a ? B.cards[it.bi] : A.cards[it.ai];
             uint16_t* out = out_arr + it.slot;
             // Probe in array order and compact in order: output stays sorted.
@@ -359,8 +365,8 @@ __global__ __launch_bounds__(EXEC_NT) void so_exec(Side A, Side B, const Item* i
             break;
         }
         case CAT_AA: {
-            const uint16_t* x = A.arr + (A.offsets[it.ai] >> 1);
-            const uint16_t* y = B.arr + (B.offsets[it.bi] >> 1);
+            const uint16_t* x = A.arr + (it.aoff >> 1);
+            const uint16_t* y = B.arr + (it.boff >> 1);
             uint32_t nx = A.cards[it.ai], ny = B.cards[it.bi];
             // Iterate one side in order and binary-search the other, staged in LDS
             // when it fits (sorted unique arrays: same result as a merge).
@@ -417,10 +423,14 @@ __global__ __launch_bounds__(EXEC_NT) void so_exec(Side A, Side B, const Item* i
             const bool from_a = it.ai >= 0;
             const Side& S = from_a ? A : B;
             const int32_t idx = from_a ? it.ai : it.bi;
-            const uint4* src = reinterpret_cast<const uint4*>(S.bmp + (S.offsets[idx] >> 3));
-            uint4* dst = reinterpret_cast<uint4*>(out_bmp + it.slot * 1024ull);
-            dst[t] = src[t];
-            dst[t + EXEC_NT] = src[t + EXEC_NT];
+            const uint64_t* src = S.bmp + ((from_a ? it.aoff : it.boff) >> 3);
+            uint64_t* dst = out_bmp + it.slot * 1024ull;
+            if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
+                reinterpret_cast<uint4*>(dst)[t] = reinterpret_cast<const uint4*>(src)[t];
+                reinterpret_cast<uint4*>(dst)[t + EXEC_NT] = reinterpret_cast<const uint4*>(src)[t + EXEC_NT];
+            } else {
+                for (uint32_t i = t; i < 1024u; i += EXEC_NT) dst[i] = src[i];
+            }
             card = S.cards[idx];
             break;
         }
@@ -439,10 +449,7 @@ __global__ __launch_bounds__(EXEC_NT) void so_exec(Side A, Side B, const Item* i
         }
         default: break;
         }
-        if (t == 0) {
-            item_card[w] = card | (keep ? 0x80000000u : 0u);
-            if (keep) atomicAdd(&tile_keep[w >> 10], 1u);
-        }
+        if (t == 0) item_card[w] = card | (keep ? 0x80000000u : 0u);
         __syncthreads();
     }
 }
@@ -458,10 +465,11 @@ __global__ __launch_bounds__(PLAN_NT) void so_compact(const Item* items, const u
     const uint32_t tile = blockIdx.x;
     if (tile * PLAN_NT >= n_items) return;
     const uint32_t t = threadIdx.x;
-    if (t == 0) {
+    {  // kept items before this tile, counted cooperatively
         uint32_t b = 0;
-        for (uint32_t i = 0; i < tile; ++i) b += tile_keep[i];
-        s_base = b;
+        for (uint32_t i = t; i < tile * PLAN_NT; i += PLAN_NT) b += item_card[i] >> 31;
+        b = block_sum<PLAN_NT>(b, lds);
+        if (t == 0) s_base = b;
     }
     const uint32_t w = tile * PLAN_NT + t;
     bool keep = false;

@@ -42,7 +42,36 @@ struct IdsGeom {
     uint32_t K;      // keys in the universe (max_key + 1)
     uint32_t NB;     // buckets
     uint32_t NW;     // presence words
+    bool vec;        // ids pointer 16-byte aligned (chunks are multiples of the tile)
 };
+
+// Ids are consumed in tiles of 8 per thread (8192 per workgroup): two 16-byte
+// loads per lane when the tile is whole and 16-byte aligned, else guarded
+// scalar loads.  `valid` marks the loaded slots.
+constexpr uint32_t TILE = 8 * HP_NT;
+
+__device__ __forceinline__ void load_tile(const uint32_t* __restrict__ ids, uint64_t base, uint64_t hi, bool vec,
+                                          uint32_t (&v)[8], uint32_t& valid)
+{
+    const uint32_t t = threadIdx.x;
+    if (vec && base + TILE <= hi) {
+        const uint4 a = reinterpret_cast<const uint4*>(ids + base)[t];
+        const uint4 b = reinterpret_cast<const uint4*>(ids + base + TILE / 2)[t];
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+        valid = 0xFFu;
+        return;
+    }
+    valid = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint64_t i = base + t + static_cast<uint64_t>(j) * HP_NT;
+        v[j] = 0;
+        if (i < hi) {
+            v[j] = ids[i];
+            valid |= 1u << j;
+        }
+    }
+}
 
 __global__ __launch_bounds__(HP_NT) void ids_hist(const uint32_t* __restrict__ ids, IdsGeom g, uint32_t* ghist,
                                                   uint32_t* gpres, IdsTotals* tot)
@@ -62,17 +91,23 @@ __global__ __launch_bounds__(HP_NT) void ids_hist(const uint32_t* __restrict__ i
     const uint64_t hi = min(g.n, lo + g.chunk);
     const uint32_t max_key = g.K - 1;
     uint32_t err = 0, mx = 0;
-    for (uint64_t i = lo + t; i < hi; i += HP_NT) {
-        const uint32_t id = ids[i];
-        const uint32_t key = id >> 16;
-        mx = max(mx, id);
-        if (key > max_key) {
-            err = 1;
-            continue;
+    for (uint64_t base = lo; base < hi; base += TILE) {
+        uint32_t v[8], valid;
+        load_tile(ids, base, hi, g.vec, v, valid);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (!((valid >> j) & 1u)) continue;
+            const uint32_t id = v[j];
+            const uint32_t key = id >> 16;
+            mx = max(mx, id);
+            if (key > max_key) {
+                err = 1;
+                continue;
+            }
+            atomicAdd(&hist[key >> BK_SHIFT], 1u);
+            const uint32_t bit = 1u << (key & 31u);
+            if (!(pres[key >> 5] & bit)) atomicOr(&pres[key >> 5], bit);
         }
-        atomicAdd(&hist[key >> BK_SHIFT], 1u);
-        const uint32_t bit = 1u << (key & 31u);
-        if (!(pres[key >> 5] & bit)) atomicOr(&pres[key >> 5], bit);
     }
     if (err) atomicOr(&s_err, 1u);
     atomicMax(&s_max, mx);
@@ -176,24 +211,65 @@ __global__ __launch_bounds__(1024) void ids_keyscan(IdsGeom g, const uint32_t* b
     }
 }
 
+// Each 8192-id tile is counting-sorted by bucket in LDS first, so the global
+// writes leave as bucket-contiguous runs (consecutive lanes, consecutive
+// addresses) instead of one scattered 4-byte store per id.
 __global__ __launch_bounds__(HP_NT) void ids_partition(const uint32_t* __restrict__ ids, IdsGeom g,
                                                        const uint32_t* ghist_off, const uint32_t* bbase,
                                                        uint32_t* __restrict__ part)
 {
-    __shared__ uint32_t cur[MAX_BUCKETS];
+    __shared__ uint32_t buf[TILE];
+    __shared__ uint32_t cur[MAX_BUCKETS];  // next global position of each bucket
+    __shared__ uint32_t cnt[MAX_BUCKETS];  // ids of the tile per bucket
+    __shared__ uint32_t ofs[MAX_BUCKETS];  // tile-local start of each bucket
+    __shared__ uint32_t lds[16];
     const uint32_t t = threadIdx.x;
     const uint32_t* off = ghist_off + static_cast<uint64_t>(blockIdx.x) * g.NB;
     for (uint32_t i = t; i < g.NB; i += HP_NT) cur[i] = bbase[i] + off[i];
-    __syncthreads();
     const uint64_t lo = static_cast<uint64_t>(blockIdx.x) * g.chunk;
     const uint64_t hi = min(g.n, lo + g.chunk);
     const uint32_t max_key = g.K - 1;
-    for (uint64_t i = lo + t; i < hi; i += HP_NT) {
-        const uint32_t id = ids[i];
-        const uint32_t key = id >> 16;
-        if (key > max_key) continue;
-        const uint32_t pos = atomicAdd(&cur[key >> BK_SHIFT], 1u);
-        part[pos] = id;
+    constexpr uint32_t BPT = MAX_BUCKETS / HP_NT;  // buckets scanned per thread
+    for (uint64_t base = lo; base < hi; base += TILE) {
+        uint32_t v[8], valid, rank[8];
+        load_tile(ids, base, hi, g.vec, v, valid);
+        for (uint32_t i = t; i < g.NB; i += HP_NT) cnt[i] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (((valid >> j) & 1u) && (v[j] >> 16) <= max_key)
+                rank[j] = atomicAdd(&cnt[v[j] >> (16 + BK_SHIFT)], 1u);
+            else
+                valid &= ~(1u << j);
+        }
+        __syncthreads();
+        uint32_t c[BPT], s = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < BPT; ++q) {
+            const uint32_t b = t * BPT + q;
+            c[q] = b < g.NB ? cnt[b] : 0u;
+            s += c[q];
+        }
+        uint32_t tile_n;
+        uint32_t run = block_excl_scan<HP_NT>(s, lds, tile_n);
+#pragma unroll
+        for (uint32_t q = 0; q < BPT; ++q) {
+            const uint32_t b = t * BPT + q;
+            if (b < g.NB) ofs[b] = run;
+            run += c[q];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if ((valid >> j) & 1u) buf[ofs[v[j] >> (16 + BK_SHIFT)] + rank[j]] = v[j];
+        __syncthreads();
+        for (uint32_t p = t; p < tile_n; p += HP_NT) {
+            const uint32_t id = buf[p];
+            const uint32_t b = id >> (16 + BK_SHIFT);
+            part[cur[b] + (p - ofs[b])] = id;
+        }
+        __syncthreads();
+        for (uint32_t i = t; i < g.NB; i += HP_NT) cur[i] += cnt[i];
     }
 }
 
@@ -215,11 +291,26 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
     for (uint32_t i = t; i < BK_KEYS * 2048u; i += BUILD_NT) bits[i] = 0;
     __syncthreads();
     const uint32_t start = bbase[b], cnt = btotal[b];
-    for (uint32_t i = t; i < cnt; i += BUILD_NT) {
-        const uint32_t id = part[start + i];
+    auto set_bit = [&](uint32_t id) {
         const uint32_t local = (((id >> 16) & (BK_KEYS - 1)) << 11) | ((id & 0xFFFFu) >> 5);
         atomicOr(&bits[local], 1u << (id & 31u));
+    };
+    // scalar head up to 16-byte alignment, 16-byte body (two loads in flight), scalar tail
+    const uint32_t head = min(cnt, (4u - (start & 3u)) & 3u);
+    if (t < head) set_bit(part[start + t]);
+    const uint32_t body = (cnt - head) & ~3u;
+    const uint4* p4 = reinterpret_cast<const uint4*>(part + start + head);
+    const uint32_t n4 = body >> 2;
+    for (uint32_t i = t; i < n4; i += 2 * BUILD_NT) {
+        const uint4 x = p4[i];
+        uint4 y = make_uint4(0, 0, 0, 0);
+        const bool has_y = i + BUILD_NT < n4;
+        if (has_y) y = p4[i + BUILD_NT];
+        set_bit(x.x), set_bit(x.y), set_bit(x.z), set_bit(x.w);
+        if (has_y) set_bit(y.x), set_bit(y.y), set_bit(y.z), set_bit(y.w);
     }
+    const uint32_t tail0 = head + body;
+    if (tail0 + t < cnt) set_bit(part[start + tail0 + t]);
     __syncthreads();
     const uint32_t c = t >> 6;  // wave c owns container c of the bucket
     const uint32_t lane = __lane_id();
@@ -248,8 +339,9 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
     }
     if (pc == 0) return;
     const uint32_t rank = key_index[key];
-    uint32_t* dst = reinterpret_cast<uint32_t*>(pool) + static_cast<uint64_t>(rank) * 2048u;
-    for (uint32_t i = lane; i < 2048u; i += 64) dst[i] = cb[i];
+    uint4* dst = reinterpret_cast<uint4*>(pool + static_cast<uint64_t>(rank) * 1024u);
+    const uint4* src = reinterpret_cast<const uint4*>(cb);
+    for (uint32_t i = lane; i < 512u; i += 64) dst[i] = src[i];
     if (lane == 0) {
         cards[rank] = static_cast<uint16_t>(pc > 65535u ? 0u : pc);
         atomicAdd(&tot->total, static_cast<unsigned long long>(pc));
@@ -538,11 +630,14 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     g.NB = (g.K + BK_KEYS - 1) / BK_KEYS;
     g.NW = (g.K + 31) / 32;
     const uint32_t cus = num_cus();
-    const uint64_t min_chunk = 16u * HP_NT;
-    uint64_t G = std::min<uint64_t>(static_cast<uint64_t>(cus), (static_cast<uint64_t>(n) + min_chunk - 1) / min_chunk);
+    // One 1024-lane workgroup per CU; chunks are whole 8192-id tiles.
+    uint64_t G = std::min<uint64_t>(static_cast<uint64_t>(cus), (static_cast<uint64_t>(n) + TILE - 1) / TILE);
     if (G == 0) G = 1;
-    g.chunk = static_cast<uint32_t>((static_cast<uint64_t>(n) + G - 1) / G);
-    g.G = static_cast<uint32_t>((static_cast<uint64_t>(n) + g.chunk - 1) / g.chunk);
+    uint64_t chunk = (static_cast<uint64_t>(n) + G - 1) / G;
+    chunk = (chunk + TILE - 1) / TILE * TILE;
+    g.chunk = static_cast<uint32_t>(chunk);
+    g.G = static_cast<uint32_t>((static_cast<uint64_t>(n) + chunk - 1) / chunk);
+    g.vec = (reinterpret_cast<uintptr_t>(d_ids) & 15u) == 0;
 
     Carver c;
     const size_t o_hist = c.add(sizeof(uint32_t) * static_cast<uint64_t>(g.G) * g.NB);

@@ -49,6 +49,10 @@ extern "C" {
 /* cr_contains_batch modes. */
 #define CR_QUERY_CONTAINS 0   /* GpuRoaringView::contains per lane */
 #define CR_QUERY_WAVEFRONT 1  /* wavefront_contains (== warp_contains) */
+/* Modes 2 and 3 always run the header functions wavefront_contains() and
+ * GpuRoaringView::contains() one query at a time (no batched fast path). */
+#define CR_QUERY_WAVEFRONT_API 2
+#define CR_QUERY_CONTAINS_API 3
 
 /*
  * Byte-identical to cu_roaring::GpuRoaring (include/cu_roaring/types.cuh:15-54):

@@ -305,7 +305,7 @@ QUERY_CASES = [("ids", 1 << 24, 0.01), ("ids", 1 << 24, 0.6), ("keep", 1 << 22, 
 
 
 @pytest.mark.parametrize("layout,universe,density", QUERY_CASES)
-@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
 def test_contains_parity(gpu, layout, universe, density, mode):
     _say("contains", layout, universe, density, mode)
     torch = _torch()
