@@ -137,6 +137,38 @@ def secondary(torch, cr, flush):
     cr.free(b)
     log("set op done", out["set_op_and_50pct_2^30"]["so_exec_GBps"], "GB/s kernel")
 
+    # ---- fused multi_and at 2^30 (config 3): k=3 {0.1,10,50}%, k=8 {2 each of 0.1,1,10,50}% ----
+    def filt(density, seed):
+        n = int(density * U)
+        d = bijective30(torch.arange(n, device="cuda", dtype=torch.int64), seed).to(torch.int32)
+        g_ = cr.upload_from_device_ids(d, U)
+        del d
+        return g_
+    for k, dens in ((3, (0.001, 0.1, 0.5)), (8, (0.001, 0.001, 0.01, 0.01, 0.1, 0.1, 0.5, 0.5))):
+        ins = [filt(d, 100 + i) for i, d in enumerate(dens)]
+        r = cr.multi_and(ins)
+        cr.free(r)
+        cr.timing_enable(True)
+        res_ = []
+        t_api = cold_time(torch, lambda: res_.append(cr.multi_and(ins)), 5, flush)
+        rep = cr.timing_report()
+        cr.timing_enable(False)
+        n_common = res_[0].n_containers
+        for r in res_:
+            cr.free(r)
+        for x in ins:
+            cr.free(x)
+        kn, kms = rep.get("mand_and", (1, float("nan")))
+        mbytes = (k + 1) * 8192 * n_common + 9 * (k + 1) * n_common
+        out[f"multi_and_k{k}_2^30"] = {
+            "densities": list(dens), "n_common": n_common, "algorithmic_bytes": mbytes,
+            "api_ms": round(t_api, 4), "api_GBps": round(mbytes / t_api / 1e6, 1),
+            "mand_and_ms": round(kms / kn, 4), "mand_and_GBps": round(mbytes / (kms / kn) / 1e6, 1),
+            "mand_and_frac_of_hbm_peak": round(mbytes / (kms / kn) / 1e6 / HBM_PEAK_GBS, 4),
+            "kernels_ms": {kk: round(v[1] / v[0], 4) for kk, v in rep.items()}, "cold": True,
+        }
+        log(f"multi_and k={k} done", out[f"multi_and_k{k}_2^30"]["mand_and_GBps"], "GB/s kernel")
+
     # ---- point queries on a 10% all-bitmap 2^30 bitmap (config 4) ----
     n_set = int(0.1 * U)
     ids = bijective30(torch.arange(n_set, device="cuda", dtype=torch.int64), 40).to(torch.int32)

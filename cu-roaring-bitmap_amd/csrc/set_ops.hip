@@ -454,6 +454,73 @@ __global__ __launch_bounds__(EXEC_NT) void so_exec(Side A, Side B, const Item* i
     }
 }
 
+// ---- bitmap x bitmap only: one wavefront per pair ----------------------------
+// When every work item is a bitmap pair (both inputs all-bitmap), each wave
+// streams one 8 KiB pair: 64 lanes x 8 x 16-byte loads per input, the op, the
+// store, and a wave-level popcount -- no workgroup barrier anywhere.
+constexpr int BB_NT = 256;
+
+template <uint32_t OP>
+__global__ __launch_bounds__(BB_NT) void so_exec_bb(const uint64_t* __restrict__ a_bmp, const uint64_t* __restrict__ b_bmp,
+                                                    const Item* __restrict__ items, const Totals* totals,
+                                                    uint64_t* __restrict__ out_bmp, uint32_t* __restrict__ item_card)
+{
+    const uint32_t n_items = totals->c[C_ITEM];
+    const uint32_t lane = __lane_id();
+    const uint32_t n_waves = gridDim.x * (BB_NT / 64);
+    uint32_t w = (blockIdx.x * BB_NT + threadIdx.x) >> 6;
+    if (w >= n_items) return;
+    Item it = items[w];
+    for (; w < n_items; w += n_waves) {
+        const Item cur = it;
+        if (w + n_waves < n_items) it = items[w + n_waves];  // prefetch the next pair's record
+        const uint64_t* pa = a_bmp + (cur.aoff >> 3);
+        const uint64_t* pb = b_bmp + (cur.boff >> 3);
+        uint64_t* po = out_bmp + cur.slot * 1024ull;
+        uint32_t pc = 0;
+        if (((cur.aoff | cur.boff) & 15u) == 0) {
+            const uint4* a4 = reinterpret_cast<const uint4*>(pa);
+            const uint4* b4 = reinterpret_cast<const uint4*>(pb);
+            uint4* o4 = reinterpret_cast<uint4*>(po);
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                uint4 x[4], y[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    x[k] = a4[lane + 64 * (4 * half + k)];
+                    y[k] = b4[lane + 64 * (4 * half + k)];
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    uint4 r;
+                    r.x = apply32<OP>(x[k].x, y[k].x);
+                    r.y = apply32<OP>(x[k].y, y[k].y);
+                    r.z = apply32<OP>(x[k].z, y[k].z);
+                    r.w = apply32<OP>(x[k].w, y[k].w);
+                    o4[lane + 64 * (4 * half + k)] = r;
+                    pc += __popc(r.x) + __popc(r.y) + __popc(r.z) + __popc(r.w);
+                }
+            }
+        } else {
+            for (uint32_t i = lane; i < 1024u; i += 64) {
+                const uint64_t x = pa[i], y = pb[i];
+                const uint64_t r =
+                    static_cast<uint64_t>(apply32<OP>(static_cast<uint32_t>(x), static_cast<uint32_t>(y))) |
+                    (static_cast<uint64_t>(apply32<OP>(static_cast<uint32_t>(x >> 32), static_cast<uint32_t>(y >> 32)))
+                     << 32);
+                po[i] = r;
+                pc += __popcll(r);
+            }
+        }
+        pc = wave_sum(pc);
+        if (lane == 0) {
+            const uint32_t card = pc > 65535u ? 0u : pc;  // 65536 stored as 0 (src/set_ops.cu:179-180)
+            const bool keep = card != 0 || OP == CR_OR;
+            item_card[w] = card | (keep ? 0x80000000u : 0u);
+        }
+    }
+}
+
 // ---- compaction of the kept containers -------------------------------------
 __global__ __launch_bounds__(PLAN_NT) void so_compact(const Item* items, const uint32_t* item_card,
                                                       const uint32_t* tile_keep, Totals* totals, uint16_t* keys,
@@ -624,7 +691,27 @@ int set_operation_impl(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_
     out->run_pool_bytes = static_cast<uint32_t>(run_u16 * 2);
 
     const unsigned g = exec_grid(n_items);
-    {
+    const bool only_bb = h.c[C_BB] == n_items && ((reinterpret_cast<uintptr_t>(a->bitmap_data) |
+                                                   reinterpret_cast<uintptr_t>(b->bitmap_data)) & 15u) == 0;
+    if (only_bb) {
+        const unsigned waves_per_cu = 32;  // 8 waves per SIMD
+        const unsigned gb = std::max(1u, std::min((n_items + 3) / 4, num_cus() * waves_per_cu / 4));
+        CR_TIMED("so_exec", s);
+        switch (op) {
+        case CR_AND:
+            so_exec_bb<CR_AND><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, items, tot, out->bitmap_data, icard);
+            break;
+        case CR_OR:
+            so_exec_bb<CR_OR><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, items, tot, out->bitmap_data, icard);
+            break;
+        case CR_ANDNOT:
+            so_exec_bb<CR_ANDNOT><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, items, tot, out->bitmap_data, icard);
+            break;
+        default:
+            so_exec_bb<CR_XOR><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, items, tot, out->bitmap_data, icard);
+            break;
+        }
+    } else {
         CR_TIMED("so_exec", s);
         switch (op) {
         case CR_AND:
@@ -749,46 +836,65 @@ __global__ __launch_bounds__(EXEC_NT) void mand_and(FusedArgs args, const uint16
                                                     uint16_t* cards, uint16_t* key_index, uint32_t kidx_len,
                                                     uint32_t* total)
 {
-    __shared__ const uint64_t* ptrs[MAX_FUSED];
-    __shared__ uint32_t red[EXEC_NT / 64];
+    // One wavefront per common key: lane k resolves input k's container, the wave
+    // then streams every input's 8 KiB (8 x 16-byte loads per lane per input)
+    // into a register accumulator.  The total cardinality is summed per wave and
+    // added once per workgroup.
+    __shared__ uint32_t wave_total[EXEC_NT / 64];
     const uint32_t n_common = *n_common_p;
-    const uint32_t t = threadIdx.x;
-    for (uint32_t c = blockIdx.x; c < n_common; c += gridDim.x) {
+    const uint32_t lane = __lane_id();
+    const uint32_t n_waves = gridDim.x * (EXEC_NT / 64);
+    uint32_t my_total = 0;
+    for (uint32_t c = (blockIdx.x * EXEC_NT + threadIdx.x) >> 6; c < n_common; c += n_waves) {
         const uint32_t key = common[c];
-        if (t < args.count) {
-            const int32_t idx = fused_lookup(args.in[t], key);
-            // The container is addressed by its index (bitmap_data + idx * 1024,
-            // src/set_ops.cu:1390), not by its offset; absent -> null (all-zeros
-            // sentinel, which a negated input turns into all-ones).
-            ptrs[t] = idx < 0 ? nullptr : args.in[t].bmp + static_cast<uint64_t>(idx) * 1024u;
-        }
-        __syncthreads();
-        uint4 acc0 = make_uint4(~0u, ~0u, ~0u, ~0u), acc1 = acc0;
+        // The container is addressed by its index (bitmap_data + idx * 1024,
+        // src/set_ops.cu:1390), not by its offset; an absent key reads as the
+        // all-zeros sentinel, which a negated input turns into all-ones.
+        const int32_t my_idx = lane < args.count ? fused_lookup(args.in[lane], key) : -1;
+        uint4 acc[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = make_uint4(~0u, ~0u, ~0u, ~0u);
         for (uint32_t k = 0; k < args.count; ++k) {
-            const uint64_t* p = ptrs[k];
+            const int32_t idx = __shfl(my_idx, static_cast<int>(k), 64);
             const bool neg = (args.neg_mask >> k) & 1u;
-            uint4 x0, x1;
-            if (p) {
-                x0 = reinterpret_cast<const uint4*>(p)[t];
-                x1 = reinterpret_cast<const uint4*>(p)[t + EXEC_NT];
+            if (idx < 0) {
+                if (!neg) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) acc[j] = make_uint4(0, 0, 0, 0);
+                }
+                continue;
+            }
+            const uint64_t* p = args.in[k].bmp + static_cast<uint64_t>(idx) * 1024u;
+            const uint32_t m = neg ? ~0u : 0u;
+            if ((reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
+                const uint4* p4 = reinterpret_cast<const uint4*>(p);
+                uint4 x[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[j] = p4[lane + 64 * j];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    acc[j] = make_uint4(acc[j].x & (x[j].x ^ m), acc[j].y & (x[j].y ^ m), acc[j].z & (x[j].z ^ m),
+                                        acc[j].w & (x[j].w ^ m));
             } else {
-                x0 = make_uint4(0, 0, 0, 0);
-                x1 = x0;
+                const uint32_t* p32 = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t b = 4 * (lane + 64 * j);
+                    acc[j] = make_uint4(acc[j].x & (p32[b] ^ m), acc[j].y & (p32[b + 1] ^ m),
+                                        acc[j].z & (p32[b + 2] ^ m), acc[j].w & (p32[b + 3] ^ m));
+                }
             }
-            if (neg) {
-                x0 = make_uint4(~x0.x, ~x0.y, ~x0.z, ~x0.w);
-                x1 = make_uint4(~x1.x, ~x1.y, ~x1.z, ~x1.w);
-            }
-            acc0 = make_uint4(acc0.x & x0.x, acc0.y & x0.y, acc0.z & x0.z, acc0.w & x0.w);
-            acc1 = make_uint4(acc1.x & x1.x, acc1.y & x1.y, acc1.z & x1.z, acc1.w & x1.w);
         }
         uint4* dst = reinterpret_cast<uint4*>(out_bmp + static_cast<uint64_t>(c) * 1024u);
-        dst[t] = acc0;
-        dst[t + EXEC_NT] = acc1;
-        uint32_t pc = __popc(acc0.x) + __popc(acc0.y) + __popc(acc0.z) + __popc(acc0.w) + __popc(acc1.x) +
-                      __popc(acc1.y) + __popc(acc1.z) + __popc(acc1.w);
-        pc = block_sum<EXEC_NT>(pc, red);
-        if (t == 0) {
+        uint32_t pc = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            dst[lane + 64 * j] = acc[j];
+            pc += __popc(acc[j].x) + __popc(acc[j].y) + __popc(acc[j].z) + __popc(acc[j].w);
+        }
+        pc = wave_sum(pc);
+        my_total += pc;
+        if (lane == 0) {
             cards[c] = static_cast<uint16_t>(pc > 65535u ? 65535u : pc);  // clamp (src/set_ops.cu:1468)
             keys[c] = static_cast<uint16_t>(key);
             types[c] = CR_BITMAP;
@@ -796,9 +902,14 @@ __global__ __launch_bounds__(EXEC_NT) void mand_and(FusedArgs args, const uint16
             // The index is sized from the universe; a key beyond it (a bitset upload
             // whose words outrun U) has no slot -- the reference writes out of bounds.
             if (key < kidx_len) key_index[key] = static_cast<uint16_t>(c);
-            atomicAdd(total, pc);
         }
-        __syncthreads();
+    }
+    if (lane == 0) wave_total[threadIdx.x >> 6] = my_total;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t s = 0;
+        for (int i = 0; i < EXEC_NT / 64; ++i) s += wave_total[i];
+        if (s) atomicAdd(total, s);  // u32 like the reference's counter (src/set_ops.cu:1652-1654)
     }
 }
 
@@ -849,7 +960,8 @@ static int fused_multi_and(const cr_gpu_roaring* in, uint32_t count, hipStream_t
     CR_RET(fill_u16(out->key_index, 0xFFFFu, kidx_len, s));
     {
         CR_TIMED("mand_and", s);
-        mand_and<<<exec_grid(n_common), EXEC_NT, 0, s>>>(args, common, cnt, out->bitmap_data, out->keys, out->types,
+        const unsigned gm = std::max(1u, std::min((n_common + 3) / 4, num_cus() * 8u));
+        mand_and<<<gm, EXEC_NT, 0, s>>>(args, common, cnt, out->bitmap_data, out->keys, out->types,
                                                          out->offsets, out->cardinalities, out->key_index,
                                                          static_cast<uint32_t>(kidx_len), cnt + 1);
     }

@@ -91,9 +91,13 @@ __global__ __launch_bounds__(HP_NT) void ids_hist(const uint32_t* __restrict__ i
     const uint64_t hi = min(g.n, lo + g.chunk);
     const uint32_t max_key = g.K - 1;
     uint32_t err = 0, mx = 0;
+    uint32_t nv[8], nvalid = 0;
+    if (lo < hi) load_tile(ids, lo, hi, g.vec, nv, nvalid);
     for (uint64_t base = lo; base < hi; base += TILE) {
-        uint32_t v[8], valid;
-        load_tile(ids, base, hi, g.vec, v, valid);
+        uint32_t v[8], valid = nvalid;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = nv[j];
+        if (base + TILE < hi) load_tile(ids, base + TILE, hi, g.vec, nv, nvalid);  // prefetch
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             if (!((valid >> j) & 1u)) continue;
@@ -165,15 +169,18 @@ __global__ __launch_bounds__(1024) void ids_colscan(IdsGeom g, uint32_t* ghist, 
     }
 }
 
-// Bucket bases and key ranks (one workgroup).  Writes keys/types/offsets and the
-// full key_index (0xFFFF for absent keys).
+// Key ranks, one thread per key and one workgroup per 1024 keys: the rank base
+// of a workgroup is the popcount of the presence words before it.  Writes
+// keys/types/offsets (coalesced) and the full key_index (0xFFFF = absent);
+// workgroup 0 also turns the bucket totals into bucket bases.
 __global__ __launch_bounds__(1024) void ids_keyscan(IdsGeom g, const uint32_t* btotal, const uint32_t* pres,
                                                     uint32_t* bbase, uint16_t* keys, uint8_t* types, uint32_t* offsets,
                                                     uint16_t* key_index, IdsTotals* tot)
 {
     __shared__ uint32_t lds[16];
     const uint32_t t = threadIdx.x;
-    {  // bucket bases: 4 buckets per thread
+    const uint32_t w = blockIdx.x;
+    if (w == 0) {  // bucket bases: 4 buckets per thread
         uint32_t v[4], s = 0;
         for (int q = 0; q < 4; ++q) {
             const uint32_t b = t * 4 + q;
@@ -188,40 +195,35 @@ __global__ __launch_bounds__(1024) void ids_keyscan(IdsGeom g, const uint32_t* b
             run += v[q];
         }
     }
-    {  // key ranks: 2 presence words (64 keys) per thread
-        const uint32_t j0 = 2 * t, j1 = 2 * t + 1;
-        const uint32_t p0 = j0 < g.NW ? pres[j0] : 0u, p1 = j1 < g.NW ? pres[j1] : 0u;
-        uint32_t total;
-        uint32_t rank = block_excl_scan<1024>(__popc(p0) + __popc(p1), lds, total);
-        for (uint32_t kk = 0; kk < 64; ++kk) {
-            const uint32_t key = 64 * t + kk;
-            if (key >= g.K) break;
-            const uint32_t word = kk < 32 ? p0 : p1;
-            if ((word >> (kk & 31u)) & 1u) {
-                keys[rank] = static_cast<uint16_t>(key);
-                types[rank] = CR_BITMAP;
-                offsets[rank] = rank * 8192u;
-                key_index[key] = static_cast<uint16_t>(rank);
-                ++rank;
-            } else {
-                key_index[key] = 0xFFFFu;
-            }
-        }
-        if (t == 0) tot->n_containers = total;
+    uint32_t before = 0;  // present keys below this workgroup's range (32 words per 1024 keys)
+    for (uint32_t j = t; j < w * 32u; j += 1024u) before += __popc(pres[j]);
+    before = block_sum<1024>(before, lds);
+    const uint32_t key = w * 1024u + t;
+    const bool present = key < g.K && ((pres[key >> 5] >> (key & 31u)) & 1u);
+    uint32_t here;
+    const uint32_t rank = before + block_excl_scan<1024>(present ? 1u : 0u, lds, here);
+    if (key < g.K) key_index[key] = present ? static_cast<uint16_t>(rank) : static_cast<uint16_t>(0xFFFFu);
+    if (present) {
+        keys[rank] = static_cast<uint16_t>(key);
+        types[rank] = CR_BITMAP;
+        offsets[rank] = rank * 8192u;
     }
+    if (t == 0 && w == gridDim.x - 1) tot->n_containers = before + here;
 }
 
 // Each 8192-id tile is counting-sorted by bucket in LDS first, so the global
 // writes leave as bucket-contiguous runs (consecutive lanes, consecutive
 // addresses) instead of one scattered 4-byte store per id.
-__global__ __launch_bounds__(HP_NT) void ids_partition(const uint32_t* __restrict__ ids, IdsGeom g,
+__global__ __launch_bounds__(HP_NT, 8) void ids_partition(const uint32_t* __restrict__ ids, IdsGeom g,
                                                        const uint32_t* ghist_off, const uint32_t* bbase,
                                                        uint32_t* __restrict__ part)
 {
+    // 64 KiB of LDS so two workgroups share a CU: the tile buffer, the global
+    // cursor of each bucket, and one array that first counts the tile's ids
+    // per bucket and is then scanned in place into tile-local bucket starts.
     __shared__ uint32_t buf[TILE];
-    __shared__ uint32_t cur[MAX_BUCKETS];  // next global position of each bucket
-    __shared__ uint32_t cnt[MAX_BUCKETS];  // ids of the tile per bucket
-    __shared__ uint32_t ofs[MAX_BUCKETS];  // tile-local start of each bucket
+    __shared__ uint32_t cur[MAX_BUCKETS];
+    __shared__ uint32_t ofs[MAX_BUCKETS + 1];
     __shared__ uint32_t lds[16];
     const uint32_t t = threadIdx.x;
     const uint32_t* off = ghist_off + static_cast<uint64_t>(blockIdx.x) * g.NB;
@@ -230,46 +232,55 @@ __global__ __launch_bounds__(HP_NT) void ids_partition(const uint32_t* __restric
     const uint64_t hi = min(g.n, lo + g.chunk);
     const uint32_t max_key = g.K - 1;
     constexpr uint32_t BPT = MAX_BUCKETS / HP_NT;  // buckets scanned per thread
+    // Two resident workgroups per CU overlap one's LDS phase with the other's loads.
     for (uint64_t base = lo; base < hi; base += TILE) {
-        uint32_t v[8], valid, rank[8];
+        uint32_t v[8], valid, rank[4] = {0, 0, 0, 0};  // tile ranks (< 8192) packed two per register
         load_tile(ids, base, hi, g.vec, v, valid);
-        for (uint32_t i = t; i < g.NB; i += HP_NT) cnt[i] = 0;
+        for (uint32_t i = t; i <= g.NB; i += HP_NT) ofs[i] = 0;
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             if (((valid >> j) & 1u) && (v[j] >> 16) <= max_key)
-                rank[j] = atomicAdd(&cnt[v[j] >> (16 + BK_SHIFT)], 1u);
+            {
+                const uint32_t r = atomicAdd(&ofs[v[j] >> (16 + BK_SHIFT)], 1u);
+                rank[j >> 1] = (j & 1) ? (rank[j >> 1] | (r << 16)) : r;
+            }
             else
                 valid &= ~(1u << j);
         }
         __syncthreads();
-        uint32_t c[BPT], s = 0;
+        uint32_t s = 0;
 #pragma unroll
         for (uint32_t q = 0; q < BPT; ++q) {
             const uint32_t b = t * BPT + q;
-            c[q] = b < g.NB ? cnt[b] : 0u;
-            s += c[q];
+            s += b < g.NB ? ofs[b] : 0u;
         }
         uint32_t tile_n;
         uint32_t run = block_excl_scan<HP_NT>(s, lds, tile_n);
 #pragma unroll
-        for (uint32_t q = 0; q < BPT; ++q) {
+        for (uint32_t q = 0; q < BPT; ++q) {  // each thread owns its BPT buckets: count -> start in place
             const uint32_t b = t * BPT + q;
-            if (b < g.NB) ofs[b] = run;
-            run += c[q];
+            if (b < g.NB) {
+                const uint32_t c = ofs[b];
+                ofs[b] = run;
+                cur[b] -= run;  // cur[b] + p - ofs[b] == (cur[b] - ofs[b]) + p
+                run += c;
+            }
         }
+        if (t == 0) ofs[g.NB] = tile_n;
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-            if ((valid >> j) & 1u) buf[ofs[v[j] >> (16 + BK_SHIFT)] + rank[j]] = v[j];
+            if ((valid >> j) & 1u)
+                buf[ofs[v[j] >> (16 + BK_SHIFT)] + ((rank[j >> 1] >> ((j & 1) * 16)) & 0xFFFFu)] = v[j];
         __syncthreads();
         for (uint32_t p = t; p < tile_n; p += HP_NT) {
             const uint32_t id = buf[p];
-            const uint32_t b = id >> (16 + BK_SHIFT);
-            part[cur[b] + (p - ofs[b])] = id;
+            part[cur[id >> (16 + BK_SHIFT)] + p] = id;
         }
         __syncthreads();
-        for (uint32_t i = t; i < g.NB; i += HP_NT) cur[i] += cnt[i];
+        for (uint32_t i = t; i < g.NB; i += HP_NT) cur[i] += ofs[i + 1];  // old cursor + count of the tile
+        __syncthreads();
     }
 }
 
@@ -301,50 +312,60 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
     const uint32_t body = (cnt - head) & ~3u;
     const uint4* p4 = reinterpret_cast<const uint4*>(part + start + head);
     const uint32_t n4 = body >> 2;
-    for (uint32_t i = t; i < n4; i += 2 * BUILD_NT) {
-        const uint4 x = p4[i];
-        uint4 y = make_uint4(0, 0, 0, 0);
-        const bool has_y = i + BUILD_NT < n4;
-        if (has_y) y = p4[i + BUILD_NT];
-        set_bit(x.x), set_bit(x.y), set_bit(x.z), set_bit(x.w);
-        if (has_y) set_bit(y.x), set_bit(y.y), set_bit(y.z), set_bit(y.w);
+    constexpr uint32_t U4 = 4;  // 16-byte loads in flight per lane
+    for (uint32_t i = t; i < n4; i += U4 * BUILD_NT) {
+        uint4 x[U4];
+#pragma unroll
+        for (uint32_t k = 0; k < U4; ++k)
+            x[k] = i + k * BUILD_NT < n4 ? p4[i + k * BUILD_NT] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (uint32_t k = 0; k < U4; ++k) {
+            if (i + k * BUILD_NT >= n4) break;
+            set_bit(x[k].x), set_bit(x[k].y), set_bit(x[k].z), set_bit(x[k].w);
+        }
     }
     const uint32_t tail0 = head + body;
     if (tail0 + t < cnt) set_bit(part[start + tail0 + t]);
     __syncthreads();
+    __shared__ uint32_t wave_pc[BUILD_NT / 64];
     const uint32_t c = t >> 6;  // wave c owns container c of the bucket
     const uint32_t lane = __lane_id();
     const uint32_t key = b * BK_KEYS + c;
-    if (key >= g.K) return;
-    uint32_t* cb = bits + c * 2048u;
-    uint32_t valid_words = 2048, tail_mask = ~0u;
-    if (complement) {
-        const uint64_t valid = min<uint64_t>(65536u, static_cast<uint64_t>(universe) - static_cast<uint64_t>(key) * 65536u);
-        valid_words = static_cast<uint32_t>(valid >> 5);
-        tail_mask = (valid & 31u) ? ((1u << (valid & 31u)) - 1u) : 0u;
-    }
     uint32_t pc = 0;
-    for (uint32_t i = lane; i < 2048u; i += 64) {
-        uint32_t w = cb[i];
+    if (key < g.K) {
+        uint32_t* cb = bits + c * 2048u;
+        uint32_t valid_words = 2048, tail_mask = ~0u;
         if (complement) {
-            w = ~w;
-            if (i >= valid_words) w = (i == valid_words) ? (w & tail_mask) : 0u;
-            cb[i] = w;
+            const uint64_t valid =
+                min<uint64_t>(65536u, static_cast<uint64_t>(universe) - static_cast<uint64_t>(key) * 65536u);
+            valid_words = static_cast<uint32_t>(valid >> 5);
+            tail_mask = (valid & 31u) ? ((1u << (valid & 31u)) - 1u) : 0u;
         }
-        pc += __popc(w);
+        for (uint32_t i = lane; i < 2048u; i += 64) {
+            uint32_t w = cb[i];
+            if (complement) {
+                w = ~w;
+                if (i >= valid_words) w = (i == valid_words) ? (w & tail_mask) : 0u;
+                cb[i] = w;
+            }
+            pc += __popc(w);
+        }
+        pc = wave_sum(pc);
+        if (!complement && key_count && lane == 0) key_count[key] = pc;
+        if (pc != 0) {
+            const uint32_t rank = key_index[key];
+            uint4* dst = reinterpret_cast<uint4*>(pool + static_cast<uint64_t>(rank) * 1024u);
+            const uint4* src = reinterpret_cast<const uint4*>(cb);
+            for (uint32_t i = lane; i < 512u; i += 64) dst[i] = src[i];
+            if (lane == 0) cards[rank] = static_cast<uint16_t>(pc > 65535u ? 0u : pc);
+        }
     }
-    pc = wave_sum(pc);
-    if (!complement && key_count) {
-        if (lane == 0) key_count[key] = pc;
-    }
-    if (pc == 0) return;
-    const uint32_t rank = key_index[key];
-    uint4* dst = reinterpret_cast<uint4*>(pool + static_cast<uint64_t>(rank) * 1024u);
-    const uint4* src = reinterpret_cast<const uint4*>(cb);
-    for (uint32_t i = lane; i < 512u; i += 64) dst[i] = src[i];
-    if (lane == 0) {
-        cards[rank] = static_cast<uint16_t>(pc > 65535u ? 0u : pc);
-        atomicAdd(&tot->total, static_cast<unsigned long long>(pc));
+    if (lane == 0) wave_pc[c] = pc;
+    __syncthreads();
+    if (t == 0) {  // one device atomic per workgroup
+        unsigned long long s = 0;
+        for (uint32_t i = 0; i < BUILD_NT / 64; ++i) s += wave_pc[i];
+        if (s) atomicAdd(&tot->total, s);
     }
 }
 
@@ -630,8 +651,8 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     g.NB = (g.K + BK_KEYS - 1) / BK_KEYS;
     g.NW = (g.K + 31) / 32;
     const uint32_t cus = num_cus();
-    // One 1024-lane workgroup per CU; chunks are whole 8192-id tiles.
-    uint64_t G = std::min<uint64_t>(static_cast<uint64_t>(cus), (static_cast<uint64_t>(n) + TILE - 1) / TILE);
+    // Two 1024-lane workgroups per CU; chunks are whole 8192-id tiles.
+    uint64_t G = std::min<uint64_t>(2ull * cus, (static_cast<uint64_t>(n) + TILE - 1) / TILE);
     if (G == 0) G = 1;
     uint64_t chunk = (static_cast<uint64_t>(n) + G - 1) / G;
     chunk = (chunk + TILE - 1) / TILE * TILE;
@@ -679,7 +700,8 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     CR_LAUNCH_CHECK();
     {
         CR_TIMED("ids_keyscan", s);
-        ids_keyscan<<<1, 1024, 0, s>>>(g, btotal, pres, bbase, out->keys, out->types, out->offsets, out->key_index, tot);
+        ids_keyscan<<<(g.K + 1023) / 1024, 1024, 0, s>>>(g, btotal, pres, bbase, out->keys, out->types, out->offsets,
+                                                         out->key_index, tot);
     }
     CR_LAUNCH_CHECK();
     {
