@@ -275,8 +275,9 @@ def main():
         sys.exit(1)
     log("timed steps done", round(ms_per_step, 4), "ms/step")
 
-    per_kernel = {k: v[1] / v[0] for k, v in rep.items()}
-    dev_ms = sum(v[1] for v in rep.values()) / args.steps
+    per_kernel = {k: v[1] / v[0] for k, v in rep.items() if not k.startswith("host:")}
+    host_ms = {k[5:]: round(v[1] / args.steps, 4) for k, v in rep.items() if k.startswith("host:")}
+    dev_ms = sum(v[1] for k, v in rep.items() if not k.startswith("host:")) / args.steps
     dom = max(("ids_hist", "ids_partition", "ids_build"), key=lambda k: per_kernel.get(k, 0.0))
     dom_bytes = upload_kernel_bytes(dom, N_IDS, n_c, 16383)
     dom_ms = per_kernel[dom]
@@ -314,8 +315,24 @@ def main():
         "pipeline": {"algorithmic_bytes": path_bytes, "device_ms": round(dev_ms, 4),
                      "achieved_GBps": round(path_bytes / dev_ms / 1e6, 1),
                      "frac": round(path_bytes / dev_ms / 1e6 / HBM_PEAK_GBS, 4),
-                     "kernels_ms": {k: round(v, 5) for k, v in per_kernel.items()}},
+                     "kernels_ms": {k: round(v, 5) for k, v in per_kernel.items()},
+                     "host_ms_per_step": host_ms},
     }
+    # Achievable-bandwidth reference: a plain 1 GiB device copy (also the known-size
+    # kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE).
+    src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    copy_ms = e0.elapsed_time(e1) / 5
+    result["copy_1GiB"] = {"ms": round(copy_ms, 4), "GBps_read_plus_write": round(2 * (1 << 30) / copy_ms / 1e6, 1)}
+    del src, dst
     if rank == 0 and not args.no_cpu:
         log("cpu baseline (10M-id sample)")
         sample = d_ids[:10_000_000].cpu().numpy().view("uint32")

@@ -38,6 +38,8 @@ inline hipStream_t as_stream(cr_stream_t s) { return reinterpret_cast<hipStream_
 // ---- stream-ordered device memory ---------------------------------------
 int dev_alloc(void** p, size_t bytes, hipStream_t s);
 int dev_free(void* p, hipStream_t s);
+// hipStreamSynchronize, timed as the host phase "sync".
+int sync_stream(hipStream_t s);
 
 // Scratch that is released (stream-ordered) when the guard leaves scope.
 struct Scratch {
@@ -203,6 +205,16 @@ struct TimedLaunch {
     ~TimedLaunch();
 };
 #define CR_TIMED(name, stream) ::crimpl::TimedLaunch cr_timed_launch__(name, stream)
+
+// Host wall-clock phases (allocation, synchronisation), reported as "host:<name>".
+void record_host_ms(const char* name, double ms);
+struct HostPhase {
+    const char* name;
+    double t0;
+    explicit HostPhase(const char* n);
+    ~HostPhase();
+};
+#define CR_HOST_PHASE(name) ::crimpl::HostPhase cr_host_phase__(name)
 
 uint64_t device_l2_bytes(int device);
 // Compute units of the current device (cached per device).

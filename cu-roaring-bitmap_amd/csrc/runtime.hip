@@ -1,6 +1,7 @@
 // Runtime pieces shared by every entry point: error state, allocation of
 // packed result blocks, free, AUTO threshold, and small utility entry points.
 #include <algorithm>
+#include <chrono>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -22,8 +23,16 @@ void set_error(const char* fmt, ...)
     g_last_error = buf;
 }
 
+int sync_stream(hipStream_t s)
+{
+    CR_HOST_PHASE("sync");
+    CR_HIP_RET(hipStreamSynchronize(s));
+    return CR_OK;
+}
+
 int dev_alloc(void** p, size_t bytes, hipStream_t s)
 {
+    CR_HOST_PHASE("alloc");
     *p = nullptr;
     if (bytes == 0) bytes = 256;
     hipError_t e = hipMallocAsync(p, bytes, s);
@@ -38,6 +47,7 @@ int dev_alloc(void** p, size_t bytes, hipStream_t s)
 int dev_free(void* p, hipStream_t s)
 {
     if (!p) return CR_OK;
+    CR_HOST_PHASE("free");
     CR_HIP_RET(hipFreeAsync(p, s));
     return CR_OK;
 }
@@ -167,6 +177,26 @@ TimedLaunch::~TimedLaunch()
     (void)hipEventRecord(stop, stream);
     std::lock_guard<std::mutex> lock(g_timing_mu);
     g_timing_recs.push_back(TimingRec{name, start, stop});
+}
+
+static std::vector<std::pair<std::string, double>> g_host_recs;
+
+static double now_ms()
+{
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+void record_host_ms(const char* name, double ms)
+{
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    g_host_recs.emplace_back(std::string("host:") + name, ms);
+}
+
+HostPhase::HostPhase(const char* n) : name(n), t0(g_timing_on ? now_ms() : 0.0) {}
+
+HostPhase::~HostPhase()
+{
+    if (g_timing_on) record_host_ms(name, now_ms() - t0);
 }
 
 uint32_t num_cus()
@@ -302,6 +332,7 @@ int cr_timing_enable(int on)
         (void)hipEventDestroy(r.stop);
     }
     g_timing_recs.clear();
+    g_host_recs.clear();
     g_timing_on = on != 0;
     return CR_OK;
 }
@@ -321,6 +352,15 @@ int cr_timing_report(char* buf, size_t cap)
         } else {
             it->second.first += 1;
             it->second.second += ms;
+        }
+    }
+    for (auto& h : g_host_recs) {
+        auto it = std::find_if(agg.begin(), agg.end(), [&](auto& a) { return a.first == h.first; });
+        if (it == agg.end()) {
+            agg.push_back({h.first, {1, h.second}});
+        } else {
+            it->second.first += 1;
+            it->second.second += h.second;
         }
     }
     std::string out;

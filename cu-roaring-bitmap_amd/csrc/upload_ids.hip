@@ -611,7 +611,7 @@ static int small_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, ui
     CR_LAUNCH_CHECK();
     uint32_t hdr[8];
     CR_HIP_RET(hipMemcpyAsync(hdr, plan, sizeof(hdr), hipMemcpyDeviceToHost, s));
-    CR_HIP_RET(hipStreamSynchronize(s));
+    CR_RET(sync_stream(s));
     const uint32_t nc = hdr[1], n_bitmap = hdr[2], n_array = hdr[3], arr_elems = hdr[4];
     out->total_cardinality = hdr[5];
     out->negated = hdr[6] != 0;
@@ -633,7 +633,7 @@ static int small_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, ui
                                            static_cast<uint32_t>(kidx_len));
     }
     CR_LAUNCH_CHECK();
-    CR_HIP_RET(hipStreamSynchronize(s));
+    CR_RET(sync_stream(s));
     return CR_OK;
 }
 
@@ -717,7 +717,7 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     CR_LAUNCH_CHECK();
     IdsTotals h{};
     CR_HIP_RET(hipMemcpyAsync(&h, tot, sizeof(h), hipMemcpyDeviceToHost, s));
-    CR_HIP_RET(hipStreamSynchronize(s));
+    CR_RET(sync_stream(s));
     if (h.err) {
         free_async(out, s);
         set_error("upload_from_ids: an id's key exceeds max_key = (universe_size-1)>>16 = %u", max_key32);
@@ -753,7 +753,7 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     }
     CR_LAUNCH_CHECK();
     CR_HIP_RET(hipMemcpyAsync(&h, tot, sizeof(h), hipMemcpyDeviceToHost, s));
-    CR_HIP_RET(hipStreamSynchronize(s));
+    CR_RET(sync_stream(s));
     free_async(out, s);
     *out = comp;
     out->universe_size = universe;

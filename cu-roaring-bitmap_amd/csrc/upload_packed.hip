@@ -224,9 +224,9 @@ int upload_containers_impl(const cr_host_container* conts, uint32_t n, uint32_t 
                                                                             out->bitmap_data);
         }
         CR_LAUNCH_CHECK();
-        CR_HIP_RET(hipStreamSynchronize(s));
+        CR_RET(sync_stream(s));
     }
-    CR_HIP_RET(hipStreamSynchronize(s));  // the staging buffer is reused by the next call
+    CR_RET(sync_stream(s));  // the staging buffer is reused by the next call
     out->n_containers = n;
     out->n_bitmap_containers = nb;
     out->n_array_containers = na;
