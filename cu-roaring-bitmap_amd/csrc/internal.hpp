@@ -187,6 +187,28 @@ __device__ __forceinline__ uint32_t lower_bound_u16(const uint16_t* a, uint32_t 
     return lo;
 }
 
+// lower_bound with a whole wavefront: 64 samples per step (log64 n dependent
+// loads instead of log2 n).  Every active lane must call it with the same
+// arguments and receives the same result.
+__device__ __forceinline__ uint32_t wave_lower_bound_u16(const uint16_t* a, uint32_t n, uint32_t key)
+{
+    const uint32_t lane = __lane_id();
+    uint32_t lo = 0, hi = n;  // the answer lies in [lo, hi]
+    while (hi - lo > 64) {
+        const uint32_t step = (hi - lo + 63) / 64;
+        const uint32_t pos = lo + lane * step;
+        const bool less = pos < hi && a[pos] < key;
+        const uint32_t cnt = static_cast<uint32_t>(__popcll(__ballot(less)));
+        if (cnt == 0) return lo;
+        const uint32_t nlo = lo + (cnt - 1) * step + 1;
+        hi = min(hi, lo + cnt * step);
+        lo = nlo;
+    }
+    const uint32_t pos = lo + lane;
+    const bool less = pos < hi && a[pos] < key;
+    return lo + static_cast<uint32_t>(__popcll(__ballot(less)));
+}
+
 // Fill kernels (used instead of hipMemsetAsync so the work stays capturable).
 __global__ void fill_u16_kernel(uint16_t* p, uint16_t v, uint64_t n);
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, uint64_t n);

@@ -30,12 +30,40 @@ int sync_stream(hipStream_t s)
     return CR_OK;
 }
 
+// Library-owned stream-ordered pool per device.  Its release threshold is
+// "never", so memory returned by hipFreeAsync (scratch, freed results) stays
+// mapped and the next allocation is a cache hit; the process's default pool is
+// left untouched.  cr_mempool_trim() returns cached memory to the device.
+static std::mutex g_pool_mu;
+static hipMemPool_t g_pools[64] = {};
+
+static hipMemPool_t library_pool()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(g_pool_mu);
+    if (!g_pools[dev]) {
+        hipMemPoolProps props{};
+        props.allocType = hipMemAllocationTypePinned;
+        props.handleTypes = hipMemHandleTypeNone;
+        props.location.type = hipMemLocationTypeDevice;
+        props.location.id = dev;
+        hipMemPool_t pool = nullptr;
+        if (hipMemPoolCreate(&pool, &props) != hipSuccess) return nullptr;
+        uint64_t never = ~0ull;
+        (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &never);
+        g_pools[dev] = pool;
+    }
+    return g_pools[dev];
+}
+
 int dev_alloc(void** p, size_t bytes, hipStream_t s)
 {
     CR_HOST_PHASE("alloc");
     *p = nullptr;
     if (bytes == 0) bytes = 256;
-    hipError_t e = hipMallocAsync(p, bytes, s);
+    hipMemPool_t pool = library_pool();
+    hipError_t e = pool ? hipMallocFromPoolAsync(p, bytes, pool, s) : hipMallocAsync(p, bytes, s);
     if (e != hipSuccess) {
         set_error("hipMallocAsync(%zu bytes) failed: %s", bytes, hipGetErrorString(e));
         *p = nullptr;
@@ -321,6 +349,16 @@ int cr_memcpy_d2h(void* dst, const void* src, size_t bytes)
 int cr_stream_synchronize(cr_stream_t stream)
 {
     CR_HIP_RET(hipStreamSynchronize(as_stream(stream)));
+    return CR_OK;
+}
+
+int cr_mempool_trim(int device_id, size_t keep_bytes)
+{
+    int dev = device_id;
+    if (dev < 0) CR_HIP_RET(hipGetDevice(&dev));
+    if (dev >= 64) return CR_ERR_INVALID;
+    std::lock_guard<std::mutex> lock(g_pool_mu);
+    if (g_pools[dev]) CR_HIP_RET(hipMemPoolTrimTo(g_pools[dev], keep_bytes));
     return CR_OK;
 }
 

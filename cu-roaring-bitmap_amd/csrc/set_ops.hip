@@ -74,10 +74,12 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_classify(Side A, Side B, uint
     __shared__ uint32_t red[PLAN_NT / 64];
     const uint32_t base = blockIdx.x * PLAN_NT;
     const uint32_t t = threadIdx.x;
-    if (t == 0) range[0] = lower_bound_u16(A.keys, A.n, base);
-    if (t == 1) range[1] = lower_bound_u16(A.keys, A.n, base + PLAN_NT);
-    if (t == 64) range[2] = lower_bound_u16(B.keys, B.n, base);
-    if (t == 65) range[3] = lower_bound_u16(B.keys, B.n, base + PLAN_NT);
+    const uint32_t wv = t >> 6;  // waves 0-3: the key range of this group in A and in B
+    if (wv < 4) {
+        const uint32_t r = wave_lower_bound_u16(wv < 2 ? A.keys : B.keys, wv < 2 ? A.n : B.n,
+                                                base + ((wv & 1u) ? PLAN_NT : 0u));
+        if ((t & 63u) == 0) range[wv] = r;
+    }
     ia[t] = -1;
     ib[t] = -1;
     __syncthreads();
@@ -766,48 +768,64 @@ struct FusedArgs {
 
 // Common keys: AND of the key-presence sets of the non-negated inputs, or the
 // universe mask [0, mkp1) when every input is negated (src/set_ops.cu:1239-1264).
-__global__ __launch_bounds__(1024) void mand_keys(FusedArgs args, uint32_t mkp1, uint16_t* common, uint32_t* n_common)
+// Two passes over the 65536-key space in 64 ranges of 1024 keys:
+//   mand_presence  (range, input): the input's sorted keys inside the range
+//                  become 32 presence words (no global atomics);
+//   mand_common    (range): AND over inputs, rank base = popcount of the AND
+//                  of all earlier words, one thread per key writes its rank.
+constexpr uint32_t KEY_RANGES = 64;
+
+__global__ __launch_bounds__(256) void mand_presence(FusedArgs args, uint32_t* gpres)
 {
-    __shared__ uint32_t acc[2048], tmp[2048];
-    __shared__ uint32_t lds[16];
-    const uint32_t t = threadIdx.x;
-    const bool any_plain = (args.neg_mask & ((args.count >= 32) ? ~0u : ((1u << args.count) - 1u))) !=
-                           ((args.count >= 32) ? ~0u : ((1u << args.count) - 1u));
-    for (uint32_t i = t; i < 2048u; i += 1024u) {
-        if (any_plain) {
-            acc[i] = ~0u;
-        } else {
-            const uint32_t lo = i * 32u;
-            acc[i] = lo >= mkp1 ? 0u : (lo + 32u <= mkp1 ? ~0u : ((1u << (mkp1 - lo)) - 1u));
-        }
-    }
-    for (uint32_t k = 0; k < args.count; ++k) {
-        if ((args.neg_mask >> k) & 1u) continue;
-        for (uint32_t i = t; i < 2048u; i += 1024u) tmp[i] = 0;
-        __syncthreads();
-        const uint16_t* keys = args.in[k].keys;
-        for (uint32_t j = t; j < args.in[k].n; j += 1024u) {
-            const uint32_t key = keys[j];
-            atomicOr(&tmp[key >> 5], 1u << (key & 31u));
-        }
-        __syncthreads();
-        for (uint32_t i = t; i < 2048u; i += 1024u) acc[i] &= tmp[i];
-        __syncthreads();
+    __shared__ uint32_t words[32];
+    __shared__ uint32_t range[2];
+    const uint32_t r = blockIdx.x, k = blockIdx.y, t = threadIdx.x;
+    if ((args.neg_mask >> k) & 1u) return;  // only non-negated inputs restrict the key set
+    const uint32_t base = r * 1024u;
+    if (t < 32) words[t] = 0;
+    if (t < 128) {  // waves 0 and 1 find the input's index range for [base, base + 1024)
+        const uint32_t v = wave_lower_bound_u16(args.in[k].keys, args.in[k].keys ? args.in[k].n : 0u,
+                                                base + (t >= 64 ? 1024u : 0u));
+        if ((t & 63u) == 0) range[t >> 6] = v;
     }
     __syncthreads();
-    const uint32_t w0 = acc[2 * t], w1 = acc[2 * t + 1];
-    uint32_t total;
-    uint32_t pos = block_excl_scan<1024>(__popc(w0) + __popc(w1), lds, total);
-    uint32_t ws[2] = {w0, w1};
-    for (int q = 0; q < 2; ++q) {
-        uint32_t x = ws[q];
-        while (x) {
-            const uint32_t b = __ffs(x) - 1;
-            common[pos++] = static_cast<uint16_t>((2 * t + q) * 32u + b);
-            x &= x - 1;
-        }
+    for (uint32_t j = range[0] + t; j < range[1]; j += 256u) {
+        const uint32_t off = args.in[k].keys[j] - base;
+        if (off < 1024u) atomicOr(&words[off >> 5], 1u << (off & 31u));
     }
-    if (t == 0) *n_common = total;
+    __syncthreads();
+    if (t < 32) gpres[k * 2048u + r * 32u + t] = words[t];
+}
+
+__device__ __forceinline__ uint32_t common_word(const FusedArgs& args, const uint32_t* gpres, bool any_plain,
+                                                uint32_t mkp1, uint32_t j)
+{
+    if (!any_plain) {
+        const uint32_t lo = j * 32u;
+        return lo >= mkp1 ? 0u : (lo + 32u <= mkp1 ? ~0u : ((1u << (mkp1 - lo)) - 1u));
+    }
+    uint32_t acc = ~0u;
+    for (uint32_t k = 0; k < args.count; ++k)
+        if (!((args.neg_mask >> k) & 1u)) acc &= gpres[k * 2048u + j];
+    return acc;
+}
+
+__global__ __launch_bounds__(1024) void mand_common(FusedArgs args, const uint32_t* gpres, uint32_t mkp1,
+                                                    uint16_t* common, uint32_t* n_common)
+{
+    __shared__ uint32_t lds[16];
+    const uint32_t w = blockIdx.x, t = threadIdx.x;
+    const uint32_t all = args.count >= 32 ? ~0u : ((1u << args.count) - 1u);
+    const bool any_plain = (args.neg_mask & all) != all;
+    uint32_t before = 0;
+    for (uint32_t j = t; j < w * 32u; j += 1024u) before += __popc(common_word(args, gpres, any_plain, mkp1, j));
+    before = block_sum<1024>(before, lds);
+    const uint32_t key = w * 1024u + t;
+    const bool present = (common_word(args, gpres, any_plain, mkp1, key >> 5) >> (key & 31u)) & 1u;
+    uint32_t here;
+    const uint32_t rank = before + block_excl_scan<1024>(present ? 1u : 0u, lds, here);
+    if (present) common[rank] = static_cast<uint16_t>(key);
+    if (t == 0 && w == KEY_RANGES - 1) *n_common = before + here;
 }
 
 __device__ __forceinline__ int32_t fused_lookup(const FusedIn& in, uint32_t key)
@@ -935,13 +953,16 @@ static int fused_multi_and(const cr_gpu_roaring* in, uint32_t count, hipStream_t
     Carver c;
     const size_t o_common = c.add(2 * 65536);
     const size_t o_cnt = c.add(2 * sizeof(uint32_t));
+    const size_t o_pres = c.add(sizeof(uint32_t) * 2048u * count);
     Scratch sc;
     CR_RET(sc.alloc(c.total, s));
     uint16_t* common = sc.at<uint16_t>(o_common);
     uint32_t* cnt = sc.at<uint32_t>(o_cnt);  // [0] n_common, [1] total cardinality
+    uint32_t* gpres = sc.at<uint32_t>(o_pres);
     {
         CR_TIMED("mand_keys", s);
-        mand_keys<<<1, 1024, 0, s>>>(args, mkp1, common, cnt);
+        mand_presence<<<dim3(KEY_RANGES, count), 256, 0, s>>>(args, gpres);
+        mand_common<<<KEY_RANGES, 1024, 0, s>>>(args, gpres, mkp1, common, cnt);
     }
     CR_LAUNCH_CHECK();
     CR_RET(fill_u32(cnt + 1, 0u, 1, s));

@@ -31,7 +31,7 @@ EXPORTS = [
     "cr_upload_from_device_bitset", "cr_upload_containers", "cr_get_meta", "cr_set_operation", "cr_multi_and",
     "cr_free", "cr_free_async", "cr_resolve_auto_threshold", "cr_make_view", "cr_contains_batch",
     "cr_topk_filtered", "cr_device_l2_bytes", "cr_device_malloc", "cr_device_free", "cr_memcpy_h2d",
-    "cr_memcpy_d2h", "cr_stream_synchronize", "cr_timing_enable", "cr_timing_report",
+    "cr_memcpy_d2h", "cr_stream_synchronize", "cr_timing_enable", "cr_timing_report", "cr_mempool_trim",
 ]
 
 
@@ -134,6 +134,7 @@ def load(path: Optional[str] = None):
         "cr_memcpy_d2h": [C.c_void_p, C.c_void_p, C.c_size_t],
         "cr_stream_synchronize": [C.c_void_p],
         "cr_timing_enable": [C.c_int],
+        "cr_mempool_trim": [C.c_int, C.c_size_t],
         "cr_timing_report": [C.c_char_p, C.c_size_t],
     }
     for name, args in sigs.items():

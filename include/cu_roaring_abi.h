@@ -187,6 +187,11 @@ int cr_device_free(void* ptr);
 int cr_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int cr_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int cr_stream_synchronize(cr_stream_t stream);
+/* The library allocates results and scratch from its own per-device HIP memory
+ * pool, which keeps freed memory cached (release threshold: never) so repeated
+ * calls do not remap device memory.  Trim it down to `keep_bytes` (-1 device =
+ * current device). */
+int cr_mempool_trim(int device_id, size_t keep_bytes);
 /* Per-kernel HIP-event timing: enable (1) / disable (0) and clear the records;
  * the report is one "kernel_name launches total_ms" line per kernel. */
 int cr_timing_enable(int on);
