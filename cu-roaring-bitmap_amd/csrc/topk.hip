@@ -1,11 +1,600 @@
-// Fused filtered brute-force top-k (placeholder until the MFMA kernel lands).
+// Fused filtered brute-force top-k on fp32 MFMA (no reference implementation;
+// the reference motivates the path only in prose, README.md:265).
+//
+// For each query q: the k smallest squared L2 distances ||q - x_i||^2 over the
+// base vectors i that pass the filter, ascending, ties broken by the smaller id.
+//
+//   1. tk_enum_count / tk_enum_write: the passing ids of [0, n_base), in
+//      ascending order, via GpuRoaringView::contains (any layout, negated too).
+//   2. tk_dist: grid = chunks of the passing ids x blocks of 256 queries.  Each
+//      wave keeps 32 queries in registers as the MFMA B operand and streams
+//      64-row base tiles through LDS (double buffered, rows gathered by id) as
+//      the A operand: d = ||q||^2 + ||x||^2 - 2 q.x with
+//      v_mfma_f32_32x32x2f32.  That expansion loses relative precision for
+//      near-duplicate vectors, so it only gates: a row that may beat its
+//      query's current k-th best gets its fp32 distance sum((q - x)^2)
+//      recomputed from the LDS tile, and enters the wave's candidate buffer
+//      if it does.  A full buffer is merged into per-(chunk, query) sorted
+//      top-k lists; every stored and returned distance is the direct one.
+//   3. tk_merge: one wave per query merges its chunk lists into the answer.
+#include <algorithm>
+#include <cstring>
+
+#include "cu_roaring/device/roaring_view.hpp"
 #include "internal.hpp"
+
+namespace crimpl {
+
+using cu_roaring::GpuRoaringView;
+
+namespace {
+
+constexpr uint32_t TK_ENUM_IDS = 8192;  // ids per enumeration workgroup
+constexpr int TK_ENUM_NT = 256;
+constexpr int TK_NT = 512;  // distance kernel: 8 waves
+constexpr int TK_WAVES = TK_NT / 64;
+constexpr uint32_t TK_QW = 32;                  // queries per wave (MFMA N)
+constexpr uint32_t TK_QB = TK_WAVES * TK_QW;    // queries per workgroup
+constexpr int TK_ROWS = 64;                     // base rows per tile (two 32-row MFMA blocks)
+constexpr uint32_t TK_CB = 512;                 // candidate buffer entries per wave
+constexpr uint32_t TK_KMAX = 256;
+constexpr uint32_t TK_NOID = 0xFFFFFFFFu;
+constexpr int TK_MERGE_NT = 256;
+// Bound on |MFMA-expansion distance - fp32 direct distance| per unit of
+// |q|^2 + |x|^2 at dim <= 128: about (2*128 + 4) unit roundoffs for the dot
+// product, the two norms and the combination, plus the direct sum's own
+// 128-term bound, rounded up.
+constexpr float TK_GATE_ERR = 4e-5f;
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Strict order of (distance, id) pairs: the output order.
+__device__ __forceinline__ bool tk_less(float ad, uint32_t ai, float bd, uint32_t bi)
+{
+    return ad < bd || (ad == bd && ai < bi);
+}
+
+// Number of entries of the sorted list (d, id)[0, n) that order before (yd, yi).
+__device__ __forceinline__ uint32_t tk_lower_bound(const float* d, const uint32_t* id, uint32_t n, float yd,
+                                                   uint32_t yi)
+{
+    uint32_t lo = 0, hi = n;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (tk_less(d[mid], id[mid], yd, yi))
+            lo = mid + 1;
+        else
+            hi = mid;
+    }
+    return lo;
+}
+
+__device__ __forceinline__ uint64_t lanemask_lt() { return (1ull << __lane_id()) - 1ull; }
+
+// ---- 1. passing ids ---------------------------------------------------------
+
+__global__ __launch_bounds__(TK_ENUM_NT) void tk_enum_count(GpuRoaringView v, uint64_t n_base, uint32_t* counts)
+{
+    __shared__ uint32_t red[TK_ENUM_NT / 64];
+    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * TK_ENUM_IDS;
+    uint32_t c = 0;
+    for (uint32_t i = 0; i < TK_ENUM_IDS / TK_ENUM_NT; ++i) {
+        const uint64_t id = base + i * TK_ENUM_NT + threadIdx.x;
+        c += (id < n_base && v.contains(static_cast<uint32_t>(id))) ? 1u : 0u;
+    }
+    c = block_sum<TK_ENUM_NT>(c, red);
+    if (threadIdx.x == 0) counts[blockIdx.x] = c;
+}
+
+__global__ __launch_bounds__(TK_ENUM_NT) void tk_enum_write(GpuRoaringView v, uint64_t n_base, const uint32_t* counts,
+                                                            uint32_t* sel, uint32_t* n_sel)
+{
+    __shared__ uint32_t red[TK_ENUM_NT / 64];
+    uint32_t pre = 0;
+    for (uint32_t i = threadIdx.x; i < blockIdx.x; i += TK_ENUM_NT) pre += counts[i];
+    uint32_t run = block_sum<TK_ENUM_NT>(pre, red);
+    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * TK_ENUM_IDS;
+    for (uint32_t i = 0; i < TK_ENUM_IDS / TK_ENUM_NT; ++i) {
+        const uint64_t id = base + i * TK_ENUM_NT + threadIdx.x;
+        const bool p = id < n_base && v.contains(static_cast<uint32_t>(id));
+        uint32_t tot;
+        const uint32_t r = block_flag_rank<TK_ENUM_NT>(p, red, tot);
+        if (p) sel[run + r] = static_cast<uint32_t>(id);
+        run += tot;
+    }
+    if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) *n_sel = run;
+}
+
+// ---- 2. distances and per-chunk selection ----------------------------------
+
+struct TkArgs {
+    const float* base;
+    const float* queries;
+    const uint32_t* sel;    // passing ids ascending (nullptr: every id of [0, n_base))
+    const uint32_t* n_sel;  // device count of sel
+    uint64_t n_base;
+    uint32_t n_q;
+    uint32_t dim;
+    uint32_t k;
+    uint32_t n_chunks;  // multiple of 8
+    uint32_t vec;       // rows are 16-B aligned with dim % 4 == 0
+    float* list_d;      // [n_chunks][n_q][k]
+    uint32_t* list_id;  // [n_chunks][n_q][k]
+    uint32_t* list_n;   // [n_chunks][n_q]
+};
+
+// Per-wave selection state in LDS.
+struct TkWave {
+    float cd[TK_CB];  // candidate buffer: distance, id, query slot (0..31)
+    uint32_t cid[TK_CB];
+    float sd[TK_CB];  // one query's candidates during a merge
+    uint32_t sid[TK_CB];
+    float ld[TK_KMAX];  // that query's current list
+    uint32_t lid[TK_KMAX];
+    float td[TK_QW];  // threshold: the k-th best so far (+inf, NOID while the list is short)
+    uint32_t tid[TK_QW];
+    uint32_t ln[TK_QW];  // list length
+    uint8_t cq[TK_CB];
+};
+
+template <int DP>
+struct TkLds {
+    float tile[2][TK_ROWS * (DP + 4)];  // rows skewed by 16 B: conflict-free b128 reads
+    float xn[2][TK_ROWS];
+    uint32_t id[2][TK_ROWS];
+    TkWave w[TK_WAVES];
+};
+
+// Merges the wave's candidate buffer into the sorted top-k lists of its 32
+// queries (global memory, [chunk][query][k]).  Wave-level: no block barrier.
+__device__ __forceinline__ void tk_flush(TkWave& W, uint32_t cnt, uint32_t k, uint32_t nq_wave, float* gd_row,
+                                      uint32_t* gi_row)
+{
+    const uint32_t lane = __lane_id();
+    for (uint32_t jj = 0; jj < nq_wave; ++jj) {
+        uint32_t nc = 0;
+        for (uint32_t e0 = 0; e0 < cnt; e0 += 64) {
+            const uint32_t e = e0 + lane;
+            const bool f = e < cnt && W.cq[e] == jj;
+            const uint64_t m = __ballot(f);
+            if (f) {
+                const uint32_t p = nc + static_cast<uint32_t>(__popcll(m & lanemask_lt()));
+                W.sd[p] = W.cd[e];
+                W.sid[p] = W.cid[e];
+            }
+            nc += static_cast<uint32_t>(__popcll(m));
+        }
+        if (nc == 0) continue;
+        const uint32_t n = W.ln[jj];
+        float* gd = gd_row + static_cast<size_t>(jj) * k;
+        uint32_t* gi = gi_row + static_cast<size_t>(jj) * k;
+        for (uint32_t i = lane; i < n; i += 64) {
+            W.ld[i] = gd[i];
+            W.lid[i] = gi[i];
+        }
+        __builtin_amdgcn_wave_barrier();
+        // New rank of a list entry = its index + candidates before it; of a
+        // candidate = candidates before it + list entries before it.  All
+        // (d, id) pairs are distinct, so the ranks are a permutation.
+        float xd[TK_KMAX / 64], yd[TK_CB / 64];
+        uint32_t xi[TK_KMAX / 64], rx[TK_KMAX / 64], yi[TK_CB / 64], ry[TK_CB / 64];
+#pragma unroll
+        for (uint32_t u = 0; u < TK_KMAX / 64; ++u) {
+            const uint32_t i = lane + 64 * u;
+            xd[u] = i < n ? W.ld[i] : 0.f;
+            xi[u] = i < n ? W.lid[i] : 0u;
+            rx[u] = i;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < TK_CB / 64; ++u) {
+            const uint32_t e = lane + 64 * u;
+            yd[u] = e < nc ? W.sd[e] : 0.f;
+            yi[u] = e < nc ? W.sid[e] : 0u;
+            ry[u] = e < nc ? tk_lower_bound(W.ld, W.lid, n, yd[u], yi[u]) : 0u;
+        }
+        for (uint32_t e = 0; e < nc; ++e) {
+            const float sd = W.sd[e];
+            const uint32_t si = W.sid[e];
+#pragma unroll
+            for (uint32_t u = 0; u < TK_KMAX / 64; ++u) rx[u] += tk_less(sd, si, xd[u], xi[u]) ? 1u : 0u;
+#pragma unroll
+            for (uint32_t u = 0; u < TK_CB / 64; ++u) ry[u] += tk_less(sd, si, yd[u], yi[u]) ? 1u : 0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < TK_KMAX / 64; ++u) {
+            if (lane + 64 * u < n && rx[u] < k) {
+                gd[rx[u]] = xd[u];
+                gi[rx[u]] = xi[u];
+                if (rx[u] == k - 1) {
+                    W.td[jj] = xd[u];
+                    W.tid[jj] = xi[u];
+                }
+            }
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < TK_CB / 64; ++u) {
+            if (lane + 64 * u < nc && ry[u] < k) {
+                gd[ry[u]] = yd[u];
+                gi[ry[u]] = yi[u];
+                if (ry[u] == k - 1) {
+                    W.td[jj] = yd[u];
+                    W.tid[jj] = yi[u];
+                }
+            }
+        }
+        if (lane == 0) W.ln[jj] = min(k, n + nc);
+        __builtin_amdgcn_wave_barrier();
+    }
+    // The lists are re-read by this wave at its next merge.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+}
+
+template <int DP>
+__device__ __forceinline__ void tk_load_rows(const TkArgs& a, uint64_t row0, uint64_t row_end, float4 (&pre)[DP / 32],
+                                             uint32_t (&pid)[DP / 32])
+{
+    constexpr int TPR = DP / 4;            // threads per row (one float4 each)
+    constexpr int RPP = TK_NT / TPR;       // rows per pass
+    const uint32_t t = threadIdx.x;
+    const uint32_t c = (t % TPR) * 4;      // first column of this thread
+#pragma unroll
+    for (int p = 0; p < DP / 32; ++p) {
+        const uint64_t r = row0 + static_cast<uint64_t>(p * RPP + t / TPR);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        uint32_t id = TK_NOID;
+        if (r < row_end) {
+            id = a.sel ? a.sel[r] : static_cast<uint32_t>(r);
+            const float* src = a.base + static_cast<size_t>(id) * a.dim;
+            if (a.vec) {
+                if (c < a.dim) v = *reinterpret_cast<const float4*>(src + c);
+            } else {
+                if (c + 0 < a.dim) v.x = src[c + 0];
+                if (c + 1 < a.dim) v.y = src[c + 1];
+                if (c + 2 < a.dim) v.z = src[c + 2];
+                if (c + 3 < a.dim) v.w = src[c + 3];
+            }
+        }
+        pre[p] = v;
+        pid[p] = id;
+    }
+}
+
+template <int DP>
+__device__ __forceinline__ void tk_store_rows(TkLds<DP>& L, int buf, const float4 (&pre)[DP / 32],
+                                              const uint32_t (&pid)[DP / 32])
+{
+    constexpr int TPR = DP / 4;
+    constexpr int RPP = TK_NT / TPR;
+    const uint32_t t = threadIdx.x;
+#pragma unroll
+    for (int p = 0; p < DP / 32; ++p) {
+        const int row = p * RPP + static_cast<int>(t / TPR);
+        const int c = static_cast<int>(t % TPR) * 4;
+        *reinterpret_cast<float4*>(&L.tile[buf][row * (DP + 4) + c]) = pre[p];
+        float ss = pre[p].x * pre[p].x + pre[p].y * pre[p].y + pre[p].z * pre[p].z + pre[p].w * pre[p].w;
+#pragma unroll
+        for (int o = TPR / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if (c == 0) {
+            L.xn[buf][row] = ss;
+            L.id[buf][row] = pid[p];
+        }
+    }
+}
+
+template <int DP>
+__global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
+{
+    __shared__ TkLds<DP> L;
+    const uint32_t lane = __lane_id();
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t h = lane >> 5;    // lane half: which half of the dimensions it feeds
+    const uint32_t j = lane & 31u;   // query column of this lane
+    TkWave& W = L.w[wave];
+
+    // Blocks are dispatched round-robin over the 8 XCDs: the blocks of one XCD
+    // take consecutive query blocks of the same chunks, so they share the
+    // chunk's base rows in that XCD's L2.
+    const uint32_t n_qb = (a.n_q + TK_QB - 1) / TK_QB;
+    const uint32_t per_xcd = gridDim.x / 8;
+    const uint32_t pidx = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    const uint32_t chunk = pidx / n_qb;
+    const uint32_t qb = pidx % n_qb;
+
+    const uint64_t n_rows = a.sel ? static_cast<uint64_t>(*a.n_sel) : a.n_base;
+    const uint64_t rpc = ((n_rows + a.n_chunks - 1) / a.n_chunks + TK_ROWS - 1) / TK_ROWS * TK_ROWS;
+    const uint64_t r0 = std::min<uint64_t>(n_rows, static_cast<uint64_t>(chunk) * rpc);
+    const uint64_t r1 = std::min<uint64_t>(n_rows, r0 + rpc);
+    const uint32_t n_tiles = static_cast<uint32_t>((r1 - r0 + TK_ROWS - 1) / TK_ROWS);
+
+    const uint32_t q0 = qb * TK_QB + wave * TK_QW;
+    const uint32_t nq_wave = q0 < a.n_q ? std::min<uint32_t>(TK_QW, a.n_q - q0) : 0u;
+    const bool qok = j < nq_wave;
+    const size_t list_row = (static_cast<size_t>(chunk) * a.n_q + q0) * a.k;
+
+    if (lane < TK_QW) {
+        W.td[lane] = __builtin_inff();
+        W.tid[lane] = TK_NOID;
+        W.ln[lane] = 0;
+    }
+
+    // B operand: this lane's query, dimensions [h*DP/2, h*DP/2 + DP/2).
+    float qreg[DP / 2];
+    float qpart = 0.f;
+#pragma unroll
+    for (int s = 0; s < DP / 2; ++s) {
+        const uint32_t c = h * (DP / 2) + s;
+        qreg[s] = (qok && c < a.dim) ? a.queries[static_cast<size_t>(q0 + j) * a.dim + c] : 0.f;
+        qpart += qreg[s] * qreg[s];
+    }
+    const float qn = qpart + __shfl_xor(qpart, 32, 64);
+
+    float4 pre[DP / 32];
+    uint32_t pid[DP / 32];
+    if (n_tiles > 0) {
+        tk_load_rows<DP>(a, r0, r1, pre, pid);
+        tk_store_rows<DP>(L, 0, pre, pid);
+    }
+    __syncthreads();
+
+    float td = __builtin_inff();
+    uint32_t tidv = TK_NOID;
+    uint32_t cnt = 0;  // wave-uniform fill of the candidate buffer
+    for (uint32_t t = 0; t < n_tiles; ++t) {
+        const int b = static_cast<int>(t & 1u);
+        if (t + 1 < n_tiles) tk_load_rows<DP>(a, r0 + static_cast<uint64_t>(t + 1) * TK_ROWS, r1, pre, pid);
+
+        f32x16 acc0 = {}, acc1 = {};
+        if (nq_wave > 0) {
+            const float* A0 = &L.tile[b][j * (DP + 4) + h * (DP / 2)];
+            const float* A1 = A0 + 32 * (DP + 4);
+#pragma unroll
+            for (int s = 0; s < DP / 2; s += 4) {
+                const float4 x0 = *reinterpret_cast<const float4*>(A0 + s);
+                const float4 x1 = *reinterpret_cast<const float4*>(A1 + s);
+                acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.x, qreg[s + 0], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.x, qreg[s + 0], acc1, 0, 0, 0);
+                acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.y, qreg[s + 1], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.y, qreg[s + 1], acc1, 0, 0, 0);
+                acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.z, qreg[s + 2], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.z, qreg[s + 2], acc1, 0, 0, 0);
+                acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.w, qreg[s + 3], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.w, qreg[s + 3], acc1, 0, 0, 0);
+            }
+            // Accumulator register r of block u holds base row
+            // u*32 + 8*(r/4) + 4*h + r%4 against query column j.  The MFMA
+            // distance only gates: it may sit up to TK_GATE_ERR * (|q|^2 + |x|^2)
+            // from the fp32 distance, so a row passes the gate when that margin
+            // could put it before the query's k-th best.
+            uint32_t pm = 0;
+            uint32_t total = 0;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row0 = 8 * (r / 4) + static_cast<int>(4 * h) + (r % 4);
+                const uint32_t i0 = L.id[b][row0], i1 = L.id[b][row0 + 32];
+                const float x0 = L.xn[b][row0], x1 = L.xn[b][row0 + 32];
+                const float d0 = qn + x0 - 2.f * acc0[r];
+                const float d1 = qn + x1 - 2.f * acc1[r];
+                const bool p0 = qok && i0 != TK_NOID && d0 - TK_GATE_ERR * (qn + x0) <= td;
+                const bool p1 = qok && i1 != TK_NOID && d1 - TK_GATE_ERR * (qn + x1) <= td;
+                pm |= (p0 ? 1u : 0u) << r;
+                pm |= (p1 ? 1u : 0u) << (16 + r);
+                total += static_cast<uint32_t>(__popcll(__ballot(p0))) + static_cast<uint32_t>(__popcll(__ballot(p1)));
+            }
+            if (total) {
+                // Append in four groups of 8 registers (at most 512 entries each),
+                // merging the buffer first when a group would not fit.
+#pragma unroll 1
+                for (int g = 0; g < 4; ++g) {
+                    uint32_t tg = 0;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) tg += static_cast<uint32_t>(__popcll(__ballot((pm >> (8 * g + i)) & 1u)));
+                    if (tg == 0) continue;
+                    if (cnt + tg > TK_CB) {
+                        tk_flush(W, cnt, a.k, nq_wave, a.list_d + list_row, a.list_id + list_row);
+                        cnt = 0;
+                        td = W.td[j];
+                        tidv = W.tid[j];
+                    }
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const int rr = 8 * g + i;
+                        const bool f = (pm >> rr) & 1u;
+                        if (__ballot(f) == 0) continue;
+                        const int r = rr & 15;
+                        const int rbase = (rr >> 4) * 32 + 8 * (r / 4) + (r % 4);
+                        const int row = rbase + static_cast<int>(4 * h);         // this lane's row
+                        const int prow = rbase + static_cast<int>(4 * (1 - h));  // the partner lane's row
+                        // fp32 distance sum((q - x)^2): each lane sums its half of the
+                        // dimensions for its own row and for the partner's row, and the
+                        // pair exchanges the partner halves.
+                        const float* xm = &L.tile[b][row * (DP + 4) + h * (DP / 2)];
+                        const float* xp = &L.tile[b][prow * (DP + 4) + h * (DP / 2)];
+                        float em = 0.f, ep = 0.f;
+#pragma unroll
+                        for (int s2 = 0; s2 < DP / 2; s2 += 4) {
+                            const float4 u = *reinterpret_cast<const float4*>(xm + s2);
+                            const float4 v = *reinterpret_cast<const float4*>(xp + s2);
+                            float e;
+                            e = qreg[s2 + 0] - u.x; em = fmaf(e, e, em);
+                            e = qreg[s2 + 1] - u.y; em = fmaf(e, e, em);
+                            e = qreg[s2 + 2] - u.z; em = fmaf(e, e, em);
+                            e = qreg[s2 + 3] - u.w; em = fmaf(e, e, em);
+                            e = qreg[s2 + 0] - v.x; ep = fmaf(e, e, ep);
+                            e = qreg[s2 + 1] - v.y; ep = fmaf(e, e, ep);
+                            e = qreg[s2 + 2] - v.z; ep = fmaf(e, e, ep);
+                            e = qreg[s2 + 3] - v.w; ep = fmaf(e, e, ep);
+                        }
+                        const float d = em + __shfl_xor(ep, 32, 64);
+                        const uint32_t id = L.id[b][row];
+                        const bool f2 = f && tk_less(d, id, td, tidv);
+                        const uint64_t m = __ballot(f2);
+                        if (f2) {
+                            const uint32_t pos = cnt + static_cast<uint32_t>(__popcll(m & lanemask_lt()));
+                            W.cd[pos] = d;
+                            W.cid[pos] = id;
+                            W.cq[pos] = static_cast<uint8_t>(j);
+                        }
+                        cnt += static_cast<uint32_t>(__popcll(m));
+                    }
+                }
+            }
+        }
+        if (t + 1 < n_tiles) tk_store_rows<DP>(L, b ^ 1, pre, pid);
+        __syncthreads();
+    }
+    if (nq_wave > 0) {
+        if (cnt) tk_flush(W, cnt, a.k, nq_wave, a.list_d + list_row, a.list_id + list_row);
+        __builtin_amdgcn_wave_barrier();
+        if (lane < nq_wave) a.list_n[static_cast<size_t>(chunk) * a.n_q + q0 + lane] = W.ln[lane];
+    }
+}
+
+// ---- 3. merge of the chunk lists -------------------------------------------
+
+__global__ __launch_bounds__(TK_MERGE_NT) void tk_merge(const float* list_d, const uint32_t* list_id,
+                                                         const uint32_t* list_n, uint32_t n_chunks, uint32_t n_q,
+                                                         uint32_t k, float* out_d, int64_t* out_id)
+{
+    constexpr int W = TK_MERGE_NT / 64;
+    __shared__ float ad[W][2][TK_KMAX];
+    __shared__ uint32_t ai[W][2][TK_KMAX];
+    __shared__ float cd[W][TK_KMAX];
+    __shared__ uint32_t ci[W][TK_KMAX];
+    const uint32_t lane = __lane_id();
+    const uint32_t w = threadIdx.x >> 6;
+    const uint32_t q = blockIdx.x * W + w;
+    if (q >= n_q) return;  // whole wave; no block barrier below
+    uint32_t n = 0;
+    int cur = 0;
+    for (uint32_t c = 0; c < n_chunks; ++c) {
+        const size_t row = static_cast<size_t>(c) * n_q + q;
+        const uint32_t m = list_n[row];
+        if (m == 0) continue;
+        for (uint32_t i = lane; i < m; i += 64) {
+            cd[w][i] = list_d[row * k + i];
+            ci[w][i] = list_id[row * k + i];
+        }
+        __builtin_amdgcn_wave_barrier();
+        for (uint32_t i = lane; i < n; i += 64) {
+            const float x = ad[w][cur][i];
+            const uint32_t xi = ai[w][cur][i];
+            const uint32_t r = i + tk_lower_bound(cd[w], ci[w], m, x, xi);
+            if (r < k) {
+                ad[w][cur ^ 1][r] = x;
+                ai[w][cur ^ 1][r] = xi;
+            }
+        }
+        for (uint32_t e = lane; e < m; e += 64) {
+            const float y = cd[w][e];
+            const uint32_t yi = ci[w][e];
+            const uint32_t r = e + tk_lower_bound(ad[w][cur], ai[w][cur], n, y, yi);
+            if (r < k) {
+                ad[w][cur ^ 1][r] = y;
+                ai[w][cur ^ 1][r] = yi;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        n = min(k, n + m);
+        cur ^= 1;
+    }
+    for (uint32_t r = lane; r < k; r += 64) {
+        out_d[static_cast<size_t>(q) * k + r] = r < n ? ad[w][cur][r] : __builtin_inff();
+        out_id[static_cast<size_t>(q) * k + r] = r < n ? static_cast<int64_t>(ai[w][cur][r]) : int64_t(-1);
+    }
+}
+
+template <int DP>
+int launch_dist(const TkArgs& a, uint32_t grid, hipStream_t s)
+{
+    tk_dist<DP><<<grid, TK_NT, 0, s>>>(a);
+    CR_LAUNCH_CHECK();
+    return CR_OK;
+}
+
+}  // namespace
+}  // namespace crimpl
 
 using namespace crimpl;
 
-extern "C" int cr_topk_filtered(const float*, uint64_t, const float*, uint32_t, uint32_t, const cr_gpu_roaring*,
-                                uint32_t, float*, int64_t*, cr_stream_t)
+extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const float* d_queries, uint32_t n_q,
+                                uint32_t dim, const cr_gpu_roaring* filter, uint32_t k, float* d_out_dist,
+                                int64_t* d_out_ids, cr_stream_t stream)
 {
-    set_error("cr_topk_filtered: not built yet");
-    return CR_ERR_UNSUPPORTED;
+    if (n_q == 0 || k == 0) return CR_OK;
+    if (!d_queries || !d_out_dist || !d_out_ids || (n_base && !d_base) || dim == 0) {
+        set_error("cr_topk_filtered: invalid argument");
+        return CR_ERR_INVALID;
+    }
+    if (dim > 128 || k > TK_KMAX || n_base > 0xFFFFFFFFull) {
+        set_error("cr_topk_filtered: supported up to dim 128, k %u and 2^32-1 base vectors (dim %u, k %u)", TK_KMAX,
+                  dim, k);
+        return CR_ERR_UNSUPPORTED;
+    }
+    hipStream_t s = as_stream(stream);
+    const uint32_t n_qb = (n_q + TK_QB - 1) / TK_QB;
+    // Enough (chunk, query block) workgroups to cover every CU once.
+    const uint32_t cus = num_cus();
+    uint32_t n_chunks = std::max<uint32_t>(8, (cus + n_qb - 1) / n_qb);
+    n_chunks = (n_chunks + 7) / 8 * 8;
+    const uint64_t nb = (n_base + TK_ENUM_IDS - 1) / TK_ENUM_IDS;
+
+    Carver cv;
+    const size_t o_counts = cv.add(filter ? nb * 4 : 0);
+    const size_t o_nsel = cv.add(4);
+    const size_t o_sel = cv.add(filter ? n_base * 4 : 0);
+    const size_t lists = static_cast<size_t>(n_chunks) * n_q * k;
+    const size_t o_ld = cv.add(lists * 4);
+    const size_t o_li = cv.add(lists * 4);
+    const size_t o_ln = cv.add(static_cast<size_t>(n_chunks) * n_q * 4);
+    Scratch sc;
+    CR_RET(sc.alloc(cv.total, s));
+
+    TkArgs a{};
+    a.base = d_base;
+    a.queries = d_queries;
+    a.n_base = n_base;
+    a.n_q = n_q;
+    a.dim = dim;
+    a.k = k;
+    a.n_chunks = n_chunks;
+    a.vec = (dim % 4 == 0) && (reinterpret_cast<uintptr_t>(d_base) % 16 == 0);
+    a.list_d = sc.at<float>(o_ld);
+    a.list_id = sc.at<uint32_t>(o_li);
+    a.list_n = sc.at<uint32_t>(o_ln);
+    if (filter) {
+        cr_gpu_roaring_view cv_view;
+        CR_RET(cr_make_view(filter, &cv_view));
+        GpuRoaringView v;
+        static_assert(sizeof(v) == sizeof(cv_view), "view layout");
+        std::memcpy(&v, &cv_view, sizeof(v));
+        a.sel = sc.at<uint32_t>(o_sel);
+        a.n_sel = sc.at<uint32_t>(o_nsel);
+        if (nb == 0) {
+            CR_RET(fill_u32(sc.at<uint32_t>(o_nsel), 0u, 1, s));
+        } else {
+            CR_TIMED("tk_enum", s);
+            tk_enum_count<<<static_cast<unsigned>(nb), TK_ENUM_NT, 0, s>>>(v, n_base, sc.at<uint32_t>(o_counts));
+            tk_enum_write<<<static_cast<unsigned>(nb), TK_ENUM_NT, 0, s>>>(v, n_base, sc.at<uint32_t>(o_counts),
+                                                                           sc.at<uint32_t>(o_sel), sc.at<uint32_t>(o_nsel));
+        }
+        CR_LAUNCH_CHECK();
+    }
+    const uint32_t grid = n_chunks * n_qb;
+    {
+        CR_TIMED("tk_dist", s);
+        if (dim <= 32) {
+            CR_RET(launch_dist<32>(a, grid, s));
+        } else if (dim <= 64) {
+            CR_RET(launch_dist<64>(a, grid, s));
+        } else {
+            CR_RET(launch_dist<128>(a, grid, s));
+        }
+    }
+    {
+        CR_TIMED("tk_merge", s);
+        tk_merge<<<(n_q + 3) / 4, TK_MERGE_NT, 0, s>>>(a.list_d, a.list_id, a.list_n, n_chunks, n_q, k, d_out_dist,
+                                                        d_out_ids);
+    }
+    CR_LAUNCH_CHECK();
+    return CR_OK;
 }

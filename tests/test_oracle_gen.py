@@ -26,3 +26,46 @@ def test_canonical_double_matches_two_draw_formula():
 def test_splitmix64_known_answer():
     # splitmix64 with state 0: first output 0xE220A8397B1DCDAF (Vigna's reference).
     assert orc.splitmix64(0) == 0xE220A8397B1DCDAF
+
+
+def _topk_numpy(base, queries, k, passing):
+    """Independent closed form: full fp64 distance matrix, lexicographic (distance, id) sort."""
+    b = base.astype(np.float64)
+    ids = np.arange(base.shape[0]) if passing is None else np.nonzero(passing)[0]
+    out_d = np.full((queries.shape[0], k), np.inf)
+    out_i = np.full((queries.shape[0], k), -1, dtype=np.int64)
+    for q in range(queries.shape[0]):
+        d = ((b[ids] - queries[q].astype(np.float64)) ** 2).sum(axis=1)
+        order = np.lexsort((ids, d))[:k]
+        out_d[q, : len(order)] = d[order]
+        out_i[q, : len(order)] = ids[order]
+    return out_d, out_i
+
+
+def test_topk_bruteforce_matches_closed_form():
+    rng = np.random.default_rng(3)
+    base = rng.standard_normal((3000, 24)).astype(np.float32)
+    queries = rng.standard_normal((9, 24)).astype(np.float32)
+    for k, passing in ((1, None), (17, None), (64, (rng.random(3000) < 0.1).astype(np.uint8))):
+        got_d, got_i = orc.topk_bruteforce(base, queries, k, passing, n_threads=3)
+        want_d, want_i = _topk_numpy(base, queries, k, passing)
+        assert np.array_equal(got_i, want_i)
+        assert np.allclose(got_d, want_d, rtol=1e-12)
+
+
+def test_topk_bruteforce_ties_padding_and_empty():
+    rng = np.random.default_rng(4)
+    uniq = rng.standard_normal((5, 8)).astype(np.float32)
+    base = np.ascontiguousarray(np.repeat(uniq, 7, axis=0)[rng.permutation(35)])  # exact ties
+    queries = np.ascontiguousarray(uniq[:2])
+    got_d, got_i = orc.topk_bruteforce(base, queries, 12, None, n_threads=2)
+    want_d, want_i = _topk_numpy(base, queries, 12, None)
+    assert np.array_equal(got_i, want_i)  # ties: smaller id first
+    assert np.all(got_d[:, :7] == 0.0)
+    passing = np.zeros(35, np.uint8)
+    passing[[3, 30]] = 1
+    got_d, got_i = orc.topk_bruteforce(base, queries, 5, passing)
+    assert np.all(got_i[:, 2:] == -1) and np.all(np.isinf(got_d[:, 2:]))
+    assert sorted(got_i[0, :2].tolist()) == [3, 30]
+    got_d, got_i = orc.topk_bruteforce(base, queries, 3, np.zeros(35, np.uint8))
+    assert np.all(got_i == -1)
