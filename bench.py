@@ -15,8 +15,11 @@ Also reported (extra fields, measured in the same run):
   cpu_baseline  the CPU port (oracle/ orc_upload_from_ids: sort, unique, build)
                 on a 10M-id sample, scaled x10, 1 thread;
   secondary     set_operation AND of two 50% all-bitmap 2^30 bitmaps (GB/s of
-                algorithmic bytes) and point queries (Gq/s) on a 10% 2^30 bitmap,
-                cold (512 MiB flush before each timed call).
+                algorithmic bytes), fused multi_and over 3 and 8 bitmaps, and point
+                queries (Gq/s) on a 10% 2^30 bitmap, cold (512 MiB flush before
+                each timed call); the fused filtered top-k (10M x 128 fp32 base,
+                1024 queries, k = 10 and 100, multi_and filters at 0.1-50%
+                selectivity and unfiltered) with its fp32 MFMA utilisation.
 
 --gpus N with N > 1 exits: this build measures one GPU only.
 """
@@ -205,6 +208,114 @@ def secondary(torch, cr, flush):
     return out
 
 
+TK_N, TK_Q, TK_DIM = 10_000_000, 1024, 128
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def zipf_predicates(torch, targets, n_tags=10_000, per_vec=8, seed=52):
+    """Per-vector tags ~ Zipf(1.1) over ranks 1..n_tags (8 per vector); for each
+    target selectivity s, three predicates "has a tag in R_j" over disjoint random
+    rank sets R_j, each sized so that P(pass) ~= s^(1/3).  Returns
+    {s: (masks [3 x N bool], achieved selectivity of the AND)}."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    ranks = torch.arange(1, n_tags + 1, device="cuda", dtype=torch.float64)
+    w = ranks.pow(-1.1)
+    w /= w.sum()
+    cdf = torch.cumsum(w, 0)
+    u = torch.rand((TK_N, per_vec), device="cuda", generator=g, dtype=torch.float64)
+    tags = torch.searchsorted(cdf, u).clamp_(max=n_tags - 1)  # 0-based rank
+    del u
+    out = {}
+    for s in targets:
+        perm = torch.randperm(n_tags, device="cuda", generator=g)
+        p1 = s ** (1.0 / 3.0)
+        w_star = 1.0 - (1.0 - p1) ** (1.0 / per_vec)  # tag mass a rank set needs
+        masks, start = [], 0
+        for _ in range(3):
+            cum = torch.cumsum(w[perm[start:]], 0)
+            take = int(torch.searchsorted(cum, torch.tensor([w_star], device="cuda", dtype=torch.float64)).item()) + 1
+            sel = torch.zeros(n_tags, dtype=torch.bool, device="cuda")
+            sel[perm[start:start + take]] = True
+            start += take
+            masks.append(sel[tags].any(dim=1))
+        both = masks[0] & masks[1] & masks[2]
+        out[s] = (masks, float(both.float().mean().item()))
+    del tags
+    return out
+
+
+def topk_secondary(torch, cr, no_cpu):
+    """Fused filtered brute-force top-k (config 5): 10M x 128 fp32 base ~ N(0,1),
+    1024 queries, squared L2, k in {10, 100}, filter = multi_and of three Zipf-tag
+    predicates at selectivities 0.1/1/10/50%, plus the unfiltered control."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(50)
+    base = torch.randn((TK_N, TK_DIM), device="cuda", dtype=torch.float32, generator=g)
+    g.manual_seed(51)
+    queries = torch.randn((TK_Q, TK_DIM), device="cuda", dtype=torch.float32, generator=g)
+    preds = zipf_predicates(torch, (0.001, 0.01, 0.1, 0.5))
+    out = {"base": f"{TK_N} x {TK_DIM} fp32 N(0,1)", "queries": TK_Q}
+    runs = [("unfiltered", None, 1.0)]
+    for s, (masks, achieved) in preds.items():
+        gs = [cr.upload_from_device_ids(torch.nonzero(m).flatten().to(torch.int32), TK_N) for m in masks]
+        f = cr.multi_and(gs)
+        for x in gs:
+            cr.free(x)
+        runs.append((f"sel_{s:g}", f, achieved))
+    del preds
+    for k in (10, 100):
+        dist = torch.empty((TK_Q, k), device="cuda", dtype=torch.float32)
+        ids = torch.empty((TK_Q, k), device="cuda", dtype=torch.int64)
+        for name, f, sel in runs:
+            cr.topk_filtered(base, queries, k, f, dist, ids)
+            torch.cuda.synchronize()
+            cr.timing_enable(True)
+            ts = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                cr.topk_filtered(base, queries, k, f, dist, ids)
+                torch.cuda.synchronize()
+                ts.append((time.perf_counter() - t0) * 1e3)
+            rep = cr.timing_report()
+            cr.timing_enable(False)
+            t = median(ts)
+            n_pass = TK_N if f is None else int(round(sel * TK_N))
+            flops = 2.0 * TK_DIM * n_pass * TK_Q
+            kd = rep.get("tk_dist", (1, float("nan")))
+            kms = kd[1] / kd[0]
+            ok = bool((ids[:, 0] >= 0).all().item()) and bool((dist[:, 1:] >= dist[:, :-1]).all().item())
+            out[f"k{k}_{name}"] = {
+                "selectivity": round(sel, 6), "ms": round(t, 3), "qps": round(TK_Q / (t / 1e3), 1),
+                "tk_dist_ms": round(kms, 3),
+                "mfma_tflops": round(flops / (kms / 1e3) / 1e12, 2),
+                "mfma_frac_fp32_peak": round(flops / (kms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+                "kernels_ms": {kk: round(v[1] / v[0], 4) for kk, v in rep.items()}, "sane": ok,
+            }
+            log(f"topk k={k} {name}", out[f"k{k}_{name}"]["ms"], "ms", out[f"k{k}_{name}"]["mfma_frac_fp32_peak"])
+    for _, f, _ in runs:
+        if f is not None:
+            cr.free(f)
+    if not no_cpu:
+        # Bounded CPU sample: the oracle's threaded fp64 brute force (the reference's
+        # CPU path for this workload is a brute-force scan) on 1M base vectors x 16
+        # queries, unfiltered, k=10; QPS scaled to the 10M base.
+        import orc
+        nb, nq = 1_000_000, 16
+        hb = base[:nb].cpu().numpy()
+        hq = queries[:nq].cpu().numpy()
+        threads = min(16, os.cpu_count() or 1)
+        t0 = time.perf_counter()
+        orc.topk_bruteforce(hb, hq, 10, None, n_threads=threads)
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {"qps": round(nq / (dt * TK_N / nb), 3), "cores": threads, "kind": "port",
+                               "sample": "orc_topk_bruteforce (fp64, threaded) on 1M x 128 base, 16 queries, "
+                                         "k=10, unfiltered; QPS scaled to the 10M base"}
+    del base, queries
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(ids_host_sample):
     import ctypes as C
 
@@ -228,6 +339,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-topk", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the sharded design is "
@@ -361,6 +473,10 @@ def main():
         del d_ids
         torch.cuda.empty_cache()
         result["secondary"] = secondary(torch, cr, flush)
+        if not args.no_topk:
+            del flush
+            torch.cuda.empty_cache()
+            result["secondary"]["topk_10M_x128_q1024"] = topk_secondary(torch, cr, args.no_cpu)
     print(json.dumps(result), flush=True)
 
 
