@@ -121,85 +121,128 @@ struct TkArgs {
     float* list_d;      // [n_chunks][n_q][k]
     uint32_t* list_id;  // [n_chunks][n_q][k]
     uint32_t* list_n;   // [n_chunks][n_q]
+    uint32_t* tau;      // [n_q] bits of the smallest k-th distance any chunk has reached
 };
 
 // Per-wave selection state in LDS.
 struct TkWave {
     float cd[TK_CB];  // candidate buffer: distance, id, query slot (0..31)
     uint32_t cid[TK_CB];
-    float sd[TK_CB];  // one query's candidates during a merge
+    float sd[TK_CB];  // the buffer grouped by query during a merge
     uint32_t sid[TK_CB];
-    float ld[TK_KMAX];  // that query's current list
+    float ld[TK_KMAX];  // one query's current list during a merge
     uint32_t lid[TK_KMAX];
-    float td[TK_QW];  // threshold: the k-th best so far (+inf, NOID while the list is short)
+    float td[TK_QW];  // the query's k-th best so far (+inf, NOID while the list is short)
     uint32_t tid[TK_QW];
     uint32_t ln[TK_QW];  // list length
+    uint32_t qcnt[TK_QW];
+    uint32_t qoff[TK_QW];
     uint8_t cq[TK_CB];
 };
 
 template <int DP>
 struct TkLds {
     float tile[2][TK_ROWS * (DP + 4)];  // rows skewed by 16 B: conflict-free b128 reads
-    float xn[2][TK_ROWS];
+    float xg[2][TK_ROWS];               // (1 - TK_GATE_ERR) |x|^2, NaN for rows past the chunk
     uint32_t id[2][TK_ROWS];
     TkWave w[TK_WAVES];
 };
 
-// Merges the wave's candidate buffer into the sorted top-k lists of its 32
-// queries (global memory, [chunk][query][k]).  Wave-level: no block barrier.
+__device__ __forceinline__ float tk_atomic_load(const uint32_t* p)
+{
+    return __uint_as_float(__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+// Merges the wave's candidate buffer into the sorted top-k lists of its
+// queries (global memory, [chunk][query][k]) and publishes every full list's
+// k-th distance to the shared per-query bound.  Wave-level: no block barrier.
 __device__ __forceinline__ void tk_flush(TkWave& W, uint32_t cnt, uint32_t k, uint32_t nq_wave, float* gd_row,
-                                      uint32_t* gi_row)
+                                         uint32_t* gi_row, uint32_t* tau_q0)
 {
     const uint32_t lane = __lane_id();
-    for (uint32_t jj = 0; jj < nq_wave; ++jj) {
-        uint32_t nc = 0;
-        for (uint32_t e0 = 0; e0 < cnt; e0 += 64) {
-            const uint32_t e = e0 + lane;
-            const bool f = e < cnt && W.cq[e] == jj;
-            const uint64_t m = __ballot(f);
-            if (f) {
-                const uint32_t p = nc + static_cast<uint32_t>(__popcll(m & lanemask_lt()));
-                W.sd[p] = W.cd[e];
-                W.sid[p] = W.cid[e];
-            }
-            nc += static_cast<uint32_t>(__popcll(m));
+    // Group the buffer by query: per-query counts, offsets, scatter.
+    if (lane < TK_QW) W.qcnt[lane] = 0;
+    __builtin_amdgcn_wave_barrier();
+    uint32_t rk[TK_CB / 64];
+#pragma unroll
+    for (uint32_t u = 0; u < TK_CB / 64; ++u) {
+        const uint32_t e = lane + 64 * u;
+        rk[u] = e < cnt ? atomicAdd(&W.qcnt[W.cq[e]], 1u) : 0u;
+    }
+    __builtin_amdgcn_wave_barrier();
+    const uint32_t c_l = lane < TK_QW ? W.qcnt[lane] : 0u;
+    const uint32_t o_l = wave_incl_scan(c_l) - c_l;
+    if (lane < TK_QW) W.qoff[lane] = o_l;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (uint32_t u = 0; u < TK_CB / 64; ++u) {
+        const uint32_t e = lane + 64 * u;
+        if (e < cnt) {
+            const uint32_t p = W.qoff[W.cq[e]] + rk[u];
+            W.sd[p] = W.cd[e];
+            W.sid[p] = W.cid[e];
         }
-        if (nc == 0) continue;
-        const uint32_t n = W.ln[jj];
-        float* gd = gd_row + static_cast<size_t>(jj) * k;
-        uint32_t* gi = gi_row + static_cast<size_t>(jj) * k;
-        for (uint32_t i = lane; i < n; i += 64) {
-            W.ld[i] = gd[i];
-            W.lid[i] = gi[i];
-        }
-        __builtin_amdgcn_wave_barrier();
-        // New rank of a list entry = its index + candidates before it; of a
-        // candidate = candidates before it + list entries before it.  All
-        // (d, id) pairs are distinct, so the ranks are a permutation.
-        float xd[TK_KMAX / 64], yd[TK_CB / 64];
-        uint32_t xi[TK_KMAX / 64], rx[TK_KMAX / 64], yi[TK_CB / 64], ry[TK_CB / 64];
+    }
+    __builtin_amdgcn_wave_barrier();
+    uint64_t todo = __ballot(lane < nq_wave && c_l > 0);
+    // The list of the next query is loaded while the current one merges.
+    float pd[TK_KMAX / 64];
+    uint32_t pi[TK_KMAX / 64];
+    auto load_list = [&](uint32_t q) {
+        const uint32_t n = W.ln[q];
+        const float* gd = gd_row + static_cast<size_t>(q) * k;
+        const uint32_t* gi = gi_row + static_cast<size_t>(q) * k;
 #pragma unroll
         for (uint32_t u = 0; u < TK_KMAX / 64; ++u) {
             const uint32_t i = lane + 64 * u;
-            xd[u] = i < n ? W.ld[i] : 0.f;
-            xi[u] = i < n ? W.lid[i] : 0u;
-            rx[u] = i;
+            pd[u] = i < n ? gd[i] : 0.f;
+            pi[u] = i < n ? gi[i] : 0u;
         }
+    };
+    if (todo) load_list(static_cast<uint32_t>(__builtin_ctzll(todo)));
+    while (todo) {
+        const uint32_t jj = static_cast<uint32_t>(__builtin_ctzll(todo));
+        todo &= todo - 1;
+        const uint32_t n = W.ln[jj];
+        const uint32_t nc = W.qcnt[jj];
+        const uint32_t off = W.qoff[jj];
+        float xd[TK_KMAX / 64];
+        uint32_t xi[TK_KMAX / 64], rx[TK_KMAX / 64];
+#pragma unroll
+        for (uint32_t u = 0; u < TK_KMAX / 64; ++u) {
+            const uint32_t i = lane + 64 * u;
+            xd[u] = pd[u];
+            xi[u] = pi[u];
+            rx[u] = i;
+            if (i < n) {
+                W.ld[i] = xd[u];
+                W.lid[i] = xi[u];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (todo) load_list(static_cast<uint32_t>(__builtin_ctzll(todo)));
+        // New rank of a list entry = its index + candidates before it; of a
+        // candidate = candidates before it + list entries before it.  All
+        // (d, id) pairs are distinct, so the ranks are a permutation.
+        float yd[TK_CB / 64];
+        uint32_t yi[TK_CB / 64], ry[TK_CB / 64];
 #pragma unroll
         for (uint32_t u = 0; u < TK_CB / 64; ++u) {
             const uint32_t e = lane + 64 * u;
-            yd[u] = e < nc ? W.sd[e] : 0.f;
-            yi[u] = e < nc ? W.sid[e] : 0u;
+            yd[u] = e < nc ? W.sd[off + e] : 0.f;
+            yi[u] = e < nc ? W.sid[off + e] : 0u;
             ry[u] = e < nc ? tk_lower_bound(W.ld, W.lid, n, yd[u], yi[u]) : 0u;
         }
         for (uint32_t e = 0; e < nc; ++e) {
-            const float sd = W.sd[e];
-            const uint32_t si = W.sid[e];
+            const float sd = W.sd[off + e];
+            const uint32_t si = W.sid[off + e];
 #pragma unroll
             for (uint32_t u = 0; u < TK_KMAX / 64; ++u) rx[u] += tk_less(sd, si, xd[u], xi[u]) ? 1u : 0u;
 #pragma unroll
             for (uint32_t u = 0; u < TK_CB / 64; ++u) ry[u] += tk_less(sd, si, yd[u], yi[u]) ? 1u : 0u;
         }
+        float* gd = gd_row + static_cast<size_t>(jj) * k;
+        uint32_t* gi = gi_row + static_cast<size_t>(jj) * k;
 #pragma unroll
         for (uint32_t u = 0; u < TK_KMAX / 64; ++u) {
             if (lane + 64 * u < n && rx[u] < k) {
@@ -225,6 +268,7 @@ __device__ __forceinline__ void tk_flush(TkWave& W, uint32_t cnt, uint32_t k, ui
         if (lane == 0) W.ln[jj] = min(k, n + nc);
         __builtin_amdgcn_wave_barrier();
     }
+    if (lane < nq_wave && W.ln[lane] == k) atomicMin(tau_q0 + lane, __float_as_uint(W.td[lane]));
     // The lists are re-read by this wave at its next merge.
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
 }
@@ -275,10 +319,17 @@ __device__ __forceinline__ void tk_store_rows(TkLds<DP>& L, int buf, const float
 #pragma unroll
         for (int o = TPR / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
         if (c == 0) {
-            L.xn[buf][row] = ss;
+            L.xg[buf][row] = pid[p] != TK_NOID ? (1.f - TK_GATE_ERR) * ss : __builtin_nanf("");
             L.id[buf][row] = pid[p];
         }
     }
+}
+
+// Base row held by accumulator register rr (0..31: block rr/16, register
+// rr%16) of the lane half hh.
+__device__ __forceinline__ int tk_row(int rr, int hh)
+{
+    return (rr >> 4) * 32 + 8 * ((rr & 15) >> 2) + 4 * hh + (rr & 3);
 }
 
 template <int DP>
@@ -310,6 +361,7 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
     const uint32_t nq_wave = q0 < a.n_q ? std::min<uint32_t>(TK_QW, a.n_q - q0) : 0u;
     const bool qok = j < nq_wave;
     const size_t list_row = (static_cast<size_t>(chunk) * a.n_q + q0) * a.k;
+    uint32_t* tau_q0 = a.tau + q0;
 
     if (lane < TK_QW) {
         W.td[lane] = __builtin_inff();
@@ -326,7 +378,7 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
         qreg[s] = (qok && c < a.dim) ? a.queries[static_cast<size_t>(q0 + j) * a.dim + c] : 0.f;
         qpart += qreg[s] * qreg[s];
     }
-    const float qn = qpart + __shfl_xor(qpart, 32, 64);
+    const float qg = (1.f - TK_GATE_ERR) * (qpart + __shfl_xor(qpart, 32, 64));
 
     float4 pre[DP / 32];
     uint32_t pid[DP / 32];
@@ -336,15 +388,20 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
     }
     __syncthreads();
 
+    // Thresholds of this lane's query: the own list's k-th best (td, tidv) and
+    // the bound shared by all chunks (tsh).  A row whose distance exceeds
+    // either cannot be in the answer.
     float td = __builtin_inff();
     uint32_t tidv = TK_NOID;
+    float tsh = __builtin_inff();
     uint32_t cnt = 0;  // wave-uniform fill of the candidate buffer
     for (uint32_t t = 0; t < n_tiles; ++t) {
         const int b = static_cast<int>(t & 1u);
         if (t + 1 < n_tiles) tk_load_rows<DP>(a, r0 + static_cast<uint64_t>(t + 1) * TK_ROWS, r1, pre, pid);
+        const float tsh_new = qok ? tk_atomic_load(tau_q0 + j) : __builtin_inff();
 
-        f32x16 acc0 = {}, acc1 = {};
         if (nq_wave > 0) {
+            f32x16 acc0 = {}, acc1 = {};
             const float* A0 = &L.tile[b][j * (DP + 4) + h * (DP / 2)];
             const float* A1 = A0 + 32 * (DP + 4);
 #pragma unroll
@@ -360,82 +417,78 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
                 acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.w, qreg[s + 3], acc0, 0, 0, 0);
                 acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.w, qreg[s + 3], acc1, 0, 0, 0);
             }
-            // Accumulator register r of block u holds base row
-            // u*32 + 8*(r/4) + 4*h + r%4 against query column j.  The MFMA
-            // distance only gates: it may sit up to TK_GATE_ERR * (|q|^2 + |x|^2)
-            // from the fp32 distance, so a row passes the gate when that margin
-            // could put it before the query's k-th best.
+            tsh = fminf(tsh, tsh_new);
+            // Gate: the MFMA distance |q|^2 + |x|^2 - 2 q.x lies within
+            // TK_GATE_ERR (|q|^2 + |x|^2) of the fp32 direct distance, so a
+            // row passes when that margin could put it at or below the
+            // thresholds.  Accumulator register r of block u holds base row
+            // tk_row(16u + r, h) against query column j.
+            const float tgate = fminf(td, tsh);
             uint32_t pm = 0;
-            uint32_t total = 0;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row0 = 8 * (r / 4) + static_cast<int>(4 * h) + (r % 4);
-                const uint32_t i0 = L.id[b][row0], i1 = L.id[b][row0 + 32];
-                const float x0 = L.xn[b][row0], x1 = L.xn[b][row0 + 32];
-                const float d0 = qn + x0 - 2.f * acc0[r];
-                const float d1 = qn + x1 - 2.f * acc1[r];
-                const bool p0 = qok && i0 != TK_NOID && d0 - TK_GATE_ERR * (qn + x0) <= td;
-                const bool p1 = qok && i1 != TK_NOID && d1 - TK_GATE_ERR * (qn + x1) <= td;
-                pm |= (p0 ? 1u : 0u) << r;
-                pm |= (p1 ? 1u : 0u) << (16 + r);
-                total += static_cast<uint32_t>(__popcll(__ballot(p0))) + static_cast<uint32_t>(__popcll(__ballot(p1)));
+            for (int rq = 0; rq < 4; ++rq) {
+                const float4 g0 = *reinterpret_cast<const float4*>(&L.xg[b][8 * rq + 4 * h]);
+                const float4 g1 = *reinterpret_cast<const float4*>(&L.xg[b][32 + 8 * rq + 4 * h]);
+                pm |= (qg + g0.x - 2.f * acc0[4 * rq + 0] <= tgate ? 1u : 0u) << (4 * rq + 0);
+                pm |= (qg + g0.y - 2.f * acc0[4 * rq + 1] <= tgate ? 1u : 0u) << (4 * rq + 1);
+                pm |= (qg + g0.z - 2.f * acc0[4 * rq + 2] <= tgate ? 1u : 0u) << (4 * rq + 2);
+                pm |= (qg + g0.w - 2.f * acc0[4 * rq + 3] <= tgate ? 1u : 0u) << (4 * rq + 3);
+                pm |= (qg + g1.x - 2.f * acc1[4 * rq + 0] <= tgate ? 1u : 0u) << (16 + 4 * rq + 0);
+                pm |= (qg + g1.y - 2.f * acc1[4 * rq + 1] <= tgate ? 1u : 0u) << (16 + 4 * rq + 1);
+                pm |= (qg + g1.z - 2.f * acc1[4 * rq + 2] <= tgate ? 1u : 0u) << (16 + 4 * rq + 2);
+                pm |= (qg + g1.w - 2.f * acc1[4 * rq + 3] <= tgate ? 1u : 0u) << (16 + 4 * rq + 3);
             }
-            if (total) {
-                // Append in four groups of 8 registers (at most 512 entries each),
-                // merging the buffer first when a group would not fit.
-#pragma unroll 1
-                for (int g = 0; g < 4; ++g) {
-                    uint32_t tg = 0;
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) tg += static_cast<uint32_t>(__popcll(__ballot((pm >> (8 * g + i)) & 1u)));
-                    if (tg == 0) continue;
-                    if (cnt + tg > TK_CB) {
-                        tk_flush(W, cnt, a.k, nq_wave, a.list_d + list_row, a.list_id + list_row);
+            if (!qok) pm = 0;
+            if (__ballot(pm != 0)) {
+                // Both lanes of a query (j and j + 32) walk the query's gated
+                // rows in the same order; each sums its half of the dimensions
+                // and the pair adds the halves.
+                uint32_t m0 = __shfl(pm, static_cast<int>(j), 64);
+                uint32_t m1 = __shfl(pm, static_cast<int>(j + 32), 64);
+                while (__ballot((m0 | m1) != 0)) {
+                    if (cnt + TK_QW > TK_CB) {
+                        tk_flush(W, cnt, a.k, nq_wave, a.list_d + list_row, a.list_id + list_row, tau_q0);
                         cnt = 0;
                         td = W.td[j];
                         tidv = W.tid[j];
+                        if (qok) tsh = fminf(tsh, tk_atomic_load(tau_q0 + j));
                     }
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const int rr = 8 * g + i;
-                        const bool f = (pm >> rr) & 1u;
-                        if (__ballot(f) == 0) continue;
-                        const int r = rr & 15;
-                        const int rbase = (rr >> 4) * 32 + 8 * (r / 4) + (r % 4);
-                        const int row = rbase + static_cast<int>(4 * h);         // this lane's row
-                        const int prow = rbase + static_cast<int>(4 * (1 - h));  // the partner lane's row
-                        // fp32 distance sum((q - x)^2): each lane sums its half of the
-                        // dimensions for its own row and for the partner's row, and the
-                        // pair exchanges the partner halves.
-                        const float* xm = &L.tile[b][row * (DP + 4) + h * (DP / 2)];
-                        const float* xp = &L.tile[b][prow * (DP + 4) + h * (DP / 2)];
-                        float em = 0.f, ep = 0.f;
+                    int row = -1;
+                    if (m0) {
+                        row = tk_row(__builtin_ctz(m0), 0);
+                        m0 &= m0 - 1;
+                    } else if (m1) {
+                        row = tk_row(__builtin_ctz(m1), 1);
+                        m1 &= m1 - 1;
+                    }
+                    float e2 = 0.f;
+                    if (row >= 0) {
+                        const float* xr = &L.tile[b][row * (DP + 4) + h * (DP / 2)];
 #pragma unroll
                         for (int s2 = 0; s2 < DP / 2; s2 += 4) {
-                            const float4 u = *reinterpret_cast<const float4*>(xm + s2);
-                            const float4 v = *reinterpret_cast<const float4*>(xp + s2);
+                            const float4 v = *reinterpret_cast<const float4*>(xr + s2);
                             float e;
-                            e = qreg[s2 + 0] - u.x; em = fmaf(e, e, em);
-                            e = qreg[s2 + 1] - u.y; em = fmaf(e, e, em);
-                            e = qreg[s2 + 2] - u.z; em = fmaf(e, e, em);
-                            e = qreg[s2 + 3] - u.w; em = fmaf(e, e, em);
-                            e = qreg[s2 + 0] - v.x; ep = fmaf(e, e, ep);
-                            e = qreg[s2 + 1] - v.y; ep = fmaf(e, e, ep);
-                            e = qreg[s2 + 2] - v.z; ep = fmaf(e, e, ep);
-                            e = qreg[s2 + 3] - v.w; ep = fmaf(e, e, ep);
+                            e = qreg[s2 + 0] - v.x; e2 = fmaf(e, e, e2);
+                            e = qreg[s2 + 1] - v.y; e2 = fmaf(e, e, e2);
+                            e = qreg[s2 + 2] - v.z; e2 = fmaf(e, e, e2);
+                            e = qreg[s2 + 3] - v.w; e2 = fmaf(e, e, e2);
                         }
-                        const float d = em + __shfl_xor(ep, 32, 64);
-                        const uint32_t id = L.id[b][row];
-                        const bool f2 = f && tk_less(d, id, td, tidv);
-                        const uint64_t m = __ballot(f2);
-                        if (f2) {
-                            const uint32_t pos = cnt + static_cast<uint32_t>(__popcll(m & lanemask_lt()));
-                            W.cd[pos] = d;
-                            W.cid[pos] = id;
-                            W.cq[pos] = static_cast<uint8_t>(j);
-                        }
-                        cnt += static_cast<uint32_t>(__popcll(m));
                     }
+                    const float d = e2 + __shfl_xor(e2, 32, 64);
+                    bool f = false;
+                    uint32_t id = 0;
+                    if (h == 0 && row >= 0) {
+                        id = L.id[b][row];
+                        f = tk_less(d, id, td, tidv) && d <= tsh;
+                    }
+                    const uint64_t m = __ballot(f);
+                    if (f) {
+                        const uint32_t pos = cnt + static_cast<uint32_t>(__popcll(m & lanemask_lt()));
+                        W.cd[pos] = d;
+                        W.cid[pos] = id;
+                        W.cq[pos] = static_cast<uint8_t>(j);
+                    }
+                    cnt += static_cast<uint32_t>(__popcll(m));
                 }
             }
         }
@@ -443,7 +496,7 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
         __syncthreads();
     }
     if (nq_wave > 0) {
-        if (cnt) tk_flush(W, cnt, a.k, nq_wave, a.list_d + list_row, a.list_id + list_row);
+        if (cnt) tk_flush(W, cnt, a.k, nq_wave, a.list_d + list_row, a.list_id + list_row, tau_q0);
         __builtin_amdgcn_wave_barrier();
         if (lane < nq_wave) a.list_n[static_cast<size_t>(chunk) * a.n_q + q0 + lane] = W.ln[lane];
     }
@@ -546,6 +599,7 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     const size_t o_ld = cv.add(lists * 4);
     const size_t o_li = cv.add(lists * 4);
     const size_t o_ln = cv.add(static_cast<size_t>(n_chunks) * n_q * 4);
+    const size_t o_tau = cv.add(static_cast<size_t>(n_q) * 4);
     Scratch sc;
     CR_RET(sc.alloc(cv.total, s));
 
@@ -561,6 +615,8 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     a.list_d = sc.at<float>(o_ld);
     a.list_id = sc.at<uint32_t>(o_li);
     a.list_n = sc.at<uint32_t>(o_ln);
+    a.tau = sc.at<uint32_t>(o_tau);
+    CR_RET(fill_u32(a.tau, 0x7F800000u, n_q, s));  // +inf
     if (filter) {
         cr_gpu_roaring_view cv_view;
         CR_RET(cr_make_view(filter, &cv_view));
