@@ -146,6 +146,7 @@ struct TkLds {
     float xg[2][TK_ROWS];               // (1 - TK_GATE_ERR) |x|^2, NaN for rows past the chunk
     uint32_t id[2][TK_ROWS];
     TkWave w[TK_WAVES];
+    uint32_t flush_req;  // tile index at which some wave asked every wave to merge
 };
 
 __device__ __forceinline__ float tk_atomic_load(const uint32_t* p)
@@ -206,62 +207,69 @@ __device__ __forceinline__ void tk_flush(TkWave& W, uint32_t cnt, uint32_t k, ui
         const uint32_t n = W.ln[jj];
         const uint32_t nc = W.qcnt[jj];
         const uint32_t off = W.qoff[jj];
-        float xd[TK_KMAX / 64];
-        uint32_t xi[TK_KMAX / 64], rx[TK_KMAX / 64];
 #pragma unroll
         for (uint32_t u = 0; u < TK_KMAX / 64; ++u) {
             const uint32_t i = lane + 64 * u;
-            xd[u] = pd[u];
-            xi[u] = pi[u];
-            rx[u] = i;
             if (i < n) {
-                W.ld[i] = xd[u];
-                W.lid[i] = xi[u];
+                W.ld[i] = pd[u];
+                W.lid[i] = pi[u];
             }
+        }
+        // The query's candidates, padded to a power of two with (+inf, NOID),
+        // sorted in cd/cid (free once the buffer is grouped) by a bitonic network.
+        uint32_t P = 1;
+        while (P < nc) P <<= 1;
+        for (uint32_t e = lane; e < P; e += 64) {
+            W.cd[e] = e < nc ? W.sd[off + e] : __builtin_inff();
+            W.cid[e] = e < nc ? W.sid[off + e] : TK_NOID;
         }
         __builtin_amdgcn_wave_barrier();
         if (todo) load_list(static_cast<uint32_t>(__builtin_ctzll(todo)));
-        // New rank of a list entry = its index + candidates before it; of a
-        // candidate = candidates before it + list entries before it.  All
-        // (d, id) pairs are distinct, so the ranks are a permutation.
-        float yd[TK_CB / 64];
-        uint32_t yi[TK_CB / 64], ry[TK_CB / 64];
-#pragma unroll
-        for (uint32_t u = 0; u < TK_CB / 64; ++u) {
-            const uint32_t e = lane + 64 * u;
-            yd[u] = e < nc ? W.sd[off + e] : 0.f;
-            yi[u] = e < nc ? W.sid[off + e] : 0u;
-            ry[u] = e < nc ? tk_lower_bound(W.ld, W.lid, n, yd[u], yi[u]) : 0u;
+        for (uint32_t size = 2; size <= P; size <<= 1) {
+            for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+                for (uint32_t pp = lane; pp < P / 2; pp += 64) {
+                    const uint32_t i = 2 * stride * (pp / stride) + (pp % stride);
+                    const uint32_t i2 = i + stride;
+                    const float a0 = W.cd[i], a1 = W.cd[i2];
+                    const uint32_t b0 = W.cid[i], b1 = W.cid[i2];
+                    const bool up = (i & size) == 0;
+                    if (tk_less(a1, b1, a0, b0) == up) {
+                        W.cd[i] = a1;
+                        W.cid[i] = b1;
+                        W.cd[i2] = a0;
+                        W.cid[i2] = b0;
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
         }
-        for (uint32_t e = 0; e < nc; ++e) {
-            const float sd = W.sd[off + e];
-            const uint32_t si = W.sid[off + e];
-#pragma unroll
-            for (uint32_t u = 0; u < TK_KMAX / 64; ++u) rx[u] += tk_less(sd, si, xd[u], xi[u]) ? 1u : 0u;
-#pragma unroll
-            for (uint32_t u = 0; u < TK_CB / 64; ++u) ry[u] += tk_less(sd, si, yd[u], yi[u]) ? 1u : 0u;
-        }
+        // Merge of two sorted runs: new rank = own index + entries of the other
+        // run before it (all (d, id) pairs are distinct).
         float* gd = gd_row + static_cast<size_t>(jj) * k;
         uint32_t* gi = gi_row + static_cast<size_t>(jj) * k;
-#pragma unroll
-        for (uint32_t u = 0; u < TK_KMAX / 64; ++u) {
-            if (lane + 64 * u < n && rx[u] < k) {
-                gd[rx[u]] = xd[u];
-                gi[rx[u]] = xi[u];
-                if (rx[u] == k - 1) {
-                    W.td[jj] = xd[u];
-                    W.tid[jj] = xi[u];
+        for (uint32_t i = lane; i < n; i += 64) {
+            const float x = W.ld[i];
+            const uint32_t xi = W.lid[i];
+            const uint32_t r = i + tk_lower_bound(W.cd, W.cid, nc, x, xi);
+            if (r < k) {
+                gd[r] = x;
+                gi[r] = xi;
+                if (r == k - 1) {
+                    W.td[jj] = x;
+                    W.tid[jj] = xi;
                 }
             }
         }
-#pragma unroll
-        for (uint32_t u = 0; u < TK_CB / 64; ++u) {
-            if (lane + 64 * u < nc && ry[u] < k) {
-                gd[ry[u]] = yd[u];
-                gi[ry[u]] = yi[u];
-                if (ry[u] == k - 1) {
-                    W.td[jj] = yd[u];
-                    W.tid[jj] = yi[u];
+        for (uint32_t e = lane; e < nc && e < k; e += 64) {
+            const float y = W.cd[e];
+            const uint32_t yi = W.cid[e];
+            const uint32_t r = e + tk_lower_bound(W.ld, W.lid, n, y, yi);
+            if (r < k) {
+                gd[r] = y;
+                gi[r] = yi;
+                if (r == k - 1) {
+                    W.td[jj] = y;
+                    W.tid[jj] = yi;
                 }
             }
         }
@@ -368,6 +376,7 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
         W.tid[lane] = TK_NOID;
         W.ln[lane] = 0;
     }
+    if (threadIdx.x == 0) L.flush_req = TK_NOID;
 
     // B operand: this lane's query, dimensions [h*DP/2, h*DP/2 + DP/2).
     float qreg[DP / 2];
@@ -492,8 +501,19 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
                 }
             }
         }
+        // Merges are taken together: a wave whose buffer is half full asks
+        // every wave to merge after the barrier, so the waves of the block
+        // stall for one merge at a time rather than one after another.
+        if (cnt > TK_CB / 2 && lane == 0) L.flush_req = t;
         if (t + 1 < n_tiles) tk_store_rows<DP>(L, b ^ 1, pre, pid);
         __syncthreads();
+        if (L.flush_req == t && cnt > 0) {
+            tk_flush(W, cnt, a.k, nq_wave, a.list_d + list_row, a.list_id + list_row, tau_q0);
+            cnt = 0;
+            td = W.td[j];
+            tidv = W.tid[j];
+            if (qok) tsh = fminf(tsh, tk_atomic_load(tau_q0 + j));
+        }
     }
     if (nq_wave > 0) {
         if (cnt) tk_flush(W, cnt, a.k, nq_wave, a.list_d + list_row, a.list_id + list_row, tau_q0);
