@@ -122,6 +122,8 @@ struct TkArgs {
     uint32_t* list_id;  // [n_chunks][n_q][k]
     uint32_t* list_n;   // [n_chunks][n_q]
     uint32_t* tau;      // [n_q] bits of the smallest k-th distance any chunk has reached
+    uint32_t* tau_m;    // [n_chunks][n_q] bits of each chunk's m_rank-th distance (+inf: fewer entries)
+    uint32_t m_rank;    // ceil(2k / n_chunks)
 };
 
 // Per-wave selection state in LDS.
@@ -133,6 +135,7 @@ struct TkWave {
     float ld[TK_KMAX];  // one query's current list during a merge
     uint32_t lid[TK_KMAX];
     float td[TK_QW];  // the query's k-th best so far (+inf, NOID while the list is short)
+    float tm[TK_QW];  // the query's m_rank-th best so far (+inf while the list is shorter)
     uint32_t tid[TK_QW];
     uint32_t ln[TK_QW];  // list length
     uint32_t qcnt[TK_QW];
@@ -154,11 +157,35 @@ __device__ __forceinline__ float tk_atomic_load(const uint32_t* p)
     return __uint_as_float(__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
+// Bound on the query's k-th distance from the chunks' m_rank-th distances: the
+// chunks that have published one hold at least m_rank rows each at or below
+// the largest of them, so once they number k / m_rank or more, that largest
+// value bounds the k-th distance of the union.  The lane pair of the query
+// (j, j + 32) splits the chunks between its two lanes.
+__device__ __forceinline__ float tk_spread_bound(const uint32_t* tau_m, uint32_t n_chunks, uint32_t n_q, uint32_t q,
+                                                 bool qok, uint32_t h, uint32_t k, uint32_t m_rank)
+{
+    float mx = 0.f;
+    uint32_t c_fin = 0;
+    if (qok) {
+        for (uint32_t c = h; c < n_chunks; c += 2) {
+            const float v = tk_atomic_load(tau_m + static_cast<size_t>(c) * n_q + q);
+            if (v != __builtin_inff()) {
+                ++c_fin;
+                mx = fmaxf(mx, v);
+            }
+        }
+    }
+    c_fin += __shfl_xor(c_fin, 32, 64);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    return c_fin * m_rank >= k ? mx : __builtin_inff();
+}
+
 // Merges the wave's candidate buffer into the sorted top-k lists of its
 // queries (global memory, [chunk][query][k]) and publishes every full list's
 // k-th distance to the shared per-query bound.  Wave-level: no block barrier.
-__device__ __forceinline__ void tk_flush(TkWave& W, uint32_t cnt, uint32_t k, uint32_t nq_wave, float* gd_row,
-                                         uint32_t* gi_row, uint32_t* tau_q0)
+__device__ __forceinline__ void tk_flush(TkWave& W, uint32_t cnt, uint32_t k, uint32_t m_rank, uint32_t nq_wave,
+                                         float* gd_row, uint32_t* gi_row, uint32_t* tau_q0, uint32_t* tau_m_q0)
 {
     const uint32_t lane = __lane_id();
     // Group the buffer by query: per-query counts, offsets, scatter.
@@ -258,6 +285,7 @@ __device__ __forceinline__ void tk_flush(TkWave& W, uint32_t cnt, uint32_t k, ui
                     W.td[jj] = x;
                     W.tid[jj] = xi;
                 }
+                if (r == m_rank - 1) W.tm[jj] = x;
             }
         }
         for (uint32_t e = lane; e < nc && e < k; e += 64) {
@@ -271,12 +299,18 @@ __device__ __forceinline__ void tk_flush(TkWave& W, uint32_t cnt, uint32_t k, ui
                     W.td[jj] = y;
                     W.tid[jj] = yi;
                 }
+                if (r == m_rank - 1) W.tm[jj] = y;
             }
         }
         if (lane == 0) W.ln[jj] = min(k, n + nc);
         __builtin_amdgcn_wave_barrier();
     }
-    if (lane < nq_wave && W.ln[lane] == k) atomicMin(tau_q0 + lane, __float_as_uint(W.td[lane]));
+    if (lane < nq_wave) {
+        if (W.ln[lane] == k) atomicMin(tau_q0 + lane, __float_as_uint(W.td[lane]));
+        if (W.ln[lane] >= m_rank)
+            __hip_atomic_store(tau_m_q0 + lane, __float_as_uint(W.tm[lane]), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
     // The lists are re-read by this wave at its next merge.
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
 }
@@ -370,9 +404,11 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
     const bool qok = j < nq_wave;
     const size_t list_row = (static_cast<size_t>(chunk) * a.n_q + q0) * a.k;
     uint32_t* tau_q0 = a.tau + q0;
+    uint32_t* tau_m_q0 = a.tau_m + static_cast<size_t>(chunk) * a.n_q + q0;
 
     if (lane < TK_QW) {
         W.td[lane] = __builtin_inff();
+        W.tm[lane] = __builtin_inff();
         W.tid[lane] = TK_NOID;
         W.ln[lane] = 0;
     }
@@ -456,11 +492,12 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
                 uint32_t m1 = __shfl(pm, static_cast<int>(j + 32), 64);
                 while (__ballot((m0 | m1) != 0)) {
                     if (cnt + TK_QW > TK_CB) {
-                        tk_flush(W, cnt, a.k, nq_wave, a.list_d + list_row, a.list_id + list_row, tau_q0);
+                        tk_flush(W, cnt, a.k, a.m_rank, nq_wave, a.list_d + list_row, a.list_id + list_row, tau_q0, tau_m_q0);
                         cnt = 0;
                         td = W.td[j];
                         tidv = W.tid[j];
                         if (qok) tsh = fminf(tsh, tk_atomic_load(tau_q0 + j));
+                        tsh = fminf(tsh, tk_spread_bound(a.tau_m, a.n_chunks, a.n_q, q0 + j, qok, h, a.k, a.m_rank));
                     }
                     int row = -1;
                     if (m0) {
@@ -504,19 +541,21 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
         // Merges are taken together: a wave whose buffer is half full asks
         // every wave to merge after the barrier, so the waves of the block
         // stall for one merge at a time rather than one after another.
-        if (cnt > TK_CB / 2 && lane == 0) L.flush_req = t;
+        if (cnt > TK_CB * 3 / 4 && lane == 0) L.flush_req = t;
         if (t + 1 < n_tiles) tk_store_rows<DP>(L, b ^ 1, pre, pid);
         __syncthreads();
         if (L.flush_req == t && cnt > 0) {
-            tk_flush(W, cnt, a.k, nq_wave, a.list_d + list_row, a.list_id + list_row, tau_q0);
+            tk_flush(W, cnt, a.k, a.m_rank, nq_wave, a.list_d + list_row, a.list_id + list_row, tau_q0, tau_m_q0);
             cnt = 0;
             td = W.td[j];
             tidv = W.tid[j];
             if (qok) tsh = fminf(tsh, tk_atomic_load(tau_q0 + j));
         }
+        if (nq_wave > 0 && (t & 7u) == 7u)
+            tsh = fminf(tsh, tk_spread_bound(a.tau_m, a.n_chunks, a.n_q, q0 + j, qok, h, a.k, a.m_rank));
     }
     if (nq_wave > 0) {
-        if (cnt) tk_flush(W, cnt, a.k, nq_wave, a.list_d + list_row, a.list_id + list_row, tau_q0);
+        if (cnt) tk_flush(W, cnt, a.k, a.m_rank, nq_wave, a.list_d + list_row, a.list_id + list_row, tau_q0, tau_m_q0);
         __builtin_amdgcn_wave_barrier();
         if (lane < nq_wave) a.list_n[static_cast<size_t>(chunk) * a.n_q + q0 + lane] = W.ln[lane];
     }
@@ -620,6 +659,7 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     const size_t o_li = cv.add(lists * 4);
     const size_t o_ln = cv.add(static_cast<size_t>(n_chunks) * n_q * 4);
     const size_t o_tau = cv.add(static_cast<size_t>(n_q) * 4);
+    const size_t o_taum = cv.add(static_cast<size_t>(n_chunks) * n_q * 4);
     Scratch sc;
     CR_RET(sc.alloc(cv.total, s));
 
@@ -636,7 +676,10 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     a.list_id = sc.at<uint32_t>(o_li);
     a.list_n = sc.at<uint32_t>(o_ln);
     a.tau = sc.at<uint32_t>(o_tau);
+    a.tau_m = sc.at<uint32_t>(o_taum);
+    a.m_rank = std::max<uint32_t>(1, (2 * k + n_chunks - 1) / n_chunks);
     CR_RET(fill_u32(a.tau, 0x7F800000u, n_q, s));  // +inf
+    CR_RET(fill_u32(a.tau_m, 0x7F800000u, static_cast<uint64_t>(n_chunks) * n_q, s));
     if (filter) {
         cr_gpu_roaring_view cv_view;
         CR_RET(cr_make_view(filter, &cv_view));
