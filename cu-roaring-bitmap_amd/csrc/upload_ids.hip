@@ -6,14 +6,17 @@
 // complement is stored when the distinct count exceeds U/2 (:356-410); up to
 // 1024 ids follow the threshold-aware small path (:421-561).
 //
-// The large path needs no sort.  Ids are partitioned by 16-key bucket
-// (1 MiB of id space), each bucket's 16 containers are built as 128 KiB of LDS
-// bitmaps (the bit-set dedupes), and each container is written once:
-//   hist      per-workgroup bucket histogram + key presence (read ids once)
-//   colscan   per-bucket prefix over workgroups, presence OR-reduce
-//   keyscan   bucket bases, key ranks -> keys/types/offsets/key_index
-//   partition scatter ids into their bucket's range (read ids again)
-//   build     one workgroup per bucket: LDS bit-set, popcount, write containers
+// The large path needs no global sort.  Ids are grouped by 16-key bucket
+// (1 MiB of id space) inside 16384-id tiles, each bucket's 16 containers are
+// built as 128 KiB of LDS bitmaps (the bit-set dedupes), and each container is
+// written once:
+//   tile_sort   read the ids once; counting-sort each tile by bucket in LDS and
+//               stream it back to the tile's own slot, with the tile's bucket
+//               starts in a small table; key presence per workgroup
+//   pres_reduce OR of the presence words
+//   keyscan     key ranks -> keys/types/offsets/key_index
+//   build       one workgroup per bucket: read the bucket's run of every tile
+//               (~16 ids at 2^30), LDS bit-set, popcount, write containers
 #include <algorithm>
 #include <vector>
 
@@ -23,9 +26,11 @@ namespace crimpl {
 
 constexpr uint32_t BK_SHIFT = 4;               // 16 keys per bucket
 constexpr uint32_t BK_KEYS = 1u << BK_SHIFT;
-constexpr int HP_NT = 1024;                    // hist / partition workgroup
 constexpr uint32_t MAX_BUCKETS = 65536 / BK_KEYS;
 constexpr uint32_t MAX_PWORDS = 65536 / 32;
+constexpr int TS_NT = 1024;                    // tile-sort workgroup
+constexpr uint32_t TS_PER = 16;                // ids per thread per tile
+constexpr uint32_t TILE = TS_NT * TS_PER;      // 16384 ids: 64 KiB of LDS, two workgroups per CU
 
 struct IdsTotals {
     uint32_t n_containers;
@@ -37,164 +42,160 @@ struct IdsTotals {
 
 struct IdsGeom {
     uint64_t n;
-    uint32_t chunk;  // ids per hist/partition workgroup
-    uint32_t G;      // hist/partition workgroups
-    uint32_t K;      // keys in the universe (max_key + 1)
-    uint32_t NB;     // buckets
-    uint32_t NW;     // presence words
-    bool vec;        // ids pointer 16-byte aligned (chunks are multiples of the tile)
+    uint32_t n_tiles;
+    uint32_t G;   // tile-sort workgroups
+    uint32_t K;   // keys in the universe (max_key + 1)
+    uint32_t NB;  // buckets
+    uint32_t NW;  // presence words
+    bool vec;     // ids pointer 16-byte aligned
 };
 
-// Ids are consumed in tiles of 8 per thread (8192 per workgroup): two 16-byte
-// loads per lane when the tile is whole and 16-byte aligned, else guarded
-// scalar loads.  `valid` marks the loaded slots.
-constexpr uint32_t TILE = 8 * HP_NT;
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) { return static_cast<uint32_t>(__popcll(m & ((1ull << __lane_id()) - 1ull))); }
 
-__device__ __forceinline__ void load_tile(const uint32_t* __restrict__ ids, uint64_t base, uint64_t hi, bool vec,
-                                          uint32_t (&v)[8], uint32_t& valid)
+// Each workgroup takes tiles round-robin.  A tile is counting-sorted by bucket
+// in LDS and written back to its own slot of `part` (tile t at t * TILE), a
+// streaming write; `tab` row t holds the tile's bucket starts (NB + 1 u16).
+// Ids whose key exceeds max_key are flagged and left out.  Key presence is
+// OR-ed per workgroup.
+__global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restrict__ ids, IdsGeom g,
+                                                       uint32_t* __restrict__ part, uint16_t* __restrict__ tab,
+                                                       uint32_t* gpres, IdsTotals* tot)
 {
-    const uint32_t t = threadIdx.x;
-    if (vec && base + TILE <= hi) {
-        const uint4 a = reinterpret_cast<const uint4*>(ids + base)[t];
-        const uint4 b = reinterpret_cast<const uint4*>(ids + base + TILE / 2)[t];
-        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
-        valid = 0xFFu;
-        return;
-    }
-    valid = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint64_t i = base + t + static_cast<uint64_t>(j) * HP_NT;
-        v[j] = 0;
-        if (i < hi) {
-            v[j] = ids[i];
-            valid |= 1u << j;
-        }
-    }
-}
-
-__global__ __launch_bounds__(HP_NT) void ids_hist(const uint32_t* __restrict__ ids, IdsGeom g, uint32_t* ghist,
-                                                  uint32_t* gpres, IdsTotals* tot)
-{
-    __shared__ uint32_t hist[MAX_BUCKETS];
+    __shared__ uint32_t buf[TILE];
+    __shared__ uint32_t cnt[MAX_BUCKETS + 1];
     __shared__ uint32_t pres[MAX_PWORDS];
+    __shared__ uint32_t lds[16];
     __shared__ uint32_t s_err, s_max;
     const uint32_t t = threadIdx.x;
-    for (uint32_t i = t; i < g.NB; i += HP_NT) hist[i] = 0;
-    for (uint32_t i = t; i < g.NW; i += HP_NT) pres[i] = 0;
+    const uint32_t lane = __lane_id();
+    for (uint32_t i = t; i < g.NW; i += TS_NT) pres[i] = 0;
     if (t == 0) {
         s_err = 0;
         s_max = 0;
     }
-    __syncthreads();
-    const uint64_t lo = static_cast<uint64_t>(blockIdx.x) * g.chunk;
-    const uint64_t hi = min(g.n, lo + g.chunk);
     const uint32_t max_key = g.K - 1;
     uint32_t err = 0, mx = 0;
-    uint32_t nv[8], nvalid = 0;
-    if (lo < hi) load_tile(ids, lo, hi, g.vec, nv, nvalid);
-    for (uint64_t base = lo; base < hi; base += TILE) {
-        uint32_t v[8], valid = nvalid;
+    for (uint32_t tile = blockIdx.x; tile < g.n_tiles; tile += g.G) {
+        const uint64_t base = static_cast<uint64_t>(tile) * TILE;
+        const uint64_t hi = min(g.n, base + TILE);
+        for (uint32_t i = t; i <= g.NB; i += TS_NT) cnt[i] = 0;
+        __syncthreads();
+        uint32_t v[TS_PER], valid = 0;
+        if (g.vec && hi - base == TILE) {
+            const uint4* src = reinterpret_cast<const uint4*>(ids + base);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = nv[j];
-        if (base + TILE < hi) load_tile(ids, base + TILE, hi, g.vec, nv, nvalid);  // prefetch
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if (!((valid >> j) & 1u)) continue;
-            const uint32_t id = v[j];
-            const uint32_t key = id >> 16;
-            mx = max(mx, id);
-            if (key > max_key) {
-                err = 1;
-                continue;
+            for (uint32_t q = 0; q < TS_PER / 4; ++q) {
+                const uint4 a = src[t + q * TS_NT];
+                v[4 * q + 0] = a.x, v[4 * q + 1] = a.y, v[4 * q + 2] = a.z, v[4 * q + 3] = a.w;
             }
-            atomicAdd(&hist[key >> BK_SHIFT], 1u);
-            const uint32_t bit = 1u << (key & 31u);
-            if (!(pres[key >> 5] & bit)) atomicOr(&pres[key >> 5], bit);
+            valid = ~0u;
+        } else {
+            const uint32_t* src = ids + base;  // wave-uniform base, 32-bit lane offsets
+            const uint32_t rem = static_cast<uint32_t>(hi - base);
+#pragma unroll
+            for (uint32_t j = 0; j < TS_PER; ++j) {
+                const uint32_t i = t + j * TS_NT;
+                v[j] = i < rem ? src[i] : 0u;
+                valid |= (i < rem ? 1u : 0u) << j;
+            }
         }
+        uint32_t rk[TS_PER / 2];  // tile ranks (< 16384) packed two per register
+#pragma unroll
+        for (uint32_t j = 0; j < TS_PER; ++j) {
+            const uint32_t key = v[j] >> 16;
+            bool ok = (valid >> j) & 1u;
+            if (ok) {
+                mx = max(mx, v[j]);
+                if (key > max_key) {
+                    err = 1;
+                    ok = false;
+                    valid &= ~(1u << j);
+                } else {
+                    const uint32_t bit = 1u << (key & 31u);
+                    if (!(pres[key >> 5] & bit)) atomicOr(&pres[key >> 5], bit);
+                }
+            }
+            // Clustered ids put a whole wave in one bucket: one atomic then.
+            const uint32_t b = key >> BK_SHIFT;
+            const uint64_t vm = __ballot(ok);
+            const uint32_t b0 = __builtin_amdgcn_readfirstlane(b);
+            const bool lane0_ok = vm & 1ull;
+            uint32_t r = 0;
+            if (lane0_ok && __ballot(ok && b != b0) == 0) {
+                uint32_t r0 = 0;
+                if (lane == 0) r0 = atomicAdd(&cnt[b0], static_cast<uint32_t>(__popcll(vm)));
+                r = __builtin_amdgcn_readfirstlane(r0) + lanes_below(vm);
+            } else if (ok) {
+                r = atomicAdd(&cnt[b], 1u);
+            }
+            if (j & 1u)
+                rk[j >> 1] |= r << 16;
+            else
+                rk[j >> 1] = r;
+        }
+        __syncthreads();
+        constexpr uint32_t BPT = MAX_BUCKETS / TS_NT;  // buckets scanned per thread
+        uint32_t cv[BPT], cs = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < BPT; ++q) {
+            const uint32_t bq = t * BPT + q;
+            cv[q] = bq < g.NB ? cnt[bq] : 0u;
+            cs += cv[q];
+        }
+        uint32_t total;
+        uint32_t st = block_excl_scan<TS_NT>(cs, lds, total);
+#pragma unroll
+        for (uint32_t q = 0; q < BPT; ++q) {
+            const uint32_t bq = t * BPT + q;
+            if (bq < g.NB) cnt[bq] = st;
+            st += cv[q];
+        }
+        if (t == 0) cnt[g.NB] = total;
+        __syncthreads();
+        uint16_t* trow = tab + static_cast<uint64_t>(tile) * (g.NB + 1);
+        for (uint32_t i = t; i <= g.NB; i += TS_NT) trow[i] = static_cast<uint16_t>(cnt[i]);
+#pragma unroll
+        for (uint32_t j = 0; j < TS_PER; ++j)
+            if ((valid >> j) & 1u) buf[cnt[v[j] >> (16 + BK_SHIFT)] + ((rk[j >> 1] >> ((j & 1u) * 16)) & 0xFFFFu)] = v[j];
+        __syncthreads();
+        uint32_t* dst = part + base;
+        const uint32_t n4 = total >> 2;
+        for (uint32_t p = t; p < n4; p += TS_NT) reinterpret_cast<uint4*>(dst)[p] = reinterpret_cast<const uint4*>(buf)[p];
+        for (uint32_t p = 4 * n4 + t; p < total; p += TS_NT) dst[p] = buf[p];
     }
     if (err) atomicOr(&s_err, 1u);
     atomicMax(&s_max, mx);
     __syncthreads();
-    uint32_t* oh = ghist + static_cast<uint64_t>(blockIdx.x) * g.NB;
-    for (uint32_t i = t; i < g.NB; i += HP_NT) oh[i] = hist[i];
     uint32_t* op = gpres + static_cast<uint64_t>(blockIdx.x) * g.NW;
-    for (uint32_t i = t; i < g.NW; i += HP_NT) op[i] = pres[i];
+    for (uint32_t i = t; i < g.NW; i += TS_NT) op[i] = pres[i];
     if (t == 0) {
         if (s_err) atomicOr(&tot->err, 1u);
         atomicMax(&tot->max_id, s_max);
     }
 }
 
-// One wave per column.  Columns [0, NB) are buckets: exclusive prefix over the
-// G workgroups (in place) and the bucket total.  Columns [NB, NB+NW) are
-// presence words: OR over workgroups.
-__global__ __launch_bounds__(1024) void ids_colscan(IdsGeom g, uint32_t* ghist, const uint32_t* gpres,
-                                                    uint32_t* btotal, uint32_t* pres)
+// One wave per presence word: OR over the tile-sort workgroups.
+__global__ __launch_bounds__(1024) void ids_pres_reduce(IdsGeom g, const uint32_t* gpres, uint32_t* pres)
 {
-    const uint32_t wave = (blockIdx.x * 1024u + threadIdx.x) >> 6;
+    const uint32_t w = (blockIdx.x * 1024u + threadIdx.x) >> 6;
     const uint32_t lane = __lane_id();
-    if (wave >= g.NB + g.NW) return;
-    const uint32_t per = (g.G + 63) / 64;  // workgroups per lane, contiguous
-    const uint32_t w0 = lane * per;
-    if (wave < g.NB) {
-        const uint32_t b = wave;
-        uint32_t s = 0;
-        for (uint32_t k = 0; k < per; ++k) {
-            const uint32_t w = w0 + k;
-            if (w < g.G) s += ghist[static_cast<uint64_t>(w) * g.NB + b];
-        }
-        const uint32_t incl = wave_incl_scan(s);
-        uint32_t run = incl - s;
-        for (uint32_t k = 0; k < per; ++k) {
-            const uint32_t w = w0 + k;
-            if (w < g.G) {
-                uint32_t* p = ghist + static_cast<uint64_t>(w) * g.NB + b;
-                const uint32_t v = *p;
-                *p = run;
-                run += v;
-            }
-        }
-        if (lane == 63) btotal[b] = incl;
-    } else {
-        const uint32_t j = wave - g.NB;
-        uint32_t acc = 0;
-        for (uint32_t k = 0; k < per; ++k) {
-            const uint32_t w = w0 + k;
-            if (w < g.G) acc |= gpres[static_cast<uint64_t>(w) * g.NW + j];
-        }
+    if (w >= g.NW) return;
+    uint32_t acc = 0;
+    for (uint32_t k = lane; k < g.G; k += 64) acc |= gpres[static_cast<uint64_t>(k) * g.NW + w];
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) acc |= __shfl_xor(acc, o, 64);
-        if (lane == 0) pres[j] = acc;
-    }
+    for (int o = 32; o > 0; o >>= 1) acc |= __shfl_xor(acc, o, 64);
+    if (lane == 0) pres[w] = acc;
 }
 
 // Key ranks, one thread per key and one workgroup per 1024 keys: the rank base
 // of a workgroup is the popcount of the presence words before it.  Writes
-// keys/types/offsets (coalesced) and the full key_index (0xFFFF = absent);
-// workgroup 0 also turns the bucket totals into bucket bases.
-__global__ __launch_bounds__(1024) void ids_keyscan(IdsGeom g, const uint32_t* btotal, const uint32_t* pres,
-                                                    uint32_t* bbase, uint16_t* keys, uint8_t* types, uint32_t* offsets,
-                                                    uint16_t* key_index, IdsTotals* tot)
+// keys/types/offsets (coalesced) and the full key_index (0xFFFF = absent).
+__global__ __launch_bounds__(1024) void ids_keyscan(IdsGeom g, const uint32_t* pres, uint16_t* keys, uint8_t* types,
+                                                    uint32_t* offsets, uint16_t* key_index, IdsTotals* tot)
 {
     __shared__ uint32_t lds[16];
     const uint32_t t = threadIdx.x;
     const uint32_t w = blockIdx.x;
-    if (w == 0) {  // bucket bases: 4 buckets per thread
-        uint32_t v[4], s = 0;
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t b = t * 4 + q;
-            v[q] = b < g.NB ? btotal[b] : 0u;
-            s += v[q];
-        }
-        uint32_t total;
-        uint32_t run = block_excl_scan<1024>(s, lds, total);
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t b = t * 4 + q;
-            if (b < g.NB) bbase[b] = run;
-            run += v[q];
-        }
-    }
     uint32_t before = 0;  // present keys below this workgroup's range (32 words per 1024 keys)
     for (uint32_t j = t; j < w * 32u; j += 1024u) before += __popc(pres[j]);
     before = block_sum<1024>(before, lds);
@@ -211,125 +212,78 @@ __global__ __launch_bounds__(1024) void ids_keyscan(IdsGeom g, const uint32_t* b
     if (t == 0 && w == gridDim.x - 1) tot->n_containers = before + here;
 }
 
-// Each 8192-id tile is counting-sorted by bucket in LDS first, so the global
-// writes leave as bucket-contiguous runs (consecutive lanes, consecutive
-// addresses) instead of one scattered 4-byte store per id.
-__global__ __launch_bounds__(HP_NT, 8) void ids_partition(const uint32_t* __restrict__ ids, IdsGeom g,
-                                                       const uint32_t* ghist_off, const uint32_t* bbase,
-                                                       uint32_t* __restrict__ part)
-{
-    // 64 KiB of LDS so two workgroups share a CU: the tile buffer, the global
-    // cursor of each bucket, and one array that first counts the tile's ids
-    // per bucket and is then scanned in place into tile-local bucket starts.
-    __shared__ uint32_t buf[TILE];
-    __shared__ uint32_t cur[MAX_BUCKETS];
-    __shared__ uint32_t ofs[MAX_BUCKETS + 1];
-    __shared__ uint32_t lds[16];
-    const uint32_t t = threadIdx.x;
-    const uint32_t* off = ghist_off + static_cast<uint64_t>(blockIdx.x) * g.NB;
-    for (uint32_t i = t; i < g.NB; i += HP_NT) cur[i] = bbase[i] + off[i];
-    const uint64_t lo = static_cast<uint64_t>(blockIdx.x) * g.chunk;
-    const uint64_t hi = min(g.n, lo + g.chunk);
-    const uint32_t max_key = g.K - 1;
-    constexpr uint32_t BPT = MAX_BUCKETS / HP_NT;  // buckets scanned per thread
-    // Two resident workgroups per CU overlap one's LDS phase with the other's loads.
-    for (uint64_t base = lo; base < hi; base += TILE) {
-        uint32_t v[8], valid, rank[4] = {0, 0, 0, 0};  // tile ranks (< 8192) packed two per register
-        load_tile(ids, base, hi, g.vec, v, valid);
-        for (uint32_t i = t; i <= g.NB; i += HP_NT) ofs[i] = 0;
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if (((valid >> j) & 1u) && (v[j] >> 16) <= max_key)
-            {
-                const uint32_t r = atomicAdd(&ofs[v[j] >> (16 + BK_SHIFT)], 1u);
-                rank[j >> 1] = (j & 1) ? (rank[j >> 1] | (r << 16)) : r;
-            }
-            else
-                valid &= ~(1u << j);
-        }
-        __syncthreads();
-        uint32_t s = 0;
-#pragma unroll
-        for (uint32_t q = 0; q < BPT; ++q) {
-            const uint32_t b = t * BPT + q;
-            s += b < g.NB ? ofs[b] : 0u;
-        }
-        uint32_t tile_n;
-        uint32_t run = block_excl_scan<HP_NT>(s, lds, tile_n);
-#pragma unroll
-        for (uint32_t q = 0; q < BPT; ++q) {  // each thread owns its BPT buckets: count -> start in place
-            const uint32_t b = t * BPT + q;
-            if (b < g.NB) {
-                const uint32_t c = ofs[b];
-                ofs[b] = run;
-                cur[b] -= run;  // cur[b] + p - ofs[b] == (cur[b] - ofs[b]) + p
-                run += c;
-            }
-        }
-        if (t == 0) ofs[g.NB] = tile_n;
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            if ((valid >> j) & 1u)
-                buf[ofs[v[j] >> (16 + BK_SHIFT)] + ((rank[j >> 1] >> ((j & 1) * 16)) & 0xFFFFu)] = v[j];
-        __syncthreads();
-        for (uint32_t p = t; p < tile_n; p += HP_NT) {
-            const uint32_t id = buf[p];
-            part[cur[id >> (16 + BK_SHIFT)] + p] = id;
-        }
-        __syncthreads();
-        for (uint32_t i = t; i < g.NB; i += HP_NT) cur[i] += ofs[i + 1];  // old cursor + count of the tile
-        __syncthreads();
-    }
-}
-
-// One workgroup per bucket: 16 containers as 16 x 2048 u32 LDS words (128 KiB).
+// One workgroup per bucket: its 16 containers as 16 x 2048 u32 LDS words
+// (128 KiB), filled from the bucket's run in every tile.  Four adjacent
+// buckets are dispatched to the same XCD (blocks go round-robin over the 8
+// XCDs), so the cache lines their runs share at run boundaries are L2 hits.
 // Normal mode writes the stored containers of present keys and each key's
 // distinct count; complement mode writes ~bits masked to [0, U) for keys whose
 // complement is non-empty.
 constexpr int BUILD_NT = 1024;
+constexpr uint32_t BUILD_WAVES = BUILD_NT / 64;
 
-__global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict__ part, const uint32_t* bbase,
-                                                      const uint32_t* btotal, IdsGeom g, uint32_t universe,
+inline uint32_t build_grid(uint32_t nb) { return (nb + 31) / 32 * 32; }
+
+__global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict__ part,
+                                                      const uint16_t* __restrict__ tab, IdsGeom g, uint32_t universe,
                                                       bool complement, const uint16_t* key_index,
                                                       uint64_t* __restrict__ pool, uint16_t* cards,
                                                       uint32_t* key_count, IdsTotals* tot)
 {
     __shared__ uint32_t bits[BK_KEYS * 2048u];  // 128 KiB of the CU's 160 KiB LDS
     const uint32_t t = threadIdx.x;
-    const uint32_t b = blockIdx.x;
+    const uint32_t xj = blockIdx.x / 8;
+    const uint32_t b = (xj / 4) * 32 + (blockIdx.x % 8) * 4 + xj % 4;
+    if (b >= g.NB) return;
     for (uint32_t i = t; i < BK_KEYS * 2048u; i += BUILD_NT) bits[i] = 0;
     __syncthreads();
-    const uint32_t start = bbase[b], cnt = btotal[b];
-    auto set_bit = [&](uint32_t id) {
-        const uint32_t local = (((id >> 16) & (BK_KEYS - 1)) << 11) | ((id & 0xFFFFu) >> 5);
-        atomicOr(&bits[local], 1u << (id & 31u));
-    };
-    // scalar head up to 16-byte alignment, 16-byte body (two loads in flight), scalar tail
-    const uint32_t head = min(cnt, (4u - (start & 3u)) & 3u);
-    if (t < head) set_bit(part[start + t]);
-    const uint32_t body = (cnt - head) & ~3u;
-    const uint4* p4 = reinterpret_cast<const uint4*>(part + start + head);
-    const uint32_t n4 = body >> 2;
-    constexpr uint32_t U4 = 4;  // 16-byte loads in flight per lane
-    for (uint32_t i = t; i < n4; i += U4 * BUILD_NT) {
-        uint4 x[U4];
+    const uint32_t wave = t >> 6;
+    const uint32_t lane = __lane_id();
+    const uint32_t grp = lane >> 4;  // four 16-lane groups, one tile each
+    const uint32_t r16 = lane & 15u;
+    const uint32_t trs = g.NB + 1;   // tab row stride
+    // Wave w takes tiles w, w + 16, ...: the run bounds of 64 of them are read
+    // at once (one tile per lane); each 16-lane group then reads one tile's
+    // run, 16 tiles per lane in flight.
+    for (uint32_t sb = 0; sb * 64u * BUILD_WAVES < g.n_tiles; ++sb) {
+        const uint32_t my_tile = wave + BUILD_WAVES * (sb * 64u + lane);
+        uint32_t ms0 = 0, ms1 = 0;
+        if (my_tile < g.n_tiles) {
+            const uint16_t* tr = tab + static_cast<uint64_t>(my_tile) * trs;
+            ms0 = tr[b];
+            ms1 = tr[b + 1];
+        }
+        uint32_t mlen = ms1 - ms0;
 #pragma unroll
-        for (uint32_t k = 0; k < U4; ++k)
-            x[k] = i + k * BUILD_NT < n4 ? p4[i + k * BUILD_NT] : make_uint4(0, 0, 0, 0);
+        for (int o = 32; o > 0; o >>= 1) mlen = max(mlen, static_cast<uint32_t>(__shfl_xor(mlen, o, 64)));
+        uint32_t s0[16], s1[16];
 #pragma unroll
-        for (uint32_t k = 0; k < U4; ++k) {
-            if (i + k * BUILD_NT >= n4) break;
-            set_bit(x[k].x), set_bit(x[k].y), set_bit(x[k].z), set_bit(x[k].w);
+        for (uint32_t u = 0; u < 16u; ++u) {
+            const int src = static_cast<int>(4u * u + grp);
+            const uint32_t tile = wave + BUILD_WAVES * (sb * 64u + 4u * u + grp);
+            s0[u] = __shfl(ms0, src, 64) + tile * TILE;  // element offsets into part (n < 2^32)
+            s1[u] = __shfl(ms1, src, 64) + tile * TILE;
+        }
+        for (uint32_t off = r16; off < mlen; off += 16u) {
+            uint32_t x[16], xm = 0;
+#pragma unroll
+            for (uint32_t u = 0; u < 16u; ++u) {
+                const uint32_t i = s0[u] + off;
+                x[u] = 0;
+                if (i < s1[u]) {
+                    x[u] = part[i];
+                    xm |= 1u << u;
+                }
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 16u; ++u)
+                if ((xm >> u) & 1u) atomicOr(&bits[((x[u] >> 16) & (BK_KEYS - 1)) << 11 | ((x[u] & 0xFFFFu) >> 5)],
+                                             1u << (x[u] & 31u));
         }
     }
-    const uint32_t tail0 = head + body;
-    if (tail0 + t < cnt) set_bit(part[start + tail0 + t]);
     __syncthreads();
-    __shared__ uint32_t wave_pc[BUILD_NT / 64];
-    const uint32_t c = t >> 6;  // wave c owns container c of the bucket
-    const uint32_t lane = __lane_id();
+    __shared__ uint32_t wave_pc[BUILD_WAVES];
+    const uint32_t c = wave;  // wave c owns container c of the bucket
     const uint32_t key = b * BK_KEYS + c;
     uint32_t pc = 0;
     if (key < g.K) {
@@ -364,7 +318,7 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
     __syncthreads();
     if (t == 0) {  // one device atomic per workgroup
         unsigned long long s = 0;
-        for (uint32_t i = 0; i < BUILD_NT / 64; ++i) s += wave_pc[i];
+        for (uint32_t i = 0; i < BUILD_WAVES; ++i) s += wave_pc[i];
         if (s) atomicAdd(&tot->total, s);
     }
 }
@@ -650,34 +604,24 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     g.K = max_key32 + 1u;
     g.NB = (g.K + BK_KEYS - 1) / BK_KEYS;
     g.NW = (g.K + 31) / 32;
-    const uint32_t cus = num_cus();
-    // Two 1024-lane workgroups per CU; chunks are whole 8192-id tiles.
-    uint64_t G = std::min<uint64_t>(2ull * cus, (static_cast<uint64_t>(n) + TILE - 1) / TILE);
-    if (G == 0) G = 1;
-    uint64_t chunk = (static_cast<uint64_t>(n) + G - 1) / G;
-    chunk = (chunk + TILE - 1) / TILE * TILE;
-    g.chunk = static_cast<uint32_t>(chunk);
-    g.G = static_cast<uint32_t>((static_cast<uint64_t>(n) + chunk - 1) / chunk);
+    g.n_tiles = static_cast<uint32_t>((static_cast<uint64_t>(n) + TILE - 1) / TILE);
+    g.G = std::max<uint32_t>(1, std::min<uint32_t>(2 * num_cus(), g.n_tiles));  // two 1024-lane workgroups per CU
     g.vec = (reinterpret_cast<uintptr_t>(d_ids) & 15u) == 0;
 
     Carver c;
-    const size_t o_hist = c.add(sizeof(uint32_t) * static_cast<uint64_t>(g.G) * g.NB);
     const size_t o_gpres = c.add(sizeof(uint32_t) * static_cast<uint64_t>(g.G) * g.NW);
-    const size_t o_bt = c.add(sizeof(uint32_t) * g.NB);
-    const size_t o_bb = c.add(sizeof(uint32_t) * g.NB);
     const size_t o_pres = c.add(sizeof(uint32_t) * g.NW);
     const size_t o_kc = c.add(sizeof(uint32_t) * g.K);
     const size_t o_tot = c.add(sizeof(IdsTotals));
+    const size_t o_tab = c.add(sizeof(uint16_t) * static_cast<uint64_t>(g.n_tiles) * (g.NB + 1));
     const size_t o_part = c.add(sizeof(uint32_t) * static_cast<uint64_t>(n));
     Scratch sc;
     CR_RET(sc.alloc(c.total, s));
-    uint32_t* ghist = sc.at<uint32_t>(o_hist);
     uint32_t* gpres = sc.at<uint32_t>(o_gpres);
-    uint32_t* btotal = sc.at<uint32_t>(o_bt);
-    uint32_t* bbase = sc.at<uint32_t>(o_bb);
     uint32_t* pres = sc.at<uint32_t>(o_pres);
     uint32_t* key_count = sc.at<uint32_t>(o_kc);
     IdsTotals* tot = sc.at<IdsTotals>(o_tot);
+    uint16_t* tab = sc.at<uint16_t>(o_tab);
     uint32_t* part = sc.at<uint32_t>(o_part);
 
     // Containers <= min(keys, ids): the pool is sized by that bound.
@@ -688,31 +632,25 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
 
     CR_RET(fill_u32(reinterpret_cast<uint32_t*>(tot), 0u, sizeof(IdsTotals) / 4, s));
     {
-        CR_TIMED("ids_hist", s);
-        ids_hist<<<g.G, HP_NT, 0, s>>>(d_ids, g, ghist, gpres, tot);
+        CR_TIMED("ids_tile_sort", s);
+        ids_tile_sort<<<g.G, TS_NT, 0, s>>>(d_ids, g, part, tab, gpres, tot);
     }
     CR_LAUNCH_CHECK();
-    const uint32_t cols = g.NB + g.NW;
     {
-        CR_TIMED("ids_colscan", s);
-        ids_colscan<<<(cols + 15) / 16, 1024, 0, s>>>(g, ghist, gpres, btotal, pres);
+        CR_TIMED("ids_pres_reduce", s);
+        ids_pres_reduce<<<(g.NW + 15) / 16, 1024, 0, s>>>(g, gpres, pres);
     }
     CR_LAUNCH_CHECK();
     {
         CR_TIMED("ids_keyscan", s);
-        ids_keyscan<<<(g.K + 1023) / 1024, 1024, 0, s>>>(g, btotal, pres, bbase, out->keys, out->types, out->offsets,
+        ids_keyscan<<<(g.K + 1023) / 1024, 1024, 0, s>>>(g, pres, out->keys, out->types, out->offsets,
                                                          out->key_index, tot);
     }
     CR_LAUNCH_CHECK();
     {
-        CR_TIMED("ids_partition", s);
-        ids_partition<<<g.G, HP_NT, 0, s>>>(d_ids, g, ghist, bbase, part);
-    }
-    CR_LAUNCH_CHECK();
-    {
         CR_TIMED("ids_build", s);
-        ids_build<<<g.NB, BUILD_NT, 0, s>>>(part, bbase, btotal, g, universe, false, out->key_index,
-                                                    out->bitmap_data, out->cardinalities, key_count, tot);
+        ids_build<<<build_grid(g.NB), BUILD_NT, 0, s>>>(part, tab, g, universe, false, out->key_index,
+                                                        out->bitmap_data, out->cardinalities, key_count, tot);
     }
     CR_LAUNCH_CHECK();
     IdsTotals h{};
@@ -748,7 +686,7 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     CR_LAUNCH_CHECK();
     {
         CR_TIMED("ids_build", s);
-        ids_build<<<g.NB, BUILD_NT, 0, s>>>(part, bbase, btotal, g, universe, true, comp.key_index,
+        ids_build<<<build_grid(g.NB), BUILD_NT, 0, s>>>(part, tab, g, universe, true, comp.key_index,
                                                     comp.bitmap_data, comp.cardinalities, nullptr, tot);
     }
     CR_LAUNCH_CHECK();
