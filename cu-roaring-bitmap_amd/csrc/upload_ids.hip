@@ -75,64 +75,86 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
     }
     const uint32_t max_key = g.K - 1;
     uint32_t err = 0, mx = 0;
-    for (uint32_t tile = blockIdx.x; tile < g.n_tiles; tile += g.G) {
-        const uint64_t base = static_cast<uint64_t>(tile) * TILE;
+    auto load_ids = [&](uint32_t tl, uint32_t (&w)[TS_PER], uint32_t& vm) {
+        const uint64_t base = static_cast<uint64_t>(tl) * TILE;
         const uint64_t hi = min(g.n, base + TILE);
-        for (uint32_t i = t; i <= g.NB; i += TS_NT) cnt[i] = 0;
-        __syncthreads();
-        uint32_t v[TS_PER], valid = 0;
+        vm = 0;
         if (g.vec && hi - base == TILE) {
             const uint4* src = reinterpret_cast<const uint4*>(ids + base);
 #pragma unroll
             for (uint32_t q = 0; q < TS_PER / 4; ++q) {
                 const uint4 a = src[t + q * TS_NT];
-                v[4 * q + 0] = a.x, v[4 * q + 1] = a.y, v[4 * q + 2] = a.z, v[4 * q + 3] = a.w;
+                w[4 * q + 0] = a.x, w[4 * q + 1] = a.y, w[4 * q + 2] = a.z, w[4 * q + 3] = a.w;
             }
-            valid = ~0u;
+            vm = ~0u;
         } else {
             const uint32_t* src = ids + base;  // wave-uniform base, 32-bit lane offsets
             const uint32_t rem = static_cast<uint32_t>(hi - base);
 #pragma unroll
             for (uint32_t j = 0; j < TS_PER; ++j) {
                 const uint32_t i = t + j * TS_NT;
-                v[j] = i < rem ? src[i] : 0u;
-                valid |= (i < rem ? 1u : 0u) << j;
+                w[j] = i < rem ? src[i] : 0u;
+                vm |= (i < rem ? 1u : 0u) << j;
             }
         }
-        uint32_t rk[TS_PER / 2];  // tile ranks (< 16384) packed two per register
+    };
+    // The next tile's ids are loaded while the current tile is ranked,
+    // scanned, scattered and written.
+    uint32_t v[TS_PER], valid = 0;
+    if (blockIdx.x < g.n_tiles) load_ids(blockIdx.x, v, valid);
+    for (uint32_t tile = blockIdx.x; tile < g.n_tiles; tile += g.G) {
+        const uint64_t base = static_cast<uint64_t>(tile) * TILE;
+        for (uint32_t i = t; i <= g.NB; i += TS_NT) cnt[i] = 0;
+        __syncthreads();
 #pragma unroll
         for (uint32_t j = 0; j < TS_PER; ++j) {
-            const uint32_t key = v[j] >> 16;
-            bool ok = (valid >> j) & 1u;
-            if (ok) {
+            if ((valid >> j) & 1u) {
                 mx = max(mx, v[j]);
-                if (key > max_key) {
+                if ((v[j] >> 16) > max_key) {
                     err = 1;
-                    ok = false;
                     valid &= ~(1u << j);
-                } else {
-                    const uint32_t bit = 1u << (key & 31u);
-                    if (!(pres[key >> 5] & bit)) atomicOr(&pres[key >> 5], bit);
                 }
             }
-            // Clustered ids put a whole wave in one bucket: one atomic then.
-            const uint32_t b = key >> BK_SHIFT;
-            const uint64_t vm = __ballot(ok);
-            const uint32_t b0 = __builtin_amdgcn_readfirstlane(b);
-            const bool lane0_ok = vm & 1ull;
-            uint32_t r = 0;
-            if (lane0_ok && __ballot(ok && b != b0) == 0) {
-                uint32_t r0 = 0;
-                if (lane == 0) r0 = atomicAdd(&cnt[b0], static_cast<uint32_t>(__popcll(vm)));
-                r = __builtin_amdgcn_readfirstlane(r0) + lanes_below(vm);
-            } else if (ok) {
-                r = atomicAdd(&cnt[b], 1u);
-            }
-            if (j & 1u)
-                rk[j >> 1] |= r << 16;
-            else
-                rk[j >> 1] = r;
         }
+        // Ranks within the tile.  When every id of the wave's pass falls in
+        // one bucket (clustered ids), a single atomic reserves them all.
+        uint32_t rk[TS_PER / 2];  // tile ranks (< 16384) packed two per register
+        const uint32_t b00 = __builtin_amdgcn_readfirstlane(v[0] >> (16 + BK_SHIFT));
+        bool diff = false;
+#pragma unroll
+        for (uint32_t j = 0; j < TS_PER; ++j) diff |= ((valid >> j) & 1u) && (v[j] >> (16 + BK_SHIFT)) != b00;
+        if (__ballot(diff) == 0) {
+            uint32_t count = 0;
+#pragma unroll
+            for (uint32_t j = 0; j < TS_PER; ++j) count += static_cast<uint32_t>(__popcll(__ballot((valid >> j) & 1u)));
+            uint32_t r0 = 0;
+            if (lane == 0 && count) r0 = atomicAdd(&cnt[b00], count);
+            uint32_t run = __builtin_amdgcn_readfirstlane(r0);
+#pragma unroll
+            for (uint32_t j = 0; j < TS_PER; ++j) {
+                const uint64_t m = __ballot((valid >> j) & 1u);
+                const uint32_t r = run + lanes_below(m);
+                run += static_cast<uint32_t>(__popcll(m));
+                if (j & 1u)
+                    rk[j >> 1] |= r << 16;
+                else
+                    rk[j >> 1] = r;
+            }
+        } else {
+#pragma unroll
+            for (uint32_t j = 0; j < TS_PER; ++j) {
+                const uint32_t r = ((valid >> j) & 1u) ? atomicAdd(&cnt[v[j] >> (16 + BK_SHIFT)], 1u) : 0u;
+                if (j & 1u)
+                    rk[j >> 1] |= r << 16;
+                else
+                    rk[j >> 1] = r;
+            }
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < TS_PER; ++j)
+            if ((valid >> j) & 1u) atomicOr(&pres[v[j] >> 21], 1u << ((v[j] >> 16) & 31u));
+        uint32_t vn[TS_PER], validn = 0;
+        if (tile + g.G < g.n_tiles) load_ids(tile + g.G, vn, validn);
         __syncthreads();
         constexpr uint32_t BPT = MAX_BUCKETS / TS_NT;  // buckets scanned per thread
         uint32_t cv[BPT], cs = 0;
@@ -162,6 +184,9 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         const uint32_t n4 = total >> 2;
         for (uint32_t p = t; p < n4; p += TS_NT) reinterpret_cast<uint4*>(dst)[p] = reinterpret_cast<const uint4*>(buf)[p];
         for (uint32_t p = 4 * n4 + t; p < total; p += TS_NT) dst[p] = buf[p];
+#pragma unroll
+        for (uint32_t j = 0; j < TS_PER; ++j) v[j] = vn[j];
+        valid = validn;
     }
     if (err) atomicOr(&s_err, 1u);
     atomicMax(&s_max, mx);
@@ -239,12 +264,12 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
     __syncthreads();
     const uint32_t wave = t >> 6;
     const uint32_t lane = __lane_id();
-    const uint32_t grp = lane >> 4;  // four 16-lane groups, one tile each
-    const uint32_t r16 = lane & 15u;
+    const uint32_t grp = lane >> 2;  // sixteen 4-lane groups, one tile each
+    const uint32_t r4 = lane & 3u;
     const uint32_t trs = g.NB + 1;   // tab row stride
     // Wave w takes tiles w, w + 16, ...: the run bounds of 64 of them are read
-    // at once (one tile per lane); each 16-lane group then reads one tile's
-    // run, 16 tiles per lane in flight.
+    // at once (one tile per lane).  Each 4-lane group then reads 16-id windows
+    // of four tiles' runs with 16-byte loads, aligned down to 4 ids.
     for (uint32_t sb = 0; sb * 64u * BUILD_WAVES < g.n_tiles; ++sb) {
         const uint32_t my_tile = wave + BUILD_WAVES * (sb * 64u + lane);
         uint32_t ms0 = 0, ms1 = 0;
@@ -253,32 +278,36 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
             ms0 = tr[b];
             ms1 = tr[b + 1];
         }
-        uint32_t mlen = ms1 - ms0;
+        uint32_t nw = ms1 > ms0 ? (ms1 - (ms0 & ~3u) + 15u) >> 4 : 0u;  // 16-id windows
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) mlen = max(mlen, static_cast<uint32_t>(__shfl_xor(mlen, o, 64)));
-        uint32_t s0[16], s1[16];
+        for (int o = 32; o > 0; o >>= 1) nw = max(nw, static_cast<uint32_t>(__shfl_xor(nw, o, 64)));
+        uint32_t ts0[4], ts1[4], tb[4];
 #pragma unroll
-        for (uint32_t u = 0; u < 16u; ++u) {
-            const int src = static_cast<int>(4u * u + grp);
-            const uint32_t tile = wave + BUILD_WAVES * (sb * 64u + 4u * u + grp);
-            s0[u] = __shfl(ms0, src, 64) + tile * TILE;  // element offsets into part (n < 2^32)
-            s1[u] = __shfl(ms1, src, 64) + tile * TILE;
+        for (uint32_t h = 0; h < 4u; ++h) {
+            const int src = static_cast<int>(16u * h + grp);
+            ts0[h] = __shfl(ms0, src, 64);
+            ts1[h] = __shfl(ms1, src, 64);
+            tb[h] = (wave + BUILD_WAVES * (sb * 64u + 16u * h + grp)) * TILE;  // n < 2^32
         }
-        for (uint32_t off = r16; off < mlen; off += 16u) {
-            uint32_t x[16], xm = 0;
+        for (uint32_t k = 0; k < nw; ++k) {
+            uint4 x[4];
+            uint32_t lo[4];
 #pragma unroll
-            for (uint32_t u = 0; u < 16u; ++u) {
-                const uint32_t i = s0[u] + off;
-                x[u] = 0;
-                if (i < s1[u]) {
-                    x[u] = part[i];
-                    xm |= 1u << u;
-                }
+            for (uint32_t h = 0; h < 4u; ++h) {
+                lo[h] = (ts0[h] & ~3u) + 16u * k + 4u * r4;
+                x[h] = lo[h] < ts1[h] ? *reinterpret_cast<const uint4*>(part + tb[h] + lo[h]) : make_uint4(0, 0, 0, 0);
             }
 #pragma unroll
-            for (uint32_t u = 0; u < 16u; ++u)
-                if ((xm >> u) & 1u) atomicOr(&bits[((x[u] >> 16) & (BK_KEYS - 1)) << 11 | ((x[u] & 0xFFFFu) >> 5)],
-                                             1u << (x[u] & 31u));
+            for (uint32_t h = 0; h < 4u; ++h) {
+                const uint32_t e4[4] = {x[h].x, x[h].y, x[h].z, x[h].w};
+#pragma unroll
+                for (uint32_t e = 0; e < 4u; ++e) {
+                    const uint32_t pos = lo[h] + e;
+                    if (pos >= ts0[h] && pos < ts1[h])
+                        atomicOr(&bits[((e4[e] >> 16) & (BK_KEYS - 1)) << 11 | ((e4[e] & 0xFFFFu) >> 5)],
+                                 1u << (e4[e] & 31u));
+                }
+            }
         }
     }
     __syncthreads();
@@ -614,7 +643,7 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     const size_t o_kc = c.add(sizeof(uint32_t) * g.K);
     const size_t o_tot = c.add(sizeof(IdsTotals));
     const size_t o_tab = c.add(sizeof(uint16_t) * static_cast<uint64_t>(g.n_tiles) * (g.NB + 1));
-    const size_t o_part = c.add(sizeof(uint32_t) * static_cast<uint64_t>(n));
+    const size_t o_part = c.add(sizeof(uint32_t) * (static_cast<uint64_t>(n) + 4));  // + window overrun
     Scratch sc;
     CR_RET(sc.alloc(c.total, s));
     uint32_t* gpres = sc.at<uint32_t>(o_gpres);
