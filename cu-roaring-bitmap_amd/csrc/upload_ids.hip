@@ -30,7 +30,12 @@ constexpr uint32_t MAX_BUCKETS = 65536 / BK_KEYS;
 constexpr uint32_t MAX_PWORDS = 65536 / 32;
 constexpr int TS_NT = 1024;                    // tile-sort workgroup
 constexpr uint32_t TS_PER = 16;                // ids per thread per tile
-constexpr uint32_t TILE = TS_NT * TS_PER;      // 16384 ids: 64 KiB of LDS, two workgroups per CU
+constexpr uint32_t TILE = TS_NT * TS_PER;      // 16384 ids: 64 KiB of LDS
+// Run table: tiles are grouped in blocks of TB; entry (block, bucket, slot) is
+// the start of the bucket in tile block*TB + slot, so one bucket's starts for
+// a block are TB contiguous u16 (the build reads a bucket's column).  The tile
+// sort hands out whole blocks, so a block's rows fill up in one workgroup.
+constexpr uint32_t TB = 8;
 
 struct IdsTotals {
     uint32_t n_containers;
@@ -101,8 +106,11 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
     // The next tile's ids are loaded while the current tile is ranked,
     // scanned, scattered and written.
     uint32_t v[TS_PER], valid = 0;
-    if (blockIdx.x < g.n_tiles) load_ids(blockIdx.x, v, valid);
-    for (uint32_t tile = blockIdx.x; tile < g.n_tiles; tile += g.G) {
+    // Workgroup g takes blocks g, g + G, ...; `next` steps through them.
+    auto next = [&](uint32_t tl) { return (tl % TB != TB - 1) ? tl + 1 : tl + 1 + (g.G - 1) * TB; };
+    const uint32_t first = blockIdx.x * TB;
+    if (first < g.n_tiles) load_ids(first, v, valid);
+    for (uint32_t tile = first; tile < g.n_tiles; tile = next(tile)) {
         const uint64_t base = static_cast<uint64_t>(tile) * TILE;
         for (uint32_t i = t; i <= g.NB; i += TS_NT) cnt[i] = 0;
         __syncthreads();
@@ -154,7 +162,7 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         for (uint32_t j = 0; j < TS_PER; ++j)
             if ((valid >> j) & 1u) atomicOr(&pres[v[j] >> 21], 1u << ((v[j] >> 16) & 31u));
         uint32_t vn[TS_PER], validn = 0;
-        if (tile + g.G < g.n_tiles) load_ids(tile + g.G, vn, validn);
+        if (next(tile) < g.n_tiles) load_ids(next(tile), vn, validn);
         __syncthreads();
         constexpr uint32_t BPT = MAX_BUCKETS / TS_NT;  // buckets scanned per thread
         uint32_t cv[BPT], cs = 0;
@@ -174,8 +182,8 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         }
         if (t == 0) cnt[g.NB] = total;
         __syncthreads();
-        uint16_t* trow = tab + static_cast<uint64_t>(tile) * (g.NB + 1);
-        for (uint32_t i = t; i <= g.NB; i += TS_NT) trow[i] = static_cast<uint16_t>(cnt[i]);
+        uint16_t* tcol = tab + static_cast<uint64_t>(tile / TB) * (g.NB + 1) * TB + tile % TB;
+        for (uint32_t i = t; i <= g.NB; i += TS_NT) tcol[static_cast<uint64_t>(i) * TB] = static_cast<uint16_t>(cnt[i]);
 #pragma unroll
         for (uint32_t j = 0; j < TS_PER; ++j)
             if ((valid >> j) & 1u) buf[cnt[v[j] >> (16 + BK_SHIFT)] + ((rk[j >> 1] >> ((j & 1u) * 16)) & 0xFFFFu)] = v[j];
@@ -264,49 +272,73 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
     __syncthreads();
     const uint32_t wave = t >> 6;
     const uint32_t lane = __lane_id();
-    const uint32_t grp = lane >> 2;  // sixteen 4-lane groups, one tile each
+    const uint32_t grp = lane >> 2;  // sixteen 4-lane groups
     const uint32_t r4 = lane & 3u;
-    const uint32_t trs = g.NB + 1;   // tab row stride
-    // Wave w takes tiles w, w + 16, ...: the run bounds of 64 of them are read
-    // at once (one tile per lane).  Each 4-lane group then reads 16-id windows
-    // of four tiles' runs with 16-byte loads, aligned down to 4 ids.
-    for (uint32_t sb = 0; sb * 64u * BUILD_WAVES < g.n_tiles; ++sb) {
-        const uint32_t my_tile = wave + BUILD_WAVES * (sb * 64u + lane);
-        uint32_t ms0 = 0, ms1 = 0;
-        if (my_tile < g.n_tiles) {
-            const uint16_t* tr = tab + static_cast<uint64_t>(my_tile) * trs;
-            ms0 = tr[b];
-            ms1 = tr[b + 1];
+    const uint32_t n_blk = (g.n_tiles + TB - 1) / TB;
+    // Wave w owns tile blocks w, w + 16, ...; a step covers 64 / TB of them
+    // (one tile per lane, its run bounds loaded a step ahead: the TB lanes of
+    // a block read TB contiguous u16).  Each 4-lane group reads four tiles'
+    // runs as 16-id windows with 16-byte loads aligned down to 4 ids, and the
+    // loads of the first two windows are all issued before any bit is set.
+    constexpr uint32_t BPS = 64u / TB;  // blocks per step
+    const uint32_t per_wave = n_blk > wave ? (n_blk - wave + BUILD_WAVES - 1) / BUILD_WAVES : 0u;
+    auto tile_of = [&](uint32_t st, uint32_t l) { return (wave + BUILD_WAVES * (st * BPS + l / TB)) * TB + l % TB; };
+    auto tab_load = [&](uint32_t st, uint32_t& r0, uint32_t& r1) {
+        r0 = r1 = 0;
+        const uint32_t jb = st * BPS + lane / TB;
+        const uint32_t tile = tile_of(st, lane);
+        if (jb < per_wave && tile < g.n_tiles) {
+            const uint16_t* tc =
+                tab + (static_cast<uint64_t>(wave + BUILD_WAVES * jb) * (g.NB + 1) + b) * TB + lane % TB;
+            r0 = tc[0];
+            r1 = tc[TB];
         }
-        uint32_t nw = ms1 > ms0 ? (ms1 - (ms0 & ~3u) + 15u) >> 4 : 0u;  // 16-id windows
+    };
+    auto set_window = [&](const uint4& x, uint32_t lo, uint32_t s0, uint32_t s1) {
+        const uint32_t e4[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) {
+            const uint32_t pos = lo + e;
+            if (pos >= s0 && pos < s1)
+                atomicOr(&bits[((e4[e] >> 16) & (BK_KEYS - 1)) << 11 | ((e4[e] & 0xFFFFu) >> 5)], 1u << (e4[e] & 31u));
+        }
+    };
+    uint32_t n0, n1;
+    tab_load(0, n0, n1);
+    for (uint32_t st = 0; st * BPS < per_wave; ++st) {
+        const uint32_t m0 = n0, m1 = n1;
+        tab_load(st + 1, n0, n1);
+        uint32_t nw = m1 > m0 ? (m1 - (m0 & ~3u) + 15u) >> 4 : 0u;  // 16-id windows of this lane's tile
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) nw = max(nw, static_cast<uint32_t>(__shfl_xor(nw, o, 64)));
         uint32_t ts0[4], ts1[4], tb[4];
 #pragma unroll
         for (uint32_t h = 0; h < 4u; ++h) {
-            const int src = static_cast<int>(16u * h + grp);
-            ts0[h] = __shfl(ms0, src, 64);
-            ts1[h] = __shfl(ms1, src, 64);
-            tb[h] = (wave + BUILD_WAVES * (sb * 64u + 16u * h + grp)) * TILE;  // n < 2^32
+            const uint32_t src = 16u * h + grp;
+            ts0[h] = __shfl(m0, static_cast<int>(src), 64);
+            ts1[h] = __shfl(m1, static_cast<int>(src), 64);
+            tb[h] = tile_of(st, src) * TILE;  // n < 2^32 (tiles past the end have empty runs)
         }
-        for (uint32_t k = 0; k < nw; ++k) {
-            uint4 x[4];
-            uint32_t lo[4];
+        {
+            uint4 x[4][2];
 #pragma unroll
-            for (uint32_t h = 0; h < 4u; ++h) {
-                lo[h] = (ts0[h] & ~3u) + 16u * k + 4u * r4;
-                x[h] = lo[h] < ts1[h] ? *reinterpret_cast<const uint4*>(part + tb[h] + lo[h]) : make_uint4(0, 0, 0, 0);
-            }
+            for (uint32_t h = 0; h < 4u; ++h)
 #pragma unroll
-            for (uint32_t h = 0; h < 4u; ++h) {
-                const uint32_t e4[4] = {x[h].x, x[h].y, x[h].z, x[h].w};
-#pragma unroll
-                for (uint32_t e = 0; e < 4u; ++e) {
-                    const uint32_t pos = lo[h] + e;
-                    if (pos >= ts0[h] && pos < ts1[h])
-                        atomicOr(&bits[((e4[e] >> 16) & (BK_KEYS - 1)) << 11 | ((e4[e] & 0xFFFFu) >> 5)],
-                                 1u << (e4[e] & 31u));
+                for (uint32_t k = 0; k < 2u; ++k) {
+                    const uint32_t lo = (ts0[h] & ~3u) + 16u * k + 4u * r4;
+                    x[h][k] = lo < ts1[h] ? *reinterpret_cast<const uint4*>(part + tb[h] + lo) : make_uint4(0, 0, 0, 0);
                 }
+#pragma unroll
+            for (uint32_t h = 0; h < 4u; ++h)
+#pragma unroll
+                for (uint32_t k = 0; k < 2u; ++k)
+                    set_window(x[h][k], (ts0[h] & ~3u) + 16u * k + 4u * r4, ts0[h], ts1[h]);
+        }
+        for (uint32_t k = 2; k < nw; ++k) {  // runs longer than two windows (clustered ids)
+#pragma unroll
+            for (uint32_t h = 0; h < 4u; ++h) {
+                const uint32_t lo = (ts0[h] & ~3u) + 16u * k + 4u * r4;
+                if (lo < ts1[h]) set_window(*reinterpret_cast<const uint4*>(part + tb[h] + lo), lo, ts0[h], ts1[h]);
             }
         }
     }
@@ -634,7 +666,7 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     g.NB = (g.K + BK_KEYS - 1) / BK_KEYS;
     g.NW = (g.K + 31) / 32;
     g.n_tiles = static_cast<uint32_t>((static_cast<uint64_t>(n) + TILE - 1) / TILE);
-    g.G = std::max<uint32_t>(1, std::min<uint32_t>(2 * num_cus(), g.n_tiles));  // two 1024-lane workgroups per CU
+    g.G = std::max<uint32_t>(1, std::min<uint32_t>(num_cus(), (g.n_tiles + TB - 1) / TB));  // blocks of TB tiles
     g.vec = (reinterpret_cast<uintptr_t>(d_ids) & 15u) == 0;
 
     Carver c;
@@ -642,7 +674,8 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     const size_t o_pres = c.add(sizeof(uint32_t) * g.NW);
     const size_t o_kc = c.add(sizeof(uint32_t) * g.K);
     const size_t o_tot = c.add(sizeof(IdsTotals));
-    const size_t o_tab = c.add(sizeof(uint16_t) * static_cast<uint64_t>(g.n_tiles) * (g.NB + 1));
+    const size_t o_tab =
+        c.add(sizeof(uint16_t) * static_cast<uint64_t>((g.n_tiles + TB - 1) / TB) * TB * (g.NB + 1));
     const size_t o_part = c.add(sizeof(uint32_t) * (static_cast<uint64_t>(n) + 4));  // + window overrun
     Scratch sc;
     CR_RET(sc.alloc(c.total, s));
