@@ -5,6 +5,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "internal.hpp"
@@ -57,11 +58,62 @@ static hipMemPool_t library_pool()
     return g_pools[dev];
 }
 
+// Block cache in front of the pool: a block the library frees on a stream is
+// kept and handed to the next allocation on that same stream that it fits
+// (request <= size <= 2 x request), with no runtime call -- stream order makes
+// the reuse safe.  Blocks of other streams stay until evicted (oldest first,
+// beyond CACHE_MAX_BLOCKS or CACHE_MAX_BYTES) or until cr_mempool_trim().
+struct CachedBlock {
+    void* p;
+    size_t bytes;
+    int dev;
+    hipStream_t stream;
+};
+static std::mutex g_cache_mu;
+static std::vector<CachedBlock> g_cache;            // oldest first
+static std::unordered_map<void*, std::pair<size_t, int>> g_live;  // size and device of blocks handed out
+static size_t g_cache_bytes = 0;
+constexpr size_t CACHE_MAX_BLOCKS = 32;
+constexpr size_t CACHE_MAX_BYTES = size_t(16) << 30;
+
+static void release_block(const CachedBlock& b)
+{
+    if (hipFreeAsync(b.p, b.stream) != hipSuccess) {  // e.g. the stream no longer exists
+        (void)hipGetLastError();
+        int cur = 0;
+        (void)hipGetDevice(&cur);
+        (void)hipSetDevice(b.dev);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(b.p);
+        (void)hipSetDevice(cur);
+    }
+}
+
 int dev_alloc(void** p, size_t bytes, hipStream_t s)
 {
     CR_HOST_PHASE("alloc");
     *p = nullptr;
     if (bytes == 0) bytes = 256;
+    int dev = 0;
+    CR_HIP_RET(hipGetDevice(&dev));
+    {
+        std::lock_guard<std::mutex> lock(g_cache_mu);
+        size_t best = g_cache.size();
+        for (size_t i = 0; i < g_cache.size(); ++i) {
+            const CachedBlock& b = g_cache[i];
+            if (b.dev == dev && b.stream == s && b.bytes >= bytes && b.bytes <= 2 * bytes &&
+                (best == g_cache.size() || b.bytes < g_cache[best].bytes))
+                best = i;
+        }
+        if (best != g_cache.size()) {
+            const CachedBlock b = g_cache[best];
+            g_cache.erase(g_cache.begin() + static_cast<std::ptrdiff_t>(best));
+            g_cache_bytes -= b.bytes;
+            g_live[b.p] = {b.bytes, b.dev};
+            *p = b.p;
+            return CR_OK;
+        }
+    }
     hipMemPool_t pool = library_pool();
     hipError_t e = pool ? hipMallocFromPoolAsync(p, bytes, pool, s) : hipMallocAsync(p, bytes, s);
     if (e != hipSuccess) {
@@ -69,6 +121,8 @@ int dev_alloc(void** p, size_t bytes, hipStream_t s)
         *p = nullptr;
         return e == hipErrorOutOfMemory ? CR_ERR_ALLOC : CR_ERR_HIP;
     }
+    std::lock_guard<std::mutex> lock(g_cache_mu);
+    g_live[*p] = {bytes, dev};
     return CR_OK;
 }
 
@@ -76,7 +130,24 @@ int dev_free(void* p, hipStream_t s)
 {
     if (!p) return CR_OK;
     CR_HOST_PHASE("free");
-    CR_HIP_RET(hipFreeAsync(p, s));
+    std::vector<CachedBlock> evict;
+    {
+        std::lock_guard<std::mutex> lock(g_cache_mu);
+        auto it = g_live.find(p);
+        if (it == g_live.end()) {  // not a library block
+            CR_HIP_RET(hipFreeAsync(p, s));
+            return CR_OK;
+        }
+        g_cache.push_back({p, it->second.first, it->second.second, s});
+        g_cache_bytes += it->second.first;
+        g_live.erase(it);
+        while (g_cache.size() > CACHE_MAX_BLOCKS || g_cache_bytes > CACHE_MAX_BYTES) {
+            evict.push_back(g_cache.front());
+            g_cache_bytes -= g_cache.front().bytes;
+            g_cache.erase(g_cache.begin());
+        }
+    }
+    for (const CachedBlock& b : evict) release_block(b);
     return CR_OK;
 }
 
@@ -357,8 +428,25 @@ int cr_mempool_trim(int device_id, size_t keep_bytes)
     int dev = device_id;
     if (dev < 0) CR_HIP_RET(hipGetDevice(&dev));
     if (dev >= 64) return CR_ERR_INVALID;
+    std::vector<CachedBlock> drop;
+    {
+        std::lock_guard<std::mutex> lock(g_cache_mu);
+        for (size_t i = 0; i < g_cache.size();) {
+            if (g_cache[i].dev == dev) {
+                drop.push_back(g_cache[i]);
+                g_cache_bytes -= g_cache[i].bytes;
+                g_cache.erase(g_cache.begin() + static_cast<std::ptrdiff_t>(i));
+            } else {
+                ++i;
+            }
+        }
+    }
+    for (const CachedBlock& b : drop) release_block(b);
     std::lock_guard<std::mutex> lock(g_pool_mu);
-    if (g_pools[dev]) CR_HIP_RET(hipMemPoolTrimTo(g_pools[dev], keep_bytes));
+    if (g_pools[dev]) {
+        CR_HIP_RET(hipDeviceSynchronize());
+        CR_HIP_RET(hipMemPoolTrimTo(g_pools[dev], keep_bytes));
+    }
     return CR_OK;
 }
 

@@ -189,8 +189,11 @@ int cr_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int cr_stream_synchronize(cr_stream_t stream);
 /* The library allocates results and scratch from its own per-device HIP memory
  * pool, which keeps freed memory cached (release threshold: never) so repeated
- * calls do not remap device memory.  Trim it down to `keep_bytes` (-1 device =
- * current device). */
+ * calls do not remap device memory; blocks it frees on a stream are also kept
+ * and reused by later calls on that stream without a runtime call (so a stream
+ * must not be destroyed while library work on it is in flight).  Release the
+ * cached blocks of `device_id` (-1 = current device) and trim its pool down to
+ * `keep_bytes`; synchronises the device. */
 int cr_mempool_trim(int device_id, size_t keep_bytes);
 /* Per-kernel HIP-event timing: enable (1) / disable (0) and clear the records;
  * the report is one "kernel_name launches total_ms" line per kernel. */
