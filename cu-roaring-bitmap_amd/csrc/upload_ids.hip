@@ -36,6 +36,7 @@ constexpr uint32_t TILE = TS_NT * TS_PER;      // 16384 ids: 64 KiB of LDS
 // a block are TB contiguous u16 (the build reads a bucket's column).  The tile
 // sort hands out whole blocks, so a block's rows fill up in one workgroup.
 constexpr uint32_t TB = 8;
+constexpr uint32_t STAGE_NB = 1024;  // run-table rows staged in LDS up to this many buckets
 
 struct IdsTotals {
     uint32_t n_containers;
@@ -69,10 +70,14 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
     __shared__ uint32_t buf[TILE];
     __shared__ uint32_t cnt[MAX_BUCKETS + 1];
     __shared__ uint32_t pres[MAX_PWORDS];
+    // A block's run-table rows are staged here and written as one contiguous
+    // copy when the block ends (up to STAGE_NB buckets; more write directly).
+    __shared__ uint4 stage[STAGE_NB + 1];  // row i = TB u16 starts of bucket i
     __shared__ uint32_t lds[16];
     __shared__ uint32_t s_err, s_max;
     const uint32_t t = threadIdx.x;
     const uint32_t lane = __lane_id();
+    const bool staged = g.NB <= STAGE_NB;
     for (uint32_t i = t; i < g.NW; i += TS_NT) pres[i] = 0;
     if (t == 0) {
         s_err = 0;
@@ -182,12 +187,21 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         }
         if (t == 0) cnt[g.NB] = total;
         __syncthreads();
-        uint16_t* tcol = tab + static_cast<uint64_t>(tile / TB) * (g.NB + 1) * TB + tile % TB;
-        for (uint32_t i = t; i <= g.NB; i += TS_NT) tcol[static_cast<uint64_t>(i) * TB] = static_cast<uint16_t>(cnt[i]);
+        if (staged) {
+            uint16_t* sc = reinterpret_cast<uint16_t*>(stage) + tile % TB;
+            for (uint32_t i = t; i <= g.NB; i += TS_NT) sc[i * TB] = static_cast<uint16_t>(cnt[i]);
+        } else {
+            uint16_t* tcol = tab + static_cast<uint64_t>(tile / TB) * (g.NB + 1) * TB + tile % TB;
+            for (uint32_t i = t; i <= g.NB; i += TS_NT) tcol[static_cast<uint64_t>(i) * TB] = static_cast<uint16_t>(cnt[i]);
+        }
 #pragma unroll
         for (uint32_t j = 0; j < TS_PER; ++j)
             if ((valid >> j) & 1u) buf[cnt[v[j] >> (16 + BK_SHIFT)] + ((rk[j >> 1] >> ((j & 1u) * 16)) & 0xFFFFu)] = v[j];
         __syncthreads();
+        if (staged && (tile % TB == TB - 1 || tile + 1 == g.n_tiles)) {  // the block's rows, contiguous
+            uint4* trow = reinterpret_cast<uint4*>(tab + static_cast<uint64_t>(tile / TB) * (g.NB + 1) * TB);
+            for (uint32_t i = t; i <= g.NB; i += TS_NT) trow[i] = stage[i];
+        }
         uint32_t* dst = part + base;
         const uint32_t n4 = total >> 2;
         for (uint32_t p = t; p < n4; p += TS_NT) reinterpret_cast<uint4*>(dst)[p] = reinterpret_cast<const uint4*>(buf)[p];
@@ -246,7 +260,7 @@ __global__ __launch_bounds__(1024) void ids_keyscan(IdsGeom g, const uint32_t* p
 }
 
 // One workgroup per bucket: its 16 containers as 16 x 2048 u32 LDS words
-// (128 KiB), filled from the bucket's run in every tile.  Four adjacent
+// (128 KiB), filled from the bucket's run in every tile.  Eight adjacent
 // buckets are dispatched to the same XCD (blocks go round-robin over the 8
 // XCDs), so the cache lines their runs share at run boundaries are L2 hits.
 // Normal mode writes the stored containers of present keys and each key's
@@ -255,7 +269,7 @@ __global__ __launch_bounds__(1024) void ids_keyscan(IdsGeom g, const uint32_t* p
 constexpr int BUILD_NT = 1024;
 constexpr uint32_t BUILD_WAVES = BUILD_NT / 64;
 
-inline uint32_t build_grid(uint32_t nb) { return (nb + 31) / 32 * 32; }
+inline uint32_t build_grid(uint32_t nb) { return (nb + 63) / 64 * 64; }
 
 __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict__ part,
                                                       const uint16_t* __restrict__ tab, IdsGeom g, uint32_t universe,
@@ -266,7 +280,7 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
     __shared__ uint32_t bits[BK_KEYS * 2048u];  // 128 KiB of the CU's 160 KiB LDS
     const uint32_t t = threadIdx.x;
     const uint32_t xj = blockIdx.x / 8;
-    const uint32_t b = (xj / 4) * 32 + (blockIdx.x % 8) * 4 + xj % 4;
+    const uint32_t b = (xj / 8) * 64 + (blockIdx.x % 8) * 8 + xj % 8;
     if (b >= g.NB) return;
     for (uint32_t i = t; i < BK_KEYS * 2048u; i += BUILD_NT) bits[i] = 0;
     __syncthreads();

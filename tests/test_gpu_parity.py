@@ -84,6 +84,39 @@ def test_upload_from_ids_complement_cases(gpu, case):
     gpu.free(g)
 
 
+@pytest.mark.parametrize("order", ["sorted", "reverse", "clustered_shuffled", "one_bucket", "skewed"])
+def test_upload_from_ids_input_orders(gpu, order):
+    """Inputs whose waves fall in one bucket (sorted runs), runs far longer than a
+    tile's typical bucket run, partial tile blocks and a skewed key distribution."""
+    _say("upload_from_ids order", order)
+    rng = np.random.default_rng(77)
+    U = 1 << 26
+    if order == "sorted":
+        ids = np.sort(rng.integers(0, U, 3_000_000, dtype=np.uint64)).astype(np.uint32)
+    elif order == "reverse":
+        ids = np.arange(U - 1, U - 2_500_001, -1, dtype=np.int64).astype(np.uint32)
+    elif order == "clustered_shuffled":  # runs of length U[1000, 65536), then shuffled (BASELINE clustered variant)
+        parts, total = [], 0
+        while total < 2_000_000:
+            ln = int(rng.integers(1000, 65536))
+            st = int(rng.integers(0, U - ln))
+            parts.append(np.arange(st, st + ln, dtype=np.uint32))
+            total += ln
+        ids = np.concatenate(parts)
+        ids = np.concatenate([ids, ids[rng.integers(0, ids.size, ids.size // 10)]])
+        ids = ids[rng.permutation(ids.size)]
+    elif order == "one_bucket":  # every id in one 16-key bucket, more than one tile block
+        ids = rng.integers(5 << 20, 6 << 20, 300_000, dtype=np.uint64).astype(np.uint32)
+    else:  # half the ids in one key, the rest uniform
+        ids = np.concatenate([rng.integers(7 << 16, 8 << 16, 600_000, dtype=np.uint64),
+                              rng.integers(0, U, 600_000, dtype=np.uint64)]).astype(np.uint32)
+        ids = ids[rng.permutation(ids.size)]
+    want = orc.upload_from_ids(ids, U)
+    g = gpu.upload_from_device_ids(_dev_u32(ids), U)
+    assert_same(gpu.download(g), want, strict=True, what=order)
+    gpu.free(g)
+
+
 def test_upload_from_ids_rejects_out_of_universe_keys(gpu):
     _say("upload_from_ids invalid")
     ids = np.arange(2000, dtype=np.uint32) + (5 << 16)
