@@ -13,8 +13,8 @@
 //   tile_sort   read the ids once; counting-sort each tile by bucket in LDS and
 //               stream it back to the tile's own slot, with the tile's bucket
 //               starts in a small table; key presence per workgroup
-//   pres_reduce OR of the presence words
-//   keyscan     key ranks -> keys/types/offsets/key_index
+//   rank        OR of the presence words, key ranks ->
+//               keys/types/offsets/key_index, totals
 //   build       one workgroup per bucket: read the bucket's run of every tile
 //               (~16 ids at 2^30), LDS bit-set, popcount, write containers
 #include <algorithm>
@@ -65,7 +65,7 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t m) { return static_cast
 // OR-ed per workgroup.
 __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restrict__ ids, IdsGeom g,
                                                        uint32_t* __restrict__ part, uint16_t* __restrict__ tab,
-                                                       uint32_t* gpres, IdsTotals* tot)
+                                                       uint32_t* gpres, uint32_t* gerr, uint32_t* gmax)
 {
     __shared__ uint32_t buf[TILE];
     __shared__ uint32_t cnt[MAX_BUCKETS + 1];
@@ -215,39 +215,65 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
     __syncthreads();
     uint32_t* op = gpres + static_cast<uint64_t>(blockIdx.x) * g.NW;
     for (uint32_t i = t; i < g.NW; i += TS_NT) op[i] = pres[i];
-    if (t == 0) {
-        if (s_err) atomicOr(&tot->err, 1u);
-        atomicMax(&tot->max_id, s_max);
+    if (t == 0) {  // per-workgroup partials: nothing here needs zeroed memory
+        gerr[blockIdx.x] = s_err;
+        gmax[blockIdx.x] = s_max;
     }
 }
 
-// One wave per presence word: OR over the tile-sort workgroups.
-__global__ __launch_bounds__(1024) void ids_pres_reduce(IdsGeom g, const uint32_t* gpres, uint32_t* pres)
+// Key ranks, one thread per key and one workgroup per 1024 keys.  Each
+// workgroup ORs the tile-sort workgroups' presence words up to the end of its
+// range (the 16 waves split the words and the partials), so the rank base is
+// the popcount of the words before its range.  Writes keys/types/offsets and the
+// full key_index (0xFFFF = absent); workgroup 0 also reduces the error and
+// max-id partials and zeroes the distinct count the build accumulates.
+__global__ __launch_bounds__(1024) void ids_rank(IdsGeom g, const uint32_t* gpres, const uint32_t* gerr,
+                                                 const uint32_t* gmax, uint16_t* keys, uint8_t* types,
+                                                 uint32_t* offsets, uint16_t* key_index, IdsTotals* tot)
 {
-    const uint32_t w = (blockIdx.x * 1024u + threadIdx.x) >> 6;
-    const uint32_t lane = __lane_id();
-    if (w >= g.NW) return;
-    uint32_t acc = 0;
-    for (uint32_t k = lane; k < g.G; k += 64) acc |= gpres[static_cast<uint64_t>(k) * g.NW + w];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) acc |= __shfl_xor(acc, o, 64);
-    if (lane == 0) pres[w] = acc;
-}
-
-// Key ranks, one thread per key and one workgroup per 1024 keys: the rank base
-// of a workgroup is the popcount of the presence words before it.  Writes
-// keys/types/offsets (coalesced) and the full key_index (0xFFFF = absent).
-__global__ __launch_bounds__(1024) void ids_keyscan(IdsGeom g, const uint32_t* pres, uint16_t* keys, uint8_t* types,
-                                                    uint32_t* offsets, uint16_t* key_index, IdsTotals* tot)
-{
+    __shared__ uint32_t red[1024];     // per-part ORs: [part][word]
+    __shared__ uint32_t word[MAX_PWORDS];
     __shared__ uint32_t lds[16];
     const uint32_t t = threadIdx.x;
     const uint32_t w = blockIdx.x;
+    const uint32_t wave = t >> 6, lane = __lane_id();
+    const uint32_t nw_need = min(g.NW, (w + 1) * 32u);  // words up to the end of this range
+    // Words in columns of 64 (one lane per word), at most 1024 words a pass;
+    // the 16 waves split the columns and the partials: wave = part * cols + column.
+    for (uint32_t base = 0; base < nw_need; base += 1024u) {
+        const uint32_t nb = min(nw_need - base, 1024u);
+        const uint32_t cols = (nb + 63) / 64, prt = 16u / cols;
+        if (wave < cols * prt) {
+            const uint32_t c = wave % cols, pi = wave / cols;
+            const uint32_t j = base + c * 64u + lane;
+            const uint32_t k0 = pi * g.G / prt, k1 = (pi + 1) * g.G / prt;
+            uint32_t acc = 0;
+            if (j < nw_need) {
+                uint32_t k = k0;
+                for (; k + 8 <= k1; k += 8) {
+                    uint32_t v8[8];
+#pragma unroll
+                    for (uint32_t q = 0; q < 8; ++q) v8[q] = gpres[static_cast<uint64_t>(k + q) * g.NW + j];
+#pragma unroll
+                    for (uint32_t q = 0; q < 8; ++q) acc |= v8[q];
+                }
+                for (; k < k1; ++k) acc |= gpres[static_cast<uint64_t>(k) * g.NW + j];
+            }
+            red[pi * (cols * 64u) + c * 64u + lane] = acc;
+        }
+        __syncthreads();
+        for (uint32_t j = t; j < nb; j += 1024u) {
+            uint32_t acc = 0;
+            for (uint32_t pi = 0; pi < prt; ++pi) acc |= red[pi * (cols * 64u) + j];
+            word[base + j] = acc;
+        }
+        __syncthreads();
+    }
     uint32_t before = 0;  // present keys below this workgroup's range (32 words per 1024 keys)
-    for (uint32_t j = t; j < w * 32u; j += 1024u) before += __popc(pres[j]);
+    for (uint32_t j = t; j < w * 32u; j += 1024u) before += __popc(word[j]);
     before = block_sum<1024>(before, lds);
     const uint32_t key = w * 1024u + t;
-    const bool present = key < g.K && ((pres[key >> 5] >> (key & 31u)) & 1u);
+    const bool present = key < g.K && ((word[key >> 5] >> (key & 31u)) & 1u);
     uint32_t here;
     const uint32_t rank = before + block_excl_scan<1024>(present ? 1u : 0u, lds, here);
     if (key < g.K) key_index[key] = present ? static_cast<uint16_t>(rank) : static_cast<uint16_t>(0xFFFFu);
@@ -257,6 +283,23 @@ __global__ __launch_bounds__(1024) void ids_keyscan(IdsGeom g, const uint32_t* p
         offsets[rank] = rank * 8192u;
     }
     if (t == 0 && w == gridDim.x - 1) tot->n_containers = before + here;
+    if (w == 0 && wave == 0) {
+        uint32_t e = 0, m = 0;
+        for (uint32_t k = lane; k < g.G; k += 64) {
+            e |= gerr[k];
+            m = max(m, gmax[k]);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            e |= __shfl_xor(e, o, 64);
+            m = max(m, static_cast<uint32_t>(__shfl_xor(m, o, 64)));
+        }
+        if (lane == 0) {
+            tot->err = e;
+            tot->max_id = m;
+            tot->total = 0;
+        }
+    }
 }
 
 // One workgroup per bucket: its 16 containers as 16 x 2048 u32 LDS words
@@ -685,7 +728,8 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
 
     Carver c;
     const size_t o_gpres = c.add(sizeof(uint32_t) * static_cast<uint64_t>(g.G) * g.NW);
-    const size_t o_pres = c.add(sizeof(uint32_t) * g.NW);
+    const size_t o_gerr = c.add(sizeof(uint32_t) * g.G);
+    const size_t o_gmax = c.add(sizeof(uint32_t) * g.G);
     const size_t o_kc = c.add(sizeof(uint32_t) * g.K);
     const size_t o_tot = c.add(sizeof(IdsTotals));
     const size_t o_tab =
@@ -694,7 +738,8 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     Scratch sc;
     CR_RET(sc.alloc(c.total, s));
     uint32_t* gpres = sc.at<uint32_t>(o_gpres);
-    uint32_t* pres = sc.at<uint32_t>(o_pres);
+    uint32_t* gerr = sc.at<uint32_t>(o_gerr);
+    uint32_t* gmax = sc.at<uint32_t>(o_gmax);
     uint32_t* key_count = sc.at<uint32_t>(o_kc);
     IdsTotals* tot = sc.at<IdsTotals>(o_tot);
     uint16_t* tab = sc.at<uint16_t>(o_tab);
@@ -706,21 +751,15 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     CR_RET(alloc_out(out, L, bound, g.K, bound * 1024u, 0, 0, s));
     out->max_key = max_key32;
 
-    CR_RET(fill_u32(reinterpret_cast<uint32_t*>(tot), 0u, sizeof(IdsTotals) / 4, s));
     {
         CR_TIMED("ids_tile_sort", s);
-        ids_tile_sort<<<g.G, TS_NT, 0, s>>>(d_ids, g, part, tab, gpres, tot);
+        ids_tile_sort<<<g.G, TS_NT, 0, s>>>(d_ids, g, part, tab, gpres, gerr, gmax);
     }
     CR_LAUNCH_CHECK();
     {
-        CR_TIMED("ids_pres_reduce", s);
-        ids_pres_reduce<<<(g.NW + 15) / 16, 1024, 0, s>>>(g, gpres, pres);
-    }
-    CR_LAUNCH_CHECK();
-    {
-        CR_TIMED("ids_keyscan", s);
-        ids_keyscan<<<(g.K + 1023) / 1024, 1024, 0, s>>>(g, pres, out->keys, out->types, out->offsets,
-                                                         out->key_index, tot);
+        CR_TIMED("ids_rank", s);
+        ids_rank<<<(g.K + 1023) / 1024, 1024, 0, s>>>(g, gpres, gerr, gmax, out->keys, out->types, out->offsets,
+                                                      out->key_index, tot);
     }
     CR_LAUNCH_CHECK();
     {
