@@ -458,8 +458,9 @@ __global__ __launch_bounds__(EXEC_NT) void so_exec(Side A, Side B, const Item* i
 
 // ---- bitmap x bitmap only: one wavefront per pair ----------------------------
 // When every work item is a bitmap pair (both inputs all-bitmap), each wave
-// streams one 8 KiB pair: 64 lanes x 8 x 16-byte loads per input, the op, the
-// store, and a wave-level popcount -- no workgroup barrier anywhere.
+// streams one 8 KiB pair: 64 lanes x 8 x 16-byte loads per input, all sixteen
+// issued before the op, then the stores and a wave-level popcount -- no
+// workgroup barrier anywhere.
 constexpr int BB_NT = 256;
 
 template <uint32_t OP>
@@ -484,24 +485,21 @@ __global__ __launch_bounds__(BB_NT) void so_exec_bb(const uint64_t* __restrict__
             const uint4* a4 = reinterpret_cast<const uint4*>(pa);
             const uint4* b4 = reinterpret_cast<const uint4*>(pb);
             uint4* o4 = reinterpret_cast<uint4*>(po);
+            uint4 x[8], y[8];  // all 16 loads of the pair in flight before any store
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                uint4 x[4], y[4];
+            for (int k = 0; k < 8; ++k) {
+                x[k] = a4[lane + 64 * k];
+                y[k] = b4[lane + 64 * k];
+            }
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    x[k] = a4[lane + 64 * (4 * half + k)];
-                    y[k] = b4[lane + 64 * (4 * half + k)];
-                }
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    uint4 r;
-                    r.x = apply32<OP>(x[k].x, y[k].x);
-                    r.y = apply32<OP>(x[k].y, y[k].y);
-                    r.z = apply32<OP>(x[k].z, y[k].z);
-                    r.w = apply32<OP>(x[k].w, y[k].w);
-                    o4[lane + 64 * (4 * half + k)] = r;
-                    pc += __popc(r.x) + __popc(r.y) + __popc(r.z) + __popc(r.w);
-                }
+            for (int k = 0; k < 8; ++k) {
+                uint4 r;
+                r.x = apply32<OP>(x[k].x, y[k].x);
+                r.y = apply32<OP>(x[k].y, y[k].y);
+                r.z = apply32<OP>(x[k].z, y[k].z);
+                r.w = apply32<OP>(x[k].w, y[k].w);
+                o4[lane + 64 * k] = r;
+                pc += __popc(r.x) + __popc(r.y) + __popc(r.z) + __popc(r.w);
             }
         } else {
             for (uint32_t i = lane; i < 1024u; i += 64) {
@@ -872,36 +870,50 @@ __global__ __launch_bounds__(EXEC_NT) void mand_and(FusedArgs args, const uint16
         uint4 acc[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[j] = make_uint4(~0u, ~0u, ~0u, ~0u);
-        for (uint32_t k = 0; k < args.count; ++k) {
-            const int32_t idx = __shfl(my_idx, static_cast<int>(k), 64);
-            const bool neg = (args.neg_mask >> k) & 1u;
-            if (idx < 0) {
-                if (!neg) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) acc[j] = make_uint4(0, 0, 0, 0);
-                }
-                continue;
-            }
-            const uint64_t* p = args.in[k].bmp + static_cast<uint64_t>(idx) * 1024u;
-            const uint32_t m = neg ? ~0u : 0u;
+        // Input k + 1's eight 16-byte loads are issued before input k is ANDed
+        // in, so a wave keeps two inputs' reads in flight.
+        auto src_of = [&](uint32_t k, int32_t& idx) -> const uint64_t* {
+            idx = __shfl(my_idx, static_cast<int>(k), 64);
+            return idx < 0 ? nullptr : args.in[k].bmp + static_cast<uint64_t>(idx) * 1024u;
+        };
+        auto load8 = [&](const uint64_t* p, uint4 (&x)[8]) {
+            if (!p) return;
             if ((reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
                 const uint4* p4 = reinterpret_cast<const uint4*>(p);
-                uint4 x[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) x[j] = p4[lane + 64 * j];
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    acc[j] = make_uint4(acc[j].x & (x[j].x ^ m), acc[j].y & (x[j].y ^ m), acc[j].z & (x[j].z ^ m),
-                                        acc[j].w & (x[j].w ^ m));
             } else {
                 const uint32_t* p32 = reinterpret_cast<const uint32_t*>(p);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const uint32_t b = 4 * (lane + 64 * j);
-                    acc[j] = make_uint4(acc[j].x & (p32[b] ^ m), acc[j].y & (p32[b + 1] ^ m),
-                                        acc[j].z & (p32[b + 2] ^ m), acc[j].w & (p32[b + 3] ^ m));
+                    x[j] = make_uint4(p32[b], p32[b + 1], p32[b + 2], p32[b + 3]);
                 }
             }
+        };
+        uint4 cur[8], nxt[8];
+        int32_t idx_cur = -1, idx_nxt = -1;
+        const uint64_t* p_cur = args.count ? src_of(0, idx_cur) : nullptr;
+        load8(p_cur, cur);
+        for (uint32_t k = 0; k < args.count; ++k) {
+            const uint64_t* p_nxt = k + 1 < args.count ? src_of(k + 1, idx_nxt) : nullptr;
+            load8(p_nxt, nxt);
+            const bool neg = (args.neg_mask >> k) & 1u;
+            if (idx_cur < 0) {
+                if (!neg) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) acc[j] = make_uint4(0, 0, 0, 0);
+                }
+            } else {
+                const uint32_t m = neg ? ~0u : 0u;
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    acc[j] = make_uint4(acc[j].x & (cur[j].x ^ m), acc[j].y & (cur[j].y ^ m), acc[j].z & (cur[j].z ^ m),
+                                        acc[j].w & (cur[j].w ^ m));
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) cur[j] = nxt[j];
+            idx_cur = idx_nxt;
         }
         uint4* dst = reinterpret_cast<uint4*>(out_bmp + static_cast<uint64_t>(c) * 1024u);
         uint32_t pc = 0;
