@@ -10,7 +10,8 @@
  * Three parts:
  *   1. ref-semantics  -- the reference's *output layout* rules for the GPU
  *      structs (upload_from_ids, bitset uploads, packed upload(), set_operation,
- *      multi_and, resolve_auto_threshold, contains, decompress).
+ *      multi_and, resolve_auto_threshold, contains, decompress, enumerate_ids,
+ *      promote_to_bitmap, deep copy).
  *   2. roaring-lite   -- a host Roaring bitmap with array / bitset / run
  *      containers following the public Roaring format rules (array <= 4096,
  *      run chosen iff its serialized size is smaller).  It stands in for
@@ -97,6 +98,9 @@ int orc_contains(const orc_roaring* r, uint32_t id);
 void orc_contains_many(const orc_roaring* r, const uint32_t* ids, uint64_t n, uint32_t* out);
 void orc_decompress(const orc_roaring* r, uint32_t* out_words, uint32_t n_words);
 uint64_t orc_true_cardinality(const orc_roaring* r);
+uint64_t orc_enumerate_ids(const orc_roaring* r, int64_t* out);
+int orc_promote_to_bitmap(const orc_roaring* src, orc_roaring* out);
+int orc_deep_copy(const orc_roaring* src, orc_roaring* out);
 
 /* ---- roaring-lite ------------------------------------------------------- */
 typedef struct rl_bitmap {

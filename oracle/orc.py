@@ -82,6 +82,12 @@ def lib():
         L.orc_decompress.argtypes = [P(_OrcRoaring), C.c_void_p, C.c_uint32]
         L.orc_true_cardinality.argtypes = [P(_OrcRoaring)]
         L.orc_true_cardinality.restype = C.c_uint64
+        L.orc_enumerate_ids.argtypes = [P(_OrcRoaring), C.c_void_p]
+        L.orc_enumerate_ids.restype = C.c_uint64
+        L.orc_promote_to_bitmap.argtypes = [P(_OrcRoaring), P(_OrcRoaring)]
+        L.orc_promote_to_bitmap.restype = C.c_int
+        L.orc_deep_copy.argtypes = [P(_OrcRoaring), P(_OrcRoaring)]
+        L.orc_deep_copy.restype = C.c_int
         for name in ("orc_upload_from_ids", "orc_upload_from_bitset", "orc_upload_packed",
                      "orc_set_operation", "orc_multi_and", "orc_contains"):
             getattr(L, name).restype = C.c_int
@@ -291,6 +297,37 @@ def decompress(r: HostRoaring, n_words: Optional[int] = None) -> np.ndarray:
 
 def true_cardinality(r: HostRoaring) -> int:
     return lib().orc_true_cardinality(C.byref(as_host(r).as_c()))
+
+
+def enumerate_ids(r) -> np.ndarray:
+    """enumerate_ids (src/to_csr.cu:161-220): the stored ids as int64 (negation ignored)."""
+    c = as_host(r).as_c()
+    n = lib().orc_enumerate_ids(C.byref(c), None)
+    out = np.zeros(max(n, 1), dtype=np.int64)
+    lib().orc_enumerate_ids(C.byref(c), _ptr(out))
+    return out[:n]
+
+
+def promote_to_bitmap(r) -> HostRoaring:
+    c = _OrcRoaring()
+    _check(lib().orc_promote_to_bitmap(C.byref(as_host(r).as_c()), C.byref(c)), "promote_to_bitmap")
+    return _from_c(c)
+
+
+def deep_copy(r) -> HostRoaring:
+    c = _OrcRoaring()
+    _check(lib().orc_deep_copy(C.byref(as_host(r).as_c()), C.byref(c)), "deep_copy")
+    return _from_c(c)
+
+
+def promote_auto(r, l2_bytes: int = DEFAULT_L2) -> HostRoaring:
+    """promote_auto (src/promote.cu:369-385): promote when AUTO resolves to ALL and a
+    non-bitmap container exists, else a deep copy."""
+    r = as_host(r)
+    thr = lib().orc_resolve_auto_threshold(r.universe_size, l2_bytes)
+    if thr == PROMOTE_ALL and (r.n_array_containers > 0 or r.n_run_containers > 0):
+        return promote_to_bitmap(r)
+    return deep_copy(r)
 
 
 # ---- roaring-lite -------------------------------------------------------

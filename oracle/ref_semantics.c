@@ -25,6 +25,12 @@
  *                                 bitset AND; the n_containers==1 pin at :644.
  *   orc_contains / decompress  -- exhaustive comparison with a flat bitset built
  *                                 independently from the input IDs.
+ *   orc_enumerate_ids          -- the sorted ids of the decoded set (numpy), the
+ *                                 total==0 early return on a set_operation result.
+ *   orc_promote_to_bitmap      -- test/test_promote.cu:41-150 (counts, decode
+ *                                 equality), layout invariants, negation kept
+ *                                 (test/test_complement.cu:468-497).
+ *   orc_deep_copy              -- field-by-field equality and the pool sizes.
  */
 #include "oracle.h"
 
@@ -1165,4 +1171,171 @@ uint64_t orc_true_cardinality(const orc_roaring* r)
         }
     }
     return t;
+}
+
+/* enumerate_ids -- src/to_csr.cu:161-220.  The stored set's ids in key order
+ * as int64; `negated` is ignored (the kernel reads containers only).  Nothing
+ * is written when n_containers == 0 or total_cardinality == 0 (:163), so a
+ * set_operation result (total left 0, src/set_ops.cu:1162-1175) enumerates
+ * nothing.  A bitmap container contributes its set bits; the reference sizes
+ * its slice from cardinalities[] (:150-151), which is 0 for a full container
+ * (65536 stored as 0) and 65535 for multi_and's clamped one, while its kernel
+ * writes every set bit -- an overrun into the next container's slice.  Here a
+ * bitmap's count is its popcount, the sorted list the function is for.
+ * Returns the number of ids; `out` may be NULL to count only. */
+uint64_t orc_enumerate_ids(const orc_roaring* r, int64_t* out)
+{
+    if (r->n_containers == 0 || r->total_cardinality == 0) return 0;
+    uint64_t n = 0;
+    for (uint32_t c = 0; c < r->n_containers; ++c) {
+        const uint32_t base = (uint32_t)r->keys[c] << 16, off = r->offsets[c];
+        if (r->types[c] == ORC_ARRAY) {
+            const uint16_t* arr = r->array_data + off / 2u;
+            for (uint32_t i = 0; i < r->cards[c]; ++i) {
+                if (out) out[n] = (int64_t)(base | arr[i]);
+                ++n;
+            }
+        } else if (r->types[c] == ORC_BITMAP) {
+            const uint64_t* bm = r->bitmap_data + off / 8u;
+            for (uint32_t w = 0; w < 1024u; ++w)
+                for (uint64_t x = bm[w]; x; x &= x - 1) {
+                    if (out) out[n] = (int64_t)(base | (w * 64u + (uint32_t)__builtin_ctzll(x)));
+                    ++n;
+                }
+        } else if (r->types[c] == ORC_RUN) {
+            const uint16_t* runs = r->run_data + off / 2u;
+            for (uint32_t k = 0; k < r->cards[c]; ++k) {
+                const uint32_t s = runs[2 * k], len = runs[2 * k + 1];
+                for (uint32_t v = 0; v <= len; ++v) {
+                    if (out) out[n] = (int64_t)(base | (s + v));
+                    ++n;
+                }
+            }
+        }
+    }
+    return n;
+}
+
+static int orc_build_key_index(orc_roaring* out) /* promote.cu:150-158, 307-320 */
+{
+    if (out->universe_size == 0) return ORC_OK;
+    uint32_t mk = (out->universe_size - 1u) >> 16;
+    if (mk > 0xFFFFu) mk = 0xFFFFu;
+    out->max_key = mk;
+    out->key_index_len = mk + 1u;
+    out->key_index = (uint16_t*)malloc(sizeof(uint16_t) * out->key_index_len);
+    if (!out->key_index) return ORC_ERR_ALLOC;
+    memset(out->key_index, 0xFF, sizeof(uint16_t) * out->key_index_len);
+    for (uint32_t i = 0; i < out->n_containers; ++i)
+        if (out->keys[i] <= mk) out->key_index[out->keys[i]] = (uint16_t)i;
+    return ORC_OK;
+}
+
+/* promote_to_bitmap -- src/promote.cu:233-323.  Every container becomes a
+ * BITMAP at offset i*8192; keys and cardinalities are copied verbatim (a RUN
+ * container's card keeps its n_runs); universe, total and negated carry over;
+ * max_key and key_index come from the universe (0 / none when it is 0).  With
+ * no array or run container the first n x 8 KiB of the bitmap pool are copied
+ * as they lie (:268-276).  An empty input gives the all-zero struct (:236). */
+int orc_promote_to_bitmap(const orc_roaring* src, orc_roaring* out)
+{
+    memset(out, 0, sizeof(*out));
+    const uint32_t n = src->n_containers;
+    if (n == 0) return ORC_OK;
+    out->n_containers = n;
+    out->n_bitmap_containers = n;
+    out->universe_size = src->universe_size;
+    out->total_cardinality = src->total_cardinality;
+    out->negated = src->negated;
+    out->keys = (uint16_t*)malloc(sizeof(uint16_t) * n);
+    out->types = (uint8_t*)malloc(n);
+    out->offsets = (uint32_t*)malloc(sizeof(uint32_t) * n);
+    out->cards = (uint16_t*)malloc(sizeof(uint16_t) * n);
+    out->bitmap_pool_words = n * 1024u;
+    out->bitmap_data = (uint64_t*)calloc((size_t)n * 1024u, sizeof(uint64_t));
+    if (!out->keys || !out->types || !out->offsets || !out->cards || !out->bitmap_data) {
+        orc_free(out);
+        return ORC_ERR_ALLOC;
+    }
+    memcpy(out->keys, src->keys, sizeof(uint16_t) * n);
+    memcpy(out->cards, src->cards, sizeof(uint16_t) * n);
+    const int all_bitmap = src->n_array_containers == 0 && src->n_run_containers == 0;
+    for (uint32_t c = 0; c < n; ++c) {
+        out->types[c] = ORC_BITMAP;
+        out->offsets[c] = c * 8192u;
+        uint64_t* dst = out->bitmap_data + (size_t)c * 1024u;
+        if (all_bitmap) {
+            memcpy(dst, src->bitmap_data + (size_t)c * 1024u, 8192);
+        } else if (src->types[c] == ORC_BITMAP) {
+            memcpy(dst, src->bitmap_data + src->offsets[c] / 8u, 8192);
+        } else if (src->types[c] == ORC_ARRAY) {
+            const uint16_t* arr = src->array_data + src->offsets[c] / 2u;
+            for (uint32_t i = 0; i < src->cards[c]; ++i) dst[arr[i] / 64u] |= 1ull << (arr[i] % 64u);
+        } else {
+            const uint16_t* runs = src->run_data + src->offsets[c] / 2u;
+            for (uint32_t k = 0; k < src->cards[c]; ++k) {
+                uint32_t s = runs[2 * k], e = s + runs[2 * k + 1];
+                if (e > 0xFFFFu) e = 0xFFFFu;
+                for (uint32_t v = s; v <= e; ++v) dst[v / 64u] |= 1ull << (v % 64u);
+            }
+        }
+    }
+    return orc_build_key_index(out);
+}
+
+/* gpu_roaring_deep_copy -- src/promote.cu:178-231.  Scalar fields always; for
+ * n_containers == 0 nothing else.  The bitmap pool copies n_bitmap x 8 KiB
+ * (not the whole pool), the array / run pools their *_pool_bytes, and the
+ * key_index (max_key + 1 entries) only when present and the universe is
+ * non-zero. */
+int orc_deep_copy(const orc_roaring* src, orc_roaring* out)
+{
+    memset(out, 0, sizeof(*out));
+    out->n_containers = src->n_containers;
+    out->n_bitmap_containers = src->n_bitmap_containers;
+    out->n_array_containers = src->n_array_containers;
+    out->n_run_containers = src->n_run_containers;
+    out->universe_size = src->universe_size;
+    out->total_cardinality = src->total_cardinality;
+    out->negated = src->negated;
+    out->max_key = src->max_key;
+    out->array_pool_bytes = src->array_pool_bytes;
+    out->run_pool_bytes = src->run_pool_bytes;
+    const uint32_t n = src->n_containers;
+    if (n == 0) return ORC_OK;
+    out->keys = (uint16_t*)malloc(sizeof(uint16_t) * n);
+    out->types = (uint8_t*)malloc(n);
+    out->offsets = (uint32_t*)malloc(sizeof(uint32_t) * n);
+    out->cards = (uint16_t*)malloc(sizeof(uint16_t) * n);
+    if (!out->keys || !out->types || !out->offsets || !out->cards) {
+        orc_free(out);
+        return ORC_ERR_ALLOC;
+    }
+    memcpy(out->keys, src->keys, sizeof(uint16_t) * n);
+    memcpy(out->types, src->types, n);
+    memcpy(out->offsets, src->offsets, sizeof(uint32_t) * n);
+    memcpy(out->cards, src->cards, sizeof(uint16_t) * n);
+    if (src->bitmap_data && src->n_bitmap_containers > 0) {
+        out->bitmap_pool_words = src->n_bitmap_containers * 1024u;
+        out->bitmap_data = (uint64_t*)malloc(sizeof(uint64_t) * out->bitmap_pool_words);
+        if (!out->bitmap_data) { orc_free(out); return ORC_ERR_ALLOC; }
+        memcpy(out->bitmap_data, src->bitmap_data, sizeof(uint64_t) * out->bitmap_pool_words);
+    }
+    if (src->array_data && src->array_pool_bytes > 0) {
+        out->array_data = (uint16_t*)malloc(src->array_pool_bytes);
+        if (!out->array_data) { orc_free(out); return ORC_ERR_ALLOC; }
+        memcpy(out->array_data, src->array_data, src->array_pool_bytes);
+    }
+    if (src->run_data && src->run_pool_bytes > 0) {
+        out->run_data = (uint16_t*)malloc(src->run_pool_bytes);
+        if (!out->run_data) { orc_free(out); return ORC_ERR_ALLOC; }
+        memcpy(out->run_data, src->run_data, src->run_pool_bytes);
+    }
+    if (src->key_index && src->universe_size > 0) {
+        out->key_index_len = src->max_key + 1u;
+        out->key_index = (uint16_t*)malloc(sizeof(uint16_t) * out->key_index_len);
+        if (!out->key_index) { orc_free(out); return ORC_ERR_ALLOC; }
+        memcpy(out->key_index, src->key_index, sizeof(uint16_t) * out->key_index_len);
+    }
+    return ORC_OK;
 }

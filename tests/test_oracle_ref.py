@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import orc
-from helpers import flat_from_ids, ids_from_flat, mt_bernoulli, mt_mod_filter, mt_low16_density, words_mask
+from helpers import assert_same, flat_from_ids, ids_from_flat, mt_bernoulli, mt_mod_filter, mt_low16_density, words_mask
 
 L2 = orc.DEFAULT_L2
 
@@ -408,3 +408,90 @@ def test_multi_and_routing_and_card_clamp():
     half = orc.upload_from_ids(np.arange(0, 65536, 2, dtype=np.uint32), 1 << 20)
     r = orc.multi_and([half, a, sparse])
     assert r.key_index is None and list(r.types) == [orc.ARRAY] and list(r.array_data[:1]) == [2]
+
+
+# ---- next rows: enumerate_ids, promote_to_bitmap, deep copy ------------------
+@pytest.mark.parametrize("kind", ["ids", "packed_mixed", "negated", "full_container"])
+def test_enumerate_ids_is_the_sorted_stored_set(kind):
+    """The expected list is built with numpy from the inputs: the unique ids, or
+    for a negated result the complement that is stored."""
+    rng = np.random.default_rng(5)
+    if kind == "ids":
+        ids = rng.integers(0, 1 << 22, 200000, dtype=np.uint64).astype(np.uint32)
+        r, want = orc.upload_from_ids(ids, 1 << 22), np.unique(ids)
+    elif kind == "packed_mixed":
+        ids = np.unique(np.concatenate([rng.integers(0, 65536, 300, dtype=np.uint64),
+                                        np.arange(65536, 65536 + 50000), np.arange(131072, 141072)]).astype(np.uint32))
+        r, want = orc.upload_packed(orc.Lite.from_sorted_ids(ids).run_optimize(), None, orc.PROMOTE_KEEP_DEFAULT), ids
+        assert r.n_run_containers > 0 and r.n_array_containers > 0
+    elif kind == "negated":
+        ids = np.arange(0, 90000, dtype=np.uint32)
+        r, want = orc.upload_from_ids(ids, 100000), np.arange(90000, 100000)
+        assert r.negated
+    else:
+        ids = np.arange(0, 3 * 65536 + 7, dtype=np.uint32)
+        r, want = orc.upload_from_ids(ids, 1 << 20), ids
+    got = orc.enumerate_ids(r)
+    assert np.array_equal(got, want.astype(np.int64))
+
+
+def test_enumerate_ids_set_operation_result_is_empty():  # total_cardinality left 0 (to_csr.cu:163)
+    a = orc.upload_from_ids(np.arange(0, 5000, dtype=np.uint32), 1 << 20)
+    b = orc.upload_from_ids(np.arange(2500, 7000, dtype=np.uint32), 1 << 20)
+    r = orc.set_operation(a, b, orc.AND)
+    assert r.total_cardinality == 0 and r.n_containers == 1
+    assert orc.enumerate_ids(r).size == 0
+
+
+def test_promote_mixed_containers():  # test/test_promote.cu:41-80
+    ids = np.unique(np.concatenate([np.arange(100) * 10, np.arange(65536, 65536 + 50000),
+                                    np.arange(131072, 141072)]).astype(np.uint32))
+    g = orc.upload_packed(orc.Lite.from_sorted_ids(ids).run_optimize(), None, orc.PROMOTE_KEEP_DEFAULT)
+    assert g.n_containers == 3 and g.n_array_containers + g.n_run_containers > 0
+    p = orc.promote_to_bitmap(g)
+    assert (p.n_containers, p.n_bitmap_containers, p.n_array_containers, p.n_run_containers) == (3, 3, 0, 0)
+    assert np.array_equal(orc.decompress(p), orc.decompress(g))
+    assert np.array_equal(p.offsets, np.arange(3, dtype=np.uint32) * 8192)
+    assert np.array_equal(p.cards, g.cards)  # a RUN container keeps its n_runs
+    assert p.max_key == (g.universe_size - 1) >> 16
+    assert [int(p.key_index[k]) for k in range(3)] == [0, 1, 2]
+
+
+def test_promote_all_bitmap_empty_and_arrays():  # :82-150
+    g = orc.upload_packed(orc.Lite.from_sorted_ids(np.arange(3 * 65536, dtype=np.uint32)), None,
+                          orc.PROMOTE_KEEP_DEFAULT)
+    p = orc.promote_to_bitmap(g)
+    assert p.n_bitmap_containers == 3 and np.array_equal(orc.decompress(p), orc.decompress(g))
+    e = orc.promote_to_bitmap(orc.upload_packed(orc.Lite.from_sorted_ids(np.zeros(0, np.uint32)), None))
+    assert e.n_containers == 0 and e.universe_size == 0  # GpuRoaring{} (promote.cu:236)
+    rng = np.random.default_rng(42)
+    ids = np.unique(np.concatenate([k * 65536 + rng.integers(0, 65536, 100) for k in range(50)]).astype(np.uint32))
+    a = orc.upload_packed(orc.Lite.from_sorted_ids(ids), None, orc.PROMOTE_KEEP_DEFAULT)
+    assert a.n_bitmap_containers == 0
+    p = orc.promote_to_bitmap(a)
+    assert p.n_bitmap_containers == p.n_containers == 50 and np.array_equal(orc.decompress(p), orc.decompress(a))
+
+
+def test_promote_preserves_negated():  # test/test_complement.cu:468-497
+    U = 100000
+    ids = np.array([i for i in range(U) if i % 5], dtype=np.uint32)
+    g = orc.upload_from_ids(ids, U)
+    assert g.negated
+    p = orc.promote_to_bitmap(g)
+    assert p.negated and p.n_array_containers == 0
+    q = np.arange(0, U, 13, dtype=np.uint32)
+    assert np.array_equal(orc.contains_many(p, q), (q % 5 != 0).astype(np.uint32))
+
+
+def test_deep_copy_and_promote_auto():
+    rng = np.random.default_rng(9)
+    ids = np.unique(rng.integers(0, 1 << 22, 3000, dtype=np.uint64).astype(np.uint32))
+    g = orc.upload_packed(orc.Lite.from_sorted_ids(ids), 1 << 22, orc.PROMOTE_KEEP_DEFAULT)
+    d = orc.deep_copy(g)
+    assert_same(d, g, strict=False, what="deep_copy")
+    assert d.bitmap_data.size == g.n_bitmap_containers * 1024
+    # AUTO at 2^22 (512 KiB flat) keeps the layout on a 4 MiB L2; at 2^30 it promotes
+    assert orc.promote_auto(g).n_array_containers == g.n_array_containers
+    big = orc.upload_packed(orc.Lite.from_sorted_ids(ids), 1 << 30, orc.PROMOTE_KEEP_DEFAULT)
+    p = orc.promote_auto(big)
+    assert p.n_array_containers == 0 and p.n_bitmap_containers == p.n_containers
