@@ -1,0 +1,584 @@
+// Conversions of a GpuRoaring: decompress_to_bitset, enumerate_ids,
+// promote_to_bitmap / promote_auto and the deep copy.
+//
+// Output semantics follow the reference (src/decompress.cu:104-162,
+// src/to_csr.cu:161-220, src/promote.cu:178-385).  None of these calls
+// synchronises its stream (the reference's contract for them).
+//
+// Array and run containers are expanded into a 2048-word image in LDS; a run
+// sets its head and tail words with ds_or and marks the whole words between
+// them in a difference array, whose prefix sum then fills them, so a long run
+// costs the workgroup O(1) per run plus one pass over the 2048 words.
+#include <algorithm>
+#include <cstring>
+
+#include "internal.hpp"
+
+namespace crimpl {
+
+namespace {
+
+constexpr int CV_NT = 256;            // threads of every conversion workgroup
+constexpr int CV_WPT = 2048 / CV_NT;  // image words per thread (8)
+
+struct alignas(16) Image {
+    uint32_t w[2048];
+    int32_t cover[2048];
+};
+
+__device__ __forceinline__ uint32_t bit_span(uint32_t lo, uint32_t hi)  // bits lo..hi of a word, lo <= hi < 32
+{
+    const uint32_t n = hi - lo + 1u;
+    return (n == 32u ? ~0u : ((1u << n) - 1u)) << lo;
+}
+
+// Builds container data (ARRAY values or RUN pairs, `card` of them) into
+// img->w; every thread of the workgroup calls it.  Run ends are clamped to
+// 0xFFFF (src/decompress.cu:71-72).
+__device__ void expand_to_lds(const uint8_t type, const uint16_t* data, uint32_t card, Image* img)
+{
+    const uint32_t t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < CV_WPT; ++j) {
+        img->w[j * CV_NT + t] = 0;
+        img->cover[j * CV_NT + t] = 0;
+    }
+    __syncthreads();
+    if (type == CR_ARRAY) {
+        for (uint32_t i = t; i < card; i += CV_NT) {
+            const uint32_t v = data[i];
+            atomicOr(&img->w[v >> 5], 1u << (v & 31u));
+        }
+        __syncthreads();
+        return;
+    }
+    for (uint32_t k = t; k < card; k += CV_NT) {
+        const uint32_t s = data[2 * k];
+        const uint32_t e = min(0xFFFFu, s + data[2 * k + 1]);
+        const uint32_t hw = s >> 5, tw = e >> 5;
+        if (hw == tw) {
+            atomicOr(&img->w[hw], bit_span(s & 31u, e & 31u));
+        } else {
+            atomicOr(&img->w[hw], bit_span(s & 31u, 31u));
+            atomicOr(&img->w[tw], bit_span(0u, e & 31u));
+            if (tw > hw + 1u) {
+                atomicAdd(&img->cover[hw + 1u], 1);
+                atomicAdd(&img->cover[tw], -1);
+            }
+        }
+    }
+    __syncthreads();
+    // prefix sum of the difference array: thread t owns words [8t, 8t + 8)
+    int32_t c[CV_WPT];
+    uint32_t local = 0;
+#pragma unroll
+    for (int j = 0; j < CV_WPT; ++j) {
+        c[j] = img->cover[CV_WPT * t + j];
+        local += static_cast<uint32_t>(c[j]);
+    }
+    __shared__ uint32_t red[CV_NT / 64];
+    uint32_t total;
+    int32_t run = static_cast<int32_t>(block_excl_scan<CV_NT>(local, red, total));
+#pragma unroll
+    for (int j = 0; j < CV_WPT; ++j) {
+        run += c[j];
+        if (run > 0) img->w[CV_WPT * t + j] = ~0u;
+    }
+    __syncthreads();
+}
+
+// ---- decompress_to_bitset ---------------------------------------------------
+// One workgroup per 2048-word key region of the output: the region is written
+// once (the container's bits, zeros when the key is absent), and the
+// complement of a negated bitmap is applied on the way out (words below U/32
+// inverted, the tail word's valid bits flipped, src/decompress.cu:128-150).
+// Writes stay below n_words.
+__global__ __launch_bounds__(CV_NT) void cv_decompress(cr_gpu_roaring r, uint32_t* __restrict__ out, uint32_t n_words)
+{
+    __shared__ Image img;
+    __shared__ int32_t s_c;
+    const uint32_t key = blockIdx.x;
+    const uint32_t t = threadIdx.x;
+    if (t < 64) {
+        const uint32_t pos = wave_lower_bound_u16(r.keys, r.n_containers, key);
+        if (t == 0) s_c = (pos < r.n_containers && r.keys[pos] == key) ? static_cast<int32_t>(pos) : -1;
+    }
+    __syncthreads();
+    const int32_t c = s_c;
+    const uint8_t type = c >= 0 ? r.types[c] : 0xFFu;
+    const uint32_t* src;
+    if (type == CR_BITMAP) {
+        src = reinterpret_cast<const uint32_t*>(r.bitmap_data + r.offsets[c] / 8u);
+    } else {
+        if (type == CR_ARRAY)
+            expand_to_lds(CR_ARRAY, r.array_data + r.offsets[c] / 2u, r.cardinalities[c], &img);
+        else if (type == CR_RUN)
+            expand_to_lds(CR_RUN, r.run_data + r.offsets[c] / 2u, r.cardinalities[c], &img);
+        else {
+#pragma unroll
+            for (int j = 0; j < CV_WPT; ++j) img.w[j * CV_NT + t] = 0;
+            __syncthreads();
+        }
+        src = img.w;
+    }
+    const uint64_t w0 = static_cast<uint64_t>(key) * 2048u;
+    const uint32_t full = r.universe_size / 32u, tail = r.universe_size % 32u;
+    const bool neg = r.negated;
+    uint32_t* dst = out + w0;
+    const bool vec = w0 + 2048u <= n_words &&
+                     ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15u) == 0;
+    if (vec && (!neg || w0 + 2048u <= full)) {
+        const uint4* s4 = reinterpret_cast<const uint4*>(src);
+        uint4* d4 = reinterpret_cast<uint4*>(dst);
+        uint4 v[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) v[j] = s4[j * CV_NT + t];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            if (neg) v[j] = make_uint4(~v[j].x, ~v[j].y, ~v[j].z, ~v[j].w);
+            d4[j * CV_NT + t] = v[j];
+        }
+        return;
+    }
+    for (uint32_t i = t; i < 2048u; i += CV_NT) {
+        const uint64_t w = w0 + i;
+        if (w >= n_words) break;
+        uint32_t v = src[i];
+        if (neg) {
+            if (w < full)
+                v = ~v;
+            else if (w == full && tail)
+                v ^= (1u << tail) - 1u;
+        }
+        dst[i] = v;
+    }
+}
+
+// ---- enumerate_ids ----------------------------------------------------------
+// Per-container id counts (a bitmap's popcount: the reference takes the stored
+// cardinality, which reads 0 for a full container), one exclusive scan, then
+// one workgroup per container writes its ids in order.  Bitmap and run
+// containers go through LDS: the low 16 bits of each 512-word chunk's ids are
+// staged in order and then written out as coalesced int64 stores.
+// Writes stay below `cap` ids.
+__global__ __launch_bounds__(CV_NT) void cv_enum_count(cr_gpu_roaring r, uint64_t* counts)
+{
+    const uint32_t c = (blockIdx.x * CV_NT + threadIdx.x) >> 6;
+    const uint32_t lane = __lane_id();
+    if (c >= r.n_containers) return;
+    const uint8_t type = r.types[c];
+    const uint32_t off = r.offsets[c];
+    uint32_t n = 0;
+    if (type == CR_BITMAP) {
+        const uint64_t* bm = r.bitmap_data + off / 8u;
+#pragma unroll 4
+        for (uint32_t w = lane; w < 1024u; w += 64) n += static_cast<uint32_t>(__popcll(bm[w]));
+    } else if (type == CR_ARRAY) {
+        n = lane == 0 ? r.cardinalities[c] : 0u;
+    } else if (type == CR_RUN) {
+        const uint16_t* runs = r.run_data + off / 2u;
+        for (uint32_t k = lane; k < r.cardinalities[c]; k += 64) n += static_cast<uint32_t>(runs[2 * k + 1]) + 1u;
+    }
+    n = wave_sum(n);
+    if (lane == 0) counts[c] = n;
+}
+
+// Exclusive scan of the counts in place (one workgroup of 1024; n <= 65536).
+__global__ __launch_bounds__(1024) void cv_enum_scan(uint64_t* counts, uint32_t n)
+{
+    __shared__ unsigned long long part[16];
+    const uint32_t t = threadIdx.x;
+    const uint32_t per = (n + 1023u) / 1024u;
+    const uint32_t lo = min(n, t * per), hi = min(n, lo + per);
+    unsigned long long s = 0;
+    for (uint32_t i = lo; i < hi; ++i) s += counts[i];
+    unsigned long long incl = s;
+    const uint32_t lane = __lane_id();
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const unsigned long long v = __shfl_up(incl, o, 64);
+        if (lane >= static_cast<uint32_t>(o)) incl += v;
+    }
+    const uint32_t w = t >> 6;
+    if (lane == 63) part[w] = incl;
+    __syncthreads();
+    unsigned long long run = incl - s;
+    for (uint32_t i = 0; i < w; ++i) run += part[i];
+    for (uint32_t i = lo; i < hi; ++i) {
+        const unsigned long long v = counts[i];
+        counts[i] = run;
+        run += v;
+    }
+}
+
+__global__ __launch_bounds__(CV_NT) void cv_enum_write(cr_gpu_roaring r, const uint64_t* starts, uint64_t cap,
+                                                       int64_t* __restrict__ out)
+{
+    __shared__ Image img;
+    __shared__ uint16_t stage[512 * 32];
+    __shared__ uint32_t red[CV_NT / 64];
+    const uint32_t c = blockIdx.x;
+    const uint32_t t = threadIdx.x;
+    const uint8_t type = r.types[c];
+    const uint32_t off = r.offsets[c];
+    const int64_t base = static_cast<int64_t>(r.keys[c]) << 16;
+    const uint64_t start = starts[c];
+    if (type == CR_ARRAY) {
+        const uint16_t* arr = r.array_data + off / 2u;
+        const uint32_t card = r.cardinalities[c];
+        for (uint32_t i = t; i < card; i += CV_NT)
+            if (start + i < cap) out[start + i] = base | arr[i];
+        return;
+    }
+    const uint32_t* words;
+    if (type == CR_BITMAP) {
+        words = reinterpret_cast<const uint32_t*>(r.bitmap_data + off / 8u);
+    } else if (type == CR_RUN) {
+        expand_to_lds(CR_RUN, r.run_data + off / 2u, r.cardinalities[c], &img);
+        words = img.w;
+    } else {
+        return;
+    }
+    // thread t owns words 2t, 2t+1 of each 512-word chunk
+    uint2 v[4];
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch) v[ch] = reinterpret_cast<const uint2*>(words)[ch * CV_NT + t];
+    uint64_t written = start;
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch) {
+        const uint32_t wi = ch * 512u + 2u * t;
+        uint32_t total;
+        uint32_t pos = block_excl_scan<CV_NT>(static_cast<uint32_t>(__popc(v[ch].x) + __popc(v[ch].y)), red, total);
+        for (uint32_t x = v[ch].x; x; x &= x - 1) stage[pos++] = static_cast<uint16_t>(32u * wi + __builtin_ctz(x));
+        for (uint32_t x = v[ch].y; x; x &= x - 1)
+            stage[pos++] = static_cast<uint16_t>(32u * (wi + 1u) + __builtin_ctz(x));
+        __syncthreads();
+        for (uint32_t i = t; i < total; i += CV_NT)
+            if (written + i < cap) out[written + i] = base | stage[i];
+        written += total;
+        __syncthreads();
+    }
+}
+
+// ---- promote_to_bitmap ------------------------------------------------------
+// One workgroup per container: keys and cards copied (a RUN card keeps its
+// n_runs), type BITMAP at offset c * 8192, the 8 KiB image (copied, or built
+// in LDS from an array / run container), and its key_index slot.  With no
+// array or run container the bitmap pool is copied as it lies, container c
+// taking pool words [c * 1024, c * 1024 + 1024) (src/promote.cu:268-276).
+__global__ __launch_bounds__(CV_NT) void cv_promote(cr_gpu_roaring src, bool all_bitmap, cr_gpu_roaring dst)
+{
+    __shared__ Image img;
+    const uint32_t c = blockIdx.x;
+    const uint32_t t = threadIdx.x;
+    const uint8_t type = src.types[c];
+    uint4* o4 = reinterpret_cast<uint4*>(dst.bitmap_data + static_cast<uint64_t>(c) * 1024u);
+    const uint32_t* words;
+    if (all_bitmap || type == CR_BITMAP) {
+        words = reinterpret_cast<const uint32_t*>(all_bitmap ? src.bitmap_data + static_cast<uint64_t>(c) * 1024u
+                                                             : src.bitmap_data + src.offsets[c] / 8u);
+    } else if (type == CR_ARRAY || type == CR_RUN) {
+        expand_to_lds(type, (type == CR_ARRAY ? src.array_data : src.run_data) + src.offsets[c] / 2u,
+                      src.cardinalities[c], &img);
+        words = img.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < CV_WPT; ++j) img.w[j * CV_NT + t] = 0;
+        __syncthreads();
+        words = img.w;
+    }
+    if ((reinterpret_cast<uintptr_t>(words) & 15u) == 0) {
+        const uint4* s4 = reinterpret_cast<const uint4*>(words);
+        uint4 v[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) v[j] = s4[j * CV_NT + t];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) o4[j * CV_NT + t] = v[j];
+    } else {
+        uint32_t* o = reinterpret_cast<uint32_t*>(o4);
+        for (uint32_t i = t; i < 2048u; i += CV_NT) o[i] = words[i];
+    }
+    if (t == 0) {
+        const uint16_t key = src.keys[c];
+        dst.keys[c] = key;
+        dst.cardinalities[c] = src.cardinalities[c];
+        dst.types[c] = CR_BITMAP;
+        dst.offsets[c] = c * 8192u;
+        if (dst.key_index && key <= dst.max_key) dst.key_index[key] = static_cast<uint16_t>(c);
+    }
+}
+
+// ---- deep copy: up to eight byte ranges in one launch -----------------------
+struct CopySeg {
+    const void* src;
+    void* dst;
+    uint64_t bytes;
+};
+struct CopyList {
+    CopySeg seg[8];
+    uint32_t n;
+};
+
+__global__ __launch_bounds__(256) void cv_copy(CopyList L)
+{
+    const uint32_t s = blockIdx.y;
+    if (s >= L.n) return;
+    const CopySeg g = L.seg[s];
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256u;
+    const uint64_t i0 = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
+    const uint8_t* sb = static_cast<const uint8_t*>(g.src);
+    uint8_t* db = static_cast<uint8_t*>(g.dst);
+    uint64_t done = 0;
+    if (((reinterpret_cast<uintptr_t>(g.src) | reinterpret_cast<uintptr_t>(g.dst)) & 15u) == 0) {
+        const uint64_t n4 = g.bytes / 16u;
+        const uint4* s4 = static_cast<const uint4*>(g.src);
+        uint4* d4 = static_cast<uint4*>(g.dst);
+        for (uint64_t i = i0; i < n4; i += stride) d4[i] = s4[i];
+        done = n4 * 16u;
+    }
+    for (uint64_t i = done + i0; i < g.bytes; i += stride) db[i] = sb[i];
+}
+
+int copy_segments(const CopyList& L, hipStream_t s)
+{
+    if (L.n == 0) return CR_OK;
+    uint64_t most = 0;
+    for (uint32_t i = 0; i < L.n; ++i) most = std::max(most, L.seg[i].bytes);
+    const uint64_t want = (most / 16u + 255u) / 256u;
+    const uint32_t gx = static_cast<uint32_t>(std::max<uint64_t>(1, std::min<uint64_t>(want, 4096u)));
+    cv_copy<<<dim3(gx, L.n), 256, 0, s>>>(L);
+    CR_LAUNCH_CHECK();
+    return CR_OK;
+}
+
+int deep_copy_impl(const cr_gpu_roaring* bm, hipStream_t s, cr_gpu_roaring* out)
+{
+    cr_gpu_roaring r{};
+    r.n_containers = bm->n_containers;
+    r.n_bitmap_containers = bm->n_bitmap_containers;
+    r.n_array_containers = bm->n_array_containers;
+    r.n_run_containers = bm->n_run_containers;
+    r.universe_size = bm->universe_size;
+    r.total_cardinality = bm->total_cardinality;
+    r.negated = bm->negated;
+    r.max_key = bm->max_key;
+    r.array_pool_bytes = bm->array_pool_bytes;
+    r.run_pool_bytes = bm->run_pool_bytes;
+    const uint64_t n = bm->n_containers;
+    if (n == 0) {  // src/promote.cu:194
+        *out = r;
+        return CR_OK;
+    }
+    // src/promote.cu:208-231: the bitmap pool copies n_bitmap x 8 KiB, the
+    // array / run pools their byte counts, key_index max_key + 1 entries when
+    // present and the universe is non-zero.
+    const uint64_t bmp_words = (bm->bitmap_data && bm->n_bitmap_containers) ? bm->n_bitmap_containers * 1024ull : 0;
+    const uint64_t arr_bytes = (bm->array_data && bm->array_pool_bytes) ? bm->array_pool_bytes : 0;
+    const uint64_t run_bytes = (bm->run_data && bm->run_pool_bytes) ? bm->run_pool_bytes : 0;
+    const uint64_t kidx_len = (bm->key_index && bm->universe_size > 0) ? bm->max_key + 1ull : 0;
+    const OutLayout L = plan_out(n, kidx_len, bmp_words, (arr_bytes + 1) / 2, (run_bytes + 1) / 2);
+    CR_RET(alloc_out(&r, L, n, kidx_len, bmp_words, (arr_bytes + 1) / 2, (run_bytes + 1) / 2, s));
+    CopyList cl{};
+    auto add = [&](const void* from, void* to, uint64_t bytes) {
+        if (bytes) cl.seg[cl.n++] = {from, to, bytes};
+    };
+    add(bm->keys, r.keys, n * 2u);
+    add(bm->types, r.types, n);
+    add(bm->offsets, r.offsets, n * 4u);
+    add(bm->cardinalities, r.cardinalities, n * 2u);
+    add(bm->bitmap_data, r.bitmap_data, bmp_words * 8u);
+    add(bm->array_data, r.array_data, arr_bytes);
+    add(bm->run_data, r.run_data, run_bytes);
+    add(bm->key_index, r.key_index, kidx_len * 2u);
+    int rc;
+    {
+        CR_TIMED("cv_copy", s);
+        rc = copy_segments(cl, s);
+    }
+    if (rc != CR_OK) {
+        free_async(&r, s);
+        return rc;
+    }
+    *out = r;
+    return CR_OK;
+}
+
+int promote_impl(const cr_gpu_roaring* bm, hipStream_t s, cr_gpu_roaring* out)
+{
+    cr_gpu_roaring r{};
+    const uint64_t n = bm->n_containers;
+    if (n == 0) {  // GpuRoaring{} (src/promote.cu:236)
+        *out = r;
+        return CR_OK;
+    }
+    uint64_t kidx_len = 0;
+    if (bm->universe_size > 0) {  // src/promote.cu:307-320
+        r.max_key = std::min<uint32_t>((bm->universe_size - 1u) >> 16, 0xFFFFu);
+        kidx_len = r.max_key + 1ull;
+    }
+    const OutLayout L = plan_out(n, kidx_len, n * 1024u, 0, 0);
+    CR_RET(alloc_out(&r, L, n, kidx_len, n * 1024u, 0, 0, s));
+    r.n_containers = static_cast<uint32_t>(n);
+    r.n_bitmap_containers = static_cast<uint32_t>(n);
+    r.universe_size = bm->universe_size;
+    r.total_cardinality = bm->total_cardinality;
+    r.negated = bm->negated;
+    int rc = CR_OK;
+    if (kidx_len) rc = fill_u16(r.key_index, 0xFFFFu, kidx_len, s);
+    if (rc == CR_OK) {
+        const bool all_bitmap = bm->n_array_containers == 0 && bm->n_run_containers == 0;
+        CR_TIMED("cv_promote", s);
+        cv_promote<<<static_cast<uint32_t>(n), CV_NT, 0, s>>>(*bm, all_bitmap, r);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) {
+            set_error("cv_promote launch: %s", hipGetErrorString(e));
+            rc = CR_ERR_HIP;
+        }
+    }
+    if (rc != CR_OK) {
+        free_async(&r, s);
+        return rc;
+    }
+    *out = r;
+    return CR_OK;
+}
+
+int enumerate_impl(const cr_gpu_roaring* bm, int64_t* d_out, uint64_t cap, hipStream_t s)
+{
+    if (bm->n_containers == 0 || bm->total_cardinality == 0) return CR_OK;  // src/to_csr.cu:163
+    if (!d_out) {
+        set_error("cr_enumerate_ids: null output");
+        return CR_ERR_INVALID;
+    }
+    const uint32_t n = bm->n_containers;
+    Scratch sc;
+    CR_RET(sc.alloc(n * 8ull, s));
+    uint64_t* counts = sc.at<uint64_t>(0);
+    {
+        CR_TIMED("cv_enum_count", s);
+        cv_enum_count<<<(n + 3) / 4, CV_NT, 0, s>>>(*bm, counts);
+    }
+    {
+        CR_TIMED("cv_enum_scan", s);
+        cv_enum_scan<<<1, 1024, 0, s>>>(counts, n);
+    }
+    {
+        CR_TIMED("cv_enum_write", s);
+        cv_enum_write<<<n, CV_NT, 0, s>>>(*bm, counts, cap, d_out);
+    }
+    CR_LAUNCH_CHECK();
+    return CR_OK;
+}
+
+// Ids that enumerate_ids writes for `bm`: the stored set, which for a negated
+// bitmap is the complement of its logical set within [0, U).
+uint64_t stored_cardinality(const cr_gpu_roaring* bm)
+{
+    if (!bm->negated) return bm->total_cardinality;
+    return bm->universe_size > bm->total_cardinality ? bm->universe_size - bm->total_cardinality : 0;
+}
+
+}  // namespace
+}  // namespace crimpl
+
+using namespace crimpl;
+
+extern "C" int cr_decompress_to_bitset(const cr_gpu_roaring* bm, uint32_t* d_out, uint32_t n_words,
+                                       cr_stream_t stream)
+{
+    if (!bm || (n_words && !d_out)) {
+        set_error("cr_decompress_to_bitset: invalid argument");
+        return CR_ERR_INVALID;
+    }
+    if (n_words == 0) return CR_OK;
+    hipStream_t s = as_stream(stream);
+    const uint32_t regions = static_cast<uint32_t>((static_cast<uint64_t>(n_words) + 2047u) / 2048u);
+    {
+        CR_TIMED("cv_decompress", s);
+        cv_decompress<<<regions, CV_NT, 0, s>>>(*bm, d_out, n_words);
+    }
+    CR_LAUNCH_CHECK();
+    return CR_OK;
+}
+
+extern "C" int cr_decompress_to_bitset_alloc(const cr_gpu_roaring* bm, cr_stream_t stream, uint32_t** d_out,
+                                             uint32_t* n_words)
+{
+    if (!bm || !d_out || !n_words) {
+        set_error("cr_decompress_to_bitset_alloc: invalid argument");
+        return CR_ERR_INVALID;
+    }
+    *d_out = nullptr;
+    *n_words = static_cast<uint32_t>((static_cast<uint64_t>(bm->universe_size) + 31u) / 32u);
+    if (*n_words == 0) return CR_OK;  // src/decompress.cu:155-156
+    CR_HIP_RET(hipMalloc(reinterpret_cast<void**>(d_out), *n_words * 4ull));
+    const int rc = cr_decompress_to_bitset(bm, *d_out, *n_words, stream);
+    if (rc != CR_OK) {
+        (void)hipFree(*d_out);
+        *d_out = nullptr;
+    }
+    return rc;
+}
+
+extern "C" int cr_enumerate_ids(const cr_gpu_roaring* bm, int64_t* d_out, uint64_t out_capacity, cr_stream_t stream)
+{
+    if (!bm) {
+        set_error("cr_enumerate_ids: invalid argument");
+        return CR_ERR_INVALID;
+    }
+    return enumerate_impl(bm, d_out, out_capacity, as_stream(stream));
+}
+
+extern "C" int cr_enumerate_ids_alloc(const cr_gpu_roaring* bm, cr_stream_t stream, int64_t** d_out,
+                                      uint64_t* n_out)
+{
+    if (!bm || !d_out) {
+        set_error("cr_enumerate_ids_alloc: invalid argument");
+        return CR_ERR_INVALID;
+    }
+    *d_out = nullptr;
+    if (n_out) *n_out = 0;
+    if (bm->total_cardinality == 0) return CR_OK;  // src/to_csr.cu:213
+    const uint64_t n = stored_cardinality(bm);
+    if (n == 0) return CR_OK;
+    CR_HIP_RET(hipMalloc(reinterpret_cast<void**>(d_out), n * 8ull));
+    const int rc = enumerate_impl(bm, *d_out, n, as_stream(stream));
+    if (rc != CR_OK) {
+        (void)hipFree(*d_out);
+        *d_out = nullptr;
+        return rc;
+    }
+    if (n_out) *n_out = n;
+    return CR_OK;
+}
+
+extern "C" int cr_promote_to_bitmap(const cr_gpu_roaring* bm, cr_stream_t stream, cr_gpu_roaring* out)
+{
+    if (!bm || !out) {
+        set_error("cr_promote_to_bitmap: invalid argument");
+        return CR_ERR_INVALID;
+    }
+    return promote_impl(bm, as_stream(stream), out);
+}
+
+extern "C" int cr_deep_copy(const cr_gpu_roaring* bm, cr_stream_t stream, cr_gpu_roaring* out)
+{
+    if (!bm || !out) {
+        set_error("cr_deep_copy: invalid argument");
+        return CR_ERR_INVALID;
+    }
+    return deep_copy_impl(bm, as_stream(stream), out);
+}
+
+extern "C" int cr_promote_auto(const cr_gpu_roaring* bm, cr_stream_t stream, int device_id, cr_gpu_roaring* out)
+{
+    if (!bm || !out) {
+        set_error("cr_promote_auto: invalid argument");
+        return CR_ERR_INVALID;
+    }
+    uint32_t thr = 0;
+    CR_RET(cr_resolve_auto_threshold(bm->universe_size, device_id, &thr));
+    if (thr == CR_PROMOTE_ALL && (bm->n_array_containers > 0 || bm->n_run_containers > 0))
+        return promote_impl(bm, as_stream(stream), out);  // src/promote.cu:369-385
+    return deep_copy_impl(bm, as_stream(stream), out);
+}

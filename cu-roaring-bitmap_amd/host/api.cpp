@@ -19,6 +19,53 @@ uint32_t resolve_auto_threshold(uint32_t universe_size, int device_id)
     return t;
 }
 
+GpuRoaring promote_to_bitmap(const GpuRoaring& bm, hipStream_t stream)
+{
+    GpuRoaring r;
+    throw_on_error(cr_promote_to_bitmap(to_abi(&bm), S(stream), to_abi(&r)), "promote_to_bitmap");
+    return r;
+}
+
+GpuRoaring promote_auto(const GpuRoaring& bm, hipStream_t stream, int device_id)
+{
+    GpuRoaring r;
+    throw_on_error(cr_promote_auto(to_abi(&bm), S(stream), device_id, to_abi(&r)), "promote_auto");
+    return r;
+}
+
+GpuRoaring gpu_roaring_deep_copy(const GpuRoaring& bm, hipStream_t stream)
+{
+    GpuRoaring r;
+    throw_on_error(cr_deep_copy(to_abi(&bm), S(stream), to_abi(&r)), "gpu_roaring_deep_copy");
+    return r;
+}
+
+uint32_t* decompress_to_bitset(const GpuRoaring& bitmap, hipStream_t stream)
+{
+    uint32_t* out = nullptr;
+    uint32_t n_words = 0;
+    throw_on_error(cr_decompress_to_bitset_alloc(to_abi(&bitmap), S(stream), &out, &n_words), "decompress_to_bitset");
+    return out;
+}
+
+void decompress_to_bitset(const GpuRoaring& bitmap, uint32_t* output, uint32_t output_size_words, hipStream_t stream)
+{
+    throw_on_error(cr_decompress_to_bitset(to_abi(&bitmap), output, output_size_words, S(stream)),
+                   "decompress_to_bitset");
+}
+
+void enumerate_ids(const GpuRoaring& bitmap, int64_t* output, hipStream_t stream)
+{
+    throw_on_error(cr_enumerate_ids(to_abi(&bitmap), output, UINT64_MAX, S(stream)), "enumerate_ids");
+}
+
+int64_t* enumerate_ids(const GpuRoaring& bitmap, hipStream_t stream)
+{
+    int64_t* out = nullptr;
+    throw_on_error(cr_enumerate_ids_alloc(to_abi(&bitmap), S(stream), &out, nullptr), "enumerate_ids");
+    return out;
+}
+
 GpuRoaring upload_from_ids(const uint32_t* ids, uint32_t n_ids, uint32_t universe_size, hipStream_t stream,
                            uint32_t bitmap_threshold)
 {

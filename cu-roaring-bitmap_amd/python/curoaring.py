@@ -32,6 +32,8 @@ EXPORTS = [
     "cr_free", "cr_free_async", "cr_resolve_auto_threshold", "cr_make_view", "cr_contains_batch",
     "cr_topk_filtered", "cr_device_l2_bytes", "cr_device_malloc", "cr_device_free", "cr_memcpy_h2d",
     "cr_memcpy_d2h", "cr_stream_synchronize", "cr_timing_enable", "cr_timing_report", "cr_mempool_trim",
+    "cr_decompress_to_bitset", "cr_decompress_to_bitset_alloc", "cr_enumerate_ids", "cr_enumerate_ids_alloc",
+    "cr_promote_to_bitmap", "cr_promote_auto", "cr_deep_copy",
 ]
 
 
@@ -136,6 +138,13 @@ def load(path: Optional[str] = None):
         "cr_timing_enable": [C.c_int],
         "cr_mempool_trim": [C.c_int, C.c_size_t],
         "cr_timing_report": [C.c_char_p, C.c_size_t],
+        "cr_decompress_to_bitset": [P(GpuRoaring), C.c_void_p, C.c_uint32, C.c_void_p],
+        "cr_decompress_to_bitset_alloc": [P(GpuRoaring), C.c_void_p, P(C.c_void_p), P(C.c_uint32)],
+        "cr_enumerate_ids": [P(GpuRoaring), C.c_void_p, C.c_uint64, C.c_void_p],
+        "cr_enumerate_ids_alloc": [P(GpuRoaring), C.c_void_p, P(C.c_void_p), P(C.c_uint64)],
+        "cr_promote_to_bitmap": [P(GpuRoaring), C.c_void_p, P(GpuRoaring)],
+        "cr_promote_auto": [P(GpuRoaring), C.c_void_p, C.c_int, P(GpuRoaring)],
+        "cr_deep_copy": [P(GpuRoaring), C.c_void_p, P(GpuRoaring)],
     }
     for name, args in sigs.items():
         f = getattr(L, name)
@@ -280,6 +289,61 @@ def topk_filtered(d_base, d_queries, k: int, filt: Optional[GpuRoaring], d_dist,
     _check(load().cr_topk_filtered(_dptr(d_base), n_base, _dptr(d_queries), nq, dim,
                                    C.byref(filt) if filt is not None else None, k, _dptr(d_dist), _dptr(d_ids),
                                    _stream(stream)), "topk_filtered")
+
+
+# ---- conversions (stream-ordered, no synchronisation) -------------------------
+NO_BOUND = 0xFFFFFFFFFFFFFFFF
+
+
+def decompress_to_bitset(g: GpuRoaring, d_out, n_words: Optional[int] = None, stream=None):
+    """decompress_to_bitset into d_out (a CUDA tensor of >= n_words 32-bit words)."""
+    if n_words is None:
+        n_words = d_out.numel()
+    _check(load().cr_decompress_to_bitset(C.byref(g), _dptr(d_out), n_words, _stream(stream)),
+           "decompress_to_bitset")
+
+
+def decompress_to_bitset_alloc(g: GpuRoaring, stream=None):
+    """The allocating overload: (device pointer or None, n_words); free with device_free."""
+    p, n = C.c_void_p(), C.c_uint32()
+    _check(load().cr_decompress_to_bitset_alloc(C.byref(g), _stream(stream), C.byref(p), C.byref(n)),
+           "decompress_to_bitset_alloc")
+    return p.value, n.value
+
+
+def enumerate_ids(g: GpuRoaring, d_out, capacity: int = NO_BOUND, stream=None):
+    """enumerate_ids into d_out (a CUDA int64 tensor)."""
+    _check(load().cr_enumerate_ids(C.byref(g), _dptr(d_out), capacity, _stream(stream)), "enumerate_ids")
+
+
+def enumerate_ids_alloc(g: GpuRoaring, stream=None):
+    """The allocating overload: (device pointer or None, n_ids); free with device_free."""
+    p, n = C.c_void_p(), C.c_uint64()
+    _check(load().cr_enumerate_ids_alloc(C.byref(g), _stream(stream), C.byref(p), C.byref(n)), "enumerate_ids_alloc")
+    return p.value, n.value
+
+
+def promote_to_bitmap(g: GpuRoaring, stream=None) -> GpuRoaring:
+    out = GpuRoaring()
+    _check(load().cr_promote_to_bitmap(C.byref(g), _stream(stream), C.byref(out)), "promote_to_bitmap")
+    return out
+
+
+def promote_auto(g: GpuRoaring, stream=None, device: int = -1) -> GpuRoaring:
+    out = GpuRoaring()
+    _check(load().cr_promote_auto(C.byref(g), _stream(stream), device, C.byref(out)), "promote_auto")
+    return out
+
+
+def deep_copy(g: GpuRoaring, stream=None) -> GpuRoaring:
+    out = GpuRoaring()
+    _check(load().cr_deep_copy(C.byref(g), _stream(stream), C.byref(out)), "deep_copy")
+    return out
+
+
+def device_free(ptr):
+    if ptr:
+        _check(load().cr_device_free(ptr), "device_free")
 
 
 def synchronize(stream=None):

@@ -178,6 +178,44 @@ int cr_topk_filtered(const float* d_base, uint64_t n_base, const float* d_querie
                      const cr_gpu_roaring* filter, uint32_t k, float* d_out_dist, int64_t* d_out_ids,
                      cr_stream_t stream);
 
+/* ---- conversions --------------------------------------------------------
+ * These calls are stream-ordered and do NOT synchronise `stream` (the
+ * reference's contract for them, decompress.cuh / to_csr.cuh / promote.cuh:45-47).
+ * Buffers returned by the *_alloc variants come from hipMalloc; free them
+ * with cr_device_free (hipFree). */
+/* decompress_to_bitset into a pre-allocated buffer
+ * (include/cu_roaring/detail/decompress.cuh:13-16; src/decompress.cu:104-151):
+ * d_out[0, n_words) receives the flat bitset, complemented within U when the
+ * bitmap is negated.  Writes stay below n_words (the reference's complement
+ * pass writes U/32 words whatever n_words is). */
+int cr_decompress_to_bitset(const cr_gpu_roaring* bm, uint32_t* d_out, uint32_t n_words, cr_stream_t stream);
+/* decompress_to_bitset, allocating (decompress.cuh:10-11; src/decompress.cu:153-162):
+ * *n_words = ceil(U / 32); U == 0 gives *d_out = NULL. */
+int cr_decompress_to_bitset_alloc(const cr_gpu_roaring* bm, cr_stream_t stream, uint32_t** d_out, uint32_t* n_words);
+/* enumerate_ids into a pre-allocated buffer
+ * (include/cu_roaring/detail/to_csr.cuh:35; src/to_csr.cu:161-209): the stored
+ * ids in ascending order as int64 (negation is ignored, as in the reference);
+ * nothing is written when n_containers or total_cardinality is 0.  At most
+ * `out_capacity` ids are written (UINT64_MAX: no bound, the reference's
+ * behaviour). */
+int cr_enumerate_ids(const cr_gpu_roaring* bm, int64_t* d_out, uint64_t out_capacity, cr_stream_t stream);
+/* enumerate_ids, allocating (to_csr.cuh:46; src/to_csr.cu:211-220).  The
+ * buffer holds total_cardinality ids, or U - total_cardinality for a negated
+ * bitmap (whose stored ids the call writes; the reference's buffer would be
+ * too small there); *n_out (may be NULL) receives that count.
+ * total_cardinality == 0 gives *d_out = NULL. */
+int cr_enumerate_ids_alloc(const cr_gpu_roaring* bm, cr_stream_t stream, int64_t** d_out, uint64_t* n_out);
+/* promote_to_bitmap (include/cu_roaring/detail/promote.cuh:48; src/promote.cu:233-323):
+ * a new all-bitmap GpuRoaring; cardinalities are copied verbatim (a run
+ * container's entry keeps its run count), key_index/max_key come from U. */
+int cr_promote_to_bitmap(const cr_gpu_roaring* bm, cr_stream_t stream, cr_gpu_roaring* out);
+/* promote_auto (promote.cuh:63-64; src/promote.cu:369-385): promote_to_bitmap
+ * when resolve_auto_threshold gives PROMOTE_ALL and an array or run container
+ * exists, else a deep copy.  device_id -1 = current device. */
+int cr_promote_auto(const cr_gpu_roaring* bm, cr_stream_t stream, int device_id, cr_gpu_roaring* out);
+/* gpu_roaring_deep_copy (promote.cuh:83; src/promote.cu:178-231). */
+int cr_deep_copy(const cr_gpu_roaring* bm, cr_stream_t stream, cr_gpu_roaring* out);
+
 /* ---- utilities (no reference counterpart) -------------------------------- */
 /* L2 size the AUTO rule uses for `device_id` (hipDeviceAttributeL2CacheSize). */
 int cr_device_l2_bytes(int device_id, uint64_t* out_bytes);
