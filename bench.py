@@ -202,9 +202,83 @@ def secondary(torch, cr, flush):
     q["bitmap"] = "10% of 2^30 ids (all-bitmap, 16384 containers)"
     q["queries"] = nq
     out["contains_10pct_2^30"] = q
-    cr.free(bm)
     log("queries done", q)
+    del q_uni, q_clu, win, off, res, chk, cres
+    torch.cuda.empty_cache()
+    sparse = sparse_arrays(cr, 0.005, 60)
+    out["conversions_2^30"] = conversions(torch, cr, flush, {"dense_10pct_bitmap": bm, "sparse_0.5pct_array": sparse})
+    cr.free(sparse)
+    cr.free(bm)
     return out
+
+
+def sparse_arrays(cr, density, seed):
+    """`density` of 2^30 as array containers through the packed upload
+    (upload_from_ids builds all-bitmap above 1024 ids, whatever the threshold)."""
+    import numpy as np
+    ids = np.unique(np.random.default_rng(seed).integers(0, U, int(density * U), dtype=np.uint64))
+    bounds = np.searchsorted(ids, np.arange((U >> 16) + 1, dtype=np.uint64) << np.uint64(16))
+    conts = [(k, cr.TC_ARRAY, int(bounds[k + 1] - bounds[k]),
+              (ids[bounds[k]:bounds[k + 1]] & np.uint64(0xFFFF)).astype(np.uint16))
+             for k in range(U >> 16) if bounds[k + 1] > bounds[k]]
+    return cr.upload_containers(conts, U, False, int(ids.size), cr.PROMOTE_KEEP_DEFAULT)
+
+
+def conversions(torch, cr, flush, bitmaps):
+    """decompress_to_bitset, enumerate_ids, promote_to_bitmap and the deep copy on
+    2^30 bitmaps, cold.  Algorithmic bytes: the container payloads read (8192 B per
+    bitmap, 2 B per array value), 9 B of metadata per container, plus what the call
+    writes (4 B per bitset word, 8 B per id, 8192 B per promoted container, the copy)."""
+    res = {}
+    for name, g in bitmaps.items():
+        n = g.n_containers
+        payload = 8192 * g.n_bitmap_containers + g.array_pool_bytes + g.run_pool_bytes + 9 * n
+        kidx = 2 * (g.max_key + 1) if g.key_index else 0
+        n_ids = g.total_cardinality
+        words = torch.empty(U // 32, dtype=torch.int32, device="cuda")
+        ids_out = torch.empty(n_ids, dtype=torch.int64, device="cuda")
+        cases = {
+            "decompress_to_bitset": (lambda: cr.decompress_to_bitset(g, words), payload + 4 * (U // 32),
+                                     "cv_decompress", None),
+            "enumerate_ids": (lambda: cr.enumerate_ids(g, ids_out), payload + 8 * n_ids, "cv_enum_write", None),
+            "promote_to_bitmap": (lambda: kept.append(cr.promote_to_bitmap(g)),
+                                  payload + 8192 * n + 9 * n + 2 * (g.max_key + 1), "cv_promote", True),
+            "deep_copy": (lambda: kept.append(cr.deep_copy(g)), 2 * (payload + kidx), "cv_copy", True),
+        }
+        r = {"n_containers": n, "n_bitmap": g.n_bitmap_containers, "n_array": g.n_array_containers, "ids": n_ids}
+        for cname, (fn, nbytes, kname, frees) in cases.items():
+            kept = []
+            fn()
+            torch.cuda.synchronize()
+            for x in kept:
+                cr.free(x)
+            kept.clear()
+            cr.timing_enable(True)
+            t = cold_time(torch, fn, 5, flush)
+            rep = cr.timing_report()
+            cr.timing_enable(False)
+            for x in kept:
+                cr.free(x)
+            kn, kms = rep.get(kname, (1, float("nan")))
+            k_avg = kms / kn
+            r[cname] = {"algorithmic_bytes": nbytes, "api_ms": round(t, 4), "api_GBps": round(nbytes / t / 1e6, 1),
+                        f"{kname}_ms": round(k_avg, 4), f"{kname}_GBps": round(nbytes / k_avg / 1e6, 1),
+                        "frac_of_hbm_peak": round(nbytes / k_avg / 1e6 / HBM_PEAK_GBS, 4),
+                        "kernels_ms": {k: round(v[1] / v[0], 4) for k, v in rep.items()}}
+        # size-independent checks: enumerate gives ascending ids below U, and every
+        # sampled id's bit is set in the bitset
+        cr.enumerate_ids(g, ids_out)
+        cr.decompress_to_bitset(g, words)
+        torch.cuda.synchronize()
+        assert bool((ids_out[1:] > ids_out[:-1]).all()) and int(ids_out[-1]) < U, "enumerate_ids not ascending"
+        smp = ids_out[::997]
+        bits = (words[smp >> 5].to(torch.int64) >> (smp & 31)) & 1
+        assert bool((bits == 1).all()), "decompressed bitset misses an enumerated id"
+        del words, ids_out, smp, bits
+        torch.cuda.empty_cache()
+        res[name] = r
+        log("conversions", name, {k: v.get("frac_of_hbm_peak") for k, v in r.items() if isinstance(v, dict)})
+    return res
 
 
 TK_N, TK_Q, TK_DIM = 10_000_000, 1024, 128

@@ -41,7 +41,7 @@ __device__ void expand_to_lds(const uint8_t type, const uint16_t* data, uint32_t
 #pragma unroll
     for (int j = 0; j < CV_WPT; ++j) {
         img->w[j * CV_NT + t] = 0;
-        img->cover[j * CV_NT + t] = 0;
+        if (type == CR_RUN) img->cover[j * CV_NT + t] = 0;
     }
     __syncthreads();
     if (type == CR_ARRAY) {
@@ -99,7 +99,12 @@ __global__ __launch_bounds__(CV_NT) void cv_decompress(cr_gpu_roaring r, uint32_
     __shared__ int32_t s_c;
     const uint32_t key = blockIdx.x;
     const uint32_t t = threadIdx.x;
-    if (t < 64) {
+    if (r.key_index && key <= r.max_key) {  // one load through the key index
+        if (t == 0) {
+            const uint16_t e = r.key_index[key];
+            s_c = e == 0xFFFFu ? -1 : static_cast<int32_t>(e);
+        }
+    } else if (t < 64) {
         const uint32_t pos = wave_lower_bound_u16(r.keys, r.n_containers, key);
         if (t == 0) s_c = (pos < r.n_containers && r.keys[pos] == key) ? static_cast<int32_t>(pos) : -1;
     }
@@ -170,9 +175,18 @@ __global__ __launch_bounds__(CV_NT) void cv_enum_count(cr_gpu_roaring r, uint64_
     const uint32_t off = r.offsets[c];
     uint32_t n = 0;
     if (type == CR_BITMAP) {
-        const uint64_t* bm = r.bitmap_data + off / 8u;
-#pragma unroll 4
-        for (uint32_t w = lane; w < 1024u; w += 64) n += static_cast<uint32_t>(__popcll(bm[w]));
+        const uint64_t* p = r.bitmap_data + off / 8u;
+        if ((reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
+            // 8 KiB = 64 lanes x 8 loads of 16 bytes, all in flight together
+            const ulonglong2* bm = reinterpret_cast<const ulonglong2*>(p);
+            ulonglong2 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = bm[j * 64 + lane];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) n += static_cast<uint32_t>(__popcll(v[j].x) + __popcll(v[j].y));
+        } else {
+            for (uint32_t w = lane; w < 1024u; w += 64) n += static_cast<uint32_t>(__popcll(p[w]));
+        }
     } else if (type == CR_ARRAY) {
         n = lane == 0 ? r.cardinalities[c] : 0u;
     } else if (type == CR_RUN) {
@@ -183,16 +197,45 @@ __global__ __launch_bounds__(CV_NT) void cv_enum_count(cr_gpu_roaring r, uint64_
     if (lane == 0) counts[c] = n;
 }
 
-// Exclusive scan of the counts in place (one workgroup of 1024; n <= 65536).
-__global__ __launch_bounds__(1024) void cv_enum_scan(uint64_t* counts, uint32_t n)
+// starts = exclusive scan of counts.  One workgroup per tile of 1024 counts:
+// it sums every count before its tile (coalesced, eight loads per thread in
+// flight) and scans its own tile, so no workgroup waits for another.
+constexpr int SC_NT = 1024;
+
+__device__ __forceinline__ unsigned long long block_sum64(unsigned long long v, unsigned long long* part)
 {
-    __shared__ unsigned long long part[16];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    if (__lane_id() == 0) part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    unsigned long long t = 0;
+#pragma unroll
+    for (int i = 0; i < SC_NT / 64; ++i) t += part[i];
+    __syncthreads();
+    return t;
+}
+
+__global__ __launch_bounds__(SC_NT) void cv_enum_scan(const uint64_t* __restrict__ counts, uint32_t n,
+                                                      uint64_t* __restrict__ starts)
+{
+    __shared__ unsigned long long part[SC_NT / 64];
     const uint32_t t = threadIdx.x;
-    const uint32_t per = (n + 1023u) / 1024u;
-    const uint32_t lo = min(n, t * per), hi = min(n, lo + per);
+    const uint32_t tile0 = blockIdx.x * SC_NT;
     unsigned long long s = 0;
-    for (uint32_t i = lo; i < hi; ++i) s += counts[i];
-    unsigned long long incl = s;
+    for (uint32_t i0 = 0; i0 < tile0; i0 += 8 * SC_NT) {
+        unsigned long long v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t i = i0 + j * SC_NT + t;
+            v[j] = i < tile0 ? counts[i] : 0ull;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += v[j];
+    }
+    const unsigned long long base = block_sum64(s, part);
+    const uint32_t i = tile0 + t;
+    const unsigned long long x = i < n ? counts[i] : 0ull;
+    unsigned long long incl = x;
     const uint32_t lane = __lane_id();
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -202,13 +245,9 @@ __global__ __launch_bounds__(1024) void cv_enum_scan(uint64_t* counts, uint32_t 
     const uint32_t w = t >> 6;
     if (lane == 63) part[w] = incl;
     __syncthreads();
-    unsigned long long run = incl - s;
-    for (uint32_t i = 0; i < w; ++i) run += part[i];
-    for (uint32_t i = lo; i < hi; ++i) {
-        const unsigned long long v = counts[i];
-        counts[i] = run;
-        run += v;
-    }
+    unsigned long long pre = base + incl - x;
+    for (uint32_t k = 0; k < w; ++k) pre += part[k];
+    if (i < n) starts[i] = pre;
 }
 
 __global__ __launch_bounds__(CV_NT) void cv_enum_write(cr_gpu_roaring r, const uint64_t* starts, uint64_t cap,
@@ -258,6 +297,21 @@ __global__ __launch_bounds__(CV_NT) void cv_enum_write(cr_gpu_roaring r, const u
         written += total;
         __syncthreads();
     }
+}
+
+// Arrays-only input: one wave per container, no LDS.
+__global__ __launch_bounds__(CV_NT) void cv_enum_write_arrays(cr_gpu_roaring r, const uint64_t* starts, uint64_t cap,
+                                                              int64_t* __restrict__ out)
+{
+    const uint32_t c = (blockIdx.x * CV_NT + threadIdx.x) >> 6;
+    const uint32_t lane = __lane_id();
+    if (c >= r.n_containers || r.types[c] != CR_ARRAY) return;
+    const uint16_t* arr = r.array_data + r.offsets[c] / 2u;
+    const uint32_t card = r.cardinalities[c];
+    const int64_t base = static_cast<int64_t>(r.keys[c]) << 16;
+    const uint64_t start = starts[c];
+    for (uint32_t i = lane; i < card; i += 64)
+        if (start + i < cap) out[start + i] = base | arr[i];
 }
 
 // ---- promote_to_bitmap ------------------------------------------------------
@@ -452,19 +506,23 @@ int enumerate_impl(const cr_gpu_roaring* bm, int64_t* d_out, uint64_t cap, hipSt
     }
     const uint32_t n = bm->n_containers;
     Scratch sc;
-    CR_RET(sc.alloc(n * 8ull, s));
+    CR_RET(sc.alloc(n * 16ull, s));
     uint64_t* counts = sc.at<uint64_t>(0);
+    uint64_t* starts = sc.at<uint64_t>(n * 8ull);
     {
         CR_TIMED("cv_enum_count", s);
         cv_enum_count<<<(n + 3) / 4, CV_NT, 0, s>>>(*bm, counts);
     }
     {
         CR_TIMED("cv_enum_scan", s);
-        cv_enum_scan<<<1, 1024, 0, s>>>(counts, n);
+        cv_enum_scan<<<(n + SC_NT - 1) / SC_NT, SC_NT, 0, s>>>(counts, n, starts);
     }
     {
         CR_TIMED("cv_enum_write", s);
-        cv_enum_write<<<n, CV_NT, 0, s>>>(*bm, counts, cap, d_out);
+        if (bm->n_bitmap_containers == 0 && bm->n_run_containers == 0)
+            cv_enum_write_arrays<<<(n + 3) / 4, CV_NT, 0, s>>>(*bm, starts, cap, d_out);
+        else
+            cv_enum_write<<<n, CV_NT, 0, s>>>(*bm, starts, cap, d_out);
     }
     CR_LAUNCH_CHECK();
     return CR_OK;

@@ -64,6 +64,13 @@ def _make(gpu, kind):
         g = gpu.upload_containers(lite.containers(), U, False, lite.cardinality(), orc.PROMOTE_KEEP_DEFAULT)
         assert g.n_run_containers > 0 and g.n_array_containers > 0
         return g, ids
+    if kind == "arrays_only":
+        U = 40 * 65536 + 5
+        ids = np.unique(rng.integers(0, U, 12000, dtype=np.uint64)).astype(np.uint32)
+        lite = orc.Lite.from_sorted_ids(ids)
+        g = gpu.upload_containers(lite.containers(), U, False, lite.cardinality(), orc.PROMOTE_KEEP_DEFAULT)
+        assert g.n_array_containers == g.n_containers > 0 and g.key_index
+        return g, ids
     if kind == "negated_odd_u":
         U = 100003
         keep = rng.random(U) < 0.9
@@ -93,7 +100,7 @@ def _make(gpu, kind):
     raise ValueError(kind)
 
 
-KINDS = ["ids_keep", "ids_all_bitmap", "runs_mixed", "negated_odd_u", "negated_runs", "empty", "negated_empty",
+KINDS = ["ids_keep", "ids_all_bitmap", "runs_mixed", "arrays_only", "negated_odd_u", "negated_runs", "empty", "negated_empty",
          "setop_result"]
 
 
@@ -169,7 +176,7 @@ def test_enumerate_parity(gpu, kind):
     gpu.free(g)
 
 
-@pytest.mark.parametrize("kind", ["ids_keep", "runs_mixed", "negated_odd_u"])
+@pytest.mark.parametrize("kind", ["ids_keep", "runs_mixed", "arrays_only", "negated_odd_u"])
 def test_enumerate_capacity_bound(gpu, kind):
     _say("enumerate capacity", kind)
     torch = _torch()
