@@ -129,6 +129,10 @@ void rl_container_info(const rl_bitmap* b, uint32_t i, uint16_t* key, uint8_t* t
                        const void** data);
 void rl_to_containers(const rl_bitmap* b, orc_container* out);
 void rl_count_types(const rl_bitmap* b, uint32_t* n_bitset, uint32_t* n_array, uint32_t* n_run);
+/* Roaring portable format (roaring_lite.c documents the layout). */
+uint64_t rl_portable_size(const rl_bitmap* b);
+uint64_t rl_portable_serialize(const rl_bitmap* b, uint8_t* out);
+rl_bitmap* rl_portable_deserialize(const uint8_t* buf, uint64_t len, uint64_t* consumed);
 
 /* ---- generators --------------------------------------------------------- */
 typedef struct orc_mt19937 {

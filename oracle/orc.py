@@ -116,6 +116,12 @@ def lib():
         L.rl_n_containers.restype = C.c_uint32
         L.rl_to_containers.argtypes = [C.c_void_p, C.c_void_p]
         L.rl_count_types.argtypes = [C.c_void_p, P(C.c_uint32), P(C.c_uint32), P(C.c_uint32)]
+        L.rl_portable_size.argtypes = [C.c_void_p]
+        L.rl_portable_size.restype = C.c_uint64
+        L.rl_portable_serialize.argtypes = [C.c_void_p, C.c_void_p]
+        L.rl_portable_serialize.restype = C.c_uint64
+        L.rl_portable_deserialize.argtypes = [C.c_void_p, C.c_uint64, P(C.c_uint64)]
+        L.rl_portable_deserialize.restype = C.c_void_p
         # generators
         L.orc_mt_bernoulli_ids.argtypes = [C.c_uint32, C.c_double, C.c_uint32, C.c_void_p, P(C.c_uint64)]
         L.orc_mt_raw.argtypes = [C.c_uint32, C.c_void_p, C.c_uint64]
@@ -385,6 +391,23 @@ class Lite:
 
     def n_containers(self) -> int:
         return lib().rl_n_containers(self.h)
+
+    def portable_serialize(self) -> bytes:
+        """The Roaring portable format (roaring_bitmap_portable_serialize's layout)."""
+        n = lib().rl_portable_size(self.h)
+        buf = np.zeros(max(n, 1), dtype=np.uint8)
+        w = lib().rl_portable_serialize(self.h, _ptr(buf))
+        assert w == n
+        return buf[:n].tobytes()
+
+    @staticmethod
+    def portable_deserialize(data: bytes) -> "Lite":
+        buf = np.frombuffer(bytes(data) + b"\0", dtype=np.uint8)
+        used = C.c_uint64()
+        h = lib().rl_portable_deserialize(_ptr(buf), len(data), C.byref(used))
+        if not h:
+            raise ValueError("not a well-formed portable Roaring bitmap")
+        return Lite(h)
 
     def type_counts(self):
         a, b, c = C.c_uint32(), C.c_uint32(), C.c_uint32()

@@ -18,7 +18,10 @@
  * Pinning: tests/test_oracle_lite.py checks every operation against a
  * flat-bitset brute force on random inputs (uniform, clustered, full and empty
  * containers, the 65535/65536 boundary) and the run_optimize decision against
- * the serialized-size rule computed independently in numpy.
+ * the serialized-size rule computed independently in numpy.  The portable
+ * format writer and reader are pinned by byte strings assembled in the test
+ * from the format specification (cookies, run flags, the offset-header rule,
+ * card-1, each payload kind) and by round trips.
  *
  * The same code is the CPU baseline ("port") that bench.py times: merge /
  * galloping array intersection, word-wise bitset ops with popcount.
@@ -563,4 +566,198 @@ void rl_count_types(const rl_bitmap* b, uint32_t* n_bitset, uint32_t* n_array, u
         else
             ++*n_run;
     }
+}
+
+/* ---- portable serialization ------------------------------------------------
+ * The Roaring portable format (RoaringFormatSpec, the layout CRoaring's
+ * roaring_bitmap_portable_serialize writes), all fields little-endian:
+ *   cookie   no run container: u32 12346, u32 size;
+ *            otherwise: u16 12347, u16 size-1, then ceil(size/8) bytes whose
+ *            bit i (LSB first) marks container i as a run container;
+ *   header   size x (u16 key, u16 cardinality-1);
+ *   offsets  size x u32 byte offsets from the first cookie byte to each payload,
+ *            present iff there is no run container or size >= 4;
+ *   payloads in container order: run = u16 n_runs + n_runs x (u16 start,
+ *            u16 length-1); otherwise cardinality <= 4096: cardinality x u16
+ *            sorted values, else the 1024 x u64 bitset.
+ * A reader infers the kind from the run bit, then from the cardinality, and
+ * reads the payloads in sequence (offsets are not consulted). */
+#define PORTABLE_COOKIE_NO_RUN 12346u
+#define PORTABLE_COOKIE 12347u
+#define PORTABLE_NO_OFFSET_THRESHOLD 4u
+
+static uint32_t rl_true_card(const rl_bitmap* b, uint32_t i)
+{
+    if (b->tc[i] != ORC_TC_RUN) return (uint32_t)b->card[i];
+    const uint16_t* r = (const uint16_t*)b->data[i];
+    uint32_t t = 0;
+    for (int32_t k = 0; k < b->card[i]; ++k) t += (uint32_t)r[2 * k + 1] + 1u;
+    return t;
+}
+
+static int rl_has_run(const rl_bitmap* b)
+{
+    for (uint32_t i = 0; i < b->n; ++i)
+        if (b->tc[i] == ORC_TC_RUN) return 1;
+    return 0;
+}
+
+static uint64_t portable_header_bytes(uint32_t n, int has_run)
+{
+    uint64_t h = has_run ? 4u + (n + 7u) / 8u : 8u;
+    h += 4ull * n;
+    if (!has_run || n >= PORTABLE_NO_OFFSET_THRESHOLD) h += 4ull * n;
+    return h;
+}
+
+static uint64_t portable_payload_bytes(const rl_bitmap* b, uint32_t i)
+{
+    if (b->tc[i] == ORC_TC_RUN) return 2u + 4ull * (uint32_t)b->card[i];
+    const uint32_t card = rl_true_card(b, i);
+    return card <= ARRAY_MAX ? 2ull * card : 8192u;
+}
+
+uint64_t rl_portable_size(const rl_bitmap* b)
+{
+    uint64_t t = portable_header_bytes(b->n, rl_has_run(b));
+    for (uint32_t i = 0; i < b->n; ++i) t += portable_payload_bytes(b, i);
+    return t;
+}
+
+static void put16(uint8_t* p, uint32_t v)
+{
+    p[0] = (uint8_t)v;
+    p[1] = (uint8_t)(v >> 8);
+}
+static void put32(uint8_t* p, uint32_t v)
+{
+    put16(p, v & 0xFFFFu);
+    put16(p + 2, v >> 16);
+}
+static uint32_t get16(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+static uint32_t get32(const uint8_t* p) { return get16(p) | (get16(p + 2) << 16); }
+
+uint64_t rl_portable_serialize(const rl_bitmap* b, uint8_t* out)
+{
+    const uint32_t n = b->n;
+    const int has_run = rl_has_run(b);
+    uint8_t* p = out;
+    if (has_run) {
+        put16(p, PORTABLE_COOKIE);
+        put16(p + 2, n - 1u);
+        p += 4;
+        memset(p, 0, (n + 7u) / 8u);
+        for (uint32_t i = 0; i < n; ++i)
+            if (b->tc[i] == ORC_TC_RUN) p[i / 8u] |= (uint8_t)(1u << (i % 8u));
+        p += (n + 7u) / 8u;
+    } else {
+        put32(p, PORTABLE_COOKIE_NO_RUN);
+        put32(p + 4, n);
+        p += 8;
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        put16(p, b->keys[i]);
+        put16(p + 2, rl_true_card(b, i) - 1u);
+        p += 4;
+    }
+    uint64_t off = portable_header_bytes(n, has_run);
+    if (!has_run || n >= PORTABLE_NO_OFFSET_THRESHOLD) {
+        for (uint32_t i = 0; i < n; ++i) {
+            put32(p, (uint32_t)off);
+            p += 4;
+            off += portable_payload_bytes(b, i);
+        }
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        if (b->tc[i] == ORC_TC_RUN) {
+            const uint16_t* r = (const uint16_t*)b->data[i];
+            put16(p, (uint32_t)b->card[i]);
+            p += 2;
+            for (int32_t k = 0; k < 2 * b->card[i]; ++k, p += 2) put16(p, r[k]);
+            continue;
+        }
+        const uint32_t card = rl_true_card(b, i);
+        uint64_t* bits = to_bits(b->tc[i], b->card[i], b->data[i]);
+        if (card <= ARRAY_MAX) {
+            for (uint32_t w = 0; w < 1024u; ++w)
+                for (uint64_t x = bits[w]; x; x &= x - 1, p += 2) put16(p, w * 64u + (uint32_t)__builtin_ctzll(x));
+        } else {
+            for (uint32_t w = 0; w < 1024u; ++w, p += 8) {
+                put32(p, (uint32_t)bits[w]);
+                put32(p + 4, (uint32_t)(bits[w] >> 32));
+            }
+        }
+        free(bits);
+    }
+    return (uint64_t)(p - out);
+}
+
+/* NULL when `buf` is not a well-formed portable bitmap of at most `len` bytes
+ * (truncated, bad cookie, keys not strictly increasing, a run past 0xFFFF). */
+rl_bitmap* rl_portable_deserialize(const uint8_t* buf, uint64_t len, uint64_t* consumed)
+{
+    if (len < 4) return NULL;
+    const uint32_t c0 = get32(buf);
+    uint32_t n;
+    int has_run;
+    const uint8_t* run_flags = NULL;
+    uint64_t pos;
+    if ((c0 & 0xFFFFu) == PORTABLE_COOKIE) {
+        has_run = 1;
+        n = (c0 >> 16) + 1u;
+        run_flags = buf + 4;
+        pos = 4u + (n + 7u) / 8u;
+    } else if (c0 == PORTABLE_COOKIE_NO_RUN) {
+        if (len < 8) return NULL;
+        has_run = 0;
+        n = get32(buf + 4);
+        if (n > 65536u) return NULL;
+        pos = 8;
+    } else {
+        return NULL;
+    }
+    if (pos + 4ull * n > len) return NULL;
+    const uint8_t* hdr = buf + pos;
+    pos += 4ull * n;
+    if (!has_run || n >= PORTABLE_NO_OFFSET_THRESHOLD) pos += 4ull * n;
+    if (pos > len) return NULL;
+    rl_bitmap* b = rl_create();
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t key = get16(hdr + 4u * i);
+        const uint32_t card = get16(hdr + 4u * i + 2u) + 1u;
+        if (i > 0 && key <= b->keys[b->n - 1]) goto bad;
+        if (has_run && (run_flags[i / 8u] >> (i % 8u)) & 1u) {
+            if (pos + 2 > len) goto bad;
+            const uint32_t nr = get16(buf + pos);
+            pos += 2;
+            if (pos + 4ull * nr > len) goto bad;
+            uint16_t* r = (uint16_t*)malloc(4ull * nr + 4);
+            for (uint32_t k = 0; k < 2u * nr; ++k) r[k] = (uint16_t)get16(buf + pos + 2ull * k);
+            pos += 4ull * nr;
+            for (uint32_t k = 0; k < nr; ++k)
+                if ((uint32_t)r[2 * k] + r[2 * k + 1] > 0xFFFFu) {
+                    free(r);
+                    goto bad;
+                }
+            rl_push(b, (uint16_t)key, ORC_TC_RUN, (int32_t)nr, r);
+        } else if (card <= ARRAY_MAX) {
+            if (pos + 2ull * card > len) goto bad;
+            uint16_t* a = (uint16_t*)malloc(2ull * card);
+            for (uint32_t k = 0; k < card; ++k) a[k] = (uint16_t)get16(buf + pos + 2ull * k);
+            pos += 2ull * card;
+            rl_push(b, (uint16_t)key, ORC_TC_ARRAY, (int32_t)card, a);
+        } else {
+            if (pos + 8192 > len) goto bad;
+            uint64_t* w = (uint64_t*)malloc(8192);
+            for (uint32_t k = 0; k < 1024u; ++k)
+                w[k] = (uint64_t)get32(buf + pos + 8ull * k) | ((uint64_t)get32(buf + pos + 8ull * k + 4) << 32);
+            pos += 8192;
+            rl_push(b, (uint16_t)key, ORC_TC_BITSET, (int32_t)card, w);
+        }
+    }
+    if (consumed) *consumed = pos;
+    return b;
+bad:
+    rl_destroy(b);
+    return NULL;
 }
