@@ -4,88 +4,16 @@
 // Output semantics follow the reference (src/decompress.cu:104-162,
 // src/to_csr.cu:161-220, src/promote.cu:178-385).  None of these calls
 // synchronises its stream (the reference's contract for them).
-//
-// Array and run containers are expanded into a 2048-word image in LDS; a run
-// sets its head and tail words with ds_or and marks the whole words between
-// them in a difference array, whose prefix sum then fills them, so a long run
-// costs the workgroup O(1) per run plus one pass over the 2048 words.
+
 #include <algorithm>
 #include <cstring>
 
+#include "image.hpp"
 #include "internal.hpp"
 
 namespace crimpl {
 
 namespace {
-
-constexpr int CV_NT = 256;            // threads of every conversion workgroup
-constexpr int CV_WPT = 2048 / CV_NT;  // image words per thread (8)
-
-struct alignas(16) Image {
-    uint32_t w[2048];
-    int32_t cover[2048];
-};
-
-__device__ __forceinline__ uint32_t bit_span(uint32_t lo, uint32_t hi)  // bits lo..hi of a word, lo <= hi < 32
-{
-    const uint32_t n = hi - lo + 1u;
-    return (n == 32u ? ~0u : ((1u << n) - 1u)) << lo;
-}
-
-// Builds container data (ARRAY values or RUN pairs, `card` of them) into
-// img->w; every thread of the workgroup calls it.  Run ends are clamped to
-// 0xFFFF (src/decompress.cu:71-72).
-__device__ void expand_to_lds(const uint8_t type, const uint16_t* data, uint32_t card, Image* img)
-{
-    const uint32_t t = threadIdx.x;
-#pragma unroll
-    for (int j = 0; j < CV_WPT; ++j) {
-        img->w[j * CV_NT + t] = 0;
-        if (type == CR_RUN) img->cover[j * CV_NT + t] = 0;
-    }
-    __syncthreads();
-    if (type == CR_ARRAY) {
-        for (uint32_t i = t; i < card; i += CV_NT) {
-            const uint32_t v = data[i];
-            atomicOr(&img->w[v >> 5], 1u << (v & 31u));
-        }
-        __syncthreads();
-        return;
-    }
-    for (uint32_t k = t; k < card; k += CV_NT) {
-        const uint32_t s = data[2 * k];
-        const uint32_t e = min(0xFFFFu, s + data[2 * k + 1]);
-        const uint32_t hw = s >> 5, tw = e >> 5;
-        if (hw == tw) {
-            atomicOr(&img->w[hw], bit_span(s & 31u, e & 31u));
-        } else {
-            atomicOr(&img->w[hw], bit_span(s & 31u, 31u));
-            atomicOr(&img->w[tw], bit_span(0u, e & 31u));
-            if (tw > hw + 1u) {
-                atomicAdd(&img->cover[hw + 1u], 1);
-                atomicAdd(&img->cover[tw], -1);
-            }
-        }
-    }
-    __syncthreads();
-    // prefix sum of the difference array: thread t owns words [8t, 8t + 8)
-    int32_t c[CV_WPT];
-    uint32_t local = 0;
-#pragma unroll
-    for (int j = 0; j < CV_WPT; ++j) {
-        c[j] = img->cover[CV_WPT * t + j];
-        local += static_cast<uint32_t>(c[j]);
-    }
-    __shared__ uint32_t red[CV_NT / 64];
-    uint32_t total;
-    int32_t run = static_cast<int32_t>(block_excl_scan<CV_NT>(local, red, total));
-#pragma unroll
-    for (int j = 0; j < CV_WPT; ++j) {
-        run += c[j];
-        if (run > 0) img->w[CV_WPT * t + j] = ~0u;
-    }
-    __syncthreads();
-}
 
 // ---- decompress_to_bitset ---------------------------------------------------
 // One workgroup per 2048-word key region of the output: the region is written
@@ -215,8 +143,8 @@ __device__ __forceinline__ unsigned long long block_sum64(unsigned long long v, 
     return t;
 }
 
-__global__ __launch_bounds__(SC_NT) void cv_enum_scan(const uint64_t* __restrict__ counts, uint32_t n,
-                                                      uint64_t* __restrict__ starts)
+__global__ __launch_bounds__(SC_NT) void cv_scan_u64(const uint64_t* __restrict__ counts, uint32_t n,
+                                                     uint64_t* __restrict__ starts)
 {
     __shared__ unsigned long long part[SC_NT / 64];
     const uint32_t t = threadIdx.x;
@@ -515,7 +443,7 @@ int enumerate_impl(const cr_gpu_roaring* bm, int64_t* d_out, uint64_t cap, hipSt
     }
     {
         CR_TIMED("cv_enum_scan", s);
-        cv_enum_scan<<<(n + SC_NT - 1) / SC_NT, SC_NT, 0, s>>>(counts, n, starts);
+        CR_RET(scan_exclusive_u64(counts, n, starts, s));
     }
     {
         CR_TIMED("cv_enum_write", s);
@@ -537,6 +465,15 @@ uint64_t stored_cardinality(const cr_gpu_roaring* bm)
 }
 
 }  // namespace
+
+int scan_exclusive_u64(const uint64_t* in, uint32_t n, uint64_t* out, hipStream_t s)
+{
+    if (n == 0) return CR_OK;
+    cv_scan_u64<<<(n + SC_NT - 1) / SC_NT, SC_NT, 0, s>>>(in, n, out);
+    CR_LAUNCH_CHECK();
+    return CR_OK;
+}
+
 }  // namespace crimpl
 
 using namespace crimpl;

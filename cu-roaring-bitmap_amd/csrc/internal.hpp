@@ -238,6 +238,9 @@ struct HostPhase {
 };
 #define CR_HOST_PHASE(name) ::crimpl::HostPhase cr_host_phase__(name)
 
+// out = exclusive prefix sums of in[0, n) (n <= 65536; in and out distinct).
+int scan_exclusive_u64(const uint64_t* in, uint32_t n, uint64_t* out, hipStream_t s);
+
 uint64_t device_l2_bytes(int device);
 // Compute units of the current device (cached per device).
 uint32_t num_cus();

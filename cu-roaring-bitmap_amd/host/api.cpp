@@ -8,6 +8,10 @@
 
 #include "cu_roaring/cu_roaring.hpp"
 
+namespace crimpl {
+void set_error(const char* fmt, ...);  // the C ABI's thread-local error message (csrc/runtime.hip)
+}
+
 namespace cu_roaring {
 
 static cr_stream_t S(hipStream_t s) { return reinterpret_cast<cr_stream_t>(s); }
@@ -63,6 +67,27 @@ int64_t* enumerate_ids(const GpuRoaring& bitmap, hipStream_t stream)
 {
     int64_t* out = nullptr;
     throw_on_error(cr_enumerate_ids_alloc(to_abi(&bitmap), S(stream), &out, nullptr), "enumerate_ids");
+    return out;
+}
+
+size_t portable_size_in_bytes(const GpuRoaring& bm, hipStream_t stream)
+{
+    size_t n = 0;
+    throw_on_error(cr_portable_size_in_bytes(to_abi(&bm), S(stream), &n), "portable_size_in_bytes");
+    return n;
+}
+
+size_t portable_serialize(const GpuRoaring& bm, void* buf, size_t capacity, hipStream_t stream)
+{
+    size_t w = 0;
+    throw_on_error(cr_portable_serialize(to_abi(&bm), S(stream), buf, capacity, &w), "portable_serialize");
+    return w;
+}
+
+std::vector<uint8_t> portable_serialize(const GpuRoaring& bm, hipStream_t stream)
+{
+    std::vector<uint8_t> out(portable_size_in_bytes(bm, stream));
+    out.resize(portable_serialize(bm, out.data(), out.size(), stream));
     return out;
 }
 
@@ -187,23 +212,105 @@ std::vector<HostContainer> complement_containers(const HostContainer* c, uint32_
     return out;
 }
 
-GpuRoaring upload(const HostContainer* containers, uint32_t n, uint32_t universe_size, hipStream_t stream,
-                  uint32_t bitmap_threshold)
+// upload(bm, U): the complement is stored when the cardinality exceeds U/2
+// (src/upload.cpp:296-316).
+static int upload_with_universe(const HostContainer* containers, uint32_t n, uint32_t universe_size,
+                                cr_stream_t stream, uint32_t bitmap_threshold, cr_gpu_roaring* out)
 {
     const uint64_t card = host_cardinality(containers, n);
-    GpuRoaring r;
     if (card > static_cast<uint64_t>(universe_size) / 2u) {  // src/upload.cpp:300-313
         std::vector<std::vector<uint64_t>> storage;
         auto comp = complement_containers(containers, n, universe_size, storage);
-        throw_on_error(cr_upload_containers(comp.data(), static_cast<uint32_t>(comp.size()), universe_size, true, card,
-                                            S(stream), bitmap_threshold, to_abi(&r)),
-                       "upload");
-        return r;
+        return cr_upload_containers(comp.data(), static_cast<uint32_t>(comp.size()), universe_size, true, card, stream,
+                                    bitmap_threshold, out);
     }
-    throw_on_error(
-        cr_upload_containers(containers, n, universe_size, false, card, S(stream), bitmap_threshold, to_abi(&r)),
-        "upload");
+    return cr_upload_containers(containers, n, universe_size, false, card, stream, bitmap_threshold, out);
+}
+
+GpuRoaring upload(const HostContainer* containers, uint32_t n, uint32_t universe_size, hipStream_t stream,
+                  uint32_t bitmap_threshold)
+{
+    GpuRoaring r;
+    throw_on_error(upload_with_universe(containers, n, universe_size, S(stream), bitmap_threshold, to_abi(&r)),
+                   "upload");
     return r;
+}
+
+// ---- Roaring portable format: host-side parse of the headers ----------------
+// Layout (RoaringFormatSpec, little-endian): cookie u32 12346 + u32 size, or
+// u16 12347 + u16 size-1 + ceil(size/8) run-flag bytes; size x (u16 key,
+// u16 card-1); u32 offsets iff no run container or size >= 4 (not consulted:
+// payloads are read in sequence, as CRoaring does); then each payload (run:
+// u16 n_runs + (start, length-1) pairs; card <= 4096: u16 values; else 1024 u64).
+static uint32_t rd16(const uint8_t* p) { return static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8); }
+static uint32_t rd32(const uint8_t* p) { return rd16(p) | (rd16(p + 2) << 16); }
+
+static const char* parse_portable(const uint8_t* buf, size_t len, std::vector<HostContainer>& out,
+                                  std::vector<std::vector<uint64_t>>& storage)
+{
+    out.clear();
+    storage.clear();
+    if (len < 4) return "truncated cookie";
+    const uint32_t c0 = rd32(buf);
+    uint32_t n;
+    const uint8_t* run_flags = nullptr;
+    size_t pos;
+    if ((c0 & 0xFFFFu) == 12347u) {
+        n = (c0 >> 16) + 1u;
+        run_flags = buf + 4;
+        pos = 4u + (n + 7u) / 8u;
+    } else if (c0 == 12346u) {
+        if (len < 8) return "truncated size";
+        n = rd32(buf + 4);
+        if (n > 65536u) return "more than 65536 containers";
+        pos = 8;
+    } else {
+        return "unknown cookie";
+    }
+    if (pos + 4ull * n > len) return "truncated header";
+    const uint8_t* hdr = buf + pos;
+    pos += 4ull * n;
+    if (!run_flags || n >= 4u) pos += 4ull * n;
+    if (pos > len) return "truncated offset header";
+    out.resize(n);
+    // payloads that are not 2-byte aligned in `buf` are copied to `storage`
+    auto place = [&](size_t at, size_t bytes) -> const void* {
+        if ((reinterpret_cast<uintptr_t>(buf + at) & 1u) == 0) return buf + at;
+        storage.emplace_back((bytes + 7) / 8);
+        std::memcpy(storage.back().data(), buf + at, bytes);
+        return storage.back().data();
+    };
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t key = rd16(hdr + 4u * i), card = rd16(hdr + 4u * i + 2u) + 1u;
+        if (i > 0 && key <= out[i - 1].key) return "keys not strictly increasing";
+        HostContainer& h = out[i];
+        h.key = static_cast<uint16_t>(key);
+        if (run_flags && ((run_flags[i / 8u] >> (i % 8u)) & 1u)) {
+            if (pos + 2 > len) return "truncated run container";
+            const uint32_t nr = rd16(buf + pos);
+            pos += 2;
+            if (pos + 4ull * nr > len) return "truncated run container";
+            for (uint32_t k = 0; k < nr; ++k)
+                if (rd16(buf + pos + 4ull * k) + rd16(buf + pos + 4ull * k + 2) > 0xFFFFu) return "run past 0xFFFF";
+            h.typecode = CR_TC_RUN;
+            h.cardinality = static_cast<int32_t>(nr);
+            h.data = nr ? place(pos, 4ull * nr) : nullptr;
+            pos += 4ull * nr;
+        } else if (card <= 4096u) {
+            if (pos + 2ull * card > len) return "truncated array container";
+            h.typecode = CR_TC_ARRAY;
+            h.cardinality = static_cast<int32_t>(card);
+            h.data = place(pos, 2ull * card);
+            pos += 2ull * card;
+        } else {
+            if (pos + 8192 > len) return "truncated bitset container";
+            h.typecode = CR_TC_BITSET;
+            h.cardinality = static_cast<int32_t>(card);
+            h.data = buf + pos;  // copied with memcpy by the upload
+            pos += 8192;
+        }
+    }
+    return nullptr;
 }
 
 void gpu_roaring_free(GpuRoaring& bitmap) { throw_on_error(cr_free(to_abi(&bitmap)), "gpu_roaring_free"); }
@@ -242,6 +349,45 @@ void topk_filtered(const float* d_base, uint64_t n_base, const float* d_queries,
     throw_on_error(cr_topk_filtered(d_base, n_base, d_queries, n_q, dim, filter ? to_abi(filter) : nullptr, k,
                                     d_out_dist, d_out_ids, S(stream)),
                    "topk_filtered");
+}
+
+}  // namespace cu_roaring
+
+extern "C" int cr_portable_deserialize(const void* buf, size_t len, uint32_t universe_size, cr_stream_t stream,
+                                       uint32_t bitmap_threshold, cr_gpu_roaring* out)
+{
+    if (!out || (len && !buf)) {
+        crimpl::set_error("cr_portable_deserialize: invalid argument");
+        return CR_ERR_INVALID;
+    }
+    std::vector<cu_roaring::HostContainer> conts;
+    std::vector<std::vector<uint64_t>> storage;
+    const char* err = cu_roaring::parse_portable(static_cast<const uint8_t*>(buf), len, conts, storage);
+    if (err) {
+        crimpl::set_error("cr_portable_deserialize: %s", err);
+        return CR_ERR_INVALID;
+    }
+    const uint32_t n = static_cast<uint32_t>(conts.size());
+    if (universe_size == 0) return cr_upload_containers(conts.data(), n, 0, false, 0, stream, bitmap_threshold, out);
+    return cu_roaring::upload_with_universe(conts.data(), n, universe_size, stream, bitmap_threshold, out);
+}
+
+namespace cu_roaring {
+
+GpuRoaring portable_deserialize(const void* buf, size_t len, hipStream_t stream, uint32_t bitmap_threshold)
+{
+    GpuRoaring r;
+    throw_on_error(cr_portable_deserialize(buf, len, 0, S(stream), bitmap_threshold, to_abi(&r)), "portable_deserialize");
+    return r;
+}
+
+GpuRoaring portable_deserialize(const void* buf, size_t len, uint32_t universe_size, hipStream_t stream,
+                                uint32_t bitmap_threshold)
+{
+    GpuRoaring r;
+    throw_on_error(cr_portable_deserialize(buf, len, universe_size, S(stream), bitmap_threshold, to_abi(&r)),
+                   "portable_deserialize");
+    return r;
 }
 
 }  // namespace cu_roaring

@@ -18,6 +18,7 @@ PKG_DIR = os.path.dirname(_HERE)
 LIB_PATH = os.path.join(PKG_DIR, "lib", "libcuroaring_amd.so")
 
 CR_OK = 0
+CR_ERR_HIP, CR_ERR_INVALID, CR_ERR_ALLOC, CR_ERR_UNSUPPORTED = 1, 2, 3, 4
 ARRAY, BITMAP, RUN = 0, 1, 2
 AND, OR, ANDNOT, XOR = 0, 1, 2, 3
 PROMOTE_KEEP_DEFAULT = 4096
@@ -34,6 +35,7 @@ EXPORTS = [
     "cr_memcpy_d2h", "cr_stream_synchronize", "cr_timing_enable", "cr_timing_report", "cr_mempool_trim",
     "cr_decompress_to_bitset", "cr_decompress_to_bitset_alloc", "cr_enumerate_ids", "cr_enumerate_ids_alloc",
     "cr_promote_to_bitmap", "cr_promote_auto", "cr_deep_copy",
+    "cr_portable_size_in_bytes", "cr_portable_serialize", "cr_portable_deserialize",
 ]
 
 
@@ -145,6 +147,9 @@ def load(path: Optional[str] = None):
         "cr_promote_to_bitmap": [P(GpuRoaring), C.c_void_p, P(GpuRoaring)],
         "cr_promote_auto": [P(GpuRoaring), C.c_void_p, C.c_int, P(GpuRoaring)],
         "cr_deep_copy": [P(GpuRoaring), C.c_void_p, P(GpuRoaring)],
+        "cr_portable_size_in_bytes": [P(GpuRoaring), C.c_void_p, P(C.c_size_t)],
+        "cr_portable_serialize": [P(GpuRoaring), C.c_void_p, C.c_void_p, C.c_size_t, P(C.c_size_t)],
+        "cr_portable_deserialize": [C.c_void_p, C.c_size_t, C.c_uint32, C.c_void_p, C.c_uint32, P(GpuRoaring)],
     }
     for name, args in sigs.items():
         f = getattr(L, name)
@@ -338,6 +343,31 @@ def promote_auto(g: GpuRoaring, stream=None, device: int = -1) -> GpuRoaring:
 def deep_copy(g: GpuRoaring, stream=None) -> GpuRoaring:
     out = GpuRoaring()
     _check(load().cr_deep_copy(C.byref(g), _stream(stream), C.byref(out)), "deep_copy")
+    return out
+
+
+# ---- Roaring portable format ------------------------------------------------------
+def portable_size_in_bytes(g: GpuRoaring, stream=None) -> int:
+    n = C.c_size_t()
+    _check(load().cr_portable_size_in_bytes(C.byref(g), _stream(stream), C.byref(n)), "portable_size_in_bytes")
+    return n.value
+
+
+def portable_serialize(g: GpuRoaring, stream=None) -> bytes:
+    """The logical set of g in the Roaring portable format."""
+    n = portable_size_in_bytes(g, stream)
+    buf = C.create_string_buffer(max(n, 1))
+    w = C.c_size_t()
+    _check(load().cr_portable_serialize(C.byref(g), _stream(stream), buf, n, C.byref(w)), "portable_serialize")
+    return buf.raw[:w.value]
+
+
+def portable_deserialize(data: bytes, universe: int = 0, threshold: int = PROMOTE_AUTO, stream=None) -> GpuRoaring:
+    """upload() of a portable-format bitmap (universe 0: upload(bm); else upload(bm, U))."""
+    out = GpuRoaring()
+    buf = C.create_string_buffer(bytes(data), max(len(data), 1))
+    _check(load().cr_portable_deserialize(buf, len(data), universe, _stream(stream), threshold, C.byref(out)),
+           "portable_deserialize")
     return out
 
 

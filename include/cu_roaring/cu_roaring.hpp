@@ -8,5 +8,6 @@
 #include "cu_roaring/detail/set_ops.hpp"
 #include "cu_roaring/detail/decompress.hpp"
 #include "cu_roaring/detail/to_csr.hpp"
+#include "cu_roaring/detail/serialize.hpp"
 #include "cu_roaring/detail/topk.hpp"
 #include "cu_roaring/device/make_view.hpp"

@@ -216,6 +216,28 @@ int cr_promote_auto(const cr_gpu_roaring* bm, cr_stream_t stream, int device_id,
 /* gpu_roaring_deep_copy (promote.cuh:83; src/promote.cu:178-231). */
 int cr_deep_copy(const cr_gpu_roaring* bm, cr_stream_t stream, cr_gpu_roaring* out);
 
+/* ---- Roaring portable format ----------------------------------------------
+ * The serialization format of CRoaring's roaring_bitmap_portable_serialize /
+ * _deserialize (RoaringFormatSpec).  The reference has no serializer; its
+ * from-disk bench loads CRoaring files and upload()s them
+ * (bench/CMakeLists.txt:89-93).  These calls synchronise `stream`. */
+/* Bytes cr_portable_serialize writes for `bm`. */
+int cr_portable_size_in_bytes(const cr_gpu_roaring* bm, cr_stream_t stream, size_t* out_bytes);
+/* Serializes the logical set of `bm` (a negated bitmap is complemented within
+ * [0, U)) into host memory, each container encoded as CRoaring's run_optimize
+ * would leave it (array up to 4096 values, else bitset, run when smaller);
+ * empty containers are skipped.  *written receives the size; a buffer smaller
+ * than that gives CR_ERR_INVALID. */
+int cr_portable_serialize(const cr_gpu_roaring* bm, cr_stream_t stream, void* host_buf, size_t capacity,
+                          size_t* written);
+/* upload() of a portable-format bitmap held in host memory: the same result as
+ * deserializing it with CRoaring and calling upload(bm) (universe_size 0) or
+ * upload(bm, universe_size) (include/cu_roaring/detail/upload.cuh:19-32).
+ * A malformed buffer (truncated, bad cookie, keys out of order, a run past
+ * 0xFFFF) gives CR_ERR_INVALID. */
+int cr_portable_deserialize(const void* buf, size_t len, uint32_t universe_size, cr_stream_t stream,
+                            uint32_t bitmap_threshold, cr_gpu_roaring* out);
+
 /* ---- utilities (no reference counterpart) -------------------------------- */
 /* L2 size the AUTO rule uses for `device_id` (hipDeviceAttributeL2CacheSize). */
 int cr_device_l2_bytes(int device_id, uint64_t* out_bytes);

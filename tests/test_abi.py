@@ -17,7 +17,8 @@ def test_header_declares_expected_entry_points():
     syms = _declared_symbols()
     for s in ("cr_upload_from_ids", "cr_set_operation", "cr_multi_and", "cr_contains_batch", "cr_free_async",
               "cr_resolve_auto_threshold", "cr_upload_containers", "cr_topk_filtered", "cr_decompress_to_bitset",
-              "cr_enumerate_ids", "cr_promote_to_bitmap", "cr_promote_auto", "cr_deep_copy"):
+              "cr_enumerate_ids", "cr_promote_to_bitmap", "cr_promote_auto", "cr_deep_copy",
+              "cr_portable_serialize", "cr_portable_deserialize"):
         assert s in syms
     assert set(syms) == set(curoaring.EXPORTS)
 
