@@ -290,49 +290,6 @@ __global__ __launch_bounds__(CV_NT) void cv_promote(cr_gpu_roaring src, bool all
     }
 }
 
-// ---- deep copy: up to eight byte ranges in one launch -----------------------
-struct CopySeg {
-    const void* src;
-    void* dst;
-    uint64_t bytes;
-};
-struct CopyList {
-    CopySeg seg[8];
-    uint32_t n;
-};
-
-__global__ __launch_bounds__(256) void cv_copy(CopyList L)
-{
-    const uint32_t s = blockIdx.y;
-    if (s >= L.n) return;
-    const CopySeg g = L.seg[s];
-    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256u;
-    const uint64_t i0 = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
-    const uint8_t* sb = static_cast<const uint8_t*>(g.src);
-    uint8_t* db = static_cast<uint8_t*>(g.dst);
-    uint64_t done = 0;
-    if (((reinterpret_cast<uintptr_t>(g.src) | reinterpret_cast<uintptr_t>(g.dst)) & 15u) == 0) {
-        const uint64_t n4 = g.bytes / 16u;
-        const uint4* s4 = static_cast<const uint4*>(g.src);
-        uint4* d4 = static_cast<uint4*>(g.dst);
-        for (uint64_t i = i0; i < n4; i += stride) d4[i] = s4[i];
-        done = n4 * 16u;
-    }
-    for (uint64_t i = done + i0; i < g.bytes; i += stride) db[i] = sb[i];
-}
-
-int copy_segments(const CopyList& L, hipStream_t s)
-{
-    if (L.n == 0) return CR_OK;
-    uint64_t most = 0;
-    for (uint32_t i = 0; i < L.n; ++i) most = std::max(most, L.seg[i].bytes);
-    const uint64_t want = (most / 16u + 255u) / 256u;
-    const uint32_t gx = static_cast<uint32_t>(std::max<uint64_t>(1, std::min<uint64_t>(want, 4096u)));
-    cv_copy<<<dim3(gx, L.n), 256, 0, s>>>(L);
-    CR_LAUNCH_CHECK();
-    return CR_OK;
-}
-
 int deep_copy_impl(const cr_gpu_roaring* bm, hipStream_t s, cr_gpu_roaring* out)
 {
     cr_gpu_roaring r{};
@@ -465,6 +422,39 @@ uint64_t stored_cardinality(const cr_gpu_roaring* bm)
 }
 
 }  // namespace
+
+// ---- deep copy: up to eight byte ranges in one launch -----------------------
+__global__ __launch_bounds__(256) void cv_copy(CopyList L)
+{
+    const uint32_t s = blockIdx.y;
+    if (s >= L.n) return;
+    const CopySeg g = L.seg[s];
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256u;
+    const uint64_t i0 = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
+    const uint8_t* sb = static_cast<const uint8_t*>(g.src);
+    uint8_t* db = static_cast<uint8_t*>(g.dst);
+    uint64_t done = 0;
+    if (((reinterpret_cast<uintptr_t>(g.src) | reinterpret_cast<uintptr_t>(g.dst)) & 15u) == 0) {
+        const uint64_t n4 = g.bytes / 16u;
+        const uint4* s4 = static_cast<const uint4*>(g.src);
+        uint4* d4 = static_cast<uint4*>(g.dst);
+        for (uint64_t i = i0; i < n4; i += stride) d4[i] = s4[i];
+        done = n4 * 16u;
+    }
+    for (uint64_t i = done + i0; i < g.bytes; i += stride) db[i] = sb[i];
+}
+
+int copy_segments(const CopyList& L, hipStream_t s)
+{
+    if (L.n == 0) return CR_OK;
+    uint64_t most = 0;
+    for (uint32_t i = 0; i < L.n; ++i) most = std::max(most, L.seg[i].bytes);
+    const uint64_t want = (most / 16u + 255u) / 256u;
+    const uint32_t gx = static_cast<uint32_t>(std::max<uint64_t>(1, std::min<uint64_t>(want, 4096u)));
+    cv_copy<<<dim3(gx, L.n), 256, 0, s>>>(L);
+    CR_LAUNCH_CHECK();
+    return CR_OK;
+}
 
 int scan_exclusive_u64(const uint64_t* in, uint32_t n, uint64_t* out, hipStream_t s)
 {

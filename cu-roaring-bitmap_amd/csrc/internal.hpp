@@ -2,6 +2,7 @@
 // stream-ordered allocation of packed result blocks and scratch, and wave64
 // primitives for gfx950.
 #pragma once
+#include <mutex>
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -237,6 +238,41 @@ struct HostPhase {
     ~HostPhase();
 };
 #define CR_HOST_PHASE(name) ::crimpl::HostPhase cr_host_phase__(name)
+
+// Grow-only pinned staging buffer, serialised by its mutex; a call that uses
+// it synchronises its stream before releasing the lock.
+struct PinnedStage {
+    std::mutex mu;
+    void* ptr = nullptr;
+    size_t cap = 0;
+    int reserve(size_t bytes)
+    {
+        if (bytes <= cap) return CR_OK;
+        if (ptr) (void)hipHostFree(ptr);
+        ptr = nullptr;
+        cap = 0;
+        const size_t want = bytes > (size_t(1) << 20) ? bytes : (size_t(1) << 20);
+        if (hipHostMalloc(&ptr, want, hipHostMallocDefault) != hipSuccess) {
+            ptr = nullptr;
+            set_error("hipHostMalloc(%zu) failed", want);
+            return CR_ERR_ALLOC;
+        }
+        cap = want;
+        return CR_OK;
+    }
+};
+
+// Up to eight device byte ranges copied by one kernel launch.
+struct CopySeg {
+    const void* src;
+    void* dst;
+    uint64_t bytes;
+};
+struct CopyList {
+    CopySeg seg[8];
+    uint32_t n;
+};
+int copy_segments(const CopyList& L, hipStream_t s);
 
 // out = exclusive prefix sums of in[0, n) (n <= 65536; in and out distinct).
 int scan_exclusive_u64(const uint64_t* in, uint32_t n, uint64_t* out, hipStream_t s);

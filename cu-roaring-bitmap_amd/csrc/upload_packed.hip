@@ -19,28 +19,6 @@
 
 namespace crimpl {
 
-// Grow-only pinned staging buffer, serialised by a mutex; the call syncs its
-// stream before releasing it.
-struct PinnedStage {
-    std::mutex mu;
-    void* ptr = nullptr;
-    size_t cap = 0;
-    int reserve(size_t bytes)
-    {
-        if (bytes <= cap) return CR_OK;
-        if (ptr) (void)hipHostFree(ptr);
-        ptr = nullptr;
-        cap = 0;
-        size_t want = std::max<size_t>(bytes, 1 << 20);
-        if (hipHostMalloc(&ptr, want, hipHostMallocDefault) != hipSuccess) {
-            ptr = nullptr;
-            set_error("hipHostMalloc(%zu) failed", want);
-            return CR_ERR_ALLOC;
-        }
-        cap = want;
-        return CR_OK;
-    }
-};
 static PinnedStage g_stage;
 
 struct ExpandDesc {

@@ -18,7 +18,7 @@ PKG_DIR = os.path.dirname(_HERE)
 LIB_PATH = os.path.join(PKG_DIR, "lib", "libcuroaring_amd.so")
 
 CR_OK = 0
-CR_ERR_HIP, CR_ERR_INVALID, CR_ERR_ALLOC, CR_ERR_UNSUPPORTED = 1, 2, 3, 4
+CR_ERR_HIP, CR_ERR_INVALID, CR_ERR_ALLOC, CR_ERR_UNSUPPORTED, CR_ERR_RANGE = 1, 2, 3, 4, 5
 ARRAY, BITMAP, RUN = 0, 1, 2
 AND, OR, ANDNOT, XOR = 0, 1, 2, 3
 PROMOTE_KEEP_DEFAULT = 4096
@@ -36,6 +36,8 @@ EXPORTS = [
     "cr_decompress_to_bitset", "cr_decompress_to_bitset_alloc", "cr_enumerate_ids", "cr_enumerate_ids_alloc",
     "cr_promote_to_bitmap", "cr_promote_auto", "cr_deep_copy",
     "cr_portable_size_in_bytes", "cr_portable_serialize", "cr_portable_deserialize",
+    "cr_upload_batch", "cr_free_batch", "cr_promote_batch", "cr_batch_make_view", "cr_batch_multi_and",
+    "cr_batch_decompress", "cr_batch_contains", "cr_batch_view_contains",
 ]
 
 
@@ -78,6 +80,31 @@ class GpuRoaringView(C.Structure):
         ("max_key", C.c_uint32),
         ("all_bitmap", C.c_bool),
         ("negated", C.c_bool),
+    ]
+
+
+class RoaringBatch(C.Structure):
+    """cr_roaring_batch == cu_roaring::v2::GpuRoaringBatch (v2/include/cu_roaring_v2/types.cuh:37-86)."""
+    _fields_ = [
+        ("n_bitmaps", C.c_uint32), ("total_containers", C.c_uint32), ("n_bitmap_containers_total", C.c_uint32),
+        ("array_pool_bytes", C.c_uint32), ("run_pool_bytes", C.c_uint32),
+        ("container_starts", C.c_void_p), ("key_index_starts", C.c_void_p),
+        ("keys", C.c_void_p), ("types", C.c_void_p), ("offsets", C.c_void_p), ("cardinalities", C.c_void_p),
+        ("key_indices", C.c_void_p), ("bitmap_data", C.c_void_p), ("array_data", C.c_void_p),
+        ("run_data", C.c_void_p),
+        ("host_total_cardinalities", C.POINTER(C.c_uint64)), ("host_universe_sizes", C.POINTER(C.c_uint32)),
+        ("host_container_starts", C.POINTER(C.c_uint32)), ("host_key_index_starts", C.POINTER(C.c_uint32)),
+        ("host_n_bitmap_containers", C.POINTER(C.c_uint32)),
+        ("_alloc_base", C.c_void_p), ("_host_meta_base", C.c_void_p),
+    ]
+
+
+class BatchView(C.Structure):
+    """cr_batch_view == cu_roaring::v2::GpuRoaringView (v2/include/cu_roaring_v2/types.cuh:95-107)."""
+    _fields_ = [
+        ("n_containers", C.c_uint32), ("max_key", C.c_uint32),
+        ("keys", C.c_void_p), ("types", C.c_void_p), ("offsets", C.c_void_p), ("cardinalities", C.c_void_p),
+        ("key_index", C.c_void_p), ("bitmap_data", C.c_void_p), ("array_data", C.c_void_p), ("run_data", C.c_void_p),
     ]
 
 
@@ -150,6 +177,14 @@ def load(path: Optional[str] = None):
         "cr_portable_size_in_bytes": [P(GpuRoaring), C.c_void_p, P(C.c_size_t)],
         "cr_portable_serialize": [P(GpuRoaring), C.c_void_p, C.c_void_p, C.c_size_t, P(C.c_size_t)],
         "cr_portable_deserialize": [C.c_void_p, C.c_size_t, C.c_uint32, C.c_void_p, C.c_uint32, P(GpuRoaring)],
+        "cr_upload_batch": [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, P(RoaringBatch)],
+        "cr_free_batch": [P(RoaringBatch)],
+        "cr_promote_batch": [P(RoaringBatch), C.c_void_p, P(RoaringBatch)],
+        "cr_batch_make_view": [P(RoaringBatch), C.c_uint32, P(BatchView)],
+        "cr_batch_multi_and": [P(RoaringBatch), C.c_void_p, C.c_uint32, C.c_void_p, P(RoaringBatch)],
+        "cr_batch_decompress": [P(RoaringBatch), C.c_void_p, C.c_uint64, C.c_void_p],
+        "cr_batch_contains": [P(RoaringBatch), C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p],
+        "cr_batch_view_contains": [P(BatchView), C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p],
     }
     for name, args in sigs.items():
         f = getattr(L, name)
@@ -369,6 +404,81 @@ def portable_deserialize(data: bytes, universe: int = 0, threshold: int = PROMOT
     _check(load().cr_portable_deserialize(buf, len(data), universe, _stream(stream), threshold, C.byref(out)),
            "portable_deserialize")
     return out
+
+
+# ---- the batch API (the reference's v2) -------------------------------------------
+def upload_batch(bitmaps, stream=None) -> RoaringBatch:
+    """bitmaps: a list of container lists, each [(key, typecode, card, ndarray)]."""
+    arrays = [_container_array(c) for c in bitmaps]
+    ptrs = (C.c_void_p * max(1, len(bitmaps)))(*[C.addressof(a[0]) if len(a[0]) else None for a in arrays])
+    counts = (C.c_uint32 * max(1, len(bitmaps)))(*[len(c) for c in bitmaps])
+    out = RoaringBatch()
+    _check(load().cr_upload_batch(ptrs, counts, len(bitmaps), _stream(stream), C.byref(out)), "upload_batch")
+    return out
+
+
+def free_batch(b: RoaringBatch):
+    _check(load().cr_free_batch(C.byref(b)), "free_batch")
+
+
+def promote_batch(b: RoaringBatch, stream=None) -> RoaringBatch:
+    out = RoaringBatch()
+    _check(load().cr_promote_batch(C.byref(b), _stream(stream), C.byref(out)), "promote_batch")
+    return out
+
+
+def batch_make_view(b: RoaringBatch, idx: int) -> BatchView:
+    v = BatchView()
+    _check(load().cr_batch_make_view(C.byref(b), idx, C.byref(v)), "make_view")
+    return v
+
+
+def batch_multi_and(b: RoaringBatch, indices, stream=None) -> RoaringBatch:
+    idx = np.ascontiguousarray(indices, dtype=np.uint32)
+    out = RoaringBatch()
+    _check(load().cr_batch_multi_and(C.byref(b), idx.ctypes.data if idx.size else None, idx.size, _stream(stream),
+                                     C.byref(out)), "multi_and")
+    return out
+
+
+def batch_decompress(b: RoaringBatch, d_bitsets, words_each: int, stream=None):
+    _check(load().cr_batch_decompress(C.byref(b), _dptr(d_bitsets), words_each, _stream(stream)), "decompress_batch")
+
+
+def batch_contains(b: RoaringBatch, d_ids, d_out, bitmap: int = 0, d_bitmap_idx=None, stream=None):
+    """d_out[i] = bitmap (d_bitmap_idx[i] or `bitmap`) holds d_ids[i]; d_out is a uint8 CUDA tensor."""
+    _check(load().cr_batch_contains(C.byref(b), _dptr(d_bitmap_idx) if d_bitmap_idx is not None else None, bitmap,
+                                    _dptr(d_ids), d_ids.numel(), _dptr(d_out), _stream(stream)), "batch_contains")
+
+
+def batch_view_contains(v: BatchView, d_ids, d_out, stream=None):
+    _check(load().cr_batch_view_contains(C.byref(v), _dptr(d_ids), d_ids.numel(), _dptr(d_out), _stream(stream)),
+           "batch_view_contains")
+
+
+def download_batch(b: RoaringBatch) -> SimpleNamespace:
+    """Host copy of a batch (same fields as the oracle's HostBatch); the
+    metadata arrays hold the batch's live slices only."""
+    n, T = b.n_bitmaps, b.total_containers
+    h = lambda p, k: np.ctypeslib.as_array(p, shape=(k,)).copy() if (k and p) else np.zeros(0)
+    hcs = h(b.host_container_starts, n + 1).astype(np.uint32) if n else np.zeros(0, np.uint32)
+    hks = h(b.host_key_index_starts, n + 1).astype(np.uint32) if n else np.zeros(0, np.uint32)
+    kidx = int(hks[-1]) if n else 0
+    return SimpleNamespace(
+        n_bitmaps=n, total_containers=T, n_bitmap_containers_total=b.n_bitmap_containers_total,
+        array_pool_bytes=b.array_pool_bytes, run_pool_bytes=b.run_pool_bytes,
+        container_starts=_d2h(b.container_starts, n + 1 if n else 0, np.uint32),
+        key_index_starts=_d2h(b.key_index_starts, n + 1 if n else 0, np.uint32),
+        keys=_d2h(b.keys, T, np.uint16), types=_d2h(b.types, T, np.uint8), offsets=_d2h(b.offsets, T, np.uint32),
+        cards=_d2h(b.cardinalities, T, np.uint16), key_indices=_d2h(b.key_indices, kidx, np.uint16),
+        bitmap_data=_d2h(b.bitmap_data, b.n_bitmap_containers_total * 1024, np.uint64),
+        array_data=_d2h(b.array_data, b.array_pool_bytes // 2, np.uint16),
+        run_data=_d2h(b.run_data, b.run_pool_bytes // 2, np.uint16),
+        host_total_cardinalities=h(b.host_total_cardinalities, n).astype(np.uint64) if n else np.zeros(0, np.uint64),
+        host_universe_sizes=h(b.host_universe_sizes, n).astype(np.uint32) if n else np.zeros(0, np.uint32),
+        host_container_starts=hcs, host_key_index_starts=hks,
+        host_n_bitmap_containers=h(b.host_n_bitmap_containers, n).astype(np.uint32) if n else np.zeros(0, np.uint32),
+    )
 
 
 def device_free(ptr):

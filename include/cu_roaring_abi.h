@@ -28,6 +28,7 @@ extern "C" {
 #define CR_ERR_INVALID 2      /* invalid argument (e.g. an id whose key exceeds the universe) */
 #define CR_ERR_ALLOC 3        /* device or pinned host allocation failed */
 #define CR_ERR_UNSUPPORTED 4  /* request outside what this build implements */
+#define CR_ERR_RANGE 5        /* an index out of range (the reference throws std::out_of_range) */
 
 /* ContainerType (include/cu_roaring/types.cuh:7-11). */
 #define CR_ARRAY 0
@@ -119,6 +120,55 @@ typedef struct cr_host_container {
     int32_t cardinality;
     const void* data;
 } cr_host_container;
+
+/*
+ * Byte-identical to cu_roaring::v2::GpuRoaringBatch
+ * (v2/include/cu_roaring_v2/types.cuh:37-86): N bitmaps in one device block,
+ * CSR-style.  container_starts / key_index_starts (n_bitmaps + 1 entries)
+ * slice the concatenated per-container metadata and key indices; a key index
+ * entry is the LOCAL container index within its bitmap (0xFFFF = absent);
+ * offsets are byte offsets into the per-type pools, which the batch shares.
+ * The host_* arrays mirror per-bitmap scalars in host memory.  160 bytes on LP64.
+ */
+typedef struct cr_roaring_batch {
+    uint32_t n_bitmaps;
+    uint32_t total_containers;
+    uint32_t n_bitmap_containers_total;
+    uint32_t array_pool_bytes;
+    uint32_t run_pool_bytes;
+    uint32_t* container_starts;
+    uint32_t* key_index_starts;
+    uint16_t* keys;
+    uint8_t* types;
+    uint32_t* offsets;
+    uint16_t* cardinalities;
+    uint16_t* key_indices;
+    uint64_t* bitmap_data;
+    uint16_t* array_data;
+    uint16_t* run_data;
+    const uint64_t* host_total_cardinalities;
+    const uint32_t* host_universe_sizes;
+    const uint32_t* host_container_starts;
+    const uint32_t* host_key_index_starts;
+    const uint32_t* host_n_bitmap_containers;
+    void* _alloc_base;
+    void* _host_meta_base;
+} cr_roaring_batch;
+
+/* Byte-identical to cu_roaring::v2::GpuRoaringView (v2/include/cu_roaring_v2/types.cuh:95-107):
+ * one bitmap of a batch, its metadata pointers already offset to its slice. */
+typedef struct cr_batch_view {
+    uint32_t n_containers;
+    uint32_t max_key;
+    uint16_t* keys;
+    uint8_t* types;
+    uint32_t* offsets;
+    uint16_t* cardinalities;
+    uint16_t* key_index;
+    uint64_t* bitmap_data;
+    uint16_t* array_data;
+    uint16_t* run_data;
+} cr_batch_view;
 
 typedef void* cr_stream_t;
 
@@ -237,6 +287,45 @@ int cr_portable_serialize(const cr_gpu_roaring* bm, cr_stream_t stream, void* ho
  * 0xFFFF) gives CR_ERR_INVALID. */
 int cr_portable_deserialize(const void* buf, size_t len, uint32_t universe_size, cr_stream_t stream,
                             uint32_t bitmap_threshold, cr_gpu_roaring* out);
+
+/* ---- the v2 batch API (v2/include/cu_roaring_v2/api.hpp) ------------------
+ * Container types are kept as given; only cr_promote_batch changes them. */
+/* upload_batch (api.hpp:22-24; v2/src/upload.cpp:319-360): bitmap b is the
+ * container list bitmaps[b][0, n_containers[b]) (keys strictly increasing, as
+ * in a roaring_bitmap_t).  One device block, one host-to-device copy; synchronises
+ * `stream`.  n_bitmaps 0 gives the empty batch. */
+int cr_upload_batch(const cr_host_container* const* bitmaps, const uint32_t* n_containers, uint32_t n_bitmaps,
+                    cr_stream_t stream, cr_roaring_batch* out);
+/* free_batch (api.hpp:28; v2/src/upload.cpp:362-372): synchronises the device,
+ * releases both blocks and zeroes *batch. */
+int cr_free_batch(cr_roaring_batch* batch);
+/* promote_batch (api.hpp:35-36; v2/src/promote.cu:214-304): a new all-bitmap
+ * batch; cardinalities recomputed by popcount (65536 stored as 0).
+ * Stream-ordered, no synchronisation. */
+int cr_promote_batch(const cr_roaring_batch* batch, cr_stream_t stream, cr_roaring_batch* out);
+/* make_view (api.hpp:42; v2/src/upload.cpp:374-415).  CR_ERR_RANGE when b >= n_bitmaps. */
+int cr_batch_make_view(const cr_roaring_batch* batch, uint32_t b, cr_batch_view* out);
+/* multi_and (api.hpp:52-55; v2/src/multi_and.cu:276-470): AND of the bitmaps
+ * host_indices[0, n_inputs) (every one all-bitmap, else CR_ERR_INVALID; an
+ * index out of range gives CR_ERR_RANGE) into a new 1-bitmap batch.
+ * Synchronises `stream` once (the result's counts). */
+int cr_batch_multi_and(const cr_roaring_batch* batch, const uint32_t* host_indices, uint32_t n_inputs,
+                       cr_stream_t stream, cr_roaring_batch* out);
+/* decompress_batch (api.hpp:62-65; v2/src/decompress.cu:151-178): bitmap b's
+ * containers into d_bitsets[b * words_each, (b + 1) * words_each): a bitmap
+ * container's window is stored, an array / run window OR-ed into the buffer
+ * (callers zero it first).  CR_ERR_INVALID when words_each < ceil(max universe / 64). */
+int cr_batch_decompress(const cr_roaring_batch* batch, uint64_t* d_bitsets, uint64_t words_each,
+                        cr_stream_t stream);
+/* Batched contains(batch, b, id) (v2/include/cu_roaring_v2/query.cuh:97-112):
+ * d_out[i] = 1 iff bitmap (d_bitmap_idx ? d_bitmap_idx[i] : b) holds d_ids[i].
+ * The reference's v2 tests write this launcher around the device function
+ * (v2/test/test_basic.cu:47-55). */
+int cr_batch_contains(const cr_roaring_batch* batch, const uint32_t* d_bitmap_idx, uint32_t b,
+                      const uint32_t* d_ids, uint64_t n, uint8_t* d_out, cr_stream_t stream);
+/* Batched contains(view, id) (query.cuh:75-92; v2/test/test_basic.cu:38-45). */
+int cr_batch_view_contains(const cr_batch_view* view, const uint32_t* d_ids, uint64_t n, uint8_t* d_out,
+                           cr_stream_t stream);
 
 /* ---- utilities (no reference counterpart) -------------------------------- */
 /* L2 size the AUTO rule uses for `device_id` (hipDeviceAttributeL2CacheSize). */

@@ -18,7 +18,7 @@ def test_header_declares_expected_entry_points():
     for s in ("cr_upload_from_ids", "cr_set_operation", "cr_multi_and", "cr_contains_batch", "cr_free_async",
               "cr_resolve_auto_threshold", "cr_upload_containers", "cr_topk_filtered", "cr_decompress_to_bitset",
               "cr_enumerate_ids", "cr_promote_to_bitmap", "cr_promote_auto", "cr_deep_copy",
-              "cr_portable_serialize", "cr_portable_deserialize"):
+              "cr_portable_serialize", "cr_portable_deserialize", "cr_upload_batch", "cr_batch_multi_and"):
         assert s in syms
     assert set(syms) == set(curoaring.EXPORTS)
 
@@ -38,6 +38,12 @@ def test_struct_layout_matches_reference():
     # GpuRoaringView (roaring_view.cuh:14-37): 80 bytes, flags at 76/77.
     assert ctypes.sizeof(curoaring.GpuRoaringView) == 80
     assert curoaring.GpuRoaringView.all_bitmap.offset == 76
+    # v2 GpuRoaringBatch (v2/include/cu_roaring_v2/types.cuh:37-86): 5 u32, 10 device and
+    # 5 host pointers, 2 owners -> 160 bytes; GpuRoaringView (:95-107) 72 bytes.
+    assert ctypes.sizeof(curoaring.RoaringBatch) == 160
+    assert curoaring.RoaringBatch.container_starts.offset == 24
+    assert curoaring.RoaringBatch.host_total_cardinalities.offset == 104
+    assert ctypes.sizeof(curoaring.BatchView) == 72
 
 
 def test_host_only_entry_points_without_gpu():
