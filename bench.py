@@ -19,7 +19,9 @@ Also reported (extra fields, measured in the same run):
                 queries (Gq/s) on a 10% 2^30 bitmap, cold (512 MiB flush before
                 each timed call); the fused filtered top-k (10M x 128 fp32 base,
                 1024 queries, k = 10 and 100, multi_and filters at 0.1-50%
-                selectivity and unfiltered) with its fp32 MFMA utilisation.
+                selectivity and unfiltered) with its fp32 MFMA utilisation; the
+                conversions (decompress, enumerate_ids, promote, deep copy) and the
+                portable format on 2^30 bitmaps; the batch API on 16 x 2^28 bitmaps.
 
 --gpus N with N > 1 exits: this build measures one GPU only.
 """
@@ -207,9 +209,166 @@ def secondary(torch, cr, flush):
     torch.cuda.empty_cache()
     sparse = sparse_arrays(cr, 0.005, 60)
     out["conversions_2^30"] = conversions(torch, cr, flush, {"dense_10pct_bitmap": bm, "sparse_0.5pct_array": sparse})
+    out["portable_format_2^30"] = portable(torch, cr, flush, {"dense_10pct_bitmap": bm, "sparse_0.5pct_array": sparse})
     cr.free(sparse)
     cr.free(bm)
+    torch.cuda.empty_cache()
+    out["batch_16x2^28"] = batch_api(torch, cr, flush)
     return out
+
+
+def _kernel_line(rep, name, nbytes, t_api):
+    kn, kms = rep.get(name, (1, float("nan")))
+    k = kms / kn
+    return {"algorithmic_bytes": nbytes, "api_ms": round(t_api, 4), f"{name}_ms": round(k, 4),
+            f"{name}_GBps": round(nbytes / k / 1e6, 1), "frac_of_hbm_peak": round(nbytes / k / 1e6 / HBM_PEAK_GBS, 4),
+            "kernels_ms": {kk: round(v[1] / v[0], 4) for kk, v in rep.items()}}
+
+
+def portable(torch, cr, flush, bitmaps):
+    """Roaring portable-format serialize (device planning + payload kernels, then
+    the copy of the bytes to host memory) and deserialize (host header parse,
+    then the packed upload).  Kernel bytes: ps_plan reads the payloads and
+    metadata; ps_write reads them again and writes the serialized payloads."""
+    res = {}
+    for name, g in bitmaps.items():
+        import ctypes as C
+        import numpy as np
+        payload = 8192 * g.n_bitmap_containers + g.array_pool_bytes + g.run_pool_bytes + 9 * g.n_containers
+        data = cr.portable_serialize(g)
+        # the C calls are timed on pre-touched numpy buffers (no Python marshalling)
+        hbuf = np.ones(len(data), dtype=np.uint8)
+        w = C.c_size_t()
+        lib = cr.load()
+
+        def ser():
+            assert lib.cr_portable_serialize(C.byref(g), None, hbuf.ctypes.data, hbuf.size, C.byref(w)) == 0
+        cr.timing_enable(True)
+        t_ser = cold_time(torch, ser, 3, flush)
+        rep = cr.timing_report()
+        cr.timing_enable(False)
+        assert hbuf.tobytes() == data
+        kw = rep.get("ps_write", (1, float("nan")))
+        kp = rep.get("ps_plan", (1, float("nan")))
+        write_bytes = payload + len(data)
+        r = {"serialized_bytes": len(data), "serialize_api_ms": round(t_ser, 3),
+             "serialize_api_GBps_of_output": round(len(data) / t_ser / 1e6, 2),
+             "ps_plan_ms": round(kp[1] / kp[0], 4), "ps_plan_GBps": round(payload / (kp[1] / kp[0]) / 1e6, 1),
+             "ps_write_ms": round(kw[1] / kw[0], 4), "ps_write_GBps": round(write_bytes / (kw[1] / kw[0]) / 1e6, 1),
+             "kernels_ms": {k: round(v[1] / v[0], 4) for k, v in rep.items()}}
+        h = cr.GpuRoaring()
+        ts = []
+        for _ in range(4):
+            t0 = time.perf_counter()
+            assert lib.cr_portable_deserialize(hbuf.ctypes.data, hbuf.size, U, None, cr.PROMOTE_KEEP_DEFAULT,
+                                               C.byref(h)) == 0
+            ts.append((time.perf_counter() - t0) * 1e3)
+            cr.free(h)
+        ts = ts[1:]
+        r["deserialize_api_ms"] = round(median(ts), 3)
+        r["deserialize_api_GBps_of_input"] = round(len(data) / median(ts) / 1e6, 2)
+        r["note"] = "API times include the PCIe copy of the serialized bytes (device to host, or host to device)"
+        res[name] = r
+        log("portable", name, r["serialize_api_ms"], "ms serialize", r["deserialize_api_ms"], "ms deserialize")
+    return res
+
+
+def batch_api(torch, cr, flush):
+    """The batch API on 16 bitmaps over 2^28 (4096 keys each): eight 50%-dense
+    (bitset containers) and eight 1% (array containers).  upload_batch from host
+    containers; promote_batch; multi_and over the eight dense bitmaps and over
+    four dense + four sparse (promoted); decompress_batch of all 16; 100M
+    contains with a random bitmap per query, and through one view."""
+    import numpy as np
+    Ub = 1 << 28
+    nk = Ub >> 16
+    rng = np.random.default_rng(70)
+    lists = []
+    for b in range(16):
+        if b < 8:
+            words = rng.integers(0, np.iinfo(np.uint64).max, size=(nk, 1024), dtype=np.uint64, endpoint=True)
+            cards = np.bitwise_count(words).sum(axis=1, dtype=np.int64)
+            lists.append([(k, cr.TC_BITSET, int(cards[k]), words[k]) for k in range(nk)])
+        else:
+            ids = np.unique(rng.integers(0, Ub, int(0.01 * Ub), dtype=np.uint64))
+            bounds = np.searchsorted(ids, np.arange(nk + 1, dtype=np.uint64) << np.uint64(16))
+            lists.append([(k, cr.TC_ARRAY, int(bounds[k + 1] - bounds[k]),
+                           (ids[bounds[k]:bounds[k + 1]] & np.uint64(0xFFFF)).astype(np.uint16))
+                          for k in range(nk) if bounds[k + 1] > bounds[k]])
+    # the container descriptors are marshalled once, outside the timed call
+    import ctypes as C
+    arrays = [cr._container_array(c) for c in lists]
+    ptrs = (C.c_void_p * 16)(*[C.addressof(a[0]) for a in arrays])
+    counts = (C.c_uint32 * 16)(*[len(c) for c in lists])
+    B = cr.RoaringBatch()
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        rc = cr.load().cr_upload_batch(ptrs, counts, 16, None, C.byref(B))
+        ts.append((time.perf_counter() - t0) * 1e3)
+        assert rc == 0, cr.load().cr_last_error()
+        if len(ts) < 3:
+            cr.free_batch(B)
+    t_up = median(ts)
+    del arrays
+    up_bytes = 8 * 8192 * nk + B.array_pool_bytes + 9 * B.total_containers
+    del lists
+    res = {"bitmaps": 16, "universe": Ub, "containers": B.total_containers,
+           "upload_batch": {"api_ms": round(t_up, 2), "bytes": up_bytes, "GBps": round(up_bytes / t_up / 1e6, 2),
+                            "note": "host containers packed into pinned memory, one host-to-device copy"}}
+    T = B.total_containers
+    kept = []
+    cr.timing_enable(True)
+    t = cold_time(torch, lambda: kept.append(cr.promote_batch(B)), 5, flush)
+    rep = cr.timing_report()
+    cr.timing_enable(False)
+    for x in kept[1:]:
+        cr.free_batch(x)
+    P = kept[0]
+    res["promote_batch"] = _kernel_line(rep, "bt_promote", 8 * 8192 * nk + B.array_pool_bytes + 9 * T + 8192 * T + 9 * T,
+                                        t)
+    for name, idx in (("multi_and_8_dense", list(range(8))), ("multi_and_4_dense_4_sparse", [0, 1, 2, 3, 8, 9, 10, 11])):
+        r0 = cr.batch_multi_and(P, idx)
+        n_common = r0.total_containers
+        cr.free_batch(r0)
+        outs = []
+        cr.timing_enable(True)
+        t = cold_time(torch, lambda: outs.append(cr.batch_multi_and(P, idx)), 5, flush)
+        rep = cr.timing_report()
+        cr.timing_enable(False)
+        for x in outs:
+            cr.free_batch(x)
+        nbytes = (len(idx) + 1) * 8192 * n_common + 9 * (len(idx) + 1) * n_common
+        res[name] = dict(_kernel_line(rep, "bt_and", nbytes, t), n_common=n_common)
+    words_each = Ub // 64
+    d = torch.zeros(16 * words_each, dtype=torch.int64, device="cuda")
+    cr.timing_enable(True)
+    t = cold_time(torch, lambda: cr.batch_decompress(B, d, words_each), 5, flush)
+    rep = cr.timing_report()
+    cr.timing_enable(False)
+    res["decompress_batch"] = _kernel_line(rep, "bt_decompress", 8 * 8192 * nk + B.array_pool_bytes + 9 * T +
+                                           16 * words_each * 8, t)
+    del d
+    nq = 100_000_000
+    g = torch.Generator(device="cuda")
+    g.manual_seed(71)
+    q = torch.randint(0, Ub, (nq,), device="cuda", generator=g, dtype=torch.int64).to(torch.int32)
+    qb = torch.randint(0, 16, (nq,), device="cuda", generator=g, dtype=torch.int64).to(torch.int32)
+    out = torch.empty(nq, dtype=torch.uint8, device="cuda")
+    cr.batch_contains(P, q, out, d_bitmap_idx=qb)
+    torch.cuda.synchronize()
+    t = cold_time(torch, lambda: cr.batch_contains(P, q, out, d_bitmap_idx=qb), 5, flush)
+    res["contains_per_query_bitmap_promoted_Gqps"] = round(nq / t / 1e6, 2)
+    t = cold_time(torch, lambda: cr.batch_contains(B, q, out, d_bitmap_idx=qb), 5, flush)
+    res["contains_per_query_bitmap_mixed_Gqps"] = round(nq / t / 1e6, 2)
+    v = cr.batch_make_view(P, 0)
+    t = cold_time(torch, lambda: cr.batch_view_contains(v, q, out), 5, flush)
+    res["view_contains_promoted_Gqps"] = round(nq / t / 1e6, 2)
+    del q, qb, out
+    cr.free_batch(P)
+    cr.free_batch(B)
+    log("batch api", {k: (v.get("frac_of_hbm_peak") if isinstance(v, dict) else v) for k, v in res.items()})
+    return res
 
 
 def sparse_arrays(cr, density, seed):

@@ -291,6 +291,41 @@ int plan_portable(const cr_gpu_roaring* bm, hipStream_t s, Scratch& sc, HostPlan
     return CR_OK;
 }
 
+// Device -> pageable host memory through two pinned 32 MiB chunks: the DMA of
+// one chunk overlaps the host copy of the previous one (a direct copy into
+// pageable memory runs at a fraction of the link rate).
+PinnedStage g_ser_stage;
+
+int copy_to_host(uint8_t* dst, const uint8_t* src, uint64_t bytes, hipStream_t s)
+{
+    constexpr uint64_t CH = 32ull << 20;
+    std::lock_guard<std::mutex> lock(g_ser_stage.mu);
+    CR_RET(g_ser_stage.reserve(2 * CH));
+    uint8_t* pin = static_cast<uint8_t*>(g_ser_stage.ptr);
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    for (int i = 0; i < 2; ++i) CR_HIP_RET(hipEventCreateWithFlags(&ev[i], hipEventDisableTiming));
+    const uint64_t n = (bytes + CH - 1) / CH;
+    auto drain = [&](uint64_t i) -> hipError_t {  // chunk i has landed in its pinned half: copy it out
+        const hipError_t e = hipEventSynchronize(ev[i & 1]);
+        if (e == hipSuccess) std::memcpy(dst + i * CH, pin + (i & 1) * CH, std::min(CH, bytes - i * CH));
+        return e;
+    };
+    hipError_t e = hipSuccess;
+    for (uint64_t i = 0; i < n && e == hipSuccess; ++i) {
+        if (i >= 2) e = drain(i - 2);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(pin + (i & 1) * CH, src + i * CH, std::min(CH, bytes - i * CH), hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipEventRecord(ev[i & 1], s);
+    }
+    for (uint64_t i = n > 2 ? n - 2 : 0; i < n && e == hipSuccess; ++i) e = drain(i);
+    for (int i = 0; i < 2; ++i) (void)hipEventDestroy(ev[i]);
+    if (e != hipSuccess) {
+        set_error("cr_portable_serialize: %s", hipGetErrorString(e));
+        return CR_ERR_HIP;
+    }
+    return CR_OK;
+}
+
 void put16h(uint8_t* p, uint32_t v)
 {
     p[0] = static_cast<uint8_t>(v);
@@ -389,8 +424,8 @@ extern "C" int cr_portable_serialize(const cr_gpu_roaring* bm, cr_stream_t strea
         ps_write<<<hp.n_cand, CV_NT, 0, s>>>(*bm, p.form, offs, static_cast<uint8_t*>(stage));
     }
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess) e = hipMemcpyAsync(h + hp.header, stage, hp.payload, hipMemcpyDeviceToHost, s);
-    const int rc = e == hipSuccess ? sync_stream(s) : CR_ERR_HIP;
+    int rc = e == hipSuccess ? copy_to_host(h + hp.header, static_cast<const uint8_t*>(stage), hp.payload, s)
+                             : CR_ERR_HIP;
     if (e != hipSuccess) set_error("cr_portable_serialize: %s", hipGetErrorString(e));
     dev_free(stage, s);
     return rc;
