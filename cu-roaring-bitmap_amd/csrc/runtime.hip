@@ -251,31 +251,73 @@ bool g_timing_on = false;
 struct TimingRec {
     std::string name;
     hipEvent_t start, stop;
+    int dev;
 };
 static std::mutex g_timing_mu;
 static std::vector<TimingRec> g_timing_recs;
+// Events are recycled (creating one costs far more than recording it, and the
+// timed calls should see as little of the timer as possible).  Each pool
+// entry remembers the device it was created on.
+static std::vector<std::pair<int, hipEvent_t>> g_event_pool;
+
+static int current_device()
+{
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    return dev;
+}
+
+static hipEvent_t take_event()
+{
+    const int dev = current_device();
+    {
+        std::lock_guard<std::mutex> lock(g_timing_mu);
+        for (size_t i = g_event_pool.size(); i-- > 0;) {
+            if (g_event_pool[i].first == dev) {
+                hipEvent_t e = g_event_pool[i].second;
+                g_event_pool.erase(g_event_pool.begin() + static_cast<std::ptrdiff_t>(i));
+                return e;
+            }
+        }
+    }
+    // Timing only: no system-scope fence (cache write-back) when the event is
+    // recorded, which would otherwise slow the work that follows it.
+    hipEvent_t e = nullptr;
+    return hipEventCreateWithFlags(&e, hipEventDisableSystemFence) == hipSuccess ? e : nullptr;
+}
+
+static void give_event_locked(hipEvent_t e, int dev) { g_event_pool.emplace_back(dev, e); }
+
+
+// Sampling: with period p, only every p-th launch of each kernel name is timed
+// (the event markers add a few microseconds of queue time per launch).
+static uint32_t g_timing_period = 1;
+static std::unordered_map<const char*, uint64_t> g_timing_seen;
 
 TimedLaunch::TimedLaunch(const char* n, hipStream_t s) : name(n), stream(s)
 {
     if (!g_timing_on) return;
-    if (hipEventCreate(&start) != hipSuccess) {
-        start = nullptr;
-        return;
+    {
+        std::lock_guard<std::mutex> lock(g_timing_mu);
+        if (g_timing_seen[n]++ % g_timing_period != 0) return;
     }
-    (void)hipEventRecord(start, s);
+    start = take_event();
+    if (start) (void)hipEventRecord(start, s);
 }
 
 TimedLaunch::~TimedLaunch()
 {
     if (!start) return;
-    hipEvent_t stop = nullptr;
-    if (hipEventCreate(&stop) != hipSuccess) {
-        (void)hipEventDestroy(start);
+    hipEvent_t stop = take_event();
+    const int dev = current_device();
+    if (!stop) {
+        std::lock_guard<std::mutex> lock(g_timing_mu);
+        give_event_locked(start, dev);
         return;
     }
     (void)hipEventRecord(stop, stream);
     std::lock_guard<std::mutex> lock(g_timing_mu);
-    g_timing_recs.push_back(TimingRec{name, start, stop});
+    g_timing_recs.push_back(TimingRec{name, start, stop, dev});
 }
 
 static std::vector<std::pair<std::string, double>> g_host_recs;
@@ -454,12 +496,15 @@ int cr_timing_enable(int on)
 {
     std::lock_guard<std::mutex> lock(g_timing_mu);
     for (auto& r : g_timing_recs) {
-        (void)hipEventDestroy(r.start);
-        (void)hipEventDestroy(r.stop);
+        (void)hipEventSynchronize(r.stop);  // recorded work must pass the events before they are reused
+        give_event_locked(r.start, r.dev);
+        give_event_locked(r.stop, r.dev);
     }
     g_timing_recs.clear();
     g_host_recs.clear();
+    g_timing_seen.clear();
     g_timing_on = on != 0;
+    g_timing_period = on > 1 ? static_cast<uint32_t>(on) : 1u;
     return CR_OK;
 }
 

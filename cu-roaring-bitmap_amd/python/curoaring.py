@@ -490,9 +490,10 @@ def synchronize(stream=None):
     _check(load().cr_stream_synchronize(_stream(stream)), "stream_synchronize")
 
 
-def timing_enable(on: bool = True):
-    """Start (or stop) per-kernel HIP-event timing inside the library; clears records."""
-    _check(load().cr_timing_enable(1 if on else 0), "timing_enable")
+def timing_enable(on: bool = True, every: int = 1):
+    """Start (or stop) per-kernel HIP-event timing inside the library; clears records.
+    every > 1 times only every every-th launch of each kernel."""
+    _check(load().cr_timing_enable(max(1, int(every)) if on else 0), "timing_enable")
 
 
 def timing_report() -> dict:

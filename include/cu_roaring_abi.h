@@ -344,8 +344,9 @@ int cr_stream_synchronize(cr_stream_t stream);
  * cached blocks of `device_id` (-1 = current device) and trim its pool down to
  * `keep_bytes`; synchronises the device. */
 int cr_mempool_trim(int device_id, size_t keep_bytes);
-/* Per-kernel HIP-event timing: enable (1) / disable (0) and clear the records;
- * the report is one "kernel_name launches total_ms" line per kernel. */
+/* Per-kernel HIP-event timing: enable (on >= 1) / disable (0) and clear the
+ * records; with on = p > 1 only every p-th launch of each kernel is timed.
+ * The report is one "kernel_name timed_launches total_ms" line per kernel. */
 int cr_timing_enable(int on);
 int cr_timing_report(char* buf, size_t cap);
 
