@@ -118,9 +118,10 @@ struct TkArgs {
     uint32_t k;
     uint32_t n_chunks;  // multiple of 8
     uint32_t vec;       // rows are 16-B aligned with dim % 4 == 0
-    float* list_d;      // [n_chunks][n_q][k]
-    uint32_t* list_id;  // [n_chunks][n_q][k]
-    uint32_t* list_n;   // [n_chunks][n_q]
+    float* list_d;      // two planes of [n_chunks][n_q][k]: a merge reads one, writes the other
+    uint32_t* list_id;  // the same two planes
+    size_t plane;       // elements per plane
+    uint32_t* list_n;   // [n_chunks][n_q]: list length | (plane holding the list << 31)
     uint32_t* tau;      // [n_q] bits of the smallest k-th distance any chunk has reached
     uint32_t* tau_m;    // [n_chunks][n_q] bits of each chunk's m_rank-th distance (+inf: fewer entries)
     uint32_t m_rank;    // ceil(2k / n_chunks)
@@ -130,14 +131,12 @@ struct TkArgs {
 struct TkWave {
     float cd[TK_CB];  // candidate buffer: distance, id, query slot (0..31)
     uint32_t cid[TK_CB];
-    float sd[TK_CB];  // the buffer grouped by query during a merge
-    uint32_t sid[TK_CB];
-    float ld[TK_KMAX];  // one query's current list during a merge
-    uint32_t lid[TK_KMAX];
-    float td[TK_QW];  // the query's k-th best so far (+inf, NOID while the list is short)
-    float tm[TK_QW];  // the query's m_rank-th best so far (+inf while the list is shorter)
+    uint64_t sk[TK_CB];  // sort keys during a merge: query << 32 | distance bits
+    float td[TK_QW];     // the query's k-th best so far (+inf, NOID while the list is short)
+    float tm[TK_QW];     // the query's m_rank-th best so far (+inf while the list is shorter)
     uint32_t tid[TK_QW];
-    uint32_t ln[TK_QW];  // list length
+    uint32_t ln[TK_QW];   // list length
+    uint32_t par[TK_QW];  // plane holding the list
     uint32_t qcnt[TK_QW];
     uint32_t qoff[TK_QW];
     uint8_t cq[TK_CB];
@@ -182,129 +181,102 @@ __device__ __forceinline__ float tk_spread_bound(const uint32_t* tau_m, uint32_t
 }
 
 // Merges the wave's candidate buffer into the sorted top-k lists of its
-// queries (global memory, [chunk][query][k]) and publishes every full list's
-// k-th distance to the shared per-query bound.  Wave-level: no block barrier.
+// queries (global memory, [chunk][query][k] in two planes) and publishes every
+// full list's k-th distance to the shared per-query bound.  Wave-level: no
+// block barrier.  The whole buffer is sorted by (query, distance, id) in one
+// bitonic network, which leaves each query's candidates as a sorted run; then
+// the lane of each query walks its list (read from its current plane) and
+// its run together and writes the first min(k, n + nc) of the union to the
+// other plane.  Distances are non-negative, so their bits order as values.
 __device__ __forceinline__ void tk_flush(TkWave& W, uint32_t cnt, uint32_t k, uint32_t m_rank, uint32_t nq_wave,
-                                         float* gd_row, uint32_t* gi_row, uint32_t* tau_q0, uint32_t* tau_m_q0)
+                                         float* gd_row, uint32_t* gi_row, size_t plane, uint32_t* tau_q0,
+                                         uint32_t* tau_m_q0)
 {
     const uint32_t lane = __lane_id();
-    // Group the buffer by query: per-query counts, offsets, scatter.
     if (lane < TK_QW) W.qcnt[lane] = 0;
     __builtin_amdgcn_wave_barrier();
-    uint32_t rk[TK_CB / 64];
-#pragma unroll
-    for (uint32_t u = 0; u < TK_CB / 64; ++u) {
-        const uint32_t e = lane + 64 * u;
-        rk[u] = e < cnt ? atomicAdd(&W.qcnt[W.cq[e]], 1u) : 0u;
+    for (uint32_t e = lane; e < cnt; e += 64) atomicAdd(&W.qcnt[W.cq[e]], 1u);
+    uint32_t P = 64;
+    while (P < cnt) P <<= 1;
+    for (uint32_t e = lane; e < P; e += 64) {
+        if (e < cnt) {
+            W.sk[e] = (static_cast<uint64_t>(W.cq[e]) << 32) | __float_as_uint(W.cd[e]);
+        } else {
+            W.sk[e] = ~0ull;
+            W.cid[e] = TK_NOID;
+        }
     }
     __builtin_amdgcn_wave_barrier();
     const uint32_t c_l = lane < TK_QW ? W.qcnt[lane] : 0u;
     const uint32_t o_l = wave_incl_scan(c_l) - c_l;
-    if (lane < TK_QW) W.qoff[lane] = o_l;
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (uint32_t u = 0; u < TK_CB / 64; ++u) {
-        const uint32_t e = lane + 64 * u;
-        if (e < cnt) {
-            const uint32_t p = W.qoff[W.cq[e]] + rk[u];
-            W.sd[p] = W.cd[e];
-            W.sid[p] = W.cid[e];
+    for (uint32_t size = 2; size <= P; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t pp = lane; pp < P / 2; pp += 64) {
+                const uint32_t i = 2 * stride * (pp / stride) + (pp % stride);
+                const uint32_t i2 = i + stride;
+                const uint64_t a0 = W.sk[i], a1 = W.sk[i2];
+                const uint32_t b0 = W.cid[i], b1 = W.cid[i2];
+                const bool up = (i & size) == 0;
+                const bool lt = a1 < a0 || (a1 == a0 && b1 < b0);
+                if (lt == up) {
+                    W.sk[i] = a1;
+                    W.cid[i] = b1;
+                    W.sk[i2] = a0;
+                    W.cid[i2] = b0;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
         }
     }
-    __builtin_amdgcn_wave_barrier();
-    uint64_t todo = __ballot(lane < nq_wave && c_l > 0);
-    // The list of the next query is loaded while the current one merges.
-    float pd[TK_KMAX / 64];
-    uint32_t pi[TK_KMAX / 64];
-    auto load_list = [&](uint32_t q) {
-        const uint32_t n = W.ln[q];
-        const float* gd = gd_row + static_cast<size_t>(q) * k;
-        const uint32_t* gi = gi_row + static_cast<size_t>(q) * k;
-#pragma unroll
-        for (uint32_t u = 0; u < TK_KMAX / 64; ++u) {
-            const uint32_t i = lane + 64 * u;
-            pd[u] = i < n ? gd[i] : 0.f;
-            pi[u] = i < n ? gi[i] : 0u;
-        }
-    };
-    if (todo) load_list(static_cast<uint32_t>(__builtin_ctzll(todo)));
-    while (todo) {
-        const uint32_t jj = static_cast<uint32_t>(__builtin_ctzll(todo));
-        todo &= todo - 1;
-        const uint32_t n = W.ln[jj];
-        const uint32_t nc = W.qcnt[jj];
-        const uint32_t off = W.qoff[jj];
-#pragma unroll
-        for (uint32_t u = 0; u < TK_KMAX / 64; ++u) {
-            const uint32_t i = lane + 64 * u;
-            if (i < n) {
-                W.ld[i] = pd[u];
-                W.lid[i] = pi[u];
-            }
-        }
-        // The query's candidates, padded to a power of two with (+inf, NOID),
-        // sorted in cd/cid (free once the buffer is grouped) by a bitonic network.
-        uint32_t P = 1;
-        while (P < nc) P <<= 1;
-        for (uint32_t e = lane; e < P; e += 64) {
-            W.cd[e] = e < nc ? W.sd[off + e] : __builtin_inff();
-            W.cid[e] = e < nc ? W.sid[off + e] : TK_NOID;
-        }
-        __builtin_amdgcn_wave_barrier();
-        if (todo) load_list(static_cast<uint32_t>(__builtin_ctzll(todo)));
-        for (uint32_t size = 2; size <= P; size <<= 1) {
-            for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-                for (uint32_t pp = lane; pp < P / 2; pp += 64) {
-                    const uint32_t i = 2 * stride * (pp / stride) + (pp % stride);
-                    const uint32_t i2 = i + stride;
-                    const float a0 = W.cd[i], a1 = W.cd[i2];
-                    const uint32_t b0 = W.cid[i], b1 = W.cid[i2];
-                    const bool up = (i & size) == 0;
-                    if (tk_less(a1, b1, a0, b0) == up) {
-                        W.cd[i] = a1;
-                        W.cid[i] = b1;
-                        W.cd[i2] = a0;
-                        W.cid[i2] = b0;
-                    }
+    if (lane < nq_wave && c_l > 0) {
+        const uint32_t n = W.ln[lane], par = W.par[lane];
+        const float* ind = gd_row + par * plane + static_cast<size_t>(lane) * k;
+        const uint32_t* ini = gi_row + par * plane + static_cast<size_t>(lane) * k;
+        float* outd = gd_row + (par ^ 1u) * plane + static_cast<size_t>(lane) * k;
+        uint32_t* outi = gi_row + (par ^ 1u) * plane + static_cast<size_t>(lane) * k;
+        const uint32_t m = min(k, n + c_l);
+        uint32_t ia = 0, ib = o_l;
+        const uint32_t eb = o_l + c_l;
+        float xa = n ? ind[0] : __builtin_inff();
+        uint32_t xia = n ? ini[0] : TK_NOID;
+        float yb = __uint_as_float(static_cast<uint32_t>(W.sk[ib]));
+        uint32_t yib = W.cid[ib];
+        float td = W.td[lane], tm = W.tm[lane];
+        uint32_t tid = W.tid[lane];
+        for (uint32_t r = 0; r < m; ++r) {
+            const bool take_a = ia < n && (ib >= eb || tk_less(xa, xia, yb, yib));
+            float d;
+            uint32_t id;
+            if (take_a) {
+                d = xa;
+                id = xia;
+                if (++ia < n) {
+                    xa = ind[ia];
+                    xia = ini[ia];
                 }
-                __builtin_amdgcn_wave_barrier();
-            }
-        }
-        // Merge of two sorted runs: new rank = own index + entries of the other
-        // run before it (all (d, id) pairs are distinct).
-        float* gd = gd_row + static_cast<size_t>(jj) * k;
-        uint32_t* gi = gi_row + static_cast<size_t>(jj) * k;
-        for (uint32_t i = lane; i < n; i += 64) {
-            const float x = W.ld[i];
-            const uint32_t xi = W.lid[i];
-            const uint32_t r = i + tk_lower_bound(W.cd, W.cid, nc, x, xi);
-            if (r < k) {
-                gd[r] = x;
-                gi[r] = xi;
-                if (r == k - 1) {
-                    W.td[jj] = x;
-                    W.tid[jj] = xi;
+            } else {
+                d = yb;
+                id = yib;
+                if (++ib < eb) {
+                    yb = __uint_as_float(static_cast<uint32_t>(W.sk[ib]));
+                    yib = W.cid[ib];
                 }
-                if (r == m_rank - 1) W.tm[jj] = x;
             }
-        }
-        for (uint32_t e = lane; e < nc && e < k; e += 64) {
-            const float y = W.cd[e];
-            const uint32_t yi = W.cid[e];
-            const uint32_t r = e + tk_lower_bound(W.ld, W.lid, n, y, yi);
-            if (r < k) {
-                gd[r] = y;
-                gi[r] = yi;
-                if (r == k - 1) {
-                    W.td[jj] = y;
-                    W.tid[jj] = yi;
-                }
-                if (r == m_rank - 1) W.tm[jj] = y;
+            outd[r] = d;
+            outi[r] = id;
+            if (r == k - 1) {
+                td = d;
+                tid = id;
             }
+            if (r == m_rank - 1) tm = d;
         }
-        if (lane == 0) W.ln[jj] = min(k, n + nc);
-        __builtin_amdgcn_wave_barrier();
+        W.td[lane] = td;
+        W.tid[lane] = tid;
+        W.tm[lane] = tm;
+        W.ln[lane] = m;
+        W.par[lane] = par ^ 1u;
     }
+    __builtin_amdgcn_wave_barrier();
     if (lane < nq_wave) {
         if (W.ln[lane] == k) atomicMin(tau_q0 + lane, __float_as_uint(W.td[lane]));
         if (W.ln[lane] >= m_rank)
@@ -411,6 +383,7 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
         W.tm[lane] = __builtin_inff();
         W.tid[lane] = TK_NOID;
         W.ln[lane] = 0;
+        W.par[lane] = 0;
     }
     if (threadIdx.x == 0) L.flush_req = TK_NOID;
 
@@ -492,7 +465,7 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
                 uint32_t m1 = __shfl(pm, static_cast<int>(j + 32), 64);
                 while (__ballot((m0 | m1) != 0)) {
                     if (cnt + TK_QW > TK_CB) {
-                        tk_flush(W, cnt, a.k, a.m_rank, nq_wave, a.list_d + list_row, a.list_id + list_row, tau_q0, tau_m_q0);
+                        tk_flush(W, cnt, a.k, a.m_rank, nq_wave, a.list_d + list_row, a.list_id + list_row, a.plane, tau_q0, tau_m_q0);
                         cnt = 0;
                         td = W.td[j];
                         tidv = W.tid[j];
@@ -545,7 +518,7 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
         if (t + 1 < n_tiles) tk_store_rows<DP>(L, b ^ 1, pre, pid);
         __syncthreads();
         if (L.flush_req == t && cnt > 0) {
-            tk_flush(W, cnt, a.k, a.m_rank, nq_wave, a.list_d + list_row, a.list_id + list_row, tau_q0, tau_m_q0);
+            tk_flush(W, cnt, a.k, a.m_rank, nq_wave, a.list_d + list_row, a.list_id + list_row, a.plane, tau_q0, tau_m_q0);
             cnt = 0;
             td = W.td[j];
             tidv = W.tid[j];
@@ -555,15 +528,15 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
             tsh = fminf(tsh, tk_spread_bound(a.tau_m, a.n_chunks, a.n_q, q0 + j, qok, h, a.k, a.m_rank));
     }
     if (nq_wave > 0) {
-        if (cnt) tk_flush(W, cnt, a.k, a.m_rank, nq_wave, a.list_d + list_row, a.list_id + list_row, tau_q0, tau_m_q0);
+        if (cnt) tk_flush(W, cnt, a.k, a.m_rank, nq_wave, a.list_d + list_row, a.list_id + list_row, a.plane, tau_q0, tau_m_q0);
         __builtin_amdgcn_wave_barrier();
-        if (lane < nq_wave) a.list_n[static_cast<size_t>(chunk) * a.n_q + q0 + lane] = W.ln[lane];
+        if (lane < nq_wave) a.list_n[static_cast<size_t>(chunk) * a.n_q + q0 + lane] = W.ln[lane] | (W.par[lane] << 31);
     }
 }
 
 // ---- 3. merge of the chunk lists -------------------------------------------
 
-__global__ __launch_bounds__(TK_MERGE_NT) void tk_merge(const float* list_d, const uint32_t* list_id,
+__global__ __launch_bounds__(TK_MERGE_NT) void tk_merge(const float* list_d, const uint32_t* list_id, size_t plane,
                                                          const uint32_t* list_n, uint32_t n_chunks, uint32_t n_q,
                                                          uint32_t k, float* out_d, int64_t* out_id)
 {
@@ -580,11 +553,13 @@ __global__ __launch_bounds__(TK_MERGE_NT) void tk_merge(const float* list_d, con
     int cur = 0;
     for (uint32_t c = 0; c < n_chunks; ++c) {
         const size_t row = static_cast<size_t>(c) * n_q + q;
-        const uint32_t m = list_n[row];
+        const uint32_t ln = list_n[row];
+        const uint32_t m = ln & 0x7FFFFFFFu;
         if (m == 0) continue;
+        const size_t base = (ln >> 31) * plane + row * k;
         for (uint32_t i = lane; i < m; i += 64) {
-            cd[w][i] = list_d[row * k + i];
-            ci[w][i] = list_id[row * k + i];
+            cd[w][i] = list_d[base + i];
+            ci[w][i] = list_id[base + i];
         }
         __builtin_amdgcn_wave_barrier();
         for (uint32_t i = lane; i < n; i += 64) {
@@ -655,8 +630,8 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     const size_t o_nsel = cv.add(4);
     const size_t o_sel = cv.add(filter ? n_base * 4 : 0);
     const size_t lists = static_cast<size_t>(n_chunks) * n_q * k;
-    const size_t o_ld = cv.add(lists * 4);
-    const size_t o_li = cv.add(lists * 4);
+    const size_t o_ld = cv.add(2 * lists * 4);
+    const size_t o_li = cv.add(2 * lists * 4);
     const size_t o_ln = cv.add(static_cast<size_t>(n_chunks) * n_q * 4);
     const size_t o_tau = cv.add(static_cast<size_t>(n_q) * 4);
     const size_t o_taum = cv.add(static_cast<size_t>(n_chunks) * n_q * 4);
@@ -675,6 +650,7 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     a.list_d = sc.at<float>(o_ld);
     a.list_id = sc.at<uint32_t>(o_li);
     a.list_n = sc.at<uint32_t>(o_ln);
+    a.plane = lists;
     a.tau = sc.at<uint32_t>(o_tau);
     a.tau_m = sc.at<uint32_t>(o_taum);
     a.m_rank = std::max<uint32_t>(1, (2 * k + n_chunks - 1) / n_chunks);
@@ -711,8 +687,8 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     }
     {
         CR_TIMED("tk_merge", s);
-        tk_merge<<<(n_q + 3) / 4, TK_MERGE_NT, 0, s>>>(a.list_d, a.list_id, a.list_n, n_chunks, n_q, k, d_out_dist,
-                                                        d_out_ids);
+        tk_merge<<<(n_q + 3) / 4, TK_MERGE_NT, 0, s>>>(a.list_d, a.list_id, a.plane, a.list_n, n_chunks, n_q, k,
+                                                        d_out_dist, d_out_ids);
     }
     CR_LAUNCH_CHECK();
     return CR_OK;
