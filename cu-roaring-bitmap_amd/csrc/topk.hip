@@ -45,6 +45,10 @@ constexpr int TK_MERGE_NT = 256;
 // product, the two norms and the combination, plus the direct sum's own
 // 128-term bound, rounded up.
 constexpr float TK_GATE_ERR = 4e-5f;
+// The MFMA estimate with the (1 - TK_GATE_ERR) scaling is at most the fp32
+// distance; adding TK_SEED_ERR (qg + xg) makes it at least the fp32 distance
+// (2 E / (1 - E) with E = TK_GATE_ERR, rounded up for the fp32 arithmetic).
+constexpr float TK_SEED_ERR = 3.0f * TK_GATE_ERR;
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -412,6 +416,7 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
     float td = __builtin_inff();
     uint32_t tidv = TK_NOID;
     float tsh = __builtin_inff();
+    float seed = __builtin_inff();  // bound on the chunk's k-th best from its first tile
     uint32_t cnt = 0;  // wave-uniform fill of the candidate buffer
     for (uint32_t t = 0; t < n_tiles; ++t) {
         const int b = static_cast<int>(t & 1u);
@@ -441,20 +446,69 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
             // row passes when that margin could put it at or below the
             // thresholds.  Accumulator register r of block u holds base row
             // tk_row(16u + r, h) against query column j.
-            const float tgate = fminf(td, tsh);
-            uint32_t pm = 0;
+            // The accumulators become the estimates |q|^2 + |x|^2 - 2 q.x
+            // (scaled as above; NaN for rows past the chunk).
 #pragma unroll
             for (int rq = 0; rq < 4; ++rq) {
                 const float4 g0 = *reinterpret_cast<const float4*>(&L.xg[b][8 * rq + 4 * h]);
                 const float4 g1 = *reinterpret_cast<const float4*>(&L.xg[b][32 + 8 * rq + 4 * h]);
-                pm |= (qg + g0.x - 2.f * acc0[4 * rq + 0] <= tgate ? 1u : 0u) << (4 * rq + 0);
-                pm |= (qg + g0.y - 2.f * acc0[4 * rq + 1] <= tgate ? 1u : 0u) << (4 * rq + 1);
-                pm |= (qg + g0.z - 2.f * acc0[4 * rq + 2] <= tgate ? 1u : 0u) << (4 * rq + 2);
-                pm |= (qg + g0.w - 2.f * acc0[4 * rq + 3] <= tgate ? 1u : 0u) << (4 * rq + 3);
-                pm |= (qg + g1.x - 2.f * acc1[4 * rq + 0] <= tgate ? 1u : 0u) << (16 + 4 * rq + 0);
-                pm |= (qg + g1.y - 2.f * acc1[4 * rq + 1] <= tgate ? 1u : 0u) << (16 + 4 * rq + 1);
-                pm |= (qg + g1.z - 2.f * acc1[4 * rq + 2] <= tgate ? 1u : 0u) << (16 + 4 * rq + 2);
-                pm |= (qg + g1.w - 2.f * acc1[4 * rq + 3] <= tgate ? 1u : 0u) << (16 + 4 * rq + 3);
+                acc0[4 * rq + 0] = qg + g0.x - 2.f * acc0[4 * rq + 0];
+                acc0[4 * rq + 1] = qg + g0.y - 2.f * acc0[4 * rq + 1];
+                acc0[4 * rq + 2] = qg + g0.z - 2.f * acc0[4 * rq + 2];
+                acc0[4 * rq + 3] = qg + g0.w - 2.f * acc0[4 * rq + 3];
+                acc1[4 * rq + 0] = qg + g1.x - 2.f * acc1[4 * rq + 0];
+                acc1[4 * rq + 1] = qg + g1.y - 2.f * acc1[4 * rq + 1];
+                acc1[4 * rq + 2] = qg + g1.z - 2.f * acc1[4 * rq + 2];
+                acc1[4 * rq + 3] = qg + g1.w - 2.f * acc1[4 * rq + 3];
+            }
+            if (t == 0 && a.k <= TK_ROWS) {
+                // Seed: the k-th smallest estimate of the first tile's rows
+                // (bisection on the lane pair's 64 estimates), raised to an
+                // upper estimate, bounds the chunk's k-th best distance, so
+                // the first tile yields about k candidates per query instead
+                // of all of its rows.
+                float lo = __builtin_inff(), hi = -__builtin_inff();
+                uint32_t nv = 0;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float e0 = acc0[r], e1 = acc1[r];
+                    if (e0 == e0) {
+                        lo = fminf(lo, e0);
+                        hi = fmaxf(hi, e0);
+                        ++nv;
+                    }
+                    if (e1 == e1) {
+                        lo = fminf(lo, e1);
+                        hi = fmaxf(hi, e1);
+                        ++nv;
+                    }
+                }
+                lo = fminf(lo, __shfl_xor(lo, 32, 64));
+                hi = fmaxf(hi, __shfl_xor(hi, 32, 64));
+                nv += __shfl_xor(nv, 32, 64);
+                float xgmax = L.xg[b][lane];
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) xgmax = fmaxf(xgmax, __shfl_xor(xgmax, o, 64));
+                const bool do_seed = qok && nv >= a.k;
+                for (int it = 0; it < 24; ++it) {  // invariant: at least k estimates <= hi
+                    const float mid = 0.5f * (lo + hi);
+                    uint32_t c = 0;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) c += (acc0[r] <= mid ? 1u : 0u) + (acc1[r] <= mid ? 1u : 0u);
+                    c += __shfl_xor(c, 32, 64);
+                    if (c >= a.k)
+                        hi = mid;
+                    else
+                        lo = mid;
+                }
+                if (do_seed) seed = hi + TK_SEED_ERR * (qg + xgmax);
+            }
+            const float tgate = fminf(fminf(td, tsh), seed);
+            uint32_t pm = 0;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                pm |= (acc0[r] <= tgate ? 1u : 0u) << r;
+                pm |= (acc1[r] <= tgate ? 1u : 0u) << (16 + r);
             }
             if (!qok) pm = 0;
             if (__ballot(pm != 0)) {
@@ -498,7 +552,7 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
                     uint32_t id = 0;
                     if (h == 0 && row >= 0) {
                         id = L.id[b][row];
-                        f = tk_less(d, id, td, tidv) && d <= tsh;
+                        f = tk_less(d, id, td, tidv) && d <= tsh && d <= seed;
                     }
                     const uint64_t m = __ballot(f);
                     if (f) {
