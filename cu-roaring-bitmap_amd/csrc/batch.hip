@@ -107,12 +107,17 @@ PinnedStage g_batch_stage;
 // LDS from an array / run container) written to slot c, its popcount as the
 // cardinality (65536 stored as 0), type BITMAP, offset c * 8192
 // (v2/src/promote.cu:66-169).
-__global__ __launch_bounds__(CV_NT) void bt_promote(cr_roaring_batch src, uint32_t T, uint8_t* __restrict__ types,
-                                                    uint32_t* __restrict__ offs, uint16_t* __restrict__ cards,
-                                                    uint64_t* __restrict__ pool)
+// LEAN: one wavefront per container and no run difference array (batches
+// without run containers), so more containers are in flight per CU.
+template <int NT, bool LEAN>
+__global__ __launch_bounds__(NT) void bt_promote(cr_roaring_batch src, uint32_t T, uint8_t* __restrict__ types,
+                                                 uint32_t* __restrict__ offs, uint16_t* __restrict__ cards,
+                                                 uint64_t* __restrict__ pool)
 {
-    __shared__ Image img;
-    __shared__ uint32_t red[CV_NT / 64];
+    constexpr int V = 512 / NT;  // 16-byte words per thread
+    __shared__ alignas(16) uint32_t w[2048];
+    __shared__ int32_t cover[LEAN ? 1 : 2048];
+    __shared__ uint32_t red[NT / 64];
     const uint32_t c = blockIdx.x;
     const uint32_t t = threadIdx.x;
     const uint8_t type = src.types[c];
@@ -121,20 +126,21 @@ __global__ __launch_bounds__(CV_NT) void bt_promote(cr_roaring_batch src, uint32
     if (type == CR_BITMAP) {
         s4 = reinterpret_cast<const uint4*>(src.bitmap_data + off / 8u);
     } else {
-        expand_to_lds(type, (type == CR_ARRAY ? src.array_data : src.run_data) + off / 2u, src.cardinalities[c], &img);
-        s4 = reinterpret_cast<const uint4*>(img.w);
+        expand_img<NT>(type, (type == CR_ARRAY ? src.array_data : src.run_data) + off / 2u, src.cardinalities[c], w,
+                       LEAN ? nullptr : cover);
+        s4 = reinterpret_cast<const uint4*>(w);
     }
-    uint4 v[2];
+    uint4 v[V];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) v[j] = s4[j * CV_NT + t];
+    for (int j = 0; j < V; ++j) v[j] = s4[j * NT + t];
     uint4* d4 = reinterpret_cast<uint4*>(pool + static_cast<uint64_t>(c) * 1024u);
     uint32_t pc = 0;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        d4[j * CV_NT + t] = v[j];
+    for (int j = 0; j < V; ++j) {
+        d4[j * NT + t] = v[j];
         pc += __popc(v[j].x) + __popc(v[j].y) + __popc(v[j].z) + __popc(v[j].w);
     }
-    pc = block_sum<CV_NT>(pc, red);
+    pc = block_sum<NT>(pc, red);
     if (t == 0) {
         types[c] = CR_BITMAP;
         offs[c] = c * 8192u;
@@ -277,10 +283,12 @@ __device__ uint32_t wave_owner(const uint32_t* starts, uint32_t n_bitmaps, uint3
 // One workgroup per global container: its 1024-word window of bitmap b's
 // slot (clipped at the slot end) stored for a bitmap container, OR-ed into
 // the buffer for an array / run container (v2/src/decompress.cu:42-145).
-__global__ __launch_bounds__(CV_NT) void bt_decompress(cr_roaring_batch B, uint64_t* __restrict__ out,
-                                                       uint64_t words_each)
+template <int NT, bool LEAN>
+__global__ __launch_bounds__(NT) void bt_decompress(cr_roaring_batch B, uint64_t* __restrict__ out,
+                                                    uint64_t words_each)
 {
-    __shared__ Image img;
+    __shared__ alignas(16) uint32_t w[2048];
+    __shared__ int32_t cover[LEAN ? 1 : 2048];
     __shared__ uint32_t s_b;
     const uint32_t c = blockIdx.x;
     const uint32_t t = threadIdx.x;
@@ -299,12 +307,13 @@ __global__ __launch_bounds__(CV_NT) void bt_decompress(cr_roaring_batch B, uint6
     const uint32_t off = B.offsets[c];
     if (type == CR_BITMAP) {
         const uint64_t* src = B.bitmap_data + off / 8u;
-        for (uint32_t w = t; w < window; w += CV_NT) dst[w] = src[w];
+        for (uint32_t i = t; i < window; i += NT) dst[i] = src[i];
         return;
     }
-    expand_to_lds(type, (type == CR_ARRAY ? B.array_data : B.run_data) + off / 2u, B.cardinalities[c], &img);
-    const uint64_t* img64 = reinterpret_cast<const uint64_t*>(img.w);
-    for (uint32_t w = t; w < window; w += CV_NT) dst[w] |= img64[w];
+    expand_img<NT>(type, (type == CR_ARRAY ? B.array_data : B.run_data) + off / 2u, B.cardinalities[c], w,
+                   LEAN ? nullptr : cover);
+    const uint64_t* img64 = reinterpret_cast<const uint64_t*>(w);
+    for (uint32_t i = t; i < window; i += NT) dst[i] |= img64[i];
 }
 
 // ---- queries --------------------------------------------------------------------
@@ -505,8 +514,13 @@ extern "C" int cr_promote_batch(const cr_roaring_batch* in, cr_stream_t stream, 
     rc = copy_segments(cl, s);
     if (rc == CR_OK && T) {
         CR_TIMED("bt_promote", s);
-        bt_promote<<<static_cast<uint32_t>(T), CV_NT, 0, s>>>(*in, static_cast<uint32_t>(T), out->types, out->offsets,
-                                                            out->cardinalities, out->bitmap_data);
+        if (in->run_pool_bytes == 0)
+            bt_promote<128, true><<<static_cast<uint32_t>(T), 128, 0, s>>>(*in, static_cast<uint32_t>(T), out->types,
+                                                                          out->offsets, out->cardinalities,
+                                                                          out->bitmap_data);
+        else
+            bt_promote<CV_NT, false><<<static_cast<uint32_t>(T), CV_NT, 0, s>>>(
+                *in, static_cast<uint32_t>(T), out->types, out->offsets, out->cardinalities, out->bitmap_data);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) {
             set_error("bt_promote launch: %s", hipGetErrorString(e));
@@ -698,7 +712,10 @@ extern "C" int cr_batch_decompress(const cr_roaring_batch* batch, uint64_t* d_bi
     hipStream_t s = as_stream(stream);
     {
         CR_TIMED("bt_decompress", s);
-        bt_decompress<<<batch->total_containers, CV_NT, 0, s>>>(*batch, d_bitsets, words_each);
+        if (batch->run_pool_bytes == 0)
+            bt_decompress<128, true><<<batch->total_containers, 128, 0, s>>>(*batch, d_bitsets, words_each);
+        else
+            bt_decompress<CV_NT, false><<<batch->total_containers, CV_NT, 0, s>>>(*batch, d_bitsets, words_each);
     }
     CR_LAUNCH_CHECK();
     return CR_OK;

@@ -21,9 +21,14 @@ namespace {
 // complement of a negated bitmap is applied on the way out (words below U/32
 // inverted, the tail word's valid bits flipped, src/decompress.cu:128-150).
 // Writes stay below n_words.
-__global__ __launch_bounds__(CV_NT) void cv_decompress(cr_gpu_roaring r, uint32_t* __restrict__ out, uint32_t n_words)
+// LEAN: one wavefront per region and no run difference array (inputs that
+// hold no run container), so more regions are in flight per CU.
+template <int NT, bool LEAN>
+__global__ __launch_bounds__(NT) void cv_decompress(cr_gpu_roaring r, uint32_t* __restrict__ out, uint32_t n_words)
 {
-    __shared__ Image img;
+    constexpr int WPT = 2048 / NT;
+    __shared__ alignas(16) uint32_t w[2048];
+    __shared__ int32_t cover[LEAN ? 1 : 2048];
     __shared__ int32_t s_c;
     const uint32_t key = blockIdx.x;
     const uint32_t t = threadIdx.x;
@@ -43,16 +48,15 @@ __global__ __launch_bounds__(CV_NT) void cv_decompress(cr_gpu_roaring r, uint32_
     if (type == CR_BITMAP) {
         src = reinterpret_cast<const uint32_t*>(r.bitmap_data + r.offsets[c] / 8u);
     } else {
-        if (type == CR_ARRAY)
-            expand_to_lds(CR_ARRAY, r.array_data + r.offsets[c] / 2u, r.cardinalities[c], &img);
-        else if (type == CR_RUN)
-            expand_to_lds(CR_RUN, r.run_data + r.offsets[c] / 2u, r.cardinalities[c], &img);
-        else {
+        if (type == CR_ARRAY || type == CR_RUN) {
+            expand_img<NT>(type, (type == CR_ARRAY ? r.array_data : r.run_data) + r.offsets[c] / 2u,
+                           r.cardinalities[c], w, LEAN ? nullptr : cover);
+        } else {
 #pragma unroll
-            for (int j = 0; j < CV_WPT; ++j) img.w[j * CV_NT + t] = 0;
+            for (int j = 0; j < WPT; ++j) w[j * NT + t] = 0;
             __syncthreads();
         }
-        src = img.w;
+        src = w;
     }
     const uint64_t w0 = static_cast<uint64_t>(key) * 2048u;
     const uint32_t full = r.universe_size / 32u, tail = r.universe_size % 32u;
@@ -61,26 +65,27 @@ __global__ __launch_bounds__(CV_NT) void cv_decompress(cr_gpu_roaring r, uint32_
     const bool vec = w0 + 2048u <= n_words &&
                      ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15u) == 0;
     if (vec && (!neg || w0 + 2048u <= full)) {
+        constexpr int V = 512 / NT;  // 16-byte words per thread
         const uint4* s4 = reinterpret_cast<const uint4*>(src);
         uint4* d4 = reinterpret_cast<uint4*>(dst);
-        uint4 v[2];
+        uint4 v[V];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) v[j] = s4[j * CV_NT + t];
+        for (int j = 0; j < V; ++j) v[j] = s4[j * NT + t];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < V; ++j) {
             if (neg) v[j] = make_uint4(~v[j].x, ~v[j].y, ~v[j].z, ~v[j].w);
-            d4[j * CV_NT + t] = v[j];
+            d4[j * NT + t] = v[j];
         }
         return;
     }
-    for (uint32_t i = t; i < 2048u; i += CV_NT) {
-        const uint64_t w = w0 + i;
-        if (w >= n_words) break;
+    for (uint32_t i = t; i < 2048u; i += NT) {
+        const uint64_t wd = w0 + i;
+        if (wd >= n_words) break;
         uint32_t v = src[i];
         if (neg) {
-            if (w < full)
+            if (wd < full)
                 v = ~v;
-            else if (w == full && tail)
+            else if (wd == full && tail)
                 v ^= (1u << tail) - 1u;
         }
         dst[i] = v;
@@ -248,9 +253,12 @@ __global__ __launch_bounds__(CV_NT) void cv_enum_write_arrays(cr_gpu_roaring r, 
 // in LDS from an array / run container), and its key_index slot.  With no
 // array or run container the bitmap pool is copied as it lies, container c
 // taking pool words [c * 1024, c * 1024 + 1024) (src/promote.cu:268-276).
-__global__ __launch_bounds__(CV_NT) void cv_promote(cr_gpu_roaring src, bool all_bitmap, cr_gpu_roaring dst)
+template <int NT, bool LEAN>
+__global__ __launch_bounds__(NT) void cv_promote(cr_gpu_roaring src, bool all_bitmap, cr_gpu_roaring dst)
 {
-    __shared__ Image img;
+    constexpr int WPT = 2048 / NT;
+    __shared__ alignas(16) uint32_t w[2048];
+    __shared__ int32_t cover[LEAN ? 1 : 2048];
     const uint32_t c = blockIdx.x;
     const uint32_t t = threadIdx.x;
     const uint8_t type = src.types[c];
@@ -260,25 +268,26 @@ __global__ __launch_bounds__(CV_NT) void cv_promote(cr_gpu_roaring src, bool all
         words = reinterpret_cast<const uint32_t*>(all_bitmap ? src.bitmap_data + static_cast<uint64_t>(c) * 1024u
                                                              : src.bitmap_data + src.offsets[c] / 8u);
     } else if (type == CR_ARRAY || type == CR_RUN) {
-        expand_to_lds(type, (type == CR_ARRAY ? src.array_data : src.run_data) + src.offsets[c] / 2u,
-                      src.cardinalities[c], &img);
-        words = img.w;
+        expand_img<NT>(type, (type == CR_ARRAY ? src.array_data : src.run_data) + src.offsets[c] / 2u,
+                       src.cardinalities[c], w, LEAN ? nullptr : cover);
+        words = w;
     } else {
 #pragma unroll
-        for (int j = 0; j < CV_WPT; ++j) img.w[j * CV_NT + t] = 0;
+        for (int j = 0; j < WPT; ++j) w[j * NT + t] = 0;
         __syncthreads();
-        words = img.w;
+        words = w;
     }
     if ((reinterpret_cast<uintptr_t>(words) & 15u) == 0) {
+        constexpr int V = 512 / NT;
         const uint4* s4 = reinterpret_cast<const uint4*>(words);
-        uint4 v[2];
+        uint4 v[V];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) v[j] = s4[j * CV_NT + t];
+        for (int j = 0; j < V; ++j) v[j] = s4[j * NT + t];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) o4[j * CV_NT + t] = v[j];
+        for (int j = 0; j < V; ++j) o4[j * NT + t] = v[j];
     } else {
         uint32_t* o = reinterpret_cast<uint32_t*>(o4);
-        for (uint32_t i = t; i < 2048u; i += CV_NT) o[i] = words[i];
+        for (uint32_t i = t; i < 2048u; i += NT) o[i] = words[i];
     }
     if (t == 0) {
         const uint16_t key = src.keys[c];
@@ -367,7 +376,10 @@ int promote_impl(const cr_gpu_roaring* bm, hipStream_t s, cr_gpu_roaring* out)
     if (rc == CR_OK) {
         const bool all_bitmap = bm->n_array_containers == 0 && bm->n_run_containers == 0;
         CR_TIMED("cv_promote", s);
-        cv_promote<<<static_cast<uint32_t>(n), CV_NT, 0, s>>>(*bm, all_bitmap, r);
+        if (bm->n_run_containers == 0)
+            cv_promote<128, true><<<static_cast<uint32_t>(n), 128, 0, s>>>(*bm, all_bitmap, r);
+        else
+            cv_promote<CV_NT, false><<<static_cast<uint32_t>(n), CV_NT, 0, s>>>(*bm, all_bitmap, r);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) {
             set_error("cv_promote launch: %s", hipGetErrorString(e));
@@ -480,7 +492,10 @@ extern "C" int cr_decompress_to_bitset(const cr_gpu_roaring* bm, uint32_t* d_out
     const uint32_t regions = static_cast<uint32_t>((static_cast<uint64_t>(n_words) + 2047u) / 2048u);
     {
         CR_TIMED("cv_decompress", s);
-        cv_decompress<<<regions, CV_NT, 0, s>>>(*bm, d_out, n_words);
+        if (bm->n_run_containers == 0)
+            cv_decompress<128, true><<<regions, 128, 0, s>>>(*bm, d_out, n_words);
+        else
+            cv_decompress<CV_NT, false><<<regions, CV_NT, 0, s>>>(*bm, d_out, n_words);
     }
     CR_LAUNCH_CHECK();
     return CR_OK;
