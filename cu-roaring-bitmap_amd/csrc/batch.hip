@@ -260,6 +260,70 @@ __global__ __launch_bounds__(CV_NT) void bt_and(cr_roaring_batch B, const uint32
     }
 }
 
+// Up to 64 inputs: one wavefront per surviving anchor container (grid-stride),
+// lane j resolves input j's container address, and the wave streams each
+// input's 8 KiB as eight 16-byte loads per lane with the next input's loads
+// issued before the current one is ANDed in.
+__global__ __launch_bounds__(256) void bt_and_wave(cr_roaring_batch B, const uint32_t* __restrict__ idx, uint32_t n_in,
+                                                   uint32_t a0, uint32_t an, const uint64_t* __restrict__ flags,
+                                                   const uint64_t* __restrict__ pos, AndOut o)
+{
+    __shared__ unsigned long long wave_total[4];
+    const uint32_t lane = __lane_id();
+    const uint32_t n_waves = gridDim.x * 4u;
+    unsigned long long my_total = 0;
+    for (uint32_t i = (blockIdx.x * 256u + threadIdx.x) >> 6; i < an; i += n_waves) {
+        if (flags[i] == 0) continue;  // the whole wavefront skips
+        const uint32_t k = static_cast<uint32_t>(pos[i]);
+        const uint32_t key = B.keys[a0 + i];
+        unsigned long long my_p = 0;
+        if (lane < n_in) {
+            const uint32_t b = idx[lane];
+            const uint32_t gcid = B.container_starts[b] + B.key_indices[B.key_index_starts[b] + key];
+            my_p = reinterpret_cast<unsigned long long>(B.bitmap_data + B.offsets[gcid] / 8u);
+        }
+        auto load8 = [&](uint32_t j, uint4 (&x)[8]) {
+            const uint4* p4 = reinterpret_cast<const uint4*>(__shfl(my_p, static_cast<int>(j), 64));
+#pragma unroll
+            for (int q = 0; q < 8; ++q) x[q] = p4[lane + 64 * q];
+        };
+        uint4 acc[8], cur[8], nxt[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[q] = make_uint4(~0u, ~0u, ~0u, ~0u);
+        load8(0, cur);
+        for (uint32_t j = 0; j < n_in; ++j) {
+            if (j + 1 < n_in) load8(j + 1, nxt);
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                acc[q] = make_uint4(acc[q].x & cur[q].x, acc[q].y & cur[q].y, acc[q].z & cur[q].z, acc[q].w & cur[q].w);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) cur[q] = nxt[q];
+        }
+        uint4* d4 = reinterpret_cast<uint4*>(o.pool + static_cast<uint64_t>(k) * 1024u);
+        uint32_t pc = 0;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            d4[lane + 64 * q] = acc[q];
+            pc += __popc(acc[q].x) + __popc(acc[q].y) + __popc(acc[q].z) + __popc(acc[q].w);
+        }
+        pc = wave_sum(pc);
+        my_total += pc;
+        if (lane == 0) {
+            o.keys[k] = static_cast<uint16_t>(key);
+            o.types[k] = CR_BITMAP;
+            o.offs[k] = k * 8192u;
+            o.cards[k] = static_cast<uint16_t>(pc > 65535u ? 0u : pc);
+            o.kidx[key] = static_cast<uint16_t>(k);
+        }
+    }
+    if (lane == 0) wave_total[threadIdx.x >> 6] = my_total;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned long long s = wave_total[0] + wave_total[1] + wave_total[2] + wave_total[3];
+        if (s) atomicAdd(o.total, s);
+    }
+}
+
 // ---- decompress -----------------------------------------------------------------
 // Owner of global container c: the b with container_starts[b] <= c <
 // container_starts[b + 1], found with 64 probes per step by one wavefront.
@@ -659,7 +723,12 @@ extern "C" int cr_batch_multi_and(const cr_roaring_batch* batch, const uint32_t*
         AndOut o{out->keys, out->types, out->offsets, out->cardinalities, out->key_indices, out->bitmap_data, total};
         {
             CR_TIMED("bt_and", s);
-            bt_and<<<an, CV_NT, 0, s>>>(*batch, d_idx, n_inputs, a0, flags, pos, o);
+            if (n_inputs <= 64) {
+                const uint32_t grid = std::min<uint32_t>((an + 3) / 4, 4u * num_cus());
+                bt_and_wave<<<grid, 256, 0, s>>>(*batch, d_idx, n_inputs, a0, an, flags, pos, o);
+            } else {
+                bt_and<<<an, CV_NT, 0, s>>>(*batch, d_idx, n_inputs, a0, flags, pos, o);
+            }
         }
         hipError_t e = hipGetLastError();
         if (e == hipSuccess) e = hipMemcpyAsync(&n_common, n_common_d, 4, hipMemcpyDeviceToHost, s);

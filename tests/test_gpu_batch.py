@@ -80,6 +80,7 @@ def test_multi_and_parity(gpu, seed):
     rng = np.random.default_rng(seed + 10)
     sets = [[0], [8, 9, 10], [9, 10, 11], [8, 9, 10, 11], [0, 1, 2, 4, 5], [2, 2, 5], [3, 5], list(range(12))]
     sets += [list(rng.choice(12, int(rng.integers(2, 6)), replace=True)) for _ in range(4)]
+    sets += [list(range(12)) * 6, [9] * 64, [9] * 65]  # both sides of the 64-input wavefront path
     for idx in sets:
         want = ob.multi_and(hb, idx)
         R = gpu.batch_multi_and(P, idx)
