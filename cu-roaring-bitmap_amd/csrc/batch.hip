@@ -122,22 +122,23 @@ __global__ __launch_bounds__(NT) void bt_promote(cr_roaring_batch src, uint32_t 
     const uint32_t t = threadIdx.x;
     const uint8_t type = src.types[c];
     const uint32_t off = src.offsets[c];
-    const uint4* s4;
+    uint4 v[V];
     if (type == CR_BITMAP) {
-        s4 = reinterpret_cast<const uint4*>(src.bitmap_data + off / 8u);
+        const uint4* s4 = reinterpret_cast<const uint4*>(src.bitmap_data + off / 8u);
+#pragma unroll
+        for (int j = 0; j < V; ++j) v[j] = ld_stream(s4 + j * NT + t);
     } else {
         expand_img<NT>(type, (type == CR_ARRAY ? src.array_data : src.run_data) + off / 2u, src.cardinalities[c], w,
                        LEAN ? nullptr : cover);
-        s4 = reinterpret_cast<const uint4*>(w);
-    }
-    uint4 v[V];
+        const uint4* s4 = reinterpret_cast<const uint4*>(w);
 #pragma unroll
-    for (int j = 0; j < V; ++j) v[j] = s4[j * NT + t];
+        for (int j = 0; j < V; ++j) v[j] = s4[j * NT + t];
+    }
     uint4* d4 = reinterpret_cast<uint4*>(pool + static_cast<uint64_t>(c) * 1024u);
     uint32_t pc = 0;
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-        d4[j * NT + t] = v[j];
+        st_stream(d4 + j * NT + t, v[j]);
         pc += __popc(v[j].x) + __popc(v[j].y) + __popc(v[j].z) + __popc(v[j].w);
     }
     pc = block_sum<NT>(pc, red);
@@ -222,7 +223,7 @@ __global__ __launch_bounds__(CV_NT) void bt_and(cr_roaring_batch B, const uint32
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) v[q][h] = src[j + q][h * CV_NT + t];
+            for (int h = 0; h < 2; ++h) v[q][h] = ld_stream(src[j + q] + h * CV_NT + t);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -236,7 +237,7 @@ __global__ __launch_bounds__(CV_NT) void bt_and(cr_roaring_batch B, const uint32
     for (; j < n_in; ++j)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const uint4 v = src[j][h * CV_NT + t];
+            const uint4 v = ld_stream(src[j] + h * CV_NT + t);
             acc[h].x &= v.x;
             acc[h].y &= v.y;
             acc[h].z &= v.z;
@@ -246,7 +247,7 @@ __global__ __launch_bounds__(CV_NT) void bt_and(cr_roaring_batch B, const uint32
     uint32_t pc = 0;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        d4[h * CV_NT + t] = acc[h];
+        st_stream(d4 + h * CV_NT + t, acc[h]);
         pc += __popc(acc[h].x) + __popc(acc[h].y) + __popc(acc[h].z) + __popc(acc[h].w);
     }
     pc = block_sum<CV_NT>(pc, red);
@@ -285,7 +286,7 @@ __global__ __launch_bounds__(256) void bt_and_wave(cr_roaring_batch B, const uin
         auto load8 = [&](uint32_t j, uint4 (&x)[8]) {
             const uint4* p4 = reinterpret_cast<const uint4*>(__shfl(my_p, static_cast<int>(j), 64));
 #pragma unroll
-            for (int q = 0; q < 8; ++q) x[q] = p4[lane + 64 * q];
+            for (int q = 0; q < 8; ++q) x[q] = ld_stream(p4 + lane + 64 * q);
         };
         uint4 acc[8], cur[8], nxt[8];
 #pragma unroll
@@ -303,7 +304,7 @@ __global__ __launch_bounds__(256) void bt_and_wave(cr_roaring_batch B, const uin
         uint32_t pc = 0;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            d4[lane + 64 * q] = acc[q];
+            st_stream(d4 + lane + 64 * q, acc[q]);
             pc += __popc(acc[q].x) + __popc(acc[q].y) + __popc(acc[q].z) + __popc(acc[q].w);
         }
         pc = wave_sum(pc);
@@ -369,15 +370,42 @@ __global__ __launch_bounds__(NT) void bt_decompress(cr_roaring_batch B, uint64_t
     uint64_t* dst = out + wb;
     const uint8_t type = B.types[c];
     const uint32_t off = B.offsets[c];
+    constexpr int V = 512 / NT;  // 16-byte vectors per thread for a whole window
+    const bool vec = window == 1024u && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0;
+    uint4* d4 = reinterpret_cast<uint4*>(dst);
     if (type == CR_BITMAP) {
         const uint64_t* src = B.bitmap_data + off / 8u;
-        for (uint32_t i = t; i < window; i += NT) dst[i] = src[i];
+        if (vec && (reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
+            const uint4* s4 = reinterpret_cast<const uint4*>(src);
+            uint4 v[V];
+#pragma unroll
+            for (int j = 0; j < V; ++j) v[j] = ld_stream(s4 + j * NT + t);
+#pragma unroll
+            for (int j = 0; j < V; ++j) st_stream(d4 + j * NT + t, v[j]);
+        } else {
+            for (uint32_t i = t; i < window; i += NT) dst[i] = src[i];
+        }
         return;
+    }
+    uint4 prior[V];
+    if (vec) {  // the caller's words are read while the image is built
+#pragma unroll
+        for (int j = 0; j < V; ++j) prior[j] = ld_stream(d4 + j * NT + t);
     }
     expand_img<NT>(type, (type == CR_ARRAY ? B.array_data : B.run_data) + off / 2u, B.cardinalities[c], w,
                    LEAN ? nullptr : cover);
-    const uint64_t* img64 = reinterpret_cast<const uint64_t*>(w);
-    for (uint32_t i = t; i < window; i += NT) dst[i] |= img64[i];
+    if (vec) {
+        const uint4* l4 = reinterpret_cast<const uint4*>(w);
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const uint4 m = l4[j * NT + t];
+            st_stream(d4 + j * NT + t,
+                      make_uint4(prior[j].x | m.x, prior[j].y | m.y, prior[j].z | m.z, prior[j].w | m.w));
+        }
+    } else {
+        const uint64_t* img64 = reinterpret_cast<const uint64_t*>(w);
+        for (uint32_t i = t; i < window; i += NT) dst[i] |= img64[i];
+    }
 }
 
 // ---- queries --------------------------------------------------------------------

@@ -66,15 +66,21 @@ __global__ __launch_bounds__(NT) void cv_decompress(cr_gpu_roaring r, uint32_t* 
                      ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15u) == 0;
     if (vec && (!neg || w0 + 2048u <= full)) {
         constexpr int V = 512 / NT;  // 16-byte words per thread
-        const uint4* s4 = reinterpret_cast<const uint4*>(src);
         uint4* d4 = reinterpret_cast<uint4*>(dst);
         uint4 v[V];
+        if (type == CR_BITMAP) {
+            const uint4* s4 = reinterpret_cast<const uint4*>(src);
 #pragma unroll
-        for (int j = 0; j < V; ++j) v[j] = s4[j * NT + t];
+            for (int j = 0; j < V; ++j) v[j] = ld_stream(s4 + j * NT + t);
+        } else {
+            const uint4* l4 = reinterpret_cast<const uint4*>(w);
+#pragma unroll
+            for (int j = 0; j < V; ++j) v[j] = l4[j * NT + t];
+        }
 #pragma unroll
         for (int j = 0; j < V; ++j) {
             if (neg) v[j] = make_uint4(~v[j].x, ~v[j].y, ~v[j].z, ~v[j].w);
-            d4[j * NT + t] = v[j];
+            st_stream(d4 + j * NT + t, v[j]);
         }
         return;
     }
@@ -111,12 +117,12 @@ __global__ __launch_bounds__(CV_NT) void cv_enum_count(cr_gpu_roaring r, uint64_
         const uint64_t* p = r.bitmap_data + off / 8u;
         if ((reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
             // 8 KiB = 64 lanes x 8 loads of 16 bytes, all in flight together
-            const ulonglong2* bm = reinterpret_cast<const ulonglong2*>(p);
-            ulonglong2 v[8];
+            const uint4* bm = reinterpret_cast<const uint4*>(p);
+            uint4 v[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = bm[j * 64 + lane];
+            for (int j = 0; j < 8; ++j) v[j] = ld_stream(bm + j * 64 + lane);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) n += static_cast<uint32_t>(__popcll(v[j].x) + __popcll(v[j].y));
+            for (int j = 0; j < 8; ++j) n += __popc(v[j].x) + __popc(v[j].y) + __popc(v[j].z) + __popc(v[j].w);
         } else {
             for (uint32_t w = lane; w < 1024u; w += 64) n += static_cast<uint32_t>(__popcll(p[w]));
         }
@@ -199,7 +205,7 @@ __global__ __launch_bounds__(CV_NT) void cv_enum_write(cr_gpu_roaring r, const u
         const uint16_t* arr = r.array_data + off / 2u;
         const uint32_t card = r.cardinalities[c];
         for (uint32_t i = t; i < card; i += CV_NT)
-            if (start + i < cap) out[start + i] = base | arr[i];
+            if (start + i < cap) st_stream(out + start + i, base | arr[i]);
         return;
     }
     const uint32_t* words;
@@ -226,7 +232,7 @@ __global__ __launch_bounds__(CV_NT) void cv_enum_write(cr_gpu_roaring r, const u
             stage[pos++] = static_cast<uint16_t>(32u * (wi + 1u) + __builtin_ctz(x));
         __syncthreads();
         for (uint32_t i = t; i < total; i += CV_NT)
-            if (written + i < cap) out[written + i] = base | stage[i];
+            if (written + i < cap) st_stream(out + written + i, base | stage[i]);
         written += total;
         __syncthreads();
     }
@@ -244,7 +250,7 @@ __global__ __launch_bounds__(CV_NT) void cv_enum_write_arrays(cr_gpu_roaring r, 
     const int64_t base = static_cast<int64_t>(r.keys[c]) << 16;
     const uint64_t start = starts[c];
     for (uint32_t i = lane; i < card; i += 64)
-        if (start + i < cap) out[start + i] = base | arr[i];
+        if (start + i < cap) st_stream(out + start + i, base | arr[i]);
 }
 
 // ---- promote_to_bitmap ------------------------------------------------------
@@ -264,7 +270,8 @@ __global__ __launch_bounds__(NT) void cv_promote(cr_gpu_roaring src, bool all_bi
     const uint8_t type = src.types[c];
     uint4* o4 = reinterpret_cast<uint4*>(dst.bitmap_data + static_cast<uint64_t>(c) * 1024u);
     const uint32_t* words;
-    if (all_bitmap || type == CR_BITMAP) {
+    const bool glob = all_bitmap || type == CR_BITMAP;
+    if (glob) {
         words = reinterpret_cast<const uint32_t*>(all_bitmap ? src.bitmap_data + static_cast<uint64_t>(c) * 1024u
                                                              : src.bitmap_data + src.offsets[c] / 8u);
     } else if (type == CR_ARRAY || type == CR_RUN) {
@@ -279,12 +286,18 @@ __global__ __launch_bounds__(NT) void cv_promote(cr_gpu_roaring src, bool all_bi
     }
     if ((reinterpret_cast<uintptr_t>(words) & 15u) == 0) {
         constexpr int V = 512 / NT;
-        const uint4* s4 = reinterpret_cast<const uint4*>(words);
         uint4 v[V];
+        if (glob) {
+            const uint4* s4 = reinterpret_cast<const uint4*>(words);
 #pragma unroll
-        for (int j = 0; j < V; ++j) v[j] = s4[j * NT + t];
+            for (int j = 0; j < V; ++j) v[j] = ld_stream(s4 + j * NT + t);
+        } else {
+            const uint4* l4 = reinterpret_cast<const uint4*>(w);
 #pragma unroll
-        for (int j = 0; j < V; ++j) o4[j * NT + t] = v[j];
+            for (int j = 0; j < V; ++j) v[j] = l4[j * NT + t];
+        }
+#pragma unroll
+        for (int j = 0; j < V; ++j) st_stream(o4 + j * NT + t, v[j]);
     } else {
         uint32_t* o = reinterpret_cast<uint32_t*>(o4);
         for (uint32_t i = t; i < 2048u; i += NT) o[i] = words[i];
@@ -450,7 +463,15 @@ __global__ __launch_bounds__(256) void cv_copy(CopyList L)
         const uint64_t n4 = g.bytes / 16u;
         const uint4* s4 = static_cast<const uint4*>(g.src);
         uint4* d4 = static_cast<uint4*>(g.dst);
-        for (uint64_t i = i0; i < n4; i += stride) d4[i] = s4[i];
+        for (uint64_t i = i0; i < n4; i += 4 * stride) {  // four 16-byte loads in flight
+            uint4 v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (i + k * stride < n4) v[k] = ld_stream(s4 + i + k * stride);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (i + k * stride < n4) st_stream(d4 + i + k * stride, v[k]);
+        }
         done = n4 * 16u;
     }
     for (uint64_t i = done + i0; i < g.bytes; i += stride) db[i] = sb[i];

@@ -95,6 +95,29 @@ int free_async(cr_gpu_roaring* r, hipStream_t s);
 // ---- device helpers -------------------------------------------------------
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 
+// Streaming 16-byte load and store: global_load/store_dwordx4 with the `nt`
+// (nontemporal) policy.  For data touched once (container payloads, id
+// streams) this is what lets gfx950 approach its HBM rate: on MI355X a read
+// stream of whole 8 KiB blocks runs at 6.7 TB/s with it and 4.0 TB/s without,
+// and a copy at 5.7 against 4.7 TB/s (the store needs the policy too).
+// Data read again soon by other waves (metadata, shared cache lines) keeps
+// ordinary loads.
+typedef uint32_t cr_v4u __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 ld_stream(const uint4* p)
+{
+    const cr_v4u v = __builtin_nontemporal_load(reinterpret_cast<const cr_v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ void st_stream(uint4* p, uint4 v)
+{
+    const cr_v4u x = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(x, reinterpret_cast<cr_v4u*>(p));
+}
+
+__device__ __forceinline__ void st_stream(int64_t* p, int64_t v) { __builtin_nontemporal_store(v, p); }
+
 __device__ __forceinline__ uint32_t wave_sum(uint32_t v)
 {
 #pragma unroll

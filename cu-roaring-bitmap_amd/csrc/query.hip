@@ -21,6 +21,8 @@ using cu_roaring::GpuRoaringView;
 constexpr int Q_NT = 256;
 constexpr int QPT = 8;
 
+// The id stream and the answers use nontemporal loads and stores, so they do
+// not evict the containers (reused by every query) from the caches.
 // WAVE: when every lane of the wave queries the same key, the key_index entry
 // is read once with a wave-uniform (scalar) load -- wavefront_contains'
 // amortisation -- while the QPT queries of a lane stay independent.
@@ -35,7 +37,7 @@ __global__ __launch_bounds__(Q_NT) void contains_allbitmap(GpuRoaringView v, con
 #pragma unroll
         for (int q = 0; q < QPT; ++q) {
             const uint64_t i = blk + static_cast<uint64_t>(q) * Q_NT + threadIdx.x;
-            id[q] = i < n ? ids[i] : 0u;
+            id[q] = i < n ? __builtin_nontemporal_load(ids + i) : 0u;
         }
 #pragma unroll
         for (int q = 0; q < QPT; ++q) {
@@ -61,7 +63,7 @@ __global__ __launch_bounds__(Q_NT) void contains_allbitmap(GpuRoaringView v, con
                 const uint64_t w = v.bitmap_data[(idx[q] << 10) + (low >> 6)];
                 r = (static_cast<uint32_t>(w >> (low & 63u)) & 1u) ^ neg;
             }
-            if (i < n) out[i] = r;
+            if (i < n) __builtin_nontemporal_store(r, out + i);
         }
     }
 }
@@ -76,9 +78,9 @@ __global__ __launch_bounds__(Q_NT) void contains_general(GpuRoaringView v, const
         for (int q = 0; q < QPT; ++q) {
             const uint64_t i = blk + static_cast<uint64_t>(q) * Q_NT + threadIdx.x;
             if (i < n) {
-                const uint32_t id = ids[i];
+                const uint32_t id = __builtin_nontemporal_load(ids + i);
                 const bool r = MODE == CR_QUERY_WAVEFRONT ? cu_roaring::wavefront_contains(v, id) : v.contains(id);
-                out[i] = r ? 1u : 0u;
+                __builtin_nontemporal_store(r ? 1u : 0u, out + i);
             }
         }
     }

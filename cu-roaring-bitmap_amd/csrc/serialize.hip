@@ -63,8 +63,17 @@ __device__ uint32_t ps_image(const cr_gpu_roaring& r, uint32_t i, Image* img, in
     const uint8_t type = c >= 0 ? r.types[c] : 0xFFu;
     if (type == CR_BITMAP) {
         const uint32_t* src = reinterpret_cast<const uint32_t*>(r.bitmap_data + r.offsets[c] / 8u);
+        if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
+            const uint4* s4 = reinterpret_cast<const uint4*>(src);
+            uint4 v[2];
 #pragma unroll
-        for (int j = 0; j < CV_WPT; ++j) img->w[j * CV_NT + t] = src[j * CV_NT + t];
+            for (int j = 0; j < 2; ++j) v[j] = ld_stream(s4 + j * CV_NT + t);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) reinterpret_cast<uint4*>(img->w)[j * CV_NT + t] = v[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < CV_WPT; ++j) img->w[j * CV_NT + t] = src[j * CV_NT + t];
+        }
         __syncthreads();
     } else if (type == CR_ARRAY) {
         expand_to_lds(CR_ARRAY, r.array_data + r.offsets[c] / 2u, r.cardinalities[c], img);
@@ -175,7 +184,7 @@ __global__ __launch_bounds__(CV_NT) void ps_write(cr_gpu_roaring r, const uint8_
             uint4* d = reinterpret_cast<uint4*>(out + off);
             const uint4* s4 = reinterpret_cast<const uint4*>(img.w);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) d[j * CV_NT + t] = s4[j * CV_NT + t];
+            for (int j = 0; j < 2; ++j) st_stream(d + j * CV_NT + t, s4[j * CV_NT + t]);
         } else if ((off & 3u) == 0) {
             uint32_t* d = reinterpret_cast<uint32_t*>(out + off);
 #pragma unroll

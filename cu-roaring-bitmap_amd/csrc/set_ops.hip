@@ -233,7 +233,8 @@ __device__ __forceinline__ uint32_t bitmap_op_stream(const uint64_t* pa, const u
         const uint4* a = reinterpret_cast<const uint4*>(pa);
         const uint4* b = reinterpret_cast<const uint4*>(pb);
         uint4* o = reinterpret_cast<uint4*>(po);
-        const uint4 x0 = a[t], x1 = a[t + EXEC_NT], y0 = b[t], y1 = b[t + EXEC_NT];
+        const uint4 x0 = ld_stream(a + t), x1 = ld_stream(a + t + EXEC_NT), y0 = ld_stream(b + t),
+                    y1 = ld_stream(b + t + EXEC_NT);
         uint4 r0, r1;
         r0.x = apply32<OP>(x0.x, y0.x);
         r0.y = apply32<OP>(x0.y, y0.y);
@@ -243,8 +244,8 @@ __device__ __forceinline__ uint32_t bitmap_op_stream(const uint64_t* pa, const u
         r1.y = apply32<OP>(x1.y, y1.y);
         r1.z = apply32<OP>(x1.z, y1.z);
         r1.w = apply32<OP>(x1.w, y1.w);
-        o[t] = r0;
-        o[t + EXEC_NT] = r1;
+        st_stream(o + t, r0);
+        st_stream(o + t + EXEC_NT, r1);
         pc = __popc(r0.x) + __popc(r0.y) + __popc(r0.z) + __popc(r0.w) + __popc(r1.x) + __popc(r1.y) +
              __popc(r1.z) + __popc(r1.w);
     } else {
@@ -428,8 +429,9 @@ __global__ __launch_bounds__(EXEC_NT) void so_exec(Side A, Side B, const Item* i
             const uint64_t* src = S.bmp + ((from_a ? it.aoff : it.boff) >> 3);
             uint64_t* dst = out_bmp + it.slot * 1024ull;
             if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
-                reinterpret_cast<uint4*>(dst)[t] = reinterpret_cast<const uint4*>(src)[t];
-                reinterpret_cast<uint4*>(dst)[t + EXEC_NT] = reinterpret_cast<const uint4*>(src)[t + EXEC_NT];
+                st_stream(reinterpret_cast<uint4*>(dst) + t, ld_stream(reinterpret_cast<const uint4*>(src) + t));
+                st_stream(reinterpret_cast<uint4*>(dst) + t + EXEC_NT,
+                          ld_stream(reinterpret_cast<const uint4*>(src) + t + EXEC_NT));
             } else {
                 for (uint32_t i = t; i < 1024u; i += EXEC_NT) dst[i] = src[i];
             }
@@ -488,8 +490,8 @@ __global__ __launch_bounds__(BB_NT) void so_exec_bb(const uint64_t* __restrict__
             uint4 x[8], y[8];  // all 16 loads of the pair in flight before any store
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                x[k] = a4[lane + 64 * k];
-                y[k] = b4[lane + 64 * k];
+                x[k] = ld_stream(a4 + lane + 64 * k);
+                y[k] = ld_stream(b4 + lane + 64 * k);
             }
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
@@ -498,7 +500,7 @@ __global__ __launch_bounds__(BB_NT) void so_exec_bb(const uint64_t* __restrict__
                 r.y = apply32<OP>(x[k].y, y[k].y);
                 r.z = apply32<OP>(x[k].z, y[k].z);
                 r.w = apply32<OP>(x[k].w, y[k].w);
-                o4[lane + 64 * k] = r;
+                st_stream(o4 + lane + 64 * k, r);
                 pc += __popc(r.x) + __popc(r.y) + __popc(r.z) + __popc(r.w);
             }
         } else {
@@ -881,7 +883,7 @@ __global__ __launch_bounds__(EXEC_NT) void mand_and(FusedArgs args, const uint16
             if ((reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
                 const uint4* p4 = reinterpret_cast<const uint4*>(p);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) x[j] = p4[lane + 64 * j];
+                for (int j = 0; j < 8; ++j) x[j] = ld_stream(p4 + lane + 64 * j);
             } else {
                 const uint32_t* p32 = reinterpret_cast<const uint32_t*>(p);
 #pragma unroll
@@ -919,7 +921,7 @@ __global__ __launch_bounds__(EXEC_NT) void mand_and(FusedArgs args, const uint16
         uint32_t pc = 0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            dst[lane + 64 * j] = acc[j];
+            st_stream(dst + lane + 64 * j, acc[j]);
             pc += __popc(acc[j].x) + __popc(acc[j].y) + __popc(acc[j].z) + __popc(acc[j].w);
         }
         pc = wave_sum(pc);

@@ -44,12 +44,29 @@ __global__ __launch_bounds__(BS_NT) void bs_count(const uint32_t* __restrict__ w
     for (uint32_t c = blockIdx.x; c < g.n_chunks; c += gridDim.x) {
         const uint32_t base = c * 2048u;
         uint32_t a = 0, b = 0;
-        for (uint32_t k = threadIdx.x; k < 2048u; k += BS_NT) {
-            const uint32_t i = base + k;
-            if (i < g.n_words) {
-                const uint32_t w = words[i];
-                a += __popc(w);
-                b += (i == g.tail_idx) ? __popc(~w & g.tail_mask) : 32u - __popc(w);
+        if (base + 2048u <= g.n_words && (reinterpret_cast<uintptr_t>(words + base) & 15u) == 0) {
+            const uint4* s4 = reinterpret_cast<const uint4*>(words + base);
+            uint4 v[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) v[h] = ld_stream(s4 + threadIdx.x + h * BS_NT);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t i0 = base + 4u * (threadIdx.x + h * BS_NT);
+                const uint32_t x[4] = {v[h].x, v[h].y, v[h].z, v[h].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    a += __popc(x[q]);
+                    b += (i0 + q == g.tail_idx) ? __popc(~x[q] & g.tail_mask) : 32u - __popc(x[q]);
+                }
+            }
+        } else {
+            for (uint32_t k = threadIdx.x; k < 2048u; k += BS_NT) {
+                const uint32_t i = base + k;
+                if (i < g.n_words) {
+                    const uint32_t w = words[i];
+                    a += __popc(w);
+                    b += (i == g.tail_idx) ? __popc(~w & g.tail_mask) : 32u - __popc(w);
+                }
             }
         }
         a = block_sum<BS_NT>(a, red);
@@ -130,11 +147,24 @@ __global__ __launch_bounds__(BS_NT) void bs_compact(const uint32_t* __restrict__
         uint32_t* dst = reinterpret_cast<uint32_t*>(pool) + static_cast<uint64_t>(r) * 2048u;
         const uint32_t base = c * 2048u;
         const bool full = base + 2048u <= g.n_words;
-        if (full && ((reinterpret_cast<uintptr_t>(words + base) & 15u) == 0) && !negate) {
+        if (full && ((reinterpret_cast<uintptr_t>(words + base) & 15u) == 0)) {
             const uint4* s4 = reinterpret_cast<const uint4*>(words + base);
             uint4* d4 = reinterpret_cast<uint4*>(dst);
-            d4[threadIdx.x] = s4[threadIdx.x];
-            d4[threadIdx.x + BS_NT] = s4[threadIdx.x + BS_NT];
+            uint4 v[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) v[h] = ld_stream(s4 + threadIdx.x + h * BS_NT);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if (negate) {
+                    const uint32_t i0 = base + 4u * (threadIdx.x + h * BS_NT);
+                    v[h] = make_uint4(~v[h].x, ~v[h].y, ~v[h].z, ~v[h].w);
+                    if (i0 == g.tail_idx) v[h].x &= g.tail_mask;
+                    if (i0 + 1 == g.tail_idx) v[h].y &= g.tail_mask;
+                    if (i0 + 2 == g.tail_idx) v[h].z &= g.tail_mask;
+                    if (i0 + 3 == g.tail_idx) v[h].w &= g.tail_mask;
+                }
+                st_stream(d4 + threadIdx.x + h * BS_NT, v[h]);
+            }
         } else {
             for (uint32_t k = threadIdx.x; k < 2048u; k += BS_NT) {
                 const uint32_t i = base + k;

@@ -93,7 +93,7 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
             const uint4* src = reinterpret_cast<const uint4*>(ids + base);
 #pragma unroll
             for (uint32_t q = 0; q < TS_PER / 4; ++q) {
-                const uint4 a = src[t + q * TS_NT];
+                const uint4 a = ld_stream(src + t + q * TS_NT);
                 w[4 * q + 0] = a.x, w[4 * q + 1] = a.y, w[4 * q + 2] = a.z, w[4 * q + 3] = a.w;
             }
             vm = ~0u;
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         }
         uint32_t* dst = part + base;
         const uint32_t n4 = total >> 2;
-        for (uint32_t p = t; p < n4; p += TS_NT) reinterpret_cast<uint4*>(dst)[p] = reinterpret_cast<const uint4*>(buf)[p];
+        for (uint32_t p = t; p < n4; p += TS_NT) st_stream(reinterpret_cast<uint4*>(dst) + p, reinterpret_cast<const uint4*>(buf)[p]);
         for (uint32_t p = 4 * n4 + t; p < total; p += TS_NT) dst[p] = buf[p];
 #pragma unroll
         for (uint32_t j = 0; j < TS_PER; ++j) v[j] = vn[j];
@@ -428,7 +428,7 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
             const uint32_t rank = key_index[key];
             uint4* dst = reinterpret_cast<uint4*>(pool + static_cast<uint64_t>(rank) * 1024u);
             const uint4* src = reinterpret_cast<const uint4*>(cb);
-            for (uint32_t i = lane; i < 512u; i += 64) dst[i] = src[i];
+            for (uint32_t i = lane; i < 512u; i += 64) st_stream(dst + i, src[i]);
             if (lane == 0) cards[rank] = static_cast<uint16_t>(pc > 65535u ? 0u : pc);
         }
     }
