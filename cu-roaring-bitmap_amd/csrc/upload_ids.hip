@@ -12,11 +12,14 @@
 // written once:
 //   tile_sort   read the ids once; counting-sort each tile by bucket in LDS and
 //               stream it back to the tile's own slot, with the tile's bucket
-//               starts in a small table; key presence per workgroup
-//   rank        OR of the presence words, key ranks ->
-//               keys/types/offsets/key_index, totals
+//               starts in a small table; max id per workgroup
 //   build       one workgroup per bucket: read the bucket's run of every tile
-//               (~16 ids at 2^30), LDS bit-set, popcount, write containers
+//               (~16 ids at 2^30), LDS bit-set, popcount, write each present
+//               key's container to pool slot `key`
+//   rank        key ranks from the build's counts ->
+//               keys/types/offsets/cards/key_index, totals, range error
+// When the present keys are not a prefix of the key space, one more step
+// moves the containers into a block of exactly n_containers slots.
 #include <algorithm>
 #include <vector>
 
@@ -27,7 +30,6 @@ namespace crimpl {
 constexpr uint32_t BK_SHIFT = 4;               // 16 keys per bucket
 constexpr uint32_t BK_KEYS = 1u << BK_SHIFT;
 constexpr uint32_t MAX_BUCKETS = 65536 / BK_KEYS;
-constexpr uint32_t MAX_PWORDS = 65536 / 32;
 constexpr int TS_NT = 1024;                    // tile-sort workgroup
 constexpr uint32_t TS_PER = 16;                // ids per thread per tile
 constexpr uint32_t TILE = TS_NT * TS_PER;      // 16384 ids: 64 KiB of LDS
@@ -42,7 +44,7 @@ struct IdsTotals {
     uint32_t n_containers;
     uint32_t err;  // an id's key exceeded max_key
     uint32_t max_id;
-    uint32_t pad;
+    uint32_t moved;  // present keys are not a prefix: the pool needs compaction
     unsigned long long total;  // distinct ids (or complement count)
 };
 
@@ -56,39 +58,43 @@ struct IdsGeom {
     bool vec;     // ids pointer 16-byte aligned
 };
 
-__device__ __forceinline__ uint32_t lanes_below(uint64_t m) { return static_cast<uint32_t>(__popcll(m & ((1ull << __lane_id()) - 1ull))); }
-
-// Each workgroup takes tiles round-robin.  A tile is counting-sorted by bucket
-// in LDS and written back to its own slot of `part` (tile t at t * TILE), a
-// streaming write; `tab` row t holds the tile's bucket starts (NB + 1 u16).
-// Ids whose key exceeds max_key are flagged and left out.  Key presence is
-// OR-ed per workgroup.
+// Each workgroup takes blocks of TB tiles.  A tile is counting-sorted by
+// bucket in LDS and written back to its own slot of `part` (tile t at
+// t * TILE), a streaming write; `tab` row t holds the tile's bucket starts
+// (NB + 1 u16).  An id whose bucket lies past the universe's last goes to a
+// sentinel bucket NB that is sorted after the others and neither written nor
+// built; the error is raised from the maximum id, which each workgroup
+// reports.  Every lane holds an id: a partial last tile is padded with ids of
+// the sentinel bucket (which do not enter the maximum).
 __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restrict__ ids, IdsGeom g,
                                                        uint32_t* __restrict__ part, uint16_t* __restrict__ tab,
-                                                       uint32_t* gpres, uint32_t* gerr, uint32_t* gmax)
+                                                       uint32_t* gmax, IdsTotals* tot)
 {
     __shared__ uint32_t buf[TILE];
     __shared__ uint32_t cnt[MAX_BUCKETS + 1];
-    __shared__ uint32_t pres[MAX_PWORDS];
     // A block's run-table rows are staged here and written as one contiguous
     // copy when the block ends (up to STAGE_NB buckets; more write directly).
     __shared__ uint4 stage[STAGE_NB + 1];  // row i = TB u16 starts of bucket i
     __shared__ uint32_t lds[16];
-    __shared__ uint32_t s_err, s_max;
+    __shared__ uint32_t s_max;
     const uint32_t t = threadIdx.x;
     const uint32_t lane = __lane_id();
-    const bool staged = g.NB <= STAGE_NB;
-    for (uint32_t i = t; i < g.NW; i += TS_NT) pres[i] = 0;
+    const uint32_t NB = g.NB;
+    const bool staged = NB <= STAGE_NB;
     if (t == 0) {
-        s_err = 0;
         s_max = 0;
+        if (blockIdx.x == 0) {  // the build accumulates the distinct count
+            tot->total = 0;
+            tot->moved = 0;
+        }
     }
-    const uint32_t max_key = g.K - 1;
-    uint32_t err = 0, mx = 0;
-    auto load_ids = [&](uint32_t tl, uint32_t (&w)[TS_PER], uint32_t& vm) {
+    uint32_t mx = 0;
+    // Returns whether the tile is partial; a partial tile's maximum is taken
+    // here (over its real ids), a full tile's in the main loop, after the
+    // prefetched loads have landed.
+    auto load_ids = [&](uint32_t tl, uint32_t (&w)[TS_PER]) -> bool {
         const uint64_t base = static_cast<uint64_t>(tl) * TILE;
         const uint64_t hi = min(g.n, base + TILE);
-        vm = 0;
         if (g.vec && hi - base == TILE) {
             const uint4* src = reinterpret_cast<const uint4*>(ids + base);
 #pragma unroll
@@ -96,111 +102,102 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
                 const uint4 a = ld_stream(src + t + q * TS_NT);
                 w[4 * q + 0] = a.x, w[4 * q + 1] = a.y, w[4 * q + 2] = a.z, w[4 * q + 3] = a.w;
             }
-            vm = ~0u;
+            return false;
         } else {
             const uint32_t* src = ids + base;  // wave-uniform base, 32-bit lane offsets
             const uint32_t rem = static_cast<uint32_t>(hi - base);
 #pragma unroll
             for (uint32_t j = 0; j < TS_PER; ++j) {
                 const uint32_t i = t + j * TS_NT;
-                w[j] = i < rem ? src[i] : 0u;
-                vm |= (i < rem ? 1u : 0u) << j;
+                if (i < rem) {
+                    w[j] = src[i];
+                    if (rem < TILE) mx = max(mx, w[j]);
+                } else {
+                    // Padding of a partial last tile: 0xFFFFFFFF falls in the
+                    // sentinel bucket; with 65536 keys there is none, and the
+                    // pads repeat the tile's own ids, spread like the tile.
+                    w[j] = NB < MAX_BUCKETS ? 0xFFFFFFFFu : src[i % rem];
+                }
             }
+            return rem < TILE;
         }
     };
     // The next tile's ids are loaded while the current tile is ranked,
     // scanned, scattered and written.
-    uint32_t v[TS_PER], valid = 0;
+    uint32_t v[TS_PER];
+    bool partial = false;
     // Workgroup g takes blocks g, g + G, ...; `next` steps through them.
     auto next = [&](uint32_t tl) { return (tl % TB != TB - 1) ? tl + 1 : tl + 1 + (g.G - 1) * TB; };
+    auto bucket = [&](uint32_t x) { return min(x >> (16 + BK_SHIFT), NB); };
     const uint32_t first = blockIdx.x * TB;
-    if (first < g.n_tiles) load_ids(first, v, valid);
+    if (first < g.n_tiles) partial = load_ids(first, v);
     for (uint32_t tile = first; tile < g.n_tiles; tile = next(tile)) {
         const uint64_t base = static_cast<uint64_t>(tile) * TILE;
-        for (uint32_t i = t; i <= g.NB; i += TS_NT) cnt[i] = 0;
+        for (uint32_t i = t; i <= NB; i += TS_NT) cnt[i] = 0;
         __syncthreads();
+        if (!partial) {
 #pragma unroll
-        for (uint32_t j = 0; j < TS_PER; ++j) {
-            if ((valid >> j) & 1u) {
-                mx = max(mx, v[j]);
-                if ((v[j] >> 16) > max_key) {
-                    err = 1;
-                    valid &= ~(1u << j);
-                }
-            }
+            for (uint32_t j = 0; j < TS_PER; ++j) mx = max(mx, v[j]);
         }
         // Ranks within the tile.  When every id of the wave's pass falls in
         // one bucket (clustered ids), a single atomic reserves them all.
         uint32_t rk[TS_PER / 2];  // tile ranks (< 16384) packed two per register
-        const uint32_t b00 = __builtin_amdgcn_readfirstlane(v[0] >> (16 + BK_SHIFT));
+        const uint32_t b00 = __builtin_amdgcn_readfirstlane(bucket(v[0]));
         bool diff = false;
 #pragma unroll
-        for (uint32_t j = 0; j < TS_PER; ++j) diff |= ((valid >> j) & 1u) && (v[j] >> (16 + BK_SHIFT)) != b00;
+        for (uint32_t j = 0; j < TS_PER; ++j) diff |= bucket(v[j]) != b00;
         if (__ballot(diff) == 0) {
-            uint32_t count = 0;
-#pragma unroll
-            for (uint32_t j = 0; j < TS_PER; ++j) count += static_cast<uint32_t>(__popcll(__ballot((valid >> j) & 1u)));
             uint32_t r0 = 0;
-            if (lane == 0 && count) r0 = atomicAdd(&cnt[b00], count);
-            uint32_t run = __builtin_amdgcn_readfirstlane(r0);
+            if (lane == 0) r0 = atomicAdd(&cnt[b00], 64u * TS_PER);
+            const uint32_t run = __builtin_amdgcn_readfirstlane(r0) + lane;
 #pragma unroll
-            for (uint32_t j = 0; j < TS_PER; ++j) {
-                const uint64_t m = __ballot((valid >> j) & 1u);
-                const uint32_t r = run + lanes_below(m);
-                run += static_cast<uint32_t>(__popcll(m));
-                if (j & 1u)
-                    rk[j >> 1] |= r << 16;
-                else
-                    rk[j >> 1] = r;
-            }
+            for (uint32_t j = 0; j < TS_PER; j += 2) rk[j >> 1] = (run + 64u * j) | ((run + 64u * (j + 1)) << 16);
         } else {
 #pragma unroll
             for (uint32_t j = 0; j < TS_PER; ++j) {
-                const uint32_t r = ((valid >> j) & 1u) ? atomicAdd(&cnt[v[j] >> (16 + BK_SHIFT)], 1u) : 0u;
+                const uint32_t r = atomicAdd(&cnt[bucket(v[j])], 1u);
                 if (j & 1u)
                     rk[j >> 1] |= r << 16;
                 else
                     rk[j >> 1] = r;
             }
         }
-#pragma unroll
-        for (uint32_t j = 0; j < TS_PER; ++j)
-            if ((valid >> j) & 1u) atomicOr(&pres[v[j] >> 21], 1u << ((v[j] >> 16) & 31u));
-        uint32_t vn[TS_PER], validn = 0;
-        if (next(tile) < g.n_tiles) load_ids(next(tile), vn, validn);
+        uint32_t vn[TS_PER];
+        bool partial_n = false;
+        if (next(tile) < g.n_tiles) partial_n = load_ids(next(tile), vn);
         __syncthreads();
         constexpr uint32_t BPT = MAX_BUCKETS / TS_NT;  // buckets scanned per thread
         uint32_t cv[BPT], cs = 0;
 #pragma unroll
         for (uint32_t q = 0; q < BPT; ++q) {
             const uint32_t bq = t * BPT + q;
-            cv[q] = bq < g.NB ? cnt[bq] : 0u;
+            cv[q] = bq < NB ? cnt[bq] : 0u;
             cs += cv[q];
         }
-        uint32_t total;
+        uint32_t total;  // ids of the real buckets; the sentinel's follow
         uint32_t st = block_excl_scan<TS_NT>(cs, lds, total);
 #pragma unroll
         for (uint32_t q = 0; q < BPT; ++q) {
             const uint32_t bq = t * BPT + q;
-            if (bq < g.NB) cnt[bq] = st;
+            if (bq < NB) cnt[bq] = st;
             st += cv[q];
         }
-        if (t == 0) cnt[g.NB] = total;
+        if (t == 0) cnt[NB] = total;
         __syncthreads();
         if (staged) {
             uint16_t* sc = reinterpret_cast<uint16_t*>(stage) + tile % TB;
-            for (uint32_t i = t; i <= g.NB; i += TS_NT) sc[i * TB] = static_cast<uint16_t>(cnt[i]);
+            for (uint32_t i = t; i <= NB; i += TS_NT) sc[i * TB] = static_cast<uint16_t>(cnt[i]);
         } else {
-            uint16_t* tcol = tab + static_cast<uint64_t>(tile / TB) * (g.NB + 1) * TB + tile % TB;
-            for (uint32_t i = t; i <= g.NB; i += TS_NT) tcol[static_cast<uint64_t>(i) * TB] = static_cast<uint16_t>(cnt[i]);
+            uint16_t* tcol = tab + static_cast<uint64_t>(tile / TB) * (NB + 1) * TB + tile % TB;
+            for (uint32_t i = t; i <= NB; i += TS_NT) tcol[static_cast<uint64_t>(i) * TB] = static_cast<uint16_t>(cnt[i]);
         }
 #pragma unroll
         for (uint32_t j = 0; j < TS_PER; ++j)
-            if ((valid >> j) & 1u) buf[cnt[v[j] >> (16 + BK_SHIFT)] + ((rk[j >> 1] >> ((j & 1u) * 16)) & 0xFFFFu)] = v[j];
+            buf[cnt[bucket(v[j])] + ((rk[j >> 1] >> ((j & 1u) * 16)) & 0xFFFFu)] = v[j];
         __syncthreads();
         if (staged && (tile % TB == TB - 1 || tile + 1 == g.n_tiles)) {  // the block's rows, contiguous
-            uint4* trow = reinterpret_cast<uint4*>(tab + static_cast<uint64_t>(tile / TB) * (g.NB + 1) * TB);
-            for (uint32_t i = t; i <= g.NB; i += TS_NT) trow[i] = stage[i];
+            uint4* trow = reinterpret_cast<uint4*>(tab + static_cast<uint64_t>(tile / TB) * (NB + 1) * TB);
+            for (uint32_t i = t; i <= NB; i += TS_NT) trow[i] = stage[i];
         }
         uint32_t* dst = part + base;
         const uint32_t n4 = total >> 2;
@@ -208,72 +205,36 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         for (uint32_t p = 4 * n4 + t; p < total; p += TS_NT) dst[p] = buf[p];
 #pragma unroll
         for (uint32_t j = 0; j < TS_PER; ++j) v[j] = vn[j];
-        valid = validn;
+        partial = partial_n;
     }
-    if (err) atomicOr(&s_err, 1u);
-    atomicMax(&s_max, mx);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(mx, o, 64)));
+    if (lane == 0) atomicMax(&s_max, mx);
     __syncthreads();
-    uint32_t* op = gpres + static_cast<uint64_t>(blockIdx.x) * g.NW;
-    for (uint32_t i = t; i < g.NW; i += TS_NT) op[i] = pres[i];
-    if (t == 0) {  // per-workgroup partials: nothing here needs zeroed memory
-        gerr[blockIdx.x] = s_err;
-        gmax[blockIdx.x] = s_max;
-    }
+    if (t == 0) gmax[blockIdx.x] = s_max;  // per-workgroup partials: nothing here needs zeroed memory
 }
 
-// Key ranks, one thread per key and one workgroup per 1024 keys.  Each
-// workgroup ORs the tile-sort workgroups' presence words up to the end of its
-// range (the 16 waves split the words and the partials), so the rank base is
-// the popcount of the words before its range.  Writes keys/types/offsets and the
-// full key_index (0xFFFF = absent); workgroup 0 also reduces the error and
-// max-id partials and zeroes the distinct count the build accumulates.
-__global__ __launch_bounds__(1024) void ids_rank(IdsGeom g, const uint32_t* gpres, const uint32_t* gerr,
-                                                 const uint32_t* gmax, uint16_t* keys, uint8_t* types,
-                                                 uint32_t* offsets, uint16_t* key_index, IdsTotals* tot)
+// Key ranks after the build, one thread per key and one workgroup per 1024
+// keys: a key is present iff the build counted a bit in it.  The rank base
+// is the number of present keys before the workgroup's range.  Writes
+// keys/types/offsets/cards in rank order and the full key_index (0xFFFF =
+// absent), flags `moved` when a present key's rank differs from the key (the
+// build wrote container k to pool slot k), and workgroup 0 reduces the
+// max-id partials into the range error.
+__global__ __launch_bounds__(1024) void ids_rank(IdsGeom g, const uint32_t* key_count, const uint32_t* gmax,
+                                                 uint16_t* keys, uint8_t* types, uint32_t* offsets, uint16_t* cards,
+                                                 uint16_t* key_index, IdsTotals* tot)
 {
-    __shared__ uint32_t red[1024];     // per-part ORs: [part][word]
-    __shared__ uint32_t word[MAX_PWORDS];
     __shared__ uint32_t lds[16];
     const uint32_t t = threadIdx.x;
     const uint32_t w = blockIdx.x;
     const uint32_t wave = t >> 6, lane = __lane_id();
-    const uint32_t nw_need = min(g.NW, (w + 1) * 32u);  // words up to the end of this range
-    // Words in columns of 64 (one lane per word), at most 1024 words a pass;
-    // the 16 waves split the columns and the partials: wave = part * cols + column.
-    for (uint32_t base = 0; base < nw_need; base += 1024u) {
-        const uint32_t nb = min(nw_need - base, 1024u);
-        const uint32_t cols = (nb + 63) / 64, prt = 16u / cols;
-        if (wave < cols * prt) {
-            const uint32_t c = wave % cols, pi = wave / cols;
-            const uint32_t j = base + c * 64u + lane;
-            const uint32_t k0 = pi * g.G / prt, k1 = (pi + 1) * g.G / prt;
-            uint32_t acc = 0;
-            if (j < nw_need) {
-                uint32_t k = k0;
-                for (; k + 8 <= k1; k += 8) {
-                    uint32_t v8[8];
-#pragma unroll
-                    for (uint32_t q = 0; q < 8; ++q) v8[q] = gpres[static_cast<uint64_t>(k + q) * g.NW + j];
-#pragma unroll
-                    for (uint32_t q = 0; q < 8; ++q) acc |= v8[q];
-                }
-                for (; k < k1; ++k) acc |= gpres[static_cast<uint64_t>(k) * g.NW + j];
-            }
-            red[pi * (cols * 64u) + c * 64u + lane] = acc;
-        }
-        __syncthreads();
-        for (uint32_t j = t; j < nb; j += 1024u) {
-            uint32_t acc = 0;
-            for (uint32_t pi = 0; pi < prt; ++pi) acc |= red[pi * (cols * 64u) + j];
-            word[base + j] = acc;
-        }
-        __syncthreads();
-    }
-    uint32_t before = 0;  // present keys below this workgroup's range (32 words per 1024 keys)
-    for (uint32_t j = t; j < w * 32u; j += 1024u) before += __popc(word[j]);
+    uint32_t before = 0;
+    for (uint32_t j = t; j < w * 1024u; j += 1024u) before += key_count[j] != 0u ? 1u : 0u;
     before = block_sum<1024>(before, lds);
     const uint32_t key = w * 1024u + t;
-    const bool present = key < g.K && ((word[key >> 5] >> (key & 31u)) & 1u);
+    const uint32_t c = key < g.K ? key_count[key] : 0u;
+    const bool present = c != 0;
     uint32_t here;
     const uint32_t rank = before + block_excl_scan<1024>(present ? 1u : 0u, lds, here);
     if (key < g.K) key_index[key] = present ? static_cast<uint16_t>(rank) : static_cast<uint16_t>(0xFFFFu);
@@ -281,34 +242,47 @@ __global__ __launch_bounds__(1024) void ids_rank(IdsGeom g, const uint32_t* gpre
         keys[rank] = static_cast<uint16_t>(key);
         types[rank] = CR_BITMAP;
         offsets[rank] = rank * 8192u;
+        cards[rank] = static_cast<uint16_t>(c > 65535u ? 0u : c);  // 65536 stored as 0
     }
+    if (__ballot(present && rank != key) != 0ull && lane == 0) atomicOr(&tot->moved, 1u);
     if (t == 0 && w == gridDim.x - 1) tot->n_containers = before + here;
     if (w == 0 && wave == 0) {
-        uint32_t e = 0, m = 0;
-        for (uint32_t k = lane; k < g.G; k += 64) {
-            e |= gerr[k];
-            m = max(m, gmax[k]);
-        }
+        uint32_t m = 0;
+        for (uint32_t k = lane; k < g.G; k += 64) m = max(m, gmax[k]);
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            e |= __shfl_xor(e, o, 64);
-            m = max(m, static_cast<uint32_t>(__shfl_xor(m, o, 64)));
-        }
+        for (int o = 32; o > 0; o >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(m, o, 64)));
         if (lane == 0) {
-            tot->err = e;
             tot->max_id = m;
-            tot->total = 0;
+            tot->err = (m >> 16) > g.K - 1u ? 1u : 0u;
         }
     }
+}
+
+// Pool compaction when present keys are not a prefix: container i moves from
+// slot keys[i] of the key-addressed pool to slot i.  One wave per container.
+__global__ __launch_bounds__(256) void ids_gather_pool(const uint16_t* keys, uint32_t n_c,
+                                                       const uint64_t* __restrict__ src, uint64_t* __restrict__ dst)
+{
+    const uint32_t i = (blockIdx.x * 256u + threadIdx.x) >> 6;
+    const uint32_t lane = __lane_id();
+    if (i >= n_c) return;
+    const uint4* s4 = reinterpret_cast<const uint4*>(src + static_cast<uint64_t>(keys[i]) * 1024u);
+    uint4* d4 = reinterpret_cast<uint4*>(dst + static_cast<uint64_t>(i) * 1024u);
+    uint4 x[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x[k] = ld_stream(s4 + lane + 64 * k);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) st_stream(d4 + lane + 64 * k, x[k]);
 }
 
 // One workgroup per bucket: its 16 containers as 16 x 2048 u32 LDS words
 // (128 KiB), filled from the bucket's run in every tile.  Eight adjacent
 // buckets are dispatched to the same XCD (blocks go round-robin over the 8
 // XCDs), so the cache lines their runs share at run boundaries are L2 hits.
-// Normal mode writes the stored containers of present keys and each key's
-// distinct count; complement mode writes ~bits masked to [0, U) for keys whose
-// complement is non-empty.
+// Normal mode writes each present key's container to pool slot `key` (the
+// ranks come after) and every key's distinct count; complement mode writes
+// ~bits masked to [0, U) at the key_index rank of keys whose complement is
+// non-empty, with their cards.
 constexpr int BUILD_NT = 1024;
 constexpr uint32_t BUILD_WAVES = BUILD_NT / 64;
 
@@ -423,13 +397,13 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
             pc += __popc(w);
         }
         pc = wave_sum(pc);
-        if (!complement && key_count && lane == 0) key_count[key] = pc;
+        if (!complement && lane == 0) key_count[key] = pc;
         if (pc != 0) {
-            const uint32_t rank = key_index[key];
-            uint4* dst = reinterpret_cast<uint4*>(pool + static_cast<uint64_t>(rank) * 1024u);
+            const uint32_t slot = complement ? key_index[key] : key;
+            uint4* dst = reinterpret_cast<uint4*>(pool + static_cast<uint64_t>(slot) * 1024u);
             const uint4* src = reinterpret_cast<const uint4*>(cb);
             for (uint32_t i = lane; i < 512u; i += 64) st_stream(dst + i, src[i]);
-            if (lane == 0) cards[rank] = static_cast<uint16_t>(pc > 65535u ? 0u : pc);
+            if (complement && lane == 0) cards[slot] = static_cast<uint16_t>(pc > 65535u ? 0u : pc);
         }
     }
     if (lane == 0) wave_pc[c] = pc;
@@ -727,45 +701,44 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     g.vec = (reinterpret_cast<uintptr_t>(d_ids) & 15u) == 0;
 
     Carver c;
-    const size_t o_gpres = c.add(sizeof(uint32_t) * static_cast<uint64_t>(g.G) * g.NW);
-    const size_t o_gerr = c.add(sizeof(uint32_t) * g.G);
     const size_t o_gmax = c.add(sizeof(uint32_t) * g.G);
     const size_t o_kc = c.add(sizeof(uint32_t) * g.K);
     const size_t o_tot = c.add(sizeof(IdsTotals));
     const size_t o_tab =
         c.add(sizeof(uint16_t) * static_cast<uint64_t>((g.n_tiles + TB - 1) / TB) * TB * (g.NB + 1));
-    const size_t o_part = c.add(sizeof(uint32_t) * (static_cast<uint64_t>(n) + 4));  // + window overrun
+    // Whole tiles (a partial last tile is padded) + the build's window overrun.
+    const size_t o_part = c.add(sizeof(uint32_t) * (static_cast<uint64_t>(g.n_tiles) * TILE + 4));
     Scratch sc;
     CR_RET(sc.alloc(c.total, s));
-    uint32_t* gpres = sc.at<uint32_t>(o_gpres);
-    uint32_t* gerr = sc.at<uint32_t>(o_gerr);
     uint32_t* gmax = sc.at<uint32_t>(o_gmax);
     uint32_t* key_count = sc.at<uint32_t>(o_kc);
     IdsTotals* tot = sc.at<IdsTotals>(o_tot);
     uint16_t* tab = sc.at<uint16_t>(o_tab);
     uint32_t* part = sc.at<uint32_t>(o_part);
 
-    // Containers <= min(keys, ids): the pool is sized by that bound.
+    // Containers <= min(keys, ids) bounds the metadata; the pool is addressed
+    // by key (slot k holds key k's container) until the ranks are known.
     const uint64_t bound = std::min<uint64_t>(g.K, n);
-    const OutLayout L = plan_out(bound, g.K, bound * 1024u, 0, 0);
-    CR_RET(alloc_out(out, L, bound, g.K, bound * 1024u, 0, 0, s));
+    const uint64_t pool_words = static_cast<uint64_t>(g.K) * 1024u;
+    const OutLayout L = plan_out(bound, g.K, pool_words, 0, 0);
+    CR_RET(alloc_out(out, L, bound, g.K, pool_words, 0, 0, s));
     out->max_key = max_key32;
 
     {
         CR_TIMED("ids_tile_sort", s);
-        ids_tile_sort<<<g.G, TS_NT, 0, s>>>(d_ids, g, part, tab, gpres, gerr, gmax);
-    }
-    CR_LAUNCH_CHECK();
-    {
-        CR_TIMED("ids_rank", s);
-        ids_rank<<<(g.K + 1023) / 1024, 1024, 0, s>>>(g, gpres, gerr, gmax, out->keys, out->types, out->offsets,
-                                                      out->key_index, tot);
+        ids_tile_sort<<<g.G, TS_NT, 0, s>>>(d_ids, g, part, tab, gmax, tot);
     }
     CR_LAUNCH_CHECK();
     {
         CR_TIMED("ids_build", s);
-        ids_build<<<build_grid(g.NB), BUILD_NT, 0, s>>>(part, tab, g, universe, false, out->key_index,
-                                                        out->bitmap_data, out->cardinalities, key_count, tot);
+        ids_build<<<build_grid(g.NB), BUILD_NT, 0, s>>>(part, tab, g, universe, false, nullptr, out->bitmap_data,
+                                                        nullptr, key_count, tot);
+    }
+    CR_LAUNCH_CHECK();
+    {
+        CR_TIMED("ids_rank", s);
+        ids_rank<<<(g.K + 1023) / 1024, 1024, 0, s>>>(g, key_count, gmax, out->keys, out->types, out->offsets,
+                                                      out->cardinalities, out->key_index, tot);
     }
     CR_LAUNCH_CHECK();
     IdsTotals h{};
@@ -780,6 +753,37 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     out->total_cardinality = h.total;
     out->n_containers = h.n_containers;
     out->n_bitmap_containers = h.n_containers;
+    if (h.total <= static_cast<uint64_t>(universe) / 2u) {  // strict (:359)
+        if (!h.moved) return CR_OK;
+        // Present keys are not a prefix: a block of n_containers slots takes
+        // the metadata and the containers in rank order.
+        const uint64_t nc = h.n_containers;
+        cr_gpu_roaring dense;
+        reset(&dense);
+        const OutLayout L3 = plan_out(nc, g.K, nc * 1024u, 0, 0);
+        CR_RET(alloc_out(&dense, L3, nc, g.K, nc * 1024u, 0, 0, s));
+        CopyList cl{};
+        cl.seg[cl.n++] = {out->keys, dense.keys, nc * 2u};
+        cl.seg[cl.n++] = {out->types, dense.types, nc};
+        cl.seg[cl.n++] = {out->offsets, dense.offsets, nc * 4u};
+        cl.seg[cl.n++] = {out->cardinalities, dense.cardinalities, nc * 2u};
+        cl.seg[cl.n++] = {out->key_index, dense.key_index, static_cast<uint64_t>(g.K) * 2u};
+        {
+            CR_TIMED("ids_compact", s);
+            CR_RET(copy_segments(cl, s));
+            ids_gather_pool<<<static_cast<uint32_t>((nc + 3) / 4), 256, 0, s>>>(out->keys, static_cast<uint32_t>(nc),
+                                                                                out->bitmap_data, dense.bitmap_data);
+        }
+        CR_LAUNCH_CHECK();
+        dense.universe_size = universe;
+        dense.max_key = max_key32;
+        dense.total_cardinality = h.total;
+        dense.n_containers = h.n_containers;
+        dense.n_bitmap_containers = h.n_containers;
+        free_async(out, s);
+        *out = dense;
+        return sync_stream(s);
+    }
     if (h.total <= static_cast<uint64_t>(universe) / 2u) return CR_OK;  // strict (:359)
 
     // Complement path (:361-410): ids must lie in [0, U).

@@ -125,6 +125,35 @@ def test_upload_from_ids_rejects_out_of_universe_keys(gpu):
     assert e.value.code == 2
 
 
+@pytest.mark.parametrize("bad_key", [25, 40, 0xFFFF])
+def test_upload_from_ids_rejects_keys_past_the_last_bucket(gpu, bad_key):
+    """20 keys = 2 buckets of 16: key 25 lies in the last bucket but past max_key,
+    keys 40 and 0xFFFF lie past the last bucket.  One such id fails the call."""
+    _say("upload_from_ids invalid key", bad_key)
+    ids = np.arange(50000, dtype=np.uint32) * 7 % (20 * 65536)
+    ids[12345] = (bad_key << 16) | 7
+    with pytest.raises(gpu.CrError) as e:
+        gpu.upload_from_device_ids(_dev_u32(ids), 20 * 65536)
+    assert e.value.code == 2
+
+
+@pytest.mark.parametrize("n", [16384 * 3 + 5, 16384 * 9])
+def test_upload_from_ids_unaligned_pointer(gpu, n):
+    """A device pointer 4 bytes past a 16-byte boundary takes the scalar load
+    path, with and without a partial last tile."""
+    _say("upload_from_ids unaligned", n)
+    rng = np.random.default_rng(n)
+    U = 1 << 24
+    ids = rng.integers(0, U, n + 1, dtype=np.uint64).astype(np.uint32)
+    d = _dev_u32(ids)
+    view = d[1:]
+    assert view.data_ptr() % 16 == 4
+    want = orc.upload_from_ids(ids[1:], U)
+    g = gpu.upload_from_device_ids(view, U)
+    assert_same(gpu.download(g), want, strict=True, what="unaligned")
+    gpu.free(g)
+
+
 # ---- bitset uploads ----------------------------------------------------------
 BITSET_CASES = [(100000, 0.1, 1), (100000, 0.9, 2), (200000, 1 / 3, 3), (5 * 65536 + 123, 0.001, 4),
                 (5 * 65536 + 123, 0.95, 5), (1 << 22, 0.5, 6), (1 << 22, 0.55, 7), (64, 1.0, 8), (96, 0.0, 9)]
