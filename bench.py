@@ -76,7 +76,7 @@ def upload_kernel_bytes(name, n, n_c, max_key):
     """Algorithmic bytes per launch of each upload kernel."""
     return {
         "ids_tile_sort": 8 * n,                     # read every id, write it back bucket-sorted within its tile
-        "ids_build": 4 * n + 8192 * n_c + 2 * n_c,  # read the sorted ids, write containers + cards
+        "ids_build": 4 * n + 8192 * n_c + 4 * n_c,  # read the sorted ids, write containers + per-key counts
     }.get(name)
 
 
@@ -319,6 +319,8 @@ def batch_api(torch, cr, flush):
                             "note": "host containers packed into pinned memory, one host-to-device copy"}}
     T = B.total_containers
     kept = []
+    cr.free_batch(cr.promote_batch(B))  # first launch (code object load) stays out of the timing
+    torch.cuda.synchronize()
     cr.timing_enable(True)
     t = cold_time(torch, lambda: kept.append(cr.promote_batch(B)), 5, flush)
     rep = cr.timing_report()
@@ -343,6 +345,8 @@ def batch_api(torch, cr, flush):
         res[name] = dict(_kernel_line(rep, "bt_and", nbytes, t), n_common=n_common)
     words_each = Ub // 64
     d = torch.zeros(16 * words_each, dtype=torch.int64, device="cuda")
+    cr.batch_decompress(B, d, words_each)  # first launch stays out of the timing
+    torch.cuda.synchronize()
     cr.timing_enable(True)
     t = cold_time(torch, lambda: cr.batch_decompress(B, d, words_each), 5, flush)
     rep = cr.timing_report()
