@@ -54,7 +54,6 @@ struct IdsGeom {
     uint32_t G;   // tile-sort workgroups
     uint32_t K;   // keys in the universe (max_key + 1)
     uint32_t NB;  // buckets
-    uint32_t NW;  // presence words
     bool vec;     // ids pointer 16-byte aligned
 };
 
@@ -695,7 +694,6 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     g.n = n;
     g.K = max_key32 + 1u;
     g.NB = (g.K + BK_KEYS - 1) / BK_KEYS;
-    g.NW = (g.K + 31) / 32;
     g.n_tiles = static_cast<uint32_t>((static_cast<uint64_t>(n) + TILE - 1) / TILE);
     g.G = std::max<uint32_t>(1, std::min<uint32_t>(num_cus(), (g.n_tiles + TB - 1) / TB));  // blocks of TB tiles
     g.vec = (reinterpret_cast<uintptr_t>(d_ids) & 15u) == 0;
