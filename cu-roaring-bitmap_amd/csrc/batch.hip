@@ -758,14 +758,23 @@ extern "C" int cr_batch_multi_and(const cr_roaring_batch* batch, const uint32_t*
                 bt_and<<<an, CV_NT, 0, s>>>(*batch, d_idx, n_inputs, a0, flags, pos, o);
             }
         }
-        hipError_t e = hipGetLastError();
-        if (e == hipSuccess) e = hipMemcpyAsync(&n_common, n_common_d, 4, hipMemcpyDeviceToHost, s);
-        if (e == hipSuccess) e = hipMemcpyAsync(&tot, total, 8, hipMemcpyDeviceToHost, s);
-        if (e != hipSuccess) {
-            set_error("cr_batch_multi_and: %s", hipGetErrorString(e));
-            rc = CR_ERR_HIP;
-        } else {
-            rc = sync_stream(s);
+        HostSlotGuard hs;  // both totals come back through one pinned slot
+        rc = hs.acquire();
+        if (rc == CR_OK) {
+            char* hp = static_cast<char*>(hs.slot.host);
+            hipError_t e = hipGetLastError();
+            if (e == hipSuccess) e = hipMemcpyAsync(hp, total, 8, hipMemcpyDeviceToHost, s);
+            if (e == hipSuccess) e = hipMemcpyAsync(hp + 8, n_common_d, 4, hipMemcpyDeviceToHost, s);
+            if (e != hipSuccess) {
+                set_error("cr_batch_multi_and: %s", hipGetErrorString(e));
+                rc = CR_ERR_HIP;
+            } else {
+                rc = sync_stream(s);
+            }
+            if (rc == CR_OK) {
+                std::memcpy(&tot, hp, 8);
+                std::memcpy(&n_common, hp + 8, 4);
+            }
         }
     }
     if (rc != CR_OK) {

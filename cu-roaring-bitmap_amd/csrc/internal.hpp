@@ -42,6 +42,34 @@ int dev_free(void* p, hipStream_t s);
 // hipStreamSynchronize, timed as the host phase "sync".
 int sync_stream(hipStream_t s);
 
+// A 256-byte slot of pinned host memory that kernels write with ordinary
+// stores (system-coherent); the host reads it after the stream sync.  The guard
+// returns the slot to the library's pool.
+constexpr size_t HOST_SLOT_BYTES = 256;
+struct HostSlot {
+    void* host = nullptr;
+    void* dev = nullptr;
+    uint32_t id = 0;
+};
+int host_slot_acquire(HostSlot* out);
+void host_slot_release(HostSlot* slot);
+struct HostSlotGuard {
+    HostSlot slot;
+    HostSlotGuard() = default;
+    HostSlotGuard(const HostSlotGuard&) = delete;
+    HostSlotGuard& operator=(const HostSlotGuard&) = delete;
+    ~HostSlotGuard() { host_slot_release(&slot); }
+    int acquire() { return host_slot_acquire(&slot); }
+    template <class T>
+    T* dev() const { return static_cast<T*>(slot.dev); }
+    template <class T>
+    const volatile T* host() const { return static_cast<const volatile T*>(slot.host); }
+};
+
+// Copies `bytes` (<= HOST_SLOT_BYTES through a pinned slot) from device
+// memory once the stream reaches this point, then synchronises the stream.
+int read_back(void* host, const void* dev, size_t bytes, hipStream_t s);
+
 // Scratch that is released (stream-ordered) when the guard leaves scope.
 struct Scratch {
     void* ptr = nullptr;

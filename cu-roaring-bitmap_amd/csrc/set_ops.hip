@@ -676,8 +676,7 @@ int set_operation_impl(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_
     }
     CR_LAUNCH_CHECK();
     Totals h{};
-    CR_HIP_RET(hipMemcpyAsync(&h, tot, sizeof(Totals), hipMemcpyDeviceToHost, s));
-    CR_RET(sync_stream(s));
+    CR_RET(read_back(&h, tot, sizeof(Totals), s));
     const uint32_t n_items = h.c[C_ITEM];
     if (n_items == 0) return CR_OK;
 
@@ -742,8 +741,7 @@ int set_operation_impl(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_
     }
     CR_LAUNCH_CHECK();
     uint32_t n_out = 0;
-    CR_HIP_RET(hipMemcpyAsync(&n_out, &tot->n_out, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
-    CR_RET(sync_stream(s));
+    CR_RET(read_back(&n_out, &tot->n_out, sizeof(uint32_t), s));
     out->n_containers = n_out;
     // total_cardinality, key_index and max_key stay 0/null (src/set_ops.cu:1162-1175).
     return CR_OK;
@@ -981,8 +979,7 @@ static int fused_multi_and(const cr_gpu_roaring* in, uint32_t count, hipStream_t
     CR_LAUNCH_CHECK();
     CR_RET(fill_u32(cnt + 1, 0u, 1, s));
     uint32_t n_common = 0;
-    CR_HIP_RET(hipMemcpyAsync(&n_common, cnt, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
-    CR_RET(sync_stream(s));
+    CR_RET(read_back(&n_common, cnt, sizeof(uint32_t), s));
     out->n_containers = n_common;
     out->n_bitmap_containers = n_common;
     if (n_common == 0) return CR_OK;  // src/set_ops.cu:1579-1583
@@ -1002,8 +999,7 @@ static int fused_multi_and(const cr_gpu_roaring* in, uint32_t count, hipStream_t
     }
     CR_LAUNCH_CHECK();
     uint32_t total = 0;
-    CR_HIP_RET(hipMemcpyAsync(&total, cnt + 1, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
-    CR_RET(sync_stream(s));
+    CR_RET(read_back(&total, cnt + 1, sizeof(uint32_t), s));
     out->total_cardinality = total;
     return CR_OK;
 }

@@ -238,8 +238,7 @@ int upload_from_device_bitset_impl(const uint32_t* d_words, uint32_t n_words, ui
     }
     CR_LAUNCH_CHECK();
     BsTotals h{};
-    CR_HIP_RET(hipMemcpyAsync(&h, tot, sizeof(h), hipMemcpyDeviceToHost, s));
-    CR_RET(sync_stream(s));
+    CR_RET(read_back(&h, tot, sizeof(h), s));
     out->negated = h.negated != 0;
     out->total_cardinality = h.total;  // logical count either way (:740)
     out->n_containers = h.n_containers;

@@ -213,47 +213,111 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
     if (t == 0) gmax[blockIdx.x] = s_max;  // per-workgroup partials: nothing here needs zeroed memory
 }
 
-// Key ranks after the build, one thread per key and one workgroup per 1024
-// keys: a key is present iff the build counted a bit in it.  The rank base
-// is the number of present keys before the workgroup's range.  Writes
-// keys/types/offsets/cards in rank order and the full key_index (0xFFFF =
-// absent), flags `moved` when a present key's rank differs from the key (the
-// build wrote container k to pool slot k), and workgroup 0 reduces the
-// max-id partials into the range error.
+// Key ranks after the build, in one workgroup.  Round j covers keys
+// [1024 j, 1024 j + 1024), one per thread, with coalesced loads (eight rounds
+// in flight); a key is present iff the build counted a bit in it.  Ranks come
+// from per-wave ballots: each wave's count per round goes to LDS, one pass
+// turns them into wave and round bases, and a second pass over the rounds
+// writes keys/types/offsets/cards in rank order and the full key_index
+// (0xFFFF = absent).  The totals -- container count, the range error (from the
+// tile-sort workgroups' maximum ids), the distinct count the build accumulated,
+// and `moved` when a present key's rank differs from the key (the build wrote
+// container k to pool slot k) -- go to `tot` and to the caller's pinned host
+// slot.
+constexpr uint32_t RANK_ROUNDS = 65536 / 1024;
+
 __global__ __launch_bounds__(1024) void ids_rank(IdsGeom g, const uint32_t* key_count, const uint32_t* gmax,
                                                  uint16_t* keys, uint8_t* types, uint32_t* offsets, uint16_t* cards,
-                                                 uint16_t* key_index, IdsTotals* tot)
+                                                 uint16_t* key_index, IdsTotals* tot, IdsTotals* host)
 {
-    __shared__ uint32_t lds[16];
-    const uint32_t t = threadIdx.x;
-    const uint32_t w = blockIdx.x;
-    const uint32_t wave = t >> 6, lane = __lane_id();
-    uint32_t before = 0;
-    for (uint32_t j = t; j < w * 1024u; j += 1024u) before += key_count[j] != 0u ? 1u : 0u;
-    before = block_sum<1024>(before, lds);
-    const uint32_t key = w * 1024u + t;
-    const uint32_t c = key < g.K ? key_count[key] : 0u;
-    const bool present = c != 0;
-    uint32_t here;
-    const uint32_t rank = before + block_excl_scan<1024>(present ? 1u : 0u, lds, here);
-    if (key < g.K) key_index[key] = present ? static_cast<uint16_t>(rank) : static_cast<uint16_t>(0xFFFFu);
-    if (present) {
-        keys[rank] = static_cast<uint16_t>(key);
-        types[rank] = CR_BITMAP;
-        offsets[rank] = rank * 8192u;
-        cards[rank] = static_cast<uint16_t>(c > 65535u ? 0u : c);  // 65536 stored as 0
-    }
-    if (__ballot(present && rank != key) != 0ull && lane == 0) atomicOr(&tot->moved, 1u);
-    if (t == 0 && w == gridDim.x - 1) tot->n_containers = before + here;
-    if (w == 0 && wave == 0) {
-        uint32_t m = 0;
-        for (uint32_t k = lane; k < g.G; k += 64) m = max(m, gmax[k]);
+    __shared__ uint32_t wcnt[RANK_ROUNDS][16];  // present keys per (round, wave), then the wave's base
+    __shared__ uint32_t rbase[RANK_ROUNDS + 1];
+    __shared__ uint32_t s_max;
+    const uint32_t t = threadIdx.x, wave = t >> 6, lane = __lane_id();
+    const uint32_t rounds = (g.K + 1023u) / 1024u;
+    if (t == 0) s_max = 0;
+    uint64_t mine = 0;  // bit j: this thread's key of round j is present
+    for (uint32_t j0 = 0; j0 < rounds; j0 += 8) {
+        uint32_t c[8];
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(m, o, 64)));
-        if (lane == 0) {
-            tot->max_id = m;
-            tot->err = (m >> 16) > g.K - 1u ? 1u : 0u;
+        for (uint32_t q = 0; q < 8; ++q) {
+            const uint32_t k = (j0 + q) * 1024u + t;
+            c[q] = (j0 + q < rounds && k < g.K) ? key_count[k] : 0u;
         }
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) {
+            if (j0 + q >= rounds) break;
+            const uint64_t m = __ballot(c[q] != 0u);
+            if (c[q] != 0u) mine |= 1ull << (j0 + q);
+            if (lane == 0) wcnt[j0 + q][wave] = static_cast<uint32_t>(__popcll(m));
+        }
+    }
+    uint32_t mx = 0;
+    for (uint32_t k = t; k < g.G; k += 1024u) mx = max(mx, gmax[k]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(mx, o, 64)));
+    __syncthreads();  // s_max is initialised
+    if (lane == 0) atomicMax(&s_max, mx);
+    // Thread j (< rounds) sums round j; one wave scans the rounds; thread
+    // (round, wave) turns its count into the wave's base within the round.
+    uint32_t wprefix = 0, rtotal = 0;
+    if (t < rounds * 16u) {
+        const uint32_t j = t >> 4, w = t & 15u;
+        for (uint32_t v = 0; v < w; ++v) wprefix += wcnt[j][v];
+        if (w == 15u) rtotal = wprefix + wcnt[j][15];
+    }
+    __syncthreads();
+    if (t < rounds * 16u) {
+        wcnt[t >> 4][t & 15u] = wprefix;
+        if ((t & 15u) == 15u) rbase[(t >> 4) + 1] = rtotal;
+    }
+    if (t == 0) rbase[0] = 0;
+    __syncthreads();
+    if (t == 0)
+        for (uint32_t j = 1; j <= rounds; ++j) rbase[j] += rbase[j - 1];
+    __syncthreads();
+    bool moved = false;
+    for (uint32_t j0 = 0; j0 < rounds; j0 += 8) {
+        uint32_t c[8];  // the counts again (cache hits), eight rounds in flight
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) c[q] = ((mine >> (j0 + q)) & 1ull) ? key_count[(j0 + q) * 1024u + t] : 0u;
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) {
+            const uint32_t j = j0 + q;
+            if (j >= rounds) break;
+            const uint32_t k = j * 1024u + t;
+            const bool present = (mine >> j) & 1ull;
+            const uint64_t m = __ballot(present);
+            if (present) {
+                const uint32_t rank =
+                    rbase[j] + wcnt[j][wave] + static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull)));
+                keys[rank] = static_cast<uint16_t>(k);
+                types[rank] = CR_BITMAP;
+                offsets[rank] = rank * 8192u;
+                cards[rank] = static_cast<uint16_t>(c[q] > 65535u ? 0u : c[q]);  // 65536 stored as 0
+                key_index[k] = static_cast<uint16_t>(rank);
+                moved |= rank != k;
+            } else if (k < g.K) {
+                key_index[k] = 0xFFFFu;
+            }
+        }
+    }
+    const bool any_moved = __syncthreads_or(moved) != 0;
+    if (t == 0) {
+        const uint32_t m = s_max;
+        IdsTotals r;
+        r.n_containers = rbase[rounds];
+        r.err = (m >> 16) > g.K - 1u ? 1u : 0u;
+        r.max_id = m;
+        r.moved = any_moved ? 1u : 0u;
+        r.total = tot->total;
+        *tot = r;
+        volatile IdsTotals* h = host;
+        h->n_containers = r.n_containers;
+        h->err = r.err;
+        h->max_id = r.max_id;
+        h->moved = r.moved;
+        h->total = r.total;
     }
 }
 
@@ -655,8 +719,7 @@ static int small_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, ui
     }
     CR_LAUNCH_CHECK();
     uint32_t hdr[8];
-    CR_HIP_RET(hipMemcpyAsync(hdr, plan, sizeof(hdr), hipMemcpyDeviceToHost, s));
-    CR_RET(sync_stream(s));
+    CR_RET(read_back(hdr, plan, sizeof(hdr), s));
     const uint32_t nc = hdr[1], n_bitmap = hdr[2], n_array = hdr[3], arr_elems = hdr[4];
     out->total_cardinality = hdr[5];
     out->negated = hdr[6] != 0;
@@ -733,15 +796,24 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
                                                         nullptr, key_count, tot);
     }
     CR_LAUNCH_CHECK();
+    HostSlotGuard hs;
+    CR_RET(hs.acquire());
     {
         CR_TIMED("ids_rank", s);
-        ids_rank<<<(g.K + 1023) / 1024, 1024, 0, s>>>(g, key_count, gmax, out->keys, out->types, out->offsets,
-                                                      out->cardinalities, out->key_index, tot);
+        ids_rank<<<1, 1024, 0, s>>>(g, key_count, gmax, out->keys, out->types, out->offsets, out->cardinalities,
+                                    out->key_index, tot, hs.dev<IdsTotals>());
     }
     CR_LAUNCH_CHECK();
-    IdsTotals h{};
-    CR_HIP_RET(hipMemcpyAsync(&h, tot, sizeof(h), hipMemcpyDeviceToHost, s));
     CR_RET(sync_stream(s));
+    IdsTotals h{};
+    {
+        const volatile IdsTotals* hp = hs.host<IdsTotals>();
+        h.n_containers = hp->n_containers;
+        h.err = hp->err;
+        h.max_id = hp->max_id;
+        h.moved = hp->moved;
+        h.total = hp->total;
+    }
     if (h.err) {
         free_async(out, s);
         set_error("upload_from_ids: an id's key exceeds max_key = (universe_size-1)>>16 = %u", max_key32);
@@ -807,8 +879,7 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
                                                     comp.bitmap_data, comp.cardinalities, nullptr, tot);
     }
     CR_LAUNCH_CHECK();
-    CR_HIP_RET(hipMemcpyAsync(&h, tot, sizeof(h), hipMemcpyDeviceToHost, s));
-    CR_RET(sync_stream(s));
+    CR_RET(read_back(&h, tot, sizeof(h), s));
     free_async(out, s);
     *out = comp;
     out->universe_size = universe;
