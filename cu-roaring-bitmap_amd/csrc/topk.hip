@@ -18,6 +18,7 @@
 //      top-k lists; every stored and returned distance is the direct one.
 //   3. tk_merge: one wave per query merges its chunk lists into the answer.
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 
 #include "cu_roaring/device/roaring_view.hpp"
@@ -129,7 +130,21 @@ struct TkArgs {
     uint32_t* tau;      // [n_q] bits of the smallest k-th distance any chunk has reached
     uint32_t* tau_m;    // [n_chunks][n_q] bits of each chunk's m_rank-th distance (+inf: fewer entries)
     uint32_t m_rank;    // ceil(2k / n_chunks)
+    // Small sets: with at most small_max rows the distance kernel writes every
+    // estimate (pd[q][row], lower bounds of the fp32 distances) with the scaled
+    // norms (pq[q], px[row]), and tk_select picks each query's k from them.
+    uint32_t small_max;  // 0: never
+    float* pd;           // [n_q][small_max]
+    float* pq;           // [n_q]
+    float* px;           // [small_max]
 };
+
+// Rows the distance kernel covers, and whether the small-set path takes them.
+__device__ __forceinline__ uint64_t tk_rows(const TkArgs& a) { return a.sel ? static_cast<uint64_t>(*a.n_sel) : a.n_base; }
+__device__ __forceinline__ bool tk_small(const TkArgs& a, uint64_t n_rows)
+{
+    return a.small_max != 0 && n_rows <= a.small_max;
+}
 
 // Per-wave selection state in LDS.
 struct TkWave {
@@ -321,8 +336,8 @@ __device__ __forceinline__ void tk_load_rows(const TkArgs& a, uint64_t row0, uin
     }
 }
 
-template <int DP>
-__device__ __forceinline__ void tk_store_rows(TkLds<DP>& L, int buf, const float4 (&pre)[DP / 32],
+template <int DP, class Lds>
+__device__ __forceinline__ void tk_store_rows(Lds& L, int buf, const float4 (&pre)[DP / 32],
                                               const uint32_t (&pid)[DP / 32])
 {
     constexpr int TPR = DP / 4;
@@ -369,7 +384,8 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
     const uint32_t chunk = pidx / n_qb;
     const uint32_t qb = pidx % n_qb;
 
-    const uint64_t n_rows = a.sel ? static_cast<uint64_t>(*a.n_sel) : a.n_base;
+    const uint64_t n_rows = tk_rows(a);
+    if (tk_small(a, n_rows)) return;  // tk_pairs and tk_select answer small sets
     const uint64_t rpc = ((n_rows + a.n_chunks - 1) / a.n_chunks + TK_ROWS - 1) / TK_ROWS * TK_ROWS;
     const uint64_t r0 = std::min<uint64_t>(n_rows, static_cast<uint64_t>(chunk) * rpc);
     const uint64_t r1 = std::min<uint64_t>(n_rows, r0 + rpc);
@@ -590,10 +606,11 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
 
 // ---- 3. merge of the chunk lists -------------------------------------------
 
-__global__ __launch_bounds__(TK_MERGE_NT) void tk_merge(const float* list_d, const uint32_t* list_id, size_t plane,
-                                                         const uint32_t* list_n, uint32_t n_chunks, uint32_t n_q,
-                                                         uint32_t k, float* out_d, int64_t* out_id)
+__global__ __launch_bounds__(TK_MERGE_NT) void tk_merge(TkArgs a, const float* list_d, const uint32_t* list_id,
+                                                         size_t plane, const uint32_t* list_n, uint32_t n_chunks,
+                                                         uint32_t n_q, uint32_t k, float* out_d, int64_t* out_id)
 {
+    if (tk_small(a, tk_rows(a))) return;  // tk_select answers small sets
     constexpr int W = TK_MERGE_NT / 64;
     __shared__ float ad[W][2][TK_KMAX];
     __shared__ uint32_t ai[W][2][TK_KMAX];
@@ -644,11 +661,288 @@ __global__ __launch_bounds__(TK_MERGE_NT) void tk_merge(const float* list_d, con
     }
 }
 
+// ---- 2b. small sets: every estimate ------------------------------------------
+// The distance kernel's tiles and MFMA blocks without the selection: each
+// (chunk, query block) workgroup writes the estimates of its rows for its
+// queries -- (1 - TK_GATE_ERR)(|q|^2 + |x|^2) - 2 q.x, at most the fp32
+// distance -- to pd[q][row], the scaled query norms to pq (chunk 0) and the
+// scaled row norms to px (query block 0).
+template <int DP>
+struct TkPairsLds {
+    float tile[2][TK_ROWS * (DP + 4)];
+    float xg[2][TK_ROWS];
+    uint32_t id[2][TK_ROWS];
+    float est[TK_WAVES][TK_QW * (TK_ROWS + 1)];  // a wave's 32 x 64 estimates, rows padded by one
+};
+
+template <int DP>
+__global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
+{
+    const uint64_t n_rows = tk_rows(a);
+    if (!tk_small(a, n_rows)) return;  // the list path answers
+    __shared__ TkPairsLds<DP> L;
+    const uint32_t lane = __lane_id();
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t h = lane >> 5;
+    const uint32_t j = lane & 31u;
+    const uint32_t n_qb = (a.n_q + TK_QB - 1) / TK_QB;
+    const uint32_t chunk = blockIdx.x / n_qb;
+    const uint32_t qb = blockIdx.x % n_qb;
+    const uint64_t rpc = ((n_rows + a.n_chunks - 1) / a.n_chunks + TK_ROWS - 1) / TK_ROWS * TK_ROWS;
+    const uint64_t r0 = std::min<uint64_t>(n_rows, static_cast<uint64_t>(chunk) * rpc);
+    const uint64_t r1 = std::min<uint64_t>(n_rows, r0 + rpc);
+    const uint32_t n_tiles = static_cast<uint32_t>((r1 - r0 + TK_ROWS - 1) / TK_ROWS);
+    const uint32_t q0 = qb * TK_QB + wave * TK_QW;
+    const uint32_t nq_wave = q0 < a.n_q ? std::min<uint32_t>(TK_QW, a.n_q - q0) : 0u;
+    const bool qok = j < nq_wave;
+    float qreg[DP / 2];
+    float qpart = 0.f;
+#pragma unroll
+    for (int s = 0; s < DP / 2; ++s) {
+        const uint32_t c = h * (DP / 2) + s;
+        qreg[s] = (qok && c < a.dim) ? a.queries[static_cast<size_t>(q0 + j) * a.dim + c] : 0.f;
+        qpart += qreg[s] * qreg[s];
+    }
+    const float qg = (1.f - TK_GATE_ERR) * (qpart + __shfl_xor(qpart, 32, 64));
+    if (chunk == 0 && h == 0 && qok) a.pq[q0 + j] = qg;
+    float4 pre[DP / 32];
+    uint32_t pid[DP / 32];
+    if (n_tiles > 0) {
+        tk_load_rows<DP>(a, r0, r1, pre, pid);
+        tk_store_rows<DP>(L, 0, pre, pid);
+    }
+    __syncthreads();
+    for (uint32_t t = 0; t < n_tiles; ++t) {
+        const int b = static_cast<int>(t & 1u);
+        if (t + 1 < n_tiles) tk_load_rows<DP>(a, r0 + static_cast<uint64_t>(t + 1) * TK_ROWS, r1, pre, pid);
+        if (nq_wave > 0) {
+            f32x16 acc0 = {}, acc1 = {};
+            const float* A0 = &L.tile[b][j * (DP + 4) + h * (DP / 2)];
+            const float* A1 = A0 + 32 * (DP + 4);
+#pragma unroll
+            for (int s = 0; s < DP / 2; s += 4) {
+                const float4 x0 = *reinterpret_cast<const float4*>(A0 + s);
+                const float4 x1 = *reinterpret_cast<const float4*>(A1 + s);
+                acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.x, qreg[s + 0], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.x, qreg[s + 0], acc1, 0, 0, 0);
+                acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.y, qreg[s + 1], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.y, qreg[s + 1], acc1, 0, 0, 0);
+                acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.z, qreg[s + 2], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.z, qreg[s + 2], acc1, 0, 0, 0);
+                acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.w, qreg[s + 3], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.w, qreg[s + 3], acc1, 0, 0, 0);
+            }
+            // Through LDS, so each store writes 64 consecutive rows of one query.
+            float* E = L.est[wave];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row0 = tk_row(r, static_cast<int>(h)), row1 = tk_row(16 + r, static_cast<int>(h));
+                E[j * (TK_ROWS + 1) + row0] = qg + L.xg[b][row0] - 2.f * acc0[r];
+                E[j * (TK_ROWS + 1) + row1] = qg + L.xg[b][row1] - 2.f * acc1[r];
+            }
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            const uint64_t gr = r0 + static_cast<uint64_t>(t) * TK_ROWS + lane;
+            for (uint32_t qq = 0; qq < nq_wave; ++qq)
+                if (gr < r1) a.pd[static_cast<size_t>(q0 + qq) * a.small_max + gr] = E[qq * (TK_ROWS + 1) + lane];
+            __builtin_amdgcn_wave_barrier();
+        }
+        if (qb == 0 && wave == 0) {
+            const uint64_t gr = r0 + static_cast<uint64_t>(t) * TK_ROWS + lane;
+            if (gr < r1) a.px[gr] = L.xg[b][lane];
+        }
+        if (t + 1 < n_tiles) tk_store_rows<DP>(L, b ^ 1, pre, pid);
+        __syncthreads();
+    }
+}
+
+// ---- 3b. small sets: one workgroup per query selects from every estimate ---
+// Each row's estimate L is a lower bound of its fp32 distance and
+// U = L + TK_SEED_ERR (qg + xg) an upper bound.  The k-th smallest U bounds the
+// k-th smallest distance, so every row of the answer (ties included) has
+// L <= that bound: those rows get their fp32 direct distance, are sorted by
+// (distance, id) and the first k are written.
+constexpr uint32_t TK_SMALL = 16384;  // rows the small-set path takes at most
+constexpr int TK_SEL_NT = 1024;
+// Process-wide limit of the small-set path (cr_topk_set_small_limit).
+std::atomic<uint32_t> g_topk_small{TK_SMALL};
+
+__device__ __forceinline__ uint32_t tk_ordered(float f)
+{
+    const uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float tk_unordered(uint32_t u)
+{
+    return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
+}
+
+constexpr uint32_t TK_SEL_PER = TK_SMALL / TK_SEL_NT;  // rows per thread
+constexpr uint32_t TK_SEL_BINS = TK_SEL_NT;            // one histogram bin per thread
+
+__global__ __launch_bounds__(TK_SEL_NT) void tk_select(TkArgs a, float* out_d, int64_t* out_id)
+{
+    __shared__ float key[TK_SMALL];     // candidate distances
+    __shared__ uint32_t idx[TK_SMALL];  // candidate rows, then ids
+    __shared__ uint32_t hist[TK_SEL_BINS];
+    __shared__ float qv[128];
+    __shared__ uint32_t lds[TK_SEL_NT / 64];
+    __shared__ uint32_t s_lo, s_hi, s_bin, s_bound;
+    const uint64_t n_rows = tk_rows(a);
+    if (!tk_small(a, n_rows)) return;  // the list path answers
+    const uint32_t S = static_cast<uint32_t>(n_rows);
+    const uint32_t q = blockIdx.x;
+    const uint32_t t = threadIdx.x;
+    const uint32_t lane = __lane_id(), wave = t >> 6;
+    const float* lrow = a.pd + static_cast<size_t>(q) * a.small_max;
+    for (uint32_t c = t; c < a.dim; c += TK_SEL_NT) qv[c] = a.queries[static_cast<size_t>(q) * a.dim + c];
+    float bound = __builtin_inff();
+    if (S > a.k) {
+        // Upper bounds of this thread's rows, their range over the block.
+        const float qg = a.pq[q];
+        float u[TK_SEL_PER];
+        uint32_t lo = 0xFFFFFFFFu, hi = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < TK_SEL_PER; ++i) {
+            const uint32_t r = t + i * TK_SEL_NT;
+            u[i] = r < S ? lrow[r] + TK_SEED_ERR * (qg + a.px[r]) : __builtin_inff();
+            if (r < S) {
+                lo = min(lo, tk_ordered(u[i]));
+                hi = max(hi, tk_ordered(u[i]));
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            lo = min(lo, static_cast<uint32_t>(__shfl_xor(lo, o, 64)));
+            hi = max(hi, static_cast<uint32_t>(__shfl_xor(hi, o, 64)));
+        }
+        if (t == 0) {
+            s_lo = 0xFFFFFFFFu;
+            s_hi = 0;
+            s_bound = 0;
+        }
+        hist[t] = 0;
+        __syncthreads();
+        if (lane == 0) {
+            atomicMin(&s_lo, lo);
+            atomicMax(&s_hi, hi);
+        }
+        __syncthreads();
+        // A histogram over the value range: bins spread the values, so the
+        // counting atomics rarely collide.  The first bin at which the count
+        // reaches k holds the k-th smallest upper bound; the largest value in
+        // bins up to it is the bound (at least k rows lie at or below it).
+        const float vlo = tk_unordered(s_lo), vhi = tk_unordered(s_hi);
+        const float scale = vhi > vlo ? static_cast<float>(TK_SEL_BINS) / (vhi - vlo) : 0.f;
+        uint32_t bin[TK_SEL_PER];
+#pragma unroll
+        for (uint32_t i = 0; i < TK_SEL_PER; ++i) {
+            const uint32_t r = t + i * TK_SEL_NT;
+            const float f = (u[i] - vlo) * scale;
+            bin[i] = f >= static_cast<float>(TK_SEL_BINS - 1) ? TK_SEL_BINS - 1 : static_cast<uint32_t>(fmaxf(f, 0.f));
+            if (r < S) atomicAdd(&hist[bin[i]], 1u);
+        }
+        __syncthreads();
+        uint32_t total;
+        const uint32_t excl = block_excl_scan<TK_SEL_NT>(hist[t], lds, total);
+        if (excl < a.k && excl + hist[t] >= a.k) s_bin = t;
+        __syncthreads();
+        const uint32_t bstar = s_bin;
+        uint32_t m = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < TK_SEL_PER; ++i)
+            if (t + i * TK_SEL_NT < S && bin[i] <= bstar) m = max(m, tk_ordered(u[i]));
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(m, o, 64)));
+        if (lane == 0 && m) atomicMax(&s_bound, m);
+        __syncthreads();
+        bound = tk_unordered(s_bound);
+    }
+    __syncthreads();
+    // Candidates: rows whose lower bound is at or below the bound, in row order.
+    uint32_t nc = 0;
+    for (uint32_t r0 = 0; r0 < S; r0 += TK_SEL_NT) {
+        const uint32_t r = r0 + t;
+        const bool f = r < S && lrow[r] <= bound;
+        uint32_t tot;
+        const uint32_t pos = block_flag_rank<TK_SEL_NT>(f, lds, tot);
+        if (f) idx[nc + pos] = r;
+        nc += tot;
+    }
+    __syncthreads();
+    // fp32 direct distances: eight threads per candidate, 16 dims each, all
+    // loads of a pass in flight; the eight partial sums are then added.
+    for (uint32_t c0 = 0; c0 < nc; c0 += TK_SEL_NT / 8) {
+        const uint32_t c = c0 + t / 8, part = t % 8;
+        float e2 = 0.f;
+        uint32_t id = 0;
+        if (c < nc) {
+            const uint32_t r = idx[c];
+            id = a.sel ? a.sel[r] : r;
+            const float* x = a.base + static_cast<size_t>(id) * a.dim;
+#pragma unroll
+            for (uint32_t s = 0; s < 16; ++s) {
+                const uint32_t d = part * 16 + s;
+                if (d < a.dim) {
+                    const float e = qv[d] - x[d];
+                    e2 = fmaf(e, e, e2);
+                }
+            }
+        }
+        e2 += __shfl_xor(e2, 1, 64);
+        e2 += __shfl_xor(e2, 2, 64);
+        e2 += __shfl_xor(e2, 4, 64);
+        __syncthreads();  // every thread of the pass has read idx[c]
+        if (c < nc && part == 0) {
+            key[c] = e2;
+            idx[c] = id;
+        }
+    }
+    // Bitonic sort of the candidates by (distance, id), padded to a power of 2.
+    uint32_t P = 2;
+    while (P < nc) P <<= 1;
+    __syncthreads();
+    for (uint32_t i = nc + t; i < P; i += TK_SEL_NT) {
+        key[i] = __builtin_inff();
+        idx[i] = TK_NOID;
+    }
+    __syncthreads();
+    for (uint32_t size = 2; size <= P; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t i = t; i < P / 2; i += TK_SEL_NT) {
+                const uint32_t lo = 2 * i - (i & (stride - 1));
+                const uint32_t hi = lo + stride;
+                const bool up = (lo & size) == 0;
+                const float dl = key[lo], dh = key[hi];
+                const uint32_t il = idx[lo], ih = idx[hi];
+                if (tk_less(dh, ih, dl, il) == up) {
+                    key[lo] = dh;
+                    key[hi] = dl;
+                    idx[lo] = ih;
+                    idx[hi] = il;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (uint32_t r = t; r < a.k; r += TK_SEL_NT) {
+        const bool ok = r < nc;
+        out_d[static_cast<size_t>(q) * a.k + r] = ok ? key[r] : __builtin_inff();
+        out_id[static_cast<size_t>(q) * a.k + r] = ok ? static_cast<int64_t>(idx[r]) : int64_t(-1);
+    }
+}
+
 template <int DP>
 int launch_dist(const TkArgs& a, uint32_t grid, hipStream_t s)
 {
     tk_dist<DP><<<grid, TK_NT, 0, s>>>(a);
     CR_LAUNCH_CHECK();
+    if (a.small_max) {
+        CR_TIMED("tk_pairs", s);
+        tk_pairs<DP><<<grid, TK_NT, 0, s>>>(a);
+        CR_LAUNCH_CHECK();
+    }
     return CR_OK;
 }
 
@@ -689,6 +983,13 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     const size_t o_ln = cv.add(static_cast<size_t>(n_chunks) * n_q * 4);
     const size_t o_tau = cv.add(static_cast<size_t>(n_q) * 4);
     const size_t o_taum = cv.add(static_cast<size_t>(n_chunks) * n_q * 4);
+    // The small-set path keeps every estimate: n_q x small_max floats, so it is
+    // offered while that stays within 256 MiB.
+    const uint32_t small_max =
+        static_cast<uint64_t>(n_q) * TK_SMALL * 4u <= (256ull << 20) ? g_topk_small.load() : 0u;
+    const size_t o_pd = cv.add(static_cast<size_t>(n_q) * small_max * 4);
+    const size_t o_pq = cv.add(small_max ? static_cast<size_t>(n_q) * 4 : 0);
+    const size_t o_px = cv.add(static_cast<size_t>(small_max) * 4);
     Scratch sc;
     CR_RET(sc.alloc(cv.total, s));
 
@@ -708,6 +1009,10 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     a.tau = sc.at<uint32_t>(o_tau);
     a.tau_m = sc.at<uint32_t>(o_taum);
     a.m_rank = std::max<uint32_t>(1, (2 * k + n_chunks - 1) / n_chunks);
+    a.small_max = small_max;
+    a.pd = small_max ? sc.at<float>(o_pd) : nullptr;
+    a.pq = small_max ? sc.at<float>(o_pq) : nullptr;
+    a.px = small_max ? sc.at<float>(o_px) : nullptr;
     CR_RET(fill_u32(a.tau, 0x7F800000u, n_q, s));  // +inf
     CR_RET(fill_u32(a.tau_m, 0x7F800000u, static_cast<uint64_t>(n_chunks) * n_q, s));
     if (filter) {
@@ -741,9 +1046,21 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     }
     {
         CR_TIMED("tk_merge", s);
-        tk_merge<<<(n_q + 3) / 4, TK_MERGE_NT, 0, s>>>(a.list_d, a.list_id, a.plane, a.list_n, n_chunks, n_q, k,
+        tk_merge<<<(n_q + 3) / 4, TK_MERGE_NT, 0, s>>>(a, a.list_d, a.list_id, a.plane, a.list_n, n_chunks, n_q, k,
                                                         d_out_dist, d_out_ids);
     }
     CR_LAUNCH_CHECK();
+    if (small_max) {
+        CR_TIMED("tk_select", s);
+        tk_select<<<n_q, TK_SEL_NT, 0, s>>>(a, d_out_dist, d_out_ids);
+    }
+    CR_LAUNCH_CHECK();
     return CR_OK;
+}
+
+extern "C" uint32_t cr_topk_set_small_limit(uint32_t rows)
+{
+    const uint32_t prev = g_topk_small.load();
+    g_topk_small.store(std::min<uint32_t>(rows, TK_SMALL));
+    return prev;
 }

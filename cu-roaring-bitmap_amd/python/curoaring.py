@@ -31,7 +31,7 @@ EXPORTS = [
     "cr_last_error", "cr_upload_from_ids", "cr_upload_from_device_ids", "cr_upload_from_bitset",
     "cr_upload_from_device_bitset", "cr_upload_containers", "cr_get_meta", "cr_set_operation", "cr_multi_and",
     "cr_free", "cr_free_async", "cr_resolve_auto_threshold", "cr_make_view", "cr_contains_batch",
-    "cr_topk_filtered", "cr_device_l2_bytes", "cr_device_malloc", "cr_device_free", "cr_memcpy_h2d",
+    "cr_topk_filtered", "cr_topk_set_small_limit", "cr_device_l2_bytes", "cr_device_malloc", "cr_device_free", "cr_memcpy_h2d",
     "cr_memcpy_d2h", "cr_stream_synchronize", "cr_timing_enable", "cr_timing_report", "cr_mempool_trim",
     "cr_decompress_to_bitset", "cr_decompress_to_bitset_alloc", "cr_enumerate_ids", "cr_enumerate_ids_alloc",
     "cr_promote_to_bitmap", "cr_promote_auto", "cr_deep_copy",
@@ -156,6 +156,7 @@ def load(path: Optional[str] = None):
         "cr_resolve_auto_threshold": [C.c_uint32, C.c_int, P(C.c_uint32)],
         "cr_make_view": [P(GpuRoaring), P(GpuRoaringView)],
         "cr_contains_batch": [P(GpuRoaringView), C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint32, C.c_void_p],
+        "cr_topk_set_small_limit": [C.c_uint32],
         "cr_topk_filtered": [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint32, C.c_uint32, P(GpuRoaring), C.c_uint32,
                              C.c_void_p, C.c_void_p, C.c_void_p],
         "cr_device_l2_bytes": [C.c_int, P(C.c_uint64)],
@@ -190,6 +191,7 @@ def load(path: Optional[str] = None):
         f = getattr(L, name)
         f.argtypes = args
         f.restype = C.c_int
+    L.cr_topk_set_small_limit.restype = C.c_uint32
     _lib = L
     return L
 
@@ -321,6 +323,12 @@ def contains_batch(g: GpuRoaring, d_ids, d_out, mode: int = QUERY_CONTAINS, stre
     n = d_ids.numel()
     _check(load().cr_contains_batch(C.byref(v), _dptr(d_ids), n, _dptr(d_out), mode, _stream(stream)),
            "contains_batch")
+
+
+def topk_set_small_limit(rows: int) -> int:
+    """Rows at or below which the top-k keeps every estimate and selects per
+    query (capped at 16384; 0 turns that path off).  Returns the previous limit."""
+    return int(load().cr_topk_set_small_limit(rows))
 
 
 def topk_filtered(d_base, d_queries, k: int, filt: Optional[GpuRoaring], d_dist, d_ids, stream=None):

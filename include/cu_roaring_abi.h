@@ -227,6 +227,12 @@ int cr_contains_batch(const cr_gpu_roaring_view* view, const uint32_t* d_ids, ui
 int cr_topk_filtered(const float* d_base, uint64_t n_base, const float* d_queries, uint32_t n_q, uint32_t dim,
                      const cr_gpu_roaring* filter, uint32_t k, float* d_out_dist, int64_t* d_out_ids,
                      cr_stream_t stream);
+/* Tuning of cr_topk_filtered (no counterpart in the reference).  With at most
+ * `rows` passing vectors (capped at 16384; default 16384) every distance
+ * estimate is kept and one workgroup per query selects its k from them, in
+ * place of the per-chunk candidate lists; 0 turns that path off.  Both paths
+ * give the same answer.  Process-wide; returns the previous limit. */
+uint32_t cr_topk_set_small_limit(uint32_t rows);
 
 /* ---- conversions --------------------------------------------------------
  * These calls are stream-ordered and do NOT synchronise `stream` (the

@@ -10,7 +10,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def _declared_symbols():
     src = open(os.path.join(ROOT, "include", "cu_roaring_abi.h")).read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(cr_\w+)\s*\(", src, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|uint32_t|const char\*)\s+(cr_\w+)\s*\(", src, re.M)))
 
 
 def test_header_declares_expected_entry_points():

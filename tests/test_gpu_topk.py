@@ -115,12 +115,24 @@ CASES = [
     (4000, 12, 17, 30, "none", 1.0, 11),
     (2500, 7, 32, 10, "keep", 0.002, 12),  # fewer passing ids than k
     (70000, 520, 128, 10, "none", 1.0, 13),  # three query blocks
+    (16384, 40, 128, 100, "none", 1.0, 14),  # the small-set limit exactly
+    (16385, 40, 128, 100, "none", 1.0, 15),  # one row past it
 ]
 
 
+@pytest.fixture(params=["lists", "small_sets"])
+def path(request, gpu):
+    """Runs a test with the small-set path off (every case on the per-chunk
+    candidate lists) and with its default limit (cases with at most 16384
+    passing rows keep every estimate and select per query)."""
+    prev = gpu.topk_set_small_limit(0 if request.param == "lists" else 16384)
+    yield request.param
+    gpu.topk_set_small_limit(prev)
+
+
 @pytest.mark.parametrize("n_base,n_q,dim,k,kind,density,seed", CASES)
-def test_topk_parity(gpu, n_base, n_q, dim, k, kind, density, seed):
-    _say("topk", n_base, n_q, dim, k, kind, density, seed)
+def test_topk_parity(gpu, path, n_base, n_q, dim, k, kind, density, seed):
+    _say("topk", path, n_base, n_q, dim, k, kind, density, seed)
     base, queries = _data(n_base, n_q, dim, seed)
     filt, mask = _filter_from(gpu, kind, n_base, density, seed)
     got_d, got_i = _run(gpu, base, queries, k, filt)
@@ -129,7 +141,7 @@ def test_topk_parity(gpu, n_base, n_q, dim, k, kind, density, seed):
         gpu.free(filt)
 
 
-def test_topk_ties_break_by_id(gpu):
+def test_topk_ties_break_by_id(gpu, path):
     """Duplicate base vectors tie exactly; the smaller id comes first."""
     _say("topk ties")
     rng = np.random.default_rng(21)
@@ -146,7 +158,7 @@ def test_topk_ties_break_by_id(gpu):
                 assert got_i[q, a] < got_i[q, a + 1]
 
 
-def test_topk_multi_and_filter(gpu):
+def test_topk_multi_and_filter(gpu, path):
     """The workload's shape: filter = multi_and of three predicates."""
     _say("topk multi_and filter")
     n_base = 200000
