@@ -53,6 +53,22 @@ constexpr float TK_SEED_ERR = 3.0f * TK_GATE_ERR;
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// Order-preserving map of fp32 values to u32 (and back).
+__device__ __forceinline__ uint32_t tk_ordered(float f)
+{
+    const uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float tk_unordered(uint32_t u)
+{
+    return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
+}
+
+// Upper bound of a row's fp32 distance from its estimate (a lower bound) and
+// the scaled norms; one fused operation, so every kernel computes the same value.
+__device__ __forceinline__ float tk_upper(float est, float qg, float xg) { return __fmaf_rn(TK_SEED_ERR, qg + xg, est); }
+
 // Strict order of (distance, id) pairs: the output order.
 __device__ __forceinline__ bool tk_less(float ad, uint32_t ai, float bd, uint32_t bi)
 {
@@ -137,6 +153,8 @@ struct TkArgs {
     float* pd;           // [n_q][small_max]
     float* pq;           // [n_q]
     float* px;           // [small_max]
+    uint32_t* qlo;       // [n_q] order-preserving bits of the smallest upper bound of the query's rows
+    uint32_t* qhi;       // [n_q] ... and of the largest
 };
 
 // Rows the distance kernel covers, and whether the small-set path takes them.
@@ -712,6 +730,7 @@ __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
         tk_store_rows<DP>(L, 0, pre, pid);
     }
     __syncthreads();
+    uint32_t ulo = 0xFFFFFFFFu, uhi = 0;  // range of the upper bounds of this lane's rows
     for (uint32_t t = 0; t < n_tiles; ++t) {
         const int b = static_cast<int>(t & 1u);
         if (t + 1 < n_tiles) tk_load_rows<DP>(a, r0 + static_cast<uint64_t>(t + 1) * TK_ROWS, r1, pre, pid);
@@ -734,11 +753,24 @@ __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
             }
             // Through LDS, so each store writes 64 consecutive rows of one query.
             float* E = L.est[wave];
+            const uint64_t tr0 = r0 + static_cast<uint64_t>(t) * TK_ROWS;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row0 = tk_row(r, static_cast<int>(h)), row1 = tk_row(16 + r, static_cast<int>(h));
-                E[j * (TK_ROWS + 1) + row0] = qg + L.xg[b][row0] - 2.f * acc0[r];
-                E[j * (TK_ROWS + 1) + row1] = qg + L.xg[b][row1] - 2.f * acc1[r];
+                const float xg0 = L.xg[b][row0], xg1 = L.xg[b][row1];
+                const float e0 = qg + xg0 - 2.f * acc0[r], e1 = qg + xg1 - 2.f * acc1[r];
+                E[j * (TK_ROWS + 1) + row0] = e0;
+                E[j * (TK_ROWS + 1) + row1] = e1;
+                if (tr0 + row0 < r1) {
+                    const uint32_t u = tk_ordered(tk_upper(e0, qg, xg0));
+                    ulo = min(ulo, u);
+                    uhi = max(uhi, u);
+                }
+                if (tr0 + row1 < r1) {
+                    const uint32_t u = tk_ordered(tk_upper(e1, qg, xg1));
+                    ulo = min(ulo, u);
+                    uhi = max(uhi, u);
+                }
             }
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -754,6 +786,12 @@ __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
         if (t + 1 < n_tiles) tk_store_rows<DP>(L, b ^ 1, pre, pid);
         __syncthreads();
     }
+    ulo = min(ulo, static_cast<uint32_t>(__shfl_xor(ulo, 32, 64)));
+    uhi = max(uhi, static_cast<uint32_t>(__shfl_xor(uhi, 32, 64)));
+    if (h == 0 && qok && uhi != 0) {
+        atomicMin(a.qlo + q0 + j, ulo);
+        atomicMax(a.qhi + q0 + j, uhi);
+    }
 }
 
 // ---- 3b. small sets: one workgroup per query selects from every estimate ---
@@ -762,174 +800,188 @@ __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
 // k-th smallest distance, so every row of the answer (ties included) has
 // L <= that bound: those rows get their fp32 direct distance, are sorted by
 // (distance, id) and the first k are written.
-constexpr uint32_t TK_SMALL = 16384;  // rows the small-set path takes at most
+constexpr uint32_t TK_SMALL = 1u << 18;  // rows the small-set path takes at most
+constexpr uint32_t TK_SMALL_BYTES = 1u << 30;  // and the estimates it may keep
 constexpr int TK_SEL_NT = 1024;
+constexpr uint32_t TK_SEL_BINS = TK_SEL_NT;  // one histogram bin per thread
+constexpr uint32_t TK_SEL_CB = 8192;         // candidates per batch
+constexpr uint32_t TK_SEL_RPT = 4;           // rows per thread per candidate chunk
 // Process-wide limit of the small-set path (cr_topk_set_small_limit).
 std::atomic<uint32_t> g_topk_small{TK_SMALL};
 
-__device__ __forceinline__ uint32_t tk_ordered(float f)
-{
-    const uint32_t b = __float_as_uint(f);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
-__device__ __forceinline__ float tk_unordered(uint32_t u)
-{
-    return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
-}
-
-constexpr uint32_t TK_SEL_PER = TK_SMALL / TK_SEL_NT;  // rows per thread
-constexpr uint32_t TK_SEL_BINS = TK_SEL_NT;            // one histogram bin per thread
-
 __global__ __launch_bounds__(TK_SEL_NT) void tk_select(TkArgs a, float* out_d, int64_t* out_id)
 {
-    __shared__ float key[TK_SMALL];     // candidate distances
-    __shared__ uint32_t idx[TK_SMALL];  // candidate rows, then ids
-    __shared__ uint32_t hist[TK_SEL_BINS];
+    __shared__ float bd[2][TK_KMAX];  // the running best, ascending (two planes)
+    __shared__ uint32_t bi[2][TK_KMAX];
+    __shared__ float cd[TK_SEL_CB];  // a batch of candidates
+    __shared__ uint32_t ci[TK_SEL_CB];
+    __shared__ uint32_t hist[TK_SEL_BINS], bmax[TK_SEL_BINS];
     __shared__ float qv[128];
     __shared__ uint32_t lds[TK_SEL_NT / 64];
-    __shared__ uint32_t s_lo, s_hi, s_bin, s_bound;
+    __shared__ uint32_t s_bin, s_bound, s_nbatch;
     const uint64_t n_rows = tk_rows(a);
     if (!tk_small(a, n_rows)) return;  // the list path answers
     const uint32_t S = static_cast<uint32_t>(n_rows);
     const uint32_t q = blockIdx.x;
     const uint32_t t = threadIdx.x;
-    const uint32_t lane = __lane_id(), wave = t >> 6;
+    const uint32_t lane = __lane_id();
     const float* lrow = a.pd + static_cast<size_t>(q) * a.small_max;
     for (uint32_t c = t; c < a.dim; c += TK_SEL_NT) qv[c] = a.queries[static_cast<size_t>(q) * a.dim + c];
     float bound = __builtin_inff();
     if (S > a.k) {
-        // Upper bounds of this thread's rows, their range over the block.
+        // A histogram of the upper bounds over their range: the bins spread
+        // the values, so the counting atomics rarely collide.  The first bin
+        // at which the count reaches k holds the k-th smallest upper bound;
+        // the largest value in the bins up to it is the bound (at least k rows
+        // lie at or below it, so the k-th distance does).
         const float qg = a.pq[q];
-        float u[TK_SEL_PER];
-        uint32_t lo = 0xFFFFFFFFu, hi = 0;
-#pragma unroll
-        for (uint32_t i = 0; i < TK_SEL_PER; ++i) {
-            const uint32_t r = t + i * TK_SEL_NT;
-            u[i] = r < S ? lrow[r] + TK_SEED_ERR * (qg + a.px[r]) : __builtin_inff();
-            if (r < S) {
-                lo = min(lo, tk_ordered(u[i]));
-                hi = max(hi, tk_ordered(u[i]));
-            }
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            lo = min(lo, static_cast<uint32_t>(__shfl_xor(lo, o, 64)));
-            hi = max(hi, static_cast<uint32_t>(__shfl_xor(hi, o, 64)));
-        }
-        if (t == 0) {
-            s_lo = 0xFFFFFFFFu;
-            s_hi = 0;
-            s_bound = 0;
-        }
-        hist[t] = 0;
-        __syncthreads();
-        if (lane == 0) {
-            atomicMin(&s_lo, lo);
-            atomicMax(&s_hi, hi);
-        }
-        __syncthreads();
-        // A histogram over the value range: bins spread the values, so the
-        // counting atomics rarely collide.  The first bin at which the count
-        // reaches k holds the k-th smallest upper bound; the largest value in
-        // bins up to it is the bound (at least k rows lie at or below it).
-        const float vlo = tk_unordered(s_lo), vhi = tk_unordered(s_hi);
+        const float vlo = tk_unordered(a.qlo[q]), vhi = tk_unordered(a.qhi[q]);
         const float scale = vhi > vlo ? static_cast<float>(TK_SEL_BINS) / (vhi - vlo) : 0.f;
-        uint32_t bin[TK_SEL_PER];
+        hist[t] = 0;
+        bmax[t] = 0;
+        if (t == 0) s_bound = 0;
+        __syncthreads();
+        for (uint32_t r0 = t; r0 < S; r0 += 8 * TK_SEL_NT) {  // eight rows' loads in flight
+            float l8[8], x8[8];
 #pragma unroll
-        for (uint32_t i = 0; i < TK_SEL_PER; ++i) {
-            const uint32_t r = t + i * TK_SEL_NT;
-            const float f = (u[i] - vlo) * scale;
-            bin[i] = f >= static_cast<float>(TK_SEL_BINS - 1) ? TK_SEL_BINS - 1 : static_cast<uint32_t>(fmaxf(f, 0.f));
-            if (r < S) atomicAdd(&hist[bin[i]], 1u);
+            for (uint32_t i = 0; i < 8; ++i) {
+                const uint32_t r = r0 + i * TK_SEL_NT;
+                l8[i] = r < S ? lrow[r] : 0.f;
+                x8[i] = r < S ? a.px[r] : 0.f;
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < 8; ++i) {
+                if (r0 + i * TK_SEL_NT >= S) break;
+                const float u = tk_upper(l8[i], qg, x8[i]);
+                const float f = (u - vlo) * scale;
+                const uint32_t bin = f >= static_cast<float>(TK_SEL_BINS - 1) ? TK_SEL_BINS - 1
+                                                                              : static_cast<uint32_t>(fmaxf(f, 0.f));
+                atomicAdd(&hist[bin], 1u);
+                atomicMax(&bmax[bin], tk_ordered(u));
+            }
         }
         __syncthreads();
         uint32_t total;
-        const uint32_t excl = block_excl_scan<TK_SEL_NT>(hist[t], lds, total);
-        if (excl < a.k && excl + hist[t] >= a.k) s_bin = t;
+        const uint32_t h = hist[t];
+        const uint32_t excl = block_excl_scan<TK_SEL_NT>(h, lds, total);
+        if (excl < a.k && excl + h >= a.k) s_bin = t;
         __syncthreads();
-        const uint32_t bstar = s_bin;
-        uint32_t m = 0;
-#pragma unroll
-        for (uint32_t i = 0; i < TK_SEL_PER; ++i)
-            if (t + i * TK_SEL_NT < S && bin[i] <= bstar) m = max(m, tk_ordered(u[i]));
+        uint32_t m = t <= s_bin ? bmax[t] : 0u;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(m, o, 64)));
         if (lane == 0 && m) atomicMax(&s_bound, m);
         __syncthreads();
         bound = tk_unordered(s_bound);
     }
-    __syncthreads();
-    // Candidates: rows whose lower bound is at or below the bound, in row order.
-    uint32_t nc = 0;
-    for (uint32_t r0 = 0; r0 < S; r0 += TK_SEL_NT) {
-        const uint32_t r = r0 + t;
-        const bool f = r < S && lrow[r] <= bound;
-        uint32_t tot;
-        const uint32_t pos = block_flag_rank<TK_SEL_NT>(f, lds, tot);
-        if (f) idx[nc + pos] = r;
-        nc += tot;
-    }
-    __syncthreads();
-    // fp32 direct distances: eight threads per candidate, 16 dims each, all
-    // loads of a pass in flight; the eight partial sums are then added.
-    for (uint32_t c0 = 0; c0 < nc; c0 += TK_SEL_NT / 8) {
-        const uint32_t c = c0 + t / 8, part = t % 8;
-        float e2 = 0.f;
-        uint32_t id = 0;
-        if (c < nc) {
-            const uint32_t r = idx[c];
-            id = a.sel ? a.sel[r] : r;
-            const float* x = a.base + static_cast<size_t>(id) * a.dim;
+    // Candidates (rows whose estimate, a lower bound, is at or below the bound)
+    // in batches: fp32 direct distances, a sort by (distance, id), and a merge
+    // into the running best k.
+    uint32_t nb = 0, cur = 0, nbatch = 0;
+    auto flush = [&]() {
+        __syncthreads();  // the batch's rows are in ci
+        for (uint32_t c0 = 0; c0 < nbatch; c0 += TK_SEL_NT / 8) {  // eight threads per candidate
+            const uint32_t c = c0 + t / 8, part = t % 8;
+            float e2 = 0.f;
+            uint32_t id = 0;
+            if (c < nbatch) {
+                const uint32_t r = ci[c];
+                id = a.sel ? a.sel[r] : r;
+                const float* x = a.base + static_cast<size_t>(id) * a.dim;
 #pragma unroll
-            for (uint32_t s = 0; s < 16; ++s) {
-                const uint32_t d = part * 16 + s;
-                if (d < a.dim) {
-                    const float e = qv[d] - x[d];
-                    e2 = fmaf(e, e, e2);
+                for (uint32_t s2 = 0; s2 < 16; ++s2) {
+                    const uint32_t d = part * 16 + s2;
+                    if (d < a.dim) {
+                        const float e = qv[d] - x[d];
+                        e2 = fmaf(e, e, e2);
+                    }
                 }
             }
-        }
-        e2 += __shfl_xor(e2, 1, 64);
-        e2 += __shfl_xor(e2, 2, 64);
-        e2 += __shfl_xor(e2, 4, 64);
-        __syncthreads();  // every thread of the pass has read idx[c]
-        if (c < nc && part == 0) {
-            key[c] = e2;
-            idx[c] = id;
-        }
-    }
-    // Bitonic sort of the candidates by (distance, id), padded to a power of 2.
-    uint32_t P = 2;
-    while (P < nc) P <<= 1;
-    __syncthreads();
-    for (uint32_t i = nc + t; i < P; i += TK_SEL_NT) {
-        key[i] = __builtin_inff();
-        idx[i] = TK_NOID;
-    }
-    __syncthreads();
-    for (uint32_t size = 2; size <= P; size <<= 1) {
-        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-            for (uint32_t i = t; i < P / 2; i += TK_SEL_NT) {
-                const uint32_t lo = 2 * i - (i & (stride - 1));
-                const uint32_t hi = lo + stride;
-                const bool up = (lo & size) == 0;
-                const float dl = key[lo], dh = key[hi];
-                const uint32_t il = idx[lo], ih = idx[hi];
-                if (tk_less(dh, ih, dl, il) == up) {
-                    key[lo] = dh;
-                    key[hi] = dl;
-                    idx[lo] = ih;
-                    idx[hi] = il;
-                }
+            e2 += __shfl_xor(e2, 1, 64);
+            e2 += __shfl_xor(e2, 2, 64);
+            e2 += __shfl_xor(e2, 4, 64);
+            __syncthreads();  // every thread of the pass has read ci[c]
+            if (c < nbatch && part == 0) {
+                cd[c] = e2;
+                ci[c] = id;
             }
-            __syncthreads();
+        }
+        uint32_t P = 2;
+        while (P < nbatch) P <<= 1;
+        __syncthreads();
+        for (uint32_t i = nbatch + t; i < P; i += TK_SEL_NT) {
+            cd[i] = __builtin_inff();
+            ci[i] = TK_NOID;
+        }
+        __syncthreads();
+        for (uint32_t size = 2; size <= P; size <<= 1) {
+            for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+                for (uint32_t i = t; i < P / 2; i += TK_SEL_NT) {
+                    const uint32_t lo = 2 * i - (i & (stride - 1));
+                    const uint32_t hi = lo + stride;
+                    const bool up = (lo & size) == 0;
+                    const float dl = cd[lo], dh = cd[hi];
+                    const uint32_t il = ci[lo], ih = ci[hi];
+                    if (tk_less(dh, ih, dl, il) == up) {
+                        cd[lo] = dh;
+                        cd[hi] = dl;
+                        ci[lo] = ih;
+                        ci[hi] = il;
+                    }
+                }
+                __syncthreads();
+            }
+        }
+        // Merge: an entry's rank is its index plus the number of entries of
+        // the other list before it (all (distance, id) pairs are distinct).
+        const uint32_t nbt = min(nbatch, a.k);
+        if (t < nb) {
+            const uint32_t r = t + tk_lower_bound(cd, ci, nbt, bd[cur][t], bi[cur][t]);
+            if (r < a.k) {
+                bd[cur ^ 1][r] = bd[cur][t];
+                bi[cur ^ 1][r] = bi[cur][t];
+            }
+        } else if (t - nb < nbt) {
+            const uint32_t e = t - nb;
+            const uint32_t r = e + tk_lower_bound(bd[cur], bi[cur], nb, cd[e], ci[e]);
+            if (r < a.k) {
+                bd[cur ^ 1][r] = cd[e];
+                bi[cur ^ 1][r] = ci[e];
+            }
+        }
+        nb = min(a.k, nb + nbt);
+        cur ^= 1;
+        nbatch = 0;
+        if (t == 0) s_nbatch = 0;
+        __syncthreads();
+    };
+    // Candidates are few: a thread that finds one takes a batch slot with an
+    // LDS atomic.  Chunks of TK_SEL_RPT rows per thread (loads in flight); a
+    // batch that could overflow in the next chunk is flushed first.
+    if (t == 0) s_nbatch = 0;
+    for (uint32_t r0 = 0; r0 < S; r0 += TK_SEL_RPT * TK_SEL_NT) {
+        __syncthreads();  // the previous chunk's slots are taken
+        nbatch = s_nbatch;
+        __syncthreads();  // every thread has read the count before the next slots are taken
+        if (nbatch > TK_SEL_CB - TK_SEL_RPT * TK_SEL_NT) flush();
+        float l4[TK_SEL_RPT];
+#pragma unroll
+        for (uint32_t i = 0; i < TK_SEL_RPT; ++i) {
+            const uint32_t r = r0 + i * TK_SEL_NT + t;
+            l4[i] = r < S ? lrow[r] : __builtin_inff();
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < TK_SEL_RPT; ++i) {
+            const uint32_t r = r0 + i * TK_SEL_NT + t;
+            if (r < S && l4[i] <= bound) ci[atomicAdd(&s_nbatch, 1u)] = r;
         }
     }
+    __syncthreads();
+    nbatch = s_nbatch;
+    if (nbatch) flush();
     for (uint32_t r = t; r < a.k; r += TK_SEL_NT) {
-        const bool ok = r < nc;
-        out_d[static_cast<size_t>(q) * a.k + r] = ok ? key[r] : __builtin_inff();
-        out_id[static_cast<size_t>(q) * a.k + r] = ok ? static_cast<int64_t>(idx[r]) : int64_t(-1);
+        const bool ok = r < nb;
+        out_d[static_cast<size_t>(q) * a.k + r] = ok ? bd[cur][r] : __builtin_inff();
+        out_id[static_cast<size_t>(q) * a.k + r] = ok ? static_cast<int64_t>(bi[cur][r]) : int64_t(-1);
     }
 }
 
@@ -983,13 +1035,15 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     const size_t o_ln = cv.add(static_cast<size_t>(n_chunks) * n_q * 4);
     const size_t o_tau = cv.add(static_cast<size_t>(n_q) * 4);
     const size_t o_taum = cv.add(static_cast<size_t>(n_chunks) * n_q * 4);
-    // The small-set path keeps every estimate: n_q x small_max floats, so it is
-    // offered while that stays within 256 MiB.
-    const uint32_t small_max =
-        static_cast<uint64_t>(n_q) * TK_SMALL * 4u <= (256ull << 20) ? g_topk_small.load() : 0u;
+    // The small-set path keeps every estimate, n_q x small_max floats, within
+    // TK_SMALL_BYTES.
+    const uint32_t small_max = static_cast<uint32_t>(std::min<uint64_t>(
+        g_topk_small.load(), TK_SMALL_BYTES / (4ull * n_q) / TK_ROWS * TK_ROWS));
     const size_t o_pd = cv.add(static_cast<size_t>(n_q) * small_max * 4);
     const size_t o_pq = cv.add(small_max ? static_cast<size_t>(n_q) * 4 : 0);
     const size_t o_px = cv.add(static_cast<size_t>(small_max) * 4);
+    const size_t o_qlo = cv.add(small_max ? static_cast<size_t>(n_q) * 4 : 0);
+    const size_t o_qhi = cv.add(small_max ? static_cast<size_t>(n_q) * 4 : 0);
     Scratch sc;
     CR_RET(sc.alloc(cv.total, s));
 
@@ -1013,6 +1067,12 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     a.pd = small_max ? sc.at<float>(o_pd) : nullptr;
     a.pq = small_max ? sc.at<float>(o_pq) : nullptr;
     a.px = small_max ? sc.at<float>(o_px) : nullptr;
+    a.qlo = small_max ? sc.at<uint32_t>(o_qlo) : nullptr;
+    a.qhi = small_max ? sc.at<uint32_t>(o_qhi) : nullptr;
+    if (small_max) {
+        CR_RET(fill_u32(a.qlo, 0xFFFFFFFFu, n_q, s));
+        CR_RET(fill_u32(a.qhi, 0u, n_q, s));
+    }
     CR_RET(fill_u32(a.tau, 0x7F800000u, n_q, s));  // +inf
     CR_RET(fill_u32(a.tau_m, 0x7F800000u, static_cast<uint64_t>(n_chunks) * n_q, s));
     if (filter) {

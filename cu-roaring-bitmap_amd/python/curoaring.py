@@ -327,7 +327,7 @@ def contains_batch(g: GpuRoaring, d_ids, d_out, mode: int = QUERY_CONTAINS, stre
 
 def topk_set_small_limit(rows: int) -> int:
     """Rows at or below which the top-k keeps every estimate and selects per
-    query (capped at 16384; 0 turns that path off).  Returns the previous limit."""
+    query (capped at 262144; 0 turns that path off).  Returns the previous limit."""
     return int(load().cr_topk_set_small_limit(rows))
 
 

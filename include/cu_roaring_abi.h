@@ -228,10 +228,11 @@ int cr_topk_filtered(const float* d_base, uint64_t n_base, const float* d_querie
                      const cr_gpu_roaring* filter, uint32_t k, float* d_out_dist, int64_t* d_out_ids,
                      cr_stream_t stream);
 /* Tuning of cr_topk_filtered (no counterpart in the reference).  With at most
- * `rows` passing vectors (capped at 16384; default 16384) every distance
- * estimate is kept and one workgroup per query selects its k from them, in
- * place of the per-chunk candidate lists; 0 turns that path off.  Both paths
- * give the same answer.  Process-wide; returns the previous limit. */
+ * `rows` passing vectors (capped at 262144, the default, and at 1 GiB of
+ * estimates: n_q x rows x 4 bytes) every distance estimate is kept and one
+ * workgroup per query selects its k from them, in place of the per-chunk
+ * candidate lists; 0 turns that path off.  Both paths give the same answer.
+ * Process-wide; returns the previous limit. */
 uint32_t cr_topk_set_small_limit(uint32_t rows);
 
 /* ---- conversions --------------------------------------------------------

@@ -120,12 +120,16 @@ CASES = [
 ]
 
 
-@pytest.fixture(params=["lists", "small_sets"])
+SMALL_LIMITS = {"lists": 0, "small_16384": 16384, "small_default": 1 << 18}
+
+
+@pytest.fixture(params=list(SMALL_LIMITS))
 def path(request, gpu):
     """Runs a test with the small-set path off (every case on the per-chunk
-    candidate lists) and with its default limit (cases with at most 16384
-    passing rows keep every estimate and select per query)."""
-    prev = gpu.topk_set_small_limit(0 if request.param == "lists" else 16384)
+    candidate lists), with a limit of 16384 passing rows (both sides of it in
+    the cases below), and with the default limit (every case here keeps every
+    estimate and selects per query)."""
+    prev = gpu.topk_set_small_limit(SMALL_LIMITS[request.param])
     yield request.param
     gpu.topk_set_small_limit(prev)
 
