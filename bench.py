@@ -215,7 +215,101 @@ def secondary(torch, cr, flush):
     cr.free(bm)
     torch.cuda.empty_cache()
     out["batch_16x2^28"] = batch_api(torch, cr, flush)
+    torch.cuda.empty_cache()
+    out["upload_variants_2^30"] = upload_variants(torch, cr)
     return out
+
+
+def clustered_ids(torch, seed=11):
+    """BASELINE configs[1], clustered variant: runs of length U[1000, 65536) at
+    uniform starts over 2^30 until 90M ids (overlapping runs add duplicates),
+    plus 10M duplicates drawn from them, shuffled."""
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    lens = torch.randint(1000, 65536, (2 * N_DISTINCT // 33268 + 64,), device=dev, generator=g)
+    csum = torch.cumsum(lens, 0)
+    n_runs = int(torch.searchsorted(csum, torch.tensor([N_DISTINCT], device=dev)).item()) + 1
+    lens = lens[:n_runs].clone()
+    lens[-1] -= int(csum[n_runs - 1].item()) - N_DISTINCT
+    starts = torch.randint(0, U - 65536, (n_runs,), device=dev, generator=g)
+    offs = torch.cumsum(lens, 0) - lens
+    run_of = torch.repeat_interleave(torch.arange(n_runs, device=dev), lens)
+    ids = starts[run_of] + (torch.arange(N_DISTINCT, device=dev) - offs[run_of])
+    del run_of
+    dup = ids[torch.randint(0, N_DISTINCT, (N_IDS - N_DISTINCT,), device=dev, generator=g)]
+    ids = torch.cat([ids, dup])
+    ids = ids[torch.randperm(N_IDS, device=dev, generator=g)]
+    return ids.to(torch.int32).contiguous(), n_runs
+
+
+def _bitset_words(torch, density, seed):
+    """2^25 u32 words (a 2^30-bit bitset, as int32) at the given density."""
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    nw = U // 32
+    if density == 0.5:
+        return torch.randint(-(1 << 31), 1 << 31, (nw,), device=dev, generator=g, dtype=torch.int64).to(torch.int32)
+    p = density if density < 0.5 else 1.0 - density
+    ids = torch.unique(torch.randint(0, U, (int(p * U),), device=dev, generator=g))
+    w = torch.zeros(nw, device=dev, dtype=torch.int64)
+    w.index_add_(0, ids >> 5, torch.ones_like(ids) << (ids & 31))  # distinct bits: the sum is the OR
+    del ids
+    w = (w - (w >= (1 << 31)).to(torch.int64) * (1 << 32)).to(torch.int32)
+    return w if density < 0.5 else torch.bitwise_not(w)
+
+
+def upload_variants(torch, cr):
+    """The rest of BASELINE configs[1]: upload_from_ids on the clustered
+    variant (most keys absent, so the result is compacted), and
+    upload_from_device_bitset at 0.1%, 50% and 90% density (the last one
+    stored as the complement).  Hot timings (median of 5) with the kernels'
+    HIP-event times; the bitset path's algorithmic bytes are the bitset read
+    twice (count, compact) plus the containers written."""
+    res = {}
+    d, n_runs = clustered_ids(torch)
+    torch.cuda.synchronize()
+
+    def timed(fn):
+        r = fn()
+        torch.cuda.synchronize()
+        meta = (r.n_containers, r.total_cardinality, bool(r.negated))
+        cr.free(r)
+        cr.timing_enable(True)
+        ts = []
+        for _ in range(5):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            r = fn()
+            torch.cuda.synchronize()
+            ts.append((time.perf_counter() - t0) * 1e3)
+            cr.free(r)
+        rep = cr.timing_report()
+        cr.timing_enable(False)
+        return median(ts), meta, {k: round(v[1] / v[0], 4) for k, v in rep.items()}
+
+    t, (nc, card, neg), k = timed(lambda: cr.upload_from_device_ids(d, U))
+    res["ids_clustered_100M"] = {"ms": round(t, 4), "runs": n_runs, "containers": nc, "distinct": card,
+                                 "kernels_ms": k}
+    del d
+    torch.cuda.empty_cache()
+    for dens, seed in ((0.001, 71), (0.5, 72), (0.9, 73)):
+        w = _bitset_words(torch, dens, seed)
+        torch.cuda.synchronize()
+        t, (nc, card, neg), k = timed(lambda: cr.upload_from_device_bitset(w, U))
+        nbytes = 2 * (U // 8) + 8192 * nc + 9 * nc
+        dev_ms = sum(v for kk, v in k.items() if not kk.startswith("host:"))
+        res[f"bitset_{dens * 100:g}pct"] = {"ms": round(t, 4), "containers": nc, "cardinality": card,
+                                            "negated": neg, "algorithmic_bytes": nbytes,
+                                            "device_ms": round(dev_ms, 4),
+                                            "device_GBps": round(nbytes / dev_ms / 1e6, 1),
+                                            "frac_of_hbm_peak": round(nbytes / dev_ms / 1e6 / HBM_PEAK_GBS, 4),
+                                            "kernels_ms": k}
+        del w
+        torch.cuda.empty_cache()
+    log("upload variants", res)
+    return res
 
 
 def _kernel_line(rep, name, nbytes, t_api):

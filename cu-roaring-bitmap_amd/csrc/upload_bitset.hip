@@ -79,61 +79,123 @@ __global__ __launch_bounds__(BS_NT) void bs_count(const uint32_t* __restrict__ w
 }
 
 // One workgroup: complement decision, ranks of non-empty chunks, metadata.
+// One workgroup.  Round j covers chunks [1024 j, 1024 j + 1024), one per
+// thread, with coalesced loads (eight rounds in flight): the input's popcount
+// decides the negation (total > U/2, strict, src/upload_ids.cu:837), a chunk is
+// kept iff its (plain or inverted) count is non-zero, and ranks come from
+// per-wave ballots (wave counts in LDS, turned into wave and round bases).
+// Writes the chunk -> rank map, keys/types/offsets/cards, key_index, and the
+// totals to `tot` and to the caller's pinned host slot.
+constexpr uint32_t BS_ROUNDS = 65536 / 1024;
+
 __global__ __launch_bounds__(1024) void bs_plan(BsGeom g, const uint32_t* pc, const uint32_t* pci, uint32_t* cmap,
                                                 uint16_t* keys, uint8_t* types, uint32_t* offsets, uint16_t* cards,
-                                                uint16_t* key_index, BsTotals* tot)
+                                                uint16_t* key_index, BsTotals* tot, BsTotals* host)
 {
-    __shared__ uint32_t lds[16];
-    __shared__ unsigned long long s_total;
+    __shared__ uint32_t wcnt[BS_ROUNDS][16];
+    __shared__ uint32_t rbase[BS_ROUNDS + 1];
+    __shared__ unsigned long long wsum[16];
     __shared__ uint32_t s_last;
-    const uint32_t t = threadIdx.x;
-    const uint32_t per = (g.n_chunks + 1023) / 1024;
-    const uint32_t c0 = t * per;
+    const uint32_t t = threadIdx.x, wave = t >> 6, lane = __lane_id();
+    const uint32_t rounds = (g.n_chunks + 1023u) / 1024u;
     unsigned long long part = 0;
-    for (uint32_t k = 0; k < per; ++k)
-        if (c0 + k < g.n_chunks) part += pc[c0 + k];
-    if (t == 0) {
-        s_total = 0;
-        s_last = 0;
+    for (uint32_t j0 = 0; j0 < rounds; j0 += 8) {
+        uint32_t v[8];
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) {
+            const uint32_t c = (j0 + q) * 1024u + t;
+            v[q] = c < g.n_chunks ? pc[c] : 0u;
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) part += v[q];
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+    if (lane == 0) wsum[wave] = part;
+    if (t == 0) s_last = 0;
     __syncthreads();
-    atomicAdd(&s_total, part);
-    __syncthreads();
-    const unsigned long long total = s_total;
+    unsigned long long total = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) total += wsum[w];
     const bool negate = total > static_cast<unsigned long long>(g.universe / 2u);  // :837
-    uint32_t cnt = 0;
-    for (uint32_t k = 0; k < per; ++k) {
-        const uint32_t c = c0 + k;
-        if (c < g.n_chunks && (negate ? pci[c] : pc[c]) > 0) ++cnt;
-    }
-    uint32_t n_c;
-    uint32_t rank = block_excl_scan<1024>(cnt, lds, n_c);
-    uint32_t last = 0;
-    for (uint32_t k = 0; k < per; ++k) {
-        const uint32_t c = c0 + k;
-        if (c >= g.n_chunks) break;
-        const uint32_t p = negate ? pci[c] : pc[c];
-        if (p > 0) {
-            cmap[c] = rank;
-            keys[rank] = static_cast<uint16_t>(c);
-            types[rank] = CR_BITMAP;
-            offsets[rank] = rank * 8192u;
-            cards[rank] = static_cast<uint16_t>(p > 65535u ? 0u : p);
-            key_index[c] = static_cast<uint16_t>(rank);
-            last = c;
-            ++rank;
-        } else {
-            cmap[c] = 0xFFFFFFFFu;
-            key_index[c] = 0xFFFFu;
+    const uint32_t* cnt = negate ? pci : pc;
+    uint64_t mine = 0;  // bit j: this thread's chunk of round j is kept
+    for (uint32_t j0 = 0; j0 < rounds; j0 += 8) {
+        uint32_t v[8];
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) {
+            const uint32_t c = (j0 + q) * 1024u + t;
+            v[q] = (j0 + q < rounds && c < g.n_chunks) ? cnt[c] : 0u;
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) {
+            if (j0 + q >= rounds) break;
+            const uint64_t m = __ballot(v[q] != 0u);
+            if (v[q] != 0u) mine |= 1ull << (j0 + q);
+            if (lane == 0) wcnt[j0 + q][wave] = static_cast<uint32_t>(__popcll(m));
         }
     }
-    if (cnt) atomicMax(&s_last, last);
+    __syncthreads();
+    uint32_t wprefix = 0, rtotal = 0;
+    if (t < rounds * 16u) {
+        const uint32_t j = t >> 4, w = t & 15u;
+        for (uint32_t x = 0; x < w; ++x) wprefix += wcnt[j][x];
+        if (w == 15u) rtotal = wprefix + wcnt[j][15];
+    }
+    __syncthreads();
+    if (t < rounds * 16u) {
+        wcnt[t >> 4][t & 15u] = wprefix;
+        if ((t & 15u) == 15u) rbase[(t >> 4) + 1] = rtotal;
+    }
+    if (t == 0) rbase[0] = 0;
+    __syncthreads();
+    if (t == 0)
+        for (uint32_t j = 1; j <= rounds; ++j) rbase[j] += rbase[j - 1];
+    __syncthreads();
+    uint32_t last = 0;
+    for (uint32_t j0 = 0; j0 < rounds; j0 += 8) {
+        uint32_t v[8];  // the counts again (cache hits), eight rounds in flight
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) v[q] = ((mine >> (j0 + q)) & 1ull) ? cnt[(j0 + q) * 1024u + t] : 0u;
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) {
+            const uint32_t j = j0 + q;
+            if (j >= rounds) break;
+            const uint32_t c = j * 1024u + t;
+            const bool kept = (mine >> j) & 1ull;
+            const uint64_t m = __ballot(kept);
+            if (kept) {
+                const uint32_t rank =
+                    rbase[j] + wcnt[j][wave] + static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull)));
+                cmap[c] = rank;
+                keys[rank] = static_cast<uint16_t>(c);
+                types[rank] = CR_BITMAP;
+                offsets[rank] = rank * 8192u;
+                cards[rank] = static_cast<uint16_t>(v[q] > 65535u ? 0u : v[q]);
+                key_index[c] = static_cast<uint16_t>(rank);
+                last = c;
+            } else if (c < g.n_chunks) {
+                cmap[c] = 0xFFFFFFFFu;
+                key_index[c] = 0xFFFFu;
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) last = max(last, static_cast<uint32_t>(__shfl_xor(last, o, 64)));
+    if (lane == 0 && last) atomicMax(&s_last, last);
     __syncthreads();
     if (t == 0) {
-        tot->n_containers = n_c;
-        tot->negated = negate ? 1u : 0u;
-        tot->max_key = s_last;
-        tot->total = total;
+        BsTotals r{};
+        r.n_containers = rbase[rounds];
+        r.negated = negate ? 1u : 0u;
+        r.max_key = s_last;
+        r.total = total;
+        *tot = r;
+        volatile BsTotals* h = host;
+        h->n_containers = r.n_containers;
+        h->negated = r.negated;
+        h->max_key = r.max_key;
+        h->total = r.total;
     }
 }
 
@@ -226,10 +288,12 @@ int upload_from_device_bitset_impl(const uint32_t* d_words, uint32_t n_words, ui
         bs_count<<<grid_cap(g.n_chunks), BS_NT, 0, s>>>(d_words, g, pc, pci);
     }
     CR_LAUNCH_CHECK();
+    HostSlotGuard hs;
+    CR_RET(hs.acquire());
     {
         CR_TIMED("bs_plan", s);
         bs_plan<<<1, 1024, 0, s>>>(g, pc, pci, cmap, out->keys, out->types, out->offsets, out->cardinalities,
-                                   out->key_index, tot);
+                                   out->key_index, tot, hs.dev<BsTotals>());
     }
     CR_LAUNCH_CHECK();
     {
@@ -237,8 +301,15 @@ int upload_from_device_bitset_impl(const uint32_t* d_words, uint32_t n_words, ui
         bs_compact<<<grid_cap(g.n_chunks), BS_NT, 0, s>>>(d_words, g, cmap, tot, out->bitmap_data);
     }
     CR_LAUNCH_CHECK();
+    CR_RET(sync_stream(s));
     BsTotals h{};
-    CR_RET(read_back(&h, tot, sizeof(h), s));
+    {
+        const volatile BsTotals* hp = hs.host<BsTotals>();
+        h.n_containers = hp->n_containers;
+        h.negated = hp->negated;
+        h.max_key = hp->max_key;
+        h.total = hp->total;
+    }
     out->negated = h.negated != 0;
     out->total_cardinality = h.total;  // logical count either way (:740)
     out->n_containers = h.n_containers;
