@@ -8,6 +8,8 @@
 #include <algorithm>
 #include <cstring>
 
+#include <type_traits>
+
 #include "image.hpp"
 #include "internal.hpp"
 
@@ -189,12 +191,47 @@ __global__ __launch_bounds__(SC_NT) void cv_scan_u64(const uint64_t* __restrict_
     if (i < n) starts[i] = pre;
 }
 
+// A container of at most EW_STAGE ids is staged whole: one scan of the four
+// chunks' counts (packed as 16-bit fields of a u64), the ids in order as u16
+// in LDS, then one pass of coalesced int64 stores.  Denser containers go
+// chunk by chunk.  LEAN: the input holds no run container, so no run image.
+constexpr uint32_t EW_STAGE = 512u * 32u;  // 16384 ids
+
+__device__ __forceinline__ unsigned long long block_excl_scan_u64(unsigned long long v, unsigned long long* part,
+                                                                  unsigned long long& total)
+{
+    unsigned long long incl = v;
+    const uint32_t lane = __lane_id();
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const unsigned long long x = __shfl_up(incl, o, 64);
+        if (lane >= static_cast<uint32_t>(o)) incl += x;
+    }
+    const uint32_t w = threadIdx.x >> 6;
+    if (lane == 63) part[w] = incl;
+    __syncthreads();
+    unsigned long long base = 0, t = 0;
+#pragma unroll
+    for (int i = 0; i < CV_NT / 64; ++i) {
+        const unsigned long long x = part[i];
+        base += (static_cast<uint32_t>(i) < w) ? x : 0ull;
+        t += x;
+    }
+    __syncthreads();
+    total = t;
+    return base + incl - v;
+}
+
+template <bool LEAN>
 __global__ __launch_bounds__(CV_NT) void cv_enum_write(cr_gpu_roaring r, const uint64_t* starts, uint64_t cap,
                                                        int64_t* __restrict__ out)
 {
-    __shared__ Image img;
-    __shared__ uint16_t stage[512 * 32];
-    __shared__ uint32_t red[CV_NT / 64];
+    struct NoImage {
+        uint32_t w[1];
+    };
+    __shared__ std::conditional_t<LEAN, NoImage, Image> img;
+    __shared__ uint16_t stage[EW_STAGE];
+    __shared__ unsigned long long red64[CV_NT / 64];
     const uint32_t c = blockIdx.x;
     const uint32_t t = threadIdx.x;
     const uint8_t type = r.types[c];
@@ -211,9 +248,11 @@ __global__ __launch_bounds__(CV_NT) void cv_enum_write(cr_gpu_roaring r, const u
     const uint32_t* words;
     if (type == CR_BITMAP) {
         words = reinterpret_cast<const uint32_t*>(r.bitmap_data + off / 8u);
-    } else if (type == CR_RUN) {
-        expand_to_lds(CR_RUN, r.run_data + off / 2u, r.cardinalities[c], &img);
-        words = img.w;
+    } else if (!LEAN && type == CR_RUN) {
+        if constexpr (!LEAN) {
+            expand_to_lds(CR_RUN, r.run_data + off / 2u, r.cardinalities[c], &img);
+            words = img.w;
+        }
     } else {
         return;
     }
@@ -221,19 +260,46 @@ __global__ __launch_bounds__(CV_NT) void cv_enum_write(cr_gpu_roaring r, const u
     uint2 v[4];
 #pragma unroll
     for (int ch = 0; ch < 4; ++ch) v[ch] = reinterpret_cast<const uint2*>(words)[ch * CV_NT + t];
+    unsigned long long packed = 0;
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch)
+        packed |= static_cast<unsigned long long>(__popc(v[ch].x) + __popc(v[ch].y)) << (16 * ch);
+    unsigned long long totals;
+    const unsigned long long pre = block_excl_scan_u64(packed, red64, totals);
+    uint32_t tot[4], cbase[4];
+    uint32_t all = 0;
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch) {
+        tot[ch] = static_cast<uint32_t>(totals >> (16 * ch)) & 0xFFFFu;
+        cbase[ch] = all;
+        all += tot[ch];
+    }
+    if (all <= EW_STAGE) {
+#pragma unroll
+        for (int ch = 0; ch < 4; ++ch) {
+            const uint32_t wi = ch * 512u + 2u * t;
+            uint32_t pos = cbase[ch] + (static_cast<uint32_t>(pre >> (16 * ch)) & 0xFFFFu);
+            for (uint32_t x = v[ch].x; x; x &= x - 1) stage[pos++] = static_cast<uint16_t>(32u * wi + __builtin_ctz(x));
+            for (uint32_t x = v[ch].y; x; x &= x - 1)
+                stage[pos++] = static_cast<uint16_t>(32u * (wi + 1u) + __builtin_ctz(x));
+        }
+        __syncthreads();
+        for (uint32_t i = t; i < all; i += CV_NT)
+            if (start + i < cap) st_stream(out + start + i, base | stage[i]);
+        return;
+    }
     uint64_t written = start;
 #pragma unroll
     for (int ch = 0; ch < 4; ++ch) {
         const uint32_t wi = ch * 512u + 2u * t;
-        uint32_t total;
-        uint32_t pos = block_excl_scan<CV_NT>(static_cast<uint32_t>(__popc(v[ch].x) + __popc(v[ch].y)), red, total);
+        uint32_t pos = static_cast<uint32_t>(pre >> (16 * ch)) & 0xFFFFu;
         for (uint32_t x = v[ch].x; x; x &= x - 1) stage[pos++] = static_cast<uint16_t>(32u * wi + __builtin_ctz(x));
         for (uint32_t x = v[ch].y; x; x &= x - 1)
             stage[pos++] = static_cast<uint16_t>(32u * (wi + 1u) + __builtin_ctz(x));
         __syncthreads();
-        for (uint32_t i = t; i < total; i += CV_NT)
+        for (uint32_t i = t; i < tot[ch]; i += CV_NT)
             if (written + i < cap) st_stream(out + written + i, base | stage[i]);
-        written += total;
+        written += tot[ch];
         __syncthreads();
     }
 }
@@ -431,8 +497,10 @@ int enumerate_impl(const cr_gpu_roaring* bm, int64_t* d_out, uint64_t cap, hipSt
         CR_TIMED("cv_enum_write", s);
         if (bm->n_bitmap_containers == 0 && bm->n_run_containers == 0)
             cv_enum_write_arrays<<<(n + 3) / 4, CV_NT, 0, s>>>(*bm, starts, cap, d_out);
+        else if (bm->n_run_containers == 0)
+            cv_enum_write<true><<<n, CV_NT, 0, s>>>(*bm, starts, cap, d_out);
         else
-            cv_enum_write<<<n, CV_NT, 0, s>>>(*bm, starts, cap, d_out);
+            cv_enum_write<false><<<n, CV_NT, 0, s>>>(*bm, starts, cap, d_out);
     }
     CR_LAUNCH_CHECK();
     return CR_OK;
@@ -463,14 +531,15 @@ __global__ __launch_bounds__(256) void cv_copy(CopyList L)
         const uint64_t n4 = g.bytes / 16u;
         const uint4* s4 = static_cast<const uint4*>(g.src);
         uint4* d4 = static_cast<uint4*>(g.dst);
-        for (uint64_t i = i0; i < n4; i += 4 * stride) {  // four 16-byte loads in flight
-            uint4 v[4];
+        // A workgroup copies 8 x 4 KiB per step: eight 16-byte loads in flight per thread.
+        for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 2048u + threadIdx.x; i < n4; i += 8 * stride) {
+            uint4 v[8];
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if (i + k * stride < n4) v[k] = ld_stream(s4 + i + k * stride);
+            for (int k = 0; k < 8; ++k)
+                if (i + k * 256u < n4) v[k] = ld_stream(s4 + i + k * 256u);
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if (i + k * stride < n4) st_stream(d4 + i + k * stride, v[k]);
+            for (int k = 0; k < 8; ++k)
+                if (i + k * 256u < n4) st_stream(d4 + i + k * 256u, v[k]);
         }
         done = n4 * 16u;
     }
@@ -482,7 +551,7 @@ int copy_segments(const CopyList& L, hipStream_t s)
     if (L.n == 0) return CR_OK;
     uint64_t most = 0;
     for (uint32_t i = 0; i < L.n; ++i) most = std::max(most, L.seg[i].bytes);
-    const uint64_t want = (most / 16u + 255u) / 256u;
+    const uint64_t want = (most / 16u + 2047u) / 2048u;  // 2048 16-byte vectors per workgroup step
     const uint32_t gx = static_cast<uint32_t>(std::max<uint64_t>(1, std::min<uint64_t>(want, 4096u)));
     cv_copy<<<dim3(gx, L.n), 256, 0, s>>>(L);
     CR_LAUNCH_CHECK();
