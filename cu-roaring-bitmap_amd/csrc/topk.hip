@@ -640,16 +640,36 @@ __global__ __launch_bounds__(TK_MERGE_NT) void tk_merge(TkArgs a, const float* l
     if (q >= n_q) return;  // whole wave; no block barrier below
     uint32_t n = 0;
     int cur = 0;
-    for (uint32_t c = 0; c < n_chunks; ++c) {
+    // The next chunk's list is loaded into registers (k <= 256: four entries a
+    // lane) while the current one is merged.
+    constexpr int PER = TK_KMAX / 64;
+    float nd[PER];
+    uint32_t ni[PER], nm = 0;
+    auto fetch = [&](uint32_t c) {
         const size_t row = static_cast<size_t>(c) * n_q + q;
         const uint32_t ln = list_n[row];
-        const uint32_t m = ln & 0x7FFFFFFFu;
-        if (m == 0) continue;
+        nm = ln & 0x7FFFFFFFu;
         const size_t base = (ln >> 31) * plane + row * k;
-        for (uint32_t i = lane; i < m; i += 64) {
-            cd[w][i] = list_d[base + i];
-            ci[w][i] = list_id[base + i];
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            const uint32_t i = lane + 64u * e;
+            nd[e] = i < nm ? list_d[base + i] : 0.f;
+            ni[e] = i < nm ? list_id[base + i] : 0u;
         }
+    };
+    if (n_chunks) fetch(0);
+    for (uint32_t c = 0; c < n_chunks; ++c) {
+        const uint32_t m = nm;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            const uint32_t i = lane + 64u * e;
+            if (i < m) {
+                cd[w][i] = nd[e];
+                ci[w][i] = ni[e];
+            }
+        }
+        if (c + 1 < n_chunks) fetch(c + 1);
+        if (m == 0) continue;
         __builtin_amdgcn_wave_barrier();
         for (uint32_t i = lane; i < n; i += 64) {
             const float x = ad[w][cur][i];
