@@ -339,9 +339,8 @@ __global__ __launch_bounds__(256) void ids_gather_pool(const uint16_t* keys, uin
 }
 
 // One workgroup per bucket: its 16 containers as 16 x 2048 u32 LDS words
-// (128 KiB), filled from the bucket's run in every tile.  Eight adjacent
-// buckets are dispatched to the same XCD (blocks go round-robin over the 8
-// XCDs), so the cache lines their runs share at run boundaries are L2 hits.
+// (128 KiB), filled from the bucket's run in every tile (the bucket order over
+// the XCDs is below).
 // Normal mode writes each present key's container to pool slot `key` (the
 // ranks come after) and every key's distinct count; complement mode writes
 // ~bits masked to [0, U) at the key_index rank of keys whose complement is
@@ -349,7 +348,12 @@ __global__ __launch_bounds__(256) void ids_gather_pool(const uint16_t* keys, uin
 constexpr int BUILD_NT = 1024;
 constexpr uint32_t BUILD_WAVES = BUILD_NT / 64;
 
-inline uint32_t build_grid(uint32_t nb) { return (nb + 63) / 64 * 64; }
+// Workgroups go round-robin over the 8 XCDs; XCD x takes the contiguous
+// bucket range [x * per, (x + 1) * per), in order, so almost every pair of
+// neighbouring buckets -- whose runs share the cache line at their boundary in
+// every tile -- runs on one XCD, close in time, and that line comes from its L2.
+__host__ __device__ inline uint32_t build_per_xcd(uint32_t nb) { return (nb + 7) / 8; }
+inline uint32_t build_grid(uint32_t nb) { return 8 * build_per_xcd(nb); }
 
 __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict__ part,
                                                       const uint16_t* __restrict__ tab, IdsGeom g, uint32_t universe,
@@ -359,8 +363,7 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
 {
     __shared__ uint32_t bits[BK_KEYS * 2048u];  // 128 KiB of the CU's 160 KiB LDS
     const uint32_t t = threadIdx.x;
-    const uint32_t xj = blockIdx.x / 8;
-    const uint32_t b = (xj / 8) * 64 + (blockIdx.x % 8) * 8 + xj % 8;
+    const uint32_t b = (blockIdx.x % 8) * build_per_xcd(g.NB) + blockIdx.x / 8;
     if (b >= g.NB) return;
     for (uint32_t i = t; i < BK_KEYS * 2048u; i += BUILD_NT) bits[i] = 0;
     __syncthreads();
