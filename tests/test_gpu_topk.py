@@ -117,6 +117,7 @@ CASES = [
     (70000, 520, 128, 10, "none", 1.0, 13),  # three query blocks
     (16384, 40, 128, 100, "none", 1.0, 14),  # the small-set limit exactly
     (16385, 40, 128, 100, "none", 1.0, 15),  # one row past it
+    (3000, 9, 64, 10, "keep", 0.0, 16),  # no passing row: every slot is (+inf, -1)
 ]
 
 
