@@ -354,6 +354,44 @@ __device__ __forceinline__ void tk_load_rows(const TkArgs& a, uint64_t row0, uin
     }
 }
 
+// The ids of a tile's rows (the passing-id list, or the row numbers), one per
+// (thread, pass) as tk_load_rows assigns them: loaded a tile earlier, so the
+// dependent row loads do not wait for them.
+template <int DP>
+__device__ __forceinline__ void tk_load_ids(const TkArgs& a, uint64_t row0, uint64_t row_end, uint32_t (&pid)[DP / 32])
+{
+    constexpr int TPR = DP / 4;
+    constexpr int RPP = TK_NT / TPR;
+#pragma unroll
+    for (int p = 0; p < DP / 32; ++p) {
+        const uint64_t r = row0 + static_cast<uint64_t>(p * RPP + threadIdx.x / TPR);
+        pid[p] = r < row_end ? (a.sel ? a.sel[r] : static_cast<uint32_t>(r)) : TK_NOID;
+    }
+}
+
+template <int DP>
+__device__ __forceinline__ void tk_load_rows_of(const TkArgs& a, const uint32_t (&pid)[DP / 32], float4 (&pre)[DP / 32])
+{
+    constexpr int TPR = DP / 4;
+    const uint32_t c = (threadIdx.x % TPR) * 4;
+#pragma unroll
+    for (int p = 0; p < DP / 32; ++p) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (pid[p] != TK_NOID) {
+            const float* src = a.base + static_cast<size_t>(pid[p]) * a.dim;
+            if (a.vec) {
+                if (c < a.dim) v = *reinterpret_cast<const float4*>(src + c);
+            } else {
+                if (c + 0 < a.dim) v.x = src[c + 0];
+                if (c + 1 < a.dim) v.y = src[c + 1];
+                if (c + 2 < a.dim) v.z = src[c + 2];
+                if (c + 3 < a.dim) v.w = src[c + 3];
+            }
+        }
+        pre[p] = v;
+    }
+}
+
 template <int DP, class Lds>
 __device__ __forceinline__ void tk_store_rows(Lds& L, int buf, const float4 (&pre)[DP / 32],
                                               const uint32_t (&pid)[DP / 32])
@@ -744,16 +782,22 @@ __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
     const float qg = (1.f - TK_GATE_ERR) * (qpart + __shfl_xor(qpart, 32, 64));
     if (chunk == 0 && h == 0 && qok) a.pq[q0 + j] = qg;
     float4 pre[DP / 32];
-    uint32_t pid[DP / 32];
+    uint32_t pid[DP / 32], nid[DP / 32];  // ids of the next tile, and of the one after it
     if (n_tiles > 0) {
         tk_load_rows<DP>(a, r0, r1, pre, pid);
         tk_store_rows<DP>(L, 0, pre, pid);
     }
+    tk_load_ids<DP>(a, r0 + TK_ROWS, r1, nid);
     __syncthreads();
-    uint32_t ulo = 0xFFFFFFFFu, uhi = 0;  // range of the upper bounds of this lane's rows
+    float ulo = __builtin_inff(), uhi = -__builtin_inff();  // range of the upper bounds of this lane's rows
     for (uint32_t t = 0; t < n_tiles; ++t) {
         const int b = static_cast<int>(t & 1u);
-        if (t + 1 < n_tiles) tk_load_rows<DP>(a, r0 + static_cast<uint64_t>(t + 1) * TK_ROWS, r1, pre, pid);
+        if (t + 1 < n_tiles) {
+#pragma unroll
+            for (int p = 0; p < DP / 32; ++p) pid[p] = nid[p];
+            tk_load_rows_of<DP>(a, pid, pre);
+            tk_load_ids<DP>(a, r0 + static_cast<uint64_t>(t + 2) * TK_ROWS, r1, nid);
+        }
         if (nq_wave > 0) {
             f32x16 acc0 = {}, acc1 = {};
             const float* A0 = &L.tile[b][j * (DP + 4) + h * (DP / 2)];
@@ -774,6 +818,7 @@ __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
             // Through LDS, so each store writes 64 consecutive rows of one query.
             float* E = L.est[wave];
             const uint64_t tr0 = r0 + static_cast<uint64_t>(t) * TK_ROWS;
+            const int rows = static_cast<int>(std::min<uint64_t>(TK_ROWS, r1 - tr0));  // rows of this tile
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row0 = tk_row(r, static_cast<int>(h)), row1 = tk_row(16 + r, static_cast<int>(h));
@@ -781,22 +826,23 @@ __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
                 const float e0 = qg + xg0 - 2.f * acc0[r], e1 = qg + xg1 - 2.f * acc1[r];
                 E[j * (TK_ROWS + 1) + row0] = e0;
                 E[j * (TK_ROWS + 1) + row1] = e1;
-                if (tr0 + row0 < r1) {
-                    const uint32_t u = tk_ordered(tk_upper(e0, qg, xg0));
-                    ulo = min(ulo, u);
-                    uhi = max(uhi, u);
+                if (row0 < rows) {
+                    const float u = tk_upper(e0, qg, xg0);
+                    ulo = fminf(ulo, u);
+                    uhi = fmaxf(uhi, u);
                 }
-                if (tr0 + row1 < r1) {
-                    const uint32_t u = tk_ordered(tk_upper(e1, qg, xg1));
-                    ulo = min(ulo, u);
-                    uhi = max(uhi, u);
+                if (row1 < rows) {
+                    const float u = tk_upper(e1, qg, xg1);
+                    ulo = fminf(ulo, u);
+                    uhi = fmaxf(uhi, u);
                 }
             }
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            const uint64_t gr = r0 + static_cast<uint64_t>(t) * TK_ROWS + lane;
-            for (uint32_t qq = 0; qq < nq_wave; ++qq)
-                if (gr < r1) a.pd[static_cast<size_t>(q0 + qq) * a.small_max + gr] = E[qq * (TK_ROWS + 1) + lane];
+            if (static_cast<int>(lane) < rows) {
+                float* dst = a.pd + static_cast<size_t>(q0) * a.small_max + tr0 + lane;
+                for (uint32_t qq = 0; qq < nq_wave; ++qq, dst += a.small_max) *dst = E[qq * (TK_ROWS + 1) + lane];
+            }
             __builtin_amdgcn_wave_barrier();
         }
         if (qb == 0 && wave == 0) {
@@ -806,11 +852,11 @@ __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
         if (t + 1 < n_tiles) tk_store_rows<DP>(L, b ^ 1, pre, pid);
         __syncthreads();
     }
-    ulo = min(ulo, static_cast<uint32_t>(__shfl_xor(ulo, 32, 64)));
-    uhi = max(uhi, static_cast<uint32_t>(__shfl_xor(uhi, 32, 64)));
-    if (h == 0 && qok && uhi != 0) {
-        atomicMin(a.qlo + q0 + j, ulo);
-        atomicMax(a.qhi + q0 + j, uhi);
+    ulo = fminf(ulo, __shfl_xor(ulo, 32, 64));
+    uhi = fmaxf(uhi, __shfl_xor(uhi, 32, 64));
+    if (h == 0 && qok && uhi >= ulo) {  // the lane pair saw at least one row
+        atomicMin(a.qlo + q0 + j, tk_ordered(ulo));
+        atomicMax(a.qhi + q0 + j, tk_ordered(uhi));
     }
 }
 
