@@ -22,6 +22,7 @@
 #include <cstring>
 
 #include "cu_roaring/device/roaring_view.hpp"
+#include "image.hpp"
 #include "internal.hpp"
 
 namespace crimpl {
@@ -94,36 +95,74 @@ __device__ __forceinline__ uint64_t lanemask_lt() { return (1ull << __lane_id())
 
 // ---- 1. passing ids ---------------------------------------------------------
 
+// A workgroup covers 8192 consecutive ids, a 256-word slice of one key's
+// container: the container is looked up once, and thread t takes word t of the
+// slice -- from the bitmap, or from the container's image built in LDS for an
+// array or run container -- complemented for a negated filter (contains()
+// answers `negated` for absent keys) and cut at n_base.
+static_assert(TK_ENUM_IDS == 32u * TK_ENUM_NT && 65536u % TK_ENUM_IDS == 0, "one word per thread, one key per block");
+
+__device__ uint32_t tk_enum_word(const GpuRoaringView& v, uint64_t n_base, uint32_t* img, int32_t* cover, int32_t* s_c)
+{
+    const uint32_t t = threadIdx.x;
+    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * TK_ENUM_IDS;
+    const uint32_t key = static_cast<uint32_t>(base >> 16);
+    if (v.key_index && key <= v.max_key) {
+        if (t == 0) {
+            const uint16_t e = v.key_index[key];
+            *s_c = e == 0xFFFFu ? -1 : static_cast<int32_t>(e);
+        }
+    } else if (key > v.max_key && v.key_index) {
+        if (t == 0) *s_c = -1;
+    } else if (t < 64) {
+        const uint32_t pos = wave_lower_bound_u16(v.keys, v.n_containers, key);
+        if (t == 0) *s_c = (pos < v.n_containers && v.keys[pos] == key) ? static_cast<int32_t>(pos) : -1;
+    }
+    __syncthreads();
+    const int32_t c = *s_c;
+    const uint32_t w0 = static_cast<uint32_t>(base & 0xFFFFu) >> 5;  // first word of the slice in the container
+    uint32_t word = 0;
+    const uint8_t type = c >= 0 ? static_cast<uint8_t>(v.types[c]) : uint8_t(0xFF);  // block-uniform
+    if (type == CR_BITMAP) {
+        word = reinterpret_cast<const uint32_t*>(v.bitmap_data + v.offsets[c] / 8u)[w0 + t];
+    } else if (type == CR_ARRAY || type == CR_RUN) {
+        expand_img<TK_ENUM_NT>(type, (type == CR_ARRAY ? v.array_data : v.run_data) + v.offsets[c] / 2u,
+                               v.cardinalities[c], img, cover);
+        word = img[w0 + t];
+    }
+    if (v.negated) word = ~word;
+    const uint64_t id0 = base + 32u * t;
+    if (id0 >= n_base) word = 0;
+    else if (n_base - id0 < 32u) word &= (1u << (n_base - id0)) - 1u;
+    return word;
+}
+
 __global__ __launch_bounds__(TK_ENUM_NT) void tk_enum_count(GpuRoaringView v, uint64_t n_base, uint32_t* counts)
 {
+    __shared__ alignas(16) uint32_t img[2048];
+    __shared__ int32_t cover[2048];
+    __shared__ int32_t s_c;
     __shared__ uint32_t red[TK_ENUM_NT / 64];
-    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * TK_ENUM_IDS;
-    uint32_t c = 0;
-    for (uint32_t i = 0; i < TK_ENUM_IDS / TK_ENUM_NT; ++i) {
-        const uint64_t id = base + i * TK_ENUM_NT + threadIdx.x;
-        c += (id < n_base && v.contains(static_cast<uint32_t>(id))) ? 1u : 0u;
-    }
-    c = block_sum<TK_ENUM_NT>(c, red);
+    const uint32_t c = block_sum<TK_ENUM_NT>(__popc(tk_enum_word(v, n_base, img, cover, &s_c)), red);
     if (threadIdx.x == 0) counts[blockIdx.x] = c;
 }
 
 __global__ __launch_bounds__(TK_ENUM_NT) void tk_enum_write(GpuRoaringView v, uint64_t n_base, const uint32_t* counts,
                                                             uint32_t* sel, uint32_t* n_sel)
 {
+    __shared__ alignas(16) uint32_t img[2048];
+    __shared__ int32_t cover[2048];
+    __shared__ int32_t s_c;
     __shared__ uint32_t red[TK_ENUM_NT / 64];
     uint32_t pre = 0;
     for (uint32_t i = threadIdx.x; i < blockIdx.x; i += TK_ENUM_NT) pre += counts[i];
-    uint32_t run = block_sum<TK_ENUM_NT>(pre, red);
-    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * TK_ENUM_IDS;
-    for (uint32_t i = 0; i < TK_ENUM_IDS / TK_ENUM_NT; ++i) {
-        const uint64_t id = base + i * TK_ENUM_NT + threadIdx.x;
-        const bool p = id < n_base && v.contains(static_cast<uint32_t>(id));
-        uint32_t tot;
-        const uint32_t r = block_flag_rank<TK_ENUM_NT>(p, red, tot);
-        if (p) sel[run + r] = static_cast<uint32_t>(id);
-        run += tot;
-    }
-    if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) *n_sel = run;
+    const uint32_t run = block_sum<TK_ENUM_NT>(pre, red);
+    const uint32_t word = tk_enum_word(v, n_base, img, cover, &s_c);
+    uint32_t tot;
+    uint32_t pos = run + block_excl_scan<TK_ENUM_NT>(__popc(word), red, tot);
+    const uint32_t id0 = static_cast<uint32_t>(static_cast<uint64_t>(blockIdx.x) * TK_ENUM_IDS) + 32u * threadIdx.x;
+    for (uint32_t x = word; x; x &= x - 1) sel[pos++] = id0 + static_cast<uint32_t>(__builtin_ctz(x));
+    if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) *n_sel = run + tot;
 }
 
 // ---- 2. distances and per-chunk selection ----------------------------------

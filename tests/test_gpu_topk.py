@@ -92,6 +92,16 @@ def _filter_from(gpu, kind, n_base, density, seed):
         mask[run_ids] = 1
         lt = orc.Lite.from_sorted_ids(run_ids).run_optimize()
         g = gpu.upload_containers(lt.containers(), 0, False, 0, orc.PROMOTE_KEEP_DEFAULT)
+    elif kind == "setop":  # a set-operation result: no key_index, max_key 0 (found by key search)
+        other = np.nonzero(rng.random(n_base) < 0.6)[0].astype(np.uint32)
+        ga = gpu.upload_from_ids(ids, n_base)
+        gb = gpu.upload_from_ids(other, n_base)
+        g = gpu.set_operation(ga, gb, gpu.AND)
+        gpu.free(ga)
+        gpu.free(gb)
+        assert not g.key_index
+        mask = np.zeros(n_base, np.uint8)
+        mask[np.intersect1d(ids, other)] = 1
     elif kind == "beyond":  # filter ids past n_base are ignored
         extra = np.arange(n_base, n_base + 5000, dtype=np.uint32)
         g = gpu.upload_from_ids(np.concatenate([ids, extra]), n_base + 70000)
@@ -118,6 +128,7 @@ CASES = [
     (16384, 40, 128, 100, "none", 1.0, 14),  # the small-set limit exactly
     (16385, 40, 128, 100, "none", 1.0, 15),  # one row past it
     (3000, 9, 64, 10, "keep", 0.0, 16),  # no passing row: every slot is (+inf, -1)
+    (60000, 20, 64, 10, "setop", 0.3, 17),
 ]
 
 
