@@ -911,6 +911,10 @@ constexpr int TK_SEL_NT = 1024;
 constexpr uint32_t TK_SEL_BINS = TK_SEL_NT;  // one histogram bin per thread
 constexpr uint32_t TK_SEL_CB = 8192;         // candidates per batch
 constexpr uint32_t TK_SEL_RPT = 4;           // rows per thread per candidate chunk
+// Rows whose upper bounds set the first bound: a larger sample costs reads, a
+// smaller one admits about k * rows / sample candidates, each a gathered row.
+constexpr uint32_t TK_SEL_SAMPLE = 16384;
+constexpr uint32_t TK_SEL_SAMPLE_PER_K = 1024;
 // Process-wide limit of the small-set path (cr_topk_set_small_limit).
 std::atomic<uint32_t> g_topk_small{TK_SMALL};
 
@@ -934,11 +938,13 @@ __global__ __launch_bounds__(TK_SEL_NT) void tk_select(TkArgs a, float* out_d, i
     for (uint32_t c = t; c < a.dim; c += TK_SEL_NT) qv[c] = a.queries[static_cast<size_t>(q) * a.dim + c];
     float bound = __builtin_inff();
     if (S > a.k) {
-        // A histogram of the upper bounds over their range: the bins spread
-        // the values, so the counting atomics rarely collide.  The first bin
-        // at which the count reaches k holds the k-th smallest upper bound;
-        // the largest value in the bins up to it is the bound (at least k rows
-        // lie at or below it, so the k-th distance does).
+        // A histogram of the upper bounds of the first TK_SEL_SAMPLE rows over
+        // the range of all of them: the bins spread the values, so the
+        // counting atomics rarely collide.  The first bin at which the count
+        // reaches k holds the sample's k-th smallest upper bound; the largest
+        // value in the bins up to it is the bound (at least k rows lie at or
+        // below it, so the k-th distance does).  A sample only loosens it.
+        const uint32_t Sn = min(S, max(TK_SEL_SAMPLE, TK_SEL_SAMPLE_PER_K * a.k));
         const float qg = a.pq[q];
         const float vlo = tk_unordered(a.qlo[q]), vhi = tk_unordered(a.qhi[q]);
         const float scale = vhi > vlo ? static_cast<float>(TK_SEL_BINS) / (vhi - vlo) : 0.f;
@@ -946,17 +952,17 @@ __global__ __launch_bounds__(TK_SEL_NT) void tk_select(TkArgs a, float* out_d, i
         bmax[t] = 0;
         if (t == 0) s_bound = 0;
         __syncthreads();
-        for (uint32_t r0 = t; r0 < S; r0 += 8 * TK_SEL_NT) {  // eight rows' loads in flight
+        for (uint32_t r0 = t; r0 < Sn; r0 += 8 * TK_SEL_NT) {  // eight rows' loads in flight
             float l8[8], x8[8];
 #pragma unroll
             for (uint32_t i = 0; i < 8; ++i) {
                 const uint32_t r = r0 + i * TK_SEL_NT;
-                l8[i] = r < S ? lrow[r] : 0.f;
-                x8[i] = r < S ? a.px[r] : 0.f;
+                l8[i] = r < Sn ? lrow[r] : 0.f;
+                x8[i] = r < Sn ? a.px[r] : 0.f;
             }
 #pragma unroll
             for (uint32_t i = 0; i < 8; ++i) {
-                if (r0 + i * TK_SEL_NT >= S) break;
+                if (r0 + i * TK_SEL_NT >= Sn) break;
                 const float u = tk_upper(l8[i], qg, x8[i]);
                 const float f = (u - vlo) * scale;
                 const uint32_t bin = f >= static_cast<float>(TK_SEL_BINS - 1) ? TK_SEL_BINS - 1
@@ -1058,6 +1064,7 @@ __global__ __launch_bounds__(TK_SEL_NT) void tk_select(TkArgs a, float* out_d, i
         nbatch = 0;
         if (t == 0) s_nbatch = 0;
         __syncthreads();
+        if (nb == a.k) bound = fminf(bound, bd[cur][a.k - 1]);  // the k-th best so far bounds the answer
     };
     // Candidates are few: a thread that finds one takes a batch slot with an
     // LDS atomic.  Chunks of TK_SEL_RPT rows per thread (loads in flight); a
