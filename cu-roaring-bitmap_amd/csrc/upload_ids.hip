@@ -361,11 +361,11 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
                                                       uint64_t* __restrict__ pool, uint16_t* cards,
                                                       uint32_t* key_count, IdsTotals* tot)
 {
-    __shared__ uint32_t bits[BK_KEYS * 2048u];  // 128 KiB of the CU's 160 KiB LDS
+    __shared__ alignas(16) uint32_t bits[BK_KEYS * 2048u];  // 128 KiB of the CU's 160 KiB LDS
     const uint32_t t = threadIdx.x;
     const uint32_t b = (blockIdx.x % 8) * build_per_xcd(g.NB) + blockIdx.x / 8;
     if (b >= g.NB) return;
-    for (uint32_t i = t; i < BK_KEYS * 2048u; i += BUILD_NT) bits[i] = 0;
+    for (uint32_t i = t; i < BK_KEYS * 512u; i += BUILD_NT) reinterpret_cast<uint4*>(bits)[i] = make_uint4(0, 0, 0, 0);
     __syncthreads();
     const uint32_t wave = t >> 6;
     const uint32_t lane = __lane_id();
@@ -453,22 +453,29 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
             valid_words = static_cast<uint32_t>(valid >> 5);
             tail_mask = (valid & 31u) ? ((1u << (valid & 31u)) - 1u) : 0u;
         }
-        for (uint32_t i = lane; i < 2048u; i += 64) {
-            uint32_t w = cb[i];
+        // The container is read from LDS once, as eight 16-byte vectors a lane.
+        uint4 v[8];
+        const uint4* src = reinterpret_cast<const uint4*>(cb);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            v[q] = src[lane + 64 * q];
             if (complement) {
-                w = ~w;
-                if (i >= valid_words) w = (i == valid_words) ? (w & tail_mask) : 0u;
-                cb[i] = w;
+                const uint32_t i0 = 4u * (lane + 64u * q);
+                uint32_t x[4] = {~v[q].x, ~v[q].y, ~v[q].z, ~v[q].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (i0 + e >= valid_words) x[e] = (i0 + e == valid_words) ? (x[e] & tail_mask) : 0u;
+                v[q] = make_uint4(x[0], x[1], x[2], x[3]);
             }
-            pc += __popc(w);
+            pc += __popc(v[q].x) + __popc(v[q].y) + __popc(v[q].z) + __popc(v[q].w);
         }
         pc = wave_sum(pc);
         if (!complement && lane == 0) key_count[key] = pc;
         if (pc != 0) {
             const uint32_t slot = complement ? key_index[key] : key;
             uint4* dst = reinterpret_cast<uint4*>(pool + static_cast<uint64_t>(slot) * 1024u);
-            const uint4* src = reinterpret_cast<const uint4*>(cb);
-            for (uint32_t i = lane; i < 512u; i += 64) st_stream(dst + i, src[i]);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) st_stream(dst + lane + 64 * q, v[q]);
             if (complement && lane == 0) cards[slot] = static_cast<uint16_t>(pc > 65535u ? 0u : pc);
         }
     }
