@@ -75,8 +75,10 @@ def make_ids(torch, seed=10):
 def upload_kernel_bytes(name, n, n_c, max_key):
     """Algorithmic bytes per launch of each upload kernel."""
     return {
-        "ids_tile_sort": 8 * n,                     # read every id, write it back bucket-sorted within its tile
-        "ids_build": 4 * n + 8192 * n_c + 4 * n_c,  # read the sorted ids, write containers + per-key counts
+        # read every id (4 B), write it back bucket-sorted within its tile as a 20-bit field (2.5 B)
+        "ids_tile_sort": 4 * n + 5 * n // 2,
+        # read the packed fields, write containers + per-key counts
+        "ids_build": 5 * n // 2 + 8192 * n_c + 4 * n_c,
     }.get(name)
 
 

@@ -7,15 +7,16 @@
 // 1024 ids follow the threshold-aware small path (:421-561).
 //
 // The large path needs no global sort.  Ids are grouped by 16-key bucket
-// (1 MiB of id space) inside 16384-id tiles, each bucket's 16 containers are
+// (1 MiB of id space) inside 24576-id tiles, each bucket's 16 containers are
 // built as 128 KiB of LDS bitmaps (the bit-set dedupes), and each container is
 // written once:
 //   tile_sort   read the ids once; counting-sort each tile by bucket in LDS and
-//               stream it back to the tile's own slot, with the tile's bucket
-//               starts in a small table; max id per workgroup
+//               stream it back to the tile's own slot as 20-bit fields (the id
+//               within its bucket), with the tile's bucket starts in a small
+//               table; max id per workgroup
 //   build       one workgroup per bucket: read the bucket's run of every tile
-//               (~16 ids at 2^30), LDS bit-set, popcount, write each present
-//               key's container to pool slot `key`
+//               (~24 fields, 60 bytes, at 2^30), LDS bit-set, popcount, write
+//               each present key's container to pool slot `key`
 //   rank        key ranks from the build's counts ->
 //               keys/types/offsets/cards/key_index, totals, range error
 // When the present keys are not a prefix of the key space, one more step
@@ -31,8 +32,16 @@ constexpr uint32_t BK_SHIFT = 4;               // 16 keys per bucket
 constexpr uint32_t BK_KEYS = 1u << BK_SHIFT;
 constexpr uint32_t MAX_BUCKETS = 65536 / BK_KEYS;
 constexpr int TS_NT = 1024;                    // tile-sort workgroup
-constexpr uint32_t TS_PER = 16;                // ids per thread per tile
-constexpr uint32_t TILE = TS_NT * TS_PER;      // 16384 ids: 64 KiB of LDS
+constexpr uint32_t TS_PER = 24;                // ids per thread per tile
+constexpr uint32_t TILE = TS_NT * TS_PER;      // 24576 ids: 96 KiB of LDS
+// A sorted tile is stored as a bit stream of 20-bit fields, id & 0xFFFFF (the
+// bucket is implied by the field's run): field i occupies bits [20 i, 20 i + 20)
+// of the tile's slot of TILE_WORDS u32, 2.5 bytes an id.
+constexpr uint32_t FIELD_BITS = 16 + BK_SHIFT;
+constexpr uint32_t FIELD_MASK = (1u << FIELD_BITS) - 1u;
+constexpr uint32_t TILE_WORDS = TILE * FIELD_BITS / 32;
+static_assert(TILE_WORDS % 4 == 0, "tile slots hold whole 16-byte vectors");
+static_assert(TILE <= 65535, "run starts are u16");
 // Run table: tiles are grouped in blocks of TB; entry (block, bucket, slot) is
 // the start of the bucket in tile block*TB + slot, so one bucket's starts for
 // a block are TB contiguous u16 (the build reads a bucket's column).  The tile
@@ -58,9 +67,9 @@ struct IdsGeom {
 };
 
 // Each workgroup takes blocks of TB tiles.  A tile is counting-sorted by
-// bucket in LDS and written back to its own slot of `part` (tile t at
-// t * TILE), a streaming write; `tab` row t holds the tile's bucket starts
-// (NB + 1 u16).  An id whose bucket lies past the universe's last goes to a
+// bucket in LDS and written back to its own slot of `part` (tile t at word
+// t * TILE_WORDS) as packed fields, a streaming write; `tab` row t holds the
+// tile's bucket starts (NB + 1 u16, in fields).  An id whose bucket lies past the universe's last goes to a
 // sentinel bucket NB that is sorted after the others and neither written nor
 // built; the error is raised from the maximum id, which each workgroup
 // reports.  Every lane holds an id: a partial last tile is padded with ids of
@@ -121,8 +130,8 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
             return rem < TILE;
         }
     };
-    // The next tile's ids are loaded while the current tile is ranked,
-    // scanned, scattered and written.
+    // The next tile's ids are loaded into the same registers once the current
+    // tile is scattered, while it is packed and written.
     uint32_t v[TS_PER];
     bool partial = false;
     // Workgroup g takes blocks g, g + G, ...; `next` steps through them.
@@ -131,7 +140,6 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
     const uint32_t first = blockIdx.x * TB;
     if (first < g.n_tiles) partial = load_ids(first, v);
     for (uint32_t tile = first; tile < g.n_tiles; tile = next(tile)) {
-        const uint64_t base = static_cast<uint64_t>(tile) * TILE;
         for (uint32_t i = t; i <= NB; i += TS_NT) cnt[i] = 0;
         __syncthreads();
         if (!partial) {
@@ -140,7 +148,7 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         }
         // Ranks within the tile.  When every id of the wave's pass falls in
         // one bucket (clustered ids), a single atomic reserves them all.
-        uint32_t rk[TS_PER / 2];  // tile ranks (< 16384) packed two per register
+        uint32_t rk[TS_PER / 2];  // tile ranks (< 24576) packed two per register
         const uint32_t b00 = __builtin_amdgcn_readfirstlane(bucket(v[0]));
         bool diff = false;
 #pragma unroll
@@ -161,9 +169,6 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
                     rk[j >> 1] = r;
             }
         }
-        uint32_t vn[TS_PER];
-        bool partial_n = false;
-        if (next(tile) < g.n_tiles) partial_n = load_ids(next(tile), vn);
         __syncthreads();
         constexpr uint32_t BPT = MAX_BUCKETS / TS_NT;  // buckets scanned per thread
         uint32_t cv[BPT], cs = 0;
@@ -175,36 +180,60 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         }
         uint32_t total;  // ids of the real buckets; the sentinel's follow
         uint32_t st = block_excl_scan<TS_NT>(cs, lds, total);
+        // Bases, and the tile's column of the run table.
+        uint16_t* trow_col = staged ? reinterpret_cast<uint16_t*>(stage) + tile % TB
+                                    : tab + static_cast<uint64_t>(tile / TB) * (NB + 1) * TB + tile % TB;
 #pragma unroll
         for (uint32_t q = 0; q < BPT; ++q) {
             const uint32_t bq = t * BPT + q;
-            if (bq < NB) cnt[bq] = st;
+            if (bq < NB) {
+                cnt[bq] = st;
+                trow_col[static_cast<uint64_t>(bq) * TB] = static_cast<uint16_t>(st);
+            }
             st += cv[q];
         }
-        if (t == 0) cnt[NB] = total;
-        __syncthreads();
-        if (staged) {
-            uint16_t* sc = reinterpret_cast<uint16_t*>(stage) + tile % TB;
-            for (uint32_t i = t; i <= NB; i += TS_NT) sc[i * TB] = static_cast<uint16_t>(cnt[i]);
-        } else {
-            uint16_t* tcol = tab + static_cast<uint64_t>(tile / TB) * (NB + 1) * TB + tile % TB;
-            for (uint32_t i = t; i <= NB; i += TS_NT) tcol[static_cast<uint64_t>(i) * TB] = static_cast<uint16_t>(cnt[i]);
+        if (t == 0) {
+            cnt[NB] = total;
+            trow_col[static_cast<uint64_t>(NB) * TB] = static_cast<uint16_t>(total);
         }
+        __syncthreads();
 #pragma unroll
         for (uint32_t j = 0; j < TS_PER; ++j)
             buf[cnt[bucket(v[j])] + ((rk[j >> 1] >> ((j & 1u) * 16)) & 0xFFFFu)] = v[j];
         __syncthreads();
+        if (next(tile) < g.n_tiles) partial = load_ids(next(tile), v);
         if (staged && (tile % TB == TB - 1 || tile + 1 == g.n_tiles)) {  // the block's rows, contiguous
             uint4* trow = reinterpret_cast<uint4*>(tab + static_cast<uint64_t>(tile / TB) * (NB + 1) * TB);
             for (uint32_t i = t; i <= NB; i += TS_NT) trow[i] = stage[i];
         }
-        uint32_t* dst = part + base;
-        const uint32_t n4 = total >> 2;
-        for (uint32_t p = t; p < n4; p += TS_NT) st_stream(reinterpret_cast<uint4*>(dst) + p, reinterpret_cast<const uint4*>(buf)[p]);
-        for (uint32_t p = 4 * n4 + t; p < total; p += TS_NT) dst[p] = buf[p];
+        // Packing in place: thread g turns fields [8 g, 8 g + 8) (two 16-byte
+        // LDS reads) into words [5 g, 5 g + 5) of the stream, which overwrite
+        // the tile's front after a barrier; then the 16-byte vectors holding
+        // real buckets' fields stream out.
+        static_assert(FIELD_BITS == 20 && TILE % (8 * TS_NT) == 0, "8 fields -> 5 words, whole passes");
+        constexpr uint32_t GPT = TILE / (8 * TS_NT);  // 8-field groups per thread
+        uint32_t pw[GPT][5];
 #pragma unroll
-        for (uint32_t j = 0; j < TS_PER; ++j) v[j] = vn[j];
-        partial = partial_n;
+        for (uint32_t k = 0; k < GPT; ++k) {
+            const uint4* src = reinterpret_cast<const uint4*>(buf) + 2u * (t + k * TS_NT);
+            const uint4 a = src[0], c = src[1];
+            const uint32_t f0 = a.x & FIELD_MASK, f1 = a.y & FIELD_MASK, f2 = a.z & FIELD_MASK, f3 = a.w & FIELD_MASK;
+            const uint32_t f4 = c.x & FIELD_MASK, f5 = c.y & FIELD_MASK, f6 = c.z & FIELD_MASK, f7 = c.w & FIELD_MASK;
+            pw[k][0] = f0 | (f1 << 20);
+            pw[k][1] = (f1 >> 12) | (f2 << 8) | (f3 << 28);
+            pw[k][2] = (f3 >> 4) | (f4 << 16);
+            pw[k][3] = (f4 >> 16) | (f5 << 4) | (f6 << 24);
+            pw[k][4] = (f6 >> 8) | (f7 << 12);
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t k = 0; k < GPT; ++k)
+#pragma unroll
+            for (uint32_t q = 0; q < 5u; ++q) buf[5u * (t + k * TS_NT) + q] = pw[k][q];
+        __syncthreads();
+        uint4* dst = reinterpret_cast<uint4*>(part + static_cast<uint64_t>(tile) * TILE_WORDS);
+        const uint32_t n4 = (FIELD_BITS * total + 127u) >> 7;
+        for (uint32_t u = t; u < n4; u += TS_NT) st_stream(dst + u, reinterpret_cast<const uint4*>(buf)[u]);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(mx, o, 64)));
@@ -375,8 +404,11 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
     // Wave w owns tile blocks w, w + 16, ...; a step covers 64 / TB of them
     // (one tile per lane, its run bounds loaded a step ahead: the TB lanes of
     // a block read TB contiguous u16).  Each 4-lane group reads four tiles'
-    // runs as 16-id windows with 16-byte loads aligned down to 4 ids, and the
-    // loads of the first two windows are all issued before any bit is set.
+    // runs as 16-word windows (64 bytes, 25.6 fields) with 16-byte loads
+    // aligned down to 4 words, and the loads of the first two windows are all
+    // issued before any bit is set.  A lane takes the fields that start in its
+    // 4 words; one that ends past them takes its last bits from the next
+    // word: the next lane's first, or for the group's last lane one more load.
     constexpr uint32_t BPS = 64u / TB;  // blocks per step
     const uint32_t per_wave = n_blk > wave ? (n_blk - wave + BUILD_WAVES - 1) / BUILD_WAVES : 0u;
     auto tile_of = [&](uint32_t st, uint32_t l) { return (wave + BUILD_WAVES * (st * BPS + l / TB)) * TB + l % TB; };
@@ -391,13 +423,33 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
             r1 = tc[TB];
         }
     };
-    auto set_window = [&](const uint4& x, uint32_t lo, uint32_t s0, uint32_t s1) {
-        const uint32_t e4[4] = {x.x, x.y, x.z, x.w};
+    // Fields of [s0, s1) starting in words lo_w .. lo_w + 3 (x), with c4 =
+    // word lo_w + 4.  The first starts o < 20 bits in; after a funnel shift by
+    // o, field m sits at bit 20 m (m = 6 only when o < 8).
+    auto set_chunk = [&](const uint4& x, uint32_t c4, uint32_t lo_w, uint32_t s0, uint32_t s1) {
+        static_assert(FIELD_BITS == 20, "the unpacking below assumes 20-bit fields");
+        const uint32_t C = 32u * lo_w;
+        const uint32_t i0 = (C + FIELD_BITS - 1u) / FIELD_BITS;
+        const uint32_t o = FIELD_BITS * i0 - C;
+        const uint32_t d0 = __builtin_amdgcn_alignbit(x.y, x.x, o);
+        const uint32_t d1 = __builtin_amdgcn_alignbit(x.z, x.y, o);
+        const uint32_t d2 = __builtin_amdgcn_alignbit(x.w, x.z, o);
+        const uint32_t d3 = __builtin_amdgcn_alignbit(c4, x.w, o);
+        const uint32_t d4 = c4 >> o;
+        const uint32_t f[7] = {d0,
+                               __builtin_amdgcn_alignbit(d1, d0, 20),
+                               d1 >> 8,
+                               __builtin_amdgcn_alignbit(d2, d1, 28),
+                               __builtin_amdgcn_alignbit(d3, d2, 16),
+                               d3 >> 4,
+                               __builtin_amdgcn_alignbit(d4, d3, 24)};
 #pragma unroll
-        for (uint32_t e = 0; e < 4u; ++e) {
-            const uint32_t pos = lo + e;
-            if (pos >= s0 && pos < s1)
-                atomicOr(&bits[((e4[e] >> 16) & (BK_KEYS - 1)) << 11 | ((e4[e] & 0xFFFFu) >> 5)], 1u << (e4[e] & 31u));
+        for (uint32_t m = 0; m < 7u; ++m) {
+            const uint32_t i = i0 + m;
+            if (i >= s0 && i < s1 && (m < 6u || o < 8u)) {
+                const uint32_t F = f[m] & FIELD_MASK;  // key-in-bucket << 16 | low 16 bits
+                atomicOr(&bits[F >> 5], 1u << (F & 31u));
+            }
         }
     };
     uint32_t n0, n1;
@@ -405,37 +457,53 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
     for (uint32_t st = 0; st * BPS < per_wave; ++st) {
         const uint32_t m0 = n0, m1 = n1;
         tab_load(st + 1, n0, n1);
-        uint32_t nw = m1 > m0 ? (m1 - (m0 & ~3u) + 15u) >> 4 : 0u;  // 16-id windows of this lane's tile
+        // windows from the 16-byte-aligned word holding field m0 to the last
+        // word holding the run's bits
+        uint32_t nw = m1 > m0 ? (((FIELD_BITS * m1 - 1u) >> 5) - (((FIELD_BITS * m0) >> 5) & ~3u)) / 16u + 1u : 0u;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) nw = max(nw, static_cast<uint32_t>(__shfl_xor(nw, o, 64)));
-        uint32_t ts0[4], ts1[4], tb[4];
+        uint32_t ts0[4], ts1[4], tb[4], wb[4], we[4];
 #pragma unroll
         for (uint32_t h = 0; h < 4u; ++h) {
             const uint32_t src = 16u * h + grp;
             ts0[h] = __shfl(m0, static_cast<int>(src), 64);
             ts1[h] = __shfl(m1, static_cast<int>(src), 64);
-            tb[h] = tile_of(st, src) * TILE;  // n < 2^32 (tiles past the end have empty runs)
+            tb[h] = tile_of(st, src) * TILE_WORDS;  // < 2^32 words for n < 2^32 (past the end: empty runs)
+            wb[h] = ((FIELD_BITS * ts0[h]) >> 5) & ~3u;
+            we[h] = ts1[h] > ts0[h] ? (FIELD_BITS * ts1[h] - 1u) >> 5 : 0u;
         }
+        // A lane loads when its first word holds run bits (lo_w <= we, so its
+        // 4 words stay in the tile's written vectors); the last lane's extra
+        // word only when the run reaches it.
+        auto window = [&](uint32_t h, uint32_t k, uint4& x, uint32_t& e) {
+            const uint32_t lo_w = wb[h] + 16u * k + 4u * r4;
+            const bool act = ts1[h] > ts0[h] && lo_w <= we[h];
+            x = act ? *reinterpret_cast<const uint4*>(part + tb[h] + lo_w) : make_uint4(0, 0, 0, 0);
+            e = (act && r4 == 3u && lo_w + 4u <= we[h]) ? part[tb[h] + lo_w + 4u] : 0u;
+        };
         {
             uint4 x[4][2];
+            uint32_t e[4][2];
+#pragma unroll
+            for (uint32_t h = 0; h < 4u; ++h)
+#pragma unroll
+                for (uint32_t k = 0; k < 2u; ++k) window(h, k, x[h][k], e[h][k]);
 #pragma unroll
             for (uint32_t h = 0; h < 4u; ++h)
 #pragma unroll
                 for (uint32_t k = 0; k < 2u; ++k) {
-                    const uint32_t lo = (ts0[h] & ~3u) + 16u * k + 4u * r4;
-                    x[h][k] = lo < ts1[h] ? *reinterpret_cast<const uint4*>(part + tb[h] + lo) : make_uint4(0, 0, 0, 0);
+                    const uint32_t nx = __shfl_down(x[h][k].x, 1, 64);
+                    set_chunk(x[h][k], r4 == 3u ? e[h][k] : nx, wb[h] + 16u * k + 4u * r4, ts0[h], ts1[h]);
                 }
-#pragma unroll
-            for (uint32_t h = 0; h < 4u; ++h)
-#pragma unroll
-                for (uint32_t k = 0; k < 2u; ++k)
-                    set_window(x[h][k], (ts0[h] & ~3u) + 16u * k + 4u * r4, ts0[h], ts1[h]);
         }
         for (uint32_t k = 2; k < nw; ++k) {  // runs longer than two windows (clustered ids)
 #pragma unroll
             for (uint32_t h = 0; h < 4u; ++h) {
-                const uint32_t lo = (ts0[h] & ~3u) + 16u * k + 4u * r4;
-                if (lo < ts1[h]) set_window(*reinterpret_cast<const uint4*>(part + tb[h] + lo), lo, ts0[h], ts1[h]);
+                uint4 x;
+                uint32_t e;
+                window(h, k, x, e);
+                const uint32_t nx = __shfl_down(x.x, 1, 64);
+                set_chunk(x, r4 == 3u ? e : nx, wb[h] + 16u * k + 4u * r4, ts0[h], ts1[h]);
             }
         }
     }
@@ -778,7 +846,7 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     const size_t o_tab =
         c.add(sizeof(uint16_t) * static_cast<uint64_t>((g.n_tiles + TB - 1) / TB) * TB * (g.NB + 1));
     // Whole tiles (a partial last tile is padded) + the build's window overrun.
-    const size_t o_part = c.add(sizeof(uint32_t) * (static_cast<uint64_t>(g.n_tiles) * TILE + 4));
+    const size_t o_part = c.add(sizeof(uint32_t) * (static_cast<uint64_t>(g.n_tiles) * TILE_WORDS + 4));
     Scratch sc;
     CR_RET(sc.alloc(c.total, s));
     uint32_t* gmax = sc.at<uint32_t>(o_gmax);
