@@ -130,8 +130,11 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
             return rem < TILE;
         }
     };
-    // The next tile's ids are loaded into the same registers once the current
-    // tile is scattered, while it is packed and written.
+    // The next tile's ids: the first half is loaded while the current tile is
+    // scanned and scattered (into registers of its own), the second half once
+    // the current tile's ids are in LDS, while it is packed and written.  (All
+    // of it early would hold 48 ids a lane with the ranks, which spills, and a
+    // spill reload waits for every outstanding load.)
     uint32_t v[TS_PER];
     bool partial = false;
     // Workgroup g takes blocks g, g + G, ...; `next` steps through them.
@@ -169,6 +172,19 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
                     rk[j >> 1] = r;
             }
         }
+        // First half of the next tile's ids, when it is a whole aligned tile
+        // (a partial or unaligned one is loaded late, by load_ids).
+        const uint32_t nt = next(tile);
+        const bool nfull = nt < g.n_tiles && g.vec && static_cast<uint64_t>(nt + 1) * TILE <= g.n;
+        uint32_t vh[TS_PER / 2];
+        if (nfull) {
+            const uint4* src = reinterpret_cast<const uint4*>(ids + static_cast<uint64_t>(nt) * TILE);
+#pragma unroll
+            for (uint32_t q = 0; q < TS_PER / 8; ++q) {
+                const uint4 a = ld_stream(src + t + q * TS_NT);
+                vh[4 * q + 0] = a.x, vh[4 * q + 1] = a.y, vh[4 * q + 2] = a.z, vh[4 * q + 3] = a.w;
+            }
+        }
         __syncthreads();
         constexpr uint32_t BPT = MAX_BUCKETS / TS_NT;  // buckets scanned per thread
         uint32_t cv[BPT], cs = 0;
@@ -198,10 +214,27 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         }
         __syncthreads();
 #pragma unroll
-        for (uint32_t j = 0; j < TS_PER; ++j)
-            buf[cnt[bucket(v[j])] + ((rk[j >> 1] >> ((j & 1u) * 16)) & 0xFFFFu)] = v[j];
+        for (uint32_t j = 0; j < TS_PER; ++j) {
+            uint32_t x = v[j];
+            // An empty asm hides x's origin, so the bucket address is computed
+            // again here instead of being kept in registers since the ranking.
+            asm volatile("" : "+v"(x));
+            buf[cnt[bucket(x)] + ((rk[j >> 1] >> ((j & 1u) * 16)) & 0xFFFFu)] = x;
+        }
         __syncthreads();
-        if (next(tile) < g.n_tiles) partial = load_ids(next(tile), v);
+        if (nfull) {
+            const uint4* src = reinterpret_cast<const uint4*>(ids + static_cast<uint64_t>(nt) * TILE);
+#pragma unroll
+            for (uint32_t q = TS_PER / 8; q < TS_PER / 4; ++q) {
+                const uint4 a = ld_stream(src + t + q * TS_NT);
+                v[4 * q + 0] = a.x, v[4 * q + 1] = a.y, v[4 * q + 2] = a.z, v[4 * q + 3] = a.w;
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < TS_PER / 2; ++j) v[j] = vh[j];
+            partial = false;
+        } else if (nt < g.n_tiles) {
+            partial = load_ids(nt, v);
+        }
         if (staged && (tile % TB == TB - 1 || tile + 1 == g.n_tiles)) {  // the block's rows, contiguous
             uint4* trow = reinterpret_cast<uint4*>(tab + static_cast<uint64_t>(tile / TB) * (NB + 1) * TB);
             for (uint32_t i = t; i <= NB; i += TS_NT) trow[i] = stage[i];
