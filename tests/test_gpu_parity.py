@@ -40,6 +40,12 @@ ID_CASES = [
     (200000, 1 << 24, orc.PROMOTE_KEEP_DEFAULT, 8),
     (300000, 1 << 30, orc.PROMOTE_AUTO, 9),
     (50000, 0xFFFFFFFF, orc.PROMOTE_AUTO, 10),
+    # around the GPU path's 24576-id tiles and its blocks of 8 tiles
+    (24576, 1 << 26, orc.PROMOTE_AUTO, 11),
+    (24577, 1 << 26, orc.PROMOTE_AUTO, 12),
+    (24576 * 2 + 5, 1 << 24, orc.PROMOTE_AUTO, 13),
+    (24576 * 8 + 1, 1 << 28, orc.PROMOTE_AUTO, 14),
+    (24576 * 9 - 1, 1 << 30, orc.PROMOTE_KEEP_DEFAULT, 15),
 ]
 
 
@@ -137,7 +143,7 @@ def test_upload_from_ids_rejects_keys_past_the_last_bucket(gpu, bad_key):
     assert e.value.code == 2
 
 
-@pytest.mark.parametrize("n", [16384 * 3 + 5, 16384 * 9])
+@pytest.mark.parametrize("n", [16384 * 3 + 5, 24576 * 3 + 5, 24576 * 9])
 def test_upload_from_ids_unaligned_pointer(gpu, n):
     """A device pointer 4 bytes past a 16-byte boundary takes the scalar load
     path, with and without a partial last tile."""
