@@ -55,6 +55,7 @@ struct IdsTotals {
     uint32_t max_id;
     uint32_t moved;  // present keys are not a prefix: the pool needs compaction
     unsigned long long total;  // distinct ids (or complement count)
+    uint32_t done;  // rank workgroups finished
 };
 
 struct IdsGeom {
@@ -94,6 +95,9 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         if (blockIdx.x == 0) {  // the build accumulates the distinct count
             tot->total = 0;
             tot->moved = 0;
+            tot->n_containers = 0;  // the rank workgroups accumulate these
+            tot->max_id = 0;
+            tot->done = 0;
         }
     }
     uint32_t mx = 0;
@@ -275,111 +279,86 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
     if (t == 0) gmax[blockIdx.x] = s_max;  // per-workgroup partials: nothing here needs zeroed memory
 }
 
-// Key ranks after the build, in one workgroup.  Round j covers keys
-// [1024 j, 1024 j + 1024), one per thread, with coalesced loads (eight rounds
-// in flight); a key is present iff the build counted a bit in it.  Ranks come
-// from per-wave ballots: each wave's count per round goes to LDS, one pass
-// turns them into wave and round bases, and a second pass over the rounds
-// writes keys/types/offsets/cards in rank order and the full key_index
-// (0xFFFF = absent).  The totals -- container count, the range error (from the
-// tile-sort workgroups' maximum ids), the distinct count the build accumulated,
-// and `moved` when a present key's rank differs from the key (the build wrote
-// container k to pool slot k) -- go to `tot` and to the caller's pinned host
-// slot.
-constexpr uint32_t RANK_ROUNDS = 65536 / 1024;
-
+// Key ranks after the build: workgroup r ranks the 1024 keys of round r,
+// [1024 r, 1024 r + 1024), one per thread.  A key is present iff the build
+// counted a bit in it.  The present keys of the earlier rounds are counted
+// again by every workgroup (coalesced loads, eight rounds in flight, at most
+// 63 rounds), so no workgroup waits for another.  Each writes its present
+// keys' keys/types/offsets/cards at their ranks and its round of key_index
+// (0xFFFF = absent), and adds its count and `moved` (a present key whose rank
+// differs from the key: the build wrote container k to pool slot k) to `tot`;
+// workgroup 0 adds the tile-sort workgroups' maximum id.  The last workgroup
+// to finish (a counter, no waiting) writes the totals -- with the range error
+// from the maximum id and the distinct count the build accumulated -- to `tot`
+// and to the caller's pinned host slot.
 __global__ __launch_bounds__(1024) void ids_rank(IdsGeom g, const uint32_t* key_count, const uint32_t* gmax,
                                                  uint16_t* keys, uint8_t* types, uint32_t* offsets, uint16_t* cards,
                                                  uint16_t* key_index, IdsTotals* tot, IdsTotals* host)
 {
-    __shared__ uint32_t wcnt[RANK_ROUNDS][16];  // present keys per (round, wave), then the wave's base
-    __shared__ uint32_t rbase[RANK_ROUNDS + 1];
+    __shared__ uint32_t lds[16];
     __shared__ uint32_t s_max;
-    const uint32_t t = threadIdx.x, wave = t >> 6, lane = __lane_id();
-    const uint32_t rounds = (g.K + 1023u) / 1024u;
+    __shared__ bool s_last;
+    const uint32_t t = threadIdx.x, lane = __lane_id();
+    const uint32_t r = blockIdx.x;
     if (t == 0) s_max = 0;
-    uint64_t mine = 0;  // bit j: this thread's key of round j is present
-    for (uint32_t j0 = 0; j0 < rounds; j0 += 8) {
+    // Rounds before r are whole (only the last round can be partial).
+    uint32_t before = 0;
+    for (uint32_t j0 = 0; j0 < r; j0 += 8) {
         uint32_t c[8];
 #pragma unroll
-        for (uint32_t q = 0; q < 8; ++q) {
-            const uint32_t k = (j0 + q) * 1024u + t;
-            c[q] = (j0 + q < rounds && k < g.K) ? key_count[k] : 0u;
-        }
+        for (uint32_t q = 0; q < 8; ++q) c[q] = j0 + q < r ? key_count[(j0 + q) * 1024u + t] : 0u;
 #pragma unroll
-        for (uint32_t q = 0; q < 8; ++q) {
-            if (j0 + q >= rounds) break;
-            const uint64_t m = __ballot(c[q] != 0u);
-            if (c[q] != 0u) mine |= 1ull << (j0 + q);
-            if (lane == 0) wcnt[j0 + q][wave] = static_cast<uint32_t>(__popcll(m));
-        }
+        for (uint32_t q = 0; q < 8; ++q) before += c[q] != 0u ? 1u : 0u;
     }
-    uint32_t mx = 0;
-    for (uint32_t k = t; k < g.G; k += 1024u) mx = max(mx, gmax[k]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(mx, o, 64)));
-    __syncthreads();  // s_max is initialised
-    if (lane == 0) atomicMax(&s_max, mx);
-    // Thread j (< rounds) sums round j; one wave scans the rounds; thread
-    // (round, wave) turns its count into the wave's base within the round.
-    uint32_t wprefix = 0, rtotal = 0;
-    if (t < rounds * 16u) {
-        const uint32_t j = t >> 4, w = t & 15u;
-        for (uint32_t v = 0; v < w; ++v) wprefix += wcnt[j][v];
-        if (w == 15u) rtotal = wprefix + wcnt[j][15];
-    }
-    __syncthreads();
-    if (t < rounds * 16u) {
-        wcnt[t >> 4][t & 15u] = wprefix;
-        if ((t & 15u) == 15u) rbase[(t >> 4) + 1] = rtotal;
-    }
-    if (t == 0) rbase[0] = 0;
-    __syncthreads();
-    if (t == 0)
-        for (uint32_t j = 1; j <= rounds; ++j) rbase[j] += rbase[j - 1];
-    __syncthreads();
+    const uint32_t base = block_sum<1024>(before, lds);
+    const uint32_t k = r * 1024u + t;
+    const uint32_t c = k < g.K ? key_count[k] : 0u;
+    const bool present = c != 0u;
+    uint32_t count;
+    const uint32_t rank = base + block_flag_rank<1024>(present, lds, count);
     bool moved = false;
-    for (uint32_t j0 = 0; j0 < rounds; j0 += 8) {
-        uint32_t c[8];  // the counts again (cache hits), eight rounds in flight
-#pragma unroll
-        for (uint32_t q = 0; q < 8; ++q) c[q] = ((mine >> (j0 + q)) & 1ull) ? key_count[(j0 + q) * 1024u + t] : 0u;
-#pragma unroll
-        for (uint32_t q = 0; q < 8; ++q) {
-            const uint32_t j = j0 + q;
-            if (j >= rounds) break;
-            const uint32_t k = j * 1024u + t;
-            const bool present = (mine >> j) & 1ull;
-            const uint64_t m = __ballot(present);
-            if (present) {
-                const uint32_t rank =
-                    rbase[j] + wcnt[j][wave] + static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull)));
-                keys[rank] = static_cast<uint16_t>(k);
-                types[rank] = CR_BITMAP;
-                offsets[rank] = rank * 8192u;
-                cards[rank] = static_cast<uint16_t>(c[q] > 65535u ? 0u : c[q]);  // 65536 stored as 0
-                key_index[k] = static_cast<uint16_t>(rank);
-                moved |= rank != k;
-            } else if (k < g.K) {
-                key_index[k] = 0xFFFFu;
-            }
-        }
+    if (present) {
+        keys[rank] = static_cast<uint16_t>(k);
+        types[rank] = CR_BITMAP;
+        offsets[rank] = rank * 8192u;
+        cards[rank] = static_cast<uint16_t>(c > 65535u ? 0u : c);  // 65536 stored as 0
+        key_index[k] = static_cast<uint16_t>(rank);
+        moved = rank != k;
+    } else if (k < g.K) {
+        key_index[k] = 0xFFFFu;
     }
-    const bool any_moved = __syncthreads_or(moved) != 0;
+    const bool any_moved = __syncthreads_or(moved) != 0;  // also: s_max is initialised
+    if (r == 0) {
+        uint32_t mx = 0;
+        for (uint32_t i = t; i < g.G; i += 1024u) mx = max(mx, gmax[i]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(mx, o, 64)));
+        if (lane == 0) atomicMax(&s_max, mx);
+        __syncthreads();
+    }
     if (t == 0) {
-        const uint32_t m = s_max;
-        IdsTotals r;
-        r.n_containers = rbase[rounds];
-        r.err = (m >> 16) > g.K - 1u ? 1u : 0u;
-        r.max_id = m;
-        r.moved = any_moved ? 1u : 0u;
-        r.total = tot->total;
-        *tot = r;
+        if (count) atomicAdd(&tot->n_containers, count);
+        if (any_moved) atomicOr(&tot->moved, 1u);
+        if (r == 0) atomicMax(&tot->max_id, s_max);
+        __threadfence();  // the updates above before the count of finished workgroups
+        s_last = atomicAdd(&tot->done, 1u) == gridDim.x - 1u;
+    }
+    __syncthreads();
+    if (s_last && t == 0) {
+        __threadfence();
+        IdsTotals res;
+        res.n_containers = __hip_atomic_load(&tot->n_containers, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        res.max_id = __hip_atomic_load(&tot->max_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        res.moved = __hip_atomic_load(&tot->moved, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        res.total = __hip_atomic_load(&tot->total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        res.err = (res.max_id >> 16) > g.K - 1u ? 1u : 0u;
+        tot->err = res.err;
         volatile IdsTotals* h = host;
-        h->n_containers = r.n_containers;
-        h->err = r.err;
-        h->max_id = r.max_id;
-        h->moved = r.moved;
-        h->total = r.total;
+        h->n_containers = res.n_containers;
+        h->err = res.err;
+        h->max_id = res.max_id;
+        h->moved = res.moved;
+        h->total = res.total;
     }
 }
 
@@ -911,8 +890,8 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     CR_RET(hs.acquire());
     {
         CR_TIMED("ids_rank", s);
-        ids_rank<<<1, 1024, 0, s>>>(g, key_count, gmax, out->keys, out->types, out->offsets, out->cardinalities,
-                                    out->key_index, tot, hs.dev<IdsTotals>());
+        ids_rank<<<(g.K + 1023u) / 1024u, 1024, 0, s>>>(g, key_count, gmax, out->keys, out->types, out->offsets,
+                                                         out->cardinalities, out->key_index, tot, hs.dev<IdsTotals>());
     }
     CR_LAUNCH_CHECK();
     CR_RET(sync_stream(s));
