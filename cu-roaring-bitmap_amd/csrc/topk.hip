@@ -202,6 +202,17 @@ __device__ __forceinline__ bool tk_small(const TkArgs& a, uint64_t n_rows)
 {
     return a.small_max != 0 && n_rows <= a.small_max;
 }
+// Larger sets: the small-set kernels first bound each query's k-th distance
+// from the upper bounds of the first rows (at most small_max of them), and the
+// list path starts from that bound instead of from +inf.
+constexpr uint32_t TK_SEED_ROWS = 16384;
+constexpr uint32_t TK_SEED_ROWS_PER_K = 256;
+__device__ __forceinline__ uint32_t tk_seed_rows(const TkArgs& a, uint64_t n_rows)
+{
+    if (a.small_max == 0 || tk_small(a, n_rows)) return 0;
+    const uint64_t want = std::max<uint64_t>(TK_SEED_ROWS, static_cast<uint64_t>(TK_SEED_ROWS_PER_K) * a.k);
+    return static_cast<uint32_t>(std::min<uint64_t>(std::min<uint64_t>(n_rows, a.small_max), want));
+}
 
 // Per-wave selection state in LDS.
 struct TkWave {
@@ -793,8 +804,10 @@ struct TkPairsLds {
 template <int DP>
 __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
 {
-    const uint64_t n_rows = tk_rows(a);
-    if (!tk_small(a, n_rows)) return;  // the list path answers
+    // Every row of a small set, or the seed rows of a larger one.
+    const uint64_t all_rows = tk_rows(a);
+    const uint64_t n_rows = tk_small(a, all_rows) ? all_rows : tk_seed_rows(a, all_rows);
+    if (n_rows == 0) return;
     __shared__ TkPairsLds<DP> L;
     const uint32_t lane = __lane_id();
     const uint32_t wave = threadIdx.x >> 6;
@@ -918,6 +931,74 @@ constexpr uint32_t TK_SEL_SAMPLE_PER_K = 1024;
 // Process-wide limit of the small-set path (cr_topk_set_small_limit).
 std::atomic<uint32_t> g_topk_small{TK_SMALL};
 
+// A histogram of the upper bounds of rows [0, Sn) of the query's estimates
+// over the range of all of them: the bins spread the values, so the counting
+// atomics rarely collide.  The first bin at which the count reaches k holds the
+// k-th smallest upper bound; the largest value in the bins up to it is the
+// returned bound (at least k rows lie at or below it, so the k-th distance
+// does).  Every thread of the workgroup calls it.
+__device__ __forceinline__ float tk_hist_bound(const TkArgs& a, uint32_t q, const float* lrow, uint32_t Sn,
+                                               uint32_t* hist, uint32_t* bmax, uint32_t* lds, uint32_t& s_bin,
+                                               uint32_t& s_bound)
+{
+    const uint32_t t = threadIdx.x, lane = __lane_id();
+    const float qg = a.pq[q];
+    const float vlo = tk_unordered(a.qlo[q]), vhi = tk_unordered(a.qhi[q]);
+    const float scale = vhi > vlo ? static_cast<float>(TK_SEL_BINS) / (vhi - vlo) : 0.f;
+    hist[t] = 0;
+    bmax[t] = 0;
+    if (t == 0) s_bound = 0;
+    __syncthreads();
+    for (uint32_t r0 = t; r0 < Sn; r0 += 8 * TK_SEL_NT) {  // eight rows' loads in flight
+        float l8[8], x8[8];
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) {
+            const uint32_t r = r0 + i * TK_SEL_NT;
+            l8[i] = r < Sn ? lrow[r] : 0.f;
+            x8[i] = r < Sn ? a.px[r] : 0.f;
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) {
+            if (r0 + i * TK_SEL_NT >= Sn) break;
+            const float u = tk_upper(l8[i], qg, x8[i]);
+            const float f = (u - vlo) * scale;
+            const uint32_t bin = f >= static_cast<float>(TK_SEL_BINS - 1) ? TK_SEL_BINS - 1
+                                                                          : static_cast<uint32_t>(fmaxf(f, 0.f));
+            atomicAdd(&hist[bin], 1u);
+            atomicMax(&bmax[bin], tk_ordered(u));
+        }
+    }
+    __syncthreads();
+    uint32_t total;
+    const uint32_t h = hist[t];
+    const uint32_t excl = block_excl_scan<TK_SEL_NT>(h, lds, total);
+    if (excl < a.k && excl + h >= a.k) s_bin = t;
+    __syncthreads();
+    uint32_t m = t <= s_bin ? bmax[t] : 0u;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(m, o, 64)));
+    if (lane == 0 && m) atomicMax(&s_bound, m);
+    __syncthreads();
+    return tk_unordered(s_bound);
+}
+
+// Larger sets: query q's bound from the upper bounds of its seed rows (more
+// than k of them), into tau for the list path.  At least k rows have an fp32
+// distance at or below it, so the k-th best does; tau holds the bits of
+// non-negative distances.
+__global__ __launch_bounds__(TK_SEL_NT) void tk_seed_bound(TkArgs a)
+{
+    __shared__ uint32_t hist[TK_SEL_BINS], bmax[TK_SEL_BINS];
+    __shared__ uint32_t lds[TK_SEL_NT / 64];
+    __shared__ uint32_t s_bin, s_bound;
+    const uint32_t S = tk_seed_rows(a, tk_rows(a));
+    if (S <= a.k) return;
+    const uint32_t q = blockIdx.x;
+    const float bound = tk_hist_bound(a, q, a.pd + static_cast<size_t>(q) * a.small_max, S, hist, bmax, lds, s_bin,
+                                      s_bound);
+    if (threadIdx.x == 0) atomicMin(a.tau + q, __float_as_uint(fmaxf(bound, 0.f)));
+}
+
 __global__ __launch_bounds__(TK_SEL_NT) void tk_select(TkArgs a, float* out_d, int64_t* out_id)
 {
     __shared__ float bd[2][TK_KMAX];  // the running best, ascending (two planes)
@@ -933,56 +1014,14 @@ __global__ __launch_bounds__(TK_SEL_NT) void tk_select(TkArgs a, float* out_d, i
     const uint32_t S = static_cast<uint32_t>(n_rows);
     const uint32_t q = blockIdx.x;
     const uint32_t t = threadIdx.x;
-    const uint32_t lane = __lane_id();
     const float* lrow = a.pd + static_cast<size_t>(q) * a.small_max;
     for (uint32_t c = t; c < a.dim; c += TK_SEL_NT) qv[c] = a.queries[static_cast<size_t>(q) * a.dim + c];
     float bound = __builtin_inff();
     if (S > a.k) {
-        // A histogram of the upper bounds of the first TK_SEL_SAMPLE rows over
-        // the range of all of them: the bins spread the values, so the
-        // counting atomics rarely collide.  The first bin at which the count
-        // reaches k holds the sample's k-th smallest upper bound; the largest
-        // value in the bins up to it is the bound (at least k rows lie at or
-        // below it, so the k-th distance does).  A sample only loosens it.
+        // The first bound from the upper bounds of the first rows (a sample
+        // only loosens it).
         const uint32_t Sn = min(S, max(TK_SEL_SAMPLE, TK_SEL_SAMPLE_PER_K * a.k));
-        const float qg = a.pq[q];
-        const float vlo = tk_unordered(a.qlo[q]), vhi = tk_unordered(a.qhi[q]);
-        const float scale = vhi > vlo ? static_cast<float>(TK_SEL_BINS) / (vhi - vlo) : 0.f;
-        hist[t] = 0;
-        bmax[t] = 0;
-        if (t == 0) s_bound = 0;
-        __syncthreads();
-        for (uint32_t r0 = t; r0 < Sn; r0 += 8 * TK_SEL_NT) {  // eight rows' loads in flight
-            float l8[8], x8[8];
-#pragma unroll
-            for (uint32_t i = 0; i < 8; ++i) {
-                const uint32_t r = r0 + i * TK_SEL_NT;
-                l8[i] = r < Sn ? lrow[r] : 0.f;
-                x8[i] = r < Sn ? a.px[r] : 0.f;
-            }
-#pragma unroll
-            for (uint32_t i = 0; i < 8; ++i) {
-                if (r0 + i * TK_SEL_NT >= Sn) break;
-                const float u = tk_upper(l8[i], qg, x8[i]);
-                const float f = (u - vlo) * scale;
-                const uint32_t bin = f >= static_cast<float>(TK_SEL_BINS - 1) ? TK_SEL_BINS - 1
-                                                                              : static_cast<uint32_t>(fmaxf(f, 0.f));
-                atomicAdd(&hist[bin], 1u);
-                atomicMax(&bmax[bin], tk_ordered(u));
-            }
-        }
-        __syncthreads();
-        uint32_t total;
-        const uint32_t h = hist[t];
-        const uint32_t excl = block_excl_scan<TK_SEL_NT>(h, lds, total);
-        if (excl < a.k && excl + h >= a.k) s_bin = t;
-        __syncthreads();
-        uint32_t m = t <= s_bin ? bmax[t] : 0u;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(m, o, 64)));
-        if (lane == 0 && m) atomicMax(&s_bound, m);
-        __syncthreads();
-        bound = tk_unordered(s_bound);
+        bound = tk_hist_bound(a, q, lrow, Sn, hist, bmax, lds, s_bin, s_bound);
     }
     // Candidates (rows whose estimate, a lower bound, is at or below the bound)
     // in batches: fp32 direct distances, a sort by (distance, id), and a merge
@@ -1100,13 +1139,23 @@ __global__ __launch_bounds__(TK_SEL_NT) void tk_select(TkArgs a, float* out_d, i
 template <int DP>
 int launch_dist(const TkArgs& a, uint32_t grid, hipStream_t s)
 {
-    tk_dist<DP><<<grid, TK_NT, 0, s>>>(a);
-    CR_LAUNCH_CHECK();
-    if (a.small_max) {
-        CR_TIMED("tk_pairs", s);
-        tk_pairs<DP><<<grid, TK_NT, 0, s>>>(a);
+    if (a.small_max) {  // estimates of a small set, or the seed rows of a larger one, and the seed bound
+        {
+            CR_TIMED("tk_pairs", s);
+            tk_pairs<DP><<<grid, TK_NT, 0, s>>>(a);
+        }
+        CR_LAUNCH_CHECK();
+        {
+            CR_TIMED("tk_seed", s);
+            tk_seed_bound<<<a.n_q, TK_SEL_NT, 0, s>>>(a);
+        }
         CR_LAUNCH_CHECK();
     }
+    {
+        CR_TIMED("tk_dist", s);
+        tk_dist<DP><<<grid, TK_NT, 0, s>>>(a);
+    }
+    CR_LAUNCH_CHECK();
     return CR_OK;
 }
 
@@ -1206,15 +1255,12 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
         CR_LAUNCH_CHECK();
     }
     const uint32_t grid = n_chunks * n_qb;
-    {
-        CR_TIMED("tk_dist", s);
-        if (dim <= 32) {
-            CR_RET(launch_dist<32>(a, grid, s));
-        } else if (dim <= 64) {
-            CR_RET(launch_dist<64>(a, grid, s));
-        } else {
-            CR_RET(launch_dist<128>(a, grid, s));
-        }
+    if (dim <= 32) {
+        CR_RET(launch_dist<32>(a, grid, s));
+    } else if (dim <= 64) {
+        CR_RET(launch_dist<64>(a, grid, s));
+    } else {
+        CR_RET(launch_dist<128>(a, grid, s));
     }
     {
         CR_TIMED("tk_merge", s);
