@@ -21,7 +21,7 @@ struct BsTotals {
     uint32_t n_containers;
     uint32_t negated;
     uint32_t max_key;
-    uint32_t pad;
+    uint32_t done;  // planning workgroups finished
     unsigned long long total;  // popcount of the input
 };
 
@@ -36,11 +36,17 @@ struct BsGeom {
 __device__ __forceinline__ uint32_t load_word(const uint32_t* w, uint32_t i, uint32_t n) { return i < n ? w[i] : 0u; }
 
 // Per chunk: popcount of the words and of their inversion (tail word masked,
-// words past n_words are zero in both).
+// words past n_words are zero in both).  Workgroup 0 also clears the totals
+// the planning workgroups accumulate.
 __global__ __launch_bounds__(BS_NT) void bs_count(const uint32_t* __restrict__ words, BsGeom g, uint32_t* pc,
-                                                  uint32_t* pci)
+                                                  uint32_t* pci, BsTotals* tot)
 {
     __shared__ uint32_t red[BS_NT / 64];
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        tot->n_containers = 0;
+        tot->max_key = 0;
+        tot->done = 0;
+    }
     for (uint32_t c = blockIdx.x; c < g.n_chunks; c += gridDim.x) {
         const uint32_t base = c * 2048u;
         uint32_t a = 0, b = 0;
@@ -78,26 +84,26 @@ __global__ __launch_bounds__(BS_NT) void bs_count(const uint32_t* __restrict__ w
     }
 }
 
-// One workgroup: complement decision, ranks of non-empty chunks, metadata.
-// One workgroup.  Round j covers chunks [1024 j, 1024 j + 1024), one per
-// thread, with coalesced loads (eight rounds in flight): the input's popcount
-// decides the negation (total > U/2, strict, src/upload_ids.cu:837), a chunk is
-// kept iff its (plain or inverted) count is non-zero, and ranks come from
-// per-wave ballots (wave counts in LDS, turned into wave and round bases).
-// Writes the chunk -> rank map, keys/types/offsets/cards, key_index, and the
-// totals to `tot` and to the caller's pinned host slot.
-constexpr uint32_t BS_ROUNDS = 65536 / 1024;
-
+// Planning: workgroup r takes the 1024 chunks of round r, [1024 r, 1024 r +
+// 1024), one per thread.  Every workgroup sums the whole input's popcount
+// (coalesced loads, eight rounds in flight, at most 64 rounds), which decides
+// the negation (total > U/2, strict, src/upload_ids.cu:837); a chunk is kept
+// iff its (plain or inverted) count is non-zero, and the kept chunks of the
+// earlier rounds are counted again by every workgroup, so none waits for
+// another.  Each writes its round of the chunk -> rank map and key_index, its
+// kept chunks' keys/types/offsets/cards, and adds its count and its last kept
+// chunk to `tot`; the last workgroup to finish (a counter, no waiting) writes
+// the negation and the totals to `tot` and to the caller's pinned host slot.
 __global__ __launch_bounds__(1024) void bs_plan(BsGeom g, const uint32_t* pc, const uint32_t* pci, uint32_t* cmap,
                                                 uint16_t* keys, uint8_t* types, uint32_t* offsets, uint16_t* cards,
                                                 uint16_t* key_index, BsTotals* tot, BsTotals* host)
 {
-    __shared__ uint32_t wcnt[BS_ROUNDS][16];
-    __shared__ uint32_t rbase[BS_ROUNDS + 1];
     __shared__ unsigned long long wsum[16];
+    __shared__ uint32_t lds[16];
     __shared__ uint32_t s_last;
+    __shared__ bool s_done;
     const uint32_t t = threadIdx.x, wave = t >> 6, lane = __lane_id();
-    const uint32_t rounds = (g.n_chunks + 1023u) / 1024u;
+    const uint32_t r = blockIdx.x, rounds = gridDim.x;
     unsigned long long part = 0;
     for (uint32_t j0 = 0; j0 < rounds; j0 += 8) {
         uint32_t v[8];
@@ -119,83 +125,59 @@ __global__ __launch_bounds__(1024) void bs_plan(BsGeom g, const uint32_t* pc, co
     for (int w = 0; w < 16; ++w) total += wsum[w];
     const bool negate = total > static_cast<unsigned long long>(g.universe / 2u);  // :837
     const uint32_t* cnt = negate ? pci : pc;
-    uint64_t mine = 0;  // bit j: this thread's chunk of round j is kept
-    for (uint32_t j0 = 0; j0 < rounds; j0 += 8) {
+    // Rounds before r are whole (only the last round can be partial).
+    uint32_t before = 0;
+    for (uint32_t j0 = 0; j0 < r; j0 += 8) {
         uint32_t v[8];
 #pragma unroll
-        for (uint32_t q = 0; q < 8; ++q) {
-            const uint32_t c = (j0 + q) * 1024u + t;
-            v[q] = (j0 + q < rounds && c < g.n_chunks) ? cnt[c] : 0u;
-        }
+        for (uint32_t q = 0; q < 8; ++q) v[q] = j0 + q < r ? cnt[(j0 + q) * 1024u + t] : 0u;
 #pragma unroll
-        for (uint32_t q = 0; q < 8; ++q) {
-            if (j0 + q >= rounds) break;
-            const uint64_t m = __ballot(v[q] != 0u);
-            if (v[q] != 0u) mine |= 1ull << (j0 + q);
-            if (lane == 0) wcnt[j0 + q][wave] = static_cast<uint32_t>(__popcll(m));
-        }
+        for (uint32_t q = 0; q < 8; ++q) before += v[q] != 0u ? 1u : 0u;
     }
-    __syncthreads();
-    uint32_t wprefix = 0, rtotal = 0;
-    if (t < rounds * 16u) {
-        const uint32_t j = t >> 4, w = t & 15u;
-        for (uint32_t x = 0; x < w; ++x) wprefix += wcnt[j][x];
-        if (w == 15u) rtotal = wprefix + wcnt[j][15];
-    }
-    __syncthreads();
-    if (t < rounds * 16u) {
-        wcnt[t >> 4][t & 15u] = wprefix;
-        if ((t & 15u) == 15u) rbase[(t >> 4) + 1] = rtotal;
-    }
-    if (t == 0) rbase[0] = 0;
-    __syncthreads();
-    if (t == 0)
-        for (uint32_t j = 1; j <= rounds; ++j) rbase[j] += rbase[j - 1];
-    __syncthreads();
+    const uint32_t base = block_sum<1024>(before, lds);
+    const uint32_t c = r * 1024u + t;
+    const uint32_t v = c < g.n_chunks ? cnt[c] : 0u;
+    const bool kept = v != 0u;
+    uint32_t count;
+    const uint32_t rank = base + block_flag_rank<1024>(kept, lds, count);
     uint32_t last = 0;
-    for (uint32_t j0 = 0; j0 < rounds; j0 += 8) {
-        uint32_t v[8];  // the counts again (cache hits), eight rounds in flight
-#pragma unroll
-        for (uint32_t q = 0; q < 8; ++q) v[q] = ((mine >> (j0 + q)) & 1ull) ? cnt[(j0 + q) * 1024u + t] : 0u;
-#pragma unroll
-        for (uint32_t q = 0; q < 8; ++q) {
-            const uint32_t j = j0 + q;
-            if (j >= rounds) break;
-            const uint32_t c = j * 1024u + t;
-            const bool kept = (mine >> j) & 1ull;
-            const uint64_t m = __ballot(kept);
-            if (kept) {
-                const uint32_t rank =
-                    rbase[j] + wcnt[j][wave] + static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull)));
-                cmap[c] = rank;
-                keys[rank] = static_cast<uint16_t>(c);
-                types[rank] = CR_BITMAP;
-                offsets[rank] = rank * 8192u;
-                cards[rank] = static_cast<uint16_t>(v[q] > 65535u ? 0u : v[q]);
-                key_index[c] = static_cast<uint16_t>(rank);
-                last = c;
-            } else if (c < g.n_chunks) {
-                cmap[c] = 0xFFFFFFFFu;
-                key_index[c] = 0xFFFFu;
-            }
-        }
+    if (kept) {
+        cmap[c] = rank;
+        keys[rank] = static_cast<uint16_t>(c);
+        types[rank] = CR_BITMAP;
+        offsets[rank] = rank * 8192u;
+        cards[rank] = static_cast<uint16_t>(v > 65535u ? 0u : v);
+        key_index[c] = static_cast<uint16_t>(rank);
+        last = c;
+    } else if (c < g.n_chunks) {
+        cmap[c] = 0xFFFFFFFFu;
+        key_index[c] = 0xFFFFu;
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) last = max(last, static_cast<uint32_t>(__shfl_xor(last, o, 64)));
     if (lane == 0 && last) atomicMax(&s_last, last);
     __syncthreads();
     if (t == 0) {
-        BsTotals r{};
-        r.n_containers = rbase[rounds];
-        r.negated = negate ? 1u : 0u;
-        r.max_key = s_last;
-        r.total = total;
-        *tot = r;
+        if (count) atomicAdd(&tot->n_containers, count);
+        if (s_last) atomicMax(&tot->max_key, s_last);
+        __threadfence();  // the updates above before the count of finished workgroups
+        s_done = atomicAdd(&tot->done, 1u) == rounds - 1u;
+    }
+    __syncthreads();
+    if (s_done && t == 0) {
+        __threadfence();
+        BsTotals res{};
+        res.n_containers = __hip_atomic_load(&tot->n_containers, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        res.max_key = __hip_atomic_load(&tot->max_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        res.negated = negate ? 1u : 0u;
+        res.total = total;
+        tot->negated = res.negated;
+        tot->total = res.total;
         volatile BsTotals* h = host;
-        h->n_containers = r.n_containers;
-        h->negated = r.negated;
-        h->max_key = r.max_key;
-        h->total = r.total;
+        h->n_containers = res.n_containers;
+        h->negated = res.negated;
+        h->max_key = res.max_key;
+        h->total = res.total;
     }
 }
 
@@ -285,15 +267,16 @@ int upload_from_device_bitset_impl(const uint32_t* d_words, uint32_t n_words, ui
 
     {
         CR_TIMED("bs_count", s);
-        bs_count<<<grid_cap(g.n_chunks), BS_NT, 0, s>>>(d_words, g, pc, pci);
+        bs_count<<<grid_cap(g.n_chunks), BS_NT, 0, s>>>(d_words, g, pc, pci, tot);
     }
     CR_LAUNCH_CHECK();
     HostSlotGuard hs;
     CR_RET(hs.acquire());
     {
         CR_TIMED("bs_plan", s);
-        bs_plan<<<1, 1024, 0, s>>>(g, pc, pci, cmap, out->keys, out->types, out->offsets, out->cardinalities,
-                                   out->key_index, tot, hs.dev<BsTotals>());
+        bs_plan<<<(g.n_chunks + 1023u) / 1024u, 1024, 0, s>>>(g, pc, pci, cmap, out->keys, out->types, out->offsets,
+                                                               out->cardinalities, out->key_index, tot,
+                                                               hs.dev<BsTotals>());
     }
     CR_LAUNCH_CHECK();
     {

@@ -70,11 +70,12 @@ struct IdsGeom {
 // Each workgroup takes blocks of TB tiles.  A tile is counting-sorted by
 // bucket in LDS and written back to its own slot of `part` (tile t at word
 // t * TILE_WORDS) as packed fields, a streaming write; `tab` row t holds the
-// tile's bucket starts (NB + 1 u16, in fields).  An id whose bucket lies past the universe's last goes to a
-// sentinel bucket NB that is sorted after the others and neither written nor
-// built; the error is raised from the maximum id, which each workgroup
-// reports.  Every lane holds an id: a partial last tile is padded with ids of
-// the sentinel bucket (which do not enter the maximum).
+// tile's bucket starts (NB + 1 u16, in fields).  An id whose bucket lies past
+// the universe's last goes to a sentinel bucket NB that is sorted after the
+// others and neither written nor built; the error is raised from the maximum
+// id, which each workgroup reports.  Every lane holds an id: a partial last
+// tile is padded with ids of the sentinel bucket (which do not enter the
+// maximum).
 __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restrict__ ids, IdsGeom g,
                                                        uint32_t* __restrict__ part, uint16_t* __restrict__ tab,
                                                        uint32_t* gmax, IdsTotals* tot)
