@@ -695,8 +695,10 @@ int set_operation_impl(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_
     const bool only_bb = h.c[C_BB] == n_items && ((reinterpret_cast<uintptr_t>(a->bitmap_data) |
                                                    reinterpret_cast<uintptr_t>(b->bitmap_data)) & 15u) == 0;
     if (only_bb) {
-        const unsigned waves_per_cu = 32;  // 8 waves per SIMD
-        const unsigned gb = std::max(1u, std::min((n_items + 3) / 4, num_cus() * waves_per_cu / 4));
+        // One pair per wave: every pair's 16 loads are in flight at once
+        // (capping the grid at the resident waves, two pairs a wave, measured
+        // 1.5% slower at 16384 pairs).
+        const unsigned gb = std::max(1u, (n_items + 3) / 4);
         CR_TIMED("so_exec", s);
         switch (op) {
         case CR_AND:
@@ -992,7 +994,9 @@ static int fused_multi_and(const cr_gpu_roaring* in, uint32_t count, hipStream_t
     CR_RET(fill_u16(out->key_index, 0xFFFFu, kidx_len, s));
     {
         CR_TIMED("mand_and", s);
-        const unsigned gm = std::max(1u, std::min((n_common + 3) / 4, num_cus() * 8u));
+        // One common key per wave (a grid capped at 8 workgroups per CU, two
+        // keys a wave, measured 0.69 of peak against 0.71 at k = 3).
+        const unsigned gm = std::max(1u, (n_common + 3) / 4);
         mand_and<<<gm, EXEC_NT, 0, s>>>(args, common, cnt, out->bitmap_data, out->keys, out->types,
                                                          out->offsets, out->cardinalities, out->key_index,
                                                          static_cast<uint32_t>(kidx_len), cnt + 1);
