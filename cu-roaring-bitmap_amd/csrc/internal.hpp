@@ -70,6 +70,12 @@ struct HostSlotGuard {
 // memory once the stream reaches this point, then synchronises the stream.
 int read_back(void* host, const void* dev, size_t bytes, hipStream_t s);
 
+// Host (pageable) -> device copy, stream-ordered: large copies go through a
+// ring of pinned chunks, each filled by a pool of host threads while the
+// previous chunks' DMA runs; returns once every chunk is enqueued (the source
+// may then be reused).  Small copies use hipMemcpyAsync directly.
+int h2d_pageable(void* dst, const void* src, size_t bytes, hipStream_t s);
+
 // Scratch that is released (stream-ordered) when the guard leaves scope.
 struct Scratch {
     void* ptr = nullptr;

@@ -2,9 +2,11 @@
 // packed result blocks, free, AUTO threshold, and small utility entry points.
 #include <algorithm>
 #include <chrono>
+#include <condition_variable>
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
@@ -88,6 +90,117 @@ int read_back(void* host, const void* dev, size_t bytes, hipStream_t s)
     CR_HIP_RET(hipMemcpyAsync(hs.slot.host, dev, bytes, hipMemcpyDeviceToHost, s));
     CR_RET(sync_stream(s));
     std::memcpy(host, hs.slot.host, bytes);
+    return CR_OK;
+}
+
+// ---- pageable host -> device copies -----------------------------------------
+// A pageable source cannot be DMA'd directly (and registering it is not
+// available here), so it is copied into pinned chunks first.  A pool of host
+// threads fills chunk i + 1 while chunk i's DMA runs; R chunks rotate, each
+// reused only after the event of its previous DMA.  The pool and the ring live
+// for the process (never freed: worker threads may still wait on them at exit).
+namespace {
+constexpr size_t H2D_CHUNK = size_t(16) << 20;
+constexpr int H2D_RING = 4;
+constexpr size_t H2D_DIRECT = size_t(8) << 20;  // below this, hipMemcpyAsync's own staging
+
+struct CopyPool {
+    std::mutex m;
+    std::condition_variable cv, done;
+    uint64_t gen = 0;
+    int pending = 0;
+    int workers = 0;
+    const char* src = nullptr;
+    char* dst = nullptr;
+    size_t n = 0;
+
+    void part(int i, int parts)
+    {
+        const size_t lo = n * static_cast<size_t>(i) / parts, hi = n * static_cast<size_t>(i + 1) / parts;
+        if (hi > lo) std::memcpy(dst + lo, src + lo, hi - lo);
+    }
+    void worker(int i)
+    {
+        uint64_t seen = 0;
+        for (;;) {
+            {
+                std::unique_lock<std::mutex> lk(m);
+                cv.wait(lk, [&] { return gen != seen; });
+                seen = gen;
+            }
+            part(i + 1, workers + 1);  // the caller copies part 0
+            std::lock_guard<std::mutex> lk(m);
+            if (--pending == 0) done.notify_one();
+        }
+    }
+    // Copies n bytes with the workers and the calling thread.
+    void copy(char* d, const char* s_, size_t bytes)
+    {
+        {
+            std::lock_guard<std::mutex> lk(m);
+            dst = d;
+            src = s_;
+            n = bytes;
+            pending = workers;
+            ++gen;
+        }
+        cv.notify_all();
+        part(0, workers + 1);
+        std::unique_lock<std::mutex> lk(m);
+        done.wait(lk, [&] { return pending == 0; });
+    }
+};
+
+struct H2dRing {
+    std::mutex mu;  // one staged copy at a time
+    CopyPool* pool = nullptr;
+    char* chunk[H2D_RING] = {};
+    hipEvent_t ev[H2D_RING] = {};
+    bool used[H2D_RING] = {};
+    int next = 0;
+};
+H2dRing* g_h2d = new H2dRing;  // never freed (see above)
+
+int h2d_ring_init(H2dRing& r)
+{
+    if (!r.pool) {
+        const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+        auto* p = new CopyPool;
+        p->workers = static_cast<int>(std::min(7u, std::max(1u, hw / 2)) - 1);
+        for (int i = 0; i < p->workers; ++i) std::thread([p, i] { p->worker(i); }).detach();
+        r.pool = p;
+    }
+    for (int k = 0; k < H2D_RING; ++k) {
+        if (!r.chunk[k]) {
+            void* ptr = nullptr;
+            CR_HIP_RET(hipHostMalloc(&ptr, H2D_CHUNK, hipHostMallocDefault));
+            r.chunk[k] = static_cast<char*>(ptr);
+        }
+        if (!r.ev[k]) CR_HIP_RET(hipEventCreateWithFlags(&r.ev[k], hipEventDisableTiming));
+    }
+    return CR_OK;
+}
+}  // namespace
+
+int h2d_pageable(void* dst, const void* src, size_t bytes, hipStream_t s)
+{
+    if (bytes < H2D_DIRECT) {
+        if (bytes) CR_HIP_RET(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
+        return CR_OK;
+    }
+    H2dRing& r = *g_h2d;
+    std::lock_guard<std::mutex> lk(r.mu);
+    CR_RET(h2d_ring_init(r));
+    for (size_t off = 0; off < bytes; off += H2D_CHUNK) {
+        const int k = r.next;
+        r.next = (r.next + 1) % H2D_RING;
+        const size_t n = std::min(H2D_CHUNK, bytes - off);
+        if (r.used[k]) CR_HIP_RET(hipEventSynchronize(r.ev[k]));  // its previous DMA has read it
+        r.pool->copy(r.chunk[k], static_cast<const char*>(src) + off, n);
+        CR_HIP_RET(hipMemcpyAsync(static_cast<char*>(dst) + off, r.chunk[k], n, hipMemcpyHostToDevice, s));
+        CR_HIP_RET(hipEventRecord(r.ev[k], s));
+        r.used[k] = true;
+    }
     return CR_OK;
 }
 

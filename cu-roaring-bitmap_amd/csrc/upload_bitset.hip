@@ -333,6 +333,6 @@ extern "C" int cr_upload_from_bitset(const uint32_t* host_words, uint32_t n_word
     if (n_words == 0) return upload_from_device_bitset_impl(nullptr, 0, universe_size, s, out);
     Scratch sc;
     CR_RET(sc.alloc(static_cast<size_t>(n_words) * 4u, s));
-    CR_HIP_RET(hipMemcpyAsync(sc.ptr, host_words, static_cast<size_t>(n_words) * 4u, hipMemcpyHostToDevice, s));
+    CR_RET(h2d_pageable(sc.ptr, host_words, static_cast<size_t>(n_words) * 4u, s));
     return upload_from_device_bitset_impl(sc.at<uint32_t>(0), n_words, universe_size, s, out);
 }

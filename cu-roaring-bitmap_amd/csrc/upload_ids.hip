@@ -1024,6 +1024,6 @@ extern "C" int cr_upload_from_ids(const uint32_t* ids, uint32_t n_ids, uint32_t 
     if (n_ids == 0) return upload_from_device_ids_impl(nullptr, 0, universe_size, bitmap_threshold, s, out);
     Scratch sc;
     CR_RET(sc.alloc(static_cast<size_t>(n_ids) * 4u, s));
-    CR_HIP_RET(hipMemcpyAsync(sc.ptr, ids, static_cast<size_t>(n_ids) * 4u, hipMemcpyHostToDevice, s));
+    CR_RET(h2d_pageable(sc.ptr, ids, static_cast<size_t>(n_ids) * 4u, s));
     return upload_from_device_ids_impl(sc.at<uint32_t>(0), n_ids, universe_size, bitmap_threshold, s, out);
 }
