@@ -55,7 +55,8 @@ struct IdsTotals {
     uint32_t max_id;
     uint32_t moved;  // present keys are not a prefix: the pool needs compaction
     unsigned long long total;  // distinct ids (or complement count)
-    uint32_t done;  // rank workgroups finished
+    uint32_t done;    // rank workgroups finished
+    uint32_t absent;  // build workgroups that found a key of the universe with no id
 };
 
 struct IdsGeom {
@@ -99,6 +100,7 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
             tot->n_containers = 0;  // the rank workgroups accumulate these
             tot->max_id = 0;
             tot->done = 0;
+            tot->absent = 0;
         }
     }
     uint32_t mx = 0;
@@ -291,7 +293,9 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
 // workgroup 0 adds the tile-sort workgroups' maximum id.  The last workgroup
 // to finish (a counter, no waiting) writes the totals -- with the range error
 // from the maximum id and the distinct count the build accumulated -- to `tot`
-// and to the caller's pinned host slot.
+// and to the caller's pinned host slot.  When the build found every key of
+// the universe present, the ranks are the keys and the build has written the
+// metadata: workgroup 0 only writes the totals and the others return.
 __global__ __launch_bounds__(1024) void ids_rank(IdsGeom g, const uint32_t* key_count, const uint32_t* gmax,
                                                  uint16_t* keys, uint8_t* types, uint32_t* offsets, uint16_t* cards,
                                                  uint16_t* key_index, IdsTotals* tot, IdsTotals* host)
@@ -299,6 +303,38 @@ __global__ __launch_bounds__(1024) void ids_rank(IdsGeom g, const uint32_t* key_
     __shared__ uint32_t lds[16];
     __shared__ uint32_t s_max;
     __shared__ bool s_last;
+    if (tot->absent == 0) {
+        // Every key present: the ranks are the keys and the build wrote the
+        // metadata; workgroup 0 writes the totals.
+        if (blockIdx.x != 0) return;
+        const uint32_t t = threadIdx.x;
+        if (t == 0) s_max = 0;
+        __syncthreads();
+        uint32_t mx = 0;
+        for (uint32_t i = t; i < g.G; i += 1024u) mx = max(mx, gmax[i]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(mx, o, 64)));
+        if (__lane_id() == 0) atomicMax(&s_max, mx);
+        __syncthreads();
+        if (t == 0) {
+            IdsTotals res{};
+            res.n_containers = g.K;
+            res.max_id = s_max;
+            res.err = (s_max >> 16) > g.K - 1u ? 1u : 0u;
+            res.moved = 0;
+            res.total = tot->total;
+            tot->n_containers = res.n_containers;
+            tot->max_id = res.max_id;
+            tot->err = res.err;
+            volatile IdsTotals* h = host;
+            h->n_containers = res.n_containers;
+            h->err = res.err;
+            h->max_id = res.max_id;
+            h->moved = res.moved;
+            h->total = res.total;
+        }
+        return;
+    }
     const uint32_t t = threadIdx.x, lane = __lane_id();
     const uint32_t r = blockIdx.x;
     if (t == 0) s_max = 0;
@@ -397,11 +433,22 @@ constexpr uint32_t BUILD_WAVES = BUILD_NT / 64;
 __host__ __device__ inline uint32_t build_per_xcd(uint32_t nb) { return (nb + 7) / 8; }
 inline uint32_t build_grid(uint32_t nb) { return 8 * build_per_xcd(nb); }
 
+// Normal mode's metadata outputs: with every key present the ranks are the
+// keys, so the build writes keys/types/offsets/cards/key_index itself (and
+// ids_rank only the totals); otherwise ids_rank rewrites them in rank order.
+struct BuildMeta {
+    uint16_t* keys;
+    uint8_t* types;
+    uint32_t* offsets;
+    uint16_t* cards;
+    uint16_t* key_index;
+};
+
 __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict__ part,
                                                       const uint16_t* __restrict__ tab, IdsGeom g, uint32_t universe,
                                                       bool complement, const uint16_t* key_index,
                                                       uint64_t* __restrict__ pool, uint16_t* cards,
-                                                      uint32_t* key_count, IdsTotals* tot)
+                                                      uint32_t* key_count, IdsTotals* tot, BuildMeta m)
 {
     __shared__ alignas(16) uint32_t bits[BK_KEYS * 2048u];  // 128 KiB of the CU's 160 KiB LDS
     const uint32_t t = threadIdx.x;
@@ -551,7 +598,16 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
             pc += __popc(v[q].x) + __popc(v[q].y) + __popc(v[q].z) + __popc(v[q].w);
         }
         pc = wave_sum(pc);
-        if (!complement && lane == 0) key_count[key] = pc;
+        if (!complement && lane == 0) {
+            key_count[key] = pc;
+            if (pc != 0) {
+                m.keys[key] = static_cast<uint16_t>(key);
+                m.types[key] = CR_BITMAP;
+                m.offsets[key] = key * 8192u;
+                m.cards[key] = static_cast<uint16_t>(pc > 65535u ? 0u : pc);  // 65536 stored as 0
+                m.key_index[key] = static_cast<uint16_t>(key);
+            }
+        }
         if (pc != 0) {
             const uint32_t slot = complement ? key_index[key] : key;
             uint4* dst = reinterpret_cast<uint4*>(pool + static_cast<uint64_t>(slot) * 1024u);
@@ -562,10 +618,15 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
     }
     if (lane == 0) wave_pc[c] = pc;
     __syncthreads();
-    if (t == 0) {  // one device atomic per workgroup
+    if (t == 0) {  // device atomics without a return, so the workgroup retires at once
         unsigned long long s = 0;
-        for (uint32_t i = 0; i < BUILD_WAVES; ++i) s += wave_pc[i];
+        bool absent = false;
+        for (uint32_t i = 0; i < BUILD_WAVES; ++i) {
+            s += wave_pc[i];
+            absent |= b * BK_KEYS + i < g.K && wave_pc[i] == 0;
+        }
         if (s) atomicAdd(&tot->total, s);
+        if (!complement && absent) atomicAdd(&tot->absent, 1u);
     }
 }
 
@@ -881,14 +942,15 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
         ids_tile_sort<<<g.G, TS_NT, 0, s>>>(d_ids, g, part, tab, gmax, tot);
     }
     CR_LAUNCH_CHECK();
-    {
-        CR_TIMED("ids_build", s);
-        ids_build<<<build_grid(g.NB), BUILD_NT, 0, s>>>(part, tab, g, universe, false, nullptr, out->bitmap_data,
-                                                        nullptr, key_count, tot);
-    }
-    CR_LAUNCH_CHECK();
     HostSlotGuard hs;
     CR_RET(hs.acquire());
+    {
+        CR_TIMED("ids_build", s);
+        const BuildMeta bm{out->keys, out->types, out->offsets, out->cardinalities, out->key_index};
+        ids_build<<<build_grid(g.NB), BUILD_NT, 0, s>>>(part, tab, g, universe, false, nullptr, out->bitmap_data,
+                                                        nullptr, key_count, tot, bm);
+    }
+    CR_LAUNCH_CHECK();
     {
         CR_TIMED("ids_rank", s);
         ids_rank<<<(g.K + 1023u) / 1024u, 1024, 0, s>>>(g, key_count, gmax, out->keys, out->types, out->offsets,
@@ -967,7 +1029,7 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     {
         CR_TIMED("ids_build", s);
         ids_build<<<build_grid(g.NB), BUILD_NT, 0, s>>>(part, tab, g, universe, true, comp.key_index,
-                                                    comp.bitmap_data, comp.cardinalities, nullptr, tot);
+                                                    comp.bitmap_data, comp.cardinalities, nullptr, tot, BuildMeta{});
     }
     CR_LAUNCH_CHECK();
     CR_RET(read_back(&h, tot, sizeof(h), s));
