@@ -517,43 +517,53 @@ uint64_t stored_cardinality(const cr_gpu_roaring* bm)
 }  // namespace
 
 // ---- deep copy: up to eight byte ranges in one launch -----------------------
+// One flat grid over the segments: segment i takes workgroups [blk0[i],
+// blk0[i + 1]), one per 32 KiB (eight 16-byte loads in flight per thread), so
+// small metadata segments cost a workgroup or two and the pool the rest.
+constexpr uint64_t CV_COPY_BLK = 32768;
+
 __global__ __launch_bounds__(256) void cv_copy(CopyList L)
 {
-    const uint32_t s = blockIdx.y;
-    if (s >= L.n) return;
+    uint32_t s = 0;
+    while (s + 1 < L.n && blockIdx.x >= L.blk0[s + 1]) ++s;
     const CopySeg g = L.seg[s];
-    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256u;
-    const uint64_t i0 = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
+    const uint64_t blk = blockIdx.x - L.blk0[s];
+    const uint64_t lo = blk * CV_COPY_BLK, hi = std::min<uint64_t>(g.bytes, lo + CV_COPY_BLK);
+    if (lo >= hi) return;
     const uint8_t* sb = static_cast<const uint8_t*>(g.src);
     uint8_t* db = static_cast<uint8_t*>(g.dst);
-    uint64_t done = 0;
+    uint64_t done = lo;
     if (((reinterpret_cast<uintptr_t>(g.src) | reinterpret_cast<uintptr_t>(g.dst)) & 15u) == 0) {
-        const uint64_t n4 = g.bytes / 16u;
-        const uint4* s4 = static_cast<const uint4*>(g.src);
-        uint4* d4 = static_cast<uint4*>(g.dst);
-        // A workgroup copies 8 x 4 KiB per step: eight 16-byte loads in flight per thread.
-        for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 2048u + threadIdx.x; i < n4; i += 8 * stride) {
-            uint4 v[8];
+        const uint64_t n4 = (hi - lo) / 16u;
+        const uint4* s4 = reinterpret_cast<const uint4*>(sb + lo);
+        uint4* d4 = reinterpret_cast<uint4*>(db + lo);
+        uint4 v[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-                if (i + k * 256u < n4) v[k] = ld_stream(s4 + i + k * 256u);
+        for (int k = 0; k < 8; ++k)
+            if (threadIdx.x + k * 256u < n4) v[k] = ld_stream(s4 + threadIdx.x + k * 256u);
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-                if (i + k * 256u < n4) st_stream(d4 + i + k * 256u, v[k]);
-        }
-        done = n4 * 16u;
+        for (int k = 0; k < 8; ++k)
+            if (threadIdx.x + k * 256u < n4) st_stream(d4 + threadIdx.x + k * 256u, v[k]);
+        done = lo + n4 * 16u;
     }
-    for (uint64_t i = done + i0; i < g.bytes; i += stride) db[i] = sb[i];
+    for (uint64_t i = done + threadIdx.x; i < hi; i += 256u) db[i] = sb[i];
 }
 
-int copy_segments(const CopyList& L, hipStream_t s)
+int copy_segments(const CopyList& L0, hipStream_t s)
 {
-    if (L.n == 0) return CR_OK;
-    uint64_t most = 0;
-    for (uint32_t i = 0; i < L.n; ++i) most = std::max(most, L.seg[i].bytes);
-    const uint64_t want = (most / 16u + 2047u) / 2048u;  // 2048 16-byte vectors per workgroup step
-    const uint32_t gx = static_cast<uint32_t>(std::max<uint64_t>(1, std::min<uint64_t>(want, 4096u)));
-    cv_copy<<<dim3(gx, L.n), 256, 0, s>>>(L);
+    if (L0.n == 0) return CR_OK;
+    CopyList L = L0;
+    uint64_t total = 0;
+    for (uint32_t i = 0; i < L.n; ++i) {
+        L.blk0[i] = static_cast<uint32_t>(total);
+        total += std::max<uint64_t>(1, (L.seg[i].bytes + CV_COPY_BLK - 1) / CV_COPY_BLK);
+    }
+    L.blk0[L.n] = static_cast<uint32_t>(total);
+    if (total > 0xFFFFFFFFull) {
+        set_error("copy_segments: %llu bytes exceed one grid", static_cast<unsigned long long>(total * CV_COPY_BLK));
+        return CR_ERR_UNSUPPORTED;
+    }
+    cv_copy<<<static_cast<uint32_t>(total), 256, 0, s>>>(L);
     CR_LAUNCH_CHECK();
     return CR_OK;
 }

@@ -332,6 +332,7 @@ struct CopySeg {
 struct CopyList {
     CopySeg seg[8];
     uint32_t n;
+    uint32_t blk0[9];  // copy_segments: first workgroup of each segment (filled there)
 };
 int copy_segments(const CopyList& L, hipStream_t s);
 
