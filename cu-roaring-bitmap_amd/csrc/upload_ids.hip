@@ -419,10 +419,11 @@ __global__ __launch_bounds__(256) void ids_gather_pool(const uint16_t* keys, uin
 // One workgroup per bucket: its 16 containers as 16 x 2048 u32 LDS words
 // (128 KiB), filled from the bucket's run in every tile (the bucket order over
 // the XCDs is below).
-// Normal mode writes each present key's container to pool slot `key` (the
-// ranks come after) and every key's distinct count; complement mode writes
-// ~bits masked to [0, U) at the key_index rank of keys whose complement is
-// non-empty, with their cards.
+// Normal mode writes each present key's container to pool slot `key`, every
+// key's distinct count, and the metadata as if ranks were keys (right when
+// every key is present; ids_rank rewrites it otherwise, told by `absent`);
+// complement mode writes ~bits masked to [0, U) at the key_index rank of keys
+// whose complement is non-empty, with their cards.
 constexpr int BUILD_NT = 1024;
 constexpr uint32_t BUILD_WAVES = BUILD_NT / 64;
 
