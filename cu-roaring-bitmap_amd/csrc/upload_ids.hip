@@ -437,6 +437,9 @@ inline uint32_t build_grid(uint32_t nb) { return 8 * build_per_xcd(nb); }
 // Normal mode's metadata outputs: with every key present the ranks are the
 // keys, so the build writes keys/types/offsets/cards/key_index itself (and
 // ids_rank only the totals); otherwise ids_rank rewrites them in rank order.
+// The arrays hold min(K, n) entries, so the build is handed them (non-null
+// `keys`) only when n >= K: with fewer ids not every key can be present, and
+// a write at index `key` could land past the arrays.
 struct BuildMeta {
     uint16_t* keys;
     uint8_t* types;
@@ -601,7 +604,7 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
         pc = wave_sum(pc);
         if (!complement && lane == 0) {
             key_count[key] = pc;
-            if (pc != 0) {
+            if (pc != 0 && m.keys != nullptr) {
                 m.keys[key] = static_cast<uint16_t>(key);
                 m.types[key] = CR_BITMAP;
                 m.offsets[key] = key * 8192u;
@@ -947,7 +950,9 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     CR_RET(hs.acquire());
     {
         CR_TIMED("ids_build", s);
-        const BuildMeta bm{out->keys, out->types, out->offsets, out->cardinalities, out->key_index};
+        const BuildMeta bm = bound >= g.K
+                                 ? BuildMeta{out->keys, out->types, out->offsets, out->cardinalities, out->key_index}
+                                 : BuildMeta{};
         ids_build<<<build_grid(g.NB), BUILD_NT, 0, s>>>(part, tab, g, universe, false, nullptr, out->bitmap_data,
                                                         nullptr, key_count, tot, bm);
     }

@@ -46,6 +46,13 @@ ID_CASES = [
     (24576 * 2 + 5, 1 << 24, orc.PROMOTE_AUTO, 13),
     (24576 * 8 + 1, 1 << 28, orc.PROMOTE_AUTO, 14),
     (24576 * 9 - 1, 1 << 30, orc.PROMOTE_KEEP_DEFAULT, 15),
+    # more than 1024 ids but fewer than keys: the metadata arrays hold n entries, not K
+    (1025, 1 << 30, orc.PROMOTE_AUTO, 16),
+    (2000, 1 << 30, orc.PROMOTE_AUTO, 17),
+    (5000, 1 << 30, orc.PROMOTE_KEEP_DEFAULT, 18),
+    (1025, 0xFFFFFFFF, orc.PROMOTE_AUTO, 19),
+    (20000, 0xFFFFFFFF, orc.PROMOTE_AUTO, 20),
+    (16383, 1 << 30, orc.PROMOTE_AUTO, 21),
 ]
 
 
