@@ -4,9 +4,10 @@
 // per-thread kernels (bench/bench_point_query.cu:123-144).  Here each lane
 // keeps QPT independent queries in flight so the dependent key_index -> word
 // loads of different queries overlap (random queries are latency-bound gathers
-// from the 256 MB Infinity Cache / HBM).  The all-bitmap contains path is the
-// view's two-load fast path written without branches; other layouts call
-// GpuRoaringView::contains and wavefront_contains unchanged.
+// from the 256 MB Infinity Cache / HBM).  Modes 0 and 1 on an all-bitmap view
+// take the view's two-load fast path written without branches; every other
+// layout, and modes 2 and 3 on every layout, call GpuRoaringView::contains and
+// wavefront_contains unchanged.
 #include <algorithm>
 #include <cstring>
 
@@ -110,7 +111,7 @@ extern "C" int cr_contains_batch(const cr_gpu_roaring_view* view, const uint32_t
         CR_TIMED("contains", s);
         if (v.all_bitmap && mode == CR_QUERY_CONTAINS) {
             contains_allbitmap<false><<<grid, Q_NT, 0, s>>>(v, d_ids, n, d_out);
-        } else if (v.all_bitmap) {
+        } else if (v.all_bitmap && mode == CR_QUERY_WAVEFRONT) {
             contains_allbitmap<true><<<grid, Q_NT, 0, s>>>(v, d_ids, n, d_out);
         } else if (mode == CR_QUERY_WAVEFRONT || mode == CR_QUERY_WAVEFRONT_API) {
             contains_general<CR_QUERY_WAVEFRONT><<<grid, Q_NT, 0, s>>>(v, d_ids, n, d_out);

@@ -40,7 +40,12 @@ std::vector<HostContainer> complement_containers(const HostContainer* containers
 }  // namespace cu_roaring
 
 #if defined(CU_ROARING_WITH_CROARING)
+// The container structs live in CRoaring's internal headers, as in
+// src/upload.cpp:5-18 (roaring::internal in CRoaring v4.x).
 #include <roaring/roaring.h>
+#include <roaring/containers/array.h>
+#include <roaring/containers/bitset.h>
+#include <roaring/containers/run.h>
 namespace cu_roaring {
 namespace detail {
 // Walk roaring_bitmap_t::high_low_container (src/upload.cpp:31-71).
