@@ -7,7 +7,7 @@
 
 #include <algorithm>
 #include <cstring>
-
+#include <mutex>
 #include <type_traits>
 
 #include "image.hpp"
@@ -473,6 +473,26 @@ int promote_impl(const cr_gpu_roaring* bm, hipStream_t s, cr_gpu_roaring* out)
     return CR_OK;
 }
 
+// The three launches of enumerate_ids over given counts/starts buffers
+// (n_containers u64 each), untimed (enumerate_impl below times each launch).
+// cv_enum_count writes every count and the scan every start, so neither
+// buffer needs clearing first.
+int enumerate_launch(const cr_gpu_roaring* bm, int64_t* d_out, uint64_t cap, uint64_t* counts, uint64_t* starts,
+                     hipStream_t s)
+{
+    const uint32_t n = bm->n_containers;
+    cv_enum_count<<<(n + 3) / 4, CV_NT, 0, s>>>(*bm, counts);
+    CR_RET(scan_exclusive_u64(counts, n, starts, s));
+    if (bm->n_bitmap_containers == 0 && bm->n_run_containers == 0)
+        cv_enum_write_arrays<<<(n + 3) / 4, CV_NT, 0, s>>>(*bm, starts, cap, d_out);
+    else if (bm->n_run_containers == 0)
+        cv_enum_write<true><<<n, CV_NT, 0, s>>>(*bm, starts, cap, d_out);
+    else
+        cv_enum_write<false><<<n, CV_NT, 0, s>>>(*bm, starts, cap, d_out);
+    CR_LAUNCH_CHECK();
+    return CR_OK;
+}
+
 int enumerate_impl(const cr_gpu_roaring* bm, int64_t* d_out, uint64_t cap, hipStream_t s)
 {
     if (bm->n_containers == 0 || bm->total_cardinality == 0) return CR_OK;  // src/to_csr.cu:163
@@ -627,6 +647,72 @@ extern "C" int cr_enumerate_ids(const cr_gpu_roaring* bm, int64_t* d_out, uint64
         return CR_ERR_INVALID;
     }
     return enumerate_impl(bm, d_out, out_capacity, as_stream(stream));
+}
+
+// ---- enumerate_ids without allocation ---------------------------------------
+// For callers that cannot allocate device memory (code under graph capture,
+// serving loops): the per-container counts and starts live in `scratch`, a
+// file-scope device array sized for the most containers a bitmap can hold
+// (65536 keys): 2 x 65536 u64 = 1 MiB, held by every device the library runs
+// on until the process ends.  Host code never passes `scratch` itself to a
+// kernel (in host code the name is a stand-in, not a device address): the
+// entry point's first call on a device looks up that device's copy with
+// hipGetSymbolAddress and keeps the address.  All calls on one device share
+// the array, so calls that overlap on one device (different streams, or
+// threads) race; calls on one stream are ordered.
+constexpr uint32_t NOALLOC_MAX_CONTAINERS = 65536;
+static __device__ __align__(256) uint64_t scratch[2 * NOALLOC_MAX_CONTAINERS];
+
+namespace {
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+uint64_t* g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
+
+// The current device's copy of `scratch`, looked up once per device.
+int scratch_of_current_device(uint64_t** out)
+{
+    int dev = -1;
+    CR_HIP_RET(hipGetDevice(&dev));
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) {
+        set_error("cr_enumerate_ids_noalloc: device %d outside the %d devices supported", dev, NOALLOC_MAX_DEVICES);
+        return CR_ERR_UNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            set_error("cr_enumerate_ids_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                      hipGetErrorString(e));
+            return CR_ERR_HIP;
+        }
+        g_scratch_ptr[dev] = static_cast<uint64_t*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return CR_OK;
+}
+}  // namespace
+
+extern "C" int cr_enumerate_ids_noalloc(const cr_gpu_roaring* bm, int64_t* d_out, uint64_t out_capacity,
+                                        cr_stream_t stream)
+{
+    if (!bm) {
+        set_error("cr_enumerate_ids_noalloc: invalid argument");
+        return CR_ERR_INVALID;
+    }
+    if (bm->n_containers == 0 || bm->total_cardinality == 0) return CR_OK;  // src/to_csr.cu:163
+    if (!d_out) {
+        set_error("cr_enumerate_ids_noalloc: null output");
+        return CR_ERR_INVALID;
+    }
+    if (bm->n_containers > NOALLOC_MAX_CONTAINERS) {
+        set_error("cr_enumerate_ids_noalloc: %u containers exceed the scratch bound of %u", bm->n_containers,
+                  NOALLOC_MAX_CONTAINERS);
+        return CR_ERR_INVALID;
+    }
+    uint64_t* sp = nullptr;
+    CR_RET(scratch_of_current_device(&sp));
+    return enumerate_launch(bm, d_out, out_capacity, sp, sp + NOALLOC_MAX_CONTAINERS, as_stream(stream));
 }
 
 extern "C" int cr_enumerate_ids_alloc(const cr_gpu_roaring* bm, cr_stream_t stream, int64_t** d_out,

@@ -266,6 +266,16 @@ int cr_enumerate_ids(const cr_gpu_roaring* bm, int64_t* d_out, uint64_t out_capa
  * too small there); *n_out (may be NULL) receives that count.
  * total_cardinality == 0 gives *d_out = NULL. */
 int cr_enumerate_ids_alloc(const cr_gpu_roaring* bm, cr_stream_t stream, int64_t** d_out, uint64_t* n_out);
+/* enumerate_ids without any allocation.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops).  Same output as cr_enumerate_ids.  Its
+ * per-container scratch is a fixed 1 MiB device array per device (2 x 65536
+ * u64, held until the process ends); bitmaps of more than 65536 containers are
+ * rejected with CR_ERR_INVALID.  Every call on a device shares that array, so
+ * calls that overlap on one device (other streams or threads) race; calls on
+ * one stream are ordered.  The first call on a device looks the array up
+ * (with that device current). */
+int cr_enumerate_ids_noalloc(const cr_gpu_roaring* bm, int64_t* d_out, uint64_t out_capacity, cr_stream_t stream);
 /* promote_to_bitmap (include/cu_roaring/detail/promote.cuh:48; src/promote.cu:233-323):
  * a new all-bitmap GpuRoaring; cardinalities are copied verbatim (a run
  * container's entry keeps its run count), key_index/max_key come from U. */
