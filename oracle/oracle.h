@@ -116,10 +116,12 @@ rl_bitmap* rl_create(void);
 void rl_destroy(rl_bitmap* b);
 rl_bitmap* rl_from_sorted_ids(const uint32_t* ids, uint64_t n); /* sorted, unique */
 rl_bitmap* rl_from_ids(const uint32_t* ids, uint64_t n);        /* any order, dups ok */
+rl_bitmap* rl_from_words(const uint64_t* words, uint64_t n_words); /* flat bitset, bit i = id i */
 rl_bitmap* rl_copy(const rl_bitmap* b);
 void rl_run_optimize(rl_bitmap* b);
 rl_bitmap* rl_op(const rl_bitmap* a, const rl_bitmap* b, int op);
 rl_bitmap* rl_flip(const rl_bitmap* b, uint64_t lo, uint64_t hi);
+rl_bitmap* rl_slice(const rl_bitmap* b, uint32_t key_lo, uint32_t key_hi); /* keys in [lo, hi), copied */
 int rl_contains(const rl_bitmap* b, uint32_t id);
 void rl_contains_many(const rl_bitmap* b, const uint32_t* ids, uint64_t n, uint32_t* out);
 uint64_t rl_cardinality(const rl_bitmap* b);
@@ -152,6 +154,19 @@ uint64_t orc_splitmix64(uint64_t x);
 void orc_topk_bruteforce(const float* base, uint64_t n_base, const float* queries, uint32_t n_q,
                          uint32_t dim, const uint8_t* pass, uint32_t k, double* out_dist,
                          int64_t* out_ids, int n_threads);
+
+/* ---- CPU baselines timed by bench.py (cpu_baseline.c) --------------------
+ * Each returns the seconds of its timed work; threads >= 1. */
+double orc_cpu_upload_ids(const uint32_t* ids, uint64_t n, uint32_t universe, int threads, orc_roaring* out);
+double orc_cpu_setop(const rl_bitmap* const* a_shards, const rl_bitmap* const* b_shards, uint32_t n_shards, int op,
+                     int threads, uint64_t* out_card, uint64_t* out_containers);
+double orc_cpu_multi_and(const rl_bitmap* const* inputs, uint32_t k, uint32_t n_shards, int threads,
+                         uint64_t* out_card, uint64_t* out_containers);
+double orc_cpu_contains(const rl_bitmap* b, const uint32_t* q, uint64_t n, uint32_t* out, int threads);
+double orc_cpu_config0(const uint32_t* a_ids, uint64_t na, const uint32_t* b_ids, uint64_t nb, const uint32_t* q,
+                       uint64_t nq, double* t_parts, uint64_t* cards, uint64_t* hits);
+double orc_cpu_topk_fp32(const float* base, uint64_t n_base, const float* queries, uint32_t n_q, uint32_t dim,
+                         const uint8_t* pass, uint32_t k, float* out_dist, int64_t* out_ids, int threads);
 
 #ifdef __cplusplus
 }

@@ -129,6 +129,23 @@ def lib():
         L.orc_splitmix64.restype = C.c_uint64
         L.orc_topk_bruteforce.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint32, C.c_uint32,
                                           C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_int]
+        L.rl_from_words.argtypes = [C.c_void_p, C.c_uint64]
+        L.rl_from_words.restype = C.c_void_p
+        L.rl_slice.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32]
+        L.rl_slice.restype = C.c_void_p
+        # CPU baselines (cpu_baseline.c)
+        for name in ("orc_cpu_upload_ids", "orc_cpu_setop", "orc_cpu_multi_and", "orc_cpu_contains",
+                     "orc_cpu_config0", "orc_cpu_topk_fp32"):
+            getattr(L, name).restype = C.c_double
+        L.orc_cpu_upload_ids.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_int, P(_OrcRoaring)]
+        L.orc_cpu_setop.argtypes = [C.c_void_p, C.c_void_p, C.c_uint32, C.c_int, C.c_int, P(C.c_uint64),
+                                    P(C.c_uint64)]
+        L.orc_cpu_multi_and.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_int, P(C.c_uint64), P(C.c_uint64)]
+        L.orc_cpu_contains.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p, C.c_int]
+        L.orc_cpu_config0.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64,
+                                      C.c_void_p, C.c_void_p, P(C.c_uint64)]
+        L.orc_cpu_topk_fp32.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,
+                                        C.c_uint32, C.c_void_p, C.c_void_p, C.c_int]
         _lib = L
     return _lib
 
@@ -358,6 +375,14 @@ class Lite:
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
         return Lite(lib().rl_from_sorted_ids(_ptr(ids), ids.size))
 
+    @staticmethod
+    def from_words(words) -> "Lite":
+        """A flat bitset (u64 words, or u32 words reinterpreted; bit i = id i)."""
+        w = np.ascontiguousarray(words)
+        if w.dtype != np.uint64:
+            w = np.ascontiguousarray(np.frombuffer(w.tobytes() + b"\0" * (-w.nbytes % 8), dtype=np.uint64))
+        return Lite(lib().rl_from_words(_ptr(w), w.size))
+
     def copy(self) -> "Lite":
         return Lite(lib().rl_copy(self.h))
 
@@ -408,6 +433,15 @@ class Lite:
         if not h:
             raise ValueError("not a well-formed portable Roaring bitmap")
         return Lite(h)
+
+    def slice(self, key_lo: int, key_hi: int) -> "Lite":
+        """The containers of keys [key_lo, key_hi), copied."""
+        return Lite(lib().rl_slice(self.h, key_lo, key_hi))
+
+    def shards(self, n: int, n_keys: int = 65536):
+        """n slices over equal key ranges of [0, n_keys)."""
+        step = (n_keys + n - 1) // n
+        return [self.slice(i * step, min(n_keys, (i + 1) * step)) for i in range(n)]
 
     def type_counts(self):
         a, b, c = C.c_uint32(), C.c_uint32(), C.c_uint32()
@@ -486,3 +520,69 @@ def topk_bruteforce(base: np.ndarray, queries: np.ndarray, k: int, passing: Opti
     lib().orc_topk_bruteforce(_ptr(base), base.shape[0], _ptr(queries), nq, dim, _ptr(p) if p is not None else None,
                               k, _ptr(dist), _ptr(ids), n_threads)
     return dist, ids
+
+
+# ---- CPU baselines (cpu_baseline.c): each returns (seconds of timed work, result) ----
+def _handles(lites):
+    arr = (C.c_void_p * max(1, len(lites)))(*[x.h for x in lites])
+    return arr
+
+
+def cpu_upload_ids(ids, universe: int, threads: int):
+    """(seconds, HostRoaring) of the threaded bucket-build upload (all-bitmap layout)."""
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    c = _OrcRoaring()
+    t = lib().orc_cpu_upload_ids(_ptr(ids), ids.size, universe, threads, C.byref(c))
+    if t < 0:
+        raise RuntimeError("orc_cpu_upload_ids: invalid input (key past max_key, or a complement)")
+    return t, _from_c(c)
+
+
+def cpu_setop(a_shards, b_shards, op: int, threads: int):
+    """(seconds, total cardinality, containers) of rl_op over paired shards."""
+    card, nc = C.c_uint64(), C.c_uint64()
+    t = lib().orc_cpu_setop(_handles(a_shards), _handles(b_shards), len(a_shards), op, threads, C.byref(card),
+                            C.byref(nc))
+    return t, card.value, nc.value
+
+
+def cpu_multi_and(input_shards, threads: int):
+    """input_shards[j][s]: shard s of input j.  (seconds, cardinality, containers) of the AND chain."""
+    k, n = len(input_shards), len(input_shards[0])
+    flat = [x for shards in input_shards for x in shards]
+    card, nc = C.c_uint64(), C.c_uint64()
+    t = lib().orc_cpu_multi_and(_handles(flat), k, n, threads, C.byref(card), C.byref(nc))
+    return t, card.value, nc.value
+
+
+def cpu_contains(lite: "Lite", q, threads: int):
+    q = np.ascontiguousarray(q, dtype=np.uint32)
+    out = np.zeros(q.size, dtype=np.uint32)
+    t = lib().orc_cpu_contains(lite.h, _ptr(q), q.size, _ptr(out), threads)
+    return t, out
+
+
+def cpu_config0(a_ids, b_ids, q):
+    """(seconds total, [build, ops, queries] seconds, [AND, OR, ANDNOT, XOR] cards, hits)."""
+    a = np.ascontiguousarray(a_ids, dtype=np.uint32)
+    b = np.ascontiguousarray(b_ids, dtype=np.uint32)
+    q = np.ascontiguousarray(q, dtype=np.uint32)
+    parts = np.zeros(3, dtype=np.float64)
+    cards = np.zeros(4, dtype=np.uint64)
+    hits = C.c_uint64()
+    t = lib().orc_cpu_config0(_ptr(a), a.size, _ptr(b), b.size, _ptr(q), q.size, _ptr(parts), _ptr(cards),
+                              C.byref(hits))
+    return t, parts.tolist(), [int(x) for x in cards], hits.value
+
+
+def cpu_topk_fp32(base: np.ndarray, queries: np.ndarray, k: int, passing: Optional[np.ndarray], threads: int):
+    """(seconds, dist fp32 [nq, k], ids int64 [nq, k]) of the blocked fp32 brute-force scan."""
+    base = np.ascontiguousarray(base, dtype=np.float32)
+    queries = np.ascontiguousarray(queries, dtype=np.float32)
+    nq, dim = queries.shape
+    dist = np.zeros((nq, k), dtype=np.float32)
+    ids = np.zeros((nq, k), dtype=np.int64)
+    p = None if passing is None else np.ascontiguousarray(passing, dtype=np.uint8)
+    t = lib().orc_cpu_topk_fp32(_ptr(base), base.shape[0], _ptr(queries), nq, dim,
+                                _ptr(p) if p is not None else None, k, _ptr(dist), _ptr(ids), threads)
+    return t, dist, ids

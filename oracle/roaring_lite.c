@@ -137,6 +137,22 @@ rl_bitmap* rl_from_sorted_ids(const uint32_t* ids, uint64_t n)
     return r;
 }
 
+/* A flat bitset of n_words u64 (bit i = id i) as containers, typed by
+ * cardinality (array <= 4096, else bitset). */
+rl_bitmap* rl_from_words(const uint64_t* words, uint64_t n_words)
+{
+    rl_bitmap* r = rl_create();
+    for (uint64_t w0 = 0; w0 < n_words; w0 += 1024u) {
+        uint64_t* bits = (uint64_t*)calloc(1024, 8);
+        const uint64_t nw = n_words - w0 < 1024u ? n_words - w0 : 1024u;
+        memcpy(bits, words + w0, (size_t)nw * 8u);
+        int32_t card = 0;
+        for (uint32_t w = 0; w < 1024u; ++w) card += popc64(bits[w]);
+        push_from_bits(r, (uint16_t)(w0 >> 10), bits, card);
+    }
+    return r;
+}
+
 static int cmp_u32(const void* a, const void* b)
 {
     uint32_t x = *(const uint32_t*)a, y = *(const uint32_t*)b;
@@ -402,6 +418,15 @@ rl_bitmap* rl_op(const rl_bitmap* a, const rl_bitmap* b, int op)
             ++j;
         }
     }
+    return r;
+}
+
+/* The containers of keys [key_lo, key_hi), copied (a shard by key range). */
+rl_bitmap* rl_slice(const rl_bitmap* b, uint32_t key_lo, uint32_t key_hi)
+{
+    rl_bitmap* r = rl_create();
+    for (uint32_t i = 0; i < b->n; ++i)
+        if (b->keys[i] >= key_lo && b->keys[i] < key_hi) push_copy(r, b, i);
     return r;
 }
 

@@ -104,3 +104,16 @@ def test_upload_packed_auto_guard():  # src/upload.cpp:112-118
     assert r.n_bitmap_containers == 2  # promoted: 2 * 16 KiB < 8 MiB
     r = orc.upload_packed(L, U, orc.PROMOTE_ALL)  # explicit ALL ignores the guard
     assert r.n_bitmap_containers == r.n_containers
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_lite_from_words_matches_from_ids(kind):
+    U = 5 * 65536 + 100
+    rng = np.random.default_rng(11)
+    ids = _rand_set(rng, U, kind)
+    w = flat_from_ids(ids, U)
+    a, b = orc.Lite.from_words(w), orc.Lite.from_ids(ids)
+    ca, cb = a.containers(), b.containers()
+    assert len(ca) == len(cb)
+    for x, y in zip(ca, cb):
+        assert x[:3] == y[:3] and np.array_equal(x[3], y[3])
