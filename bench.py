@@ -4,24 +4,25 @@
 BASELINE.json configs[1] (the metric "upload ms @100M IDs"): 90M distinct
 uniform ids plus 10M duplicates drawn from them, shuffled, already resident in
 HBM; one step = one upload_from_device_ids() call (all kernels, its host
-sync(s) and the allocation of the result) plus the stream-ordered free.
+sync and the allocation of the result) plus the stream-ordered free.  Steps are
+timed cold: a 512 MiB read evicts the 256 MB Infinity Cache before each step,
+outside the step's interval.  The warm (back-to-back) figure is reported beside.
 
 Also reported (extra fields, measured in the same run):
-  roofline      the dominant kernel of the step: algorithmic bytes per launch /
-                its mean launch time from HIP events recorded inside the library
-                on the library's stream during the timed steps;
-  pipeline      the whole device-resident upload against the path's algorithmic
-                bytes B = 4N + 8192 n_c + 9 n_c + 2 (max_key + 1);
-  cpu_baseline  the CPU port (oracle/ orc_upload_from_ids: sort, unique, build)
-                on a 10M-id sample, scaled x10, 1 thread;
-  secondary     set_operation AND of two 50% all-bitmap 2^30 bitmaps (GB/s of
-                algorithmic bytes), fused multi_and over 3 and 8 bitmaps, and point
-                queries (Gq/s) on a 10% 2^30 bitmap, cold (512 MiB flush before
-                each timed call); the fused filtered top-k (10M x 128 fp32 base,
-                1024 queries, k = 10 and 100, multi_and filters at 0.1-50%
-                selectivity and unfiltered) with its fp32 MFMA utilisation; the
-                conversions (decompress, enumerate_ids, promote, deep copy) and the
-                portable format on 2^30 bitmaps; the batch API on 16 x 2^28 bitmaps.
+  roofline      the path's algorithmic bytes B = 4N + 8192 n_c + 9 n_c +
+                2 (max_key + 1) over the path's device time: the sum of its
+                kernels' mean launch times from HIP events recorded inside the
+                library, on the library's stream, during the timed steps;
+                `kernels` gives each kernel's own rate;
+  cpu_baseline  the CPU port of the reference's upload (sort, unique, build) on
+                a 10M-id sample, scaled x10, at 1 thread; `threads_n` is a
+                threaded CPU build on the same sample at every host thread;
+  secondary     BASELINE configs[0] on the CPU and the GPU; configs[2] (set
+                operations over the A/B/C operands, multi_and fused and
+                pairwise); configs[3] (point queries on both layouts at four
+                densities); the fused filtered top-k; the other
+                configs[1] variants; conversions, the portable format and the
+                batch API -- each cold, with its CPU baseline where one applies.
 
 --gpus N with N > 1 exits: this build measures one GPU only.
 """
@@ -82,6 +83,16 @@ def upload_kernel_bytes(name, n, n_c, max_key):
     }.get(name)
 
 
+# The kernels of one device-resident upload_from_ids call on the headline input.
+UPLOAD_PATH = ("ids_tile_sort", "ids_build", "ids_rank")
+
+
+def evict(flush):
+    """Read 512 MiB (twice the 256 MB Infinity Cache), leaving only clean lines of it cached."""
+    import torch
+    flush.view(torch.int64).sum()
+
+
 def median(xs):
     xs = sorted(xs)
     return xs[len(xs) // 2]
@@ -91,7 +102,7 @@ def cold_time(torch, fn, iters, flush):
     """Median ms of fn() with the 256 MB Infinity Cache flushed before each call."""
     ts = []
     for _ in range(iters):
-        flush.add_(1)
+        evict(flush)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         fn()
@@ -100,115 +111,35 @@ def cold_time(torch, fn, iters, flush):
     return median(ts)
 
 
-def secondary(torch, cr, flush):
-    out = {}
-    # ---- set_operation AND, two 50% all-bitmap bitmaps over 2^30 (config 3, B x B') ----
-    import numpy as np
-    conts = []
-    for seed in (32, 33):
-        r = np.random.default_rng(seed)
-        words = r.integers(0, np.iinfo(np.uint64).max, size=(16384, 1024), dtype=np.uint64, endpoint=True)
-        cards = np.bitwise_count(words).sum(axis=1, dtype=np.int64)
-        conts.append([(k, cr.TC_BITSET, int(cards[k]), words[k]) for k in range(16384)])
-    a = cr.upload_containers(conts[0], 0, False, 0, cr.PROMOTE_KEEP_DEFAULT)
-    b = cr.upload_containers(conts[1], 0, False, 0, cr.PROMOTE_KEEP_DEFAULT)
-    del conts
-    n_c = 16384
-    setop_bytes = 3 * 8192 * n_c + 9 * 3 * n_c  # 2 inputs + 1 output container each, 9 B metadata in and out
-    for _ in range(3):
-        r = cr.set_operation(a, b, cr.AND)
-        cr.free(r)
-    cr.timing_enable(True)
-    ms = []
+SECTIONS = ("config0", "config2", "config3", "conversions", "batch", "upload_variants", "topk")
 
-    def one():
-        r = cr.set_operation(a, b, cr.AND)
-        ms.append(r)
-    t_api = cold_time(torch, one, 10, flush)
-    rep = cr.timing_report()
-    cr.timing_enable(False)
-    assert ms[0].n_containers == n_c and ms[0].n_bitmap_containers == n_c
-    for r in ms:
-        cr.free(r)
-    kn, kms = rep.get("so_exec", (1, float("nan")))
-    k_avg = kms / kn
-    out["set_op_and_50pct_2^30"] = {
-        "algorithmic_bytes": setop_bytes,
-        "api_ms": round(t_api, 4), "api_GBps": round(setop_bytes / t_api / 1e6, 1),
-        "so_exec_ms": round(k_avg, 4), "so_exec_GBps": round(setop_bytes / k_avg / 1e6, 1),
-        "so_exec_frac_of_hbm_peak": round(setop_bytes / k_avg / 1e6 / HBM_PEAK_GBS, 4),
-        "kernels_ms": {k: round(v[1] / v[0], 4) for k, v in rep.items()},
-        "cold": True,
-    }
-    cr.free(a)
-    cr.free(b)
-    log("set op done", out["set_op_and_50pct_2^30"]["so_exec_GBps"], "GB/s kernel")
 
-    # ---- fused multi_and at 2^30 (config 3): k=3 {0.1,10,50}%, k=8 {2 each of 0.1,1,10,50}% ----
-    def filt(density, seed):
-        n = int(density * U)
-        d = bijective30(torch.arange(n, device="cuda", dtype=torch.int64), seed).to(torch.int32)
-        g_ = cr.upload_from_device_ids(d, U)
-        del d
-        return g_
-    for k, dens in ((3, (0.001, 0.1, 0.5)), (8, (0.001, 0.001, 0.01, 0.01, 0.1, 0.1, 0.5, 0.5))):
-        ins = [filt(d, 100 + i) for i, d in enumerate(dens)]
-        r = cr.multi_and(ins)
-        cr.free(r)
-        cr.timing_enable(True)
-        res_ = []
-        t_api = cold_time(torch, lambda: res_.append(cr.multi_and(ins)), 5, flush)
-        rep = cr.timing_report()
-        cr.timing_enable(False)
-        n_common = res_[0].n_containers
-        for r in res_:
-            cr.free(r)
-        for x in ins:
-            cr.free(x)
-        kn, kms = rep.get("mand_and", (1, float("nan")))
-        mbytes = (k + 1) * 8192 * n_common + 9 * (k + 1) * n_common
-        out[f"multi_and_k{k}_2^30"] = {
-            "densities": list(dens), "n_common": n_common, "algorithmic_bytes": mbytes,
-            "api_ms": round(t_api, 4), "api_GBps": round(mbytes / t_api / 1e6, 1),
-            "mand_and_ms": round(kms / kn, 4), "mand_and_GBps": round(mbytes / (kms / kn) / 1e6, 1),
-            "mand_and_frac_of_hbm_peak": round(mbytes / (kms / kn) / 1e6 / HBM_PEAK_GBS, 4),
-            "kernels_ms": {kk: round(v[1] / v[0], 4) for kk, v in rep.items()}, "cold": True,
-        }
-        log(f"multi_and k={k} done", out[f"multi_and_k{k}_2^30"]["mand_and_GBps"], "GB/s kernel")
+def secondary(torch, cr, flush, no_cpu, sections):
+    nt = cpu_threads()
+    out = {"cpu": cpu_info()}
+    if "config0" in sections:
+        out["config0_2^24"] = config0(torch, cr, nt)
+    if "config2" in sections:
+        out["config2_set_ops_2^30"] = config2(torch, cr, flush, nt, no_cpu)
+        torch.cuda.empty_cache()
+    if "config3" in sections:
+        out["config3_point_queries_2^30"] = config3(torch, cr, flush, nt, no_cpu)
+    if "conversions" in sections:
+        conversion_sections(torch, cr, flush, out)
+    if "batch" in sections:
+        out["batch_16x2^28"] = batch_api(torch, cr, flush)
+        torch.cuda.empty_cache()
+    if "upload_variants" in sections:
+        out["upload_variants_2^30"] = upload_variants(torch, cr)
+    return out
 
-    # ---- point queries on a 10% all-bitmap 2^30 bitmap (config 4) ----
-    n_set = int(0.1 * U)
-    ids = bijective30(torch.arange(n_set, device="cuda", dtype=torch.int64), 40).to(torch.int32)
+
+def conversion_sections(torch, cr, flush, out):
+    """The conversions and the portable format on a 10% all-bitmap 2^30 bitmap
+    and a 0.5% array-container one."""
+    ids = bijective30(torch.arange(int(0.1 * U), device="cuda", dtype=torch.int64), 40).to(torch.int32)
     bm = cr.upload_from_device_ids(ids, U)
     del ids
-    nq = 100_000_000
-    g = torch.Generator(device="cuda")
-    g.manual_seed(44)
-    q_uni = torch.randint(0, U, (nq,), device="cuda", generator=g, dtype=torch.int64).to(torch.int32)
-    win = torch.randint(0, U >> 16, (nq // 4096,), device="cuda", generator=g, dtype=torch.int64)
-    off = torch.randint(0, 65536, (nq // 4096, 4096), device="cuda", generator=g, dtype=torch.int64)
-    q_clu = ((win[:, None] << 16) + off.sort(dim=1).values).reshape(-1).to(torch.int32)
-    res = torch.empty(nq, device="cuda", dtype=torch.int32)
-    q = {}
-    for qname, qq in (("uniform", q_uni), ("clustered", q_clu)):
-        for mname, mode in (("contains", cr.QUERY_CONTAINS), ("wavefront_contains", cr.QUERY_WAVEFRONT)):
-            cr.contains_batch(bm, qq, res, mode)
-            torch.cuda.synchronize()
-            t = cold_time(torch, lambda: cr.contains_batch(bm, qq, res, mode), 5, flush)
-            nqq = qq.numel()
-            q[f"{mname}_{qname}_Gqps"] = round(nqq / t / 1e6, 2)
-            q[f"{mname}_{qname}_frac_hbm_18B"] = round(18 * nqq / t / 1e6 / HBM_PEAK_GBS, 4)
-    # correctness at full size: every set id answers 1 (sample)
-    chk = bijective30(torch.arange(0, n_set, 997, device="cuda", dtype=torch.int64), 40).to(torch.int32)
-    cres = torch.empty_like(chk)
-    cr.contains_batch(bm, chk, cres, cr.QUERY_WAVEFRONT)
-    torch.cuda.synchronize()
-    assert bool((cres == 1).all()), "point query property check failed"
-    q["bitmap"] = "10% of 2^30 ids (all-bitmap, 16384 containers)"
-    q["queries"] = nq
-    out["contains_10pct_2^30"] = q
-    log("queries done", q)
-    del q_uni, q_clu, win, off, res, chk, cres
     torch.cuda.empty_cache()
     sparse = sparse_arrays(cr, 0.005, 60)
     out["conversions_2^30"] = conversions(torch, cr, flush, {"dense_10pct_bitmap": bm, "sparse_0.5pct_array": sparse})
@@ -216,9 +147,353 @@ def secondary(torch, cr, flush):
     cr.free(sparse)
     cr.free(bm)
     torch.cuda.empty_cache()
-    out["batch_16x2^28"] = batch_api(torch, cr, flush)
+
+
+# ---- BASELINE configs[0], [2], [3]: operands, timings and CPU baselines ------------
+def cpu_threads():
+    """Host threads for the threaded CPU baselines: every hardware thread of the
+    process's CPU share, at most 16 (the GPU box's share per GPU)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return max(1, min(16, n))
+
+
+def cpu_info():
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"model": model, "os_cpu_count": os.cpu_count(), "threads_used": cpu_threads()}
+
+
+def words_bernoulli(torch, density, seed, universe=U):
+    """A flat bitset (host u64 words) of `universe` ids at `density`: exact
+    Bernoulli(1/2) per bit at 50%, else density * U uniform draws (duplicates
+    merge), on the device."""
+    import numpy as np
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    nw = universe // 32
+    if density == 0.5:
+        w = torch.randint(-(1 << 31), 1 << 31, (nw,), device="cuda", generator=g, dtype=torch.int64).to(torch.int32)
+    else:
+        ids = torch.unique(torch.randint(0, universe, (int(density * universe),), device="cuda", generator=g))
+        w64 = torch.zeros(nw, device="cuda", dtype=torch.int64)
+        w64.index_add_(0, ids >> 5, torch.ones_like(ids) << (ids & 31))  # distinct bits: the sum is the OR
+        w = (w64 - (w64 >= (1 << 31)).to(torch.int64) * (1 << 32)).to(torch.int32)
+        del ids, w64
+    return np.ascontiguousarray(w.cpu().numpy()).view(np.uint64)
+
+
+def words_runs(coverage, seed, universe=U):
+    """Runs of length U[1000, 65536) at uniform starts until they cover
+    `coverage` of the universe (overlaps merge), as host u64 words."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    nw = universe // 64
+    w = np.zeros(nw, dtype=np.uint64)
+    covered, target = 0, int(coverage * universe)
+    full = np.uint64(0xFFFFFFFFFFFFFFFF)
+    while covered < target:
+        ln = int(rng.integers(1000, 65536))
+        st = int(rng.integers(0, universe - ln))
+        e = st + ln
+        a, b = st >> 6, (e - 1) >> 6
+        lo_mask = full << np.uint64(st & 63)
+        hi_mask = full >> np.uint64(63 - ((e - 1) & 63))
+        if a == b:
+            w[a] |= lo_mask & hi_mask
+        else:
+            w[a] |= lo_mask
+            w[a + 1:b] = full
+            w[b] |= hi_mask
+        covered += ln
+    return w
+
+
+def keep_upload(cr, lite, universe=U):
+    """The packed upload with PROMOTE_KEEP_DEFAULT (container types kept), not
+    negated (universe inferred from the last key, no complement)."""
+    return cr.upload_containers(lite.containers(), 0, False, 0, cr.PROMOTE_KEEP_DEFAULT)
+
+
+def container_bytes(cr, g):
+    """Host (keys, per-container payload bytes): bitmap 8192, array 2 card, run 4 n_runs."""
+    import numpy as np
+    n = g.n_containers
+    keys = cr._d2h(g.keys, n, np.uint16)
+    types = cr._d2h(g.types, n, np.uint8)
+    cards = cr._d2h(g.cardinalities, n, np.uint16).astype(np.int64)
+    b = np.where(types == 1, 8192, np.where(types == 0, 2 * cards, 4 * cards))
+    return keys, b
+
+
+def setop_algorithmic_bytes(cr, a, b, r, op):
+    """Input containers that take part in `op`, the output containers, 9 B of
+    metadata per container in and out."""
+    import numpy as np
+    ka, ba = container_bytes(cr, a)
+    kb, bb = container_bytes(cr, b)
+    ia = np.isin(ka, kb)
+    ib = np.isin(kb, ka)
+    if op == cr.AND:
+        nin, byin = ia.sum() + ib.sum(), ba[ia].sum() + bb[ib].sum()
+    elif op == cr.ANDNOT:
+        nin, byin = ka.size + ib.sum(), ba.sum() + bb[ib].sum()
+    else:
+        nin, byin = ka.size + kb.size, ba.sum() + bb.sum()
+    out = 8192 * r.n_bitmap_containers + r.array_pool_bytes + r.run_pool_bytes
+    return int(byin + out + 9 * (nin + r.n_containers))
+
+
+def config0(torch, cr, nt):
+    """BASELINE configs[0] at U = 2^24: A 1% and B 10% uniform draws (with
+    replacement), AND/OR/ANDNOT/XOR with their cardinalities, then 1M uniform
+    point queries.  CPU: roaring-lite at 1 thread (CRoaring's algorithms).
+    GPU: the same work through the library (ids already on the device), warm."""
+    import numpy as np
+    import orc
+    U0 = 1 << 24
+    rng1, rng2, rng3 = (np.random.default_rng(s) for s in (1, 2, 3))
+    a = rng1.integers(0, U0, 167_772, dtype=np.uint64).astype(np.uint32)
+    b = rng2.integers(0, U0, 1_677_722, dtype=np.uint64).astype(np.uint32)
+    q = rng3.integers(0, U0, 1_000_000, dtype=np.uint64).astype(np.uint32)
+    ts = [orc.cpu_config0(a, b, q) for _ in range(3)]
+    t_cpu, parts, cards, hits = sorted(ts, key=lambda x: x[0])[1]
+    da = torch.from_numpy(a.view(np.int32)).cuda()
+    db = torch.from_numpy(b.view(np.int32)).cuda()
+    dq = torch.from_numpy(q.view(np.int32)).cuda()
+    res = torch.empty_like(dq)
+
+    def gpu_run():
+        ga = cr.upload_from_device_ids(da, U0)
+        gb = cr.upload_from_device_ids(db, U0)
+        t1 = time.perf_counter()
+        c = []
+        for op in (cr.AND, cr.OR, cr.ANDNOT, cr.XOR):
+            r = cr.set_operation(ga, gb, op)
+            c.append(cr.cardinality(r))
+            cr.free_async(r)
+        t2 = time.perf_counter()
+        cr.contains_batch(ga, dq, res, cr.QUERY_CONTAINS)
+        torch.cuda.synchronize()
+        t3 = time.perf_counter()
+        cr.free_async(ga)
+        cr.free_async(gb)
+        return c, (t1, t2, t3)
+    gpu_run()
+    torch.cuda.synchronize()
+    runs = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        c, (t1, t2, t3) = gpu_run()
+        torch.cuda.synchronize()
+        runs.append(((time.perf_counter() - t0) * 1e3, (t1 - t0) * 1e3, (t2 - t1) * 1e3, (t3 - t2) * 1e3, c))
+    runs.sort(key=lambda x: x[0])
+    g_ms, g_build, g_ops, g_q, g_cards = runs[len(runs) // 2]
+    g_hits = int(res.sum().item())
+    assert g_cards == cards and g_hits == hits, ("configs[0] GPU and CPU disagree", g_cards, cards, g_hits, hits)
+    out = {"universe": U0, "a_draws": int(a.size), "b_draws": int(b.size), "queries": int(q.size),
+           "cardinalities_and_or_andnot_xor": cards, "query_hits": hits,
+           "cpu_1t": {"ms": round(t_cpu * 1e3, 3), "build_ms": round(parts[0] * 1e3, 3),
+                      "ops_ms": round(parts[1] * 1e3, 3), "queries_ms": round(parts[2] * 1e3, 3),
+                      "Mqps": round(q.size / parts[2] / 1e6, 2)},
+           "gpu": {"ms": round(g_ms, 3), "build_ms": round(g_build, 3), "ops_with_cardinality_ms": round(g_ops, 3),
+                   "queries_ms": round(g_q, 3), "note": "warm; ids on the device; each call synchronises"},
+           "same_answers": True}
+    log("configs[0]", out["cpu_1t"]["ms"], "ms CPU,", out["gpu"]["ms"], "ms GPU")
+    return out
+
+
+def config2_operands(torch, cr):
+    """configs[2] over 2^30: A/A' 0.1% (array containers), B/B' 50% (bitmaps),
+    C/C' runs U[1k,64k) to 20% (run_optimize -> run containers), as roaring-lite
+    bitmaps and their KEEP uploads.  Returns {name: (Lite, GpuRoaring)}."""
+    import orc
+    ops = {}
+    for name, make in (("A", lambda: words_bernoulli(torch, 0.001, 30)), ("A'", lambda: words_bernoulli(torch, 0.001, 31)),
+                       ("B", lambda: words_bernoulli(torch, 0.5, 32)), ("B'", lambda: words_bernoulli(torch, 0.5, 33)),
+                       ("C", lambda: words_runs(0.2, 34)), ("C'", lambda: words_runs(0.2, 35))):
+        lite = orc.Lite.from_words(make())
+        if name.startswith("C"):
+            lite.run_optimize()
+        ops[name] = (lite, keep_upload(cr, lite))
+    return ops
+
+
+SETOP_PAIRS = (("A", "B"), ("B", "A"), ("A", "C"), ("C", "A"), ("B", "C"), ("C", "B"),
+               ("A", "A'"), ("B", "B'"), ("C", "C'"))
+
+
+def config2(torch, cr, flush, nt, no_cpu):
+    """the nine operand pairs x four operations (cold, median of 3),
+    GB/s of the algorithmic bytes; the CPU baseline at 1 and nt threads."""
+    import orc
+    ops = config2_operands(torch, cr)
+    names = {cr.AND: "AND", cr.OR: "OR", cr.ANDNOT: "ANDNOT", cr.XOR: "XOR"}
+    out = {"operands": {k: {"containers": v[1].n_containers, "bitmap": v[1].n_bitmap_containers,
+                            "array": v[1].n_array_containers, "run": v[1].n_run_containers,
+                            "cardinality": int(v[0].cardinality())} for k, v in ops.items()}}
+    shards = {} if no_cpu else {k: v[0].shards(4 * nt, U >> 16) for k, v in ops.items()}
+    for x, y in SETOP_PAIRS:
+        (la, ga), (lb, gb) = ops[x], ops[y]
+        for op, oname in names.items():
+            r = cr.set_operation(ga, gb, op)  # untimed first call
+            nbytes = setop_algorithmic_bytes(cr, ga, gb, r, op)
+            card = cr.cardinality(r)
+            cr.free(r)
+            kept = []
+            cr.timing_enable(True)
+            t = cold_time(torch, lambda: kept.append(cr.set_operation(ga, gb, op)), 3, flush)
+            rep = cr.timing_report()
+            cr.timing_enable(False)
+            for rr in kept:
+                cr.free(rr)
+            kern = {k: v[1] / v[0] for k, v in rep.items() if not k.startswith("host:")}
+            dev = sum(kern.values())
+            exec_ms = kern.get("so_exec_bb", kern.get("so_exec", float("nan")))
+            line = {"algorithmic_bytes": nbytes, "api_ms": round(t, 4), "api_GBps": round(nbytes / t / 1e6, 1),
+                    "device_ms": round(dev, 4), "device_GBps": round(nbytes / dev / 1e6, 1),
+                    "exec_kernel_ms": round(exec_ms, 4),
+                    "exec_frac_of_hbm_peak": round(nbytes / exec_ms / 1e6 / HBM_PEAK_GBS, 4),
+                    "cardinality": card, "kernels_ms": {k: round(v, 4) for k, v in kern.items()}}
+            if not no_cpu:
+                t1, c1, _ = orc.cpu_setop([la], [lb], op, 1)
+                tn, cn, _ = orc.cpu_setop(shards[x], shards[y], op, nt)
+                # The reference stores a full (65536) result container's card as 0
+                # and then drops zero-card results of AND/ANDNOT/XOR
+                # (src/set_ops.cu:179-180,1111,1145); roaring-lite keeps them.
+                dropped = c1 - card
+                assert c1 == cn and dropped >= 0 and dropped % 65536 == 0 and (op != cr.OR or dropped == 0), \
+                    (x, y, oname, c1, cn, card)
+                line["cpu_1t_ms"] = round(t1 * 1e3, 3)
+                line[f"cpu_{nt}t_ms"] = round(tn * 1e3, 3)
+                if dropped:
+                    line["full_containers_dropped_as_in_reference"] = dropped // 65536
+            out[f"{x}{y}_{oname}"] = line
+        log("set ops", x, y, {o: out[f"{x}{y}_{o}"]["api_ms"] for o in names.values()})
+    # multi_and from KEEP uploads of Bernoulli bitmaps: pairwise (mixed types), and
+    # the fused path on all-bitmap uploads of the same sets
+    for k, dens in ((3, (0.001, 0.1, 0.5)), (8, (0.001, 0.001, 0.01, 0.01, 0.1, 0.1, 0.5, 0.5))):
+        lites = [orc.Lite.from_words(words_bernoulli(torch, d, 100 + i)) for i, d in enumerate(dens)]
+        for route, mk in (("pairwise_keep", lambda lt: keep_upload(cr, lt)),
+                          ("fused_all_bitmap", lambda lt: cr.upload_containers(lt.containers(), 0, False, 0,
+                                                                               cr.PROMOTE_ALL))):
+            ins = [mk(lt) for lt in lites]
+            r = cr.multi_and(ins)
+            card = cr.cardinality(r)
+            n_common = r.n_containers
+            outb = 8192 * r.n_bitmap_containers + r.array_pool_bytes + r.run_pool_bytes
+            cr.free(r)
+            kept = []
+            cr.timing_enable(True)
+            t = cold_time(torch, lambda: kept.append(cr.multi_and(ins)), 3, flush)
+            rep = cr.timing_report()
+            cr.timing_enable(False)
+            for rr in kept:
+                cr.free(rr)
+            inb = sum(int(container_bytes(cr, g)[1].sum()) + 9 * g.n_containers for g in ins)
+            kern = {kk: v[1] / v[0] for kk, v in rep.items() if not kk.startswith("host:")}
+            line = {"densities": list(dens), "route": route, "n_result_containers": n_common, "cardinality": card,
+                    "api_ms": round(t, 4), "device_ms": round(sum(kern.values()), 4),
+                    "kernels_ms": {kk: round(v, 4) for kk, v in kern.items()}}
+            if route == "fused_all_bitmap":
+                mb = (k + 1) * 8192 * n_common + 9 * (k + 1) * n_common
+                ka = kern.get("mand_and", float("nan"))
+                line.update({"algorithmic_bytes": mb, "mand_and_GBps": round(mb / ka / 1e6, 1),
+                             "mand_and_frac_of_hbm_peak": round(mb / ka / 1e6 / HBM_PEAK_GBS, 4),
+                             "api_GBps": round(mb / t / 1e6, 1)})
+            else:
+                line.update({"input_bytes": inb, "output_bytes": outb})
+            for g in ins:
+                cr.free(g)
+            out[f"multi_and_k{k}_{route}"] = line
+        if not no_cpu:
+            t1, c1, _ = orc.cpu_multi_and([[lt] for lt in lites], 1)
+            tn, cn, _ = orc.cpu_multi_and([lt.shards(4 * nt, U >> 16) for lt in lites], nt)
+            assert c1 == cn == out[f"multi_and_k{k}_fused_all_bitmap"]["cardinality"] == \
+                out[f"multi_and_k{k}_pairwise_keep"]["cardinality"]
+            out[f"multi_and_k{k}_cpu"] = {"cpu_1t_ms": round(t1 * 1e3, 3), f"cpu_{nt}t_ms": round(tn * 1e3, 3),
+                                          "algorithm": "copy of the first input ANDed with each other one"}
+        log(f"multi_and k={k}", {r_: out[f"multi_and_k{k}_{r_}"]["api_ms"] for r_ in ("pairwise_keep",
+                                                                                    "fused_all_bitmap")})
+    for _, g in ops.values():
+        cr.free(g)
+    return out
+
+
+def query_sets(torch, nq=100_000_000):
+    """configs[3] queries: uniform over 2^30 (seed 44), and sorted-clustered
+    (each group of 4096 uniform within one random 65536-aligned window, sorted;
+    seed 45)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(44)
+    q_uni = torch.randint(0, U, (nq,), device="cuda", generator=g, dtype=torch.int64).to(torch.int32)
+    g.manual_seed(45)
+    win = torch.randint(0, U >> 16, (nq // 4096,), device="cuda", generator=g, dtype=torch.int64)
+    off = torch.randint(0, 65536, (nq // 4096, 4096), device="cuda", generator=g, dtype=torch.int64)
+    q_clu = ((win[:, None] << 16) + off.sort(dim=1).values).reshape(-1).to(torch.int32)
+    return {"uniform": q_uni, "clustered": q_clu}
+
+
+def config3(torch, cr, flush, nt, no_cpu):
+    """Bernoulli bitmaps over 2^30 at 0.1/1/10/50% (seeds 40-43) in
+    the compressed layout (KEEP upload: arrays at 0.1/1%) and the promoted one
+    (ALL), 100M uniform and sorted-clustered queries, every query mode, cold.
+    Gq/s and the fraction of HBM peak at 18 B per query.  CPU: roaring-lite
+    contains on a 10M-query uniform sample at 1 and nt threads."""
+    import numpy as np
+    import orc
+    qs = query_sets(torch)
+    nq = qs["uniform"].numel()
+    res = torch.empty(nq, device="cuda", dtype=torch.int32)
+    modes = {"contains": cr.QUERY_CONTAINS, "wavefront_contains": cr.QUERY_WAVEFRONT,
+             "wavefront_contains_api": cr.QUERY_WAVEFRONT_API, "contains_api": cr.QUERY_CONTAINS_API}
+    out = {"queries": nq}
+    for j, dens in enumerate((0.001, 0.01, 0.1, 0.5)):
+        lite = orc.Lite.from_words(words_bernoulli(torch, dens, 40 + j))
+        layouts = {"compressed": keep_upload(cr, lite),
+                   "promoted": cr.upload_containers(lite.containers(), 0, False, 0, cr.PROMOTE_ALL)}
+        d = {"cardinality": int(lite.cardinality()),
+             "compressed_types": {"array": layouts["compressed"].n_array_containers,
+                                  "bitmap": layouts["compressed"].n_bitmap_containers}}
+        ref = None
+        for lname, g in layouts.items():
+            for qname, q in qs.items():
+                for mname, mode in modes.items():
+                    cr.contains_batch(g, q, res, mode)
+                    torch.cuda.synchronize()
+                    t = cold_time(torch, lambda: cr.contains_batch(g, q, res, mode), 3, flush)
+                    d[f"{lname}_{qname}_{mname}_Gqps"] = round(nq / t / 1e6, 2)
+                    if mname == "contains":
+                        d[f"{lname}_{qname}_{mname}_frac_hbm_18B"] = round(18 * nq / t / 1e6 / HBM_PEAK_GBS, 4)
+                    # every mode and layout gives the same answers (checksum of the answer vector)
+                    s_ = int((res.to(torch.int64) * (torch.arange(nq, device="cuda") % 1021 + 1)).sum().item())
+                    key = qname
+                    if ref is None:
+                        ref = {}
+                    if key not in ref:
+                        ref[key] = s_
+                    assert ref[key] == s_, ("query modes disagree", dens, lname, qname, mname)
+        if not no_cpu:
+            hq = qs["uniform"][:10_000_000].cpu().numpy().view(np.uint32)
+            t1, a1 = orc.cpu_contains(lite, hq[:2_000_000], 1)
+            tn, an = orc.cpu_contains(lite, hq, nt)
+            d["cpu_1t_Mqps"] = round(2_000_000 / t1 / 1e6, 2)
+            d[f"cpu_{nt}t_Mqps"] = round(hq.size / tn / 1e6, 2)
+            # the CPU answers equal the GPU's on the sample
+            cr.contains_batch(layouts["compressed"], qs["uniform"][:10_000_000], res[:10_000_000], cr.QUERY_CONTAINS)
+            torch.cuda.synchronize()
+            assert np.array_equal(an, res[:10_000_000].cpu().numpy().view(np.uint32)), "CPU and GPU answers differ"
+        for g in layouts.values():
+            cr.free(g)
+        out[f"density_{dens * 100:g}pct"] = d
+        log("configs[3]", dens, {k: v for k, v in d.items() if k.endswith("contains_Gqps")})
+    del qs, res
     torch.cuda.empty_cache()
-    out["upload_variants_2^30"] = upload_variants(torch, cr)
     return out
 
 
@@ -632,39 +907,80 @@ def topk_secondary(torch, cr, no_cpu):
         if f is not None:
             cr.free(f)
     if not no_cpu:
-        # Bounded CPU sample: the oracle's threaded fp64 brute force (the reference's
-        # CPU path for this workload is a brute-force scan) on 1M base vectors x 16
-        # queries, unfiltered, k=10; QPS scaled to the 10M base.
+        # Bounded CPU samples of the same workload (unfiltered): the blocked fp32
+        # brute-force scan (orc_cpu_topk_fp32) over all 10M base vectors for 64
+        # queries at every host thread, and over 1M base vectors for 16 queries at
+        # one thread (QPS scaled to the 10M base).
         import orc
-        nb, nq = 1_000_000, 16
-        hb = base[:nb].cpu().numpy()
-        hq = queries[:nq].cpu().numpy()
-        threads = min(16, os.cpu_count() or 1)
-        t0 = time.perf_counter()
-        orc.topk_bruteforce(hb, hq, 10, None, n_threads=threads)
-        dt = time.perf_counter() - t0
-        out["cpu_baseline"] = {"qps": round(nq / (dt * TK_N / nb), 3), "cores": threads, "kind": "port",
-                               "sample": "orc_topk_bruteforce (fp64, threaded) on 1M x 128 base, 16 queries, "
-                                         "k=10, unfiltered; QPS scaled to the 10M base"}
+        nt = cpu_threads()
+        hb = base.cpu().numpy()
+        hq = queries[:64].cpu().numpy()
+        cpu = {"kind": "port", "cores": nt, "cpu": cpu_info()}
+        import numpy as np
+        agree = True
+        for k in (10, 100):
+            tn, d_, i_ = orc.cpu_topk_fp32(hb, hq, k, None, nt)
+            t1, _, _ = orc.cpu_topk_fp32(hb[:1_000_000], hq[:16], k, None, 1)
+            cpu[f"k{k}_qps_{nt}t"] = round(hq.shape[0] / tn, 2)
+            cpu[f"k{k}_qps_1t"] = round(16 / (t1 * TK_N / 1_000_000), 3)
+            # the GPU's answer for the same 64 queries equals the CPU scan's
+            gd = torch.empty((64, k), device="cuda", dtype=torch.float32)
+            gi = torch.empty((64, k), device="cuda", dtype=torch.int64)
+            cr.topk_filtered(base, queries[:64], k, None, gd, gi)
+            torch.cuda.synchronize()
+            agree &= bool(np.allclose(gd.cpu().numpy(), d_, rtol=1e-4, atol=0))
+            agree &= all(set(a) == set(b) for a, b in zip(gi.cpu().numpy().tolist(), i_.tolist()))
+        cpu["gpu_answers_equal_cpu_scan"] = agree
+        cpu["sample"] = (f"orc_cpu_topk_fp32 (blocked fp32 scan, direct squared L2, AVX2) unfiltered: 10M x 128 "
+                         f"base x 64 queries at {nt} threads; 1M x 128 x 16 queries at 1 thread, scaled to 10M")
+        out["cpu_baseline"] = cpu
+        del hb
     del base, queries
     torch.cuda.empty_cache()
     return out
 
 
 def cpu_baseline(ids_host_sample):
+    """The CPU upload on a sample of the headline ids, scaled to 100M ids:
+    the reference's own CPU algorithm (sort + unique + bitmap build, 1 thread:
+    orc_upload_from_ids), and a threaded bucket build (orc_cpu_upload_ids) at 1
+    and at every host thread.  Each is the median of 3 runs."""
     import ctypes as C
 
     import numpy as np
     import orc
     lib = orc.lib()
-    c = orc._OrcRoaring()
     s = np.ascontiguousarray(ids_host_sample, dtype=np.uint32)
-    t0 = time.perf_counter()
-    rc = lib.orc_upload_from_ids(s.ctypes.data, s.size, U, orc.PROMOTE_AUTO, orc.DEFAULT_L2, C.byref(c))
-    dt = time.perf_counter() - t0
-    assert rc == 0
-    lib.orc_free(C.byref(c))
-    return dt * 1e3 * (N_IDS / s.size)
+    scale = N_IDS / s.size
+
+    def sort_based():
+        c = orc._OrcRoaring()
+        t0 = time.perf_counter()
+        rc = lib.orc_upload_from_ids(s.ctypes.data, s.size, U, orc.PROMOTE_AUTO, orc.DEFAULT_L2, C.byref(c))
+        dt = time.perf_counter() - t0
+        assert rc == 0
+        n_c = c.n_containers
+        lib.orc_free(C.byref(c))
+        return dt, n_c
+    t_sort, n_c = sorted(sort_based() for _ in range(3))[1]
+    nt = cpu_threads()
+    res = {}
+    for th in (1, nt):
+        runs = []
+        for _ in range(3):
+            t, r = orc.cpu_upload_ids(s, U, th)
+            assert r.n_containers == n_c
+            runs.append(t)
+        res[th] = sorted(runs)[1]
+    return {"value": round(res[nt] * 1e3 * scale, 1), "unit": "ms", "cores": nt, "kind": "port",
+            "sample": f"the first {s.size // 1_000_000}M of the 100M headline ids, scaled x{scale:g}: "
+                      f"orc_cpu_upload_ids (bucket partition by key range + bit set + popcount, the same "
+                      f"all-bitmap layout) at {nt} threads",
+            "one_thread_ms": round(res[1] * 1e3 * scale, 1),
+            "reference_algorithm_one_thread_ms": round(t_sort * 1e3 * scale, 1),
+            "reference_algorithm": "orc_upload_from_ids: qsort + unique + bitmap build, the reference's CPU "
+                                   "pipeline (std::sort + unique + upload, bench/bench_upload_scale.cu:177-201)",
+            "cpu": cpu_info()}
 
 
 def main():
@@ -675,6 +991,8 @@ def main():
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-topk", action="store_true")
+    ap.add_argument("--sections", default=",".join(SECTIONS),
+                    help="comma-separated secondary sections to run (default: all of " + ",".join(SECTIONS) + ")")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the sharded design is "
@@ -698,23 +1016,29 @@ def main():
     torch.cuda.synchronize()
     log("warmup done")
 
-    # HIP events around every EVENT_EVERY-th launch of each kernel: the markers
-    # cost queue time, so sampling keeps the timed steps close to untimed ones
+    # Timed steps, cold: before each step a 512 MiB read evicts the 256 MB
+    # Infinity Cache (outside the step's interval); each step is bracketed by a
+    # device synchronisation on both sides.  HIP events around every
+    # EVENT_EVERY-th launch of each kernel give the device time of the path
+    # (the markers cost queue time, so sampling keeps the steps close to
+    # untimed ones).
     cr.timing_enable(True, every=EVENT_EVERY)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
+    step_ms = []
     last = None
     for k in range(args.steps):
+        evict(flush)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
         g = cr.upload_from_device_ids(d_ids, U)
         if k == args.steps - 1:
             last = g
         else:
             cr.free_async(g)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        step_ms.append((time.perf_counter() - t0) * 1e3)
     rep = cr.timing_report()
     cr.timing_enable(False)
-    ms_per_step = elapsed * 1e3 / args.steps
+    ms_per_step = sum(step_ms) / len(step_ms)
     n_c = last.n_containers
     total = last.total_cardinality
     ok = (n_c == 16384 and total == N_DISTINCT and not last.negated and last.max_key == 16383)
@@ -722,23 +1046,39 @@ def main():
     if not ok:
         log("PROPERTY CHECK FAILED", n_c, total)
         sys.exit(1)
-    log("timed steps done", round(ms_per_step, 4), "ms/step")
+    log("timed steps done (cold)", round(ms_per_step, 4), "ms/step")
+
+    # The same steps back to back with no eviction (warm), reported beside.
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        g = cr.upload_from_device_ids(d_ids, U)
+        cr.free_async(g)
+    torch.cuda.synchronize()
+    warm_ms = (time.perf_counter() - t0) * 1e3 / args.steps
 
     per_kernel = {k: v[1] / v[0] for k, v in rep.items() if not k.startswith("host:")}
     host_ms = {k[5:]: round(v[1] / args.steps, 4) for k, v in rep.items() if k.startswith("host:")}
-    dev_ms = sum(per_kernel.values())  # each kernel launches once per step
-    dom = max(("ids_tile_sort", "ids_build"), key=lambda k: per_kernel.get(k, 0.0))
-    dom_bytes = upload_kernel_bytes(dom, N_IDS, n_c, 16383)
-    dom_ms = per_kernel[dom]
-    achieved = dom_bytes / dom_ms / 1e6
+    path = [k for k in UPLOAD_PATH if k in per_kernel]
+    dev_ms = sum(per_kernel[k] for k in path)  # each kernel launches once per step
+    dom = max(path, key=lambda k: per_kernel[k])
+    path_bytes = 4 * N_IDS + 8192 * n_c + 9 * n_c + 2 * (16383 + 1)
+    achieved = path_bytes / dev_ms / 1e6
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_upload_ids.json")
     if os.path.exists(tpath):
         try:
-            traffic = json.load(open(tpath)).get(dom)
+            tj = json.load(open(tpath))
+            traffic = sum(int(tj[k]) for k in path)
         except Exception:
             traffic = None
-    path_bytes = 4 * N_IDS + 8192 * n_c + 9 * n_c + 2 * (16383 + 1)
+    kernels = {}
+    for k in path:
+        kb = upload_kernel_bytes(k, N_IDS, n_c, 16383)
+        kernels[k] = {"mean_launch_ms": round(per_kernel[k], 5), "timed_launches": rep[k][0]}
+        if kb:
+            kernels[k].update({"algorithmic_bytes": kb, "GBps": round(kb / per_kernel[k] / 1e6, 1),
+                               "frac": round(kb / per_kernel[k] / 1e6 / HBM_PEAK_GBS, 4)})
 
     result = {
         "metric": "upload ms @100M IDs",
@@ -757,16 +1097,19 @@ def main():
         "config": {"workload": "upload_from_ids, 100M unsorted u32 ids (~10% duplicates), universe 2^30, "
                                "PROMOTE_AUTO (BASELINE configs[1], uniform variant)",
                    "universe": U, "n_ids": N_IDS, "distinct": N_DISTINCT, "parallelism": "single GPU"},
+        "timing": "cold: a 512 MiB read evicts the Infinity Cache before each step, outside its interval; "
+                  "value = mean of the steps, each bracketed by device synchronisation",
+        "warm_ms_per_step": round(warm_ms, 4),
         "ids_per_s": round(N_IDS / (ms_per_step / 1e3), 1),
-        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+        "roofline": {"bound": "hbm", "kernel": "upload_from_ids path (" + " + ".join(path) + ")",
+                     "dominant_kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes_per_launch": dom_bytes, "mean_launch_ms": round(dom_ms, 5),
-                     "timed_launches": rep.get(dom, (0, 0))[0], "events_every": EVENT_EVERY},
-        "pipeline": {"algorithmic_bytes": path_bytes, "device_ms": round(dev_ms, 4),
-                     "achieved_GBps": round(path_bytes / dev_ms / 1e6, 1),
-                     "frac": round(path_bytes / dev_ms / 1e6 / HBM_PEAK_GBS, 4),
-                     "kernels_ms": {k: round(v, 5) for k, v in per_kernel.items()},
-                     "host_ms_per_step": host_ms},
+                     "algorithmic_bytes_per_launch": path_bytes,
+                     "algorithmic_bytes_formula": "4 N + 8192 n_c + 9 n_c + 2 (max_key + 1)",
+                     "mean_launch_ms": round(dev_ms, 5), "events_every": EVENT_EVERY,
+                     "end_to_end_frac": round(path_bytes / ms_per_step / 1e6 / HBM_PEAK_GBS, 4)},
+        "kernels": kernels,
+        "host_ms_per_step": host_ms,
     }
     # Achievable-bandwidth reference: a plain 1 GiB device copy (also the known-size
     # kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE).
@@ -802,16 +1145,14 @@ def main():
     if rank == 0 and not args.no_cpu:
         log("cpu baseline (10M-id sample)")
         sample = d_ids[:10_000_000].cpu().numpy().view("uint32")
-        cms = cpu_baseline(sample)
-        result["cpu_baseline"] = {"value": round(cms, 1), "unit": "ms", "cores": 1, "kind": "port",
-                                  "sample": "orc_upload_from_ids (qsort + unique + bitmap build, the reference's "
-                                            "sort/unique/build pipeline on the CPU) on the first 10M of the 100M "
-                                            "ids, scaled x10"}
+        result["cpu_baseline"] = cpu_baseline(sample)
+        log("cpu baseline", result["cpu_baseline"])
     if not args.no_secondary:
         del d_ids
         torch.cuda.empty_cache()
-        result["secondary"] = secondary(torch, cr, flush)
-        if not args.no_topk:
+        sections = set(args.sections.split(","))
+        result["secondary"] = secondary(torch, cr, flush, args.no_cpu, sections)
+        if not args.no_topk and "topk" in sections:
             del flush
             torch.cuda.empty_cache()
             result["secondary"]["topk_10M_x128_q1024"] = topk_secondary(torch, cr, args.no_cpu)

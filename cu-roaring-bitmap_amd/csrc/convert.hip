@@ -107,11 +107,11 @@ __global__ __launch_bounds__(NT) void cv_decompress(cr_gpu_roaring r, uint32_t* 
 // containers go through LDS: the low 16 bits of each 512-word chunk's ids are
 // staged in order and then written out as coalesced int64 stores.
 // Writes stay below `cap` ids.
-__global__ __launch_bounds__(CV_NT) void cv_enum_count(cr_gpu_roaring r, uint64_t* counts)
+// Ids stored in container c (a wave computes it; every lane returns the sum):
+// a bitmap's popcount (8 loads of 16 B per lane in flight), an array's
+// cardinality, a run container's sum of (length + 1).
+__device__ inline uint32_t container_count(const cr_gpu_roaring& r, uint32_t c, uint32_t lane)
 {
-    const uint32_t c = (blockIdx.x * CV_NT + threadIdx.x) >> 6;
-    const uint32_t lane = __lane_id();
-    if (c >= r.n_containers) return;
     const uint8_t type = r.types[c];
     const uint32_t off = r.offsets[c];
     uint32_t n = 0;
@@ -134,9 +134,30 @@ __global__ __launch_bounds__(CV_NT) void cv_enum_count(cr_gpu_roaring r, uint64_
         const uint16_t* runs = r.run_data + off / 2u;
         for (uint32_t k = lane; k < r.cardinalities[c]; k += 64) n += static_cast<uint32_t>(runs[2 * k + 1]) + 1u;
     }
-    n = wave_sum(n);
+    return wave_sum(n);
+}
+
+__global__ __launch_bounds__(CV_NT) void cv_enum_count(cr_gpu_roaring r, uint64_t* counts)
+{
+    const uint32_t c = (blockIdx.x * CV_NT + threadIdx.x) >> 6;
+    const uint32_t lane = __lane_id();
+    if (c >= r.n_containers) return;
+    const uint32_t n = container_count(r, c, lane);
     if (lane == 0) counts[c] = n;
 }
+
+// Sum of the containers' counts into *total (zeroed by the caller's stream
+// order): one non-returning atomic per wave.
+__global__ __launch_bounds__(CV_NT) void cv_card_sum(cr_gpu_roaring r, unsigned long long* total)
+{
+    const uint32_t c = (blockIdx.x * CV_NT + threadIdx.x) >> 6;
+    const uint32_t lane = __lane_id();
+    if (c >= r.n_containers) return;
+    const uint32_t n = container_count(r, c, lane);
+    if (lane == 0 && n) atomicAdd(total, static_cast<unsigned long long>(n));
+}
+
+__global__ void cv_zero_u64(unsigned long long* p) { *p = 0; }
 
 // starts = exclusive scan of counts.  One workgroup per tile of 1024 counts:
 // it sums every count before its tile (coalesced, eight loads per thread in
@@ -647,6 +668,32 @@ extern "C" int cr_enumerate_ids(const cr_gpu_roaring* bm, int64_t* d_out, uint64
         return CR_ERR_INVALID;
     }
     return enumerate_impl(bm, d_out, out_capacity, as_stream(stream));
+}
+
+// ---- cardinality ---------------------------------------------------------------
+extern "C" int cr_cardinality(const cr_gpu_roaring* bm, cr_stream_t stream, uint64_t* out)
+{
+    if (!bm || !out) {
+        set_error("cr_cardinality: invalid argument");
+        return CR_ERR_INVALID;
+    }
+    uint64_t stored = 0;
+    if (bm->n_containers) {
+        hipStream_t s = as_stream(stream);
+        Scratch sc;
+        CR_RET(sc.alloc(256, s));
+        unsigned long long* d_total = sc.at<unsigned long long>(0);
+        {
+            CR_TIMED("cv_card_sum", s);
+            cv_zero_u64<<<1, 1, 0, s>>>(d_total);
+            cv_card_sum<<<(bm->n_containers + 3) / 4, CV_NT, 0, s>>>(*bm, d_total);
+        }
+        CR_LAUNCH_CHECK();
+        CR_RET(read_back(&stored, d_total, sizeof(stored), s));
+    }
+    // the logical set: a negated bitmap stores its complement within [0, U)
+    *out = bm->negated ? (bm->universe_size > stored ? bm->universe_size - stored : 0) : stored;
+    return CR_OK;
 }
 
 // ---- enumerate_ids without allocation ---------------------------------------

@@ -70,6 +70,13 @@ int64_t* enumerate_ids(const GpuRoaring& bitmap, hipStream_t stream)
     return out;
 }
 
+uint64_t cardinality(const GpuRoaring& bitmap, hipStream_t stream)
+{
+    uint64_t n = 0;
+    throw_on_error(cr_cardinality(to_abi(&bitmap), S(stream), &n), "cardinality");
+    return n;
+}
+
 size_t portable_size_in_bytes(const GpuRoaring& bm, hipStream_t stream)
 {
     size_t n = 0;

@@ -34,7 +34,7 @@ EXPORTS = [
     "cr_topk_filtered", "cr_topk_set_small_limit", "cr_device_l2_bytes", "cr_device_malloc", "cr_device_free", "cr_memcpy_h2d",
     "cr_memcpy_d2h", "cr_stream_synchronize", "cr_timing_enable", "cr_timing_report", "cr_mempool_trim",
     "cr_decompress_to_bitset", "cr_decompress_to_bitset_alloc", "cr_enumerate_ids", "cr_enumerate_ids_alloc",
-    "cr_enumerate_ids_noalloc",
+    "cr_enumerate_ids_noalloc", "cr_cardinality",
     "cr_promote_to_bitmap", "cr_promote_auto", "cr_deep_copy",
     "cr_portable_size_in_bytes", "cr_portable_serialize", "cr_portable_deserialize",
     "cr_upload_batch", "cr_free_batch", "cr_promote_batch", "cr_batch_make_view", "cr_batch_multi_and",
@@ -174,6 +174,7 @@ def load(path: Optional[str] = None):
         "cr_enumerate_ids": [P(GpuRoaring), C.c_void_p, C.c_uint64, C.c_void_p],
         "cr_enumerate_ids_alloc": [P(GpuRoaring), C.c_void_p, P(C.c_void_p), P(C.c_uint64)],
         "cr_enumerate_ids_noalloc": [P(GpuRoaring), C.c_void_p, C.c_uint64, C.c_void_p],
+        "cr_cardinality": [P(GpuRoaring), C.c_void_p, P(C.c_uint64)],
         "cr_promote_to_bitmap": [P(GpuRoaring), C.c_void_p, P(GpuRoaring)],
         "cr_promote_auto": [P(GpuRoaring), C.c_void_p, C.c_int, P(GpuRoaring)],
         "cr_deep_copy": [P(GpuRoaring), C.c_void_p, P(GpuRoaring)],
@@ -364,6 +365,13 @@ def decompress_to_bitset_alloc(g: GpuRoaring, stream=None):
 def enumerate_ids(g: GpuRoaring, d_out, capacity: int = NO_BOUND, stream=None):
     """enumerate_ids into d_out (a CUDA int64 tensor)."""
     _check(load().cr_enumerate_ids(C.byref(g), _dptr(d_out), capacity, _stream(stream)), "enumerate_ids")
+
+
+def cardinality(g: GpuRoaring, stream=None) -> int:
+    """The logical cardinality counted on the device (set-operation results included)."""
+    n = C.c_uint64()
+    _check(load().cr_cardinality(C.byref(g), _stream(stream), C.byref(n)), "cardinality")
+    return n.value
 
 
 def enumerate_ids_noalloc(g: GpuRoaring, d_out, capacity: int = NO_BOUND, stream=None):

@@ -15,4 +15,11 @@ void enumerate_ids(const GpuRoaring& bitmap, int64_t* output, hipStream_t stream
 // the caller frees the buffer with hipFree.
 int64_t* enumerate_ids(const GpuRoaring& bitmap, hipStream_t stream = 0);
 
+// The logical cardinality, counted on the device from the containers (no
+// reference counterpart): set_operation leaves total_cardinality at 0 and a
+// stored card of 0 can mean 65536, so this is the exact count of any result.
+// A negated bitmap counts its complement within [0, universe_size).
+// Synchronises `stream`.
+uint64_t cardinality(const GpuRoaring& bitmap, hipStream_t stream = 0);
+
 }  // namespace cu_roaring

@@ -266,6 +266,13 @@ int cr_enumerate_ids(const cr_gpu_roaring* bm, int64_t* d_out, uint64_t out_capa
  * too small there); *n_out (may be NULL) receives that count.
  * total_cardinality == 0 gives *d_out = NULL. */
 int cr_enumerate_ids_alloc(const cr_gpu_roaring* bm, cr_stream_t stream, int64_t** d_out, uint64_t* n_out);
+/* The logical cardinality, counted on the device from the containers' bits
+ * (popcount for bitmaps, cards for arrays, sum of lengths for runs); a negated
+ * bitmap counts its complement within [0, U).  No counterpart in the
+ * reference, which has no accessor: set_operation leaves total_cardinality 0
+ * (src/set_ops.cu:1162-1175) and a stored card of 0 may mean 65536.
+ * Synchronises the stream. */
+int cr_cardinality(const cr_gpu_roaring* bm, cr_stream_t stream, uint64_t* out);
 /* enumerate_ids without any allocation.  No counterpart in the reference: it
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops).  Same output as cr_enumerate_ids.  Its

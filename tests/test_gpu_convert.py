@@ -210,3 +210,18 @@ def test_conversions_large_properties(gpu):
     assert np.array_equal(out.cpu().numpy(), want.astype(np.int64))
     gpu.free(p)
     gpu.free(g)
+
+
+# ---- cardinality ---------------------------------------------------------------------
+@pytest.mark.parametrize("kind", KINDS)
+def test_cardinality(gpu, kind):
+    """The device count equals the popcount of the oracle's logical decode of the
+    same structure (set-operation results, whose total_cardinality is 0, included)."""
+    _say("cardinality", kind)
+    g, stored = _make(gpu, kind)
+    host = gpu.download(g)
+    want = int(np.bitwise_count(orc.decompress(host)).sum()) if host.universe_size else orc.true_cardinality(host)
+    if stored is not None and not g.negated:
+        assert want == stored.size
+    assert gpu.cardinality(g) == want
+    gpu.free(g)
