@@ -98,16 +98,20 @@ def median(xs):
     return xs[len(xs) // 2]
 
 
-def cold_time(torch, fn, iters, flush):
-    """Median ms of fn() with the 256 MB Infinity Cache flushed before each call."""
+def cold_time(torch, fn, iters, flush, after=None):
+    """Median ms of fn() with the 256 MB Infinity Cache flushed before each call;
+    after(result), if given, runs outside the timed interval (a result freed
+    there returns its block to the library's cache, as in a steady state)."""
     ts = []
     for _ in range(iters):
         evict(flush)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        fn()
+        r = fn()
         torch.cuda.synchronize()
         ts.append((time.perf_counter() - t0) * 1e3)
+        if after is not None:
+            after(r)
     return median(ts)
 
 
@@ -345,13 +349,10 @@ def config2(torch, cr, flush, nt, no_cpu):
             nbytes = setop_algorithmic_bytes(cr, ga, gb, r, op)
             card = cr.cardinality(r)
             cr.free(r)
-            kept = []
             cr.timing_enable(True)
-            t = cold_time(torch, lambda: kept.append(cr.set_operation(ga, gb, op)), 3, flush)
+            t = cold_time(torch, lambda: cr.set_operation(ga, gb, op), 3, flush, after=cr.free)
             rep = cr.timing_report()
             cr.timing_enable(False)
-            for rr in kept:
-                cr.free(rr)
             kern = {k: v[1] / v[0] for k, v in rep.items() if not k.startswith("host:")}
             dev = sum(kern.values())
             exec_ms = kern.get("so_exec_bb", kern.get("so_exec", float("nan")))
@@ -388,13 +389,10 @@ def config2(torch, cr, flush, nt, no_cpu):
             n_common = r.n_containers
             outb = 8192 * r.n_bitmap_containers + r.array_pool_bytes + r.run_pool_bytes
             cr.free(r)
-            kept = []
             cr.timing_enable(True)
-            t = cold_time(torch, lambda: kept.append(cr.multi_and(ins)), 3, flush)
+            t = cold_time(torch, lambda: cr.multi_and(ins), 3, flush, after=cr.free)
             rep = cr.timing_report()
             cr.timing_enable(False)
-            for rr in kept:
-                cr.free(rr)
             inb = sum(int(container_bytes(cr, g)[1].sum()) + 9 * g.n_containers for g in ins)
             kern = {kk: v[1] / v[0] for kk, v in rep.items() if not kk.startswith("host:")}
             line = {"densities": list(dens), "route": route, "n_result_containers": n_common, "cardinality": card,

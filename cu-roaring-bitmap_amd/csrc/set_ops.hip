@@ -7,8 +7,9 @@
 // (:1715-1745).  The structure is new: container matching runs on the device
 // over the 65536-key space (one thread per key), every pair type runs in one
 // grid-stride kernel (one workgroup per output container), and the output
-// metadata is compacted on the device, so a call costs two host syncs instead
-// of the reference's per-class round trips.
+// metadata is compacted on the device, so a call costs one host sync (its
+// output is sized from the inputs' container counts) instead of the
+// reference's per-class round trips.
 #include <algorithm>
 
 #include "internal.hpp"
@@ -41,8 +42,23 @@ enum { C_ITEM, C_BB, C_MX, C_CB, C_BAE, C_AAE, C_CAE, C_CRP, C_BA, C_AA, C_CA, C
 
 struct Totals {
     uint32_t c[C_N];
-    uint32_t n_out;  // containers kept after the zero-card drop
-    uint32_t pad[3];
+    uint32_t n_out;     // containers kept after the zero-card drop
+    uint32_t overflow;  // the plan needs more output than the caller's capacity
+    uint32_t pad[2];
+};
+
+// What the host reads after the call's one synchronisation (a pinned slot).
+struct SetOpHost {
+    uint32_t c[C_N];
+    uint32_t n_out;
+    uint32_t overflow;
+};
+
+// Output capacity the host allocated before planning: work items (metadata
+// entries), bitmap slots, array elements, run u16s.  0xFFFFFFFF = unbounded.
+struct Caps {
+    uint32_t items, bmp, arr, run_u16;
+    uint32_t bb_only;  // the host launches the bitmap-only kernel: every item must be BB or COPY_BMP
 };
 
 struct Side {  // the parts of a GpuRoaring the kernels read
@@ -152,7 +168,7 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_classify(Side A, Side B, uint
 // ---- plan pass 2: slot assignment in key order -----------------------------
 __global__ __launch_bounds__(PLAN_NT) void so_plan_assign(const KeyRec* recs, const uint32_t* group_counts,
                                                           Item* items, Totals* totals, uint32_t* tile_keep,
-                                                          uint32_t n_tiles)
+                                                          uint32_t n_tiles, Caps caps)
 {
     __shared__ uint32_t gbase[C_N], gtot[C_N];
     __shared__ uint32_t scan_lds[PLAN_NT / 64];
@@ -173,6 +189,10 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_assign(const KeyRec* recs, co
     __syncthreads();
     if (blockIdx.x == 0 && t < C_N) totals->c[t] = gtot[t];
     if (blockIdx.x == 0 && t == C_N) totals->n_out = 0;
+    if (blockIdx.x == 0 && t == C_N + 1)
+        totals->overflow = gtot[C_ITEM] > caps.items || gtot[C_BB] + gtot[C_MX] + gtot[C_CB] > caps.bmp ||
+                           gtot[C_BAE] + gtot[C_AAE] + gtot[C_CAE] > caps.arr || 2u * gtot[C_CRP] > caps.run_u16 ||
+                           (caps.bb_only && gtot[C_BB] + gtot[C_CB] != gtot[C_ITEM]);
 
     const uint32_t key = blockIdx.x * PLAN_NT + t;
     const KeyRec rec = recs[key];
@@ -208,6 +228,109 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_assign(const KeyRec* recs, co
     it.boff = rec.boff;
     it.slot = slot;
     items[item_pos] = it;
+}
+
+// ---- plan for two all-bitmap inputs with key indexes -------------------------
+// Every pair is bitmap x bitmap and every one-sided key a bitmap copy, so a
+// key's category follows from its presence in the two key_index arrays alone
+// (an entry below n_containers).  One workgroup per 1024 keys; each first
+// counts, over the whole key space with 16-byte loads, the items and pairs
+// before its keys and in total (no workgroup waits on another), then ranks its
+// own keys: item position in key order, bitmap slot with pairs first and
+// copies after them, the reference's pool order (src/set_ops.cu:695-701).  The
+// last workgroup writes the totals and flags an overflow when the key indexes
+// do not name exactly n_containers keys per side or the plan outgrows the
+// output capacity; an item whose container is not a bitmap is marked invalid
+// (the compaction reports it).  Either way the host redoes the call on the
+// exact path.
+constexpr int KP_NT = 1024;
+
+__device__ __forceinline__ uint64_t kidx_presence64(const uint16_t* kidx, uint32_t len, uint32_t n, uint32_t k0)
+{
+    uint64_t p = 0;
+    if ((reinterpret_cast<uintptr_t>(kidx) & 15u) == 0 && k0 + 64u <= len) {
+        const uint4* v = reinterpret_cast<const uint4*>(kidx + k0);
+        uint4 x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = v[j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t w[4] = {x[j].x, x[j].y, x[j].z, x[j].w};
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                p |= static_cast<uint64_t>((w[h] & 0xFFFFu) < n) << (8 * j + 2 * h);
+                p |= static_cast<uint64_t>((w[h] >> 16) < n) << (8 * j + 2 * h + 1);
+            }
+        }
+    } else {
+        for (uint32_t k = 0; k < 64u && k0 + k < len; ++k) p |= static_cast<uint64_t>(kidx[k0 + k] < n) << k;
+    }
+    return p;
+}
+
+__global__ __launch_bounds__(KP_NT) void so_plan_bitmap(const uint16_t* __restrict__ kidx_a, uint32_t len_a,
+                                                        const uint16_t* __restrict__ kidx_b, uint32_t len_b,
+                                                        const uint32_t* __restrict__ off_a,
+                                                        const uint32_t* __restrict__ off_b,
+                                                        const uint8_t* __restrict__ ty_a,
+                                                        const uint8_t* __restrict__ ty_b, uint32_t na, uint32_t nb,
+                                                        uint32_t op, Caps caps, Item* items, Totals* totals)
+{
+    __shared__ uint32_t lds[KP_NT / 64];
+    const uint32_t t = threadIdx.x, g = blockIdx.x;
+    const uint32_t kbase = g * KP_NT;
+    auto item_mask = [op](uint64_t a, uint64_t b) {
+        return op == CR_AND ? (a & b) : (op == CR_ANDNOT ? a : (a | b));
+    };
+    // Counts over the whole key space: thread t takes keys [64 t, 64 t + 64).
+    const uint64_t pa = kidx_presence64(kidx_a, len_a, na, 64u * t);
+    const uint64_t pb = kidx_presence64(kidx_b, len_b, nb, 64u * t);
+    const uint64_t m = item_mask(pa, pb), mbb = m & pa & pb;
+    // keys of this thread's 64 that lie before this workgroup's range
+    const uint64_t before = 64u * t + 64u <= kbase ? ~0ull : (64u * t >= kbase ? 0ull : ((1ull << (kbase - 64u * t)) - 1ull));
+    const uint32_t it_before = block_sum<KP_NT>(static_cast<uint32_t>(__popcll(m & before)), lds);
+    const uint32_t bb_before = block_sum<KP_NT>(static_cast<uint32_t>(__popcll(mbb & before)), lds);
+    const uint32_t bb_total = block_sum<KP_NT>(static_cast<uint32_t>(__popcll(mbb)), lds);
+    // This workgroup's keys, one per thread.
+    const uint32_t key = kbase + t;
+    const uint32_t xa = key < len_a ? kidx_a[key] : 0xFFFFu;
+    const uint32_t xb = key < len_b ? kidx_b[key] : 0xFFFFu;
+    const bool ina = xa < na, inb = xb < nb;
+    const bool is_item = (item_mask(ina, inb) & 1u) != 0;
+    const bool is_bb = is_item && ina && inb;
+    uint32_t n_here, bb_here, cb_here;
+    const uint32_t r_item = block_flag_rank<KP_NT>(is_item, lds, n_here);
+    const uint32_t r_bb = block_flag_rank<KP_NT>(is_bb, lds, bb_here);
+    const uint32_t r_cb = block_flag_rank<KP_NT>(is_item && !is_bb, lds, cb_here);
+    const uint32_t pos = it_before + r_item;
+    if (is_item && pos < caps.items) {
+        Item it;
+        it.key = static_cast<uint16_t>(key);
+        it.pad = 0;
+        it.ai = ina ? static_cast<int32_t>(xa) : -1;
+        it.bi = inb ? static_cast<int32_t>(xb) : -1;
+        it.aoff = ina ? off_a[xa] : 0u;
+        it.boff = inb ? off_b[xb] : 0u;
+        // a container that is not a bitmap (counts that misdescribe the input)
+        // makes the item invalid: the exec skips it and the compaction reports it
+        const bool bitmaps = (!ina || ty_a[xa] == CR_BITMAP) && (!inb || ty_b[xb] == CR_BITMAP);
+        it.cat = !bitmaps ? CAT_NONE : (is_bb ? CAT_BB : CAT_COPY_BMP);
+        it.slot = is_bb ? bb_before + r_bb : bb_total + (it_before - bb_before) + r_cb;
+        items[pos] = it;
+    }
+    if (g == gridDim.x - 1) {  // the last workgroup sees every key before its own
+        const uint32_t n_items = it_before + n_here;
+        const uint32_t n_a = block_sum<KP_NT>(static_cast<uint32_t>(__popcll(pa)), lds);
+        const uint32_t n_b = block_sum<KP_NT>(static_cast<uint32_t>(__popcll(pb)), lds);
+        if (t == 0) {
+            for (int k = 0; k < C_N; ++k) totals->c[k] = 0;
+            totals->c[C_ITEM] = n_items;
+            totals->c[C_BB] = bb_total;
+            totals->c[C_CB] = n_items - bb_total;
+            totals->n_out = 0;
+            totals->overflow = (n_a != na || n_b != nb || n_items > caps.items || n_items > caps.bmp) ? 1u : 0u;
+        }
+    }
 }
 
 // ---- execution: one workgroup per item --------------------------------------
@@ -312,6 +435,7 @@ __global__ __launch_bounds__(EXEC_NT) void so_exec(Side A, Side B, const Item* i
 {
     __shared__ uint32_t lds[4096];  // 16 KiB: two expanded bitmaps, or a staged array
     __shared__ uint32_t red[EXEC_NT / 64];
+    if (totals->overflow) return;  // the output was not allocated for this plan
     const uint32_t n_items = totals->c[C_ITEM];
     const uint32_t t = threadIdx.x;
     for (uint32_t w = blockIdx.x; w < n_items; w += gridDim.x) {
@@ -458,18 +582,26 @@ __global__ __launch_bounds__(EXEC_NT) void so_exec(Side A, Side B, const Item* i
     }
 }
 
+// item_card: bit 31 = keep, bit 30 = an invalid item (the plan found a
+// container that is not a bitmap), low 16 bits = the stored card.
+constexpr uint32_t ITEM_INVALID = 0x40000000u;
+
 // ---- bitmap x bitmap only: one wavefront per pair ----------------------------
-// When every work item is a bitmap pair (both inputs all-bitmap), each wave
-// streams one 8 KiB pair: 64 lanes x 8 x 16-byte loads per input, all sixteen
-// issued before the op, then the stores and a wave-level popcount -- no
-// workgroup barrier anywhere.
+// When both inputs are all-bitmap every work item is a bitmap pair or a
+// one-sided bitmap copy.  Each wave streams one item: for a pair 64 lanes x 8
+// x 16-byte loads per input, all sixteen issued before the op, then the stores
+// and a wave-level popcount; a copy moves one side's 8 KiB.  No workgroup
+// barrier anywhere.
 constexpr int BB_NT = 256;
 
 template <uint32_t OP>
 __global__ __launch_bounds__(BB_NT) void so_exec_bb(const uint64_t* __restrict__ a_bmp, const uint64_t* __restrict__ b_bmp,
+                                                    const uint16_t* __restrict__ a_cards,
+                                                    const uint16_t* __restrict__ b_cards,
                                                     const Item* __restrict__ items, const Totals* totals,
                                                     uint64_t* __restrict__ out_bmp, uint32_t* __restrict__ item_card)
 {
+    if (totals->overflow) return;  // the output was not allocated for this plan
     const uint32_t n_items = totals->c[C_ITEM];
     const uint32_t lane = __lane_id();
     const uint32_t n_waves = gridDim.x * (BB_NT / 64);
@@ -478,11 +610,30 @@ __global__ __launch_bounds__(BB_NT) void so_exec_bb(const uint64_t* __restrict__
     Item it = items[w];
     for (; w < n_items; w += n_waves) {
         const Item cur = it;
-        if (w + n_waves < n_items) it = items[w + n_waves];  // prefetch the next pair's record
+        if (w + n_waves < n_items) it = items[w + n_waves];  // prefetch the next item's record
         const uint64_t* pa = a_bmp + (cur.aoff >> 3);
         const uint64_t* pb = b_bmp + (cur.boff >> 3);
         uint64_t* po = out_bmp + cur.slot * 1024ull;
         uint32_t pc = 0;
+        if (cur.cat != CAT_BB && cur.cat != CAT_COPY_BMP) {  // invalid (not bitmaps): nothing read or written
+            if (lane == 0) item_card[w] = ITEM_INVALID;
+            continue;
+        }
+        if (cur.cat == CAT_COPY_BMP) {  // a one-sided key: its container and stored card copied, always kept
+            const bool from_a = cur.ai >= 0;
+            const uint64_t* src = from_a ? pa : pb;
+            if (((from_a ? cur.aoff : cur.boff) & 15u) == 0) {
+                uint4 x[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) x[k] = ld_stream(reinterpret_cast<const uint4*>(src) + lane + 64 * k);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) st_stream(reinterpret_cast<uint4*>(po) + lane + 64 * k, x[k]);
+            } else {
+                for (uint32_t i = lane; i < 1024u; i += 64) po[i] = src[i];
+            }
+            if (lane == 0) item_card[w] = static_cast<uint32_t>(from_a ? a_cards[cur.ai] : b_cards[cur.bi]) | 0x80000000u;
+            continue;
+        }
         if (((cur.aoff | cur.boff) & 15u) == 0) {
             const uint4* a4 = reinterpret_cast<const uint4*>(pa);
             const uint4* b4 = reinterpret_cast<const uint4*>(pb);
@@ -523,20 +674,136 @@ __global__ __launch_bounds__(BB_NT) void so_exec_bb(const uint64_t* __restrict__
     }
 }
 
+// ---- two dense all-bitmap inputs: no plan -------------------------------------
+// When both inputs hold a bitmap for every key of [0, n) (n_containers ==
+// max_key + 1 with sorted unique keys, so container i has key i), pair i is
+// key i on both sides, its output slot is i, and there is nothing to plan.
+// One wave per pair, as so_exec_bb; cards go to item_card for the compaction.
+template <uint32_t OP>
+__global__ __launch_bounds__(BB_NT) void so_exec_dense(const uint64_t* __restrict__ a_bmp,
+                                                       const uint64_t* __restrict__ b_bmp,
+                                                       const uint32_t* __restrict__ off_a,
+                                                       const uint32_t* __restrict__ off_b, uint32_t n,
+                                                       uint64_t* __restrict__ out_bmp, uint32_t* __restrict__ item_card)
+{
+    const uint32_t lane = __lane_id();
+    const uint32_t w = (blockIdx.x * BB_NT + threadIdx.x) >> 6;
+    if (w >= n) return;
+    const uint32_t oa = off_a[w], ob = off_b[w];
+    const uint64_t* pa = a_bmp + (oa >> 3);
+    const uint64_t* pb = b_bmp + (ob >> 3);
+    uint64_t* po = out_bmp + static_cast<uint64_t>(w) * 1024u;
+    uint32_t pc = 0;
+    if (((oa | ob) & 15u) == 0) {
+        const uint4* a4 = reinterpret_cast<const uint4*>(pa);
+        const uint4* b4 = reinterpret_cast<const uint4*>(pb);
+        uint4* o4 = reinterpret_cast<uint4*>(po);
+        uint4 x[8], y[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            x[k] = ld_stream(a4 + lane + 64 * k);
+            y[k] = ld_stream(b4 + lane + 64 * k);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            uint4 r;
+            r.x = apply32<OP>(x[k].x, y[k].x);
+            r.y = apply32<OP>(x[k].y, y[k].y);
+            r.z = apply32<OP>(x[k].z, y[k].z);
+            r.w = apply32<OP>(x[k].w, y[k].w);
+            st_stream(o4 + lane + 64 * k, r);
+            pc += __popc(r.x) + __popc(r.y) + __popc(r.z) + __popc(r.w);
+        }
+    } else {
+        for (uint32_t i = lane; i < 1024u; i += 64) {
+            const uint64_t x = pa[i], y = pb[i];
+            const uint64_t r = static_cast<uint64_t>(apply32<OP>(static_cast<uint32_t>(x), static_cast<uint32_t>(y))) |
+                               (static_cast<uint64_t>(apply32<OP>(static_cast<uint32_t>(x >> 32),
+                                                                  static_cast<uint32_t>(y >> 32)))
+                                << 32);
+            po[i] = r;
+            pc += __popcll(r);
+        }
+    }
+    pc = wave_sum(pc);
+    if (lane == 0) {
+        const uint32_t card = pc > 65535u ? 0u : pc;  // 65536 stored as 0 (src/set_ops.cu:179-180)
+        const bool keep = card != 0 || OP == CR_OR;
+        item_card[w] = card | (keep ? 0x80000000u : 0u);
+    }
+}
+
+// Compaction of the dense path: item i is key i in bitmap slot i.  One
+// workgroup per 1024 items, each counting the kept items before it; the last
+// writes the totals (every item a bitmap pair) into the pinned host slot.
+__global__ __launch_bounds__(PLAN_NT) void so_compact_dense(const uint32_t* item_card, uint32_t n, uint16_t* keys,
+                                                            uint8_t* types, uint32_t* offsets, uint16_t* cards,
+                                                            SetOpHost* host)
+{
+    __shared__ uint32_t lds[PLAN_NT / 64];
+    const uint32_t tile = blockIdx.x, t = threadIdx.x;
+    uint32_t b = 0;
+    for (uint32_t i = t; i < tile * PLAN_NT; i += PLAN_NT) b += item_card[i] >> 31;
+    const uint32_t base = block_sum<PLAN_NT>(b, lds);
+    const uint32_t w = tile * PLAN_NT + t;
+    const uint32_t c = w < n ? item_card[w] : 0u;
+    const bool keep = (c & 0x80000000u) != 0;
+    uint32_t tot;
+    const uint32_t r = block_flag_rank<PLAN_NT>(keep, lds, tot);
+    if (keep) {
+        const uint32_t o = base + r;
+        keys[o] = static_cast<uint16_t>(w);
+        types[o] = CR_BITMAP;
+        offsets[o] = w * 8192u;
+        cards[o] = static_cast<uint16_t>(c & 0xFFFFu);
+    }
+    if ((tile + 1) * PLAN_NT >= n && t < 64) {
+        volatile uint32_t* h = reinterpret_cast<volatile uint32_t*>(host);
+        if (t < C_N) h[t] = t == C_ITEM || t == C_BB ? n : 0u;
+        if (t == C_N) h[C_N] = base + tot;
+        if (t == C_N + 1) h[C_N + 1] = 0u;
+    }
+}
+
 // ---- compaction of the kept containers -------------------------------------
+// Lanes 0 .. C_N + 1 of a wave each write one field, so the posted writes to
+// host memory go out together.
+__device__ void write_host_totals(const Totals* totals, uint32_t n_out, uint32_t overflow, SetOpHost* host,
+                                  uint32_t lane)
+{
+    volatile uint32_t* h = reinterpret_cast<volatile uint32_t*>(host);
+    if (lane < C_N) h[lane] = totals->c[lane];
+    if (lane == C_N) h[C_N] = n_out;
+    if (lane == C_N + 1) h[C_N + 1] = overflow;
+}
+
+// The last tile's workgroup writes the kept count (and, given `host`, every
+// total into the pinned slot); with no items or an overflowed plan workgroup 0
+// does, and nothing is compacted.
 __global__ __launch_bounds__(PLAN_NT) void so_compact(const Item* items, const uint32_t* item_card,
                                                       const uint32_t* tile_keep, Totals* totals, uint16_t* keys,
-                                                      uint8_t* types, uint32_t* offsets, uint16_t* cards)
+                                                      uint8_t* types, uint32_t* offsets, uint16_t* cards,
+                                                      SetOpHost* host)
 {
     __shared__ uint32_t lds[PLAN_NT / 64];
     __shared__ uint32_t s_base;
     const uint32_t n_items = totals->c[C_ITEM];
     const uint32_t tile = blockIdx.x;
+    if (totals->overflow || n_items == 0) {
+        if (tile == 0 && threadIdx.x < 64 && host) write_host_totals(totals, 0, totals->overflow, host, threadIdx.x);
+        return;
+    }
     if (tile * PLAN_NT >= n_items) return;
     const uint32_t t = threadIdx.x;
-    {  // kept items before this tile, counted cooperatively
+    const bool last = (tile + 1) * PLAN_NT >= n_items;
+    uint32_t invalid = 0;
+    {  // kept items before this tile, counted cooperatively (the last tile also counts invalid ones)
         uint32_t b = 0;
-        for (uint32_t i = t; i < tile * PLAN_NT; i += PLAN_NT) b += item_card[i] >> 31;
+        for (uint32_t i = t; i < tile * PLAN_NT; i += PLAN_NT) {
+            const uint32_t x = item_card[i];
+            b += x >> 31;
+            invalid += (x >> 30) & 1u;
+        }
         b = block_sum<PLAN_NT>(b, lds);
         if (t == 0) s_base = b;
     }
@@ -547,8 +814,10 @@ __global__ __launch_bounds__(PLAN_NT) void so_compact(const Item* items, const u
     if (w < n_items) {
         c = item_card[w];
         keep = (c & 0x80000000u) != 0;
+        invalid += (c >> 30) & 1u;
         it = items[w];
     }
+    if (last) invalid = block_sum<PLAN_NT>(invalid, lds);
     uint32_t tot;
     const uint32_t r = block_flag_rank<PLAN_NT>(keep, lds, tot);
     const uint32_t base = s_base;
@@ -577,7 +846,10 @@ __global__ __launch_bounds__(PLAN_NT) void so_compact(const Item* items, const u
         offsets[o] = off;
         cards[o] = static_cast<uint16_t>(c & 0xFFFFu);
     }
-    if (t == 0 && (tile + 1) * PLAN_NT >= n_items) totals->n_out = base + tot;
+    if (t < 64 && last) {
+        if (t == 0) totals->n_out = base + tot;
+        if (host) write_host_totals(totals, base + tot, invalid ? 1u : 0u, host, t);
+    }
 }
 
 // DeMorgan rewrite (src/set_ops.cu:533-565).
@@ -635,6 +907,277 @@ static unsigned exec_grid(uint32_t n_items)
     return std::max(1u, std::min(n_items, cap));
 }
 
+// Output capacity known on the host before planning, from the inputs'
+// container counts by type (src/set_ops.cu:626-692 fixes which pair gives
+// which output type):
+//   AND     bitmaps: pairs of two non-array containers, or a run and an array;
+//           arrays: bitmap x array keeps the array side's values, array x
+//           array at most the smaller side's -- both within the inputs' array
+//           pools; no runs;
+//   OR/XOR  every matched pair gives a bitmap, one-sided keys copy their
+//           container: bitmaps <= m + min(bmp_a, na - m) + min(bmp_b, nb - m)
+//           over the unknown number m of matched keys; arrays and runs <= the
+//           inputs' pools;
+//   ANDNOT  as OR with only A's one-sided keys copied.
+// For inputs whose counts describe their containers (every upload, and
+// set-operation results, whose counts include dropped slots) the plan fits;
+// the plan kernel checks it anyway, and a plan that does not fit is redone by
+// the exact two-pass path.
+static Caps setop_caps(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_t op, uint32_t bound)
+{
+    const uint64_t na = a->n_containers, nb = b->n_containers;
+    const uint64_t ba = a->n_bitmap_containers, bb = b->n_bitmap_containers;
+    const uint64_t ra = a->n_run_containers, rb = b->n_run_containers;
+    const uint64_t aa = a->n_array_containers, ab = b->n_array_containers;
+    const uint64_t ea = a->array_pool_bytes / 2u, eb = b->array_pool_bytes / 2u;
+    const uint64_t pa = a->run_pool_bytes / 2u, pb = b->run_pool_bytes / 2u;  // u16 entries
+    const uint64_t m_max = std::min(na, nb);
+    uint64_t bmp = 0, arr = 0, run = 0;
+    auto clampm = [&](int64_t m) { return static_cast<uint64_t>(std::max<int64_t>(0, std::min<int64_t>(m, m_max))); };
+    if (op == CR_AND) {
+        bmp = std::min(ba + ra, bb + rb) + std::min(ra, ab) + std::min(aa, rb);
+        bmp = std::min(bmp, m_max);
+        arr = ea + eb;
+    } else if (op == CR_ANDNOT) {
+        for (int64_t m : {int64_t(0), int64_t(m_max), int64_t(na) - int64_t(ba)}) {
+            const uint64_t mm = clampm(m);
+            bmp = std::max(bmp, mm + std::min(ba, na - mm));
+        }
+        arr = ea;
+        run = pa;
+    } else {
+        for (int64_t m : {int64_t(0), int64_t(m_max), int64_t(na) - int64_t(ba), int64_t(nb) - int64_t(bb)}) {
+            const uint64_t mm = clampm(m);
+            bmp = std::max(bmp, mm + std::min(ba, na - mm) + std::min(bb, nb - mm));
+        }
+        arr = ea + eb;
+        run = pa + pb;
+    }
+    auto c32 = [](uint64_t x) { return static_cast<uint32_t>(std::min<uint64_t>(x, 0xFFFFFFFFull)); };
+    return Caps{bound, c32(std::min<uint64_t>(bmp, bound)), c32(arr), c32(run), 0u};
+}
+
+// The plan (classify + assign) for `bound` work items into fresh scratch.
+struct SetOpPlan {
+    Scratch sc;
+    Item* items;
+    Totals* tot;
+    uint32_t* icard;
+    uint32_t* tile_keep;
+    uint32_t n_tiles;
+};
+
+static int plan_set_operation(const Side& A, const Side& B, uint32_t op, uint32_t bound, const Caps& caps,
+                              hipStream_t s, SetOpPlan& P)
+{
+    P.n_tiles = (bound + PLAN_NT - 1) / PLAN_NT;
+    Carver c;
+    const size_t o_recs = c.add(sizeof(KeyRec) * 65536);
+    const size_t o_gc = c.add(sizeof(uint32_t) * PLAN_GROUPS * C_N);
+    const size_t o_items = c.add(sizeof(Item) * bound);
+    const size_t o_tot = c.add(sizeof(Totals));
+    const size_t o_card = c.add(sizeof(uint32_t) * bound);
+    const size_t o_tile = c.add(sizeof(uint32_t) * P.n_tiles);
+    CR_RET(P.sc.alloc(c.total, s));
+    KeyRec* recs = P.sc.at<KeyRec>(o_recs);
+    uint32_t* gc = P.sc.at<uint32_t>(o_gc);
+    P.items = P.sc.at<Item>(o_items);
+    P.tot = P.sc.at<Totals>(o_tot);
+    P.icard = P.sc.at<uint32_t>(o_card);
+    P.tile_keep = P.sc.at<uint32_t>(o_tile);
+    {
+        CR_TIMED("so_plan_classify", s);
+        so_plan_classify<<<PLAN_GROUPS, PLAN_NT, 0, s>>>(A, B, op, recs, gc);
+    }
+    CR_LAUNCH_CHECK();
+    {
+        CR_TIMED("so_plan_assign", s);
+        so_plan_assign<<<PLAN_GROUPS, PLAN_NT, 0, s>>>(recs, gc, P.items, P.tot, P.tile_keep, P.n_tiles, caps);
+    }
+    CR_LAUNCH_CHECK();
+    return CR_OK;
+}
+
+// The key-index plan of two all-bitmap inputs (so_plan_bitmap).
+static int plan_bitmap_keyed(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_t op, uint32_t bound,
+                             const Caps& caps, hipStream_t s, SetOpPlan& P)
+{
+    P.n_tiles = (bound + PLAN_NT - 1) / PLAN_NT;
+    Carver c;
+    const size_t o_items = c.add(sizeof(Item) * bound);
+    const size_t o_tot = c.add(sizeof(Totals));
+    const size_t o_card = c.add(sizeof(uint32_t) * bound);
+    const size_t o_tile = c.add(sizeof(uint32_t) * P.n_tiles);
+    CR_RET(P.sc.alloc(c.total, s));
+    P.items = P.sc.at<Item>(o_items);
+    P.tot = P.sc.at<Totals>(o_tot);
+    P.icard = P.sc.at<uint32_t>(o_card);
+    P.tile_keep = P.sc.at<uint32_t>(o_tile);
+    {
+        CR_TIMED("so_plan_bitmap", s);
+        const uint32_t len_a = a->max_key + 1u, len_b = b->max_key + 1u;
+        const uint32_t groups = (std::max(len_a, len_b) + KP_NT - 1) / KP_NT;
+        so_plan_bitmap<<<groups, KP_NT, 0, s>>>(a->key_index, len_a, b->key_index, len_b, a->offsets, b->offsets,
+                                                a->types, b->types, a->n_containers, b->n_containers, op, caps,
+                                                P.items, P.tot);
+    }
+    CR_LAUNCH_CHECK();
+    return CR_OK;
+}
+
+// Execution and compaction of a plan into `out` (allocated for at most
+// `bound` items); `host` (optional) receives the totals.
+static int exec_set_operation(const Side& A, const Side& B, uint32_t op, uint32_t bound, bool only_bb,
+                              const SetOpPlan& P, cr_gpu_roaring* out, SetOpHost* host, hipStream_t s)
+{
+    if (only_bb) {
+        // One item per wave: every pair's 16 loads are in flight at once
+        // (capping the grid at the resident waves, two pairs a wave, measured
+        // 1.5% slower at 16384 pairs).  Waves past the plan's item count exit.
+        const unsigned gb = std::max(1u, (bound + 3) / 4);
+        CR_TIMED("so_exec", s);
+        switch (op) {
+        case CR_AND:
+            so_exec_bb<CR_AND><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, A.cards, B.cards, P.items, P.tot, out->bitmap_data,
+                                                    P.icard);
+            break;
+        case CR_OR:
+            so_exec_bb<CR_OR><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, A.cards, B.cards, P.items, P.tot, out->bitmap_data,
+                                                   P.icard);
+            break;
+        case CR_ANDNOT:
+            so_exec_bb<CR_ANDNOT><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, A.cards, B.cards, P.items, P.tot,
+                                                       out->bitmap_data, P.icard);
+            break;
+        default:
+            so_exec_bb<CR_XOR><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, A.cards, B.cards, P.items, P.tot, out->bitmap_data,
+                                                    P.icard);
+            break;
+        }
+    } else {
+        const unsigned g = exec_grid(bound);
+        CR_TIMED("so_exec", s);
+        switch (op) {
+        case CR_AND:
+            so_exec<CR_AND><<<g, EXEC_NT, 0, s>>>(A, B, P.items, P.tot, out->bitmap_data, out->array_data,
+                                                  out->run_data, P.icard, P.tile_keep);
+            break;
+        case CR_OR:
+            so_exec<CR_OR><<<g, EXEC_NT, 0, s>>>(A, B, P.items, P.tot, out->bitmap_data, out->array_data,
+                                                 out->run_data, P.icard, P.tile_keep);
+            break;
+        case CR_ANDNOT:
+            so_exec<CR_ANDNOT><<<g, EXEC_NT, 0, s>>>(A, B, P.items, P.tot, out->bitmap_data, out->array_data,
+                                                     out->run_data, P.icard, P.tile_keep);
+            break;
+        default:
+            so_exec<CR_XOR><<<g, EXEC_NT, 0, s>>>(A, B, P.items, P.tot, out->bitmap_data, out->array_data,
+                                                  out->run_data, P.icard, P.tile_keep);
+            break;
+        }
+    }
+    CR_LAUNCH_CHECK();
+    {
+        CR_TIMED("so_compact", s);
+        so_compact<<<std::max(1u, P.n_tiles), PLAN_NT, 0, s>>>(P.items, P.icard, P.tile_keep, P.tot, out->keys,
+                                                               out->types, out->offsets, out->cardinalities, host);
+    }
+    CR_LAUNCH_CHECK();
+    return CR_OK;
+}
+
+static void set_counts(cr_gpu_roaring* out, const uint32_t* c)
+{
+    out->n_bitmap_containers = c[C_BB] + c[C_MX] + c[C_CB];
+    out->n_array_containers = c[C_BA] + c[C_AA] + c[C_CA];
+    out->n_run_containers = c[C_CR];
+    out->array_pool_bytes = (c[C_BAE] + c[C_AAE] + c[C_CAE]) * 2u;
+    out->run_pool_bytes = c[C_CRP] * 4u;
+}
+
+// The exact path: plan, read the totals back (first sync), allocate the output
+// exactly, execute, compact, read the kept count (second sync).
+static bool aligned_bitmaps(const cr_gpu_roaring* a, const cr_gpu_roaring* b)
+{
+    return ((reinterpret_cast<uintptr_t>(a->bitmap_data) | reinterpret_cast<uintptr_t>(b->bitmap_data)) & 15u) == 0;
+}
+
+static int set_operation_exact(const cr_gpu_roaring* a, const cr_gpu_roaring* b, const Side& A, const Side& B,
+                               uint32_t op, uint32_t bound, hipStream_t s, cr_gpu_roaring* out)
+{
+    SetOpPlan P;
+    const Caps unbounded{0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0u};
+    CR_RET(plan_set_operation(A, B, op, bound, unbounded, s, P));
+    Totals h{};
+    CR_RET(read_back(&h, P.tot, sizeof(Totals), s));
+    const uint32_t n_items = h.c[C_ITEM];
+    if (n_items == 0) return CR_OK;
+    const uint64_t n_bmp = static_cast<uint64_t>(h.c[C_BB]) + h.c[C_MX] + h.c[C_CB];
+    const uint64_t arr_elems = static_cast<uint64_t>(h.c[C_BAE]) + h.c[C_AAE] + h.c[C_CAE];
+    const uint64_t run_u16 = 2ull * h.c[C_CRP];
+    const OutLayout L = plan_out(n_items, 0, n_bmp * 1024, arr_elems, run_u16);
+    CR_RET(alloc_out(out, L, n_items, 0, n_bmp * 1024, arr_elems, run_u16, s));
+    set_counts(out, h.c);
+    const bool only_bb = h.c[C_BB] + h.c[C_CB] == n_items && aligned_bitmaps(a, b);
+    CR_RET(exec_set_operation(A, B, op, n_items, only_bb, P, out, nullptr, s));
+    uint32_t n_out = 0;
+    CR_RET(read_back(&n_out, &P.tot->n_out, sizeof(uint32_t), s));
+    out->n_containers = n_out;
+    return CR_OK;
+}
+
+// Both inputs hold a bitmap for every key of [0, n): pair i is key i, no plan.
+// One synchronisation; the output is allocated exactly (n bitmap slots).
+static int set_operation_dense(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_t op, hipStream_t s,
+                               cr_gpu_roaring* out)
+{
+    const uint32_t n = a->n_containers;
+    const OutLayout L = plan_out(n, 0, static_cast<uint64_t>(n) * 1024u, 0, 0);
+    CR_RET(alloc_out(out, L, n, 0, static_cast<uint64_t>(n) * 1024u, 0, 0, s));
+    HostSlotGuard hs;
+    CR_RET(hs.acquire());
+    {
+        Scratch sc;
+        CR_RET(sc.alloc(sizeof(uint32_t) * n, s));
+        uint32_t* icard = sc.at<uint32_t>(0);
+        const unsigned gb = (n + 3) / 4;
+        {
+            CR_TIMED("so_exec", s);
+            switch (op) {
+            case CR_AND:
+                so_exec_dense<CR_AND><<<gb, BB_NT, 0, s>>>(a->bitmap_data, b->bitmap_data, a->offsets, b->offsets, n,
+                                                           out->bitmap_data, icard);
+                break;
+            case CR_OR:
+                so_exec_dense<CR_OR><<<gb, BB_NT, 0, s>>>(a->bitmap_data, b->bitmap_data, a->offsets, b->offsets, n,
+                                                          out->bitmap_data, icard);
+                break;
+            case CR_ANDNOT:
+                so_exec_dense<CR_ANDNOT><<<gb, BB_NT, 0, s>>>(a->bitmap_data, b->bitmap_data, a->offsets, b->offsets,
+                                                              n, out->bitmap_data, icard);
+                break;
+            default:
+                so_exec_dense<CR_XOR><<<gb, BB_NT, 0, s>>>(a->bitmap_data, b->bitmap_data, a->offsets, b->offsets, n,
+                                                           out->bitmap_data, icard);
+                break;
+            }
+        }
+        CR_LAUNCH_CHECK();
+        {
+            CR_TIMED("so_compact", s);
+            so_compact_dense<<<(n + PLAN_NT - 1) / PLAN_NT, PLAN_NT, 0, s>>>(icard, n, out->keys, out->types,
+                                                                             out->offsets, out->cardinalities,
+                                                                             hs.dev<SetOpHost>());
+        }
+        CR_LAUNCH_CHECK();
+        CR_RET(sync_stream(s));
+    }
+    const uint32_t n_out = hs.host<SetOpHost>()->n_out;
+    out->n_bitmap_containers = n;  // allocated slots, dropped ones included (src/set_ops.cu:695-701)
+    out->n_containers = n_out;
+    return CR_OK;
+}
+
 int set_operation_impl(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_t op, hipStream_t s,
                        cr_gpu_roaring* out)
 {
@@ -646,104 +1189,48 @@ int set_operation_impl(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_
     const uint32_t na = a->n_containers, nb = b->n_containers;
     uint32_t bound = op == CR_AND ? std::min(na, nb) : (op == CR_ANDNOT ? na : na + nb);
     if (bound == 0) return CR_OK;  // empty work list (src/set_ops.cu:588-593)
-
-    const uint32_t n_tiles = (bound + PLAN_NT - 1) / PLAN_NT;
-    Carver c;
-    const size_t o_recs = c.add(sizeof(KeyRec) * 65536);
-    const size_t o_gc = c.add(sizeof(uint32_t) * PLAN_GROUPS * C_N);
-    const size_t o_items = c.add(sizeof(Item) * bound);
-    const size_t o_tot = c.add(sizeof(Totals));
-    const size_t o_card = c.add(sizeof(uint32_t) * bound);
-    const size_t o_tile = c.add(sizeof(uint32_t) * n_tiles);
-    Scratch sc;
-    CR_RET(sc.alloc(c.total, s));
-    KeyRec* recs = sc.at<KeyRec>(o_recs);
-    uint32_t* gc = sc.at<uint32_t>(o_gc);
-    Item* items = sc.at<Item>(o_items);
-    Totals* tot = sc.at<Totals>(o_tot);
-    uint32_t* icard = sc.at<uint32_t>(o_card);
-    uint32_t* tile_keep = sc.at<uint32_t>(o_tile);
-
     const Side A = side_of(a), B = side_of(b);
-    {
-        CR_TIMED("so_plan_classify", s);
-        so_plan_classify<<<PLAN_GROUPS, PLAN_NT, 0, s>>>(A, B, op, recs, gc);
-    }
-    CR_LAUNCH_CHECK();
-    {
-        CR_TIMED("so_plan_assign", s);
-        so_plan_assign<<<PLAN_GROUPS, PLAN_NT, 0, s>>>(recs, gc, items, tot, tile_keep, n_tiles);
-    }
-    CR_LAUNCH_CHECK();
-    Totals h{};
-    CR_RET(read_back(&h, tot, sizeof(Totals), s));
-    const uint32_t n_items = h.c[C_ITEM];
-    if (n_items == 0) return CR_OK;
 
-    const uint64_t n_bmp = static_cast<uint64_t>(h.c[C_BB]) + h.c[C_MX] + h.c[C_CB];
-    const uint64_t arr_elems = static_cast<uint64_t>(h.c[C_BAE]) + h.c[C_AAE] + h.c[C_CAE];
-    const uint64_t run_u16 = 2ull * h.c[C_CRP];
-    const OutLayout L = plan_out(n_items, 0, n_bmp * 1024, arr_elems, run_u16);
-    CR_RET(alloc_out(out, L, n_items, 0, n_bmp * 1024, arr_elems, run_u16, s));
-    out->n_bitmap_containers = static_cast<uint32_t>(n_bmp);
-    out->n_array_containers = h.c[C_BA] + h.c[C_AA] + h.c[C_CA];
-    out->n_run_containers = h.c[C_CR];
-    out->array_pool_bytes = static_cast<uint32_t>(arr_elems * 2);
-    out->run_pool_bytes = static_cast<uint32_t>(run_u16 * 2);
-
-    const unsigned g = exec_grid(n_items);
-    const bool only_bb = h.c[C_BB] == n_items && ((reinterpret_cast<uintptr_t>(a->bitmap_data) |
-                                                   reinterpret_cast<uintptr_t>(b->bitmap_data)) & 15u) == 0;
-    if (only_bb) {
-        // One pair per wave: every pair's 16 loads are in flight at once
-        // (capping the grid at the resident waves, two pairs a wave, measured
-        // 1.5% slower at 16384 pairs).
-        const unsigned gb = std::max(1u, (n_items + 3) / 4);
-        CR_TIMED("so_exec", s);
-        switch (op) {
-        case CR_AND:
-            so_exec_bb<CR_AND><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, items, tot, out->bitmap_data, icard);
-            break;
-        case CR_OR:
-            so_exec_bb<CR_OR><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, items, tot, out->bitmap_data, icard);
-            break;
-        case CR_ANDNOT:
-            so_exec_bb<CR_ANDNOT><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, items, tot, out->bitmap_data, icard);
-            break;
-        default:
-            so_exec_bb<CR_XOR><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, items, tot, out->bitmap_data, icard);
-            break;
-        }
-    } else {
-        CR_TIMED("so_exec", s);
-        switch (op) {
-        case CR_AND:
-            so_exec<CR_AND><<<g, EXEC_NT, 0, s>>>(A, B, items, tot, out->bitmap_data, out->array_data, out->run_data,
-                                                  icard, tile_keep);
-            break;
-        case CR_OR:
-            so_exec<CR_OR><<<g, EXEC_NT, 0, s>>>(A, B, items, tot, out->bitmap_data, out->array_data, out->run_data,
-                                                 icard, tile_keep);
-            break;
-        case CR_ANDNOT:
-            so_exec<CR_ANDNOT><<<g, EXEC_NT, 0, s>>>(A, B, items, tot, out->bitmap_data, out->array_data,
-                                                     out->run_data, icard, tile_keep);
-            break;
-        default:
-            so_exec<CR_XOR><<<g, EXEC_NT, 0, s>>>(A, B, items, tot, out->bitmap_data, out->array_data, out->run_data,
-                                                  icard, tile_keep);
-            break;
-        }
-    }
-    CR_LAUNCH_CHECK();
+    // One synchronisation: the output is allocated before planning, at the
+    // capacity the inputs' counts bound; the compaction writes the totals into
+    // a pinned host slot.
+    Caps caps = setop_caps(a, b, op, bound);
+    // Both inputs all-bitmap: every item is a bitmap pair or a bitmap copy (the
+    // plan verifies it), and one wave streams each.
+    const bool only_bb = a->n_array_containers == 0 && a->n_run_containers == 0 && b->n_array_containers == 0 &&
+                         b->n_run_containers == 0 && aligned_bitmaps(a, b);
+    if (only_bb && a->key_index && b->key_index && a->max_key == b->max_key && na == a->max_key + 1u &&
+        nb == na && a->n_bitmap_containers == na && b->n_bitmap_containers == nb)
+        return set_operation_dense(a, b, op, s, out);
+    caps.bb_only = only_bb ? 1u : 0u;
+    const uint64_t cap_bmp_words = static_cast<uint64_t>(caps.bmp) * 1024u;
+    const OutLayout L = plan_out(bound, 0, cap_bmp_words, caps.arr, caps.run_u16);
+    CR_RET(alloc_out(out, L, bound, 0, cap_bmp_words, caps.arr, caps.run_u16, s));
+    HostSlotGuard hs;
+    CR_RET(hs.acquire());
     {
-        CR_TIMED("so_compact", s);
-        so_compact<<<(n_items + PLAN_NT - 1) / PLAN_NT, PLAN_NT, 0, s>>>(items, icard, tile_keep, tot, out->keys,
-                                                                         out->types, out->offsets, out->cardinalities);
+        SetOpPlan P;
+        if (only_bb && a->key_index && b->key_index) {
+            CR_RET(plan_bitmap_keyed(a, b, op, bound, caps, s, P));
+        } else {
+            CR_RET(plan_set_operation(A, B, op, bound, caps, s, P));
+        }
+        CR_RET(exec_set_operation(A, B, op, bound, only_bb, P, out, hs.dev<SetOpHost>(), s));
+        CR_RET(sync_stream(s));
     }
-    CR_LAUNCH_CHECK();
-    uint32_t n_out = 0;
-    CR_RET(read_back(&n_out, &tot->n_out, sizeof(uint32_t), s));
+    const volatile SetOpHost* h = hs.host<SetOpHost>();
+    uint32_t c[C_N];
+    for (int k = 0; k < C_N; ++k) c[k] = h->c[k];
+    const uint32_t n_out = h->n_out, overflow = h->overflow;
+    if (overflow || c[C_ITEM] == 0) {
+        free_async(out, s);
+        reset(out);
+        out->universe_size = std::max(a->universe_size, b->universe_size);
+        out->negated = neg;
+        if (c[C_ITEM] == 0 && !overflow) return CR_OK;
+        return set_operation_exact(a, b, A, B, op, bound, s, out);  // counts that do not describe the inputs
+    }
+    set_counts(out, c);
     out->n_containers = n_out;
     // total_cardinality, key_index and max_key stay 0/null (src/set_ops.cu:1162-1175).
     return CR_OK;
@@ -850,16 +1337,16 @@ __device__ __forceinline__ int32_t fused_lookup(const FusedIn& in, uint32_t key)
 }
 
 __global__ __launch_bounds__(EXEC_NT) void mand_and(FusedArgs args, const uint16_t* common, const uint32_t* n_common_p,
-                                                    uint64_t* out_bmp, uint16_t* keys, uint8_t* types, uint32_t* offsets,
-                                                    uint16_t* cards, uint16_t* key_index, uint32_t kidx_len,
-                                                    uint32_t* total)
+                                                    uint32_t cap, uint64_t* out_bmp, uint16_t* keys, uint8_t* types,
+                                                    uint32_t* offsets, uint16_t* cards, uint16_t* key_index,
+                                                    uint32_t kidx_len, uint32_t* total)
 {
     // One wavefront per common key: lane k resolves input k's container, the wave
     // then streams every input's 8 KiB (8 x 16-byte loads per lane per input)
     // into a register accumulator.  The total cardinality is summed per wave and
     // added once per workgroup.
     __shared__ uint32_t wave_total[EXEC_NT / 64];
-    const uint32_t n_common = *n_common_p;
+    const uint32_t n_common = min(*n_common_p, cap);  // cap: the containers the output was allocated for
     const uint32_t lane = __lane_id();
     const uint32_t n_waves = gridDim.x * (EXEC_NT / 64);
     uint32_t my_total = 0;
@@ -945,6 +1432,14 @@ __global__ __launch_bounds__(EXEC_NT) void mand_and(FusedArgs args, const uint16
     }
 }
 
+// n_common and the total cardinality, for the host's one read after the sync.
+__global__ void mand_finish(const uint32_t* cnt, uint32_t* host)
+{
+    volatile uint32_t* h = host;
+    h[0] = cnt[0];
+    h[1] = cnt[1];
+}
+
 static int fused_multi_and(const cr_gpu_roaring* in, uint32_t count, hipStream_t s, cr_gpu_roaring* out)
 {
     FusedArgs args{};
@@ -980,30 +1475,48 @@ static int fused_multi_and(const cr_gpu_roaring* in, uint32_t count, hipStream_t
     }
     CR_LAUNCH_CHECK();
     CR_RET(fill_u32(cnt + 1, 0u, 1, s));
-    uint32_t n_common = 0;
-    CR_RET(read_back(&n_common, cnt, sizeof(uint32_t), s));
-    out->n_containers = n_common;
-    out->n_bitmap_containers = n_common;
-    if (n_common == 0) return CR_OK;  // src/set_ops.cu:1579-1583
 
+    // One synchronisation: the output is allocated for the most common keys
+    // there can be -- the fewest containers of a non-negated input (the common
+    // keys are a subset of each one's keys), or every key of the universe when
+    // all inputs are negated -- before they are counted.
+    uint32_t cap = 0xFFFFFFFFu;
+    for (uint32_t i = 0; i < count; ++i)
+        if (!in[i].negated) cap = std::min(cap, in[i].n_containers);
+    if (cap == 0xFFFFFFFFu) cap = mkp1;
     const uint32_t max_key = mkp1 == 0 ? 0u : mkp1 - 1u;
     const uint64_t kidx_len = static_cast<uint64_t>(max_key) + 1u;
-    const OutLayout L = plan_out(n_common, kidx_len, static_cast<uint64_t>(n_common) * 1024u, 0, 0);
-    CR_RET(alloc_out(out, L, n_common, kidx_len, static_cast<uint64_t>(n_common) * 1024u, 0, 0, s));
-    out->max_key = max_key;
-    CR_RET(fill_u16(out->key_index, 0xFFFFu, kidx_len, s));
-    {
+    HostSlotGuard hs;
+    CR_RET(hs.acquire());
+    if (cap > 0) {
+        const OutLayout L = plan_out(cap, kidx_len, static_cast<uint64_t>(cap) * 1024u, 0, 0);
+        CR_RET(alloc_out(out, L, cap, kidx_len, static_cast<uint64_t>(cap) * 1024u, 0, 0, s));
+        out->max_key = max_key;
+        CR_RET(fill_u16(out->key_index, 0xFFFFu, kidx_len, s));
         CR_TIMED("mand_and", s);
         // One common key per wave (a grid capped at 8 workgroups per CU, two
-        // keys a wave, measured 0.69 of peak against 0.71 at k = 3).
-        const unsigned gm = std::max(1u, (n_common + 3) / 4);
-        mand_and<<<gm, EXEC_NT, 0, s>>>(args, common, cnt, out->bitmap_data, out->keys, out->types,
-                                                         out->offsets, out->cardinalities, out->key_index,
-                                                         static_cast<uint32_t>(kidx_len), cnt + 1);
+        // keys a wave, measured 0.69 of peak against 0.71 at k = 3); waves past
+        // the common keys exit.
+        const unsigned gm = std::max(1u, (cap + 3) / 4);
+        mand_and<<<gm, EXEC_NT, 0, s>>>(args, common, cnt, cap, out->bitmap_data, out->keys, out->types,
+                                        out->offsets, out->cardinalities, out->key_index,
+                                        static_cast<uint32_t>(kidx_len), cnt + 1);
     }
     CR_LAUNCH_CHECK();
-    uint32_t total = 0;
-    CR_RET(read_back(&total, cnt + 1, sizeof(uint32_t), s));
+    mand_finish<<<1, 1, 0, s>>>(cnt, hs.dev<uint32_t>());
+    CR_LAUNCH_CHECK();
+    CR_RET(sync_stream(s));
+    const volatile uint32_t* h = hs.host<uint32_t>();
+    const uint32_t h0 = h[0], total = h[1];
+    const uint32_t n_common = std::min(h0, cap);
+    if (n_common == 0) {  // src/set_ops.cu:1579-1583
+        free_async(out, s);
+        reset(out);
+        out->universe_size = universe;
+        return CR_OK;
+    }
+    out->n_containers = n_common;
+    out->n_bitmap_containers = n_common;
     out->total_cardinality = total;
     return CR_OK;
 }

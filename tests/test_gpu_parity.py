@@ -318,6 +318,62 @@ def test_set_operation_all_bitmap_large(gpu, op):
         gpu.free(x)
 
 
+@pytest.mark.parametrize("op", [orc.AND, orc.OR, orc.ANDNOT, orc.XOR])
+def test_set_operation_understated_counts_fall_back(gpu, op):
+    """Inputs whose type counts and pool sizes understate their containers (all
+    zero: the struct claims to be all-bitmap with empty pools).  The one-sync
+    path sizes its output from those counts; the plan kernel finds that the
+    plan does not fit (or is not bitmap-only), nothing is written, and the call
+    redoes the work on the exact two-pass path: the result is the oracle's."""
+    _say("set_operation understated counts", op)
+    U, la, lb = _build_operands(3)
+    ga, oa = _upload_pair(gpu, la, U, orc.PROMOTE_KEEP_DEFAULT)
+    gb, ob = _upload_pair(gpu, lb, U, orc.PROMOTE_KEEP_DEFAULT)
+    assert ga.n_array_containers + ga.n_run_containers > 0
+    want = orc.set_operation(oa, ob, op)
+    bad = []
+    for g in (ga, gb):
+        x = gpu.GpuRoaring.from_buffer_copy(g)  # aliases g's device block; not freed itself
+        x.n_bitmap_containers = x.n_array_containers = x.n_run_containers = 0
+        x.array_pool_bytes = x.run_pool_bytes = 0
+        bad.append(x)
+    r = gpu.set_operation(bad[0], bad[1], op)
+    assert_same(gpu.download(r), want, strict=True, what=f"understated counts {op}")
+    for x in (r, ga, gb):
+        gpu.free(x)
+
+
+@pytest.mark.parametrize("op", [orc.AND, orc.OR, orc.ANDNOT, orc.XOR])
+@pytest.mark.parametrize("case", ["random", "identical", "with_empty_results"])
+def test_set_operation_dense_all_bitmap(gpu, op, case):
+    """Two all-bitmap inputs with a container for every key of [0, max_key]: the
+    plan-free path (pair i is key i).  Identical inputs drop every XOR and ANDNOT
+    result; disjoint halves of each key drop AND results; full containers are
+    stored with card 0 and dropped by AND."""
+    _say("set_operation dense", op, case)
+    rng = np.random.default_rng(5 + op)
+    U = 40 * 65536
+    a = np.nonzero(rng.random(U) < 0.3)[0].astype(np.uint32)
+    if case == "random":
+        b = np.nonzero(rng.random(U) < 0.6)[0].astype(np.uint32)
+    elif case == "identical":
+        b = a.copy()
+    else:  # keys 0-9: a low half, b high half (empty AND); key 11 full in both
+        low = (a & 0xFFFF) < 32768
+        a = np.concatenate([a[(a >> 16 >= 10) | low], np.arange(11 << 16, 12 << 16)]).astype(np.uint32)
+        b = np.nonzero(rng.random(U) < 0.4)[0].astype(np.uint32)
+        b = np.concatenate([b[(b >> 16 >= 10) | ((b & 0xFFFF) >= 32768)], np.arange(11 << 16, 12 << 16)])
+        a, b = np.unique(a), np.unique(b.astype(np.uint32))
+    oa, ob = orc.upload_from_ids(a, U), orc.upload_from_ids(b, U)
+    ga, gb = gpu.upload_from_ids(a, U), gpu.upload_from_ids(b, U)
+    assert ga.n_containers == gb.n_containers == ga.max_key + 1 == 40
+    want = orc.set_operation(oa, ob, op)
+    g = gpu.set_operation(ga, gb, op)
+    assert_same(gpu.download(g), want, strict=True, what=f"dense {case}")
+    for x in (g, ga, gb):
+        gpu.free(x)
+
+
 def test_set_operation_empty_and_identical(gpu):
     _say("set_operation empty/identical")
     a = orc.Lite.from_sorted_ids(np.arange(1000, dtype=np.uint32))
