@@ -115,7 +115,7 @@ def cold_time(torch, fn, iters, flush, after=None):
     return median(ts)
 
 
-SECTIONS = ("config0", "config2", "config3", "conversions", "batch", "upload_variants", "topk")
+SECTIONS = ("config0", "config2", "config3", "conversions", "batch", "upload_variants", "promote_sweep", "topk")
 
 
 def secondary(torch, cr, flush, no_cpu, sections):
@@ -135,6 +135,8 @@ def secondary(torch, cr, flush, no_cpu, sections):
         torch.cuda.empty_cache()
     if "upload_variants" in sections:
         out["upload_variants_2^30"] = upload_variants(torch, cr)
+    if "promote_sweep" in sections:
+        out["promote_auto_sweep"] = promote_sweep(torch, cr, flush)
     return out
 
 
@@ -493,6 +495,54 @@ def config3(torch, cr, flush, nt, no_cpu):
     del qs, res
     torch.cuda.empty_cache()
     return out
+
+
+def promote_sweep(torch, cr, flush):
+    """PROMOTE_AUTO on gfx950, from measurement: the compressed layout (KEEP:
+    arrays up to 4096 values) against the promoted one (ALL: every container
+    an 8 KiB bitmap) over U = 2^20 .. 2^30 at 0.1 / 1 / 10% density.  For each:
+    10M uniform and 10M sorted-clustered point queries (Gq/s, cold) and the AND
+    of two such bitmaps (API ms, cold), plus each layout's bytes.  The ratio
+    promoted / compressed > 1 means promotion pays."""
+    import orc
+    res = {}
+    nq = 10_000_000
+    out = torch.empty(nq, device="cuda", dtype=torch.int32)
+    for lg in (20, 22, 24, 26, 28, 30):
+        Uu = 1 << lg
+        g = torch.Generator(device="cuda")
+        g.manual_seed(900 + lg)
+        q_uni = torch.randint(0, Uu, (nq,), device="cuda", generator=g, dtype=torch.int64).to(torch.int32)
+        nwin = max(1, Uu >> 16)
+        win = torch.randint(0, nwin, (nq // 4096,), device="cuda", generator=g, dtype=torch.int64)
+        off = torch.randint(0, min(65536, Uu), (nq // 4096, 4096), device="cuda", generator=g, dtype=torch.int64)
+        q_clu = ((win[:, None] << 16) + off.sort(dim=1).values).reshape(-1).to(torch.int32)
+        for dens in (0.001, 0.01, 0.1):
+            lites = [orc.Lite.from_words(words_bernoulli(torch, dens, 910 + lg + i, universe=Uu)) for i in (0, 1)]
+            row = {}
+            for lname, thr in (("compressed", cr.PROMOTE_KEEP_DEFAULT), ("promoted", cr.PROMOTE_ALL)):
+                gs = [cr.upload_containers(lt.containers(), Uu, False, lt.cardinality(), thr) for lt in lites]
+                a = gs[0]
+                row[f"{lname}_bytes"] = int(8192 * a.n_bitmap_containers + a.array_pool_bytes + a.run_pool_bytes +
+                                            9 * a.n_containers + 2 * (a.max_key + 1))
+                for qname, q in (("uniform", q_uni), ("clustered", q_clu)):
+                    cr.contains_batch(a, q, out, cr.QUERY_CONTAINS)
+                    t = cold_time(torch, lambda: cr.contains_batch(a, q, out, cr.QUERY_CONTAINS), 3, flush)
+                    row[f"{lname}_{qname}_Gqps"] = round(nq / t / 1e6, 2)
+                cr.free(cr.set_operation(gs[0], gs[1], cr.AND))
+                row[f"{lname}_and_ms"] = round(cold_time(torch, lambda: cr.set_operation(gs[0], gs[1], cr.AND), 3,
+                                                         flush, after=cr.free), 4)
+                for x in gs:
+                    cr.free(x)
+            for k in ("uniform_Gqps", "clustered_Gqps"):
+                row[f"promoted_over_compressed_{k}"] = round(row[f"promoted_{k}"] / row[f"compressed_{k}"], 3)
+            row["promoted_over_compressed_and_speed"] = round(row["compressed_and_ms"] / row["promoted_and_ms"], 3)
+            res[f"2^{lg}_{dens * 100:g}pct"] = row
+            log("promote sweep", lg, dens, {k: v for k, v in row.items() if "over" in k})
+        del q_uni, q_clu, win, off
+    res["device_l2_bytes"] = cr.device_l2_bytes()
+    res["auto_threshold"] = {f"2^{lg}": cr.resolve_auto_threshold(1 << lg) for lg in (20, 22, 24, 26, 28, 30)}
+    return res
 
 
 def clustered_ids(torch, seed=11):

@@ -536,16 +536,26 @@ uint64_t device_l2_bytes(int device)
     return static_cast<uint64_t>(l2);
 }
 
-// PROMOTE_AUTO (src/promote.cu:334-367).  hipDeviceAttributeL2CacheSize
-// reports one XCD's L2 on gfx950 (4 MiB).  Point queries from every XCD hit
-// their own L2 copy of a flat bitset, so the per-XCD L2 -- not the 256 MB
-// Infinity Cache shared by all XCDs -- is the capacity that decides whether
-// a flat bitset "fits"; the rule stays `2 * ceil(U/8) > L2`.
+// PROMOTE_AUTO, re-derived for gfx950 (the reference's rule is
+// `2 * ceil(U/8) > L2`, src/promote.cu:334-367).  hipDeviceAttributeL2CacheSize
+// reports one XCD's L2 (4 MiB); every XCD caches its own copy of what its waves
+// read, and the 256 MB Infinity Cache behind them holds a whole 2^30 flat
+// bitmap.  A sweep of the compressed (KEEP) and promoted (ALL) layouts over
+// U = 2^20 .. 2^30 at 0.1 / 1 / 10% density (bench.py promote_sweep; the
+// table is in profiles/promote_auto_sweep.md) found the promoted layout
+// faster for uniform point queries by 1.8-5.4x at every universe where the
+// layouts differ -- the lookup is one dependent load instead of a key index
+// load plus a binary search, and both layouts stay cache-resident -- and its
+// AND as fast (2^30, 0.1%) or up to 2.1x faster.  So on gfx950 promotion pays from the smallest
+// universe swept, and the crossover moves down to where the reference's
+// pinned verdicts allow: U = 10^6 must stay compressed
+// (test/test_promote.cu:257-305), so promote once the flat bitmap exceeds
+// 1/32 of one XCD's L2, i.e. 128 KiB (U > 2^20) on MI355X.
 uint32_t resolve_auto_threshold(uint32_t universe_size, int device)
 {
     if (universe_size == 0) return CR_PROMOTE_KEEP_DEFAULT;
     const uint64_t flat = (static_cast<uint64_t>(universe_size) + 7u) / 8u;
-    return flat * 2u > device_l2_bytes(device) ? CR_PROMOTE_ALL : CR_PROMOTE_KEEP_DEFAULT;
+    return flat * 32u > device_l2_bytes(device) ? CR_PROMOTE_ALL : CR_PROMOTE_KEEP_DEFAULT;
 }
 
 }  // namespace crimpl

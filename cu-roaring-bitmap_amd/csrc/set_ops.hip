@@ -12,6 +12,7 @@
 // reference's per-class round trips.
 #include <algorithm>
 
+#include "image.hpp"
 #include "internal.hpp"
 
 namespace crimpl {
@@ -385,47 +386,30 @@ __device__ __forceinline__ uint32_t bitmap_op_stream(const uint64_t* pa, const u
     return pc;
 }
 
-// Expand one container of any type into a 2048-word LDS bitmap (caller syncs after).
-__device__ __forceinline__ void expand_to_lds(const Side& S, int32_t idx, uint32_t* lds)
+// Expand one container of any type into a 2048-word LDS bitmap (caller syncs
+// after).  A bitmap is copied; array and run containers go through expand_img,
+// whose difference array (`cover`, 2048 words) makes a run cost O(1) however
+// long it is (runs ending past 0xFFFF are clamped, as expand_to_bitmap_kernel
+// does, src/set_ops.cu:355-359).
+__device__ __forceinline__ void expand_to_lds(const Side& S, int32_t idx, uint32_t* lds, int32_t* cover)
 {
     const uint32_t t = threadIdx.x;
     const uint32_t type = S.types[idx];
     const uint32_t off = S.offsets[idx];
     if (type == CR_BITMAP) {
         const uint32_t* src = reinterpret_cast<const uint32_t*>(S.bmp) + (off >> 2);
-        for (uint32_t i = t; i < 2048u; i += EXEC_NT) lds[i] = src[i];
+        if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {  // 16-byte loads, both in flight
+            const uint4 x0 = ld_stream(reinterpret_cast<const uint4*>(src) + t);
+            const uint4 x1 = ld_stream(reinterpret_cast<const uint4*>(src) + t + EXEC_NT);
+            reinterpret_cast<uint4*>(lds)[t] = x0;
+            reinterpret_cast<uint4*>(lds)[t + EXEC_NT] = x1;
+        } else {
+            for (uint32_t i = t; i < 2048u; i += EXEC_NT) lds[i] = src[i];
+        }
         return;
     }
-    for (uint32_t i = t; i < 2048u; i += EXEC_NT) lds[i] = 0;
-    __syncthreads();
-    const uint32_t card = S.cards[idx];
-    if (type == CR_ARRAY) {
-        const uint16_t* arr = S.arr + (off >> 1);
-        for (uint32_t i = t; i < card; i += EXEC_NT) {
-            const uint32_t v = arr[i];
-            atomicOr(&lds[v >> 5], 1u << (v & 31u));
-        }
-    } else if (type == CR_RUN) {
-        // One lane per run: partial boundary words with atomicOr, interior words
-        // stored as all-ones (idempotent even if runs overlap).  The end is
-        // clamped to 0xFFFF as in expand_to_bitmap_kernel (src/set_ops.cu:355-359).
-        const uint16_t* runs = S.run + (off >> 1);
-        for (uint32_t r = t; r < card; r += EXEC_NT) {
-            const uint32_t s = runs[2 * r];
-            uint32_t e = s + runs[2 * r + 1];
-            if (e > 0xFFFFu) e = 0xFFFFu;
-            const uint32_t ws = s >> 5, we = e >> 5;
-            const uint32_t ms = ~0u << (s & 31u);
-            const uint32_t me = ~0u >> (31u - (e & 31u));
-            if (ws == we) {
-                atomicOr(&lds[ws], ms & me);
-            } else {
-                atomicOr(&lds[ws], ms);
-                for (uint32_t w = ws + 1; w < we; ++w) lds[w] = ~0u;
-                atomicOr(&lds[we], me);
-            }
-        }
-    }
+    const uint16_t* data = (type == CR_ARRAY ? S.arr : S.run) + (off >> 1);
+    expand_img<EXEC_NT>(static_cast<uint8_t>(type), data, S.cards[idx], lds, cover);
 }
 
 template <uint32_t OP>
@@ -433,7 +417,8 @@ __global__ __launch_bounds__(EXEC_NT) void so_exec(Side A, Side B, const Item* i
                                                    uint64_t* out_bmp, uint16_t* out_arr, uint16_t* out_run,
                                                    uint32_t* item_card, uint32_t* tile_keep)
 {
-    __shared__ uint32_t lds[4096];  // 16 KiB: two expanded bitmaps, or a staged array
+    __shared__ uint32_t lds[4096];    // 16 KiB: two expanded bitmaps, or a staged array
+    __shared__ int32_t cover[2048];   // the run difference array of expand_img
     __shared__ uint32_t red[EXEC_NT / 64];
     if (totals->overflow) return;  // the output was not allocated for this plan
     const uint32_t n_items = totals->c[C_ITEM];
@@ -452,16 +437,24 @@ __global__ __launch_bounds__(EXEC_NT) void so_exec(Side A, Side B, const Item* i
             break;
         }
         case CAT_MIXED: {
-            expand_to_lds(A, it.ai, lds);
+            expand_to_lds(A, it.ai, lds, cover);
             __syncthreads();
-            expand_to_lds(B, it.bi, lds + 2048);
+            expand_to_lds(B, it.bi, lds + 2048, cover);
             __syncthreads();
             uint32_t pc = 0;
-            uint32_t* dst = reinterpret_cast<uint32_t*>(out_bmp + it.slot * 1024ull);
-            for (uint32_t i = t; i < 2048u; i += EXEC_NT) {
-                const uint32_t r = apply32<OP>(lds[i], lds[2048 + i]);
-                dst[i] = r;
-                pc += __popc(r);
+            uint4* dst = reinterpret_cast<uint4*>(out_bmp + it.slot * 1024ull);  // 8 KiB slots: 16-byte aligned
+            const uint4* la = reinterpret_cast<const uint4*>(lds);
+            const uint4* lb = reinterpret_cast<const uint4*>(lds + 2048);
+#pragma unroll
+            for (uint32_t h = 0; h < 2u; ++h) {
+                const uint4 x = la[t + h * EXEC_NT], y = lb[t + h * EXEC_NT];
+                uint4 r;
+                r.x = apply32<OP>(x.x, y.x);
+                r.y = apply32<OP>(x.y, y.y);
+                r.z = apply32<OP>(x.z, y.z);
+                r.w = apply32<OP>(x.w, y.w);
+                st_stream(dst + t + h * EXEC_NT, r);
+                pc += __popc(r.x) + __popc(r.y) + __popc(r.z) + __popc(r.w);
             }
             pc = block_sum<EXEC_NT>(pc, red);
             card = pc > 65535u ? 0u : pc;

@@ -6,6 +6,13 @@ import numpy as np
 import orc
 
 
+def auto_l2(gpu) -> int:
+    """The L2 size for which the reference's PROMOTE_AUTO rule (2 ceil(U/8) > L2,
+    which the oracle restates) gives the library's gfx950 verdicts
+    (32 ceil(U/8) > one XCD's L2): that L2 / 16."""
+    return gpu.device_l2_bytes() // 16
+
+
 def flat_from_ids(ids, universe: int, n_words=None) -> np.ndarray:
     """Independent truth: a flat uint32 bitset with bit i set for each id < 32*n_words."""
     if n_words is None:

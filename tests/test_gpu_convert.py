@@ -11,7 +11,7 @@ import pytest
 
 import orc
 from gpu_inputs import KINDS, make_bitmap as _make
-from helpers import assert_same, flat_from_ids
+from helpers import assert_same, flat_from_ids, auto_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -172,9 +172,9 @@ def test_promote_auto_parity(gpu, universe):
     host = gpu.download(g)
     p = gpu.promote_auto(g)
     gpu.synchronize()
-    want = orc.promote_auto(host, gpu.device_l2_bytes())
+    want = orc.promote_auto(host, auto_l2(gpu))
     assert_same(gpu.download(p), want, strict=True, what="promote_auto")
-    if orc.resolve_auto_threshold(universe, gpu.device_l2_bytes()) == orc.PROMOTE_ALL:
+    if orc.resolve_auto_threshold(universe, auto_l2(gpu)) == orc.PROMOTE_ALL:
         assert p.n_array_containers == 0 and p.n_bitmap_containers == p.n_containers
     gpu.free(p)
     gpu.free(g)

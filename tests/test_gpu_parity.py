@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import orc
-from helpers import assert_same, flat_from_ids, mt_bernoulli, mt_mod_filter, words_mask
+from helpers import assert_same, flat_from_ids, mt_bernoulli, mt_mod_filter, words_mask, auto_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -63,7 +63,7 @@ def test_upload_from_ids_parity(gpu, n, universe, thr, seed):
     ids = rng.integers(0, universe, n, dtype=np.uint64).astype(np.uint32)
     if n > 10:
         ids[: n // 10] = ids[n // 10: 2 * (n // 10)]  # ~10% duplicates
-    want = orc.upload_from_ids(ids, universe, thr, gpu.device_l2_bytes())
+    want = orc.upload_from_ids(ids, universe, thr, auto_l2(gpu))
     g = gpu.upload_from_ids(ids, universe, thr)
     got = gpu.download(g)
     assert_same(got, want, strict=True, what="upload_from_ids")
@@ -167,6 +167,25 @@ def test_upload_from_ids_unaligned_pointer(gpu, n):
     gpu.free(g)
 
 
+# ---- PROMOTE_AUTO on gfx950 ----------------------------------------------------
+def test_resolve_auto_threshold_gfx950(gpu):
+    """The re-derived rule (32 ceil(U/8) > one XCD's L2) keeps the reference's five
+    pinned verdicts (test/test_promote.cu:257-381) and, at MI355X's 4 MiB per-XCD
+    L2, promotes from U > 2^20, where the reference's rule keeps 2^21 .. 2^24
+    compressed."""
+    _say("resolve_auto_threshold")
+    keep, all_ = orc.PROMOTE_KEEP_DEFAULT, orc.PROMOTE_ALL
+    for u, want in ((1_000_000, keep), (1_000_000_000, all_), (100_000, keep), (1 << 30, all_), (10_000, keep),
+                    (0, keep)):
+        assert gpu.resolve_auto_threshold(u) == want, u
+    if gpu.device_l2_bytes() == 4 << 20:
+        assert gpu.resolve_auto_threshold(1 << 20) == keep
+        assert gpu.resolve_auto_threshold((1 << 20) + 8) == all_
+        for lg in (21, 22, 24):
+            assert gpu.resolve_auto_threshold(1 << lg) == all_
+            assert orc.resolve_auto_threshold(1 << lg, gpu.device_l2_bytes()) == keep  # the reference's rule
+
+
 # ---- bitset uploads ----------------------------------------------------------
 BITSET_CASES = [(100000, 0.1, 1), (100000, 0.9, 2), (200000, 1 / 3, 3), (5 * 65536 + 123, 0.001, 4),
                 (5 * 65536 + 123, 0.95, 5), (1 << 22, 0.5, 6), (1 << 22, 0.55, 7), (64, 1.0, 8), (96, 0.0, 9)]
@@ -217,7 +236,7 @@ def test_upload_containers_parity(gpu, name, thr, with_u):
     _say("upload_containers", name, thr, with_u)
     U, sets = _lite_sets()
     lite = orc.Lite.from_sorted_ids(sets[name]).run_optimize()
-    want = orc.upload_packed(lite, U if with_u else None, thr, gpu.device_l2_bytes())
+    want = orc.upload_packed(lite, U if with_u else None, thr, auto_l2(gpu))
     if with_u and lite.cardinality() > U // 2:
         src, comp = lite.flip(0, U), True
     else:
@@ -258,12 +277,12 @@ def _build_operands(seed):
 def _upload_pair(gpu, lite, U, thr, negate=False):
     if negate:
         comp = lite.flip(0, U)
-        want = orc.upload_packed(comp, None, thr, gpu.device_l2_bytes())
+        want = orc.upload_packed(comp, None, thr, auto_l2(gpu))
         want.negated, want.universe_size, want.total_cardinality, want._c = True, U, lite.cardinality(), None
         g = gpu.upload_containers(comp.containers(), 0, False, 0, thr)
         g.negated, g.universe_size, g.total_cardinality = True, U, lite.cardinality()
         return g, want
-    want = orc.upload_packed(lite, None, thr, gpu.device_l2_bytes())
+    want = orc.upload_packed(lite, None, thr, auto_l2(gpu))
     return gpu.upload_containers(lite.containers(), 0, False, 0, thr), want
 
 
@@ -417,7 +436,7 @@ def test_multi_and_parity(gpu, case):
     lites = [orc.Lite.from_sorted_ids(np.asarray(l, dtype=np.uint32)) for l in logicals]
     gs, os_ = [], []
     for lt in lites:
-        want = orc.upload_packed(lt, U, thr, gpu.device_l2_bytes())
+        want = orc.upload_packed(lt, U, thr, auto_l2(gpu))
         src, comp = (lt.flip(0, U), True) if lt.cardinality() > U // 2 else (lt, False)
         gs.append(gpu.upload_containers(src.containers(), U, comp, lt.cardinality(), thr))
         os_.append(want)

@@ -12,7 +12,7 @@ import pytest
 
 import orc
 from gpu_inputs import KINDS, make_bitmap
-from helpers import assert_same, ids_from_flat
+from helpers import assert_same, ids_from_flat, auto_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -69,7 +69,7 @@ def test_deserialize_parity(gpu, name, with_u, thr):
     U, lites = _lites()
     data = lites[name].portable_serialize()
     lite = orc.Lite.portable_deserialize(data)
-    want = orc.upload_packed(lite, U if with_u else None, thr, gpu.device_l2_bytes())
+    want = orc.upload_packed(lite, U if with_u else None, thr, auto_l2(gpu))
     g = gpu.portable_deserialize(data, U if with_u else 0, thr)
     assert_same(gpu.download(g), want, strict=True, what="portable_deserialize")
     # and back: the GPU writer gives the run-optimized bytes of the same logical
