@@ -451,7 +451,8 @@ def config3(torch, cr, flush, nt, no_cpu):
     nq = qs["uniform"].numel()
     res = torch.empty(nq, device="cuda", dtype=torch.int32)
     modes = {"contains": cr.QUERY_CONTAINS, "wavefront_contains": cr.QUERY_WAVEFRONT,
-             "wavefront_contains_api": cr.QUERY_WAVEFRONT_API, "contains_api": cr.QUERY_CONTAINS_API}
+             "wavefront_contains_api": cr.QUERY_WAVEFRONT_API, "contains_api": cr.QUERY_CONTAINS_API,
+             "partitioned": cr.QUERY_PARTITIONED}
     out = {"queries": nq}
     for j, dens in enumerate((0.001, 0.01, 0.1, 0.5)):
         lite = orc.Lite.from_words(words_bernoulli(torch, dens, 40 + j))
@@ -468,7 +469,7 @@ def config3(torch, cr, flush, nt, no_cpu):
                     torch.cuda.synchronize()
                     t = cold_time(torch, lambda: cr.contains_batch(g, q, res, mode), 3, flush)
                     d[f"{lname}_{qname}_{mname}_Gqps"] = round(nq / t / 1e6, 2)
-                    if mname == "contains":
+                    if mname in ("contains", "partitioned"):
                         d[f"{lname}_{qname}_{mname}_frac_hbm_18B"] = round(18 * nq / t / 1e6 / HBM_PEAK_GBS, 4)
                     # every mode and layout gives the same answers (checksum of the answer vector)
                     s_ = int((res.to(torch.int64) * (torch.arange(nq, device="cuda") % 1021 + 1)).sum().item())
@@ -491,7 +492,7 @@ def config3(torch, cr, flush, nt, no_cpu):
         for g in layouts.values():
             cr.free(g)
         out[f"density_{dens * 100:g}pct"] = d
-        log("configs[3]", dens, {k: v for k, v in d.items() if k.endswith("contains_Gqps")})
+        log("configs[3]", dens, {k: v for k, v in d.items() if k.endswith("contains_Gqps") or "partitioned_Gqps" in k})
     del qs, res
     torch.cuda.empty_cache()
     return out

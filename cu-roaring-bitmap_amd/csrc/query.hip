@@ -14,6 +14,7 @@
 #include "cu_roaring/device/roaring_view.hpp"
 #include "cu_roaring/device/roaring_wavefront_query.hpp"
 #include "internal.hpp"
+#include "tiles.hpp"
 
 namespace crimpl {
 
@@ -87,6 +88,235 @@ __global__ __launch_bounds__(Q_NT) void contains_general(GpuRoaringView v, const
     }
 }
 
+// ---- partitioned point queries (CR_QUERY_PARTITIONED) ----------------------------
+// Uniform random queries over a large bitmap are bound by the memory system's
+// random-request rate: every query is one dependent read of a cache line (100M
+// queries = 100M fabric read requests).  Partitioned, the same answers cost a
+// few streaming bytes per query and one read of each container:
+//   ids_tile_sort<true>  tile-sort the query ids by 16-key bucket (the
+//                        upload's tile sort), recording each query's sorted
+//                        position within its tile (perm, u16);
+//   qp_answer            one workgroup per bucket loads the bucket's 16
+//                        containers into LDS as bitmaps and answers every query
+//                        of the bucket from LDS: a byte at its sorted position;
+//   qp_unpermute         one workgroup per tile stages the tile's answer bytes
+//                        in LDS and writes out[i] = answer[perm[i]] in input
+//                        order.
+// A query whose key lies past the bitmap's last bucket (sorted into the tile
+// sort's sentinel run) answers `negated`, as contains() does for key > max_key.
+
+// One wave fills `w` (2048 words) with key's container as a bitmap -- zeros
+// when the key is absent -- found by contains()'s own lookup rules.
+__device__ void qp_load_container(const GpuRoaringView& v, uint32_t key, uint32_t* w, uint32_t lane)
+{
+    int idx = -1;
+    if (v.all_bitmap) {
+        if (key <= v.max_key) {
+            const uint32_t x = v.key_index[key];
+            idx = x == 0xFFFFu ? -1 : static_cast<int>(x);
+        }
+    } else {
+        idx = v.lookup_key(key);
+    }
+    uint4* w4 = reinterpret_cast<uint4*>(w);
+    uint32_t type = CR_BITMAP, off = 0, card = 0;
+    if (idx >= 0 && !v.all_bitmap) {
+        type = static_cast<uint32_t>(v.types[idx]);
+        off = v.offsets[idx];
+        card = v.cardinalities[idx];
+    }
+    if (idx >= 0 && type == CR_BITMAP) {
+        const uint64_t* src = v.all_bitmap ? v.bitmap_data + (static_cast<uint64_t>(idx) << 10) : v.bitmap_data + (off >> 3);
+        if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
+            uint4 x[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = ld_stream(reinterpret_cast<const uint4*>(src) + lane + 64 * j);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) w4[lane + 64 * j] = x[j];
+        } else {
+            const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
+            for (uint32_t i = lane; i < 2048u; i += 64) w[i] = s32[i];
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w4[lane + 64 * j] = make_uint4(0, 0, 0, 0);
+    if (idx < 0) return;
+    if (type == CR_ARRAY) {  // the wave's LDS operations retire in order: the zeros land first
+        const uint16_t* arr = v.array_data + (off >> 1);
+        for (uint32_t i = lane; i < card; i += 64) {
+            const uint32_t x = arr[i];
+            atomicOr(&w[x >> 5], 1u << (x & 31u));
+        }
+    } else if (type == CR_RUN) {
+        // Lane l owns words [32 l, 32 l + 32) (bits [1024 l, 1024 l + 1024)):
+        // a binary search finds the first run ending at or after them, then the
+        // sorted runs that overlap them set their bits.  Ends are clamped to
+        // 0xFFFF, as contains() accepts any low <= 0xFFFF past a run's start.
+        const uint16_t* runs = v.run_data + (off >> 1);
+        const uint32_t lo = 1024u * lane, hi = lo + 1023u;
+        int a = 0, z = static_cast<int>(card);  // first run with start + len >= lo
+        while (a < z) {
+            const int mid = (a + z) >> 1;
+            if (static_cast<uint32_t>(runs[2 * mid]) + runs[2 * mid + 1] < lo)
+                a = mid + 1;
+            else
+                z = mid;
+        }
+        for (uint32_t r = static_cast<uint32_t>(a); r < card; ++r) {
+            const uint32_t s = runs[2 * r];
+            if (s > hi) break;
+            const uint32_t e = min(min(0xFFFFu, s + runs[2 * r + 1]), hi);
+            const uint32_t b0 = max(s, lo);
+            for (uint32_t x = b0; x <= e;) {  // word by word within the lane's range
+                const uint32_t wi = x >> 5, sb = x & 31u;
+                const uint32_t eb = min(31u, e - (x & ~31u));
+                w[wi] |= (eb - sb == 31u ? ~0u : ((1u << (eb - sb + 1u)) - 1u)) << sb;
+                x = (wi + 1u) << 5;
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(BUILD_NT) void qp_answer(const uint32_t* __restrict__ part,
+                                                      const uint16_t* __restrict__ tab, IdsGeom g, GpuRoaringView v,
+                                                      uint8_t* __restrict__ ans)
+{
+    __shared__ alignas(16) uint32_t bits[BK_KEYS * 2048u];  // the bucket's 16 containers, 128 KiB
+    const uint32_t t = threadIdx.x;
+    const uint32_t b = (blockIdx.x % 8) * build_per_xcd(g.NB) + blockIdx.x / 8;
+    if (b >= g.NB) return;
+    const uint32_t wave = t >> 6, lane = __lane_id();
+    const uint32_t key = b * BK_KEYS + wave;
+    if (key < g.K) {
+        qp_load_container(v, key, bits + wave * 2048u, lane);
+    } else {
+        uint4* w4 = reinterpret_cast<uint4*>(bits + wave * 2048u);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w4[lane + 64 * j] = make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+    const uint32_t neg = v.negated ? 1u : 0u;
+    // A lane's consecutive fields give consecutive answer bytes: written with
+    // at most three naturally aligned stores (byte, short, dword) instead of a
+    // byte store each.
+    walk_bucket<true>(part, tab, g, b, wave, lane, [&](uint32_t tile, uint32_t i, uint32_t n, const uint32_t* f) {
+        uint64_t v = 0;
+#pragma unroll
+        for (uint32_t m = 0; m < 7u; ++m) {
+            const uint32_t F = f[m] & FIELD_MASK;
+            const uint64_t a = ((bits[F >> 5] >> (F & 31u)) & 1u) ^ neg;
+            v |= m < n ? a << (8u * m) : 0ull;
+        }
+        uint8_t* p = ans + static_cast<uint64_t>(tile) * TILE + i;
+        uint32_t left = n;
+        if (reinterpret_cast<uintptr_t>(p) & 1u) {
+            *p = static_cast<uint8_t>(v);
+            v >>= 8;
+            ++p;
+            --left;
+        }
+        if (left >= 2u && (reinterpret_cast<uintptr_t>(p) & 2u)) {
+            *reinterpret_cast<uint16_t*>(p) = static_cast<uint16_t>(v);
+            v >>= 16;
+            p += 2;
+            left -= 2u;
+        }
+        if (left >= 4u) {
+            *reinterpret_cast<uint32_t*>(p) = static_cast<uint32_t>(v);
+            v >>= 32;
+            p += 4;
+            left -= 4u;
+        }
+        if (left >= 2u) {
+            *reinterpret_cast<uint16_t*>(p) = static_cast<uint16_t>(v);
+            v >>= 16;
+            p += 2;
+            left -= 2u;
+        }
+        if (left) *p = static_cast<uint8_t>(v);
+    });
+}
+
+constexpr int QU_NT = 1024;
+
+__global__ __launch_bounds__(QU_NT) void qp_unpermute(const uint16_t* __restrict__ perm,
+                                                      const uint8_t* __restrict__ ans,
+                                                      const uint16_t* __restrict__ tab, IdsGeom g, uint32_t neg,
+                                                      uint32_t* __restrict__ out)
+{
+    __shared__ alignas(16) uint8_t a[TILE];
+    const uint32_t tile = blockIdx.x, t = threadIdx.x;
+    const uint64_t base = static_cast<uint64_t>(tile) * TILE;
+    // queries of the real buckets; the sentinel run (keys past the last bucket) follows
+    const uint32_t in_range =
+        tab[(static_cast<uint64_t>(tile / TB) * (g.NB + 1) + g.NB) * TB + tile % TB];
+    const uint4* a_src = reinterpret_cast<const uint4*>(ans + base);
+    for (uint32_t u = t; u < TILE / 16u; u += QU_NT) reinterpret_cast<uint4*>(a)[u] = ld_stream(a_src + u);
+    __syncthreads();
+    auto answer = [&](uint32_t sp) { return sp < in_range ? static_cast<uint32_t>(a[sp]) : neg; };
+    if (base + TILE <= g.n && (reinterpret_cast<uintptr_t>(out) & 15u) == 0) {
+        // four queries a thread: 8-byte perm loads, 16-byte answer stores
+        const uint2* p2 = reinterpret_cast<const uint2*>(perm + base);
+        uint4* o4 = reinterpret_cast<uint4*>(out + base);
+#pragma unroll
+        for (uint32_t k = 0; k < TILE / (4u * QU_NT); ++k) {
+            const uint32_t q = t + k * QU_NT;
+            const uint2 pp = p2[q];
+            st_stream(o4 + q, make_uint4(answer(pp.x & 0xFFFFu), answer(pp.x >> 16), answer(pp.y & 0xFFFFu),
+                                         answer(pp.y >> 16)));
+        }
+    } else {
+        for (uint32_t p = t; p < TILE && base + p < g.n; p += QU_NT) out[base + p] = answer(perm[base + p]);
+    }
+}
+
+int contains_partitioned(const GpuRoaringView& v, const uint32_t* d_ids, uint64_t n, uint32_t* d_out, hipStream_t s)
+{
+    IdsGeom g{};
+    g.n = n;
+    g.K = v.key_index ? v.max_key + 1u : 65536u;  // without a key index every key may hold a container
+    g.NB = (g.K + BK_KEYS - 1) / BK_KEYS;
+    const uint64_t n_tiles = (n + TILE - 1) / TILE;
+    if (n_tiles > 0xFFFFFFFFull / TILE_WORDS) {
+        set_error("cr_contains_batch: %llu queries exceed the partitioned mode's tile count",
+                  static_cast<unsigned long long>(n));
+        return CR_ERR_UNSUPPORTED;
+    }
+    g.n_tiles = static_cast<uint32_t>(n_tiles);
+    g.G = std::max<uint32_t>(1, std::min<uint32_t>(num_cus(), (g.n_tiles + TB - 1) / TB));
+    g.vec = (reinterpret_cast<uintptr_t>(d_ids) & 15u) == 0;
+    Carver c;
+    const size_t o_part = c.add(sizeof(uint32_t) * (static_cast<uint64_t>(g.n_tiles) * TILE_WORDS + 4));
+    const size_t o_tab = c.add(sizeof(uint16_t) * static_cast<uint64_t>((g.n_tiles + TB - 1) / TB) * TB * (g.NB + 1));
+    const size_t o_perm = c.add(sizeof(uint16_t) * static_cast<uint64_t>(g.n_tiles) * TILE);
+    const size_t o_ans = c.add(static_cast<uint64_t>(g.n_tiles) * TILE);
+    const size_t o_gmax = c.add(sizeof(uint32_t) * g.G);
+    const size_t o_tot = c.add(sizeof(IdsTotals));
+    Scratch sc;
+    CR_RET(sc.alloc(c.total, s));
+    {
+        CR_TIMED("qp_tile_sort", s);
+        ids_tile_sort<true><<<g.G, TS_NT, 0, s>>>(d_ids, g, sc.at<uint32_t>(o_part), sc.at<uint16_t>(o_tab),
+                                                  sc.at<uint32_t>(o_gmax), sc.at<IdsTotals>(o_tot),
+                                                  sc.at<uint16_t>(o_perm));
+    }
+    CR_LAUNCH_CHECK();
+    {
+        CR_TIMED("qp_answer", s);
+        qp_answer<<<build_grid(g.NB), BUILD_NT, 0, s>>>(sc.at<uint32_t>(o_part), sc.at<uint16_t>(o_tab), g, v,
+                                                        sc.at<uint8_t>(o_ans));
+    }
+    CR_LAUNCH_CHECK();
+    {
+        CR_TIMED("qp_unpermute", s);
+        qp_unpermute<<<g.n_tiles, QU_NT, 0, s>>>(sc.at<uint16_t>(o_perm), sc.at<uint8_t>(o_ans),
+                                                 sc.at<uint16_t>(o_tab), g, v.negated ? 1u : 0u, d_out);
+    }
+    CR_LAUNCH_CHECK();
+    return CR_OK;
+}
+
 }  // namespace crimpl
 
 using namespace crimpl;
@@ -94,7 +324,7 @@ using namespace crimpl;
 extern "C" int cr_contains_batch(const cr_gpu_roaring_view* view, const uint32_t* d_ids, uint64_t n, uint32_t* d_out,
                                  uint32_t mode, cr_stream_t stream)
 {
-    if (!view || (n && (!d_ids || !d_out)) || mode > CR_QUERY_CONTAINS_API) {
+    if (!view || (n && (!d_ids || !d_out)) || mode > CR_QUERY_PARTITIONED) {
         set_error("cr_contains_batch: invalid argument");
         return CR_ERR_INVALID;
     }
@@ -103,6 +333,7 @@ extern "C" int cr_contains_batch(const cr_gpu_roaring_view* view, const uint32_t
     static_assert(sizeof(v) == sizeof(*view), "view layout");
     std::memcpy(&v, view, sizeof(v));
     hipStream_t s = as_stream(stream);
+    if (mode == CR_QUERY_PARTITIONED) return contains_partitioned(v, d_ids, n, d_out, s);
     const uint32_t cus = num_cus();
     const uint64_t per_block = static_cast<uint64_t>(Q_NT) * QPT;
     const unsigned grid = static_cast<unsigned>(

@@ -25,7 +25,7 @@ PROMOTE_KEEP_DEFAULT = 4096
 PROMOTE_ALL = 0
 PROMOTE_AUTO = 0xFFFFFFFF
 TC_BITSET, TC_ARRAY, TC_RUN = 1, 2, 3
-QUERY_CONTAINS, QUERY_WAVEFRONT, QUERY_WAVEFRONT_API, QUERY_CONTAINS_API = 0, 1, 2, 3
+QUERY_CONTAINS, QUERY_WAVEFRONT, QUERY_WAVEFRONT_API, QUERY_CONTAINS_API, QUERY_PARTITIONED = 0, 1, 2, 3, 4
 
 EXPORTS = [
     "cr_last_error", "cr_upload_from_ids", "cr_upload_from_device_ids", "cr_upload_from_bitset",

@@ -58,6 +58,13 @@ extern "C" {
  * GpuRoaringView::contains() one query at a time, on every layout. */
 #define CR_QUERY_WAVEFRONT_API 2
 #define CR_QUERY_CONTAINS_API 3
+/* Mode 4 gives the same answers by partitioning: the queries are sorted by
+ * 16-key bucket on the device, each bucket's containers are loaded once into
+ * LDS and its queries answered there, and the answers are written back in
+ * input order.  Fastest for many uniform queries over a large bitmap (one
+ * random memory request per query otherwise); it allocates scratch of about
+ * 5.5 bytes per query from the library's pool, stream-ordered. */
+#define CR_QUERY_PARTITIONED 4
 
 /*
  * Byte-identical to cu_roaring::GpuRoaring (include/cu_roaring/types.cuh:15-54):

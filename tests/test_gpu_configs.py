@@ -59,7 +59,7 @@ def test_config0(gpu, torch):
         gpu.free(r)
     dq = torch.from_numpy(q.view(np.int32)).cuda()
     out = torch.empty_like(dq)
-    for mode in (0, 1, 2, 3):
+    for mode in (0, 1, 2, 3, 4):
         gpu.contains_batch(ga, dq, out, mode)
         torch.cuda.synchronize()
         assert np.array_equal(out.cpu().numpy().view(np.uint32), np.isin(q, sa).astype(np.uint32))
@@ -142,7 +142,7 @@ def test_config3_point_queries(gpu, torch, queries, j, dens):
         truth = ((w32[q64 >> 5].to(torch.int64) >> (q64 & 31)) & 1).to(torch.int32)
         out = torch.empty_like(q)
         for lname, g in layouts.items():
-            for mode in (0, 1, 2, 3):
+            for mode in (0, 1, 2, 3, 4):
                 _say("configs[3]", dens, lname, qname, mode)
                 out.fill_(-1)
                 gpu.contains_batch(g, q, out, mode)

@@ -167,6 +167,27 @@ def test_upload_from_ids_unaligned_pointer(gpu, n):
     gpu.free(g)
 
 
+@pytest.mark.parametrize("offset", [1, 3])
+def test_contains_partitioned_unaligned_and_partial_tiles(gpu, offset):
+    """Mode 4 with a query pointer off a 16-byte boundary (the tile sort's scalar
+    loads and the permutation in that order), an unaligned output, and a tile
+    count that is not a multiple of the tile blocks."""
+    _say("contains partitioned unaligned", offset)
+    torch = _torch()
+    rng = np.random.default_rng(90 + offset)
+    U = 1 << 26
+    ids = np.nonzero(rng.random(U) < 0.05)[0].astype(np.uint32)
+    g, want = gpu.upload_from_ids(ids, U), orc.upload_from_ids(ids, U)
+    q = rng.integers(0, 2 * U, 24576 * 9 + 77, dtype=np.uint64).astype(np.uint32)
+    dq = _dev_u32(np.concatenate([np.zeros(offset, np.uint32), q]))[offset:]
+    out = torch.empty(q.size + offset, dtype=torch.int32, device="cuda")[offset:]
+    assert dq.data_ptr() % 16 != 0 and out.data_ptr() % 16 != 0
+    gpu.contains_batch(g, dq, out, 4)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), orc.contains_many(want, q))
+    gpu.free(g)
+
+
 # ---- PROMOTE_AUTO on gfx950 ----------------------------------------------------
 def test_resolve_auto_threshold_gfx950(gpu):
     """The re-derived rule (32 ceil(U/8) > one XCD's L2) keeps the reference's five
@@ -455,7 +476,7 @@ QUERY_CASES = [("ids", 1 << 24, 0.01), ("ids", 1 << 24, 0.6), ("keep", 1 << 22, 
 
 
 @pytest.mark.parametrize("layout,universe,density", QUERY_CASES)
-@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3, 4])
 def test_contains_parity(gpu, layout, universe, density, mode):
     _say("contains", layout, universe, density, mode)
     torch = _torch()
