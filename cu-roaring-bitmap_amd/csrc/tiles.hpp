@@ -162,9 +162,21 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
 #pragma unroll
             for (uint32_t j = 0; j < TS_PER; j += 2) rk[j >> 1] = (run + 64u * j) | ((run + 64u * (j + 1)) << 16);
         } else {
+            // Per pass j, likewise when the wave's j-th ids share a bucket
+            // (sorted or clustered ids spread over a few buckets per tile);
+            // otherwise an atomic a lane.
 #pragma unroll
             for (uint32_t j = 0; j < TS_PER; ++j) {
-                const uint32_t r = atomicAdd(&cnt[bucket(v[j])], 1u);
+                const uint32_t bj = bucket(v[j]);
+                const uint32_t b0 = __builtin_amdgcn_readfirstlane(bj);
+                uint32_t r;
+                if (__ballot(bj != b0) == 0) {
+                    uint32_t r0 = 0;
+                    if (lane == 0) r0 = atomicAdd(&cnt[b0], 64u);
+                    r = __builtin_amdgcn_readfirstlane(r0) + lane;
+                } else {
+                    r = atomicAdd(&cnt[bj], 1u);
+                }
                 if (j & 1u)
                     rk[j >> 1] |= r << 16;
                 else
@@ -309,11 +321,22 @@ inline uint32_t build_grid(uint32_t nb) { return 8 * build_per_xcd(nb); }
 // With CHUNKS the callback is on_chunk(tile, i, n, f): the n (1..7) fields
 // i .. i + n - 1 that start in one lane's 4 words, f[0 .. n) (unmasked), so
 // a consumer can handle a lane's consecutive fields together.
+// Runs longer than two windows (clustered or sorted ids) are queued in LDS
+// and their remaining windows shared by the whole workgroup after the walk,
+// so that a bucket whose ids sit in a few tiles -- one wave's blocks -- keeps
+// all sixteen waves busy (a run that finds the queue full is finished by its
+// own wave).  Every thread of the workgroup must call this.
+constexpr uint32_t WALK_QCAP = 2048;  // 16 KiB of LDS beside the callers' 128 KiB
+
 template <bool CHUNKS = false, class OnField>
 __device__ __forceinline__ void walk_bucket(const uint32_t* __restrict__ part, const uint16_t* __restrict__ tab,
                                             const IdsGeom& g, uint32_t b, uint32_t wave, uint32_t lane,
                                             OnField on_field)
 {
+    __shared__ uint2 q_ent[WALK_QCAP];  // {tile, s0 | s1 << 16}
+    __shared__ uint32_t q_n;
+    if (threadIdx.x == 0) q_n = 0;
+    __syncthreads();
     const uint32_t grp = lane >> 2;  // sixteen 4-lane groups
     const uint32_t r4 = lane & 3u;
     const uint32_t n_blk = (g.n_tiles + TB - 1) / TB;
@@ -421,10 +444,14 @@ __device__ __forceinline__ void walk_bucket(const uint32_t* __restrict__ part, c
                     set_chunk(x[h][k], r4 == 3u ? e[h][k] : nx, wb[h] + 16u * k + 4u * r4, ts0[h], ts1[h], tl[h]);
                 }
         }
-        // Runs longer than two windows (clustered ids): one tile at a time,
-        // its remaining windows shared by all sixteen groups, so that a long
-        // run in one tile of the step does not leave the other groups idle.
-        uint64_t longs = __ballot(own_nw > 2u);
+        // Runs longer than two windows: queued for the workgroup; one that
+        // finds the queue full is finished here, one tile at a time, its
+        // remaining windows shared by the wave's sixteen groups.
+        const bool is_long = own_nw > 2u;
+        uint32_t slot = WALK_QCAP;
+        if (is_long) slot = atomicAdd(&q_n, 1u);
+        if (is_long && slot < WALK_QCAP) q_ent[slot] = make_uint2(tile_of(st, lane), m0 | (m1 << 16));
+        uint64_t longs = __ballot(is_long && slot >= WALK_QCAP);
         while (longs) {
             const uint32_t src = static_cast<uint32_t>(__builtin_ctzll(longs));
             longs &= longs - 1u;
@@ -444,6 +471,28 @@ __device__ __forceinline__ void walk_bucket(const uint32_t* __restrict__ part, c
                 if (act) set_chunk(x, r4 == 3u ? e : nx, lo_w, s0, s1, tile);
             }
         }
+    }
+    // The queued runs: windows 2, 3, ... of each in chunks of sixteen (one a
+    // group), the chunks of all runs dealt to the waves in turn.
+    __syncthreads();
+    const uint32_t nq = min(q_n, WALK_QCAP);
+    uint32_t off = 0;  // chunks of the runs before
+    for (uint32_t j = 0; j < nq; ++j) {
+        const uint2 ent = q_ent[j];
+        const uint32_t tile = ent.x, s0 = ent.y & 0xFFFFu, s1 = ent.y >> 16;
+        const uint32_t base = tile * TILE_WORDS;
+        const uint32_t w0 = ((FIELD_BITS * s0) >> 5) & ~3u;
+        const uint32_t w1 = (FIELD_BITS * s1 - 1u) >> 5;
+        const uint32_t nch = ((w1 - w0) / 16u - 1u + 15u) / 16u;  // windows 2 .. (w1 - w0) / 16
+        for (uint32_t c = (wave + BUILD_WAVES - off % BUILD_WAVES) % BUILD_WAVES; c < nch; c += BUILD_WAVES) {
+            const uint32_t lo_w = w0 + 16u * (2u + 16u * c + grp) + 4u * r4;
+            const bool act = lo_w <= w1;
+            const uint4 x = act ? *reinterpret_cast<const uint4*>(part + base + lo_w) : make_uint4(0, 0, 0, 0);
+            const uint32_t e = (act && r4 == 3u && lo_w + 4u <= w1) ? part[base + lo_w + 4u] : 0u;
+            const uint32_t nx = __shfl_down(x.x, 1, 64);
+            if (act) set_chunk(x, r4 == 3u ? e : nx, lo_w, s0, s1, tile);
+        }
+        off += nch;
     }
 }
 

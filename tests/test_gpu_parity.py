@@ -188,6 +188,49 @@ def test_contains_partitioned_unaligned_and_partial_tiles(gpu, offset):
     gpu.free(g)
 
 
+def _skewed_ids(case, rng):
+    """Inputs whose tiles each fall in a few key buckets (16 keys a bucket):
+    long runs per (bucket, tile), shared by the whole build workgroup.
+    "overflow" gives the single bucket of U = 2^20 more such tiles (2054) than
+    the workgroup's queue holds (2048); the rest are finished by their wave."""
+    if case == "sorted":
+        U = 1 << 26
+        return U, np.sort(rng.integers(0, U, 24576 * 20 + 77, dtype=np.uint64)).astype(np.uint32)
+    if case == "clustered":  # groups of 4096 sorted ids in random 65536-aligned windows
+        U = 1 << 28
+        win = rng.integers(0, U >> 16, 150, dtype=np.uint64)
+        off = np.sort(rng.integers(0, 65536, (150, 4096), dtype=np.uint64), axis=1)
+        return U, ((win[:, None] << 16) + off).reshape(-1).astype(np.uint32)
+    U = 1 << 20
+    allowed = np.nonzero(rng.random(U) < 0.9)[0].astype(np.uint32)
+    return U, allowed[rng.integers(0, allowed.size, 24576 * 2054 + 5)]
+
+
+@pytest.mark.parametrize("case", ["sorted", "clustered", "overflow"])
+def test_upload_and_partitioned_skewed(gpu, case):
+    """upload_from_ids and mode 4 on inputs whose tiles hit few buckets: the
+    walk's queued long runs, and its in-wave path once the queue is full."""
+    _say("skewed ids", case)
+    torch = _torch()
+    rng = np.random.default_rng({"sorted": 70, "clustered": 71, "overflow": 72}[case])
+    U, ids = _skewed_ids(case, rng)
+    want = orc.upload_from_ids(ids, U, orc.PROMOTE_AUTO, auto_l2(gpu))
+    dq = _dev_u32(ids)
+    g = gpu.upload_from_device_ids(dq, U)
+    assert_same(gpu.download(g), want, strict=True, what=f"upload {case}")
+    # the same skew as queries: every id is a member; shifted ones mostly not
+    flat = np.zeros(U + 1, np.uint8)
+    flat[ids] = 1
+    out = torch.empty(ids.size, dtype=torch.int32, device="cuda")
+    for shift in (0, 1):
+        q = dq if shift == 0 else _dev_u32((ids + 1) % U)
+        gpu.contains_batch(g, q, out, 4)
+        torch.cuda.synchronize()
+        want_q = flat[(ids.astype(np.int64) + shift) % U].astype(np.uint32)
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), want_q), (case, shift)
+    gpu.free(g)
+
+
 # ---- PROMOTE_AUTO on gfx950 ----------------------------------------------------
 def test_resolve_auto_threshold_gfx950(gpu):
     """The re-derived rule (32 ceil(U/8) > one XCD's L2) keeps the reference's five
@@ -436,7 +479,7 @@ def test_set_operation_empty_and_identical(gpu):
                                   "fused_absent_negated_key", "single", "fused_8"])
 def test_multi_and_parity(gpu, case):
     _say("multi_and", case)
-    rng = np.random.default_rng(hash(case) & 0xFFFF)
+    rng = np.random.default_rng(sum(map(ord, case)))
     if case == "fused_absent_negated_key":  # test/test_complement.cu:604-679
         U = 3 * 65536
         la = np.nonzero(rng.random(U) < 0.2)[0]
