@@ -48,10 +48,12 @@ extern "C" {
 #define CR_TC_ARRAY 2
 #define CR_TC_RUN 3
 /* cr_contains_batch modes. */
-/* Modes 0 and 1 answer as GpuRoaringView::contains does; on an all-bitmap
- * view they run a batched copy of its two-load fast path (mode 1 reads the
+/* Modes 0 and 1 answer as GpuRoaringView::contains does, in batched kernels:
+ * on an all-bitmap view a copy of its two-load fast path (mode 1 reads a
  * key_index entry once when the whole wave shares a key, as
- * wavefront_contains does), on other layouts the header functions. */
+ * wavefront_contains does); on other layouts mode 0 calls the header function
+ * per query and mode 1 runs its lookup rules with each lane's queries searched
+ * in lockstep, for wave-coherent (clustered) batches. */
 #define CR_QUERY_CONTAINS 0   /* GpuRoaringView::contains per lane */
 #define CR_QUERY_WAVEFRONT 1  /* wavefront_contains (== warp_contains) */
 /* Modes 2 and 3 always run the header functions wavefront_contains() and

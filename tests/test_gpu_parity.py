@@ -515,7 +515,7 @@ def test_multi_and_parity(gpu, case):
 # ---- point queries ------------------------------------------------------------
 QUERY_CASES = [("ids", 1 << 24, 0.01), ("ids", 1 << 24, 0.6), ("keep", 1 << 22, 0.001), ("keep", 1 << 22, 0.3),
                ("runs", 1 << 20, 0.0), ("bitset_neg", 1 << 21, 0.8), ("empty", 1 << 20, 0.0),
-               ("small", 5000, 0.1)]
+               ("small", 5000, 0.1), ("setop", 1 << 22, 0.002)]
 
 
 @pytest.mark.parametrize("layout,universe,density", QUERY_CASES)
@@ -539,6 +539,18 @@ def test_contains_parity(gpu, layout, universe, density, mode):
     elif layout == "bitset_neg":
         w = flat_from_ids(ids, universe)
         g, want = gpu.upload_from_bitset(w, universe), orc.upload_from_bitset(w, universe)
+    elif layout == "setop":  # a set-operation result: no key_index, containers found by a search of keys
+        half = np.nonzero(rng.random(universe) < 0.3)[0].astype(np.uint32)
+        half = half[(half >> 16) % 3 == 0]  # bitmaps in every third key, arrays (ids) elsewhere
+        la, lb = orc.Lite.from_sorted_ids(ids), orc.Lite.from_sorted_ids(half)
+        ga = gpu.upload_containers(la.containers(), universe, False, la.cardinality(), orc.PROMOTE_KEEP_DEFAULT)
+        gb = gpu.upload_containers(lb.containers(), universe, False, lb.cardinality(), orc.PROMOTE_KEEP_DEFAULT)
+        oa = orc.upload_packed(la, universe, orc.PROMOTE_KEEP_DEFAULT)
+        ob = orc.upload_packed(lb, universe, orc.PROMOTE_KEEP_DEFAULT)
+        g, want = gpu.set_operation(ga, gb, orc.OR), orc.set_operation(oa, ob, orc.OR)
+        gpu.free(ga)
+        gpu.free(gb)
+        assert not g.key_index and g.n_array_containers > 0 and g.n_bitmap_containers > 0
     elif layout == "empty":
         lt = orc.Lite.from_sorted_ids(np.zeros(0, np.uint32))
         g = gpu.upload_containers([], 0, False, 0, orc.PROMOTE_AUTO)
