@@ -217,16 +217,29 @@ __global__ __launch_bounds__(Q_NT) void contains_general(GpuRoaringView v, const
 // queries = 100M fabric read requests).  Partitioned, the same answers cost a
 // few streaming bytes per query and one read of each container:
 //   ids_tile_sort<true>  tile-sort the query ids by 16-key bucket (the
-//                        upload's tile sort), recording each query's sorted
-//                        position within its tile (perm, u16);
+//                        upload's tile sort), recording each query's padded
+//                        sorted position within its tile (perm, u16);
 //   qp_answer            one workgroup per bucket loads the bucket's 16
 //                        containers into LDS as bitmaps and answers every query
-//                        of the bucket from LDS: a byte at its sorted position;
-//   qp_unpermute         one workgroup per tile stages the tile's answer bytes
+//                        of the bucket from LDS: a bit at its padded sorted
+//                        position, eight answers to a byte;
+//   qp_unpermute         one workgroup per tile stages the tile's answer bits
 //                        in LDS and writes out[i] = answer[perm[i]] in input
 //                        order.
 // A query whose key lies past the bitmap's last bucket (sorted into the tile
 // sort's sentinel run) answers `negated`, as contains() does for key > max_key.
+
+// Answer-bit layout of a tile (see qp_answer): bucket b's run starting at
+// sorted position S is answered from bit qp_pstart(S, b); a tile's bits take
+// qp_abytes(NB) bytes (16-byte multiple), at most QA_MAX_ABYTES.
+__host__ __device__ inline uint32_t qp_pstart(uint32_t s, uint32_t b) { return (s + 7u * b + 7u) & ~7u; }
+__host__ __device__ inline uint32_t qp_abytes(uint32_t nb)
+{
+    return ((TILE + 7u * nb + 7u + 7u) / 8u + 15u) & ~15u;  // the sentinel run ends below TILE + 7 NB + 7
+}
+constexpr uint32_t QA_MAX_ABYTES = ((TILE + 7u * MAX_BUCKETS + 14u) / 8u + 15u) & ~15u;
+constexpr uint32_t QA_LONG = 64;    // groups of 8 answers above which a run is shared by the workgroup
+constexpr uint32_t QA_QCAP = 2048;  // long runs queued per workgroup (16 KiB of LDS)
 
 // One wave fills `w` (2048 words) with key's container as a bitmap -- zeros
 // when the key is absent -- found by contains()'s own lookup rules.
@@ -301,15 +314,25 @@ __device__ void qp_load_container(const GpuRoaringView& v, uint32_t key, uint32_
     }
 }
 
+// The answers of a tile are bits at *padded* positions: bucket b's run of the
+// tile, sorted positions [S, S + C), is answered at [P, P + C) with
+// P = qp_pstart(S, b), a multiple of 8, and the bits up to the next bucket's
+// start belong to b as well.  So a lane that answers 8 consecutive fields of
+// one run writes one whole byte that no other lane writes (no partial stores,
+// one store per 8 queries).  ids_tile_sort<true> records each query's padded
+// position in perm.
 __global__ __launch_bounds__(BUILD_NT) void qp_answer(const uint32_t* __restrict__ part,
                                                       const uint16_t* __restrict__ tab, IdsGeom g, GpuRoaringView v,
                                                       uint8_t* __restrict__ ans)
 {
     __shared__ alignas(16) uint32_t bits[BK_KEYS * 2048u];  // the bucket's 16 containers, 128 KiB
+    __shared__ uint2 q_ent[QA_QCAP];                        // long runs: {tile, S | E << 16}
+    __shared__ uint32_t q_n;
     const uint32_t t = threadIdx.x;
     const uint32_t b = (blockIdx.x % 8) * build_per_xcd(g.NB) + blockIdx.x / 8;
     if (b >= g.NB) return;
     const uint32_t wave = t >> 6, lane = __lane_id();
+    if (t == 0) q_n = 0;
     const uint32_t key = b * BK_KEYS + wave;
     if (key < g.K) {
         qp_load_container(v, key, bits + wave * 2048u, lane);
@@ -319,46 +342,140 @@ __global__ __launch_bounds__(BUILD_NT) void qp_answer(const uint32_t* __restrict
         for (int j = 0; j < 8; ++j) w4[lane + 64 * j] = make_uint4(0, 0, 0, 0);
     }
     __syncthreads();
-    const uint32_t neg = v.negated ? 1u : 0u;
-    // A lane's consecutive fields give consecutive answer bytes: written with
-    // at most three naturally aligned stores (byte, short, dword) instead of a
-    // byte store each.
-    walk_bucket<true>(part, tab, g, b, wave, lane, [&](uint32_t tile, uint32_t i, uint32_t n, const uint32_t* f) {
-        uint64_t v = 0;
+    const uint32_t flip = v.negated ? 0xFFu : 0u;
+    const uint32_t abytes = qp_abytes(g.NB);
+    // Fields [S + 8 j, S + 8 j + 8) of the tile: 160 bits, which start o bits
+    // into word w0; load() fetches the 6 words from w0 (as 4 aligned word
+    // pairs), answer() turns them into one byte.  Fields past the run answer
+    // into b's padding; any 20-bit value indexes the LDS image.
+    struct Grp {
+        uint32_t x[6];
+        uint32_t o;
+    };
+    auto load = [&](uint32_t tile, uint32_t S, uint32_t j, Grp& q) {
+        const uint32_t bit = FIELD_BITS * (S + 8u * j);
+        const uint32_t w0 = bit >> 5;
+        q.o = bit & 31u;
+        const uint2* src = reinterpret_cast<const uint2*>(part + static_cast<uint64_t>(tile) * TILE_WORDS + (w0 & ~1u));
+        const uint2 p0 = src[0], p1 = src[1], p2 = src[2], p3 = src[3];
+        const bool odd = (w0 & 1u) != 0u;
+        q.x[0] = odd ? p0.y : p0.x, q.x[1] = odd ? p1.x : p0.y, q.x[2] = odd ? p1.y : p1.x;
+        q.x[3] = odd ? p2.x : p1.y, q.x[4] = odd ? p2.y : p2.x, q.x[5] = odd ? p3.x : p2.y;
+    };
+    auto answer = [&](uint32_t tile, uint32_t S, uint32_t j, const Grp& q) {
+        static_assert(FIELD_BITS == 20, "8 fields = 5 words");
+        const uint32_t d0 = __builtin_amdgcn_alignbit(q.x[1], q.x[0], q.o);
+        const uint32_t d1 = __builtin_amdgcn_alignbit(q.x[2], q.x[1], q.o);
+        const uint32_t d2 = __builtin_amdgcn_alignbit(q.x[3], q.x[2], q.o);
+        const uint32_t d3 = __builtin_amdgcn_alignbit(q.x[4], q.x[3], q.o);
+        const uint32_t d4 = __builtin_amdgcn_alignbit(q.x[5], q.x[4], q.o);
+        const uint32_t f[8] = {d0,
+                               __builtin_amdgcn_alignbit(d1, d0, 20),
+                               d1 >> 8,
+                               __builtin_amdgcn_alignbit(d2, d1, 28),
+                               __builtin_amdgcn_alignbit(d3, d2, 16),
+                               d3 >> 4,
+                               __builtin_amdgcn_alignbit(d4, d3, 24),
+                               d4 >> 12};
+        uint32_t a = 0;
 #pragma unroll
-        for (uint32_t m = 0; m < 7u; ++m) {
-            const uint32_t F = f[m] & FIELD_MASK;
-            const uint64_t a = ((bits[F >> 5] >> (F & 31u)) & 1u) ^ neg;
-            v |= m < n ? a << (8u * m) : 0ull;
+        for (uint32_t k = 0; k < 8u; ++k) {
+            const uint32_t F = f[k] & FIELD_MASK;
+            a |= ((bits[F >> 5] >> (F & 31u)) & 1u) << k;
         }
-        uint8_t* p = ans + static_cast<uint64_t>(tile) * TILE + i;
-        uint32_t left = n;
-        if (reinterpret_cast<uintptr_t>(p) & 1u) {
-            *p = static_cast<uint8_t>(v);
-            v >>= 8;
-            ++p;
-            --left;
+        ans[static_cast<uint64_t>(tile) * abytes + (qp_pstart(S, b) >> 3) + j] = static_cast<uint8_t>(a ^ flip);
+    };
+    auto group = [&](uint32_t tile, uint32_t S, uint32_t j) {
+        Grp q;
+        load(tile, S, j, q);
+        answer(tile, S, j, q);
+    };
+    // Wave w owns tile blocks w, w + 16, ...; a step covers 64 / TB of them,
+    // one tile per lane, whose run bounds are loaded a step ahead.  The step's
+    // groups are numbered across the wave (an exclusive scan of the lanes'
+    // group counts) and dealt to the lanes in rounds of 64, so neighbouring
+    // lanes answer neighbouring groups of one run and their loads share cache
+    // lines; four rounds are loaded before any is answered.  A run of more
+    // than QA_LONG groups is queued for the whole workgroup instead (or, with
+    // the queue full, dealt with the rest).
+    constexpr uint32_t BPS = 64u / TB;
+    const uint32_t n_blk = (g.n_tiles + TB - 1) / TB;
+    const uint32_t per_wave = n_blk > wave ? (n_blk - wave + BUILD_WAVES - 1) / BUILD_WAVES : 0u;
+    auto tile_of = [&](uint32_t st, uint32_t l) { return (wave + BUILD_WAVES * (st * BPS + l / TB)) * TB + l % TB; };
+    auto tab_load = [&](uint32_t st, uint32_t& r0, uint32_t& r1) {
+        r0 = r1 = 0;
+        const uint32_t jb = st * BPS + lane / TB;
+        if (jb < per_wave && tile_of(st, lane) < g.n_tiles) {
+            const uint16_t* tc =
+                tab + (static_cast<uint64_t>(wave + BUILD_WAVES * jb) * (g.NB + 1) + b) * TB + lane % TB;
+            r0 = tc[0];
+            r1 = tc[TB];
         }
-        if (left >= 2u && (reinterpret_cast<uintptr_t>(p) & 2u)) {
-            *reinterpret_cast<uint16_t*>(p) = static_cast<uint16_t>(v);
-            v >>= 16;
-            p += 2;
-            left -= 2u;
+    };
+    uint32_t n0, n1;
+    tab_load(0, n0, n1);
+    for (uint32_t st = 0; st * BPS < per_wave; ++st) {
+        const uint32_t S = n0, E = n1;
+        tab_load(st + 1, n0, n1);
+        uint32_t G = (E - S + 7u) / 8u;  // E >= S
+        if (G > QA_LONG) {
+            const uint32_t slot = atomicAdd(&q_n, 1u);
+            if (slot < QA_QCAP) {
+                q_ent[slot] = make_uint2(tile_of(st, lane), S | (E << 16));
+                G = 0;
+            }
         }
-        if (left >= 4u) {
-            *reinterpret_cast<uint32_t*>(p) = static_cast<uint32_t>(v);
-            v >>= 32;
-            p += 4;
-            left -= 4u;
+        // exclusive scan of G over the wave
+        uint32_t P = G;
+#pragma unroll
+        for (uint32_t d = 1; d < 64u; d <<= 1) {
+            const uint32_t y = __shfl_up(P, d, 64);
+            if (lane >= d) P += y;
         }
-        if (left >= 2u) {
-            *reinterpret_cast<uint16_t*>(p) = static_cast<uint16_t>(v);
-            v >>= 16;
-            p += 2;
-            left -= 2u;
+        const uint32_t T = static_cast<uint32_t>(__shfl(P, 63, 64));
+        P -= G;
+        for (uint32_t r0 = 0; 64u * r0 < T; r0 += 4u) {
+            Grp q[4];
+            uint32_t tl[4], ss[4], jj[4];
+            bool ok[4];
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; ++k) {
+                const uint32_t u = 64u * (r0 + k) + lane;
+                // the last lane whose first group is <= u holds group u
+                uint32_t l = 0;
+#pragma unroll
+                for (uint32_t step = 32; step > 0; step >>= 1) {
+                    const uint32_t c = l + step;
+                    const uint32_t pc = static_cast<uint32_t>(__shfl(P, static_cast<int>(c & 63u), 64));
+                    if (c < 64u && pc <= u) l = c;
+                }
+                ok[k] = u < T;
+                ss[k] = static_cast<uint32_t>(__shfl(S, static_cast<int>(l), 64));
+                jj[k] = u - static_cast<uint32_t>(__shfl(P, static_cast<int>(l), 64));
+                tl[k] = tile_of(st, l);
+                if (ok[k]) load(tl[k], ss[k], jj[k], q[k]);
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; ++k)
+                if (ok[k]) answer(tl[k], ss[k], jj[k], q[k]);
         }
-        if (left) *p = static_cast<uint8_t>(v);
-    });
+    }
+    // The queued runs: their groups in chunks of 64 (one a lane), the chunks of
+    // all runs dealt to the waves in turn.
+    __syncthreads();
+    const uint32_t nq = min(q_n, QA_QCAP);
+    uint32_t off = 0;
+    for (uint32_t i = 0; i < nq; ++i) {
+        const uint2 ent = q_ent[i];
+        const uint32_t S = ent.y & 0xFFFFu, E = ent.y >> 16;
+        const uint32_t G = (E - S + 7u) / 8u;
+        const uint32_t nch = (G + 63u) / 64u;
+        for (uint32_t c = (wave + BUILD_WAVES - off % BUILD_WAVES) % BUILD_WAVES; c < nch; c += BUILD_WAVES) {
+            const uint32_t j = 64u * c + lane;
+            if (j < G) group(ent.x, S, j);
+        }
+        off += nch;
+    }
 }
 
 constexpr int QU_NT = 1024;
@@ -368,16 +485,17 @@ __global__ __launch_bounds__(QU_NT) void qp_unpermute(const uint16_t* __restrict
                                                       const uint16_t* __restrict__ tab, IdsGeom g, uint32_t neg,
                                                       uint32_t* __restrict__ out)
 {
-    __shared__ alignas(16) uint8_t a[TILE];
+    __shared__ alignas(16) uint8_t a[QA_MAX_ABYTES];
     const uint32_t tile = blockIdx.x, t = threadIdx.x;
     const uint64_t base = static_cast<uint64_t>(tile) * TILE;
-    // queries of the real buckets; the sentinel run (keys past the last bucket) follows
+    const uint32_t abytes = qp_abytes(g.NB);
+    // queries of the real buckets sit below the sentinel run's padded start
     const uint32_t in_range =
-        tab[(static_cast<uint64_t>(tile / TB) * (g.NB + 1) + g.NB) * TB + tile % TB];
-    const uint4* a_src = reinterpret_cast<const uint4*>(ans + base);
-    for (uint32_t u = t; u < TILE / 16u; u += QU_NT) reinterpret_cast<uint4*>(a)[u] = ld_stream(a_src + u);
+        qp_pstart(tab[(static_cast<uint64_t>(tile / TB) * (g.NB + 1) + g.NB) * TB + tile % TB], g.NB);
+    const uint4* a_src = reinterpret_cast<const uint4*>(ans + static_cast<uint64_t>(tile) * abytes);
+    for (uint32_t u = t; u < abytes / 16u; u += QU_NT) reinterpret_cast<uint4*>(a)[u] = ld_stream(a_src + u);
     __syncthreads();
-    auto answer = [&](uint32_t sp) { return sp < in_range ? static_cast<uint32_t>(a[sp]) : neg; };
+    auto answer = [&](uint32_t pp) { return pp < in_range ? (static_cast<uint32_t>(a[pp >> 3]) >> (pp & 7u)) & 1u : neg; };
     if (base + TILE <= g.n && (reinterpret_cast<uintptr_t>(out) & 15u) == 0) {
         // four queries a thread: 8-byte perm loads, 16-byte answer stores
         const uint2* p2 = reinterpret_cast<const uint2*>(perm + base);
@@ -410,10 +528,11 @@ int contains_partitioned(const GpuRoaringView& v, const uint32_t* d_ids, uint64_
     g.G = std::max<uint32_t>(1, std::min<uint32_t>(num_cus(), (g.n_tiles + TB - 1) / TB));
     g.vec = (reinterpret_cast<uintptr_t>(d_ids) & 15u) == 0;
     Carver c;
-    const size_t o_part = c.add(sizeof(uint32_t) * (static_cast<uint64_t>(g.n_tiles) * TILE_WORDS + 4));
+    // qp_answer reads up to 7 words past a field group's first: slack past the last tile
+    const size_t o_part = c.add(sizeof(uint32_t) * (static_cast<uint64_t>(g.n_tiles) * TILE_WORDS + 8));
     const size_t o_tab = c.add(sizeof(uint16_t) * static_cast<uint64_t>((g.n_tiles + TB - 1) / TB) * TB * (g.NB + 1));
     const size_t o_perm = c.add(sizeof(uint16_t) * static_cast<uint64_t>(g.n_tiles) * TILE);
-    const size_t o_ans = c.add(static_cast<uint64_t>(g.n_tiles) * TILE);
+    const size_t o_ans = c.add(static_cast<uint64_t>(g.n_tiles) * qp_abytes(g.NB));
     const size_t o_gmax = c.add(sizeof(uint32_t) * g.G);
     const size_t o_tot = c.add(sizeof(IdsTotals));
     Scratch sc;

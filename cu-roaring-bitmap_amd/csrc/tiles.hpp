@@ -61,8 +61,11 @@ struct IdsGeom {
 // others and neither written nor built; the error is raised from the maximum
 // id, which each workgroup reports.  Every lane holds an id: a partial last
 // tile is padded with ids of the sentinel bucket (which do not enter the
-// maximum).  With PERM, perm[t * TILE + p] receives the sorted position (within
-// tile t) of the tile's p-th id, padding included.
+// maximum).  With PERM, perm[t * TILE + p] receives the padded sorted position
+// (within tile t) of the tile's p-th id, padding ids included: rank r in
+// bucket b, whose run starts at sorted position S, gets ((S + 7 b + 7) & ~7) + r,
+// so every bucket's positions start at a multiple of 8 and no two buckets'
+// positions share a group of 8.
 template <bool PERM>
 __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restrict__ ids, IdsGeom g,
                                                        uint32_t* __restrict__ part, uint16_t* __restrict__ tab,
@@ -214,13 +217,14 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         for (uint32_t q = 0; q < BPT; ++q) {
             const uint32_t bq = t * BPT + q;
             if (bq < NB) {
-                cnt[bq] = st;
+                // with PERM the padded start rides in the high half
+                cnt[bq] = PERM ? st | (((st + 7u * bq + 7u) & ~7u) << 16) : st;
                 trow_col[static_cast<uint64_t>(bq) * TB] = static_cast<uint16_t>(st);
             }
             st += cv[q];
         }
         if (t == 0) {
-            cnt[NB] = total;
+            cnt[NB] = PERM ? total | (((total + 7u * NB + 7u) & ~7u) << 16) : total;
             trow_col[static_cast<uint64_t>(NB) * TB] = static_cast<uint16_t>(total);
         }
         __syncthreads();
@@ -230,10 +234,17 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
             // An empty asm hides x's origin, so the bucket address is computed
             // again here instead of being kept in registers since the ranking.
             asm volatile("" : "+v"(x));
-            const uint32_t sp = cnt[bucket(x)] + ((rk[j >> 1] >> ((j & 1u) * 16)) & 0xFFFFu);
-            buf[sp] = x;
-            if constexpr (PERM)  // the rank's half of rk now holds the sorted position
-                rk[j >> 1] = (j & 1u) ? ((rk[j >> 1] & 0xFFFFu) | (sp << 16)) : ((rk[j >> 1] & 0xFFFF0000u) | sp);
+            const uint32_t c = cnt[bucket(x)];
+            const uint32_t r = (rk[j >> 1] >> ((j & 1u) * 16)) & 0xFFFFu;
+            buf[(PERM ? c & 0xFFFFu : c) + r] = x;
+            if constexpr (PERM) {
+                // the rank's half of rk now holds the padded sorted position:
+                // bucket b's run starts at (start + 7 b) rounded up to a
+                // multiple of 8, so each bucket's answers fill whole bytes
+                // (< 24576 + 7 * 4096 + 7, fits 16 bits)
+                const uint32_t pp = (c >> 16) + r;
+                rk[j >> 1] = (j & 1u) ? ((rk[j >> 1] & 0xFFFFu) | (pp << 16)) : ((rk[j >> 1] & 0xFFFF0000u) | pp);
+            }
         }
         if constexpr (PERM) {  // the ids' sorted positions, in the order load_ids placed them
             uint16_t* pt = perm + static_cast<uint64_t>(tile) * TILE;
@@ -318,9 +329,6 @@ inline uint32_t build_grid(uint32_t nb) { return 8 * build_per_xcd(nb); }
 // (key-in-bucket << 16 | low 16 bits).  Every thread of the BUILD_NT-thread
 // workgroup calls it (wave = t >> 6, lane = its lane); fields arrive in no
 // particular order and each exactly once.
-// With CHUNKS the callback is on_chunk(tile, i, n, f): the n (1..7) fields
-// i .. i + n - 1 that start in one lane's 4 words, f[0 .. n) (unmasked), so
-// a consumer can handle a lane's consecutive fields together.
 // Runs longer than two windows (clustered or sorted ids) are queued in LDS
 // and their remaining windows shared by the whole workgroup after the walk,
 // so that a bucket whose ids sit in a few tiles -- one wave's blocks -- keeps
@@ -328,7 +336,7 @@ inline uint32_t build_grid(uint32_t nb) { return 8 * build_per_xcd(nb); }
 // own wave).  Every thread of the workgroup must call this.
 constexpr uint32_t WALK_QCAP = 2048;  // 16 KiB of LDS beside the callers' 128 KiB
 
-template <bool CHUNKS = false, class OnField>
+template <class OnField>
 __device__ __forceinline__ void walk_bucket(const uint32_t* __restrict__ part, const uint16_t* __restrict__ tab,
                                             const IdsGeom& g, uint32_t b, uint32_t wave, uint32_t lane,
                                             OnField on_field)
@@ -382,22 +390,10 @@ __device__ __forceinline__ void walk_bucket(const uint32_t* __restrict__ part, c
                                __builtin_amdgcn_alignbit(d3, d2, 16),
                                d3 >> 4,
                                __builtin_amdgcn_alignbit(d4, d3, 24)};
-        if constexpr (CHUNKS) {
-            // fields m in [lo, hi): inside the run [s0, s1) and starting in these 4 words
-            const uint32_t lo = s0 > i0 ? min(s0 - i0, 7u) : 0u;
-            const uint32_t hi = min(s1 > i0 ? s1 - i0 : 0u, o < 8u ? 7u : 6u);
-            if (hi > lo) {
-                uint32_t fs[7];
 #pragma unroll
-                for (uint32_t m = 0; m < 7u; ++m) fs[m] = f[(m + lo) < 7u ? m + lo : 6u];
-                on_field(tile, i0 + lo, hi - lo, fs);
-            }
-        } else {
-#pragma unroll
-            for (uint32_t m = 0; m < 7u; ++m) {
-                const uint32_t i = i0 + m;
-                if (i >= s0 && i < s1 && (m < 6u || o < 8u)) on_field(tile, i, f[m] & FIELD_MASK);
-            }
+        for (uint32_t m = 0; m < 7u; ++m) {
+            const uint32_t i = i0 + m;
+            if (i >= s0 && i < s1 && (m < 6u || o < 8u)) on_field(tile, i, f[m] & FIELD_MASK);
         }
     };
     uint32_t n0, n1;
