@@ -329,12 +329,14 @@ inline uint32_t build_grid(uint32_t nb) { return 8 * build_per_xcd(nb); }
 // (key-in-bucket << 16 | low 16 bits).  Every thread of the BUILD_NT-thread
 // workgroup calls it (wave = t >> 6, lane = its lane); fields arrive in no
 // particular order and each exactly once.
-// Runs longer than two windows (clustered or sorted ids) are queued in LDS
-// and their remaining windows shared by the whole workgroup after the walk,
-// so that a bucket whose ids sit in a few tiles -- one wave's blocks -- keeps
-// all sixteen waves busy (a run that finds the queue full is finished by its
-// own wave).  Every thread of the workgroup must call this.
+// Runs longer than WALK_LONG windows (sorted or clustered ids) are queued in
+// LDS and their remaining windows shared by the whole workgroup after the
+// walk, so that a bucket whose ids sit in a few tiles -- one wave's blocks --
+// keeps all sixteen waves busy (a run that finds the queue full is finished by
+// its own wave); shorter runs stay with their own groups.  Every thread of the
+// workgroup must call this.
 constexpr uint32_t WALK_QCAP = 2048;  // 16 KiB of LDS beside the callers' 128 KiB
+constexpr uint32_t WALK_LONG = 16;    // windows above which a run is queued (one window a group)
 
 template <class OnField>
 __device__ __forceinline__ void walk_bucket(const uint32_t* __restrict__ part, const uint16_t* __restrict__ tab,
@@ -440,10 +442,30 @@ __device__ __forceinline__ void walk_bucket(const uint32_t* __restrict__ part, c
                     set_chunk(x[h][k], r4 == 3u ? e[h][k] : nx, wb[h] + 16u * k + 4u * r4, ts0[h], ts1[h], tl[h]);
                 }
         }
-        // Runs longer than two windows: queued for the workgroup; one that
-        // finds the queue full is finished here, one tile at a time, its
-        // remaining windows shared by the wave's sixteen groups.
-        const bool is_long = own_nw > 2u;
+        // Runs of 3 .. WALK_LONG windows: the rest of their windows by their
+        // own groups, all of the wave's runs together (the loop runs to the
+        // wave's longest such run).
+        uint32_t nw_mid = own_nw <= WALK_LONG ? own_nw : 0u;
+#pragma unroll
+        for (int d = 32; d > 0; d >>= 1) nw_mid = max(nw_mid, static_cast<uint32_t>(__shfl_xor(nw_mid, d, 64)));
+        bool mid[4];
+#pragma unroll
+        for (uint32_t h = 0; h < 4u; ++h)
+            mid[h] = static_cast<uint32_t>(__shfl(own_nw, static_cast<int>(16u * h + grp), 64)) <= WALK_LONG;
+        for (uint32_t k = 2; k < nw_mid; ++k) {
+#pragma unroll
+            for (uint32_t h = 0; h < 4u; ++h) {
+                uint4 x = make_uint4(0, 0, 0, 0);
+                uint32_t e = 0;
+                if (mid[h]) window(h, k, x, e);
+                const uint32_t nx = __shfl_down(x.x, 1, 64);
+                if (mid[h]) set_chunk(x, r4 == 3u ? e : nx, wb[h] + 16u * k + 4u * r4, ts0[h], ts1[h], tl[h]);
+            }
+        }
+        // Longer runs: queued for the workgroup; one that finds the queue full
+        // is finished here, one tile at a time, its remaining windows shared
+        // by the wave's sixteen groups.
+        const bool is_long = own_nw > WALK_LONG;
         uint32_t slot = WALK_QCAP;
         if (is_long) slot = atomicAdd(&q_n, 1u);
         if (is_long && slot < WALK_QCAP) q_ent[slot] = make_uint2(tile_of(st, lane), m0 | (m1 << 16));
