@@ -64,8 +64,9 @@ extern "C" {
  * 16-key bucket on the device, each bucket's containers are loaded once into
  * LDS and its queries answered there, and the answers are written back in
  * input order.  Fastest for many uniform queries over a large bitmap (one
- * random memory request per query otherwise); it allocates scratch of about
- * 5.5 bytes per query from the library's pool, stream-ordered. */
+ * random memory request per query otherwise; sorted or clustered batches
+ * are faster in modes 0/1); it allocates scratch of about 4.8 bytes per query
+ * from the library's pool, stream-ordered. */
 #define CR_QUERY_PARTITIONED 4
 
 /*

@@ -157,8 +157,9 @@ def test_multi_and_full_size(gpu, torch):
 
 
 def test_contains_full_size(gpu, torch):
-    """100M uniform queries against the headline bitmap: the answer is the
-    bit of the independently built bitset."""
+    """100M uniform queries against the headline bitmap, in the batched,
+    wavefront and partitioned modes: the answer is the bit of the
+    independently built bitset."""
     _say("contains full size")
     d_ids = bench.make_ids(torch)
     want, _ = _bitset_of_ids(torch, d_ids)
@@ -170,7 +171,7 @@ def test_contains_full_size(gpu, torch):
     out = torch.empty(q.numel(), device="cuda", dtype=torch.int32)
     qi = q.to(torch.int32)
     del q
-    for mode in (gpu.QUERY_CONTAINS, gpu.QUERY_WAVEFRONT):
+    for mode in (gpu.QUERY_CONTAINS, gpu.QUERY_WAVEFRONT, gpu.QUERY_PARTITIONED):
         out.fill_(7)
         gpu.contains_batch(g, qi, out, mode)
         torch.cuda.synchronize()
