@@ -238,8 +238,6 @@ __host__ __device__ inline uint32_t qp_abytes(uint32_t nb)
     return ((TILE + 7u * nb + 7u + 7u) / 8u + 15u) & ~15u;  // the sentinel run ends below TILE + 7 NB + 7
 }
 constexpr uint32_t QA_MAX_ABYTES = ((TILE + 7u * MAX_BUCKETS + 14u) / 8u + 15u) & ~15u;
-constexpr uint32_t QA_LONG = 64;    // groups of 8 answers above which a run is shared by the workgroup
-constexpr uint32_t QA_QCAP = 2048;  // long runs queued per workgroup (16 KiB of LDS)
 
 // One wave fills `w` (2048 words) with key's container as a bitmap -- zeros
 // when the key is absent -- found by contains()'s own lookup rules.
@@ -326,13 +324,10 @@ __global__ __launch_bounds__(BUILD_NT) void qp_answer(const uint32_t* __restrict
                                                       uint8_t* __restrict__ ans)
 {
     __shared__ alignas(16) uint32_t bits[BK_KEYS * 2048u];  // the bucket's 16 containers, 128 KiB
-    __shared__ uint2 q_ent[QA_QCAP];                        // long runs: {tile, S | E << 16}
-    __shared__ uint32_t q_n;
     const uint32_t t = threadIdx.x;
     const uint32_t b = (blockIdx.x % 8) * build_per_xcd(g.NB) + blockIdx.x / 8;
     if (b >= g.NB) return;
     const uint32_t wave = t >> 6, lane = __lane_id();
-    if (t == 0) q_n = 0;
     const uint32_t key = b * BK_KEYS + wave;
     if (key < g.K) {
         qp_load_container(v, key, bits + wave * 2048u, lane);
@@ -341,141 +336,23 @@ __global__ __launch_bounds__(BUILD_NT) void qp_answer(const uint32_t* __restrict
 #pragma unroll
         for (int j = 0; j < 8; ++j) w4[lane + 64 * j] = make_uint4(0, 0, 0, 0);
     }
-    __syncthreads();
+    // (walk_groups' first barrier publishes the image)
     const uint32_t flip = v.negated ? 0xFFu : 0u;
     const uint32_t abytes = qp_abytes(g.NB);
-    // Fields [S + 8 j, S + 8 j + 8) of the tile: 160 bits, which start o bits
-    // into word w0; load() fetches the 6 words from w0 (as 4 aligned word
-    // pairs), answer() turns them into one byte.  Fields past the run answer
-    // into b's padding; any 20-bit value indexes the LDS image.
-    struct Grp {
-        uint32_t x[6];
-        uint32_t o;
-    };
-    auto load = [&](uint32_t tile, uint32_t S, uint32_t j, Grp& q) {
-        const uint32_t bit = FIELD_BITS * (S + 8u * j);
-        const uint32_t w0 = bit >> 5;
-        q.o = bit & 31u;
-        const uint2* src = reinterpret_cast<const uint2*>(part + static_cast<uint64_t>(tile) * TILE_WORDS + (w0 & ~1u));
-        const uint2 p0 = src[0], p1 = src[1], p2 = src[2], p3 = src[3];
-        const bool odd = (w0 & 1u) != 0u;
-        q.x[0] = odd ? p0.y : p0.x, q.x[1] = odd ? p1.x : p0.y, q.x[2] = odd ? p1.y : p1.x;
-        q.x[3] = odd ? p2.x : p1.y, q.x[4] = odd ? p2.y : p2.x, q.x[5] = odd ? p3.x : p2.y;
-    };
-    auto answer = [&](uint32_t tile, uint32_t S, uint32_t j, const Grp& q) {
-        static_assert(FIELD_BITS == 20, "8 fields = 5 words");
-        const uint32_t d0 = __builtin_amdgcn_alignbit(q.x[1], q.x[0], q.o);
-        const uint32_t d1 = __builtin_amdgcn_alignbit(q.x[2], q.x[1], q.o);
-        const uint32_t d2 = __builtin_amdgcn_alignbit(q.x[3], q.x[2], q.o);
-        const uint32_t d3 = __builtin_amdgcn_alignbit(q.x[4], q.x[3], q.o);
-        const uint32_t d4 = __builtin_amdgcn_alignbit(q.x[5], q.x[4], q.o);
-        const uint32_t f[8] = {d0,
-                               __builtin_amdgcn_alignbit(d1, d0, 20),
-                               d1 >> 8,
-                               __builtin_amdgcn_alignbit(d2, d1, 28),
-                               __builtin_amdgcn_alignbit(d3, d2, 16),
-                               d3 >> 4,
-                               __builtin_amdgcn_alignbit(d4, d3, 24),
-                               d4 >> 12};
-        uint32_t a = 0;
+    // All 8 answers of a group go into one byte that only this lane writes:
+    // fields past the run answer into b's padding, and any 20-bit value
+    // indexes the LDS image.
+    walk_groups(part, tab, g, b, wave, lane,
+                [&](uint32_t tile, uint32_t S, uint32_t j, uint32_t, const uint32_t (&f)[8]) {
+                    uint32_t a = 0;
 #pragma unroll
-        for (uint32_t k = 0; k < 8u; ++k) {
-            const uint32_t F = f[k] & FIELD_MASK;
-            a |= ((bits[F >> 5] >> (F & 31u)) & 1u) << k;
-        }
-        ans[static_cast<uint64_t>(tile) * abytes + (qp_pstart(S, b) >> 3) + j] = static_cast<uint8_t>(a ^ flip);
-    };
-    auto group = [&](uint32_t tile, uint32_t S, uint32_t j) {
-        Grp q;
-        load(tile, S, j, q);
-        answer(tile, S, j, q);
-    };
-    // Wave w owns tile blocks w, w + 16, ...; a step covers 64 / TB of them,
-    // one tile per lane, whose run bounds are loaded a step ahead.  The step's
-    // groups are numbered across the wave (an exclusive scan of the lanes'
-    // group counts) and dealt to the lanes in rounds of 64, so neighbouring
-    // lanes answer neighbouring groups of one run and their loads share cache
-    // lines; four rounds are loaded before any is answered.  A run of more
-    // than QA_LONG groups is queued for the whole workgroup instead (or, with
-    // the queue full, dealt with the rest).
-    constexpr uint32_t BPS = 64u / TB;
-    const uint32_t n_blk = (g.n_tiles + TB - 1) / TB;
-    const uint32_t per_wave = n_blk > wave ? (n_blk - wave + BUILD_WAVES - 1) / BUILD_WAVES : 0u;
-    auto tile_of = [&](uint32_t st, uint32_t l) { return (wave + BUILD_WAVES * (st * BPS + l / TB)) * TB + l % TB; };
-    auto tab_load = [&](uint32_t st, uint32_t& r0, uint32_t& r1) {
-        r0 = r1 = 0;
-        const uint32_t jb = st * BPS + lane / TB;
-        if (jb < per_wave && tile_of(st, lane) < g.n_tiles) {
-            const uint16_t* tc =
-                tab + (static_cast<uint64_t>(wave + BUILD_WAVES * jb) * (g.NB + 1) + b) * TB + lane % TB;
-            r0 = tc[0];
-            r1 = tc[TB];
-        }
-    };
-    uint32_t n0, n1;
-    tab_load(0, n0, n1);
-    for (uint32_t st = 0; st * BPS < per_wave; ++st) {
-        const uint32_t S = n0, E = n1;
-        tab_load(st + 1, n0, n1);
-        uint32_t G = (E - S + 7u) / 8u;  // E >= S
-        if (G > QA_LONG) {
-            const uint32_t slot = atomicAdd(&q_n, 1u);
-            if (slot < QA_QCAP) {
-                q_ent[slot] = make_uint2(tile_of(st, lane), S | (E << 16));
-                G = 0;
-            }
-        }
-        // exclusive scan of G over the wave
-        uint32_t P = G;
-#pragma unroll
-        for (uint32_t d = 1; d < 64u; d <<= 1) {
-            const uint32_t y = __shfl_up(P, d, 64);
-            if (lane >= d) P += y;
-        }
-        const uint32_t T = static_cast<uint32_t>(__shfl(P, 63, 64));
-        P -= G;
-        for (uint32_t r0 = 0; 64u * r0 < T; r0 += 4u) {
-            Grp q[4];
-            uint32_t tl[4], ss[4], jj[4];
-            bool ok[4];
-#pragma unroll
-            for (uint32_t k = 0; k < 4u; ++k) {
-                const uint32_t u = 64u * (r0 + k) + lane;
-                // the last lane whose first group is <= u holds group u
-                uint32_t l = 0;
-#pragma unroll
-                for (uint32_t step = 32; step > 0; step >>= 1) {
-                    const uint32_t c = l + step;
-                    const uint32_t pc = static_cast<uint32_t>(__shfl(P, static_cast<int>(c & 63u), 64));
-                    if (c < 64u && pc <= u) l = c;
-                }
-                ok[k] = u < T;
-                ss[k] = static_cast<uint32_t>(__shfl(S, static_cast<int>(l), 64));
-                jj[k] = u - static_cast<uint32_t>(__shfl(P, static_cast<int>(l), 64));
-                tl[k] = tile_of(st, l);
-                if (ok[k]) load(tl[k], ss[k], jj[k], q[k]);
-            }
-#pragma unroll
-            for (uint32_t k = 0; k < 4u; ++k)
-                if (ok[k]) answer(tl[k], ss[k], jj[k], q[k]);
-        }
-    }
-    // The queued runs: their groups in chunks of 64 (one a lane), the chunks of
-    // all runs dealt to the waves in turn.
-    __syncthreads();
-    const uint32_t nq = min(q_n, QA_QCAP);
-    uint32_t off = 0;
-    for (uint32_t i = 0; i < nq; ++i) {
-        const uint2 ent = q_ent[i];
-        const uint32_t S = ent.y & 0xFFFFu, E = ent.y >> 16;
-        const uint32_t G = (E - S + 7u) / 8u;
-        const uint32_t nch = (G + 63u) / 64u;
-        for (uint32_t c = (wave + BUILD_WAVES - off % BUILD_WAVES) % BUILD_WAVES; c < nch; c += BUILD_WAVES) {
-            const uint32_t j = 64u * c + lane;
-            if (j < G) group(ent.x, S, j);
-        }
-        off += nch;
-    }
+                    for (uint32_t k = 0; k < 8u; ++k) {
+                        const uint32_t F = f[k] & FIELD_MASK;
+                        a |= ((bits[F >> 5] >> (F & 31u)) & 1u) << k;
+                    }
+                    ans[static_cast<uint64_t>(tile) * abytes + (qp_pstart(S, b) >> 3) + j] =
+                        static_cast<uint8_t>(a ^ flip);
+                });
 }
 
 constexpr int QU_NT = 1024;

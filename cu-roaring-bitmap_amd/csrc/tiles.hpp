@@ -324,191 +324,184 @@ constexpr uint32_t BUILD_WAVES = BUILD_NT / 64;
 __host__ __device__ inline uint32_t build_per_xcd(uint32_t nb) { return (nb + 7) / 8; }
 inline uint32_t build_grid(uint32_t nb) { return 8 * build_per_xcd(nb); }
 
-// Calls on_field(tile, i, F) for every field of bucket b's run in every tile:
-// field i of tile `tile`'s sorted order, F = the id's low FIELD_BITS bits
-// (key-in-bucket << 16 | low 16 bits).  Every thread of the BUILD_NT-thread
-// workgroup calls it (wave = t >> 6, lane = its lane); fields arrive in no
-// particular order and each exactly once.
-// Runs longer than WALK_LONG windows (sorted or clustered ids) are queued in
-// LDS and their remaining windows shared by the whole workgroup after the
-// walk, so that a bucket whose ids sit in a few tiles -- one wave's blocks --
-// keeps all sixteen waves busy (a run that finds the queue full is finished by
-// its own wave); shorter runs stay with their own groups.  Every thread of the
-// workgroup must call this.
-constexpr uint32_t WALK_QCAP = 2048;  // 16 KiB of LDS beside the callers' 128 KiB
-constexpr uint32_t WALK_LONG = 16;    // windows above which a run is queued (one window a group)
+// Calls on_group(tile, S, j, n, f) for every group of 8 consecutive fields of
+// bucket b's run in every tile: the run holds sorted positions [S, E) of the
+// tile, group j its fields S + 8 j .. S + 8 j + 7, of which the first
+// n = min(8, E - S - 8 j) are the run's (the rest are whatever follows in the
+// tile's stream, possibly past what the tile sort wrote: any 20-bit value);
+// f[k] is field k's 20 bits, unmasked above them.  Every thread of the
+// BUILD_NT-thread workgroup calls it (wave = t >> 6, lane = its lane).  Reads
+// reach 7 words past a group's first word: `part` needs 8 words of slack past
+// the last tile.
+//
+// Wave w owns tile blocks w, w + 16, ...; a step covers 2 x 64 / TB of them,
+// two tiles per lane, whose run bounds are loaded a step ahead.  The step's
+// groups are numbered across the wave (an exclusive scan of the lanes' group
+// counts) and dealt to the lanes in rounds of 64, so neighbouring lanes take
+// neighbouring groups of one run (their loads share cache lines, and nearly
+// every lane has 8 fields); eight rounds are loaded (six words a group) before
+// any is handed on.  A run of more than GROUP_LONG groups (sorted or clustered
+// ids: a bucket's fields in a few tiles, all in one wave's blocks) is queued in
+// LDS and its groups dealt to all sixteen waves after the walk; one that finds
+// the queue full is dealt with its wave's other runs.
+// Measured against a walk of 16-word windows by 4-lane groups (100M ids at
+// 2^30, ids_build): uniform ids 0.124 against 0.125-0.131 ms; sorted ids 0.101
+// against 0.19 ms; sorted groups of 4096 0.106 against 0.196 ms.
+constexpr uint32_t GROUP_LONG = 64;
+constexpr uint32_t GROUP_QCAP = 2048;  // 16 KiB of LDS beside the callers' 128 KiB
 
-template <class OnField>
-__device__ __forceinline__ void walk_bucket(const uint32_t* __restrict__ part, const uint16_t* __restrict__ tab,
-                                            const IdsGeom& g, uint32_t b, uint32_t wave, uint32_t lane,
-                                            OnField on_field)
+struct FieldGroup {
+    uint32_t x[6];  // words w0 .. w0 + 5
+    uint32_t o;     // the first field's bit within word w0
+};
+
+__device__ __forceinline__ void group_load(const uint32_t* __restrict__ part, uint32_t tile, uint32_t S, uint32_t j,
+                                           FieldGroup& q)
 {
-    __shared__ uint2 q_ent[WALK_QCAP];  // {tile, s0 | s1 << 16}
+    const uint32_t bit = FIELD_BITS * (S + 8u * j);
+    const uint32_t w0 = bit >> 5;
+    q.o = bit & 31u;
+    const uint2* src = reinterpret_cast<const uint2*>(part + static_cast<uint64_t>(tile) * TILE_WORDS + (w0 & ~1u));
+    const uint2 p0 = src[0], p1 = src[1], p2 = src[2], p3 = src[3];
+    const bool odd = (w0 & 1u) != 0u;
+    q.x[0] = odd ? p0.y : p0.x, q.x[1] = odd ? p1.x : p0.y, q.x[2] = odd ? p1.y : p1.x;
+    q.x[3] = odd ? p2.x : p1.y, q.x[4] = odd ? p2.y : p2.x, q.x[5] = odd ? p3.x : p2.y;
+}
+
+__device__ __forceinline__ void group_fields(const FieldGroup& q, uint32_t (&f)[8])
+{
+    static_assert(FIELD_BITS == 20, "8 fields = 5 words");
+    const uint32_t d0 = __builtin_amdgcn_alignbit(q.x[1], q.x[0], q.o);
+    const uint32_t d1 = __builtin_amdgcn_alignbit(q.x[2], q.x[1], q.o);
+    const uint32_t d2 = __builtin_amdgcn_alignbit(q.x[3], q.x[2], q.o);
+    const uint32_t d3 = __builtin_amdgcn_alignbit(q.x[4], q.x[3], q.o);
+    const uint32_t d4 = __builtin_amdgcn_alignbit(q.x[5], q.x[4], q.o);
+    f[0] = d0;
+    f[1] = __builtin_amdgcn_alignbit(d1, d0, 20);
+    f[2] = d1 >> 8;
+    f[3] = __builtin_amdgcn_alignbit(d2, d1, 28);
+    f[4] = __builtin_amdgcn_alignbit(d3, d2, 16);
+    f[5] = d3 >> 4;
+    f[6] = __builtin_amdgcn_alignbit(d4, d3, 24);
+    f[7] = d4 >> 12;
+}
+
+template <class OnGroup>
+__device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, const uint16_t* __restrict__ tab,
+                                            const IdsGeom& g, uint32_t b, uint32_t wave, uint32_t lane,
+                                            OnGroup on_group)
+{
+    __shared__ uint2 q_ent[GROUP_QCAP];  // {tile, S | E << 16}
     __shared__ uint32_t q_n;
     if (threadIdx.x == 0) q_n = 0;
     __syncthreads();
-    const uint32_t grp = lane >> 2;  // sixteen 4-lane groups
-    const uint32_t r4 = lane & 3u;
+    auto handle = [&](uint32_t tile, uint32_t S, uint32_t E, uint32_t j, const FieldGroup& q) {
+        uint32_t f[8];
+        group_fields(q, f);
+        on_group(tile, S, j, min(E - S - 8u * j, 8u), f);
+    };
+    constexpr uint32_t BPS = 64u / TB;
     const uint32_t n_blk = (g.n_tiles + TB - 1) / TB;
-    // Wave w owns tile blocks w, w + 16, ...; a step covers 64 / TB of them
-    // (one tile per lane, its run bounds loaded a step ahead: the TB lanes of
-    // a block read TB contiguous u16).  Each 4-lane group reads four tiles'
-    // runs as 16-word windows (64 bytes, 25.6 fields) with 16-byte loads
-    // aligned down to 4 words, and the loads of the first two windows are all
-    // issued before any bit is set.  A lane takes the fields that start in its
-    // 4 words; one that ends past them takes its last bits from the next
-    // word: the next lane's first, or for the group's last lane one more load.
-    constexpr uint32_t BPS = 64u / TB;  // blocks per step
     const uint32_t per_wave = n_blk > wave ? (n_blk - wave + BUILD_WAVES - 1) / BUILD_WAVES : 0u;
     auto tile_of = [&](uint32_t st, uint32_t l) { return (wave + BUILD_WAVES * (st * BPS + l / TB)) * TB + l % TB; };
     auto tab_load = [&](uint32_t st, uint32_t& r0, uint32_t& r1) {
         r0 = r1 = 0;
         const uint32_t jb = st * BPS + lane / TB;
-        const uint32_t tile = tile_of(st, lane);
-        if (jb < per_wave && tile < g.n_tiles) {
+        if (jb < per_wave && tile_of(st, lane) < g.n_tiles) {
             const uint16_t* tc =
                 tab + (static_cast<uint64_t>(wave + BUILD_WAVES * jb) * (g.NB + 1) + b) * TB + lane % TB;
             r0 = tc[0];
             r1 = tc[TB];
         }
     };
-    // Fields of [s0, s1) starting in words lo_w .. lo_w + 3 (x), with c4 =
-    // word lo_w + 4.  The first starts o < 20 bits in; after a funnel shift by
-    // o, field m sits at bit 20 m (m = 6 only when o < 8).
-    auto set_chunk = [&](const uint4& x, uint32_t c4, uint32_t lo_w, uint32_t s0, uint32_t s1, uint32_t tile) {
-        static_assert(FIELD_BITS == 20, "the unpacking below assumes 20-bit fields");
-        const uint32_t C = 32u * lo_w;
-        const uint32_t i0 = (C + FIELD_BITS - 1u) / FIELD_BITS;
-        const uint32_t o = FIELD_BITS * i0 - C;
-        const uint32_t d0 = __builtin_amdgcn_alignbit(x.y, x.x, o);
-        const uint32_t d1 = __builtin_amdgcn_alignbit(x.z, x.y, o);
-        const uint32_t d2 = __builtin_amdgcn_alignbit(x.w, x.z, o);
-        const uint32_t d3 = __builtin_amdgcn_alignbit(c4, x.w, o);
-        const uint32_t d4 = c4 >> o;
-        const uint32_t f[7] = {d0,
-                               __builtin_amdgcn_alignbit(d1, d0, 20),
-                               d1 >> 8,
-                               __builtin_amdgcn_alignbit(d2, d1, 28),
-                               __builtin_amdgcn_alignbit(d3, d2, 16),
-                               d3 >> 4,
-                               __builtin_amdgcn_alignbit(d4, d3, 24)};
-#pragma unroll
-        for (uint32_t m = 0; m < 7u; ++m) {
-            const uint32_t i = i0 + m;
-            if (i >= s0 && i < s1 && (m < 6u || o < 8u)) on_field(tile, i, f[m] & FIELD_MASK);
+    // A step covers 2 x 64 / TB blocks, two tiles per lane (halves 0 and 1),
+    // whose run bounds are loaded a step ahead.  The lanes' group counts (both
+    // tiles) are scanned over the wave, and the step's groups are dealt out in
+    // batches of eight rounds of 64, all eight loaded before any is handed on.
+    uint32_t a0, a1, b0, b1;
+    tab_load(0, a0, a1);
+    tab_load(1, b0, b1);
+    for (uint32_t st = 0; 2u * st * BPS < per_wave; ++st) {
+        const uint32_t Sa = a0, Ea = a1, Sb = b0, Eb = b1;
+        tab_load(2u * st + 2u, a0, a1);
+        tab_load(2u * st + 3u, b0, b1);
+        const uint32_t ta = tile_of(2u * st, lane), tb = tile_of(2u * st + 1u, lane);
+        uint32_t Ga = (Ea - Sa + 7u) / 8u, Gb = (Eb - Sb + 7u) / 8u;  // E >= S
+        if (Ga > GROUP_LONG) {
+            const uint32_t slot = atomicAdd(&q_n, 1u);
+            if (slot < GROUP_QCAP) q_ent[slot] = make_uint2(ta, Sa | (Ea << 16)), Ga = 0;
         }
-    };
-    uint32_t n0, n1;
-    tab_load(0, n0, n1);
-    for (uint32_t st = 0; st * BPS < per_wave; ++st) {
-        const uint32_t m0 = n0, m1 = n1;
-        tab_load(st + 1, n0, n1);
-        // windows from the 16-byte-aligned word holding field m0 to the last
-        // word holding the run's bits
-        const uint32_t own_nw =
-            m1 > m0 ? (((FIELD_BITS * m1 - 1u) >> 5) - (((FIELD_BITS * m0) >> 5) & ~3u)) / 16u + 1u : 0u;
-        uint32_t ts0[4], ts1[4], tb[4], wb[4], we[4], tl[4];
-#pragma unroll
-        for (uint32_t h = 0; h < 4u; ++h) {
-            const uint32_t src = 16u * h + grp;
-            ts0[h] = __shfl(m0, static_cast<int>(src), 64);
-            ts1[h] = __shfl(m1, static_cast<int>(src), 64);
-            tl[h] = tile_of(st, src);
-            tb[h] = tl[h] * TILE_WORDS;  // < 2^32 words for n < 2^32 (past the end: empty runs)
-            wb[h] = ((FIELD_BITS * ts0[h]) >> 5) & ~3u;
-            we[h] = ts1[h] > ts0[h] ? (FIELD_BITS * ts1[h] - 1u) >> 5 : 0u;
+        if (Gb > GROUP_LONG) {
+            const uint32_t slot = atomicAdd(&q_n, 1u);
+            if (slot < GROUP_QCAP) q_ent[slot] = make_uint2(tb, Sb | (Eb << 16)), Gb = 0;
         }
-        // A lane loads when its first word holds run bits (lo_w <= we, so its
-        // 4 words stay in the tile's written vectors); the last lane's extra
-        // word only when the run reaches it.
-        auto window = [&](uint32_t h, uint32_t k, uint4& x, uint32_t& e) {
-            const uint32_t lo_w = wb[h] + 16u * k + 4u * r4;
-            const bool act = ts1[h] > ts0[h] && lo_w <= we[h];
-            x = act ? *reinterpret_cast<const uint4*>(part + tb[h] + lo_w) : make_uint4(0, 0, 0, 0);
-            e = (act && r4 == 3u && lo_w + 4u <= we[h]) ? part[tb[h] + lo_w + 4u] : 0u;
-        };
-        {
-            uint4 x[4][2];
-            uint32_t e[4][2];
+        const uint32_t G = Ga + Gb;
+        uint32_t P = G;  // exclusive scan of G over the wave
 #pragma unroll
-            for (uint32_t h = 0; h < 4u; ++h)
+        for (uint32_t d = 1; d < 64u; d <<= 1) {
+            const uint32_t y = __shfl_up(P, d, 64);
+            if (lane >= d) P += y;
+        }
+        const uint32_t T = static_cast<uint32_t>(__shfl(P, 63, 64));
+        P -= G;
+        for (uint32_t r0 = 0; 64u * r0 < T; r0 += 8u) {
+            uint32_t w[8][6], tl[8], ss[8], ee[8], jj[8];
 #pragma unroll
-                for (uint32_t k = 0; k < 2u; ++k) window(h, k, x[h][k], e[h][k]);
+            for (uint32_t k = 0; k < 8u; ++k) {
+                const uint32_t u = 64u * (r0 + k) + lane;
+                uint32_t l = 0;  // the last lane whose first group is <= u holds group u
 #pragma unroll
-            for (uint32_t h = 0; h < 4u; ++h)
-#pragma unroll
-                for (uint32_t k = 0; k < 2u; ++k) {
-                    const uint32_t nx = __shfl_down(x[h][k].x, 1, 64);
-                    set_chunk(x[h][k], r4 == 3u ? e[h][k] : nx, wb[h] + 16u * k + 4u * r4, ts0[h], ts1[h], tl[h]);
+                for (uint32_t step = 32; step > 0; step >>= 1) {
+                    const uint32_t c = l + step;
+                    const uint32_t pc = static_cast<uint32_t>(__shfl(P, static_cast<int>(c & 63u), 64));
+                    if (c < 64u && pc <= u) l = c;
                 }
-        }
-        // Runs of 3 .. WALK_LONG windows: the rest of their windows by their
-        // own groups, all of the wave's runs together (the loop runs to the
-        // wave's longest such run).
-        uint32_t nw_mid = own_nw <= WALK_LONG ? own_nw : 0u;
+                const uint32_t jl = u - static_cast<uint32_t>(__shfl(P, static_cast<int>(l), 64));
+                const uint32_t ga = static_cast<uint32_t>(__shfl(Ga, static_cast<int>(l), 64));
+                const bool in_a = jl < ga;
+                const uint32_t sa = static_cast<uint32_t>(__shfl(Sa, static_cast<int>(l), 64));
+                const uint32_t ea = static_cast<uint32_t>(__shfl(Ea, static_cast<int>(l), 64));
+                const uint32_t sb = static_cast<uint32_t>(__shfl(Sb, static_cast<int>(l), 64));
+                const uint32_t eb = static_cast<uint32_t>(__shfl(Eb, static_cast<int>(l), 64));
+                ss[k] = in_a ? sa : sb;
+                ee[k] = u < T ? (in_a ? ea : eb) : ss[k];  // an empty slot: no fields
+                jj[k] = in_a ? jl : jl - ga;
+                tl[k] = tile_of(2u * st + (in_a ? 0u : 1u), l);
+                if (u < T) {
+                    const uint32_t* src = part + static_cast<uint64_t>(tl[k]) * TILE_WORDS +
+                                          ((FIELD_BITS * (ss[k] + 8u * jj[k])) >> 5);
 #pragma unroll
-        for (int d = 32; d > 0; d >>= 1) nw_mid = max(nw_mid, static_cast<uint32_t>(__shfl_xor(nw_mid, d, 64)));
-        bool mid[4];
-#pragma unroll
-        for (uint32_t h = 0; h < 4u; ++h)
-            mid[h] = static_cast<uint32_t>(__shfl(own_nw, static_cast<int>(16u * h + grp), 64)) <= WALK_LONG;
-        for (uint32_t k = 2; k < nw_mid; ++k) {
-#pragma unroll
-            for (uint32_t h = 0; h < 4u; ++h) {
-                uint4 x = make_uint4(0, 0, 0, 0);
-                uint32_t e = 0;
-                if (mid[h]) window(h, k, x, e);
-                const uint32_t nx = __shfl_down(x.x, 1, 64);
-                if (mid[h]) set_chunk(x, r4 == 3u ? e : nx, wb[h] + 16u * k + 4u * r4, ts0[h], ts1[h], tl[h]);
+                    for (uint32_t i = 0; i < 6u; ++i) w[k][i] = src[i];
+                }
             }
-        }
-        // Longer runs: queued for the workgroup; one that finds the queue full
-        // is finished here, one tile at a time, its remaining windows shared
-        // by the wave's sixteen groups.
-        const bool is_long = own_nw > WALK_LONG;
-        uint32_t slot = WALK_QCAP;
-        if (is_long) slot = atomicAdd(&q_n, 1u);
-        if (is_long && slot < WALK_QCAP) q_ent[slot] = make_uint2(tile_of(st, lane), m0 | (m1 << 16));
-        uint64_t longs = __ballot(is_long && slot >= WALK_QCAP);
-        while (longs) {
-            const uint32_t src = static_cast<uint32_t>(__builtin_ctzll(longs));
-            longs &= longs - 1u;
-            const uint32_t s0 = __shfl(m0, static_cast<int>(src), 64);
-            const uint32_t s1 = __shfl(m1, static_cast<int>(src), 64);
-            const uint32_t tile = tile_of(st, src);
-            const uint32_t base = tile * TILE_WORDS;
-            const uint32_t w0 = ((FIELD_BITS * s0) >> 5) & ~3u;
-            const uint32_t w1 = (FIELD_BITS * s1 - 1u) >> 5;
-            const uint32_t nwt = (w1 - w0) / 16u + 1u;
-            for (uint32_t kb = 2; kb < nwt; kb += 16u) {  // wave-uniform trip count
-                const uint32_t lo_w = w0 + 16u * (kb + grp) + 4u * r4;
-                const bool act = lo_w <= w1;
-                const uint4 x = act ? *reinterpret_cast<const uint4*>(part + base + lo_w) : make_uint4(0, 0, 0, 0);
-                const uint32_t e = (act && r4 == 3u && lo_w + 4u <= w1) ? part[base + lo_w + 4u] : 0u;
-                const uint32_t nx = __shfl_down(x.x, 1, 64);
-                if (act) set_chunk(x, r4 == 3u ? e : nx, lo_w, s0, s1, tile);
+#pragma unroll
+            for (uint32_t k = 0; k < 8u; ++k) {
+                if (ee[k] == ss[k]) continue;
+                FieldGroup q;
+#pragma unroll
+                for (uint32_t i = 0; i < 6u; ++i) q.x[i] = w[k][i];
+                q.o = (FIELD_BITS * (ss[k] + 8u * jj[k])) & 31u;
+                handle(tl[k], ss[k], ee[k], jj[k], q);
             }
         }
     }
-    // The queued runs: windows 2, 3, ... of each in chunks of sixteen (one a
-    // group), the chunks of all runs dealt to the waves in turn.
+    // The queued runs: their groups in chunks of 64 (one a lane), the chunks of
+    // all runs dealt to the waves in turn.
     __syncthreads();
-    const uint32_t nq = min(q_n, WALK_QCAP);
-    uint32_t off = 0;  // chunks of the runs before
-    for (uint32_t j = 0; j < nq; ++j) {
-        const uint2 ent = q_ent[j];
-        const uint32_t tile = ent.x, s0 = ent.y & 0xFFFFu, s1 = ent.y >> 16;
-        const uint32_t base = tile * TILE_WORDS;
-        const uint32_t w0 = ((FIELD_BITS * s0) >> 5) & ~3u;
-        const uint32_t w1 = (FIELD_BITS * s1 - 1u) >> 5;
-        const uint32_t nch = ((w1 - w0) / 16u - 1u + 15u) / 16u;  // windows 2 .. (w1 - w0) / 16
+    const uint32_t nq = min(q_n, GROUP_QCAP);
+    uint32_t off = 0;
+    for (uint32_t i = 0; i < nq; ++i) {
+        const uint2 ent = q_ent[i];
+        const uint32_t S = ent.y & 0xFFFFu, E = ent.y >> 16;
+        const uint32_t G = (E - S + 7u) / 8u;
+        const uint32_t nch = (G + 63u) / 64u;
         for (uint32_t c = (wave + BUILD_WAVES - off % BUILD_WAVES) % BUILD_WAVES; c < nch; c += BUILD_WAVES) {
-            const uint32_t lo_w = w0 + 16u * (2u + 16u * c + grp) + 4u * r4;
-            const bool act = lo_w <= w1;
-            const uint4 x = act ? *reinterpret_cast<const uint4*>(part + base + lo_w) : make_uint4(0, 0, 0, 0);
-            const uint32_t e = (act && r4 == 3u && lo_w + 4u <= w1) ? part[base + lo_w + 4u] : 0u;
-            const uint32_t nx = __shfl_down(x.x, 1, 64);
-            if (act) set_chunk(x, r4 == 3u ? e : nx, lo_w, s0, s1, tile);
+            const uint32_t j = 64u * c + lane;
+            if (j < G) {
+                FieldGroup q;
+                group_load(part, ent.x, S, j, q);
+                handle(ent.x, S, E, j, q);
+            }
         }
         off += nch;
     }

@@ -200,9 +200,14 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
     __syncthreads();
     const uint32_t wave = t >> 6;
     const uint32_t lane = __lane_id();
-    walk_bucket(part, tab, g, b, wave, lane, [&](uint32_t, uint32_t, uint32_t F) {
-        atomicOr(&bits[F >> 5], 1u << (F & 31u));  // key-in-bucket << 16 | low 16 bits
-    });
+    walk_groups(part, tab, g, b, wave, lane,
+                [&](uint32_t, uint32_t, uint32_t, uint32_t n, const uint32_t (&f)[8]) {
+#pragma unroll
+                    for (uint32_t k = 0; k < 8u; ++k) {
+                        const uint32_t F = f[k] & FIELD_MASK;  // key-in-bucket << 16 | low 16 bits
+                        if (k < n) atomicOr(&bits[F >> 5], 1u << (F & 31u));
+                    }
+                });
     __syncthreads();
     __shared__ uint32_t wave_pc[BUILD_WAVES];
     const uint32_t c = wave;  // wave c owns container c of the bucket
@@ -556,7 +561,8 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     const size_t o_tab =
         c.add(sizeof(uint16_t) * static_cast<uint64_t>((g.n_tiles + TB - 1) / TB) * TB * (g.NB + 1));
     // Whole tiles (a partial last tile is padded) + the build's window overrun.
-    const size_t o_part = c.add(sizeof(uint32_t) * (static_cast<uint64_t>(g.n_tiles) * TILE_WORDS + 4));
+    // the build's field groups read up to 7 words past a group's first: slack past the last tile
+    const size_t o_part = c.add(sizeof(uint32_t) * (static_cast<uint64_t>(g.n_tiles) * TILE_WORDS + 8));
     Scratch sc;
     CR_RET(sc.alloc(c.total, s));
     uint32_t* gmax = sc.at<uint32_t>(o_gmax);
