@@ -567,3 +567,45 @@ def test_contains_parity(gpu, layout, universe, density, mode):
     got = out.cpu().numpy().view(np.uint32)
     assert np.array_equal(got, orc.contains_many(want, q))
     gpu.free(g)
+
+
+# ---- randomized sweep over the tile-sort paths -------------------------------
+def _sweep_case(i):
+    """Case i of a seeded sweep: a universe, an id distribution (uniform,
+    sorted, clustered windows, a few hot keys) and a size around the tile
+    sort's 24576-id tiles and 8-tile blocks."""
+    rng = np.random.default_rng(1000 + i)
+    U = int(rng.choice([70000, 1 << 20, (1 << 22) + 5, 1 << 26, 1 << 30, 0xFFFFFFFF]))
+    n = int(rng.choice([1025, 24575, 24577, 8 * 24576 + 3, 200_000, 700_000]))
+    kind = ["uniform", "sorted", "windows", "hot"][i % 4]
+    if kind == "uniform":
+        ids = rng.integers(0, U, n, dtype=np.uint64)
+    elif kind == "sorted":
+        ids = np.sort(rng.integers(0, U, n, dtype=np.uint64))
+    elif kind == "windows":  # runs of sorted ids in random 65536-aligned windows
+        w = rng.integers(0, max(1, U >> 16), (n + 4095) // 4096, dtype=np.uint64)
+        off = np.sort(rng.integers(0, 65536, ((n + 4095) // 4096, 4096), dtype=np.uint64), axis=1)
+        ids = ((w[:, None] << 16) + off).reshape(-1)[:n] % U
+    else:  # most ids in three keys, the rest uniform
+        hot = rng.integers(0, max(1, U >> 16), 3, dtype=np.uint64)
+        ids = np.where(rng.random(n) < 0.8, (hot[rng.integers(0, 3, n)] << 16) + rng.integers(0, 65536, n, dtype=np.uint64),
+                       rng.integers(0, U, n, dtype=np.uint64)) % U
+    return U, kind, ids.astype(np.uint32), rng
+
+
+@pytest.mark.parametrize("i", range(16))
+def test_tile_sort_paths_random_sweep(gpu, i):
+    """upload_from_device_ids (strict, against the oracle) and partitioned
+    queries (the ids themselves, the ids + 1, and uniform queries past U)."""
+    U, kind, ids, rng = _sweep_case(i)
+    _say("tile-sort sweep", i, U, kind, ids.size)
+    torch = _torch()
+    want = orc.upload_from_ids(ids, U, orc.PROMOTE_AUTO, auto_l2(gpu))
+    g = gpu.upload_from_device_ids(_dev_u32(ids), U)
+    assert_same(gpu.download(g), want, strict=True, what=f"sweep {i} {kind}")
+    q = np.concatenate([ids, ids + np.uint32(1), rng.integers(0, 0xFFFFFFFF, 30_001, dtype=np.uint64).astype(np.uint32)])
+    out = torch.empty(q.size, dtype=torch.int32, device="cuda")
+    gpu.contains_batch(g, _dev_u32(q), out, 4)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), orc.contains_many(want, q)), (i, kind)
+    gpu.free(g)
