@@ -164,15 +164,34 @@ def cpu_threads():
 
 
 def cpu_info():
-    model = "unknown"
+    """The host CPU as /proc/cpuinfo and lscpu describe it (a virtualised box
+    may report only "AMD EPYC" as its model name, so family/model/stepping,
+    cache and vector-ISA flags are kept too)."""
+    info = {"model": "unknown"}
+    keys = {"model name": "model", "cpu family": "family", "model": "model_number", "stepping": "stepping",
+            "cache size": "cache"}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
+            k, _, v = line.partition(":")
+            k = k.strip()
+            if k in keys and keys[k] not in info or (k == "model name" and info["model"] == "unknown"):
+                info[keys[k]] = v.strip()
+            if k == "flags":
+                fl = set(v.split())
+                info["isa"] = [f for f in ("avx2", "avx512f", "avx512_bf16", "avx512_vnni") if f in fl]
+            if not line.strip() and "family" in info:
                 break
     except OSError:
         pass
-    return {"model": model, "os_cpu_count": os.cpu_count(), "threads_used": cpu_threads()}
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        want = ("Model name", "Socket(s)", "Core(s) per socket", "Thread(s) per core", "L3 cache", "CPU max MHz")
+        info["lscpu"] = {k: v.strip() for k, _, v in (ln.partition(":") for ln in out.splitlines()) if k.strip() in want}
+    except Exception:
+        pass
+    info.update({"os_cpu_count": os.cpu_count(), "threads_used": cpu_threads()})
+    return info
 
 
 def words_bernoulli(torch, density, seed, universe=U):
