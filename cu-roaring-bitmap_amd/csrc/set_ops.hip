@@ -386,30 +386,82 @@ __device__ __forceinline__ uint32_t bitmap_op_stream(const uint64_t* pa, const u
     return pc;
 }
 
-// Expand one container of any type into a 2048-word LDS bitmap (caller syncs
-// after).  A bitmap is copied; array and run containers go through expand_img,
-// whose difference array (`cover`, 2048 words) makes a run cost O(1) however
-// long it is (runs ending past 0xFFFF are clamped, as expand_to_bitmap_kernel
-// does, src/set_ops.cu:355-359).
-__device__ __forceinline__ void expand_to_lds(const Side& S, int32_t idx, uint32_t* lds, int32_t* cover)
+// Mixed pairs: thread t builds words [8 t, 8 t + 8) (bits [256 t, 256 t + 256))
+// of both sides' 8 KiB images in registers.  A bitmap's words are loaded; a
+// run container's come from the runs that meet the thread's range (a binary
+// search for the last run starting at or below its end, then back over the
+// runs that reach into it; a run ending past 0xFFFF is clamped, as
+// expand_to_bitmap_kernel does, src/set_ops.cu:355-359).  An array's values
+// are scattered with LDS atomics into an image that every thread then reads
+// its words from -- the only case that needs workgroup barriers.
+struct MixMeta {
+    uint32_t type, off, card;
+};
+
+__device__ __forceinline__ MixMeta mix_meta(const Side& S, int32_t idx)
+{
+    return MixMeta{S.types[idx], S.offsets[idx], S.cards[idx]};
+}
+
+// A bitmap or run side's words of this thread; for an array side zeroes the
+// thread's words of `img` and returns zeros (the caller syncs, scatters, syncs
+// and reads them back).
+struct Words8 {
+    uint32_t w0, w1, w2, w3, w4, w5, w6, w7;
+};
+
+__device__ __forceinline__ Words8 mix_words(const Side& S, const MixMeta& m, uint32_t* img)
 {
     const uint32_t t = threadIdx.x;
-    const uint32_t type = S.types[idx];
-    const uint32_t off = S.offsets[idx];
-    if (type == CR_BITMAP) {
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(S.bmp) + (off >> 2);
-        if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {  // 16-byte loads, both in flight
-            const uint4 x0 = ld_stream(reinterpret_cast<const uint4*>(src) + t);
-            const uint4 x1 = ld_stream(reinterpret_cast<const uint4*>(src) + t + EXEC_NT);
-            reinterpret_cast<uint4*>(lds)[t] = x0;
-            reinterpret_cast<uint4*>(lds)[t + EXEC_NT] = x1;
-        } else {
-            for (uint32_t i = t; i < 2048u; i += EXEC_NT) lds[i] = src[i];
+    if (m.type == CR_BITMAP) {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(S.bmp) + (m.off >> 2) + 8u * t;
+        if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
+            const uint4 x0 = ld_stream(reinterpret_cast<const uint4*>(src));
+            const uint4 x1 = ld_stream(reinterpret_cast<const uint4*>(src) + 1);
+            return Words8{x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         }
-        return;
+        return Words8{src[0], src[1], src[2], src[3], src[4], src[5], src[6], src[7]};
     }
-    const uint16_t* data = (type == CR_ARRAY ? S.arr : S.run) + (off >> 1);
-    expand_img<EXEC_NT>(static_cast<uint8_t>(type), data, S.cards[idx], lds, cover);
+    Words8 r{0, 0, 0, 0, 0, 0, 0, 0};
+    if (m.type == CR_ARRAY) {
+        reinterpret_cast<uint4*>(img)[2 * t] = make_uint4(0, 0, 0, 0);
+        reinterpret_cast<uint4*>(img)[2 * t + 1] = make_uint4(0, 0, 0, 0);
+        return r;
+    }
+    if (m.type != CR_RUN || m.card == 0) return r;
+    const uint16_t* runs = S.run + (m.off >> 1);
+    const uint32_t lo = 256u * t, hi = lo + 255u;
+    uint32_t a = 0, b = m.card;  // first run starting past hi
+    while (a < b) {
+        const uint32_t mid = (a + b) >> 1;
+        if (runs[2 * mid] <= hi)
+            a = mid + 1;
+        else
+            b = mid;
+    }
+    // bits of word j (j = 0..7) inside [s, e], the thread's bits 0..255
+    auto span = [](uint32_t s, uint32_t e, uint32_t j) {
+        const uint32_t wl = 32u * j, wh = wl + 31u;
+        return (e >= wl && s <= wh) ? bit_span(max(s, wl) - wl, min(e, wh) - wl) : 0u;
+    };
+    for (uint32_t k = a; k > 0; --k) {
+        const uint32_t s0 = runs[2 * (k - 1)];
+        const uint32_t e0 = min(0xFFFFu, s0 + runs[2 * (k - 1) + 1]);
+        if (e0 < lo) break;  // runs are sorted and disjoint: none before reaches the range
+        const uint32_t s = max(s0, lo) - lo, e = min(e0, hi) - lo;
+        r.w0 |= span(s, e, 0), r.w1 |= span(s, e, 1), r.w2 |= span(s, e, 2), r.w3 |= span(s, e, 3);
+        r.w4 |= span(s, e, 4), r.w5 |= span(s, e, 5), r.w6 |= span(s, e, 6), r.w7 |= span(s, e, 7);
+    }
+    return r;
+}
+
+__device__ __forceinline__ void mix_scatter(const Side& S, const MixMeta& m, uint32_t* img)
+{
+    const uint16_t* vals = S.arr + (m.off >> 1);
+    for (uint32_t i = threadIdx.x; i < m.card; i += EXEC_NT) {
+        const uint32_t v = vals[i];
+        atomicOr(&img[v >> 5], 1u << (v & 31u));
+    }
 }
 
 template <uint32_t OP>
@@ -417,8 +469,7 @@ __global__ __launch_bounds__(EXEC_NT) void so_exec(Side A, Side B, const Item* i
                                                    uint64_t* out_bmp, uint16_t* out_arr, uint16_t* out_run,
                                                    uint32_t* item_card, uint32_t* tile_keep)
 {
-    __shared__ uint32_t lds[4096];    // 16 KiB: two expanded bitmaps, or a staged array
-    __shared__ int32_t cover[2048];   // the run difference array of expand_img
+    __shared__ alignas(16) uint32_t lds[4096];  // 16 KiB: two array images, or a staged array
     __shared__ uint32_t red[EXEC_NT / 64];
     if (totals->overflow) return;  // the output was not allocated for this plan
     const uint32_t n_items = totals->c[C_ITEM];
@@ -437,25 +488,36 @@ __global__ __launch_bounds__(EXEC_NT) void so_exec(Side A, Side B, const Item* i
             break;
         }
         case CAT_MIXED: {
-            expand_to_lds(A, it.ai, lds, cover);
-            __syncthreads();
-            expand_to_lds(B, it.bi, lds + 2048, cover);
-            __syncthreads();
-            uint32_t pc = 0;
-            uint4* dst = reinterpret_cast<uint4*>(out_bmp + it.slot * 1024ull);  // 8 KiB slots: 16-byte aligned
-            const uint4* la = reinterpret_cast<const uint4*>(lds);
-            const uint4* lb = reinterpret_cast<const uint4*>(lds + 2048);
-#pragma unroll
-            for (uint32_t h = 0; h < 2u; ++h) {
-                const uint4 x = la[t + h * EXEC_NT], y = lb[t + h * EXEC_NT];
-                uint4 r;
-                r.x = apply32<OP>(x.x, y.x);
-                r.y = apply32<OP>(x.y, y.y);
-                r.z = apply32<OP>(x.z, y.z);
-                r.w = apply32<OP>(x.w, y.w);
-                st_stream(dst + t + h * EXEC_NT, r);
-                pc += __popc(r.x) + __popc(r.y) + __popc(r.z) + __popc(r.w);
+            // both sides' metadata, then both sides' words, loaded together
+            const MixMeta ma = mix_meta(A, it.ai), mb = mix_meta(B, it.bi);
+            Words8 wa = mix_words(A, ma, lds);
+            Words8 wb = mix_words(B, mb, lds + 2048);
+            const bool arr_a = ma.type == CR_ARRAY, arr_b = mb.type == CR_ARRAY;  // the same in every thread
+            if (arr_a || arr_b) {
+                __syncthreads();  // the array images are zeroed
+                if (arr_a) mix_scatter(A, ma, lds);
+                if (arr_b) mix_scatter(B, mb, lds + 2048);
+                __syncthreads();
+                if (arr_a) {
+                    const uint4 x0 = reinterpret_cast<const uint4*>(lds)[2 * t];
+                    const uint4 x1 = reinterpret_cast<const uint4*>(lds)[2 * t + 1];
+                    wa = Words8{x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                }
+                if (arr_b) {
+                    const uint4 y0 = reinterpret_cast<const uint4*>(lds + 2048)[2 * t];
+                    const uint4 y1 = reinterpret_cast<const uint4*>(lds + 2048)[2 * t + 1];
+                    wb = Words8{y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+                }
             }
+            const uint4 r0 = make_uint4(apply32<OP>(wa.w0, wb.w0), apply32<OP>(wa.w1, wb.w1),
+                                        apply32<OP>(wa.w2, wb.w2), apply32<OP>(wa.w3, wb.w3));
+            const uint4 r1 = make_uint4(apply32<OP>(wa.w4, wb.w4), apply32<OP>(wa.w5, wb.w5),
+                                        apply32<OP>(wa.w6, wb.w6), apply32<OP>(wa.w7, wb.w7));
+            uint4* dst = reinterpret_cast<uint4*>(out_bmp + it.slot * 1024ull) + 2 * t;  // 8 KiB slots: 16-byte aligned
+            st_stream(dst, r0);
+            st_stream(dst + 1, r1);
+            uint32_t pc = __popc(r0.x) + __popc(r0.y) + __popc(r0.z) + __popc(r0.w) + __popc(r1.x) + __popc(r1.y) +
+                          __popc(r1.z) + __popc(r1.w);
             pc = block_sum<EXEC_NT>(pc, red);
             card = pc > 65535u ? 0u : pc;
             keep = card != 0 || OP == CR_OR;
