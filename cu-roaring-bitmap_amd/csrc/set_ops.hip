@@ -386,14 +386,16 @@ __device__ __forceinline__ uint32_t bitmap_op_stream(const uint64_t* pa, const u
     return pc;
 }
 
-// Mixed pairs: thread t builds words [8 t, 8 t + 8) (bits [256 t, 256 t + 256))
-// of both sides' 8 KiB images in registers.  A bitmap's words are loaded; a
-// run container's come from the runs that meet the thread's range (a binary
-// search for the last run starting at or below its end, then back over the
-// runs that reach into it; a run ending past 0xFFFF is clamped, as
-// expand_to_bitmap_kernel does, src/set_ops.cu:355-359).  An array's values
-// are scattered with LDS atomics into an image that every thread then reads
-// its words from -- the only case that needs workgroup barriers.
+// Mixed pairs: thread t builds 128-bit chunks t and t + 256 of both sides' 8 KiB
+// images (words [4 t, 4 t + 4) and [1024 + 4 t, 1024 + 4 t + 4)) in registers,
+// so each of its two 16-byte stores is part of one contiguous 4 KiB store of
+// the workgroup.  A bitmap's chunks are loaded; a run container's come from
+// the runs that meet each chunk (a binary search for the last run starting at
+// or below its end, then back over the runs that reach into it; a run ending
+// past 0xFFFF is clamped, as expand_to_bitmap_kernel does,
+// src/set_ops.cu:355-359).  An array's values are scattered with LDS atomics
+// into an image that every thread then reads its chunks from -- the only case
+// that needs workgroup barriers.
 struct MixMeta {
     uint32_t type, off, card;
 };
@@ -403,35 +405,11 @@ __device__ __forceinline__ MixMeta mix_meta(const Side& S, int32_t idx)
     return MixMeta{S.types[idx], S.offsets[idx], S.cards[idx]};
 }
 
-// A bitmap or run side's words of this thread; for an array side zeroes the
-// thread's words of `img` and returns zeros (the caller syncs, scatters, syncs
-// and reads them back).
-struct Words8 {
-    uint32_t w0, w1, w2, w3, w4, w5, w6, w7;
-};
-
-__device__ __forceinline__ Words8 mix_words(const Side& S, const MixMeta& m, uint32_t* img)
+// The 4 words of bits [lo, lo + 128) of a run container.
+__device__ __forceinline__ uint4 run_chunk(const uint16_t* runs, uint32_t card, uint32_t lo)
 {
-    const uint32_t t = threadIdx.x;
-    if (m.type == CR_BITMAP) {
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(S.bmp) + (m.off >> 2) + 8u * t;
-        if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
-            const uint4 x0 = ld_stream(reinterpret_cast<const uint4*>(src));
-            const uint4 x1 = ld_stream(reinterpret_cast<const uint4*>(src) + 1);
-            return Words8{x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        }
-        return Words8{src[0], src[1], src[2], src[3], src[4], src[5], src[6], src[7]};
-    }
-    Words8 r{0, 0, 0, 0, 0, 0, 0, 0};
-    if (m.type == CR_ARRAY) {
-        reinterpret_cast<uint4*>(img)[2 * t] = make_uint4(0, 0, 0, 0);
-        reinterpret_cast<uint4*>(img)[2 * t + 1] = make_uint4(0, 0, 0, 0);
-        return r;
-    }
-    if (m.type != CR_RUN || m.card == 0) return r;
-    const uint16_t* runs = S.run + (m.off >> 1);
-    const uint32_t lo = 256u * t, hi = lo + 255u;
-    uint32_t a = 0, b = m.card;  // first run starting past hi
+    const uint32_t hi = lo + 127u;
+    uint32_t a = 0, b = card;  // first run starting past hi
     while (a < b) {
         const uint32_t mid = (a + b) >> 1;
         if (runs[2 * mid] <= hi)
@@ -439,20 +417,50 @@ __device__ __forceinline__ Words8 mix_words(const Side& S, const MixMeta& m, uin
         else
             b = mid;
     }
-    // bits of word j (j = 0..7) inside [s, e], the thread's bits 0..255
+    // bits of word j (j = 0..3) inside [s, e], the chunk's bits 0..127
     auto span = [](uint32_t s, uint32_t e, uint32_t j) {
         const uint32_t wl = 32u * j, wh = wl + 31u;
         return (e >= wl && s <= wh) ? bit_span(max(s, wl) - wl, min(e, wh) - wl) : 0u;
     };
+    uint4 r = make_uint4(0, 0, 0, 0);
     for (uint32_t k = a; k > 0; --k) {
         const uint32_t s0 = runs[2 * (k - 1)];
         const uint32_t e0 = min(0xFFFFu, s0 + runs[2 * (k - 1) + 1]);
-        if (e0 < lo) break;  // runs are sorted and disjoint: none before reaches the range
+        if (e0 < lo) break;  // runs are sorted and disjoint: none before reaches the chunk
         const uint32_t s = max(s0, lo) - lo, e = min(e0, hi) - lo;
-        r.w0 |= span(s, e, 0), r.w1 |= span(s, e, 1), r.w2 |= span(s, e, 2), r.w3 |= span(s, e, 3);
-        r.w4 |= span(s, e, 4), r.w5 |= span(s, e, 5), r.w6 |= span(s, e, 6), r.w7 |= span(s, e, 7);
+        r.x |= span(s, e, 0), r.y |= span(s, e, 1), r.z |= span(s, e, 2), r.w |= span(s, e, 3);
     }
     return r;
+}
+
+// A bitmap or run side's two chunks of this thread; for an array side zeroes
+// the thread's chunks of `img` and returns zeros (the caller syncs, scatters,
+// syncs and reads them back).
+struct Chunks2 {
+    uint4 c0, c1;
+};
+
+__device__ __forceinline__ Chunks2 mix_words(const Side& S, const MixMeta& m, uint32_t* img)
+{
+    const uint32_t t = threadIdx.x;
+    if (m.type == CR_BITMAP) {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(S.bmp) + (m.off >> 2);
+        if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0)
+            return Chunks2{ld_stream(reinterpret_cast<const uint4*>(src) + t),
+                           ld_stream(reinterpret_cast<const uint4*>(src) + t + EXEC_NT)};
+        const uint32_t* p0 = src + 4u * t;
+        const uint32_t* p1 = p0 + 4u * EXEC_NT;
+        return Chunks2{make_uint4(p0[0], p0[1], p0[2], p0[3]), make_uint4(p1[0], p1[1], p1[2], p1[3])};
+    }
+    const uint4 z = make_uint4(0, 0, 0, 0);
+    if (m.type == CR_ARRAY) {
+        reinterpret_cast<uint4*>(img)[t] = z;
+        reinterpret_cast<uint4*>(img)[t + EXEC_NT] = z;
+        return Chunks2{z, z};
+    }
+    if (m.type != CR_RUN || m.card == 0) return Chunks2{z, z};
+    const uint16_t* runs = S.run + (m.off >> 1);
+    return Chunks2{run_chunk(runs, m.card, 128u * t), run_chunk(runs, m.card, 128u * (t + EXEC_NT))};
 }
 
 __device__ __forceinline__ void mix_scatter(const Side& S, const MixMeta& m, uint32_t* img)
@@ -488,34 +496,29 @@ __global__ __launch_bounds__(EXEC_NT) void so_exec(Side A, Side B, const Item* i
             break;
         }
         case CAT_MIXED: {
-            // both sides' metadata, then both sides' words, loaded together
+            // both sides' metadata, then both sides' chunks, loaded together
             const MixMeta ma = mix_meta(A, it.ai), mb = mix_meta(B, it.bi);
-            Words8 wa = mix_words(A, ma, lds);
-            Words8 wb = mix_words(B, mb, lds + 2048);
+            Chunks2 wa = mix_words(A, ma, lds);
+            Chunks2 wb = mix_words(B, mb, lds + 2048);
             const bool arr_a = ma.type == CR_ARRAY, arr_b = mb.type == CR_ARRAY;  // the same in every thread
             if (arr_a || arr_b) {
                 __syncthreads();  // the array images are zeroed
                 if (arr_a) mix_scatter(A, ma, lds);
                 if (arr_b) mix_scatter(B, mb, lds + 2048);
                 __syncthreads();
-                if (arr_a) {
-                    const uint4 x0 = reinterpret_cast<const uint4*>(lds)[2 * t];
-                    const uint4 x1 = reinterpret_cast<const uint4*>(lds)[2 * t + 1];
-                    wa = Words8{x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                }
-                if (arr_b) {
-                    const uint4 y0 = reinterpret_cast<const uint4*>(lds + 2048)[2 * t];
-                    const uint4 y1 = reinterpret_cast<const uint4*>(lds + 2048)[2 * t + 1];
-                    wb = Words8{y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
-                }
+                if (arr_a)
+                    wa = Chunks2{reinterpret_cast<const uint4*>(lds)[t], reinterpret_cast<const uint4*>(lds)[t + EXEC_NT]};
+                if (arr_b)
+                    wb = Chunks2{reinterpret_cast<const uint4*>(lds + 2048)[t],
+                                 reinterpret_cast<const uint4*>(lds + 2048)[t + EXEC_NT]};
             }
-            const uint4 r0 = make_uint4(apply32<OP>(wa.w0, wb.w0), apply32<OP>(wa.w1, wb.w1),
-                                        apply32<OP>(wa.w2, wb.w2), apply32<OP>(wa.w3, wb.w3));
-            const uint4 r1 = make_uint4(apply32<OP>(wa.w4, wb.w4), apply32<OP>(wa.w5, wb.w5),
-                                        apply32<OP>(wa.w6, wb.w6), apply32<OP>(wa.w7, wb.w7));
-            uint4* dst = reinterpret_cast<uint4*>(out_bmp + it.slot * 1024ull) + 2 * t;  // 8 KiB slots: 16-byte aligned
-            st_stream(dst, r0);
-            st_stream(dst + 1, r1);
+            const uint4 r0 = make_uint4(apply32<OP>(wa.c0.x, wb.c0.x), apply32<OP>(wa.c0.y, wb.c0.y),
+                                        apply32<OP>(wa.c0.z, wb.c0.z), apply32<OP>(wa.c0.w, wb.c0.w));
+            const uint4 r1 = make_uint4(apply32<OP>(wa.c1.x, wb.c1.x), apply32<OP>(wa.c1.y, wb.c1.y),
+                                        apply32<OP>(wa.c1.z, wb.c1.z), apply32<OP>(wa.c1.w, wb.c1.w));
+            uint4* dst = reinterpret_cast<uint4*>(out_bmp + it.slot * 1024ull);  // 8 KiB slots: 16-byte aligned
+            st_stream(dst + t, r0);
+            st_stream(dst + t + EXEC_NT, r1);
             uint32_t pc = __popc(r0.x) + __popc(r0.y) + __popc(r0.z) + __popc(r0.w) + __popc(r1.x) + __popc(r1.y) +
                           __popc(r1.z) + __popc(r1.w);
             pc = block_sum<EXEC_NT>(pc, red);
