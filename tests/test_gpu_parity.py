@@ -476,7 +476,7 @@ def test_set_operation_empty_and_identical(gpu):
 
 # ---- multi_and ----------------------------------------------------------------
 @pytest.mark.parametrize("case", ["fused_plain", "fused_negated", "fused_all_negated", "pairwise_arrays",
-                                  "fused_absent_negated_key", "single", "fused_8"])
+                                  "fused_absent_negated_key", "single", "fused_8", "fused_32", "pairwise_33"])
 def test_multi_and_parity(gpu, case):
     _say("multi_and", case)
     rng = np.random.default_rng(sum(map(ord, case)))
@@ -489,6 +489,12 @@ def test_multi_and_parity(gpu, case):
     elif case == "fused_8":
         U = 8 * 65536
         logicals = [np.nonzero(rng.random(U) < (0.2 if i % 2 == 0 else 0.85))[0] for i in range(8)]
+        thr = orc.PROMOTE_ALL
+    elif case in ("fused_32", "pairwise_33"):  # the fused path's largest k (src/set_ops.cu:1715-1745), then one more
+        k = 32 if case == "fused_32" else 33
+        U = 4 * 65536
+        # dense sets (most above U/2: complemented) so that the AND is not empty
+        logicals = [np.nonzero(rng.random(U) < (0.97 if i % 4 else 0.6))[0] for i in range(k)]
         thr = orc.PROMOTE_ALL
     else:
         U = 200000
