@@ -329,20 +329,21 @@ __global__ __launch_bounds__(BUILD_NT) void qp_answer(const uint32_t* __restrict
     if (b >= g.NB) return;
     const uint32_t wave = t >> 6, lane = __lane_id();
     const uint32_t key = b * BK_KEYS + wave;
-    if (key < g.K) {
-        qp_load_container(v, key, bits + wave * 2048u, lane);
-    } else {
-        uint4* w4 = reinterpret_cast<uint4*>(bits + wave * 2048u);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) w4[lane + 64 * j] = make_uint4(0, 0, 0, 0);
-    }
-    // (walk_groups' first barrier publishes the image)
     const uint32_t flip = v.negated ? 0xFFu : 0u;
     const uint32_t abytes = qp_abytes(g.NB);
     // All 8 answers of a group go into one byte that only this lane writes:
     // fields past the run answer into b's padding, and any 20-bit value
     // indexes the LDS image.
     walk_groups(part, tab, g, b, wave, lane,
+                [&] {  // wave w loads container w of the bucket (zeros past the last key)
+                    if (key < g.K) {
+                        qp_load_container(v, key, bits + wave * 2048u, lane);
+                    } else {
+                        uint4* w4 = reinterpret_cast<uint4*>(bits + wave * 2048u);
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) w4[lane + 64 * j] = make_uint4(0, 0, 0, 0);
+                    }
+                },
                 [&](uint32_t tile, uint32_t S, uint32_t j, uint32_t, const uint32_t (&f)[8]) {
                     uint32_t a = 0;
 #pragma unroll

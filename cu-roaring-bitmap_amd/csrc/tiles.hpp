@@ -329,8 +329,11 @@ inline uint32_t build_grid(uint32_t nb) { return 8 * build_per_xcd(nb); }
 // tile, group j its fields S + 8 j .. S + 8 j + 7, of which the first
 // n = min(8, E - S - 8 j) are the run's (the rest are whatever follows in the
 // tile's stream, possibly past what the tile sort wrote: any 20-bit value);
-// f[k] is field k's 20 bits, unmasked above them.  Every thread of the
-// BUILD_NT-thread workgroup calls it (wave = t >> 6, lane = its lane).  Reads
+// f[k] is field k's 20 bits, unmasked above them.  prologue() runs first, in
+// every thread, once the first run bounds are requested: the caller's LDS
+// set-up, published by a workgroup barrier before the first on_group.  Every
+// thread of the BUILD_NT-thread workgroup calls it (wave = t >> 6, lane = its
+// lane).  Reads
 // reach 7 words past a group's first word: `part` needs 8 words of slack past
 // the last tile.
 //
@@ -386,15 +389,13 @@ __device__ __forceinline__ void group_fields(const FieldGroup& q, uint32_t (&f)[
     f[7] = d4 >> 12;
 }
 
-template <class OnGroup>
+template <class Prologue, class OnGroup>
 __device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, const uint16_t* __restrict__ tab,
                                             const IdsGeom& g, uint32_t b, uint32_t wave, uint32_t lane,
-                                            OnGroup on_group)
+                                            Prologue prologue, OnGroup on_group)
 {
     __shared__ uint2 q_ent[GROUP_QCAP];  // {tile, S | E << 16}
     __shared__ uint32_t q_n;
-    if (threadIdx.x == 0) q_n = 0;
-    __syncthreads();
     auto handle = [&](uint32_t tile, uint32_t S, uint32_t E, uint32_t j, const FieldGroup& q) {
         uint32_t f[8];
         group_fields(q, f);
@@ -421,6 +422,11 @@ __device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, c
     uint32_t a0, a1, b0, b1;
     tab_load(0, a0, a1);
     tab_load(1, b0, b1);
+    // The caller's set-up of its LDS (the first run bounds are in flight
+    // meanwhile); the barrier publishes it.
+    prologue();
+    if (threadIdx.x == 0) q_n = 0;
+    __syncthreads();
     for (uint32_t st = 0; 2u * st * BPS < per_wave; ++st) {
         const uint32_t Sa = a0, Ea = a1, Sb = b0, Eb = b1;
         tab_load(2u * st + 2u, a0, a1);

@@ -196,11 +196,13 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
     const uint32_t t = threadIdx.x;
     const uint32_t b = (blockIdx.x % 8) * build_per_xcd(g.NB) + blockIdx.x / 8;
     if (b >= g.NB) return;
-    for (uint32_t i = t; i < BK_KEYS * 512u; i += BUILD_NT) reinterpret_cast<uint4*>(bits)[i] = make_uint4(0, 0, 0, 0);
-    __syncthreads();
     const uint32_t wave = t >> 6;
     const uint32_t lane = __lane_id();
     walk_groups(part, tab, g, b, wave, lane,
+                [&] {
+                    for (uint32_t i = t; i < BK_KEYS * 512u; i += BUILD_NT)
+                        reinterpret_cast<uint4*>(bits)[i] = make_uint4(0, 0, 0, 0);
+                },
                 [&](uint32_t, uint32_t, uint32_t, uint32_t n, const uint32_t (&f)[8]) {
 #pragma unroll
                     for (uint32_t k = 0; k < 8u; ++k) {
