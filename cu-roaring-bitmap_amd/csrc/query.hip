@@ -324,6 +324,7 @@ __global__ __launch_bounds__(BUILD_NT) void qp_answer(const uint32_t* __restrict
                                                       uint8_t* __restrict__ ans)
 {
     __shared__ alignas(16) uint32_t bits[BK_KEYS * 2048u];  // the bucket's 16 containers, 128 KiB
+    __shared__ GroupQueue queue;
     const uint32_t t = threadIdx.x;
     const uint32_t b = (blockIdx.x % 8) * build_per_xcd(g.NB) + blockIdx.x / 8;
     if (b >= g.NB) return;
@@ -334,7 +335,7 @@ __global__ __launch_bounds__(BUILD_NT) void qp_answer(const uint32_t* __restrict
     // All 8 answers of a group go into one byte that only this lane writes:
     // fields past the run answer into b's padding, and any 20-bit value
     // indexes the LDS image.
-    walk_groups(part, tab, g, b, wave, lane,
+    walk_groups(part, tab, g, b, wave, lane, queue,
                 [&] {  // wave w loads container w of the bucket (zeros past the last key)
                     if (key < g.K) {
                         qp_load_container(v, key, bits + wave * 2048u, lane);
@@ -419,7 +420,7 @@ int contains_partitioned(const GpuRoaringView& v, const uint32_t* d_ids, uint64_
         CR_TIMED("qp_tile_sort", s);
         ids_tile_sort<true><<<g.G, TS_NT, 0, s>>>(d_ids, g, sc.at<uint32_t>(o_part), sc.at<uint16_t>(o_tab),
                                                   sc.at<uint32_t>(o_gmax), sc.at<IdsTotals>(o_tot),
-                                                  sc.at<uint16_t>(o_perm));
+                                                  sc.at<uint16_t>(o_perm), nullptr);
     }
     CR_LAUNCH_CHECK();
     {

@@ -42,6 +42,7 @@ struct IdsTotals {
     unsigned long long total;  // distinct ids (or complement count)
     uint32_t done;    // rank workgroups finished
     uint32_t absent;  // build workgroups that found a key of the universe with no id
+    uint32_t ticket[8];  // the build's next bucket (in its order) per XCD's range
 };
 
 struct IdsGeom {
@@ -65,14 +66,18 @@ struct IdsGeom {
 // (within tile t) of the tile's p-th id, padding ids included: rank r in
 // bucket b, whose run starts at sorted position S, gets ((S + 7 b + 7) & ~7) + r,
 // so every bucket's positions start at a multiple of 8 and no two buckets'
-// positions share a group of 8.
+// positions share a group of 8.  With `wg_count` non-null, row w (NB u32)
+// receives the number of ids workgroup w sorted into each real bucket, which
+// the build sums into per-bucket totals to order its buckets.
 template <bool PERM>
 __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restrict__ ids, IdsGeom g,
                                                        uint32_t* __restrict__ part, uint16_t* __restrict__ tab,
-                                                       uint32_t* gmax, IdsTotals* tot, uint16_t* __restrict__ perm)
+                                                       uint32_t* gmax, IdsTotals* tot, uint16_t* __restrict__ perm,
+                                                       uint32_t* __restrict__ wg_count)
 {
     __shared__ uint32_t buf[TILE];
     __shared__ uint32_t cnt[MAX_BUCKETS + 1];
+    __shared__ uint32_t acc[PERM ? 1 : MAX_BUCKETS];  // this workgroup's ids per bucket, over its tiles
     // A block's run-table rows are staged here and written as one contiguous
     // copy when the block ends (up to STAGE_NB buckets; more write directly).
     __shared__ uint4 stage[STAGE_NB + 1];  // row i = TB u16 starts of bucket i
@@ -91,7 +96,14 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
             tot->max_id = 0;
             tot->done = 0;
             tot->absent = 0;
+#pragma unroll
+            for (uint32_t x = 0; x < 8; ++x) tot->ticket[x] = 0;
         }
+    }
+    constexpr uint32_t BPT = MAX_BUCKETS / TS_NT;  // buckets scanned per thread: t * BPT + q
+    if constexpr (!PERM) {
+#pragma unroll
+        for (uint32_t q = 0; q < BPT; ++q) acc[t * BPT + q] = 0;  // each thread's own entries: no barrier needed
     }
     uint32_t mx = 0;
     // Returns whether the tile is partial; a partial tile's maximum is taken
@@ -200,13 +212,13 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
             }
         }
         __syncthreads();
-        constexpr uint32_t BPT = MAX_BUCKETS / TS_NT;  // buckets scanned per thread
         uint32_t cv[BPT], cs = 0;
 #pragma unroll
         for (uint32_t q = 0; q < BPT; ++q) {
             const uint32_t bq = t * BPT + q;
             cv[q] = bq < NB ? cnt[bq] : 0u;
             cs += cv[q];
+            if constexpr (!PERM) atomicAdd(&acc[bq], cv[q]);  // no return: the wave does not wait
         }
         uint32_t total;  // ids of the real buckets; the sentinel's follow
         uint32_t st = block_excl_scan<TS_NT>(cs, lds, total);
@@ -312,6 +324,8 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
     if (lane == 0) atomicMax(&s_max, mx);
     __syncthreads();
     if (t == 0) gmax[blockIdx.x] = s_max;  // per-workgroup partials: nothing here needs zeroed memory
+    if (!PERM && wg_count != nullptr)
+        for (uint32_t i = t; i < NB; i += TS_NT) wg_count[static_cast<uint64_t>(blockIdx.x) * NB + i] = acc[i];
 }
 
 constexpr int BUILD_NT = 1024;
@@ -323,6 +337,11 @@ constexpr uint32_t BUILD_WAVES = BUILD_NT / 64;
 // every tile -- runs on one XCD, close in time, and that line comes from its L2.
 __host__ __device__ inline uint32_t build_per_xcd(uint32_t nb) { return (nb + 7) / 8; }
 inline uint32_t build_grid(uint32_t nb) { return 8 * build_per_xcd(nb); }
+// The persistent build: up to one workgroup per CU, none without a bucket.
+inline uint32_t build_grid_persistent(uint32_t nb, uint32_t cus)
+{
+    return 8 * std::min(build_per_xcd(nb), std::max(1u, cus / 8));
+}
 
 // Calls on_group(tile, S, j, n, f) for every group of 8 consecutive fields of
 // bucket b's run in every tile: the run holds sorted positions [S, E) of the
@@ -346,12 +365,20 @@ inline uint32_t build_grid(uint32_t nb) { return 8 * build_per_xcd(nb); }
 // any is handed on.  A run of more than GROUP_LONG groups (sorted or clustered
 // ids: a bucket's fields in a few tiles, all in one wave's blocks) is queued in
 // LDS and its groups dealt to all sixteen waves after the walk; one that finds
-// the queue full is dealt with its wave's other runs.
+// the queue full is dealt with its wave's other runs.  `queue` is the
+// workgroup's LDS queue.
 // Measured against a walk of 16-word windows by 4-lane groups (100M ids at
 // 2^30, ids_build): uniform ids 0.124 against 0.125-0.131 ms; sorted ids 0.101
 // against 0.19 ms; sorted groups of 4096 0.106 against 0.196 ms.
 constexpr uint32_t GROUP_LONG = 64;
 constexpr uint32_t GROUP_QCAP = 2048;  // 16 KiB of LDS beside the callers' 128 KiB
+
+// LDS queue of long runs, declared by walk_groups' caller: one per
+// workgroup, whatever the number of walk_groups instances it inlines.
+struct GroupQueue {
+    uint2 ent[GROUP_QCAP];  // {tile, S | E << 16}
+    uint32_t n;
+};
 
 struct FieldGroup {
     uint32_t x[6];  // words w0 .. w0 + 5
@@ -392,10 +419,10 @@ __device__ __forceinline__ void group_fields(const FieldGroup& q, uint32_t (&f)[
 template <class Prologue, class OnGroup>
 __device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, const uint16_t* __restrict__ tab,
                                             const IdsGeom& g, uint32_t b, uint32_t wave, uint32_t lane,
-                                            Prologue prologue, OnGroup on_group)
+                                            GroupQueue& queue, Prologue prologue, OnGroup on_group)
 {
-    __shared__ uint2 q_ent[GROUP_QCAP];  // {tile, S | E << 16}
-    __shared__ uint32_t q_n;
+    uint2* q_ent = queue.ent;
+    uint32_t& q_n = queue.n;
     auto handle = [&](uint32_t tile, uint32_t S, uint32_t E, uint32_t j, const FieldGroup& q) {
         uint32_t f[8];
         group_fields(q, f);
@@ -442,13 +469,8 @@ __device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, c
             if (slot < GROUP_QCAP) q_ent[slot] = make_uint2(tb, Sb | (Eb << 16)), Gb = 0;
         }
         const uint32_t G = Ga + Gb;
-        uint32_t P = G;  // exclusive scan of G over the wave
-#pragma unroll
-        for (uint32_t d = 1; d < 64u; d <<= 1) {
-            const uint32_t y = __shfl_up(P, d, 64);
-            if (lane >= d) P += y;
-        }
-        const uint32_t T = static_cast<uint32_t>(__shfl(P, 63, 64));
+        uint32_t P = wave_incl_scan(G);  // then exclusive: the lane's first group
+        const uint32_t T = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(P), 63));
         P -= G;
         for (uint32_t r0 = 0; 64u * r0 < T; r0 += 8u) {
             uint32_t w[8][6], tl[8], ss[8], ee[8], jj[8];
