@@ -211,6 +211,38 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* lds, u
     return base + incl - v;
 }
 
+// K block-wide exclusive scans with one LDS exchange: each wave scans its K
+// values with DPP moves, lane 63 publishes the wave totals, and every thread
+// adds the totals of the waves before its own.  `lds` needs K * NT/64 slots;
+// v[k] becomes value k's exclusive prefix and total[k] its block total.
+template <int NT, int K>
+__device__ __forceinline__ void block_excl_scan_multi(uint32_t (&v)[K], uint32_t* lds, uint32_t (&total)[K])
+{
+    constexpr int NW = NT / 64;
+    const uint32_t w = threadIdx.x >> 6;
+    uint32_t incl[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) incl[k] = wave_incl_scan(v[k]);
+    if (__lane_id() == 63) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) lds[k * NW + w] = incl[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        uint32_t base = 0, t = 0;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            const uint32_t x = lds[k * NW + i];
+            base += (static_cast<uint32_t>(i) < w) ? x : 0u;
+            t += x;
+        }
+        total[k] = t;
+        v[k] = base + incl[k] - v[k];
+    }
+    __syncthreads();  // lds may be reused
+}
+
 // Ordered compaction helper: exclusive rank of `flag` among the block's lanes
 // (ballot per wave, wave counts through LDS).  `lds` needs NT/64 slots.
 template <int NT>

@@ -88,7 +88,7 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_classify(Side A, Side B, uint
 {
     __shared__ int32_t ia[PLAN_NT], ib[PLAN_NT];
     __shared__ uint32_t range[4];
-    __shared__ uint32_t red[PLAN_NT / 64];
+    __shared__ uint32_t red[C_N * (PLAN_NT / 64)];
     const uint32_t base = blockIdx.x * PLAN_NT;
     const uint32_t t = threadIdx.x;
     const uint32_t wv = t >> 6;  // waves 0-3: the key range of this group in A and in B
@@ -159,33 +159,38 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_classify(Side A, Side B, uint
     }
     if (rec.cat != CAT_NONE) cnt[C_ITEM] = 1;
     recs[base + t] = rec;
+    // The group's counters: wave sums (DPP), then one thread per counter over
+    // the waves -- a single barrier.
+    constexpr uint32_t NW = PLAN_NT / 64;
 #pragma unroll
     for (int k = 0; k < C_N; ++k) {
-        const uint32_t s = block_sum<PLAN_NT>(cnt[k], red);
-        if (t == 0) group_counts[blockIdx.x * C_N + k] = s;
+        const uint32_t ws = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(cnt[k])), 63));
+        if (__lane_id() == 0) red[k * NW + wv] = ws;
+    }
+    __syncthreads();
+    if (t < C_N) {
+        uint32_t sum = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < NW; ++i) sum += red[t * NW + i];
+        group_counts[blockIdx.x * C_N + t] = sum;
     }
 }
 
 // ---- plan pass 2: slot assignment in key order -----------------------------
 __global__ __launch_bounds__(PLAN_NT) void so_plan_assign(const KeyRec* recs, const uint32_t* group_counts,
-                                                          Item* items, Totals* totals, uint32_t* tile_keep,
-                                                          uint32_t n_tiles, Caps caps)
+                                                          Item* items, Totals* totals, Caps caps)
 {
     __shared__ uint32_t gbase[C_N], gtot[C_N];
-    __shared__ uint32_t scan_lds[PLAN_NT / 64];
+    __shared__ uint32_t scan_lds[8 * (PLAN_NT / 64)];
     const uint32_t t = threadIdx.x;
-    if (t < C_N) {
-        uint32_t b = 0, s = 0;
-        for (uint32_t g = 0; g < PLAN_GROUPS; ++g) {
-            const uint32_t v = group_counts[g * C_N + t];
-            if (g < blockIdx.x) b += v;
-            s += v;
-        }
-        gbase[t] = b;
-        gtot[t] = s;
-    }
-    if (blockIdx.x == 0) {
-        for (uint32_t i = t; i < n_tiles; i += PLAN_NT) tile_keep[i] = 0;
+    static_assert(PLAN_GROUPS == 64 && C_N <= PLAN_NT / 64, "one wave per counter, one lane per group");
+    if ((t >> 6) < C_N) {  // wave k: counter k over the 64 groups, before this one and in total
+        const uint32_t k = t >> 6, g = __lane_id();
+        const uint32_t v = group_counts[g * C_N + k];
+        const uint32_t sb = static_cast<uint32_t>(
+            __builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(g < blockIdx.x ? v : 0u)), 63));
+        const uint32_t st = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(v)), 63));
+        if (g == 0) gbase[k] = sb, gtot[k] = st;
     }
     __syncthreads();
     if (blockIdx.x == 0 && t < C_N) totals->c[t] = gtot[t];
@@ -198,16 +203,20 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_assign(const KeyRec* recs, co
     const uint32_t key = blockIdx.x * PLAN_NT + t;
     const KeyRec rec = recs[key];
     const uint8_t cat = rec.cat;
-    // Per-thread contribution to the counters that define positions.
-    uint32_t tot;
-    const uint32_t item_pos = gbase[C_ITEM] + block_excl_scan<PLAN_NT>(cat != CAT_NONE ? 1u : 0u, scan_lds, tot);
-    const uint32_t p_bb = block_excl_scan<PLAN_NT>(cat == CAT_BB, scan_lds, tot);
-    const uint32_t p_mx = block_excl_scan<PLAN_NT>(cat == CAT_MIXED, scan_lds, tot);
-    const uint32_t p_cb = block_excl_scan<PLAN_NT>(cat == CAT_COPY_BMP, scan_lds, tot);
-    const uint32_t p_ba = block_excl_scan<PLAN_NT>(cat == CAT_BA ? rec.size : 0u, scan_lds, tot);
-    const uint32_t p_aa = block_excl_scan<PLAN_NT>(cat == CAT_AA ? rec.size : 0u, scan_lds, tot);
-    const uint32_t p_ca = block_excl_scan<PLAN_NT>(cat == CAT_COPY_ARR ? rec.size : 0u, scan_lds, tot);
-    const uint32_t p_cr = block_excl_scan<PLAN_NT>(cat == CAT_COPY_RUN ? rec.size : 0u, scan_lds, tot);
+    // Per-thread contributions to the counters that define positions, scanned
+    // over the group together.
+    uint32_t pv[8] = {cat != CAT_NONE ? 1u : 0u,
+                      cat == CAT_BB ? 1u : 0u,
+                      cat == CAT_MIXED ? 1u : 0u,
+                      cat == CAT_COPY_BMP ? 1u : 0u,
+                      cat == CAT_BA ? rec.size : 0u,
+                      cat == CAT_AA ? rec.size : 0u,
+                      cat == CAT_COPY_ARR ? rec.size : 0u,
+                      cat == CAT_COPY_RUN ? rec.size : 0u};
+    uint32_t ptot[8];
+    block_excl_scan_multi<PLAN_NT, 8>(pv, scan_lds, ptot);
+    const uint32_t item_pos = gbase[C_ITEM] + pv[0];
+    const uint32_t p_bb = pv[1], p_mx = pv[2], p_cb = pv[3], p_ba = pv[4], p_aa = pv[5], p_ca = pv[6], p_cr = pv[7];
     if (cat == CAT_NONE) return;
     uint32_t slot = 0;
     switch (cat) {
@@ -475,7 +484,7 @@ __device__ __forceinline__ void mix_scatter(const Side& S, const MixMeta& m, uin
 template <uint32_t OP>
 __global__ __launch_bounds__(EXEC_NT) void so_exec(Side A, Side B, const Item* items, const Totals* totals,
                                                    uint64_t* out_bmp, uint16_t* out_arr, uint16_t* out_run,
-                                                   uint32_t* item_card, uint32_t* tile_keep)
+                                                   uint32_t* item_card)
 {
     __shared__ alignas(16) uint32_t lds[4096];  // 16 KiB: two array images, or a staged array
     __shared__ uint32_t red[EXEC_NT / 64];
@@ -839,7 +848,7 @@ __device__ void write_host_totals(const Totals* totals, uint32_t n_out, uint32_t
 // total into the pinned slot); with no items or an overflowed plan workgroup 0
 // does, and nothing is compacted.
 __global__ __launch_bounds__(PLAN_NT) void so_compact(const Item* items, const uint32_t* item_card,
-                                                      const uint32_t* tile_keep, Totals* totals, uint16_t* keys,
+                                                      Totals* totals, uint16_t* keys,
                                                       uint8_t* types, uint32_t* offsets, uint16_t* cards,
                                                       SetOpHost* host)
 {
@@ -855,12 +864,23 @@ __global__ __launch_bounds__(PLAN_NT) void so_compact(const Item* items, const u
     const uint32_t t = threadIdx.x;
     const bool last = (tile + 1) * PLAN_NT >= n_items;
     uint32_t invalid = 0;
-    {  // kept items before this tile, counted cooperatively (the last tile also counts invalid ones)
+    {  // kept items before this tile, counted cooperatively (the last tile also counts invalid ones):
+       // 16-byte loads of the cards (whole tiles of PLAN_NT, 256-byte aligned), four in flight a thread
         uint32_t b = 0;
-        for (uint32_t i = t; i < tile * PLAN_NT; i += PLAN_NT) {
-            const uint32_t x = item_card[i];
-            b += x >> 31;
-            invalid += (x >> 30) & 1u;
+        const uint4* c4 = reinterpret_cast<const uint4*>(item_card);
+        const uint32_t n4 = tile * (PLAN_NT / 4);
+        for (uint32_t i0 = t; i0 < n4; i0 += 4u * PLAN_NT) {
+            uint4 x[4];
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; ++k) {
+                const uint32_t j = i0 + k * PLAN_NT;
+                x[k] = j < n4 ? c4[j] : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; ++k) {
+                b += (x[k].x >> 31) + (x[k].y >> 31) + (x[k].z >> 31) + (x[k].w >> 31);
+                invalid += ((x[k].x >> 30) & 1u) + ((x[k].y >> 30) & 1u) + ((x[k].z >> 30) & 1u) + ((x[k].w >> 30) & 1u);
+            }
         }
         b = block_sum<PLAN_NT>(b, lds);
         if (t == 0) s_base = b;
@@ -1021,7 +1041,6 @@ struct SetOpPlan {
     Item* items;
     Totals* tot;
     uint32_t* icard;
-    uint32_t* tile_keep;
     uint32_t n_tiles;
 };
 
@@ -1035,14 +1054,12 @@ static int plan_set_operation(const Side& A, const Side& B, uint32_t op, uint32_
     const size_t o_items = c.add(sizeof(Item) * bound);
     const size_t o_tot = c.add(sizeof(Totals));
     const size_t o_card = c.add(sizeof(uint32_t) * bound);
-    const size_t o_tile = c.add(sizeof(uint32_t) * P.n_tiles);
     CR_RET(P.sc.alloc(c.total, s));
     KeyRec* recs = P.sc.at<KeyRec>(o_recs);
     uint32_t* gc = P.sc.at<uint32_t>(o_gc);
     P.items = P.sc.at<Item>(o_items);
     P.tot = P.sc.at<Totals>(o_tot);
     P.icard = P.sc.at<uint32_t>(o_card);
-    P.tile_keep = P.sc.at<uint32_t>(o_tile);
     {
         CR_TIMED("so_plan_classify", s);
         so_plan_classify<<<PLAN_GROUPS, PLAN_NT, 0, s>>>(A, B, op, recs, gc);
@@ -1050,7 +1067,7 @@ static int plan_set_operation(const Side& A, const Side& B, uint32_t op, uint32_
     CR_LAUNCH_CHECK();
     {
         CR_TIMED("so_plan_assign", s);
-        so_plan_assign<<<PLAN_GROUPS, PLAN_NT, 0, s>>>(recs, gc, P.items, P.tot, P.tile_keep, P.n_tiles, caps);
+        so_plan_assign<<<PLAN_GROUPS, PLAN_NT, 0, s>>>(recs, gc, P.items, P.tot, caps);
     }
     CR_LAUNCH_CHECK();
     return CR_OK;
@@ -1065,12 +1082,10 @@ static int plan_bitmap_keyed(const cr_gpu_roaring* a, const cr_gpu_roaring* b, u
     const size_t o_items = c.add(sizeof(Item) * bound);
     const size_t o_tot = c.add(sizeof(Totals));
     const size_t o_card = c.add(sizeof(uint32_t) * bound);
-    const size_t o_tile = c.add(sizeof(uint32_t) * P.n_tiles);
     CR_RET(P.sc.alloc(c.total, s));
     P.items = P.sc.at<Item>(o_items);
     P.tot = P.sc.at<Totals>(o_tot);
     P.icard = P.sc.at<uint32_t>(o_card);
-    P.tile_keep = P.sc.at<uint32_t>(o_tile);
     {
         CR_TIMED("so_plan_bitmap", s);
         const uint32_t len_a = a->max_key + 1u, len_b = b->max_key + 1u;
@@ -1118,26 +1133,26 @@ static int exec_set_operation(const Side& A, const Side& B, uint32_t op, uint32_
         switch (op) {
         case CR_AND:
             so_exec<CR_AND><<<g, EXEC_NT, 0, s>>>(A, B, P.items, P.tot, out->bitmap_data, out->array_data,
-                                                  out->run_data, P.icard, P.tile_keep);
+                                                  out->run_data, P.icard);
             break;
         case CR_OR:
             so_exec<CR_OR><<<g, EXEC_NT, 0, s>>>(A, B, P.items, P.tot, out->bitmap_data, out->array_data,
-                                                 out->run_data, P.icard, P.tile_keep);
+                                                 out->run_data, P.icard);
             break;
         case CR_ANDNOT:
             so_exec<CR_ANDNOT><<<g, EXEC_NT, 0, s>>>(A, B, P.items, P.tot, out->bitmap_data, out->array_data,
-                                                     out->run_data, P.icard, P.tile_keep);
+                                                     out->run_data, P.icard);
             break;
         default:
             so_exec<CR_XOR><<<g, EXEC_NT, 0, s>>>(A, B, P.items, P.tot, out->bitmap_data, out->array_data,
-                                                  out->run_data, P.icard, P.tile_keep);
+                                                  out->run_data, P.icard);
             break;
         }
     }
     CR_LAUNCH_CHECK();
     {
         CR_TIMED("so_compact", s);
-        so_compact<<<std::max(1u, P.n_tiles), PLAN_NT, 0, s>>>(P.items, P.icard, P.tile_keep, P.tot, out->keys,
+        so_compact<<<std::max(1u, P.n_tiles), PLAN_NT, 0, s>>>(P.items, P.icard, P.tot, out->keys,
                                                                out->types, out->offsets, out->cardinalities, host);
     }
     CR_LAUNCH_CHECK();
