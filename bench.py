@@ -830,10 +830,11 @@ def sparse_arrays(cr, density, seed):
 
 
 def conversions(torch, cr, flush, bitmaps):
-    """decompress_to_bitset, enumerate_ids, promote_to_bitmap and the deep copy on
-    2^30 bitmaps, cold.  Algorithmic bytes: the container payloads read (8192 B per
-    bitmap, 2 B per array value), 9 B of metadata per container, plus what the call
-    writes (4 B per bitset word, 8 B per id, 8192 B per promoted container, the copy)."""
+    """decompress_to_bitset, enumerate_ids, promote_to_bitmap, the deep copy and
+    cardinality on 2^30 bitmaps, cold.  Algorithmic bytes: the container payloads
+    read (8192 B per bitmap, 2 B per array value), 9 B of metadata per container,
+    plus what the call writes (4 B per bitset word, 8 B per id, 8192 B per promoted
+    container, the copy; cardinality writes one count)."""
     res = {}
     for name, g in bitmaps.items():
         n = g.n_containers
@@ -849,6 +850,7 @@ def conversions(torch, cr, flush, bitmaps):
             "promote_to_bitmap": (lambda: kept.append(cr.promote_to_bitmap(g)),
                                   payload + 8192 * n + 9 * n + 2 * (g.max_key + 1), "cv_promote", True),
             "deep_copy": (lambda: kept.append(cr.deep_copy(g)), 2 * (payload + kidx), "cv_copy", True),
+            "cardinality": (lambda: cr.cardinality(g), payload, "cv_card_sum", None),
         }
         r = {"n_containers": n, "n_bitmap": g.n_bitmap_containers, "n_array": g.n_array_containers, "ids": n_ids}
         for cname, (fn, nbytes, kname, frees) in cases.items():

@@ -147,14 +147,28 @@ __global__ __launch_bounds__(CV_NT) void cv_enum_count(cr_gpu_roaring r, uint64_
 }
 
 // Sum of the containers' counts into *total (zeroed by the caller's stream
-// order): one non-returning atomic per wave.
-__global__ __launch_bounds__(CV_NT) void cv_card_sum(cr_gpu_roaring r, unsigned long long* total)
+// order).  Each wave takes containers wave, wave + all waves, ...; the
+// workgroup's waves meet in LDS and one non-returning atomic a workgroup adds
+// them up (an atomic a container, all on the one total, serialised: 16384 of
+// them took 80-200 us).
+constexpr int CS_NT = 1024;
+
+__global__ __launch_bounds__(CS_NT) void cv_card_sum(cr_gpu_roaring r, unsigned long long* total)
 {
-    const uint32_t c = (blockIdx.x * CV_NT + threadIdx.x) >> 6;
+    __shared__ unsigned long long part[CS_NT / 64];
+    const uint32_t wave = threadIdx.x >> 6;
     const uint32_t lane = __lane_id();
-    if (c >= r.n_containers) return;
-    const uint32_t n = container_count(r, c, lane);
-    if (lane == 0 && n) atomicAdd(total, static_cast<unsigned long long>(n));
+    const uint32_t nw = gridDim.x * (CS_NT / 64);
+    unsigned long long n = 0;
+    for (uint32_t c = blockIdx.x * (CS_NT / 64) + wave; c < r.n_containers; c += nw) n += container_count(r, c, lane);
+    if (lane == 0) part[wave] = n;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long s = 0;
+#pragma unroll
+        for (int i = 0; i < CS_NT / 64; ++i) s += part[i];
+        if (s) atomicAdd(total, s);
+    }
 }
 
 __global__ void cv_zero_u64(unsigned long long* p) { *p = 0; }
@@ -686,7 +700,8 @@ extern "C" int cr_cardinality(const cr_gpu_roaring* bm, cr_stream_t stream, uint
         {
             CR_TIMED("cv_card_sum", s);
             cv_zero_u64<<<1, 1, 0, s>>>(d_total);
-            cv_card_sum<<<(bm->n_containers + 3) / 4, CV_NT, 0, s>>>(*bm, d_total);
+            const uint32_t grid = std::min<uint32_t>((bm->n_containers + CS_NT / 64 - 1) / (CS_NT / 64), 2 * num_cus());
+            cv_card_sum<<<grid, CS_NT, 0, s>>>(*bm, d_total);
         }
         CR_LAUNCH_CHECK();
         CR_RET(read_back(&stored, d_total, sizeof(stored), s));
