@@ -192,7 +192,9 @@ def _skewed_ids(case, rng):
     """Inputs whose tiles each fall in a few key buckets (16 keys a bucket):
     long runs per (bucket, tile), shared by the whole build workgroup.
     "overflow" gives the single bucket of U = 2^20 more such tiles (2054) than
-    the workgroup's queue holds (2048); the rest are finished by their wave."""
+    the workgroup's queue holds (2048); the rest are finished by their wave.
+    "heavy" puts half of 3M ids over 2^30 into four buckets, which the
+    persistent build takes first among its ticketed buckets."""
     if case == "sorted":
         U = 1 << 26
         return U, np.sort(rng.integers(0, U, 24576 * 20 + 77, dtype=np.uint64)).astype(np.uint32)
@@ -201,18 +203,26 @@ def _skewed_ids(case, rng):
         win = rng.integers(0, U >> 16, 150, dtype=np.uint64)
         off = np.sort(rng.integers(0, 65536, (150, 4096), dtype=np.uint64), axis=1)
         return U, ((win[:, None] << 16) + off).reshape(-1).astype(np.uint32)
+    if case == "heavy":  # a few buckets hold half the ids: the build's ordered tickets carry them
+        U = 1 << 30
+        uni = rng.integers(0, U, 1_500_000, dtype=np.uint64)
+        # buckets 356, 704 and 1023 sit past their XCD range's static first round
+        # (32 of 128 buckets at 2^30), bucket 131 inside it
+        heavy = [(b << 20) + rng.integers(0, 1 << 20, 375_000, dtype=np.uint64) for b in (131, 356, 704, 1023)]
+        ids = np.concatenate([uni] + heavy)
+        return U, ids[rng.permutation(ids.size)].astype(np.uint32)
     U = 1 << 20
     allowed = np.nonzero(rng.random(U) < 0.9)[0].astype(np.uint32)
     return U, allowed[rng.integers(0, allowed.size, 24576 * 2054 + 5)]
 
 
-@pytest.mark.parametrize("case", ["sorted", "clustered", "overflow"])
+@pytest.mark.parametrize("case", ["sorted", "clustered", "overflow", "heavy"])
 def test_upload_and_partitioned_skewed(gpu, case):
     """upload_from_ids and mode 4 on inputs whose tiles hit few buckets: the
     walk's queued long runs, and its in-wave path once the queue is full."""
     _say("skewed ids", case)
     torch = _torch()
-    rng = np.random.default_rng({"sorted": 70, "clustered": 71, "overflow": 72}[case])
+    rng = np.random.default_rng({"sorted": 70, "clustered": 71, "overflow": 72, "heavy": 73}[case])
     U, ids = _skewed_ids(case, rng)
     want = orc.upload_from_ids(ids, U, orc.PROMOTE_AUTO, auto_l2(gpu))
     dq = _dev_u32(ids)
