@@ -43,9 +43,18 @@ __device__ inline void expand_img(const uint8_t type, const uint16_t* data, uint
     }
     __syncthreads();
     if (type == CR_ARRAY) {
-        for (uint32_t i = t; i < card; i += NT) {
-            const uint32_t v = data[i];
-            atomicOr(&w[v >> 5], 1u << (v & 31u));
+        // eight values a thread loaded before any is set: one load latency per
+        // 8 NT values rather than one per NT
+        for (uint32_t i0 = t; i0 < card; i0 += 8u * NT) {
+            uint32_t v[8];
+#pragma unroll
+            for (uint32_t k = 0; k < 8u; ++k) {
+                const uint32_t i = i0 + k * NT;
+                v[k] = i < card ? static_cast<uint32_t>(data[i]) : 0xFFFFFFFFu;
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < 8u; ++k)
+                if (v[k] != 0xFFFFFFFFu) atomicOr(&w[v[k] >> 5], 1u << (v[k] & 31u));
         }
         __syncthreads();
         return;
