@@ -276,8 +276,16 @@ __global__ __launch_bounds__(CV_NT) void cv_enum_write(cr_gpu_roaring r, const u
     if (type == CR_ARRAY) {
         const uint16_t* arr = r.array_data + off / 2u;
         const uint32_t card = r.cardinalities[c];
-        for (uint32_t i = t; i < card; i += CV_NT)
-            if (start + i < cap) st_stream(out + start + i, base | arr[i]);
+        for (uint32_t i0 = t; i0 < card; i0 += 4u * CV_NT) {  // four values a thread in flight
+            uint32_t x[4];
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; ++k) x[k] = i0 + CV_NT * k < card ? static_cast<uint32_t>(arr[i0 + CV_NT * k]) : 0u;
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; ++k) {
+                const uint32_t i = i0 + CV_NT * k;
+                if (i < card && start + i < cap) st_stream(out + start + i, base | x[k]);
+            }
+        }
         return;
     }
     const uint32_t* words;
@@ -350,8 +358,16 @@ __global__ __launch_bounds__(CV_NT) void cv_enum_write_arrays(cr_gpu_roaring r, 
     const uint32_t card = r.cardinalities[c];
     const int64_t base = static_cast<int64_t>(r.keys[c]) << 16;
     const uint64_t start = starts[c];
-    for (uint32_t i = lane; i < card; i += 64)
-        if (start + i < cap) st_stream(out + start + i, base | arr[i]);
+    for (uint32_t i0 = lane; i0 < card; i0 += 8u * 64u) {  // eight values a lane in flight
+        uint32_t x[8];
+#pragma unroll
+        for (uint32_t k = 0; k < 8u; ++k) x[k] = i0 + 64u * k < card ? static_cast<uint32_t>(arr[i0 + 64u * k]) : 0u;
+#pragma unroll
+        for (uint32_t k = 0; k < 8u; ++k) {
+            const uint32_t i = i0 + 64u * k;
+            if (i < card && start + i < cap) st_stream(out + start + i, base | x[k]);
+        }
+    }
 }
 
 // ---- promote_to_bitmap ------------------------------------------------------

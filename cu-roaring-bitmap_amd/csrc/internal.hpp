@@ -211,15 +211,17 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* lds, u
     return base + incl - v;
 }
 
-// K block-wide exclusive scans with one LDS exchange: each wave scans its K
-// values with DPP moves, lane 63 publishes the wave totals, and every thread
-// adds the totals of the waves before its own.  `lds` needs K * NT/64 slots;
-// v[k] becomes value k's exclusive prefix and total[k] its block total.
+// K block-wide exclusive scans: each wave scans its K values with DPP moves
+// and lane 63 publishes the wave totals; K * NT/64 threads then turn them into
+// per-wave prefixes (and the K block totals), and every thread adds its
+// wave's prefix.  `lds` needs 2 K NT/64 + K slots; v[k] becomes value k's
+// exclusive prefix and total[k] its block total.
 template <int NT, int K>
 __device__ __forceinline__ void block_excl_scan_multi(uint32_t (&v)[K], uint32_t* lds, uint32_t (&total)[K])
 {
     constexpr int NW = NT / 64;
-    const uint32_t w = threadIdx.x >> 6;
+    static_assert(K * NW <= NT, "one thread per (value, wave)");
+    const uint32_t t = threadIdx.x, w = t >> 6;
     uint32_t incl[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) incl[k] = wave_incl_scan(v[k]);
@@ -228,17 +230,23 @@ __device__ __forceinline__ void block_excl_scan_multi(uint32_t (&v)[K], uint32_t
         for (int k = 0; k < K; ++k) lds[k * NW + w] = incl[k];
     }
     __syncthreads();
+    if (t < static_cast<uint32_t>(K * NW)) {  // thread (k, i): the totals of value k's waves before wave i
+        const uint32_t k = t / NW, i = t % NW;
+        uint32_t pre = 0, all = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < static_cast<uint32_t>(NW); ++j) {
+            const uint32_t x = lds[k * NW + j];
+            pre += j < i ? x : 0u;
+            all += x;
+        }
+        lds[K * NW + t] = pre;
+        if (i == 0) lds[2 * K * NW + k] = all;
+    }
+    __syncthreads();
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        uint32_t base = 0, t = 0;
-#pragma unroll
-        for (int i = 0; i < NW; ++i) {
-            const uint32_t x = lds[k * NW + i];
-            base += (static_cast<uint32_t>(i) < w) ? x : 0u;
-            t += x;
-        }
-        total[k] = t;
-        v[k] = base + incl[k] - v[k];
+        v[k] = lds[K * NW + k * NW + w] + incl[k] - v[k];
+        total[k] = lds[2 * K * NW + k];
     }
     __syncthreads();  // lds may be reused
 }

@@ -278,9 +278,13 @@ __device__ void qp_load_container(const GpuRoaringView& v, uint32_t key, uint32_
     if (idx < 0) return;
     if (type == CR_ARRAY) {  // the wave's LDS operations retire in order: the zeros land first
         const uint16_t* arr = v.array_data + (off >> 1);
-        for (uint32_t i = lane; i < card; i += 64) {
-            const uint32_t x = arr[i];
-            atomicOr(&w[x >> 5], 1u << (x & 31u));
+        for (uint32_t i0 = lane; i0 < card; i0 += 8u * 64u) {  // eight values a lane in flight
+            uint32_t x[8];
+#pragma unroll
+            for (uint32_t k = 0; k < 8u; ++k) x[k] = i0 + 64u * k < card ? static_cast<uint32_t>(arr[i0 + 64u * k]) : ~0u;
+#pragma unroll
+            for (uint32_t k = 0; k < 8u; ++k)
+                if (x[k] != ~0u) atomicOr(&w[x[k] >> 5], 1u << (x[k] & 31u));
         }
     } else if (type == CR_RUN) {
         // Lane l owns words [32 l, 32 l + 32) (bits [1024 l, 1024 l + 1024)):

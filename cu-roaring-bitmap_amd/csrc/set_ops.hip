@@ -181,7 +181,7 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_assign(const KeyRec* recs, co
                                                           Item* items, Totals* totals, Caps caps)
 {
     __shared__ uint32_t gbase[C_N], gtot[C_N];
-    __shared__ uint32_t scan_lds[8 * (PLAN_NT / 64)];
+    __shared__ uint32_t scan_lds[2 * 8 * (PLAN_NT / 64) + 8];
     const uint32_t t = threadIdx.x;
     static_assert(PLAN_GROUPS == 64 && C_N <= PLAN_NT / 64, "one wave per counter, one lane per group");
     if ((t >> 6) < C_N) {  // wave k: counter k over the 64 groups, before this one and in total
@@ -475,9 +475,13 @@ __device__ __forceinline__ Chunks2 mix_words(const Side& S, const MixMeta& m, ui
 __device__ __forceinline__ void mix_scatter(const Side& S, const MixMeta& m, uint32_t* img)
 {
     const uint16_t* vals = S.arr + (m.off >> 1);
-    for (uint32_t i = threadIdx.x; i < m.card; i += EXEC_NT) {
-        const uint32_t v = vals[i];
-        atomicOr(&img[v >> 5], 1u << (v & 31u));
+    for (uint32_t i0 = threadIdx.x; i0 < m.card; i0 += 8u * EXEC_NT) {  // eight values a thread in flight
+        uint32_t v[8];
+#pragma unroll
+        for (uint32_t k = 0; k < 8u; ++k) v[k] = i0 + EXEC_NT * k < m.card ? static_cast<uint32_t>(vals[i0 + EXEC_NT * k]) : ~0u;
+#pragma unroll
+        for (uint32_t k = 0; k < 8u; ++k)
+            if (v[k] != ~0u) atomicOr(&img[v[k] >> 5], 1u << (v[k] & 31u));
     }
 }
 

@@ -45,7 +45,14 @@ __global__ __launch_bounds__(256) void expand_containers(const ExpandDesc* desc,
         __syncthreads();
         const uint16_t* p = reinterpret_cast<const uint16_t*>(raw + d.raw_off);
         if (d.type == CR_TC_ARRAY) {
-            for (uint32_t k = t; k < d.card; k += 256) atomicOr(&bm[p[k] >> 5], 1u << (p[k] & 31u));
+            for (uint32_t k0 = t; k0 < d.card; k0 += 8u * 256u) {  // eight values a thread in flight
+                uint32_t x[8];
+#pragma unroll
+                for (uint32_t j = 0; j < 8u; ++j) x[j] = k0 + 256u * j < d.card ? static_cast<uint32_t>(p[k0 + 256u * j]) : ~0u;
+#pragma unroll
+                for (uint32_t j = 0; j < 8u; ++j)
+                    if (x[j] != ~0u) atomicOr(&bm[x[j] >> 5], 1u << (x[j] & 31u));
+            }
         } else {
             for (uint32_t r = t; r < d.card; r += 256) {  // [start, start+len], src/upload.cpp:194-197
                 const uint32_t s = p[2 * r];
