@@ -135,7 +135,11 @@ __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 // stream of whole 8 KiB blocks runs at 6.7 TB/s with it and 4.0 TB/s without,
 // and a copy at 5.7 against 4.7 TB/s (the store needs the policy too).
 // Data read again soon by other waves (metadata, shared cache lines) keeps
-// ordinary loads.
+// ordinary loads.  So does data that the next kernel of the same call reads
+// again and that fits in the 256 MB Infinity Cache (the upload's packed tiles,
+// a bitset read twice): nontemporal loads and stores do not allocate there, so
+// ordinary stores (or loads) of it, beside nontemporal streams of everything
+// else, leave it in that cache for the second read.
 typedef uint32_t cr_v4u __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint4 ld_stream(const uint4* p)
@@ -151,6 +155,12 @@ __device__ __forceinline__ void st_stream(uint4* p, uint4 v)
 }
 
 __device__ __forceinline__ void st_stream(int64_t* p, int64_t v) { __builtin_nontemporal_store(v, p); }
+
+__device__ __forceinline__ void st_stream(uint2* p, uint2 v)
+{
+    __builtin_nontemporal_store(static_cast<uint64_t>(v.x) | (static_cast<uint64_t>(v.y) << 32),
+                                reinterpret_cast<uint64_t*>(p));
+}
 
 __device__ __forceinline__ uint32_t wave_sum(uint32_t v)
 {

@@ -67,7 +67,9 @@ __device__ uint32_t ps_image(const cr_gpu_roaring& r, uint32_t i, Image* img, in
             const uint4* s4 = reinterpret_cast<const uint4*>(src);
             uint4 v[2];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) v[j] = ld_stream(s4 + j * CV_NT + t);
+            // Ordinary loads: ps_plan's read keeps the payload in the Infinity
+            // Cache for ps_write's (60 -> 55 us on 16384 bitmaps).
+            for (int j = 0; j < 2; ++j) v[j] = s4[j * CV_NT + t];
 #pragma unroll
             for (int j = 0; j < 2; ++j) reinterpret_cast<uint4*>(img->w)[j * CV_NT + t] = v[j];
         } else {

@@ -56,7 +56,8 @@ struct IdsGeom {
 
 // Each workgroup takes blocks of TB tiles.  A tile is counting-sorted by
 // bucket in LDS and written back to its own slot of `part` (tile t at word
-// t * TILE_WORDS) as packed fields, a streaming write; `tab` row t holds the
+// t * TILE_WORDS) as packed fields (ordinary stores, so that the tiles stay in
+// the Infinity Cache for their reader); `tab` row t holds the
 // tile's bucket starts (NB + 1 u16, in fields).  An id whose bucket lies past
 // the universe's last goes to a sentinel bucket NB that is sorted after the
 // others and neither written nor built; the error is raised from the maximum
@@ -260,10 +261,12 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         }
         if constexpr (PERM) {  // the ids' sorted positions, in the order load_ids placed them
             uint16_t* pt = perm + static_cast<uint64_t>(tile) * TILE;
+            // Nontemporal: read only at the end of the call, in order, and kept
+            // out of the Infinity Cache, which then holds the packed tiles.
             if (tile_vec) {  // id j = 4 q + r sits at 4 (t + q TS_NT) + r: one 8-byte store per q
 #pragma unroll
                 for (uint32_t q = 0; q < TS_PER / 4; ++q)
-                    reinterpret_cast<uint2*>(pt)[t + q * TS_NT] = make_uint2(rk[2 * q], rk[2 * q + 1]);
+                    st_stream(reinterpret_cast<uint2*>(pt) + t + q * TS_NT, make_uint2(rk[2 * q], rk[2 * q + 1]));
             } else {  // id j sits at t + j TS_NT
 #pragma unroll
                 for (uint32_t j = 0; j < TS_PER; ++j)
@@ -317,7 +320,10 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         __syncthreads();
         uint4* dst = reinterpret_cast<uint4*>(part + static_cast<uint64_t>(tile) * TILE_WORDS);
         const uint32_t n4 = (FIELD_BITS * total + 127u) >> 7;
-        for (uint32_t u = t; u < n4; u += TS_NT) st_stream(dst + u, reinterpret_cast<const uint4*>(buf)[u]);
+        // Ordinary stores, so the packed tiles are kept in the Infinity Cache
+        // for the kernel that reads them next; the ids come in through
+        // nontemporal loads, which do not displace them.
+        for (uint32_t u = t; u < n4; u += TS_NT) dst[u] = reinterpret_cast<const uint4*>(buf)[u];
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(mx, o, 64)));

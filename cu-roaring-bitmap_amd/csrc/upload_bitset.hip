@@ -54,7 +54,9 @@ __global__ __launch_bounds__(BS_NT) void bs_count(const uint32_t* __restrict__ w
             const uint4* s4 = reinterpret_cast<const uint4*>(words + base);
             uint4 v[2];
 #pragma unroll
-            for (int h = 0; h < 2; ++h) v[h] = ld_stream(s4 + threadIdx.x + h * BS_NT);
+            // Ordinary loads: the bitset (U/8 bytes, 128 MiB at 2^30) stays in
+            // the Infinity Cache for bs_compact, which reads it again.
+            for (int h = 0; h < 2; ++h) v[h] = s4[threadIdx.x + h * BS_NT];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const uint32_t i0 = base + 4u * (threadIdx.x + h * BS_NT);
