@@ -33,6 +33,7 @@ static_assert(TILE <= 65535, "run starts are u16");
 // sort hands out whole blocks, so a block's rows fill up in one workgroup.
 constexpr uint32_t TB = 8;
 constexpr uint32_t STAGE_NB = 1024;  // run-table rows staged in LDS up to this many buckets
+constexpr uint32_t STAGE_W = STAGE_NB + 8;  // u16 per staged slot: buckets 0..STAGE_NB, 16-byte rows
 
 struct IdsTotals {
     uint32_t n_containers;
@@ -77,13 +78,15 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
                                                        uint32_t* __restrict__ wg_count)
 {
     __shared__ uint32_t buf[TILE];
-    __shared__ uint32_t cnt[MAX_BUCKETS + 1];
-    __shared__ uint32_t acc[PERM ? 1 : MAX_BUCKETS];  // this workgroup's ids per bucket, over its tiles
-    // A block's run-table rows are staged here and written as one contiguous
-    // copy when the block ends (up to STAGE_NB buckets; more write directly).
-    __shared__ uint4 stage[STAGE_NB + 1];  // row i = TB u16 starts of bucket i
-    __shared__ uint32_t lds[16];
-    __shared__ uint32_t s_max;
+    __shared__ alignas(16) uint32_t cnt[MAX_BUCKETS + 1];
+    __shared__ alignas(16) uint32_t acc[PERM ? 4 : MAX_BUCKETS];  // this workgroup's ids per bucket, over its tiles
+    // A block's run-table columns are staged here, slot s (tile s of the
+    // block) at stage[s * STAGE_W + b], and written out as the table's rows,
+    // TB contiguous u16 per bucket, when the block ends (up to STAGE_NB
+    // buckets; more write the table directly).
+    __shared__ alignas(16) uint16_t stage[TB * STAGE_W];
+    __shared__ uint32_t lds[4];
+    __shared__ uint32_t s_max, s_total;
     const uint32_t t = threadIdx.x;
     const uint32_t lane = __lane_id();
     const uint32_t NB = g.NB;
@@ -101,10 +104,8 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
             for (uint32_t x = 0; x < 8; ++x) tot->ticket[x] = 0;
         }
     }
-    constexpr uint32_t BPT = MAX_BUCKETS / TS_NT;  // buckets scanned per thread: t * BPT + q
     if constexpr (!PERM) {
-#pragma unroll
-        for (uint32_t q = 0; q < BPT; ++q) acc[t * BPT + q] = 0;  // each thread's own entries: no barrier needed
+        for (uint32_t i = t; i < MAX_BUCKETS; i += TS_NT) acc[i] = 0;  // before the barrier ahead of the loop
     }
     uint32_t mx = 0;
     // Returns whether the tile is partial; a partial tile's maximum is taken
@@ -157,9 +158,14 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         partial = load_ids(first, v);
         tile_vec = whole_vec(first);
     }
+    for (uint32_t i = t; i <= NB; i += TS_NT) cnt[i] = 0;  // the first tile's counts; each tile zeroes the next's
+    __syncthreads();
     for (uint32_t tile = first; tile < g.n_tiles; tile = next(tile)) {
-        for (uint32_t i = t; i <= NB; i += TS_NT) cnt[i] = 0;
-        __syncthreads();
+        // The thread index, opaque to the compiler here, so per-lane addresses
+        // are formed inside the loop rather than hoisted out of it and
+        // spilled (a spill reload waits for every outstanding load).
+        uint32_t t = threadIdx.x;
+        asm volatile("" : "+v"(t));
         if (!partial) {
 #pragma unroll
             for (uint32_t j = 0; j < TS_PER; ++j) mx = max(mx, v[j]);
@@ -213,32 +219,87 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
             }
         }
         __syncthreads();
-        uint32_t cv[BPT], cs = 0;
+        // Bucket starts: wave w < W scans buckets [1024 w, 1024 w + 1024), 16
+        // consecutive ones a lane (four 16-byte LDS reads, one DPP scan), so
+        // up to 1024 buckets need no block-wide step.  The pass writes each
+        // bucket's start over its count (with PERM the padded start in the
+        // high half) and into the tile's slot of the run table (two 16-byte
+        // writes when staged); the sentinel bucket NB gets the total, the
+        // start of the ids past the universe.  The workgroup's per-bucket
+        // totals are taken from the staged starts when a block is written
+        // out (unstaged, here).
+        {
+            const uint32_t W = max(1u, (NB + 1023u) >> 10);  // scanning waves (NB <= 4096)
+            const uint32_t wave = t >> 6;
+            const uint32_t b0 = 16u * t;  // = 1024 wave + 16 lane
+            uint4* c4 = reinterpret_cast<uint4*>(cnt + b0);
+            auto real = [&](uint32_t c, uint32_t b) { return b < NB ? c : 0u; };
+            uint32_t s = 0, incl = 0, seg = 0;
+            if (wave < W) {
 #pragma unroll
-        for (uint32_t q = 0; q < BPT; ++q) {
-            const uint32_t bq = t * BPT + q;
-            cv[q] = bq < NB ? cnt[bq] : 0u;
-            cs += cv[q];
-            if constexpr (!PERM) atomicAdd(&acc[bq], cv[q]);  // no return: the wave does not wait
-        }
-        uint32_t total;  // ids of the real buckets; the sentinel's follow
-        uint32_t st = block_excl_scan<TS_NT>(cs, lds, total);
-        // Bases, and the tile's column of the run table.
-        uint16_t* trow_col = staged ? reinterpret_cast<uint16_t*>(stage) + tile % TB
-                                    : tab + static_cast<uint64_t>(tile / TB) * (NB + 1) * TB + tile % TB;
-#pragma unroll
-        for (uint32_t q = 0; q < BPT; ++q) {
-            const uint32_t bq = t * BPT + q;
-            if (bq < NB) {
-                // with PERM the padded start rides in the high half
-                cnt[bq] = PERM ? st | (((st + 7u * bq + 7u) & ~7u) << 16) : st;
-                trow_col[static_cast<uint64_t>(bq) * TB] = static_cast<uint16_t>(st);
+                for (uint32_t q = 0; q < 4; ++q) {
+                    const uint4 c = c4[q];
+                    const uint32_t b = b0 + 4u * q;
+                    s += real(c.x, b) + real(c.y, b + 1u) + real(c.z, b + 2u) + real(c.w, b + 3u);
+                }
+                incl = wave_incl_scan(s);
+                seg = __builtin_amdgcn_readlane(incl, 63);
+                if (W > 1u && lane == 63) lds[wave] = seg;
             }
-            st += cv[q];
-        }
-        if (t == 0) {
-            cnt[NB] = PERM ? total | (((total + 7u * NB + 7u) & ~7u) << 16) : total;
-            trow_col[static_cast<uint64_t>(NB) * TB] = static_cast<uint16_t>(total);
+            if (W > 1u) __syncthreads();  // uniform: NB is the workgroup's
+            if (wave < W) {
+                uint32_t prefix = 0, total_ = seg;
+                if (W > 1u) {
+                    total_ = 0;
+                    for (uint32_t x = 0; x < W; ++x) {
+                        const uint32_t y = lds[x];
+                        prefix += x < wave ? y : 0u;
+                        total_ += y;
+                    }
+                }
+                uint32_t run = prefix + incl - s;
+                auto start = [&](uint32_t st, uint32_t b) {
+                    return PERM ? st | (((st + 7u * b + 7u) & ~7u) << 16) : st;
+                };
+                uint32_t st[8];  // the lane's 16 starts as u16 pairs
+#pragma unroll
+                for (uint32_t q = 0; q < 4; ++q) {
+                    const uint4 c = c4[q];
+                    const uint32_t b = b0 + 4u * q;
+                    const uint32_t cx = real(c.x, b), cy = real(c.y, b + 1u), cz = real(c.z, b + 2u), cw = real(c.w, b + 3u);
+                    const uint32_t s0 = run, s1 = s0 + cx, s2 = s1 + cy, s3 = s2 + cz;
+                    run = s3 + cw;
+                    c4[q] = make_uint4(start(s0, b), start(s1, b + 1u), start(s2, b + 2u), start(s3, b + 3u));
+                    st[2 * q] = s0 | (s1 << 16);
+                    st[2 * q + 1] = s2 | (s3 << 16);
+                    if (!staged) {  // straight into the table (entries b <= NB), and the totals
+                        uint16_t* rp = tab + (static_cast<uint64_t>(tile / TB) * (NB + 1) + b) * TB + tile % TB;
+                        if (b <= NB) rp[0] = static_cast<uint16_t>(s0);
+                        if (b + 1u <= NB) rp[TB] = static_cast<uint16_t>(s1);
+                        if (b + 2u <= NB) rp[2 * TB] = static_cast<uint16_t>(s2);
+                        if (b + 3u <= NB) rp[3 * TB] = static_cast<uint16_t>(s3);
+                        if constexpr (!PERM) {
+                            uint4* a4 = reinterpret_cast<uint4*>(acc + b);
+                            const uint4 a = *a4;
+                            *a4 = make_uint4(a.x + cx, a.y + cy, a.z + cz, a.w + cw);
+                        }
+                    }
+                }
+                if (staged) {  // W = 1: buckets 16 t .. 16 t + 15 < STAGE_W
+                    uint4* sp = reinterpret_cast<uint4*>(stage + (tile % TB) * STAGE_W + b0);
+                    sp[0] = make_uint4(st[0], st[1], st[2], st[3]);
+                    sp[1] = make_uint4(st[4], st[5], st[6], st[7]);
+                }
+                // NB a multiple of 1024: the sentinel lies past the last wave's range
+                if (wave == W - 1u && lane == 63 && (NB & 1023u) == 0) {
+                    cnt[NB] = start(total_, NB);
+                    if (staged)
+                        stage[(tile % TB) * STAGE_W + NB] = static_cast<uint16_t>(total_);
+                    else
+                        tab[(static_cast<uint64_t>(tile / TB) * (NB + 1) + NB) * TB + tile % TB] = static_cast<uint16_t>(total_);
+                }
+                if (t == 0) s_total = total_;
+            }
         }
         __syncthreads();
 #pragma unroll
@@ -274,6 +335,31 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
             }
         }
         __syncthreads();
+        const uint32_t total = s_total;  // ids of the real buckets; the sentinel's follow
+        for (uint32_t i = t; i <= NB; i += TS_NT) cnt[i] = 0;  // for the next tile's ranks
+        if (staged && (tile % TB == TB - 1 || tile + 1 == g.n_tiles)) {
+            // The block's rows (TB starts of bucket i, 16 contiguous bytes), and
+            // the ids of its tiles in each bucket, start[i + 1] - start[i],
+            // added to the workgroup's totals (slots past the block's last
+            // tile hold nothing of it).
+            uint4* trow = reinterpret_cast<uint4*>(tab + static_cast<uint64_t>(tile / TB) * (NB + 1) * TB);
+            const uint32_t used = tile % TB + 1u;
+            for (uint32_t i = t; i <= NB; i += TS_NT) {
+                uint32_t r[TB];
+#pragma unroll
+                for (uint32_t sl = 0; sl < TB; ++sl) r[sl] = stage[sl * STAGE_W + i];
+                trow[i] = make_uint4(r[0] | (r[1] << 16), r[2] | (r[3] << 16), r[4] | (r[5] << 16), r[6] | (r[7] << 16));
+                if constexpr (!PERM) {
+                    if (i < NB) {
+                        uint32_t n = 0;
+#pragma unroll
+                        for (uint32_t sl = 0; sl < TB; ++sl)
+                            n += sl < used ? static_cast<uint32_t>(stage[sl * STAGE_W + i + 1u]) - r[sl] : 0u;
+                        acc[i] += n;
+                    }
+                }
+            }
+        }
         if (nfull) {
             const uint4* src = reinterpret_cast<const uint4*>(ids + static_cast<uint64_t>(nt) * TILE);
 #pragma unroll
@@ -288,10 +374,6 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         } else if (nt < g.n_tiles) {
             partial = load_ids(nt, v);
             tile_vec = whole_vec(nt);
-        }
-        if (staged && (tile % TB == TB - 1 || tile + 1 == g.n_tiles)) {  // the block's rows, contiguous
-            uint4* trow = reinterpret_cast<uint4*>(tab + static_cast<uint64_t>(tile / TB) * (NB + 1) * TB);
-            for (uint32_t i = t; i <= NB; i += TS_NT) trow[i] = stage[i];
         }
         // Packing in place: thread g turns fields [8 g, 8 g + 8) (two 16-byte
         // LDS reads) into words [5 g, 5 g + 5) of the stream, which overwrite
@@ -312,7 +394,7 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
             pw[k][3] = (f4 >> 16) | (f5 << 4) | (f6 << 24);
             pw[k][4] = (f6 >> 8) | (f7 << 12);
         }
-        __syncthreads();
+        __syncthreads();  // also: the counts are zeroed for the next tile's ranks
 #pragma unroll
         for (uint32_t k = 0; k < GPT; ++k)
 #pragma unroll
@@ -322,7 +404,8 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         const uint32_t n4 = (FIELD_BITS * total + 127u) >> 7;
         // Ordinary stores, so the packed tiles are kept in the Infinity Cache
         // for the kernel that reads them next; the ids come in through
-        // nontemporal loads, which do not displace them.
+        // nontemporal loads, which do not displace them.  The next tile's
+        // scatter overwrites buf only after two more barriers.
         for (uint32_t u = t; u < n4; u += TS_NT) dst[u] = reinterpret_cast<const uint4*>(buf)[u];
     }
 #pragma unroll

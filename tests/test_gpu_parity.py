@@ -53,6 +53,9 @@ ID_CASES = [
     (1025, 0xFFFFFFFF, orc.PROMOTE_AUTO, 19),
     (20000, 0xFFFFFFFF, orc.PROMOTE_AUTO, 20),
     (16383, 1 << 30, orc.PROMOTE_AUTO, 21),
+    # 2048 and 3072 buckets: the tile sort's bucket scan spans two and three waves
+    (60000, 1 << 31, orc.PROMOTE_AUTO, 22),
+    (70000, 3 << 30, orc.PROMOTE_AUTO, 23),
 ]
 
 
@@ -183,6 +186,25 @@ def test_contains_partitioned_unaligned_and_partial_tiles(gpu, offset):
     out = torch.empty(q.size + offset, dtype=torch.int32, device="cuda")[offset:]
     assert dq.data_ptr() % 16 != 0 and out.data_ptr() % 16 != 0
     gpu.contains_batch(g, dq, out, 4)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), orc.contains_many(want, q))
+    gpu.free(g)
+
+
+@pytest.mark.parametrize("universe", [1 << 31, 3 << 30, 0xFFFFFFFF])
+def test_contains_partitioned_many_buckets(gpu, universe):
+    """Mode 4 on bitmaps whose keys reach 2^31, 3 * 2^30 and 2^32: 2048 to 4096
+    buckets of 16 keys, so the tile sort's bucket scan spans two to four waves
+    and its run table is written straight to memory; queries past the last key
+    fall in the sentinel bucket (none at 2^32)."""
+    _say("contains partitioned many buckets", universe)
+    torch = _torch()
+    rng = np.random.default_rng(95 + (universe >> 30))
+    ids = rng.integers(0, universe, 400000, dtype=np.uint64).astype(np.uint32)
+    g, want = gpu.upload_from_ids(ids, universe), orc.upload_from_ids(ids, universe)
+    q = np.concatenate([ids[:100000], rng.integers(0, 1 << 32, 24576 * 5 + 11, dtype=np.uint64).astype(np.uint32)])
+    out = torch.empty(q.size, dtype=torch.int32, device="cuda")
+    gpu.contains_batch(g, _dev_u32(q), out, 4)
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy().view(np.uint32), orc.contains_many(want, q))
     gpu.free(g)
