@@ -183,6 +183,20 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
             const uint32_t run = __builtin_amdgcn_readfirstlane(r0) + lane;
 #pragma unroll
             for (uint32_t j = 0; j < TS_PER; j += 2) rk[j >> 1] = (run + 64u * j) | ((run + 64u * (j + 1)) << 16);
+        } else if (__ballot(bucket(v[0]) != b00) != 0ull &&
+                   __ballot(bucket(v[TS_PER - 1]) !=
+                            static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(bucket(v[TS_PER - 1])))) != 0ull) {
+            // The wave's first and last passes (ids 256 apart in a sorted
+            // tile) both span several buckets: random ids, an atomic a lane
+            // throughout, without a test per pass.
+#pragma unroll
+            for (uint32_t j = 0; j < TS_PER; ++j) {
+                const uint32_t r = atomicAdd(&cnt[bucket(v[j])], 1u);
+                if (j & 1u)
+                    rk[j >> 1] |= r << 16;
+                else
+                    rk[j >> 1] = r;
+            }
         } else {
             // Per pass j, likewise when the wave's j-th ids share a bucket
             // (sorted or clustered ids spread over a few buckets per tile);
