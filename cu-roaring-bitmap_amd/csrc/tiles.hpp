@@ -170,25 +170,21 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
 #pragma unroll
             for (uint32_t j = 0; j < TS_PER; ++j) mx = max(mx, v[j]);
         }
-        // Ranks within the tile.  When every id of the wave's pass falls in
-        // one bucket (clustered ids), a single atomic reserves them all.
+        // Ranks within the tile.  A wave whose first and last passes (ids 256
+        // apart in a sorted tile) both span several buckets holds random ids:
+        // an atomic a lane throughout, with no further test.  Otherwise, when
+        // every id of the wave's tile falls in one bucket (clustered ids), a
+        // single atomic reserves them all.
         uint32_t rk[TS_PER / 2];  // tile ranks (< 24576) packed two per register
         const uint32_t b00 = __builtin_amdgcn_readfirstlane(bucket(v[0]));
-        bool diff = false;
+        const uint32_t bl0 = __builtin_amdgcn_readfirstlane(bucket(v[TS_PER - 1]));
+        auto one_bucket = [&](uint32_t b) {  // every id of the wave's tile in bucket b
+            bool diff = false;
 #pragma unroll
-        for (uint32_t j = 0; j < TS_PER; ++j) diff |= bucket(v[j]) != b00;
-        if (__ballot(diff) == 0) {
-            uint32_t r0 = 0;
-            if (lane == 0) r0 = atomicAdd(&cnt[b00], 64u * TS_PER);
-            const uint32_t run = __builtin_amdgcn_readfirstlane(r0) + lane;
-#pragma unroll
-            for (uint32_t j = 0; j < TS_PER; j += 2) rk[j >> 1] = (run + 64u * j) | ((run + 64u * (j + 1)) << 16);
-        } else if (__ballot(bucket(v[0]) != b00) != 0ull &&
-                   __ballot(bucket(v[TS_PER - 1]) !=
-                            static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(bucket(v[TS_PER - 1])))) != 0ull) {
-            // The wave's first and last passes (ids 256 apart in a sorted
-            // tile) both span several buckets: random ids, an atomic a lane
-            // throughout, without a test per pass.
+            for (uint32_t j = 0; j < TS_PER; ++j) diff |= bucket(v[j]) != b;
+            return __ballot(diff) == 0ull;
+        };
+        if (__ballot(bucket(v[0]) != b00) != 0ull && __ballot(bucket(v[TS_PER - 1]) != bl0) != 0ull) {
 #pragma unroll
             for (uint32_t j = 0; j < TS_PER; ++j) {
                 const uint32_t r = atomicAdd(&cnt[bucket(v[j])], 1u);
@@ -197,6 +193,12 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
                 else
                     rk[j >> 1] = r;
             }
+        } else if (one_bucket(b00)) {
+            uint32_t r0 = 0;
+            if (lane == 0) r0 = atomicAdd(&cnt[b00], 64u * TS_PER);
+            const uint32_t run = __builtin_amdgcn_readfirstlane(r0) + lane;
+#pragma unroll
+            for (uint32_t j = 0; j < TS_PER; j += 2) rk[j >> 1] = (run + 64u * j) | ((run + 64u * (j + 1)) << 16);
         } else {
             // Per pass j, likewise when the wave's j-th ids share a bucket
             // (sorted or clustered ids spread over a few buckets per tile);
