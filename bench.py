@@ -115,6 +115,18 @@ def cold_time(torch, fn, iters, flush, after=None):
     return median(ts)
 
 
+def cold_time_and_kernels(torch, cr, fn, iters, flush, after=None):
+    """cold_time() of fn with the library's kernel timer off (its event markers
+    add queue time to every launch), then the per-kernel report of as many more
+    cold calls with it on: the API time never carries the markers."""
+    t = cold_time(torch, fn, iters, flush, after=after)
+    cr.timing_enable(True)
+    cold_time(torch, fn, iters, flush, after=after)
+    rep = cr.timing_report()
+    cr.timing_enable(False)
+    return t, rep
+
+
 SECTIONS = ("config0", "config2", "config3", "conversions", "batch", "upload_variants", "promote_sweep", "topk")
 
 
@@ -370,10 +382,7 @@ def config2(torch, cr, flush, nt, no_cpu):
             nbytes = setop_algorithmic_bytes(cr, ga, gb, r, op)
             card = cr.cardinality(r)
             cr.free(r)
-            cr.timing_enable(True)
-            t = cold_time(torch, lambda: cr.set_operation(ga, gb, op), 3, flush, after=cr.free)
-            rep = cr.timing_report()
-            cr.timing_enable(False)
+            t, rep = cold_time_and_kernels(torch, cr, lambda: cr.set_operation(ga, gb, op), 3, flush, after=cr.free)
             kern = {k: v[1] / v[0] for k, v in rep.items() if not k.startswith("host:")}
             dev = sum(kern.values())
             exec_ms = kern.get("so_exec_bb", kern.get("so_exec", float("nan")))
@@ -410,10 +419,7 @@ def config2(torch, cr, flush, nt, no_cpu):
             n_common = r.n_containers
             outb = 8192 * r.n_bitmap_containers + r.array_pool_bytes + r.run_pool_bytes
             cr.free(r)
-            cr.timing_enable(True)
-            t = cold_time(torch, lambda: cr.multi_and(ins), 3, flush, after=cr.free)
-            rep = cr.timing_report()
-            cr.timing_enable(False)
+            t, rep = cold_time_and_kernels(torch, cr, lambda: cr.multi_and(ins), 3, flush, after=cr.free)
             inb = sum(int(container_bytes(cr, g)[1].sum()) + 9 * g.n_containers for g in ins)
             kern = {kk: v[1] / v[0] for kk, v in rep.items() if not kk.startswith("host:")}
             line = {"densities": list(dens), "route": route, "n_result_containers": n_common, "cardinality": card,
@@ -623,18 +629,23 @@ def upload_variants(torch, cr):
         torch.cuda.synchronize()
         meta = (r.n_containers, r.total_cardinality, bool(r.negated))
         cr.free_async(r)
+
+        def calls():
+            ts = []
+            for _ in range(5):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                r = fn()
+                torch.cuda.synchronize()
+                ts.append((time.perf_counter() - t0) * 1e3)
+                cr.free_async(r)
+            return median(ts)
+        t = calls()  # the kernel timer off: its markers would add queue time
         cr.timing_enable(True)
-        ts = []
-        for _ in range(5):
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            r = fn()
-            torch.cuda.synchronize()
-            ts.append((time.perf_counter() - t0) * 1e3)
-            cr.free_async(r)
+        calls()
         rep = cr.timing_report()
         cr.timing_enable(False)
-        return median(ts), meta, {k: round(v[1] / v[0], 4) for k, v in rep.items()}
+        return t, meta, {k: round(v[1] / v[0], 4) for k, v in rep.items()}
 
     t, (nc, card, neg), k = timed(lambda: cr.upload_from_device_ids(d, U))
     res["ids_clustered_100M"] = {"ms": round(t, 4), "runs": n_runs, "containers": nc, "distinct": card,
@@ -685,10 +696,7 @@ def portable(torch, cr, flush, bitmaps):
 
         def ser():
             assert lib.cr_portable_serialize(C.byref(g), None, hbuf.ctypes.data, hbuf.size, C.byref(w)) == 0
-        cr.timing_enable(True)
-        t_ser = cold_time(torch, ser, 3, flush)
-        rep = cr.timing_report()
-        cr.timing_enable(False)
+        t_ser, rep = cold_time_and_kernels(torch, cr, ser, 3, flush)
         assert hbuf.tobytes() == data
         kw = rep.get("ps_write", (1, float("nan")))
         kp = rep.get("ps_plan", (1, float("nan")))
@@ -763,30 +771,21 @@ def batch_api(torch, cr, flush):
     # the library's cache, as in a steady state)
     P = cr.promote_batch(B)  # also the first launch (code object load), out of the timing
     torch.cuda.synchronize()
-    cr.timing_enable(True)
-    t = cold_time(torch, lambda: cr.promote_batch(B), 5, flush, after=cr.free_batch)
-    rep = cr.timing_report()
-    cr.timing_enable(False)
+    t, rep = cold_time_and_kernels(torch, cr, lambda: cr.promote_batch(B), 5, flush, after=cr.free_batch)
     res["promote_batch"] = _kernel_line(rep, "bt_promote", 8 * 8192 * nk + B.array_pool_bytes + 9 * T + 8192 * T + 9 * T,
                                         t)
     for name, idx in (("multi_and_8_dense", list(range(8))), ("multi_and_4_dense_4_sparse", [0, 1, 2, 3, 8, 9, 10, 11])):
         r0 = cr.batch_multi_and(P, idx)
         n_common = r0.total_containers
         cr.free_batch(r0)
-        cr.timing_enable(True)
-        t = cold_time(torch, lambda: cr.batch_multi_and(P, idx), 5, flush, after=cr.free_batch)
-        rep = cr.timing_report()
-        cr.timing_enable(False)
+        t, rep = cold_time_and_kernels(torch, cr, lambda: cr.batch_multi_and(P, idx), 5, flush, after=cr.free_batch)
         nbytes = (len(idx) + 1) * 8192 * n_common + 9 * (len(idx) + 1) * n_common
         res[name] = dict(_kernel_line(rep, "bt_and", nbytes, t), n_common=n_common)
     words_each = Ub // 64
     d = torch.zeros(16 * words_each, dtype=torch.int64, device="cuda")
     cr.batch_decompress(B, d, words_each)  # first launch stays out of the timing
     torch.cuda.synchronize()
-    cr.timing_enable(True)
-    t = cold_time(torch, lambda: cr.batch_decompress(B, d, words_each), 5, flush)
-    rep = cr.timing_report()
-    cr.timing_enable(False)
+    t, rep = cold_time_and_kernels(torch, cr, lambda: cr.batch_decompress(B, d, words_each), 5, flush)
     res["decompress_batch"] = _kernel_line(rep, "bt_decompress", 8 * 8192 * nk + B.array_pool_bytes + 9 * T +
                                            16 * words_each * 8, t)
     del d
@@ -856,10 +855,7 @@ def conversions(torch, cr, flush, bitmaps):
             torch.cuda.synchronize()
             if frees:
                 cr.free(x)
-            cr.timing_enable(True)
-            t = cold_time(torch, fn, 5, flush, after=after)
-            rep = cr.timing_report()
-            cr.timing_enable(False)
+            t, rep = cold_time_and_kernels(torch, cr, fn, 5, flush, after=after)
             kn, kms = rep.get(kname, (1, float("nan")))
             k_avg = kms / kn
             r[cname] = {"algorithmic_bytes": nbytes, "api_ms": round(t, 4), "api_GBps": round(nbytes / t / 1e6, 1),
