@@ -386,7 +386,9 @@ __global__ __launch_bounds__(QU_NT) void qp_unpermute(const uint16_t* __restrict
 #pragma unroll
         for (uint32_t k = 0; k < TILE / (4u * QU_NT); ++k) {
             const uint32_t q = t + k * QU_NT;
-            const uint2 pp = p2[q];
+            // the permutation is read once, in order: a nontemporal stream
+            const uint64_t pp64 = __builtin_nontemporal_load(reinterpret_cast<const uint64_t*>(p2) + q);
+            const uint2 pp = make_uint2(static_cast<uint32_t>(pp64), static_cast<uint32_t>(pp64 >> 32));
             st_stream(o4 + q, make_uint4(answer(pp.x & 0xFFFFu), answer(pp.x >> 16), answer(pp.y & 0xFFFFu),
                                          answer(pp.y >> 16)));
         }
