@@ -71,12 +71,14 @@ struct Side {  // the parts of a GpuRoaring the kernels read
     const uint16_t* arr;
     const uint16_t* run;
     uint32_t n;
+    const uint16_t* kidx;  // key -> container index (0xFFFF: absent) for keys <= max_key, or null
+    uint32_t kidx_n;       // max_key + 1 with kidx
 };
 
 static Side side_of(const cr_gpu_roaring* r)
 {
     return Side{r->keys, r->types, r->offsets, r->cardinalities, r->bitmap_data, r->array_data, r->run_data,
-                r->n_containers};
+                r->n_containers, r->key_index, r->key_index ? r->max_key + 1u : 0u};
 }
 
 constexpr int PLAN_NT = 1024;
@@ -91,26 +93,39 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_classify(Side A, Side B, uint
     __shared__ uint32_t red[C_N * (PLAN_NT / 64)];
     const uint32_t base = blockIdx.x * PLAN_NT;
     const uint32_t t = threadIdx.x;
-    const uint32_t wv = t >> 6;  // waves 0-3: the key range of this group in A and in B
-    if (wv < 4) {
-        const uint32_t r = wave_lower_bound_u16(wv < 2 ? A.keys : B.keys, wv < 2 ? A.n : B.n,
-                                                base + ((wv & 1u) ? PLAN_NT : 0u));
-        if ((t & 63u) == 0) range[wv] = r;
+    int32_t ai, bi;
+    if (A.kidx && B.kidx && A.n < 0xFFFFu && B.n < 0xFFFFu) {
+        // Both sides index their keys (and 0xFFFF cannot be a real index):
+        // one coalesced load a side, no search of the keys.
+        const uint32_t key = base + t;
+        auto look = [&](const Side& S) -> int32_t {
+            const uint32_t x = key < S.kidx_n ? S.kidx[key] : 0xFFFFu;
+            return x < S.n ? static_cast<int32_t>(x) : -1;
+        };
+        ai = look(A);
+        bi = look(B);
+    } else {
+        const uint32_t wv = t >> 6;  // waves 0-3: the key range of this group in A and in B
+        if (wv < 4) {
+            const uint32_t r = wave_lower_bound_u16(wv < 2 ? A.keys : B.keys, wv < 2 ? A.n : B.n,
+                                                    base + ((wv & 1u) ? PLAN_NT : 0u));
+            if ((t & 63u) == 0) range[wv] = r;
+        }
+        ia[t] = -1;
+        ib[t] = -1;
+        __syncthreads();
+        for (uint32_t j = range[0] + t; j < range[1]; j += PLAN_NT) {
+            const uint32_t k = A.keys[j] - base;  // in range for sorted keys; guarded for malformed input
+            if (k < PLAN_NT) ia[k] = static_cast<int32_t>(j);
+        }
+        for (uint32_t j = range[2] + t; j < range[3]; j += PLAN_NT) {
+            const uint32_t k = B.keys[j] - base;
+            if (k < PLAN_NT) ib[k] = static_cast<int32_t>(j);
+        }
+        __syncthreads();
+        ai = ia[t];
+        bi = ib[t];
     }
-    ia[t] = -1;
-    ib[t] = -1;
-    __syncthreads();
-    for (uint32_t j = range[0] + t; j < range[1]; j += PLAN_NT) {
-        const uint32_t k = A.keys[j] - base;  // in range for sorted keys; guarded for malformed input
-        if (k < PLAN_NT) ia[k] = static_cast<int32_t>(j);
-    }
-    for (uint32_t j = range[2] + t; j < range[3]; j += PLAN_NT) {
-        const uint32_t k = B.keys[j] - base;
-        if (k < PLAN_NT) ib[k] = static_cast<int32_t>(j);
-    }
-    __syncthreads();
-
-    const int32_t ai = ia[t], bi = ib[t];
     KeyRec rec{};
     rec.ai = ai;
     rec.bi = bi;
@@ -165,7 +180,7 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_classify(Side A, Side B, uint
 #pragma unroll
     for (int k = 0; k < C_N; ++k) {
         const uint32_t ws = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(cnt[k])), 63));
-        if (__lane_id() == 0) red[k * NW + wv] = ws;
+        if (__lane_id() == 0) red[k * NW + (t >> 6)] = ws;
     }
     __syncthreads();
     if (t < C_N) {

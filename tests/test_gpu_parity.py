@@ -397,6 +397,27 @@ def test_set_operation_mixed_parity(gpu, seed, op):
 
 
 @pytest.mark.parametrize("op", [orc.AND, orc.OR, orc.ANDNOT, orc.XOR])
+@pytest.mark.parametrize("order", ["result_first", "result_second"])
+def test_set_operation_on_a_result(gpu, op, order):
+    """One operand is a set-operation result, which carries no key_index, the
+    other an upload, which does: the plan finds the result's keys by searching
+    them, the upload's through its key_index."""
+    _say("set_operation on a result", op, order)
+    U, la, lb = _build_operands(3)
+    _, lc = _build_operands(4)[1:]
+    ga, oa = _upload_pair(gpu, la, U, orc.PROMOTE_KEEP_DEFAULT)
+    gb, ob = _upload_pair(gpu, lb, U, orc.PROMOTE_KEEP_DEFAULT)
+    gc, oc = _upload_pair(gpu, lc, U, orc.PROMOTE_KEEP_DEFAULT)
+    gr, orr = gpu.set_operation(ga, gb, orc.OR), orc.set_operation(oa, ob, orc.OR)
+    assert not gr.key_index and gc.key_index
+    x, ox, y, oy = (gr, orr, gc, oc) if order == "result_first" else (gc, oc, gr, orr)
+    g = gpu.set_operation(x, y, op)
+    assert_same(gpu.download(g), orc.set_operation(ox, oy, op), strict=True, what=f"setop on a result {op}")
+    for h in (g, gr, ga, gb, gc):
+        gpu.free(h)
+
+
+@pytest.mark.parametrize("op", [orc.AND, orc.OR, orc.ANDNOT, orc.XOR])
 @pytest.mark.parametrize("na", [False, True])
 @pytest.mark.parametrize("nb", [False, True])
 def test_set_operation_demorgan_parity(gpu, op, na, nb):  # test/test_complement.cu:367-462
