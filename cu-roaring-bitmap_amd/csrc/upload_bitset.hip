@@ -101,44 +101,61 @@ __global__ __launch_bounds__(1024) void bs_plan(BsGeom g, const uint32_t* pc, co
                                                 uint16_t* key_index, BsTotals* tot, BsTotals* host)
 {
     __shared__ unsigned long long wsum[16];
-    __shared__ uint32_t lds[16];
+    __shared__ uint32_t lds[16], lds_i[16];
     __shared__ uint32_t s_last;
     __shared__ bool s_done;
     const uint32_t t = threadIdx.x, wave = t >> 6, lane = __lane_id();
     const uint32_t r = blockIdx.x, rounds = gridDim.x;
+    // One pass of loads, sixteen rounds in flight a thread: the plain counts of
+    // every round (their sum decides the negation) and both counts of the
+    // rounds before r (kept chunks, plain and inverted), so nothing waits for
+    // the negation before loading.
+    const uint32_t c = r * 1024u + t;  // this thread's chunk: both counts
+    const uint32_t own_p = c < g.n_chunks ? pc[c] : 0u, own_i = c < g.n_chunks ? pci[c] : 0u;
     unsigned long long part = 0;
-    for (uint32_t j0 = 0; j0 < rounds; j0 += 8) {
-        uint32_t v[8];
+    uint32_t bef_p = 0, bef_i = 0;
+    for (uint32_t j0 = 0; j0 < rounds; j0 += 16) {
+        uint32_t v[16], w[16];
 #pragma unroll
-        for (uint32_t q = 0; q < 8; ++q) {
-            const uint32_t c = (j0 + q) * 1024u + t;
-            v[q] = c < g.n_chunks ? pc[c] : 0u;
+        for (uint32_t q = 0; q < 16; ++q) {
+            const uint32_t cq = (j0 + q) * 1024u + t;
+            v[q] = cq < g.n_chunks ? pc[cq] : 0u;
+            w[q] = j0 + q < r ? pci[cq] : 0u;  // rounds before r are whole
         }
 #pragma unroll
-        for (uint32_t q = 0; q < 8; ++q) part += v[q];
+        for (uint32_t q = 0; q < 16; ++q) {
+            part += v[q];
+            bef_p += j0 + q < r && v[q] != 0u ? 1u : 0u;
+            bef_i += w[q] != 0u ? 1u : 0u;
+        }
     }
+    // One block reduction of the three: the total, and the kept chunks before
+    // this round either way.
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
-    if (lane == 0) wsum[wave] = part;
+    for (int o = 32; o > 0; o >>= 1) {
+        part += __shfl_xor(part, o, 64);
+        bef_p += __shfl_xor(bef_p, o, 64);
+        bef_i += __shfl_xor(bef_i, o, 64);
+    }
+    if (lane == 0) {
+        wsum[wave] = part;
+        lds[wave] = bef_p;
+        lds_i[wave] = bef_i;
+    }
     if (t == 0) s_last = 0;
     __syncthreads();
     unsigned long long total = 0;
+    uint32_t base_p = 0, base_i = 0;
 #pragma unroll
-    for (int w = 0; w < 16; ++w) total += wsum[w];
-    const bool negate = total > static_cast<unsigned long long>(g.universe / 2u);  // :837
-    const uint32_t* cnt = negate ? pci : pc;
-    // Rounds before r are whole (only the last round can be partial).
-    uint32_t before = 0;
-    for (uint32_t j0 = 0; j0 < r; j0 += 8) {
-        uint32_t v[8];
-#pragma unroll
-        for (uint32_t q = 0; q < 8; ++q) v[q] = j0 + q < r ? cnt[(j0 + q) * 1024u + t] : 0u;
-#pragma unroll
-        for (uint32_t q = 0; q < 8; ++q) before += v[q] != 0u ? 1u : 0u;
+    for (int w = 0; w < 16; ++w) {
+        total += wsum[w];
+        base_p += lds[w];
+        base_i += lds_i[w];
     }
-    const uint32_t base = block_sum<1024>(before, lds);
-    const uint32_t c = r * 1024u + t;
-    const uint32_t v = c < g.n_chunks ? cnt[c] : 0u;
+    const bool negate = total > static_cast<unsigned long long>(g.universe / 2u);  // :837
+    const uint32_t base = negate ? base_i : base_p;
+    __syncthreads();  // lds is reused by the rank below
+    const uint32_t v = negate ? own_i : own_p;
     const bool kept = v != 0u;
     uint32_t count;
     const uint32_t rank = base + block_flag_rank<1024>(kept, lds, count);
