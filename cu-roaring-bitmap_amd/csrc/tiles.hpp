@@ -3,7 +3,7 @@
 // bucket's LDS containers) and the partitioned point queries (which test it).
 //
 // Ids are grouped by 16-key bucket (1 MiB of id space) inside 24576-id tiles:
-// each tile is counting-sorted by bucket in LDS and streamed back to its own
+// each tile is counting-sorted by bucket in LDS and written back to its own
 // slot as 20-bit fields (the id within its bucket), with the tile's bucket
 // starts in a small table.  A bucket's consumer -- one workgroup holding the
 // bucket's 16 containers in 128 KiB of LDS -- then reads the bucket's run in
