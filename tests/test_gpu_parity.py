@@ -287,6 +287,28 @@ BITSET_CASES = [(100000, 0.1, 1), (100000, 0.9, 2), (200000, 1 / 3, 3), (5 * 655
                 (5 * 65536 + 123, 0.95, 5), (1 << 22, 0.5, 6), (1 << 22, 0.55, 7), (64, 1.0, 8), (96, 0.0, 9)]
 
 
+@pytest.mark.parametrize("invert", [False, True])
+def test_upload_from_bitset_past_16_rounds(gpu, invert):
+    """A universe just past 2^30: 16390 chunks, 17 rounds of the plan's 1024
+    (the last partial), so its counts come in two passes of 16 rounds; sparse,
+    and inverted (stored as the complement, from the inverted counts)."""
+    _say("upload_from_bitset past 16 rounds", invert)
+    U = (1 << 30) + 5 * 65536 + 123
+    rng = np.random.default_rng(31 + int(invert))
+    ids = np.unique(np.concatenate([rng.integers(0, U, 20000, dtype=np.uint64),
+                                    U - 1 - 7 * np.arange(3000, dtype=np.uint64)])).astype(np.uint32)
+    words = np.zeros((U + 31) // 32, np.uint32)  # built directly: no 2^30-entry bool array
+    np.bitwise_or.at(words, (ids >> 5).astype(np.int64), np.left_shift(np.uint32(1), ids & np.uint32(31)))
+    if invert:
+        words = ~words
+        words[-1] &= np.uint32((1 << (U % 32)) - 1)  # no bits past the universe
+    want = orc.upload_from_bitset(words, U)
+    g = gpu.upload_from_bitset(words, U)
+    assert bool(g.negated) == invert
+    assert_same(gpu.download(g), want, strict=True, what="bitset past 16 rounds")
+    gpu.free(g)
+
+
 @pytest.mark.parametrize("universe,density,seed", BITSET_CASES)
 def test_upload_from_bitset_parity(gpu, universe, density, seed):
     _say("upload_from_bitset", universe, density, seed)
