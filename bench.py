@@ -118,13 +118,42 @@ def cold_time(torch, fn, iters, flush, after=None):
 def cold_time_and_kernels(torch, cr, fn, iters, flush, after=None):
     """cold_time() of fn with the library's kernel timer off (its event markers
     add queue time to every launch), then the per-kernel report of as many more
-    cold calls with it on: the API time never carries the markers."""
+    cold calls with it on: the API time never carries the markers.  The report
+    is {name: (launches, total_ms, median_ms)}; callers use the median."""
     t = cold_time(torch, fn, iters, flush, after=after)
     cr.timing_enable(True)
     cold_time(torch, fn, iters, flush, after=after)
     rep = cr.timing_report()
     cr.timing_enable(False)
     return t, rep
+
+
+def kernel_medians(rep):
+    """{kernel: median launch ms} from a timing report, host phases left out."""
+    return {k: v[2] for k, v in rep.items() if not k.startswith("host:")}
+
+
+# Lines whose summed kernel medians exceed the whole call's median time (the
+# kernels of one call cannot take longer than the call): each is named here
+# and counted in the headline line.
+DEVICE_GT_API = []
+
+
+def device_le_api(dev_ms, api_ms, tol=1.02):
+    ok = bool(dev_ms <= api_ms * tol)
+    if not ok:
+        import inspect
+        DEVICE_GT_API.append(f"{inspect.stack()[1].function}: device {dev_ms:.4f} ms > api {api_ms:.4f} ms")
+        log("WARNING device time exceeds API time:", DEVICE_GT_API[-1])
+    return ok
+
+
+def cpu_median(fn, reps):
+    """Median seconds (and the first answer) of `reps` runs of an orc CPU
+    baseline call returning (seconds, answer, ...)."""
+    runs = [fn() for _ in range(reps)]
+    ts = sorted(r[0] for r in runs)
+    return ts[len(ts) // 2], runs[0][1]
 
 
 SECTIONS = ("config0", "config2", "config3", "conversions", "batch", "upload_variants", "promote_sweep", "topk")
@@ -383,17 +412,18 @@ def config2(torch, cr, flush, nt, no_cpu):
             card = cr.cardinality(r)
             cr.free(r)
             t, rep = cold_time_and_kernels(torch, cr, lambda: cr.set_operation(ga, gb, op), 3, flush, after=cr.free)
-            kern = {k: v[1] / v[0] for k, v in rep.items() if not k.startswith("host:")}
+            kern = kernel_medians(rep)
             dev = sum(kern.values())
             exec_ms = kern.get("so_exec_bb", kern.get("so_exec", float("nan")))
             line = {"algorithmic_bytes": nbytes, "api_ms": round(t, 4), "api_GBps": round(nbytes / t / 1e6, 1),
                     "device_ms": round(dev, 4), "device_GBps": round(nbytes / dev / 1e6, 1),
                     "exec_kernel_ms": round(exec_ms, 4),
                     "exec_frac_of_hbm_peak": round(nbytes / exec_ms / 1e6 / HBM_PEAK_GBS, 4),
-                    "cardinality": card, "kernels_ms": {k: round(v, 4) for k, v in kern.items()}}
+                    "cardinality": card, "kernels_ms": {k: round(v, 4) for k, v in kern.items()},
+                    "device_le_api": device_le_api(dev, t)}
             if not no_cpu:
-                t1, c1, _ = orc.cpu_setop([la], [lb], op, 1)
-                tn, cn, _ = orc.cpu_setop(shards[x], shards[y], op, nt)
+                t1, c1 = cpu_median(lambda: orc.cpu_setop([la], [lb], op, 1), 3)
+                tn, cn = cpu_median(lambda: orc.cpu_setop(shards[x], shards[y], op, nt), 7)
                 # The reference stores a full (65536) result container's card as 0
                 # and then drops zero-card results of AND/ANDNOT/XOR
                 # (src/set_ops.cu:179-180,1111,1145); roaring-lite keeps them.
@@ -421,10 +451,11 @@ def config2(torch, cr, flush, nt, no_cpu):
             cr.free(r)
             t, rep = cold_time_and_kernels(torch, cr, lambda: cr.multi_and(ins), 3, flush, after=cr.free)
             inb = sum(int(container_bytes(cr, g)[1].sum()) + 9 * g.n_containers for g in ins)
-            kern = {kk: v[1] / v[0] for kk, v in rep.items() if not kk.startswith("host:")}
+            kern = kernel_medians(rep)
             line = {"densities": list(dens), "route": route, "n_result_containers": n_common, "cardinality": card,
                     "api_ms": round(t, 4), "device_ms": round(sum(kern.values()), 4),
-                    "kernels_ms": {kk: round(v, 4) for kk, v in kern.items()}}
+                    "kernels_ms": {kk: round(v, 4) for kk, v in kern.items()},
+                    "device_le_api": device_le_api(sum(kern.values()), t)}
             if route == "fused_all_bitmap":
                 mb = (k + 1) * 8192 * n_common + 9 * (k + 1) * n_common
                 ka = kern.get("mand_and", float("nan"))
@@ -437,8 +468,9 @@ def config2(torch, cr, flush, nt, no_cpu):
                 cr.free(g)
             out[f"multi_and_k{k}_{route}"] = line
         if not no_cpu:
-            t1, c1, _ = orc.cpu_multi_and([[lt] for lt in lites], 1)
-            tn, cn, _ = orc.cpu_multi_and([lt.shards(4 * nt, U >> 16) for lt in lites], nt)
+            t1, c1 = cpu_median(lambda: orc.cpu_multi_and([[lt] for lt in lites], 1), 3)
+            shl = [lt.shards(4 * nt, U >> 16) for lt in lites]
+            tn, cn = cpu_median(lambda: orc.cpu_multi_and(shl, nt), 7)
             assert c1 == cn == out[f"multi_and_k{k}_fused_all_bitmap"]["cardinality"] == \
                 out[f"multi_and_k{k}_pairwise_keep"]["cardinality"]
             out[f"multi_and_k{k}_cpu"] = {"cpu_1t_ms": round(t1 * 1e3, 3), f"cpu_{nt}t_ms": round(tn * 1e3, 3),
@@ -645,7 +677,7 @@ def upload_variants(torch, cr):
         calls()
         rep = cr.timing_report()
         cr.timing_enable(False)
-        return t, meta, {k: round(v[1] / v[0], 4) for k, v in rep.items()}
+        return t, meta, {k: round(v[2], 4) for k, v in rep.items()}
 
     t, (nc, card, neg), k = timed(lambda: cr.upload_from_device_ids(d, U))
     res["ids_clustered_100M"] = {"ms": round(t, 4), "runs": n_runs, "containers": nc, "distinct": card,
@@ -671,11 +703,11 @@ def upload_variants(torch, cr):
 
 
 def _kernel_line(rep, name, nbytes, t_api):
-    kn, kms = rep.get(name, (1, float("nan")))
-    k = kms / kn
+    k = rep.get(name, (1, float("nan"), float("nan")))[2]
     return {"algorithmic_bytes": nbytes, "api_ms": round(t_api, 4), f"{name}_ms": round(k, 4),
             f"{name}_GBps": round(nbytes / k / 1e6, 1), "frac_of_hbm_peak": round(nbytes / k / 1e6 / HBM_PEAK_GBS, 4),
-            "kernels_ms": {kk: round(v[1] / v[0], 4) for kk, v in rep.items()}}
+            "kernels_ms": {kk: round(v, 4) for kk, v in kernel_medians(rep).items()},
+            "device_le_api": device_le_api(sum(kernel_medians(rep).values()), t_api)}
 
 
 def portable(torch, cr, flush, bitmaps):
@@ -698,14 +730,15 @@ def portable(torch, cr, flush, bitmaps):
             assert lib.cr_portable_serialize(C.byref(g), None, hbuf.ctypes.data, hbuf.size, C.byref(w)) == 0
         t_ser, rep = cold_time_and_kernels(torch, cr, ser, 3, flush)
         assert hbuf.tobytes() == data
-        kw = rep.get("ps_write", (1, float("nan")))
-        kp = rep.get("ps_plan", (1, float("nan")))
+        kw = rep.get("ps_write", (1, float("nan"), float("nan")))[2]
+        kp = rep.get("ps_plan", (1, float("nan"), float("nan")))[2]
         write_bytes = payload + len(data)
         r = {"serialized_bytes": len(data), "serialize_api_ms": round(t_ser, 3),
              "serialize_api_GBps_of_output": round(len(data) / t_ser / 1e6, 2),
-             "ps_plan_ms": round(kp[1] / kp[0], 4), "ps_plan_GBps": round(payload / (kp[1] / kp[0]) / 1e6, 1),
-             "ps_write_ms": round(kw[1] / kw[0], 4), "ps_write_GBps": round(write_bytes / (kw[1] / kw[0]) / 1e6, 1),
-             "kernels_ms": {k: round(v[1] / v[0], 4) for k, v in rep.items()}}
+             "ps_plan_ms": round(kp, 4), "ps_plan_GBps": round(payload / kp / 1e6, 1),
+             "ps_write_ms": round(kw, 4), "ps_write_GBps": round(write_bytes / kw / 1e6, 1),
+             "kernels_ms": {k: round(v, 4) for k, v in kernel_medians(rep).items()},
+             "device_le_api": device_le_api(sum(kernel_medians(rep).values()), t_ser)}
         h = cr.GpuRoaring()
         ts = []
         for _ in range(4):
@@ -856,12 +889,12 @@ def conversions(torch, cr, flush, bitmaps):
             if frees:
                 cr.free(x)
             t, rep = cold_time_and_kernels(torch, cr, fn, 5, flush, after=after)
-            kn, kms = rep.get(kname, (1, float("nan")))
-            k_avg = kms / kn
+            k_avg = rep.get(kname, (1, float("nan"), float("nan")))[2]
             r[cname] = {"algorithmic_bytes": nbytes, "api_ms": round(t, 4), "api_GBps": round(nbytes / t / 1e6, 1),
                         f"{kname}_ms": round(k_avg, 4), f"{kname}_GBps": round(nbytes / k_avg / 1e6, 1),
                         "frac_of_hbm_peak": round(nbytes / k_avg / 1e6 / HBM_PEAK_GBS, 4),
-                        "kernels_ms": {k: round(v[1] / v[0], 4) for k, v in rep.items()}}
+                        "kernels_ms": {k: round(v, 4) for k, v in kernel_medians(rep).items()},
+                        "device_le_api": device_le_api(sum(kernel_medians(rep).values()), t)}
         # size-independent checks: enumerate gives ascending ids below U, and every
         # sampled id's bit is set in the bitset
         cr.enumerate_ids(g, ids_out)
@@ -953,14 +986,15 @@ def topk_secondary(torch, cr, no_cpu):
             n_pass = TK_N if f is None else int(round(sel * TK_N))
             flops = 2.0 * TK_DIM * n_pass * TK_Q
             # the MFMA kernels: tk_dist (list path) and tk_pairs (small sets' estimates, larger sets' seed rows)
-            kms = sum(v[1] / v[0] for kk, v in rep.items() if kk in ("tk_dist", "tk_pairs"))
+            kms = sum(v[2] for kk, v in rep.items() if kk in ("tk_dist", "tk_pairs"))
             ok = bool((ids[:, 0] >= 0).all().item()) and bool((dist[:, 1:] >= dist[:, :-1]).all().item())
             out[f"k{k}_{name}"] = {
                 "selectivity": round(sel, 6), "ms": round(t, 3), "qps": round(TK_Q / (t / 1e3), 1),
                 "mfma_kernels_ms": round(kms, 3),
                 "mfma_tflops": round(flops / (kms / 1e3) / 1e12, 2),
                 "mfma_frac_fp32_peak": round(flops / (kms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
-                "kernels_ms": {kk: round(v[1] / v[0], 4) for kk, v in rep.items()}, "sane": ok,
+                "kernels_ms": {kk: round(v, 4) for kk, v in kernel_medians(rep).items()}, "sane": ok,
+                "device_le_api": device_le_api(sum(kernel_medians(rep).values()), t),
             }
             log(f"topk k={k} {name}", out[f"k{k}_{name}"]["ms"], "ms", out[f"k{k}_{name}"]["mfma_frac_fp32_peak"])
     for _, f, _ in runs:
@@ -1010,7 +1044,7 @@ def cpu_baseline(ids_host):
 
     import numpy as np
     import orc
-    lib = orc.lib()
+    lib = orc.cpu_lib()
     full = np.ascontiguousarray(ids_host, dtype=np.uint32)
     s = full[:10_000_000]
     scale = N_IDS / s.size
@@ -1045,8 +1079,8 @@ def cpu_baseline(ids_host):
             "one_thread_sample": f"the first {s.size // 1_000_000}M ids, scaled x{scale:g}",
             "reference_algorithm_one_thread_ms": round(t_sort * 1e3 * scale, 1),
             "reference_algorithm": "orc_upload_from_ids: qsort + unique + bitmap build, the reference's CPU "
-                                   "pipeline (std::sort + unique + upload, bench/bench_upload_scale.cu:177-201)",
-            "cpu": cpu_info()}
+                                   "pipeline (std::sort + unique + upload, bench/bench_upload_scale.cu:102-125)",
+            "isa": orc.cpu_isa(), "cpu": cpu_info()}
 
 
 def main():
@@ -1057,6 +1091,8 @@ def main():
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-topk", action="store_true")
+    ap.add_argument("--secondary-out", default=None,
+                    help="where the secondary sections' JSON goes (default gpurun_out/bench_secondary.json)")
     ap.add_argument("--sections", default=",".join(SECTIONS),
                     help="comma-separated secondary sections to run (default: all of " + ",".join(SECTIONS) + ")")
     args = ap.parse_args()
@@ -1124,6 +1160,7 @@ def main():
     warm_ms = (time.perf_counter() - t0) * 1e3 / args.steps
 
     per_kernel = {k: v[1] / v[0] for k, v in rep.items() if not k.startswith("host:")}
+    per_kernel_median = kernel_medians(rep)
     host_ms = {k[5:]: round(v[1] / args.steps, 4) for k, v in rep.items() if k.startswith("host:")}
     path = [k for k in UPLOAD_PATH if k in per_kernel]
     dev_ms = sum(per_kernel[k] for k in path)  # each kernel launches once per step
@@ -1141,10 +1178,25 @@ def main():
     kernels = {}
     for k in path:
         kb = upload_kernel_bytes(k, N_IDS, n_c, 16383)
-        kernels[k] = {"mean_launch_ms": round(per_kernel[k], 5), "timed_launches": rep[k][0]}
+        kernels[k] = {"mean_ms": round(per_kernel[k], 5), "median_ms": round(per_kernel_median[k], 5),
+                      "launches": rep[k][0]}
         if kb:
-            kernels[k].update({"algorithmic_bytes": kb, "GBps": round(kb / per_kernel[k] / 1e6, 1),
-                               "frac": round(kb / per_kernel[k] / 1e6 / HBM_PEAK_GBS, 4)})
+            kernels[k].update({"bytes": kb, "frac": round(kb / per_kernel[k] / 1e6 / HBM_PEAK_GBS, 4)})
+
+    # BASELINE configs[1] names the three threshold variants: above 1024 ids the
+    # reference builds all-bitmap whatever the threshold (src/upload_ids.cu:573-587),
+    # so each must give the AUTO result; each is timed cold like the headline.
+    variants = {}
+    for tname, thr in (("AUTO", cr.PROMOTE_AUTO), ("KEEP_DEFAULT", cr.PROMOTE_KEEP_DEFAULT),
+                       ("ALL", cr.PROMOTE_ALL)):
+        t = cold_time(torch, lambda: cr.upload_from_device_ids(d_ids, U, thr), 7, flush, after=cr.free_async)
+        g = cr.upload_from_device_ids(d_ids, U, thr)
+        same = (g.n_containers, g.total_cardinality, g.n_bitmap_containers, g.max_key) == (n_c, total, n_c, 16383)
+        cr.free(g)
+        variants[tname] = {"ms": round(t, 4), "same_result": same}
+        if not same:
+            log("THRESHOLD VARIANT DIFFERS", tname)
+            sys.exit(1)
 
     result = {
         "metric": "upload ms @100M IDs",
@@ -1176,6 +1228,7 @@ def main():
                      "end_to_end_frac": round(path_bytes / ms_per_step / 1e6 / HBM_PEAK_GBS, 4)},
         "kernels": kernels,
         "host_ms_per_step": host_ms,
+        "threshold_variants_ms": variants,
     }
     # Achievable-bandwidth reference: a plain 1 GiB device copy (also the known-size
     # kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE).
@@ -1213,16 +1266,69 @@ def main():
         sample = d_ids.cpu().numpy().view("uint32")
         result["cpu_baseline"] = cpu_baseline(sample)
         log("cpu baseline", result["cpu_baseline"])
+    sec = None
     if not args.no_secondary:
         del d_ids
         torch.cuda.empty_cache()
         sections = set(args.sections.split(","))
-        result["secondary"] = secondary(torch, cr, flush, args.no_cpu, sections)
+        sec = secondary(torch, cr, flush, args.no_cpu, sections)
         if not args.no_topk and "topk" in sections:
             del flush
             torch.cuda.empty_cache()
-            result["secondary"]["topk_10M_x128_q1024"] = topk_secondary(torch, cr, args.no_cpu)
-    print(json.dumps(result), flush=True)
+            sec["topk_10M_x128_q1024"] = topk_secondary(torch, cr, args.no_cpu)
+        sec["device_gt_api"] = DEVICE_GT_API
+        # The full secondary tree (tens of KB) goes to its own file; the stdout
+        # line carries the headline and a few figures from it.
+        out_path = args.secondary_out or os.path.join(ROOT, "gpurun_out", "bench_secondary.json")
+        try:
+            os.makedirs(os.path.dirname(out_path), exist_ok=True)
+            with open(out_path, "w") as f:
+                json.dump(sec, f, indent=1)
+            result["secondary_file"] = os.path.relpath(out_path, ROOT)
+        except OSError as e:
+            log("could not write the secondary sections:", e)
+        result["secondary_highlights"] = highlights(sec)
+        result["device_time_exceeds_api_lines"] = len(DEVICE_GT_API)
+    line = json.dumps(result, separators=(",", ":"))
+    if len(line) > 6000:  # keep the driver-parsed line small
+        result.pop("secondary_highlights", None)
+        line = json.dumps(result, separators=(",", ":"))
+    print(line, flush=True)
+
+
+def highlights(sec):
+    """A few figures of the secondary sections, for the headline line (each is
+    taken only if its section ran)."""
+    h = {}
+
+    def take(name, fn):
+        try:
+            h[name] = fn()
+        except (KeyError, TypeError, ValueError, ZeroDivisionError):
+            pass
+    c3 = sec.get("config3_point_queries_2^30", {})
+    take("queries_10pct_uniform_partitioned_Gqps", lambda: c3["density_10pct"]["compressed_uniform_partitioned_Gqps"])
+    take("queries_10pct_uniform_partitioned_frac_18B",
+         lambda: c3["density_10pct"]["compressed_uniform_partitioned_frac_hbm_18B"])
+    take("queries_10pct_uniform_contains_Gqps", lambda: c3["density_10pct"]["compressed_uniform_contains_Gqps"])
+    take("queries_1pct_uniform_partitioned_Gqps", lambda: c3["density_1pct"]["compressed_uniform_partitioned_Gqps"])
+    c2 = sec.get("config2_set_ops_2^30", {})
+    for pair in ("BB'_AND", "AB_OR", "AB_AND", "BC_OR", "AC_OR", "CC'_AND", "AA'_AND"):
+        take(f"setop_{pair}_exec_frac", lambda p=pair: c2[p]["exec_frac_of_hbm_peak"])
+        take(f"setop_{pair}_api_ms", lambda p=pair: c2[p]["api_ms"])
+    take("multi_and_k8_fused_frac", lambda: c2["multi_and_k8_fused_all_bitmap"]["mand_and_frac_of_hbm_peak"])
+    take("multi_and_k8_fused_api_ms", lambda: c2["multi_and_k8_fused_all_bitmap"]["api_ms"])
+    uv = sec.get("upload_variants_2^30", {})
+    take("upload_clustered_100M_ms", lambda: uv["ids_clustered_100M"]["ms"])
+    take("upload_bitset_0.1pct_ms", lambda: uv["bitset_0.1pct"]["ms"])
+    take("upload_bitset_0.1pct_frac", lambda: uv["bitset_0.1pct"]["frac_of_hbm_peak"])
+    tk = sec.get("topk_10M_x128_q1024", {})
+    for case in ("k10_unfiltered", "k10_sel_0.1", "k10_sel_0.01", "k10_sel_0.001", "k100_sel_0.1"):
+        take(f"topk_{case}_ms", lambda c=case: tk[c]["ms"])
+        take(f"topk_{case}_mfma_frac", lambda c=case: tk[c]["mfma_frac_fp32_peak"])
+    cv = sec.get("conversions_2^30", {})
+    take("decompress_10pct_frac", lambda: cv["dense_10pct_bitmap"]["decompress_to_bitset"]["frac_of_hbm_peak"])
+    return h
 
 
 if __name__ == "__main__":

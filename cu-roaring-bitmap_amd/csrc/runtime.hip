@@ -262,6 +262,10 @@ static void release_block(const CachedBlock& b)
     }
 }
 
+// Test fault injection (cr_debug_fail_device_allocs): the allocations to let
+// through, then the ones to fail.  Read under g_cache_mu.
+static uint32_t g_fail_skip = 0, g_fail_count = 0;
+
 int dev_alloc(void** p, size_t bytes, hipStream_t s)
 {
     CR_HOST_PHASE("alloc");
@@ -271,6 +275,15 @@ int dev_alloc(void** p, size_t bytes, hipStream_t s)
     CR_HIP_RET(hipGetDevice(&dev));
     {
         std::lock_guard<std::mutex> lock(g_cache_mu);
+        if (g_fail_count) {
+            if (g_fail_skip) {
+                --g_fail_skip;
+            } else {
+                --g_fail_count;
+                set_error("device allocation of %zu bytes failed (injected out-of-memory)", bytes);
+                return CR_ERR_ALLOC;
+            }
+        }
         size_t best = g_cache.size();
         for (size_t i = 0; i < g_cache.size(); ++i) {
             const CachedBlock& b = g_cache[i];
@@ -675,6 +688,14 @@ int cr_mempool_trim(int device_id, size_t keep_bytes)
     return CR_OK;
 }
 
+int cr_debug_fail_device_allocs(uint32_t skip, uint32_t count)
+{
+    std::lock_guard<std::mutex> lock(g_cache_mu);
+    g_fail_skip = count ? skip : 0u;
+    g_fail_count = count;
+    return CR_OK;
+}
+
 int cr_timing_enable(int on)
 {
     std::lock_guard<std::mutex> lock(g_timing_mu);
@@ -695,33 +716,32 @@ int cr_timing_report(char* buf, size_t cap)
 {
     if (!buf || cap == 0) return CR_ERR_INVALID;
     std::lock_guard<std::mutex> lock(g_timing_mu);
-    std::vector<std::pair<std::string, std::pair<uint64_t, double>>> agg;
+    // name -> every timed launch's ms, in first-seen order
+    std::vector<std::pair<std::string, std::vector<double>>> agg;
+    auto slot = [&](const std::string& name) -> std::vector<double>& {
+        auto it = std::find_if(agg.begin(), agg.end(), [&](auto& a) { return a.first == name; });
+        if (it != agg.end()) return it->second;
+        agg.push_back({name, {}});
+        return agg.back().second;
+    };
     for (auto& r : g_timing_recs) {
         CR_HIP_RET(hipEventSynchronize(r.stop));
         float ms = 0.f;
         CR_HIP_RET(hipEventElapsedTime(&ms, r.start, r.stop));
-        auto it = std::find_if(agg.begin(), agg.end(), [&](auto& a) { return a.first == r.name; });
-        if (it == agg.end()) {
-            agg.push_back({r.name, {1, ms}});
-        } else {
-            it->second.first += 1;
-            it->second.second += ms;
-        }
+        slot(r.name).push_back(ms);
     }
-    for (auto& h : g_host_recs) {
-        auto it = std::find_if(agg.begin(), agg.end(), [&](auto& a) { return a.first == h.first; });
-        if (it == agg.end()) {
-            agg.push_back({h.first, {1, h.second}});
-        } else {
-            it->second.first += 1;
-            it->second.second += h.second;
-        }
-    }
+    for (auto& h : g_host_recs) slot(h.first).push_back(h.second);
+    // one line per name: launches, total ms, median ms (the upper median for an
+    // even count, so a single outlier launch cannot move it)
     std::string out;
     char line[256];
     for (auto& a : agg) {
-        snprintf(line, sizeof(line), "%s %llu %.6f\n", a.first.c_str(), static_cast<unsigned long long>(a.second.first),
-                 a.second.second);
+        std::vector<double> v = a.second;
+        double total = 0.0;
+        for (double x : v) total += x;
+        std::sort(v.begin(), v.end());
+        snprintf(line, sizeof(line), "%s %llu %.6f %.6f\n", a.first.c_str(), static_cast<unsigned long long>(v.size()),
+                 total, v[v.size() / 2]);
         out += line;
     }
     snprintf(buf, cap, "%s", out.c_str());

@@ -38,7 +38,7 @@ EXPORTS = [
     "cr_promote_to_bitmap", "cr_promote_auto", "cr_deep_copy",
     "cr_portable_size_in_bytes", "cr_portable_serialize", "cr_portable_deserialize",
     "cr_upload_batch", "cr_free_batch", "cr_promote_batch", "cr_batch_make_view", "cr_batch_multi_and",
-    "cr_batch_decompress", "cr_batch_contains", "cr_batch_view_contains",
+    "cr_batch_decompress", "cr_batch_contains", "cr_batch_view_contains", "cr_debug_fail_device_allocs",
 ]
 
 
@@ -189,6 +189,7 @@ def load(path: Optional[str] = None):
         "cr_batch_decompress": [P(RoaringBatch), C.c_void_p, C.c_uint64, C.c_void_p],
         "cr_batch_contains": [P(RoaringBatch), C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p],
         "cr_batch_view_contains": [P(BatchView), C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p],
+        "cr_debug_fail_device_allocs": [C.c_uint32, C.c_uint32],
     }
     for name, args in sigs.items():
         f = getattr(L, name)
@@ -521,13 +522,13 @@ def timing_enable(on: bool = True, every: int = 1):
 
 
 def timing_report() -> dict:
-    """{kernel_name: (launches, total_ms)} for the launches since timing_enable()."""
+    """{kernel_name: (launches, total_ms, median_ms)} for the launches since timing_enable()."""
     buf = C.create_string_buffer(1 << 16)
     _check(load().cr_timing_report(buf, len(buf)), "timing_report")
     out = {}
     for line in buf.value.decode().splitlines():
-        name, n, ms = line.split()
-        out[name] = (int(n), float(ms))
+        name, n, ms, med = line.split()
+        out[name] = (int(n), float(ms), float(med))
     return out
 
 

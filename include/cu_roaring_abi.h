@@ -384,9 +384,16 @@ int cr_stream_synchronize(cr_stream_t stream);
 int cr_mempool_trim(int device_id, size_t keep_bytes);
 /* Per-kernel HIP-event timing: enable (on >= 1) / disable (0) and clear the
  * records; with on = p > 1 only every p-th launch of each kernel is timed.
- * The report is one "kernel_name timed_launches total_ms" line per kernel. */
+ * The report is one "kernel_name timed_launches total_ms median_ms" line per
+ * kernel (host phases are named "host:<phase>"). */
 int cr_timing_enable(int on);
 int cr_timing_report(char* buf, size_t cap);
+/* Fault injection for tests of the error contract (no counterpart in the
+ * reference, whose failures come only from the CUDA runtime): after `skip`
+ * more successful device allocations, the next `count` fail as an
+ * out-of-memory would, with CR_ERR_ALLOC (count = 0 turns it off).  Process-
+ * wide; calls made meanwhile on other threads see it too. */
+int cr_debug_fail_device_allocs(uint32_t skip, uint32_t count);
 
 #ifdef __cplusplus
 }

@@ -5,7 +5,7 @@
  *
  * The reference's CPU path is CRoaring (third_party/CRoaring, absent from the
  * checkout) plus std::sort + unique for the id upload
- * (bench/bench_upload_scale.cu:177-201, bench/bench_multi_and.cu:144-156,
+ * (bench/bench_upload_scale.cu:102-125, bench/bench_multi_and.cu:144-156,
  * bench/bench_set_ops.cu:43-60).  These functions time the same work with
  * roaring-lite's CRoaring-equivalent algorithms (merge / galloping array
  * intersection, word-wise bitset ops with popcount), at 1 thread -- CRoaring is

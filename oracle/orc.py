@@ -14,6 +14,11 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "lib", "liborc.so")
+# The same sources built for x86-64-v4 (AVX-512): the CPU baselines run from it
+# when the host supports that level, so a baseline is never held to AVX2 on an
+# AVX-512 machine.  The checker functions always come from the v3 build.
+_LIB_V4_PATH = os.path.join(_HERE, "lib", "liborc_x86_64_v4.so")
+_V4_FLAGS = ("avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl")
 
 ARRAY, BITMAP, RUN = 0, 1, 2
 AND, OR, ANDNOT, XOR = 0, 1, 2, 3
@@ -59,95 +64,125 @@ class _OrcContainer(C.Structure):
 
 
 _lib = None
+_cpu_lib = None
 
 
 def lib():
     global _lib
     if _lib is None:
-        if not os.path.exists(_LIB_PATH):
-            raise RuntimeError(f"oracle library not built: {_LIB_PATH} (run `make -C oracle`)")
-        L = C.CDLL(_LIB_PATH)
-        P = C.POINTER
-        L.orc_free.argtypes = [P(_OrcRoaring)]
-        L.orc_resolve_auto_threshold.argtypes = [C.c_uint32, C.c_uint64]
-        L.orc_resolve_auto_threshold.restype = C.c_uint32
-        L.orc_upload_from_ids.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64, P(_OrcRoaring)]
-        L.orc_upload_from_bitset.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, P(_OrcRoaring)]
-        L.orc_upload_packed.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_int, C.c_uint64, C.c_uint32,
-                                        C.c_uint64, P(_OrcRoaring)]
-        L.orc_set_operation.argtypes = [P(_OrcRoaring), P(_OrcRoaring), C.c_int, P(_OrcRoaring)]
-        L.orc_multi_and.argtypes = [C.c_void_p, C.c_uint32, P(_OrcRoaring)]
-        L.orc_contains.argtypes = [P(_OrcRoaring), C.c_uint32]
-        L.orc_contains_many.argtypes = [P(_OrcRoaring), C.c_void_p, C.c_uint64, C.c_void_p]
-        L.orc_decompress.argtypes = [P(_OrcRoaring), C.c_void_p, C.c_uint32]
-        L.orc_true_cardinality.argtypes = [P(_OrcRoaring)]
-        L.orc_true_cardinality.restype = C.c_uint64
-        L.orc_enumerate_ids.argtypes = [P(_OrcRoaring), C.c_void_p]
-        L.orc_enumerate_ids.restype = C.c_uint64
-        L.orc_promote_to_bitmap.argtypes = [P(_OrcRoaring), P(_OrcRoaring)]
-        L.orc_promote_to_bitmap.restype = C.c_int
-        L.orc_deep_copy.argtypes = [P(_OrcRoaring), P(_OrcRoaring)]
-        L.orc_deep_copy.restype = C.c_int
-        for name in ("orc_upload_from_ids", "orc_upload_from_bitset", "orc_upload_packed",
-                     "orc_set_operation", "orc_multi_and", "orc_contains"):
-            getattr(L, name).restype = C.c_int
-        # roaring-lite
-        L.rl_create.restype = C.c_void_p
-        L.rl_destroy.argtypes = [C.c_void_p]
-        L.rl_from_sorted_ids.argtypes = [C.c_void_p, C.c_uint64]
-        L.rl_from_sorted_ids.restype = C.c_void_p
-        L.rl_from_ids.argtypes = [C.c_void_p, C.c_uint64]
-        L.rl_from_ids.restype = C.c_void_p
-        L.rl_copy.argtypes = [C.c_void_p]
-        L.rl_copy.restype = C.c_void_p
-        L.rl_run_optimize.argtypes = [C.c_void_p]
-        L.rl_op.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
-        L.rl_op.restype = C.c_void_p
-        L.rl_flip.argtypes = [C.c_void_p, C.c_uint64, C.c_uint64]
-        L.rl_flip.restype = C.c_void_p
-        L.rl_contains.argtypes = [C.c_void_p, C.c_uint32]
-        L.rl_contains.restype = C.c_int
-        L.rl_contains_many.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]
-        L.rl_cardinality.argtypes = [C.c_void_p]
-        L.rl_cardinality.restype = C.c_uint64
-        L.rl_to_ids.argtypes = [C.c_void_p, C.c_void_p]
-        L.rl_to_ids.restype = C.c_uint64
-        L.rl_n_containers.argtypes = [C.c_void_p]
-        L.rl_n_containers.restype = C.c_uint32
-        L.rl_to_containers.argtypes = [C.c_void_p, C.c_void_p]
-        L.rl_count_types.argtypes = [C.c_void_p, P(C.c_uint32), P(C.c_uint32), P(C.c_uint32)]
-        L.rl_portable_size.argtypes = [C.c_void_p]
-        L.rl_portable_size.restype = C.c_uint64
-        L.rl_portable_serialize.argtypes = [C.c_void_p, C.c_void_p]
-        L.rl_portable_serialize.restype = C.c_uint64
-        L.rl_portable_deserialize.argtypes = [C.c_void_p, C.c_uint64, P(C.c_uint64)]
-        L.rl_portable_deserialize.restype = C.c_void_p
-        # generators
-        L.orc_mt_bernoulli_ids.argtypes = [C.c_uint32, C.c_double, C.c_uint32, C.c_void_p, P(C.c_uint64)]
-        L.orc_mt_raw.argtypes = [C.c_uint32, C.c_void_p, C.c_uint64]
-        L.orc_splitmix64.argtypes = [C.c_uint64]
-        L.orc_splitmix64.restype = C.c_uint64
-        L.orc_topk_bruteforce.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint32, C.c_uint32,
-                                          C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_int]
-        L.rl_from_words.argtypes = [C.c_void_p, C.c_uint64]
-        L.rl_from_words.restype = C.c_void_p
-        L.rl_slice.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32]
-        L.rl_slice.restype = C.c_void_p
-        # CPU baselines (cpu_baseline.c)
-        for name in ("orc_cpu_upload_ids", "orc_cpu_setop", "orc_cpu_multi_and", "orc_cpu_contains",
-                     "orc_cpu_config0", "orc_cpu_topk_fp32"):
-            getattr(L, name).restype = C.c_double
-        L.orc_cpu_upload_ids.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_int, P(_OrcRoaring)]
-        L.orc_cpu_setop.argtypes = [C.c_void_p, C.c_void_p, C.c_uint32, C.c_int, C.c_int, P(C.c_uint64),
-                                    P(C.c_uint64)]
-        L.orc_cpu_multi_and.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_int, P(C.c_uint64), P(C.c_uint64)]
-        L.orc_cpu_contains.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p, C.c_int]
-        L.orc_cpu_config0.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64,
-                                      C.c_void_p, C.c_void_p, P(C.c_uint64)]
-        L.orc_cpu_topk_fp32.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,
-                                        C.c_uint32, C.c_void_p, C.c_void_p, C.c_int]
-        _lib = L
+        _lib = _load(_LIB_PATH)
     return _lib
+
+
+def host_supports_v4() -> bool:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    fl = set(line.split(":", 1)[1].split())
+                    return all(x in fl for x in _V4_FLAGS)
+    except OSError:
+        pass
+    return False
+
+
+def cpu_lib():
+    """The oracle build the CPU baselines run from: x86-64-v4 when the host has
+    AVX-512 (and that build exists), else the x86-64-v3 one."""
+    global _cpu_lib
+    if _cpu_lib is None:
+        _cpu_lib = _load(_LIB_V4_PATH) if host_supports_v4() and os.path.exists(_LIB_V4_PATH) else lib()
+    return _cpu_lib
+
+
+def cpu_isa() -> str:
+    return "x86-64-v4" if cpu_lib() is not lib() else "x86-64-v3"
+
+
+def _load(path):
+    if not os.path.exists(path):
+        raise RuntimeError(f"oracle library not built: {path} (run `make -C oracle`)")
+    L = C.CDLL(path)
+    P = C.POINTER
+    L.orc_free.argtypes = [P(_OrcRoaring)]
+    L.orc_resolve_auto_threshold.argtypes = [C.c_uint32, C.c_uint64]
+    L.orc_resolve_auto_threshold.restype = C.c_uint32
+    L.orc_upload_from_ids.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64, P(_OrcRoaring)]
+    L.orc_upload_from_bitset.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, P(_OrcRoaring)]
+    L.orc_upload_packed.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_int, C.c_uint64, C.c_uint32,
+                                    C.c_uint64, P(_OrcRoaring)]
+    L.orc_set_operation.argtypes = [P(_OrcRoaring), P(_OrcRoaring), C.c_int, P(_OrcRoaring)]
+    L.orc_multi_and.argtypes = [C.c_void_p, C.c_uint32, P(_OrcRoaring)]
+    L.orc_contains.argtypes = [P(_OrcRoaring), C.c_uint32]
+    L.orc_contains_many.argtypes = [P(_OrcRoaring), C.c_void_p, C.c_uint64, C.c_void_p]
+    L.orc_decompress.argtypes = [P(_OrcRoaring), C.c_void_p, C.c_uint32]
+    L.orc_true_cardinality.argtypes = [P(_OrcRoaring)]
+    L.orc_true_cardinality.restype = C.c_uint64
+    L.orc_enumerate_ids.argtypes = [P(_OrcRoaring), C.c_void_p]
+    L.orc_enumerate_ids.restype = C.c_uint64
+    L.orc_promote_to_bitmap.argtypes = [P(_OrcRoaring), P(_OrcRoaring)]
+    L.orc_promote_to_bitmap.restype = C.c_int
+    L.orc_deep_copy.argtypes = [P(_OrcRoaring), P(_OrcRoaring)]
+    L.orc_deep_copy.restype = C.c_int
+    for name in ("orc_upload_from_ids", "orc_upload_from_bitset", "orc_upload_packed",
+                 "orc_set_operation", "orc_multi_and", "orc_contains"):
+        getattr(L, name).restype = C.c_int
+    # roaring-lite
+    L.rl_create.restype = C.c_void_p
+    L.rl_destroy.argtypes = [C.c_void_p]
+    L.rl_from_sorted_ids.argtypes = [C.c_void_p, C.c_uint64]
+    L.rl_from_sorted_ids.restype = C.c_void_p
+    L.rl_from_ids.argtypes = [C.c_void_p, C.c_uint64]
+    L.rl_from_ids.restype = C.c_void_p
+    L.rl_copy.argtypes = [C.c_void_p]
+    L.rl_copy.restype = C.c_void_p
+    L.rl_run_optimize.argtypes = [C.c_void_p]
+    L.rl_op.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+    L.rl_op.restype = C.c_void_p
+    L.rl_flip.argtypes = [C.c_void_p, C.c_uint64, C.c_uint64]
+    L.rl_flip.restype = C.c_void_p
+    L.rl_contains.argtypes = [C.c_void_p, C.c_uint32]
+    L.rl_contains.restype = C.c_int
+    L.rl_contains_many.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]
+    L.rl_cardinality.argtypes = [C.c_void_p]
+    L.rl_cardinality.restype = C.c_uint64
+    L.rl_to_ids.argtypes = [C.c_void_p, C.c_void_p]
+    L.rl_to_ids.restype = C.c_uint64
+    L.rl_n_containers.argtypes = [C.c_void_p]
+    L.rl_n_containers.restype = C.c_uint32
+    L.rl_to_containers.argtypes = [C.c_void_p, C.c_void_p]
+    L.rl_count_types.argtypes = [C.c_void_p, P(C.c_uint32), P(C.c_uint32), P(C.c_uint32)]
+    L.rl_portable_size.argtypes = [C.c_void_p]
+    L.rl_portable_size.restype = C.c_uint64
+    L.rl_portable_serialize.argtypes = [C.c_void_p, C.c_void_p]
+    L.rl_portable_serialize.restype = C.c_uint64
+    L.rl_portable_deserialize.argtypes = [C.c_void_p, C.c_uint64, P(C.c_uint64)]
+    L.rl_portable_deserialize.restype = C.c_void_p
+    # generators
+    L.orc_mt_bernoulli_ids.argtypes = [C.c_uint32, C.c_double, C.c_uint32, C.c_void_p, P(C.c_uint64)]
+    L.orc_mt_raw.argtypes = [C.c_uint32, C.c_void_p, C.c_uint64]
+    L.orc_splitmix64.argtypes = [C.c_uint64]
+    L.orc_splitmix64.restype = C.c_uint64
+    L.orc_topk_bruteforce.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint32, C.c_uint32,
+                                      C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_int]
+    L.rl_from_words.argtypes = [C.c_void_p, C.c_uint64]
+    L.rl_from_words.restype = C.c_void_p
+    L.rl_slice.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32]
+    L.rl_slice.restype = C.c_void_p
+    # CPU baselines (cpu_baseline.c)
+    for name in ("orc_cpu_upload_ids", "orc_cpu_setop", "orc_cpu_multi_and", "orc_cpu_contains",
+                 "orc_cpu_config0", "orc_cpu_topk_fp32"):
+        getattr(L, name).restype = C.c_double
+    L.orc_cpu_upload_ids.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_int, P(_OrcRoaring)]
+    L.orc_cpu_setop.argtypes = [C.c_void_p, C.c_void_p, C.c_uint32, C.c_int, C.c_int, P(C.c_uint64),
+                                P(C.c_uint64)]
+    L.orc_cpu_multi_and.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_int, P(C.c_uint64), P(C.c_uint64)]
+    L.orc_cpu_contains.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p, C.c_int]
+    L.orc_cpu_config0.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64,
+                                  C.c_void_p, C.c_void_p, P(C.c_uint64)]
+    L.orc_cpu_topk_fp32.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,
+                                    C.c_uint32, C.c_void_p, C.c_void_p, C.c_int]
+    return L
 
 
 def _ptr(a: np.ndarray) -> int:
@@ -532,7 +567,7 @@ def cpu_upload_ids(ids, universe: int, threads: int):
     """(seconds, HostRoaring) of the threaded bucket-build upload (all-bitmap layout)."""
     ids = np.ascontiguousarray(ids, dtype=np.uint32)
     c = _OrcRoaring()
-    t = lib().orc_cpu_upload_ids(_ptr(ids), ids.size, universe, threads, C.byref(c))
+    t = cpu_lib().orc_cpu_upload_ids(_ptr(ids), ids.size, universe, threads, C.byref(c))
     if t < 0:
         raise RuntimeError("orc_cpu_upload_ids: invalid input (key past max_key, or a complement)")
     return t, _from_c(c)
@@ -541,7 +576,7 @@ def cpu_upload_ids(ids, universe: int, threads: int):
 def cpu_setop(a_shards, b_shards, op: int, threads: int):
     """(seconds, total cardinality, containers) of rl_op over paired shards."""
     card, nc = C.c_uint64(), C.c_uint64()
-    t = lib().orc_cpu_setop(_handles(a_shards), _handles(b_shards), len(a_shards), op, threads, C.byref(card),
+    t = cpu_lib().orc_cpu_setop(_handles(a_shards), _handles(b_shards), len(a_shards), op, threads, C.byref(card),
                             C.byref(nc))
     return t, card.value, nc.value
 
@@ -551,14 +586,14 @@ def cpu_multi_and(input_shards, threads: int):
     k, n = len(input_shards), len(input_shards[0])
     flat = [x for shards in input_shards for x in shards]
     card, nc = C.c_uint64(), C.c_uint64()
-    t = lib().orc_cpu_multi_and(_handles(flat), k, n, threads, C.byref(card), C.byref(nc))
+    t = cpu_lib().orc_cpu_multi_and(_handles(flat), k, n, threads, C.byref(card), C.byref(nc))
     return t, card.value, nc.value
 
 
 def cpu_contains(lite: "Lite", q, threads: int):
     q = np.ascontiguousarray(q, dtype=np.uint32)
     out = np.zeros(q.size, dtype=np.uint32)
-    t = lib().orc_cpu_contains(lite.h, _ptr(q), q.size, _ptr(out), threads)
+    t = cpu_lib().orc_cpu_contains(lite.h, _ptr(q), q.size, _ptr(out), threads)
     return t, out
 
 
@@ -570,7 +605,7 @@ def cpu_config0(a_ids, b_ids, q):
     parts = np.zeros(3, dtype=np.float64)
     cards = np.zeros(4, dtype=np.uint64)
     hits = C.c_uint64()
-    t = lib().orc_cpu_config0(_ptr(a), a.size, _ptr(b), b.size, _ptr(q), q.size, _ptr(parts), _ptr(cards),
+    t = cpu_lib().orc_cpu_config0(_ptr(a), a.size, _ptr(b), b.size, _ptr(q), q.size, _ptr(parts), _ptr(cards),
                               C.byref(hits))
     return t, parts.tolist(), [int(x) for x in cards], hits.value
 
@@ -583,6 +618,6 @@ def cpu_topk_fp32(base: np.ndarray, queries: np.ndarray, k: int, passing: Option
     dist = np.zeros((nq, k), dtype=np.float32)
     ids = np.zeros((nq, k), dtype=np.int64)
     p = None if passing is None else np.ascontiguousarray(passing, dtype=np.uint8)
-    t = lib().orc_cpu_topk_fp32(_ptr(base), base.shape[0], _ptr(queries), nq, dim,
+    t = cpu_lib().orc_cpu_topk_fp32(_ptr(base), base.shape[0], _ptr(queries), nq, dim,
                                 _ptr(p) if p is not None else None, k, _ptr(dist), _ptr(ids), threads)
     return t, dist, ids
