@@ -822,7 +822,8 @@ extern "C" int cr_promote_to_bitmap(const cr_gpu_roaring* bm, cr_stream_t stream
         set_error("cr_promote_to_bitmap: invalid argument");
         return CR_ERR_INVALID;
     }
-    return promote_impl(bm, as_stream(stream), out);
+    reset(out);
+    return produced(promote_impl(bm, as_stream(stream), out), out, as_stream(stream));
 }
 
 extern "C" int cr_deep_copy(const cr_gpu_roaring* bm, cr_stream_t stream, cr_gpu_roaring* out)
@@ -831,7 +832,8 @@ extern "C" int cr_deep_copy(const cr_gpu_roaring* bm, cr_stream_t stream, cr_gpu
         set_error("cr_deep_copy: invalid argument");
         return CR_ERR_INVALID;
     }
-    return deep_copy_impl(bm, as_stream(stream), out);
+    reset(out);
+    return produced(deep_copy_impl(bm, as_stream(stream), out), out, as_stream(stream));
 }
 
 extern "C" int cr_promote_auto(const cr_gpu_roaring* bm, cr_stream_t stream, int device_id, cr_gpu_roaring* out)
@@ -842,7 +844,8 @@ extern "C" int cr_promote_auto(const cr_gpu_roaring* bm, cr_stream_t stream, int
     }
     uint32_t thr = 0;
     CR_RET(cr_resolve_auto_threshold(bm->universe_size, device_id, &thr));
+    reset(out);
     if (thr == CR_PROMOTE_ALL && (bm->n_array_containers > 0 || bm->n_run_containers > 0))
-        return promote_impl(bm, as_stream(stream), out);  // src/promote.cu:369-385
-    return deep_copy_impl(bm, as_stream(stream), out);
+        return produced(promote_impl(bm, as_stream(stream), out), out, as_stream(stream));  // src/promote.cu:369-385
+    return produced(deep_copy_impl(bm, as_stream(stream), out), out, as_stream(stream));
 }

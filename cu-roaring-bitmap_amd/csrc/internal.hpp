@@ -126,6 +126,16 @@ int alloc_out(cr_gpu_roaring* out, const OutLayout& L, uint64_t n_meta, uint64_t
 void reset(cr_gpu_roaring* r);
 int free_async(cr_gpu_roaring* r, hipStream_t s);
 
+// The last step of every producing entry point.  `out` is output-only and was
+// reset before the call's work began; a call that fails after allocating part
+// of its result releases it on its stream and hands back an empty struct, so
+// no failure leaks device memory.
+inline int produced(int rc, cr_gpu_roaring* out, hipStream_t s)
+{
+    if (rc != CR_OK) (void)free_async(out, s);
+    return rc;
+}
+
 // ---- device helpers -------------------------------------------------------
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 

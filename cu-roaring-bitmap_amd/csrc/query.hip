@@ -459,6 +459,9 @@ extern "C" int cr_contains_batch(const cr_gpu_roaring_view* view, const uint32_t
     GpuRoaringView v;
     static_assert(sizeof(v) == sizeof(*view), "view layout");
     std::memcpy(&v, view, sizeof(v));
+    // The all-bitmap fast paths read key_index; a view without one takes the
+    // general lookup, as contains() does (roaring_view.cuh:45).
+    v.all_bitmap = v.all_bitmap && v.key_index != nullptr;
     hipStream_t s = as_stream(stream);
     if (mode == CR_QUERY_PARTITIONED) return contains_partitioned(v, d_ids, n, d_out, s);
     const uint32_t cus = num_cus();

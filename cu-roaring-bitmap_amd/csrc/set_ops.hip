@@ -38,8 +38,11 @@ struct Item {
     uint32_t aoff, boff;  // byte offsets of the source containers (0 when absent)
 };
 
-// Counters accumulated per 1024-key group and totalled over all groups.
-enum { C_ITEM, C_BB, C_MX, C_CB, C_BAE, C_AAE, C_CAE, C_CRP, C_BA, C_AA, C_CA, C_CR, C_N };
+// Counters accumulated per 1024-key group and totalled over all groups.  The
+// last three check the key indexes when the classification reads them: the keys
+// each side's index names (entries below n_containers) and the named keys whose
+// container holds another key.
+enum { C_ITEM, C_BB, C_MX, C_CB, C_BAE, C_AAE, C_CAE, C_CRP, C_BA, C_AA, C_CA, C_CR, C_KA, C_KB, C_KBAD, C_N };
 
 struct Totals {
     uint32_t c[C_N];
@@ -57,10 +60,21 @@ struct SetOpHost {
 
 // Output capacity the host allocated before planning: work items (metadata
 // entries), bitmap slots, array elements, run u16s.  0xFFFFFFFF = unbounded.
+// `items` also bounds the plan's own item scratch, so it is never unbounded.
 struct Caps {
     uint32_t items, bmp, arr, run_u16;
     uint32_t bb_only;  // the host launches the bitmap-only kernel: every item must be BB or COPY_BMP
+    // With check_kidx the classification read both key indexes: the plan is
+    // only valid if they name exactly na and nb keys, each the key its
+    // container holds (the reference matches on `keys`, src/set_ops.cu:76-122).
+    uint32_t check_kidx, na, nb;
 };
+
+// The classification reads the key indexes instead of searching the keys.
+__host__ __device__ inline bool use_kidx(const uint16_t* kidx_a, uint32_t na, const uint16_t* kidx_b, uint32_t nb)
+{
+    return kidx_a && kidx_b && na < 0xFFFFu && nb < 0xFFFFu;
+}
 
 struct Side {  // the parts of a GpuRoaring the kernels read
     const uint16_t* keys;
@@ -94,9 +108,12 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_classify(Side A, Side B, uint
     const uint32_t base = blockIdx.x * PLAN_NT;
     const uint32_t t = threadIdx.x;
     int32_t ai, bi;
-    if (A.kidx && B.kidx && A.n < 0xFFFFu && B.n < 0xFFFFu) {
+    uint32_t cnt[C_N] = {};
+    if (use_kidx(A.kidx, A.n, B.kidx, B.n)) {
         // Both sides index their keys (and 0xFFFF cannot be a real index):
-        // one coalesced load a side, no search of the keys.
+        // one coalesced load a side, no search of the keys.  Each named key is
+        // checked against its container's key, and the named keys are counted;
+        // the plan flags an index that does not describe `keys` exactly.
         const uint32_t key = base + t;
         auto look = [&](const Side& S) -> int32_t {
             const uint32_t x = key < S.kidx_n ? S.kidx[key] : 0xFFFFu;
@@ -104,6 +121,9 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_classify(Side A, Side B, uint
         };
         ai = look(A);
         bi = look(B);
+        cnt[C_KA] = ai >= 0 ? 1u : 0u;
+        cnt[C_KB] = bi >= 0 ? 1u : 0u;
+        cnt[C_KBAD] = (ai >= 0 && A.keys[ai] != key) || (bi >= 0 && B.keys[bi] != key) ? 1u : 0u;
     } else {
         const uint32_t wv = t >> 6;  // waves 0-3: the key range of this group in A and in B
         if (wv < 4) {
@@ -131,7 +151,6 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_classify(Side A, Side B, uint
     rec.bi = bi;
     rec.aoff = ai >= 0 ? A.offsets[ai] : 0u;
     rec.boff = bi >= 0 ? B.offsets[bi] : 0u;
-    uint32_t cnt[C_N] = {};
     const bool keep_a_only = op != CR_AND;                 // OR, XOR, ANDNOT copy A-only keys
     const bool keep_b_only = op == CR_OR || op == CR_XOR;  // OR, XOR copy B-only keys
     if (ai >= 0 && bi >= 0) {
@@ -213,7 +232,8 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_assign(const KeyRec* recs, co
     if (blockIdx.x == 0 && t == C_N + 1)
         totals->overflow = gtot[C_ITEM] > caps.items || gtot[C_BB] + gtot[C_MX] + gtot[C_CB] > caps.bmp ||
                            gtot[C_BAE] + gtot[C_AAE] + gtot[C_CAE] > caps.arr || 2u * gtot[C_CRP] > caps.run_u16 ||
-                           (caps.bb_only && gtot[C_BB] + gtot[C_CB] != gtot[C_ITEM]);
+                           (caps.bb_only && gtot[C_BB] + gtot[C_CB] != gtot[C_ITEM]) ||
+                           (caps.check_kidx && (gtot[C_KA] != caps.na || gtot[C_KB] != caps.nb || gtot[C_KBAD] != 0));
 
     const uint32_t key = blockIdx.x * PLAN_NT + t;
     const KeyRec rec = recs[key];
@@ -252,7 +272,7 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_assign(const KeyRec* recs, co
     it.aoff = rec.aoff;
     it.boff = rec.boff;
     it.slot = slot;
-    items[item_pos] = it;
+    if (item_pos < caps.items) items[item_pos] = it;  // the item scratch holds caps.items
 }
 
 // ---- plan for two all-bitmap inputs with key indexes -------------------------
@@ -298,8 +318,11 @@ __global__ __launch_bounds__(KP_NT) void so_plan_bitmap(const uint16_t* __restri
                                                         const uint32_t* __restrict__ off_a,
                                                         const uint32_t* __restrict__ off_b,
                                                         const uint8_t* __restrict__ ty_a,
-                                                        const uint8_t* __restrict__ ty_b, uint32_t na, uint32_t nb,
-                                                        uint32_t op, Caps caps, Item* items, Totals* totals)
+                                                        const uint8_t* __restrict__ ty_b,
+                                                        const uint16_t* __restrict__ keys_a,
+                                                        const uint16_t* __restrict__ keys_b, uint32_t na, uint32_t nb,
+                                                        uint32_t op, Caps caps, Item* items, Totals* totals,
+                                                        uint32_t* kbad)
 {
     __shared__ uint32_t lds[KP_NT / 64];
     const uint32_t t = threadIdx.x, g = blockIdx.x;
@@ -323,6 +346,11 @@ __global__ __launch_bounds__(KP_NT) void so_plan_bitmap(const uint16_t* __restri
     const bool ina = xa < na, inb = xb < nb;
     const bool is_item = (item_mask(ina, inb) & 1u) != 0;
     const bool is_bb = is_item && ina && inb;
+    // Every named key must be the key its container holds; with the counts
+    // checked below, the indexes then describe `keys` exactly.  The compaction
+    // reads these per-workgroup counts (it runs after every workgroup here).
+    const uint32_t bad = block_sum<KP_NT>((ina && keys_a[xa] != key) || (inb && keys_b[xb] != key) ? 1u : 0u, lds);
+    if (t == 0) kbad[g] = bad;
     uint32_t n_here, bb_here, cb_here;
     const uint32_t r_item = block_flag_rank<KP_NT>(is_item, lds, n_here);
     const uint32_t r_bb = block_flag_rank<KP_NT>(is_bb, lds, bb_here);
@@ -872,14 +900,23 @@ __device__ void write_host_totals(const Totals* totals, uint32_t n_out, uint32_t
 __global__ __launch_bounds__(PLAN_NT) void so_compact(const Item* items, const uint32_t* item_card,
                                                       Totals* totals, uint16_t* keys,
                                                       uint8_t* types, uint32_t* offsets, uint16_t* cards,
-                                                      SetOpHost* host)
+                                                      SetOpHost* host, const uint32_t* kbad, uint32_t n_kbad)
 {
     __shared__ uint32_t lds[PLAN_NT / 64];
     __shared__ uint32_t s_base;
     const uint32_t n_items = totals->c[C_ITEM];
     const uint32_t tile = blockIdx.x;
-    if (totals->overflow || n_items == 0) {
-        if (tile == 0 && threadIdx.x < 64 && host) write_host_totals(totals, 0, totals->overflow, host, threadIdx.x);
+    // The key-index plan's check of its named keys (n_kbad <= 64 workgroups):
+    // a mismatch invalidates the plan like an overflow.
+    // Each wave reads all the counts itself, so every wave decides alike.
+    uint32_t kb = 0;
+    if (n_kbad) {
+        const uint32_t lane = __lane_id();
+        kb = __ballot(lane < min(n_kbad, 64u) && kbad[lane] != 0u) != 0ull ? 1u : 0u;
+    }
+    const uint32_t overflow = totals->overflow | kb;
+    if (overflow || n_items == 0) {
+        if (tile == 0 && threadIdx.x < 64 && host) write_host_totals(totals, 0, overflow, host, threadIdx.x);
         return;
     }
     if (tile * PLAN_NT >= n_items) return;
@@ -1064,6 +1101,8 @@ struct SetOpPlan {
     Totals* tot;
     uint32_t* icard;
     uint32_t n_tiles;
+    uint32_t* kbad = nullptr;  // key-index plan: per-workgroup counts of mismatched named keys
+    uint32_t n_kbad = 0;
 };
 
 static int plan_set_operation(const Side& A, const Side& B, uint32_t op, uint32_t bound, const Caps& caps,
@@ -1104,17 +1143,20 @@ static int plan_bitmap_keyed(const cr_gpu_roaring* a, const cr_gpu_roaring* b, u
     const size_t o_items = c.add(sizeof(Item) * bound);
     const size_t o_tot = c.add(sizeof(Totals));
     const size_t o_card = c.add(sizeof(uint32_t) * bound);
+    const size_t o_bad = c.add(sizeof(uint32_t) * 64);
     CR_RET(P.sc.alloc(c.total, s));
     P.items = P.sc.at<Item>(o_items);
     P.tot = P.sc.at<Totals>(o_tot);
     P.icard = P.sc.at<uint32_t>(o_card);
+    P.kbad = P.sc.at<uint32_t>(o_bad);
     {
         CR_TIMED("so_plan_bitmap", s);
         const uint32_t len_a = a->max_key + 1u, len_b = b->max_key + 1u;
-        const uint32_t groups = (std::max(len_a, len_b) + KP_NT - 1) / KP_NT;
+        const uint32_t groups = (std::max(len_a, len_b) + KP_NT - 1) / KP_NT;  // max_key <= 0xFFFF: <= 64
+        P.n_kbad = groups;
         so_plan_bitmap<<<groups, KP_NT, 0, s>>>(a->key_index, len_a, b->key_index, len_b, a->offsets, b->offsets,
-                                                a->types, b->types, a->n_containers, b->n_containers, op, caps,
-                                                P.items, P.tot);
+                                                a->types, b->types, a->keys, b->keys, a->n_containers,
+                                                b->n_containers, op, caps, P.items, P.tot, P.kbad);
     }
     CR_LAUNCH_CHECK();
     return CR_OK;
@@ -1175,7 +1217,8 @@ static int exec_set_operation(const Side& A, const Side& B, uint32_t op, uint32_
     {
         CR_TIMED("so_compact", s);
         so_compact<<<std::max(1u, P.n_tiles), PLAN_NT, 0, s>>>(P.items, P.icard, P.tot, out->keys,
-                                                               out->types, out->offsets, out->cardinalities, host);
+                                                               out->types, out->offsets, out->cardinalities, host,
+                                                               P.kbad, P.n_kbad);
     }
     CR_LAUNCH_CHECK();
     return CR_OK;
@@ -1201,10 +1244,20 @@ static int set_operation_exact(const cr_gpu_roaring* a, const cr_gpu_roaring* b,
                                uint32_t op, uint32_t bound, hipStream_t s, cr_gpu_roaring* out)
 {
     SetOpPlan P;
-    const Caps unbounded{0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0u};
-    CR_RET(plan_set_operation(A, B, op, bound, unbounded, s, P));
+    // Matched on `keys` (a key search, not the key indexes, which this path
+    // does not trust), with room for `bound` items: with sorted keys each
+    // container yields at most one item, so more means malformed input.
+    Side As = A, Bs = B;
+    As.kidx = Bs.kidx = nullptr;
+    As.kidx_n = Bs.kidx_n = 0;
+    const Caps unbounded{bound, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0u, 0u, 0u, 0u};
+    CR_RET(plan_set_operation(As, Bs, op, bound, unbounded, s, P));
     Totals h{};
     CR_RET(read_back(&h, P.tot, sizeof(Totals), s));
+    if (h.overflow) {
+        set_error("set_operation: an input's keys name more containers than it holds");
+        return CR_ERR_INVALID;
+    }
     const uint32_t n_items = h.c[C_ITEM];
     if (n_items == 0) return CR_OK;
     const uint64_t n_bmp = static_cast<uint64_t>(h.c[C_BB]) + h.c[C_MX] + h.c[C_CB];
@@ -1214,7 +1267,7 @@ static int set_operation_exact(const cr_gpu_roaring* a, const cr_gpu_roaring* b,
     CR_RET(alloc_out(out, L, n_items, 0, n_bmp * 1024, arr_elems, run_u16, s));
     set_counts(out, h.c);
     const bool only_bb = h.c[C_BB] + h.c[C_CB] == n_items && aligned_bitmaps(a, b);
-    CR_RET(exec_set_operation(A, B, op, n_items, only_bb, P, out, nullptr, s));
+    CR_RET(exec_set_operation(As, Bs, op, n_items, only_bb, P, out, nullptr, s));
     uint32_t n_out = 0;
     CR_RET(read_back(&n_out, &P.tot->n_out, sizeof(uint32_t), s));
     out->n_containers = n_out;
@@ -1298,6 +1351,11 @@ int set_operation_impl(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_
         nb == na && a->n_bitmap_containers == na && b->n_bitmap_containers == nb)
         return set_operation_dense(a, b, op, s, out);
     caps.bb_only = only_bb ? 1u : 0u;
+    if (use_kidx(A.kidx, A.n, B.kidx, B.n)) {
+        caps.check_kidx = 1u;
+        caps.na = na;
+        caps.nb = nb;
+    }
     const uint64_t cap_bmp_words = static_cast<uint64_t>(caps.bmp) * 1024u;
     const OutLayout L = plan_out(bound, 0, cap_bmp_words, caps.arr, caps.run_u16);
     CR_RET(alloc_out(out, L, bound, 0, cap_bmp_words, caps.arr, caps.run_u16, s));
@@ -1649,7 +1707,8 @@ extern "C" int cr_set_operation(const cr_gpu_roaring* a, const cr_gpu_roaring* b
         set_error("cr_set_operation: invalid argument");
         return CR_ERR_INVALID;
     }
-    return set_operation_impl(a, b, op, as_stream(stream), out);
+    reset(out);
+    return produced(set_operation_impl(a, b, op, as_stream(stream), out), out, as_stream(stream));
 }
 
 extern "C" int cr_multi_and(const cr_gpu_roaring* bitmaps, uint32_t count, cr_stream_t stream, cr_gpu_roaring* out)
@@ -1658,5 +1717,6 @@ extern "C" int cr_multi_and(const cr_gpu_roaring* bitmaps, uint32_t count, cr_st
         set_error("cr_multi_and: invalid argument");
         return CR_ERR_INVALID;
     }
-    return multi_and_impl(bitmaps, count, as_stream(stream), out);
+    reset(out);
+    return produced(multi_and_impl(bitmaps, count, as_stream(stream), out), out, as_stream(stream));
 }

@@ -338,7 +338,9 @@ extern "C" int cr_upload_from_device_bitset(const uint32_t* d_words, uint32_t n_
         set_error("cr_upload_from_device_bitset: invalid argument");
         return CR_ERR_INVALID;
     }
-    return upload_from_device_bitset_impl(d_words, n_words, universe_size, as_stream(stream), out);
+    reset(out);
+    return produced(upload_from_device_bitset_impl(d_words, n_words, universe_size, as_stream(stream), out), out,
+                    as_stream(stream));
 }
 
 extern "C" int cr_upload_from_bitset(const uint32_t* host_words, uint32_t n_words, uint32_t universe_size,
@@ -349,9 +351,10 @@ extern "C" int cr_upload_from_bitset(const uint32_t* host_words, uint32_t n_word
         return CR_ERR_INVALID;
     }
     hipStream_t s = as_stream(stream);
-    if (n_words == 0) return upload_from_device_bitset_impl(nullptr, 0, universe_size, s, out);
+    reset(out);
+    if (n_words == 0) return produced(upload_from_device_bitset_impl(nullptr, 0, universe_size, s, out), out, s);
     Scratch sc;
     CR_RET(sc.alloc(static_cast<size_t>(n_words) * 4u, s));
     CR_RET(h2d_pageable(sc.ptr, host_words, static_cast<size_t>(n_words) * 4u, s));
-    return upload_from_device_bitset_impl(sc.at<uint32_t>(0), n_words, universe_size, s, out);
+    return produced(upload_from_device_bitset_impl(sc.at<uint32_t>(0), n_words, universe_size, s, out), out, s);
 }

@@ -818,7 +818,9 @@ extern "C" int cr_upload_from_device_ids(const uint32_t* d_ids, uint32_t n_ids, 
         set_error("cr_upload_from_device_ids: invalid argument");
         return CR_ERR_INVALID;
     }
-    return upload_from_device_ids_impl(d_ids, n_ids, universe_size, bitmap_threshold, as_stream(stream), out);
+    reset(out);
+    return produced(upload_from_device_ids_impl(d_ids, n_ids, universe_size, bitmap_threshold, as_stream(stream), out),
+                    out, as_stream(stream));
 }
 
 extern "C" int cr_upload_from_ids(const uint32_t* ids, uint32_t n_ids, uint32_t universe_size, cr_stream_t stream,
@@ -829,9 +831,11 @@ extern "C" int cr_upload_from_ids(const uint32_t* ids, uint32_t n_ids, uint32_t 
         return CR_ERR_INVALID;
     }
     hipStream_t s = as_stream(stream);
-    if (n_ids == 0) return upload_from_device_ids_impl(nullptr, 0, universe_size, bitmap_threshold, s, out);
+    reset(out);
+    if (n_ids == 0) return produced(upload_from_device_ids_impl(nullptr, 0, universe_size, bitmap_threshold, s, out), out, s);
     Scratch sc;
     CR_RET(sc.alloc(static_cast<size_t>(n_ids) * 4u, s));
     CR_RET(h2d_pageable(sc.ptr, ids, static_cast<size_t>(n_ids) * 4u, s));
-    return upload_from_device_ids_impl(sc.at<uint32_t>(0), n_ids, universe_size, bitmap_threshold, s, out);
+    return produced(upload_from_device_ids_impl(sc.at<uint32_t>(0), n_ids, universe_size, bitmap_threshold, s, out),
+                    out, s);
 }

@@ -240,8 +240,10 @@ extern "C" int cr_upload_containers(const cr_host_container* containers, uint32_
         set_error("cr_upload_containers: invalid argument");
         return CR_ERR_INVALID;
     }
-    return upload_containers_impl(containers, n, universe_size, complemented, logical_cardinality, as_stream(stream),
-                                  bitmap_threshold, out);
+    reset(out);
+    return produced(upload_containers_impl(containers, n, universe_size, complemented, logical_cardinality,
+                                           as_stream(stream), bitmap_threshold, out),
+                    out, as_stream(stream));
 }
 
 extern "C" int cr_get_meta(const cr_host_container* c, uint32_t n, cr_meta* out)

@@ -39,7 +39,7 @@ struct GpuRoaringView {
     {
         const uint32_t key = id >> 16;
         const uint32_t low = id & 0xFFFFu;
-        if (all_bitmap) {  // two dependent loads: key_index, then one bitmap word
+        if (all_bitmap && key_index) {  // two dependent loads: key_index, then one bitmap word
             if (key > max_key) return negated;
             const uint32_t idx = key_index[key];
             if (idx == 0xFFFFu) return negated;

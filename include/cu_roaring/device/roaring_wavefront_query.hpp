@@ -34,7 +34,7 @@ __device__ __forceinline__ bool wavefront_contains(const GpuRoaringView& r, uint
         const unsigned long long members = __ballot(mine);
         if (round == 0 && __popcll(members) < detail::kMinSharedLanes) break;
         // Uniform lookup: every lane computes the same address (one request).
-        if (r.all_bitmap) {
+        if (r.all_bitmap && r.key_index) {
             int idx = -1;
             if (lk <= r.max_key) {
                 const uint32_t v = r.key_index[lk];

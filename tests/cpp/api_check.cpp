@@ -11,6 +11,7 @@
 #include <random>
 #include <set>
 #include <stdexcept>
+#include <string>
 #include <vector>
 
 #include <cu_roaring/cu_roaring.cuh>
@@ -233,6 +234,34 @@ int main()
     v2::free_batch(anded);
     v2::free_batch(pb);
     v2::free_batch(batch);
+
+    // ---- an allocation failure surfaces as std::runtime_error -------------------------
+    // (the reference's CUDA_CHECK contract, include/cu_roaring/detail/utils.cuh:9-18):
+    // the first, then the third device allocation of each call fails.
+    for (uint32_t skip : {0u, 2u}) {
+        int caught = 0;
+        cr_debug_fail_device_allocs(skip, 1);
+        try {
+            cr::GpuRoaring X = cr::upload_from_ids(a_ids.data(), static_cast<uint32_t>(a_ids.size()), U);
+            cr::gpu_roaring_free(X);
+        } catch (const std::runtime_error& e) {
+            caught = std::string(e.what()).find("out-of-memory") != std::string::npos ? 1 : 2;
+        }
+        cr_debug_fail_device_allocs(0, 1);
+        try {
+            cr::GpuRoaring X = cr::set_operation(A, B, cr::SetOp::OR);
+            cr::gpu_roaring_free(X);
+        } catch (const std::runtime_error& e) {
+            caught += std::string(e.what()).find("out-of-memory") != std::string::npos ? 10 : 20;
+        }
+        cr_debug_fail_device_allocs(0, 0);
+        CHECK(caught == 11 || (skip == 2 && caught == 10));  // an upload may make fewer than 3 allocations
+    }
+    {  // and the library still works afterwards
+        cr::GpuRoaring X = cr::upload_from_ids(a_ids.data(), static_cast<uint32_t>(a_ids.size()), U);
+        CHECK(X.total_cardinality == sa.size());
+        cr::gpu_roaring_free(X);
+    }
     for (cr::GpuRoaring* g : {&A, &B, &AB, &M, &P, &D, &R}) cr::gpu_roaring_free(*g);
     HIP_OK(hipFree(dq));
     HIP_OK(hipFree(dw));
