@@ -329,6 +329,7 @@ __global__ __launch_bounds__(BUILD_NT) void qp_answer(const uint32_t* __restrict
 {
     __shared__ alignas(16) uint32_t bits[BK_KEYS * 2048u];  // the bucket's 16 containers, 128 KiB
     __shared__ GroupQueue queue;
+    __shared__ uint32_t desc[BUILD_WAVES * DESC_CAP];
     const uint32_t t = threadIdx.x;
     const uint32_t b = (blockIdx.x % 8) * build_per_xcd(g.NB) + blockIdx.x / 8;
     if (b >= g.NB) return;
@@ -339,7 +340,7 @@ __global__ __launch_bounds__(BUILD_NT) void qp_answer(const uint32_t* __restrict
     // All 8 answers of a group go into one byte that only this lane writes:
     // fields past the run answer into b's padding, and any 20-bit value
     // indexes the LDS image.
-    walk_groups(part, tab, g, b, wave, lane, queue,
+    walk_groups(part, tab, g, b, wave, lane, queue, desc,
                 [&] {  // wave w loads container w of the bucket (zeros past the last key)
                     if (key < g.K) {
                         qp_load_container(v, key, bits + wave * 2048u, lane);
@@ -349,15 +350,16 @@ __global__ __launch_bounds__(BUILD_NT) void qp_answer(const uint32_t* __restrict
                         for (int j = 0; j < 8; ++j) w4[lane + 64 * j] = make_uint4(0, 0, 0, 0);
                     }
                 },
-                [&](uint32_t tile, uint32_t S, uint32_t j, uint32_t, const uint32_t (&f)[8]) {
+                [&](uint32_t tile, uint32_t p, uint32_t n, const uint32_t (&f)[8]) {
                     uint32_t a = 0;
 #pragma unroll
                     for (uint32_t k = 0; k < 8u; ++k) {
                         const uint32_t F = f[k] & FIELD_MASK;
                         a |= ((bits[F >> 5] >> (F & 31u)) & 1u) << k;
                     }
-                    ans[static_cast<uint64_t>(tile) * abytes + (qp_pstart(S, b) >> 3) + j] =
-                        static_cast<uint8_t>(a ^ flip);
+                    // p = S + 8 j for the run's start S: qp_pstart(p, b) = qp_pstart(S, b) + 8 j
+                    if (n != 0u)
+                        ans[static_cast<uint64_t>(tile) * abytes + (qp_pstart(p, b) >> 3)] = static_cast<uint8_t>(a ^ flip);
                 });
 }
 

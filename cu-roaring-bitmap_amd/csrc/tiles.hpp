@@ -448,35 +448,39 @@ inline uint32_t build_grid_persistent(uint32_t nb, uint32_t cus)
     return 8 * std::min(build_per_xcd(nb), std::max(1u, cus / 8));
 }
 
-// Calls on_group(tile, S, j, n, f) for every group of 8 consecutive fields of
+// Calls on_group(tile, p, n, f) for every group of 8 consecutive fields of
 // bucket b's run in every tile: the run holds sorted positions [S, E) of the
-// tile, group j its fields S + 8 j .. S + 8 j + 7, of which the first
-// n = min(8, E - S - 8 j) are the run's (the rest are whatever follows in the
-// tile's stream, possibly past what the tile sort wrote: any 20-bit value);
-// f[k] is field k's 20 bits, unmasked above them.  prologue() runs first, in
-// every thread, once the first run bounds are requested: the caller's LDS
-// set-up, published by a workgroup barrier before the first on_group.  Every
-// thread of the BUILD_NT-thread workgroup calls it (wave = t >> 6, lane = its
-// lane).  Reads
-// reach 7 words past a group's first word: `part` needs 8 words of slack past
-// the last tile.
+// tile, a group the fields p .. p + 7 with p = S + 8 j, of which the first
+// n = min(8, E - p) are the run's (the rest are whatever follows in the tile's
+// stream, possibly past what the tile sort wrote: any 20-bit value); f[k] is
+// field k's 20 bits, unmasked above them.  n = 0 marks an empty slot of a
+// round, whose fields are any of the tile's: on_group must then leave no trace.  prologue() runs first, in every
+// thread, once the first run bounds are requested: the caller's LDS set-up,
+// published by a workgroup barrier before the first on_group.  Every thread of
+// the BUILD_NT-thread workgroup calls it (wave = t >> 6, lane = its lane).
+// Reads reach 8 words past a group's first word, rounded down to an even word:
+// `part` needs 8 words of slack past the last tile.
 //
 // Wave w owns tile blocks w, w + 16, ...; a step covers 2 x 64 / TB of them,
 // two tiles per lane, whose run bounds are loaded a step ahead.  The step's
 // groups are numbered across the wave (an exclusive scan of the lanes' group
-// counts) and dealt to the lanes in rounds of 64, so neighbouring lanes take
-// neighbouring groups of one run (their loads share cache lines, and nearly
-// every lane has 8 fields); eight rounds are loaded (six words a group) before
-// any is handed on.  A run of more than GROUP_LONG groups (sorted or clustered
-// ids: a bucket's fields in a few tiles, all in one wave's blocks) is queued in
-// LDS and its groups dealt to all sixteen waves after the walk; one that finds
-// the queue full is dealt with its wave's other runs.  `queue` is the
-// workgroup's LDS queue.
-// Measured against a walk of 16-word windows by 4-lane groups (100M ids at
-// 2^30, ids_build): uniform ids 0.124 against 0.125-0.131 ms; sorted ids 0.101
-// against 0.19 ms; sorted groups of 4096 0.106 against 0.196 ms.
+// counts); each lane writes a 4-byte descriptor of each of its groups into the
+// wave's LDS list `desc` (DESC_CAP entries: longer steps go in chunks), and the
+// lanes then take the groups in rounds of 64, lane l the l-th of each round, so
+// neighbouring lanes read neighbouring words of one run (their loads share
+// cache lines); eight rounds are loaded before any is handed on.  A descriptor
+// is the owner lane (6 bits), which of its two tiles (1), the group's first
+// sorted position p (15: p < TILE) and n - 1 (3).  A run of more than
+// GROUP_LONG groups (sorted or clustered ids: a bucket's fields in a few tiles,
+// all in one wave's blocks) is queued in LDS and its groups dealt to all
+// sixteen waves after the walk; one that finds the queue full is dealt with its
+// wave's other runs.  `queue` is the workgroup's LDS queue.
 constexpr uint32_t GROUP_LONG = 64;
-constexpr uint32_t GROUP_QCAP = 2048;  // 16 KiB of LDS beside the callers' 128 KiB
+constexpr uint32_t GROUP_QCAP = 1024;  // 8 KiB of LDS beside the callers' 128 KiB image
+constexpr uint32_t DESC_CAP = 256;     // descriptors per wave: 16 KiB for sixteen waves
+constexpr uint32_t DESC_EMPTY = 1u << 31;  // a round's slot past the step's last group (n = 0)
+constexpr uint32_t WALK_ROUNDS = DESC_CAP / 64;  // groups a lane has in flight: one batch a chunk
+static_assert(TILE <= 32768, "descriptor positions are 15 bits");
 
 // LDS queue of long runs, declared by walk_groups' caller: one per
 // workgroup, whatever the number of walk_groups instances it inlines.
@@ -490,17 +494,31 @@ struct FieldGroup {
     uint32_t o;     // the first field's bit within word w0
 };
 
-__device__ __forceinline__ void group_load(const uint32_t* __restrict__ part, uint32_t tile, uint32_t S, uint32_t j,
-                                           FieldGroup& q)
+// The words of the group whose first field sits at sorted position p of
+// `tile`: four 8-byte loads from the even word at or below w0.
+struct GroupWords {
+    uint2 p[4];
+    uint32_t odd, o;
+};
+
+__device__ __forceinline__ void group_issue(const uint32_t* __restrict__ part, uint32_t tile, uint32_t p,
+                                            GroupWords& q)
 {
-    const uint32_t bit = FIELD_BITS * (S + 8u * j);
+    const uint32_t bit = FIELD_BITS * p;
     const uint32_t w0 = bit >> 5;
     q.o = bit & 31u;
+    q.odd = w0 & 1u;
     const uint2* src = reinterpret_cast<const uint2*>(part + static_cast<uint64_t>(tile) * TILE_WORDS + (w0 & ~1u));
-    const uint2 p0 = src[0], p1 = src[1], p2 = src[2], p3 = src[3];
-    const bool odd = (w0 & 1u) != 0u;
-    q.x[0] = odd ? p0.y : p0.x, q.x[1] = odd ? p1.x : p0.y, q.x[2] = odd ? p1.y : p1.x;
-    q.x[3] = odd ? p2.x : p1.y, q.x[4] = odd ? p2.y : p2.x, q.x[5] = odd ? p3.x : p2.y;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q.p[i] = src[i];
+}
+
+__device__ __forceinline__ void group_words(const GroupWords& w, FieldGroup& q)
+{
+    const bool odd = w.odd != 0u;
+    q.x[0] = odd ? w.p[0].y : w.p[0].x, q.x[1] = odd ? w.p[1].x : w.p[0].y, q.x[2] = odd ? w.p[1].y : w.p[1].x;
+    q.x[3] = odd ? w.p[2].x : w.p[1].y, q.x[4] = odd ? w.p[2].y : w.p[2].x, q.x[5] = odd ? w.p[3].x : w.p[2].y;
+    q.o = w.o;
 }
 
 __device__ __forceinline__ void group_fields(const FieldGroup& q, uint32_t (&f)[8])
@@ -521,17 +539,28 @@ __device__ __forceinline__ void group_fields(const FieldGroup& q, uint32_t (&f)[
     f[7] = d4 >> 12;
 }
 
+// The wave's own LDS writes are visible to its later LDS reads (its LDS
+// operations retire in order); this keeps the compiler from moving them across.
+__device__ __forceinline__ void wave_lds_fence()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <class Prologue, class OnGroup>
 __device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, const uint16_t* __restrict__ tab,
                                             const IdsGeom& g, uint32_t b, uint32_t wave, uint32_t lane,
-                                            GroupQueue& queue, Prologue prologue, OnGroup on_group)
+                                            GroupQueue& queue, uint32_t* desc, Prologue prologue, OnGroup on_group)
 {
     uint2* q_ent = queue.ent;
     uint32_t& q_n = queue.n;
-    auto handle = [&](uint32_t tile, uint32_t S, uint32_t E, uint32_t j, const FieldGroup& q) {
+    auto handle = [&](uint32_t tile, uint32_t p, uint32_t n, const GroupWords& w) {
+        FieldGroup q;
+        group_words(w, q);
         uint32_t f[8];
         group_fields(q, f);
-        on_group(tile, S, j, min(E - S - 8u * j, 8u), f);
+        on_group(tile, p, n, f);
     };
     constexpr uint32_t BPS = 64u / TB;
     const uint32_t n_blk = (g.n_tiles + TB - 1) / TB;
@@ -547,10 +576,7 @@ __device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, c
             r1 = tc[TB];
         }
     };
-    // A step covers 2 x 64 / TB blocks, two tiles per lane (halves 0 and 1),
-    // whose run bounds are loaded a step ahead.  The lanes' group counts (both
-    // tiles) are scanned over the wave, and the step's groups are dealt out in
-    // batches of eight rounds of 64, all eight loaded before any is handed on.
+    uint32_t* wdesc = desc + wave * DESC_CAP;
     uint32_t a0, a1, b0, b1;
     tab_load(0, a0, a1);
     tab_load(1, b0, b1);
@@ -563,59 +589,65 @@ __device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, c
         const uint32_t Sa = a0, Ea = a1, Sb = b0, Eb = b1;
         tab_load(2u * st + 2u, a0, a1);
         tab_load(2u * st + 3u, b0, b1);
-        const uint32_t ta = tile_of(2u * st, lane), tb = tile_of(2u * st + 1u, lane);
         uint32_t Ga = (Ea - Sa + 7u) / 8u, Gb = (Eb - Sb + 7u) / 8u;  // E >= S
         if (Ga > GROUP_LONG) {
             const uint32_t slot = atomicAdd(&q_n, 1u);
-            if (slot < GROUP_QCAP) q_ent[slot] = make_uint2(ta, Sa | (Ea << 16)), Ga = 0;
+            if (slot < GROUP_QCAP) q_ent[slot] = make_uint2(tile_of(2u * st, lane), Sa | (Ea << 16)), Ga = 0;
         }
         if (Gb > GROUP_LONG) {
             const uint32_t slot = atomicAdd(&q_n, 1u);
-            if (slot < GROUP_QCAP) q_ent[slot] = make_uint2(tb, Sb | (Eb << 16)), Gb = 0;
+            if (slot < GROUP_QCAP) q_ent[slot] = make_uint2(tile_of(2u * st + 1u, lane), Sb | (Eb << 16)), Gb = 0;
         }
         const uint32_t G = Ga + Gb;
         uint32_t P = wave_incl_scan(G);  // then exclusive: the lane's first group
         const uint32_t T = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(P), 63));
         P -= G;
-        for (uint32_t r0 = 0; 64u * r0 < T; r0 += 8u) {
-            uint32_t w[8][6], tl[8], ss[8], ee[8], jj[8];
+        for (uint32_t c0 = 0; c0 < T; c0 += DESC_CAP) {
+            // This lane's groups numbered [c0, c0 + DESC_CAP): their descriptors.
+            const uint32_t u_hi = min(P + G, c0 + DESC_CAP);
+            for (uint32_t u = max(P, c0); u < u_hi; ++u) {
+                const uint32_t j = u - P;
+                const bool in_a = j < Ga;
+                const uint32_t p = in_a ? Sa + 8u * j : Sb + 8u * (j - Ga);
+                const uint32_t n = min((in_a ? Ea : Eb) - p, 8u);
+                wdesc[u - c0] = lane | (in_a ? 0u : 64u) | (p << 7) | ((n - 1u) << 22);
+            }
+            wave_lds_fence();
+            const uint32_t nh = min(T - c0, DESC_CAP);
+            // WALK_ROUNDS groups a lane in flight: their descriptors are read,
+            // their addresses formed and all their loads issued before any is
+            // used, with no branch between (an empty slot reads the tile's first
+            // group and is handed on with n = 0), so the loads overlap.
+            for (uint32_t r0 = 0; 64u * r0 < nh; r0 += WALK_ROUNDS) {
+                uint32_t dd[WALK_ROUNDS];
 #pragma unroll
-            for (uint32_t k = 0; k < 8u; ++k) {
-                const uint32_t u = 64u * (r0 + k) + lane;
-                uint32_t l = 0;  // the last lane whose first group is <= u holds group u
-#pragma unroll
-                for (uint32_t step = 32; step > 0; step >>= 1) {
-                    const uint32_t c = l + step;
-                    const uint32_t pc = static_cast<uint32_t>(__shfl(P, static_cast<int>(c & 63u), 64));
-                    if (c < 64u && pc <= u) l = c;
+                for (uint32_t k = 0; k < WALK_ROUNDS; ++k) {
+                    const uint32_t u = 64u * (r0 + k) + lane;
+                    dd[k] = wdesc[min(u, nh - 1u)] | (u < nh ? 0u : DESC_EMPTY);
                 }
-                const uint32_t jl = u - static_cast<uint32_t>(__shfl(P, static_cast<int>(l), 64));
-                const uint32_t ga = static_cast<uint32_t>(__shfl(Ga, static_cast<int>(l), 64));
-                const bool in_a = jl < ga;
-                const uint32_t sa = static_cast<uint32_t>(__shfl(Sa, static_cast<int>(l), 64));
-                const uint32_t ea = static_cast<uint32_t>(__shfl(Ea, static_cast<int>(l), 64));
-                const uint32_t sb = static_cast<uint32_t>(__shfl(Sb, static_cast<int>(l), 64));
-                const uint32_t eb = static_cast<uint32_t>(__shfl(Eb, static_cast<int>(l), 64));
-                ss[k] = in_a ? sa : sb;
-                ee[k] = u < T ? (in_a ? ea : eb) : ss[k];  // an empty slot: no fields
-                jj[k] = in_a ? jl : jl - ga;
-                tl[k] = tile_of(2u * st + (in_a ? 0u : 1u), l);
-                if (u < T) {
-                    const uint32_t* src = part + static_cast<uint64_t>(tl[k]) * TILE_WORDS +
-                                          ((FIELD_BITS * (ss[k] + 8u * jj[k])) >> 5);
+                const uint2* src[WALK_ROUNDS];
 #pragma unroll
-                    for (uint32_t i = 0; i < 6u; ++i) w[k][i] = src[i];
+                for (uint32_t k = 0; k < WALK_ROUNDS; ++k) {
+                    const uint32_t tile = tile_of(2u * st + ((dd[k] >> 6) & 1u), dd[k] & 63u);
+                    const uint32_t w0 = (FIELD_BITS * ((dd[k] >> 7) & 0x7FFFu)) >> 5;
+                    src[k] = reinterpret_cast<const uint2*>(part + static_cast<uint64_t>(tile) * TILE_WORDS + (w0 & ~1u));
+                }
+                GroupWords w[WALK_ROUNDS];
+#pragma unroll
+                for (uint32_t k = 0; k < WALK_ROUNDS; ++k)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) w[k].p[i] = src[k][i];
+#pragma unroll
+                for (uint32_t k = 0; k < WALK_ROUNDS; ++k) {
+                    const uint32_t p = (dd[k] >> 7) & 0x7FFFu;
+                    const uint32_t bit = FIELD_BITS * p;
+                    w[k].o = bit & 31u;
+                    w[k].odd = (bit >> 5) & 1u;
+                    const uint32_t tile = tile_of(2u * st + ((dd[k] >> 6) & 1u), dd[k] & 63u);
+                    handle(tile, p, (dd[k] & DESC_EMPTY) ? 0u : ((dd[k] >> 22) & 7u) + 1u, w[k]);
                 }
             }
-#pragma unroll
-            for (uint32_t k = 0; k < 8u; ++k) {
-                if (ee[k] == ss[k]) continue;
-                FieldGroup q;
-#pragma unroll
-                for (uint32_t i = 0; i < 6u; ++i) q.x[i] = w[k][i];
-                q.o = (FIELD_BITS * (ss[k] + 8u * jj[k])) & 31u;
-                handle(tl[k], ss[k], ee[k], jj[k], q);
-            }
+            wave_lds_fence();  // every read of the list is done before the next chunk's writes
         }
     }
     // The queued runs: their groups in chunks of 64 (one a lane), the chunks of
@@ -631,9 +663,9 @@ __device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, c
         for (uint32_t c = (wave + BUILD_WAVES - off % BUILD_WAVES) % BUILD_WAVES; c < nch; c += BUILD_WAVES) {
             const uint32_t j = 64u * c + lane;
             if (j < G) {
-                FieldGroup q;
-                group_load(part, ent.x, S, j, q);
-                handle(ent.x, S, E, j, q);
+                GroupWords w;
+                group_issue(part, ent.x, S + 8u * j, w);
+                handle(ent.x, S + 8u * j, min(E - S - 8u * j, 8u), w);
             }
         }
         off += nch;

@@ -214,6 +214,7 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
     __shared__ uint32_t wave_pc[BUILD_WAVES];
     __shared__ uint32_t s_next, s_wmax;
     __shared__ GroupQueue queue;
+    __shared__ uint32_t desc[BUILD_WAVES * DESC_CAP];
     const uint32_t t = threadIdx.x;
     const uint32_t wave = t >> 6;
     const uint32_t x = blockIdx.x % 8, slot = blockIdx.x / 8;
@@ -282,17 +283,20 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
         // registers across the whole loop.
         uint32_t lane = __lane_id();
         asm volatile("" : "+v"(lane));
-        walk_groups(part, tab, g, b, wave, lane, queue,
+        walk_groups(part, tab, g, b, wave, lane, queue, desc,
                     [&] {
                         for (uint32_t i = t; i < BK_KEYS * 512u; i += BUILD_NT)
                             reinterpret_cast<uint4*>(bits)[i] = make_uint4(0, 0, 0, 0);
                         if constexpr (decltype(first)::value) compute_order();
                     },
-                    [&](uint32_t, uint32_t, uint32_t, uint32_t n, const uint32_t (&f)[8]) {
+                    [&](uint32_t, uint32_t, uint32_t n, const uint32_t (&f)[8]) {
+                        // Fields past the run OR in nothing (no branch per field); an
+                        // empty slot sets nothing (its lanes would all hit one group's words).
+                        if (n == 0u) return;
 #pragma unroll
                         for (uint32_t k = 0; k < 8u; ++k) {
                             const uint32_t F = f[k] & FIELD_MASK;  // key-in-bucket << 16 | low 16 bits
-                            if (k < n) atomicOr(&bits[F >> 5], 1u << (F & 31u));
+                            atomicOr(&bits[F >> 5], k < n ? 1u << (F & 31u) : 0u);
                         }
                     });
         __syncthreads();
