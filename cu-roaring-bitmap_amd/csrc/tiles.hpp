@@ -479,7 +479,8 @@ constexpr uint32_t GROUP_LONG = 64;
 constexpr uint32_t GROUP_QCAP = 1024;  // 8 KiB of LDS beside the callers' 128 KiB image
 constexpr uint32_t DESC_CAP = 256;     // descriptors per wave: 16 KiB for sixteen waves
 constexpr uint32_t DESC_EMPTY = 1u << 31;  // a round's slot past the step's last group (n = 0)
-constexpr uint32_t WALK_ROUNDS = DESC_CAP / 64;  // groups a lane has in flight: one batch a chunk
+constexpr uint32_t DESC_ROUNDS = DESC_CAP / 64;  // rounds of 64 groups the list holds
+constexpr uint32_t WALK_ROUNDS = 2 * DESC_ROUNDS;   // groups a lane has in flight
 static_assert(TILE <= 32768, "descriptor positions are 15 bits");
 
 // LDS queue of long runs, declared by walk_groups' caller: one per
@@ -602,52 +603,60 @@ __device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, c
         uint32_t P = wave_incl_scan(G);  // then exclusive: the lane's first group
         const uint32_t T = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(P), 63));
         P -= G;
-        for (uint32_t c0 = 0; c0 < T; c0 += DESC_CAP) {
-            // This lane's groups numbered [c0, c0 + DESC_CAP): their descriptors.
-            const uint32_t u_hi = min(P + G, c0 + DESC_CAP);
-            for (uint32_t u = max(P, c0); u < u_hi; ++u) {
-                const uint32_t j = u - P;
-                const bool in_a = j < Ga;
-                const uint32_t p = in_a ? Sa + 8u * j : Sb + 8u * (j - Ga);
-                const uint32_t n = min((in_a ? Ea : Eb) - p, 8u);
-                wdesc[u - c0] = lane | (in_a ? 0u : 64u) | (p << 7) | ((n - 1u) << 22);
-            }
-            wave_lds_fence();
-            const uint32_t nh = min(T - c0, DESC_CAP);
-            // WALK_ROUNDS groups a lane in flight: their descriptors are read,
-            // their addresses formed and all their loads issued before any is
-            // used, with no branch between (an empty slot reads the tile's first
-            // group and is handed on with n = 0), so the loads overlap.
-            for (uint32_t r0 = 0; 64u * r0 < nh; r0 += WALK_ROUNDS) {
-                uint32_t dd[WALK_ROUNDS];
+        // Batches of WALK_ROUNDS rounds (64 groups a round): the descriptor
+        // list holds DESC_ROUNDS rounds, so it is filled and read into
+        // registers WALK_ROUNDS / DESC_ROUNDS times per batch before any load.
+        for (uint32_t c0 = 0; c0 < T; c0 += 64u * WALK_ROUNDS) {
+            uint32_t dd[WALK_ROUNDS];
 #pragma unroll
-                for (uint32_t k = 0; k < WALK_ROUNDS; ++k) {
-                    const uint32_t u = 64u * (r0 + k) + lane;
-                    dd[k] = wdesc[min(u, nh - 1u)] | (u < nh ? 0u : DESC_EMPTY);
-                }
-                const uint2* src[WALK_ROUNDS];
+            for (uint32_t h = 0; h < WALK_ROUNDS / DESC_ROUNDS; ++h) {
+                const uint32_t w0 = c0 + h * DESC_CAP;  // wave-uniform
+                if (w0 < T) {
+                    // This lane's groups numbered [w0, w0 + DESC_CAP): their descriptors.
+                    const uint32_t u_hi = min(P + G, w0 + DESC_CAP);
+                    for (uint32_t u = max(P, w0); u < u_hi; ++u) {
+                        const uint32_t j = u - P;
+                        const bool in_a = j < Ga;
+                        const uint32_t p = in_a ? Sa + 8u * j : Sb + 8u * (j - Ga);
+                        const uint32_t n = min((in_a ? Ea : Eb) - p, 8u);
+                        wdesc[u - w0] = lane | (in_a ? 0u : 64u) | (p << 7) | ((n - 1u) << 22);
+                    }
+                    wave_lds_fence();
 #pragma unroll
-                for (uint32_t k = 0; k < WALK_ROUNDS; ++k) {
-                    const uint32_t tile = tile_of(2u * st + ((dd[k] >> 6) & 1u), dd[k] & 63u);
-                    const uint32_t w0 = (FIELD_BITS * ((dd[k] >> 7) & 0x7FFFu)) >> 5;
-                    src[k] = reinterpret_cast<const uint2*>(part + static_cast<uint64_t>(tile) * TILE_WORDS + (w0 & ~1u));
-                }
-                GroupWords w[WALK_ROUNDS];
+                    for (uint32_t k = 0; k < DESC_ROUNDS; ++k) {
+                        const uint32_t u = w0 + 64u * k + lane;
+                        // an empty slot repeats the step's last group, marked empty
+                        dd[h * DESC_ROUNDS + k] = wdesc[min(u, T - 1u) - w0] | (u < T ? 0u : DESC_EMPTY);
+                    }
+                    wave_lds_fence();  // the reads are done before the list is written again
+                } else {
 #pragma unroll
-                for (uint32_t k = 0; k < WALK_ROUNDS; ++k)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) w[k].p[i] = src[k][i];
-#pragma unroll
-                for (uint32_t k = 0; k < WALK_ROUNDS; ++k) {
-                    const uint32_t p = (dd[k] >> 7) & 0x7FFFu;
-                    const uint32_t bit = FIELD_BITS * p;
-                    w[k].o = bit & 31u;
-                    w[k].odd = (bit >> 5) & 1u;
-                    const uint32_t tile = tile_of(2u * st + ((dd[k] >> 6) & 1u), dd[k] & 63u);
-                    handle(tile, p, (dd[k] & DESC_EMPTY) ? 0u : ((dd[k] >> 22) & 7u) + 1u, w[k]);
+                    for (uint32_t k = 0; k < DESC_ROUNDS; ++k) dd[h * DESC_ROUNDS + k] = dd[h * DESC_ROUNDS - 1u] | DESC_EMPTY;
                 }
             }
-            wave_lds_fence();  // every read of the list is done before the next chunk's writes
+            // All the batch's addresses, then all its loads, then the groups:
+            // no branch between, so the loads are in flight together.
+            const uint2* src[WALK_ROUNDS];
+#pragma unroll
+            for (uint32_t k = 0; k < WALK_ROUNDS; ++k) {
+                const uint32_t tile = tile_of(2u * st + ((dd[k] >> 6) & 1u), dd[k] & 63u);
+                const uint32_t w0 = (FIELD_BITS * ((dd[k] >> 7) & 0x7FFFu)) >> 5;
+                src[k] = reinterpret_cast<const uint2*>(part + static_cast<uint64_t>(tile) * TILE_WORDS + (w0 & ~1u));
+            }
+            GroupWords w[WALK_ROUNDS];
+#pragma unroll
+            for (uint32_t k = 0; k < WALK_ROUNDS; ++k)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w[k].p[i] = src[k][i];
+#pragma unroll
+            for (uint32_t k = 0; k < WALK_ROUNDS; ++k) {
+                const uint32_t p = (dd[k] >> 7) & 0x7FFFu;
+                const uint32_t bit = FIELD_BITS * p;
+                w[k].o = bit & 31u;
+                w[k].odd = (bit >> 5) & 1u;
+                const uint32_t tile = tile_of(2u * st + ((dd[k] >> 6) & 1u), dd[k] & 63u);
+                handle(tile, p, (dd[k] & DESC_EMPTY) ? 0u : ((dd[k] >> 22) & 7u) + 1u, w[k]);
+            }
         }
     }
     // The queued runs: their groups in chunks of 64 (one a lane), the chunks of
