@@ -684,6 +684,16 @@ def upload_variants(torch, cr):
                                  "kernels_ms": k}
     del d
     torch.cuda.empty_cache()
+    # Sparse uploads at 2^30: up to 1024 ids take the small path; above that,
+    # fewer ids than keys (16384) build each container at its rank in a pool of
+    # n slots; from 16384 ids on the pool is addressed by key.
+    g = torch.Generator(device="cuda")
+    g.manual_seed(74)
+    for n_s in (1000, 1025, 10_000, 100_000, 1_000_000):
+        ids_s = torch.randint(0, U, (n_s,), device="cuda", generator=g, dtype=torch.int64).to(torch.int32)
+        t, (nc, card, neg), k = timed(lambda: cr.upload_from_device_ids(ids_s, U))
+        res[f"ids_sparse_{n_s}"] = {"ms": round(t, 4), "containers": nc, "distinct": card, "kernels_ms": k}
+    log("sparse uploads", {kk: v["ms"] for kk, v in res.items() if kk.startswith("ids_sparse")})
     for dens, seed in ((0.001, 71), (0.5, 72), (0.9, 73)):
         w = _bitset_words(torch, dens, seed)
         torch.cuda.synchronize()

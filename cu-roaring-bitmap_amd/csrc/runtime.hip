@@ -563,7 +563,11 @@ uint64_t device_l2_bytes(int device)
 // universe swept, and the crossover moves down to where the reference's
 // pinned verdicts allow: U = 10^6 must stay compressed
 // (test/test_promote.cu:257-305), so promote once the flat bitmap exceeds
-// 1/32 of one XCD's L2, i.e. 128 KiB (U > 2^20) on MI355X.
+// 1/32 of one XCD's L2, i.e. 128 KiB (U > 2^20) on MI355X.  The rule sees only
+// U; the memory term sits where the container count is known: upload() under
+// AUTO keeps the layout when n_containers x 8 KiB x 2 >= ceil(U/8)
+// (src/upload.cpp:106-118), so a sparse bitmap with a container at every key
+// of 2^30 (2.3 MB at 0.1%) is not promoted to 134 MB there.
 uint32_t resolve_auto_threshold(uint32_t universe_size, int device)
 {
     if (universe_size == 0) return CR_PROMOTE_KEEP_DEFAULT;

@@ -45,7 +45,7 @@ namespace crimpl {
 // metadata: workgroup 0 only writes the totals and the others return.
 __global__ __launch_bounds__(1024) void ids_rank(IdsGeom g, const uint32_t* key_count, const uint32_t* gmax,
                                                  uint16_t* keys, uint8_t* types, uint32_t* offsets, uint16_t* cards,
-                                                 uint16_t* key_index, IdsTotals* tot, IdsTotals* host)
+                                                 uint16_t* key_index, IdsTotals* tot, IdsTotals* host, bool slotted)
 {
     __shared__ uint32_t lds[16];
     __shared__ uint32_t s_max;
@@ -107,7 +107,7 @@ __global__ __launch_bounds__(1024) void ids_rank(IdsGeom g, const uint32_t* key_
         offsets[rank] = rank * 8192u;
         cards[rank] = static_cast<uint16_t>(c > 65535u ? 0u : c);  // 65536 stored as 0
         key_index[k] = static_cast<uint16_t>(rank);
-        moved = rank != k;
+        moved = !slotted && rank != k;  // slotted: the build wrote the container at its rank
     } else if (k < g.K) {
         key_index[k] = 0xFFFFu;
     }
@@ -143,6 +143,54 @@ __global__ __launch_bounds__(1024) void ids_rank(IdsGeom g, const uint32_t* key_
         h->max_id = res.max_id;
         h->moved = res.moved;
         h->total = res.total;
+    }
+}
+
+// Fewer ids than keys (n < K): at most n containers, so the pool holds n
+// slots, not K, and each container is built straight at its rank.  The keys
+// present among the ids are marked as bits (an id whose key is past max_key is
+// left to the error check), then ranked into key_index (0xFFFF: absent), which
+// the build reads as its slot map and ids_rank rewrites with the same values.
+__global__ __launch_bounds__(256) void ids_presence(const uint32_t* __restrict__ ids, uint32_t n, uint32_t K,
+                                                    uint32_t* bits)
+{
+    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n; i += gridDim.x * 256u) {
+        const uint32_t k = ids[i] >> 16;
+        if (k < K) atomicOr(&bits[k >> 5], 1u << (k & 31u));
+    }
+}
+
+__global__ __launch_bounds__(1024) void ids_slots(const uint32_t* __restrict__ bits, uint32_t K, uint16_t* key_index)
+{
+    __shared__ uint32_t lds[16];
+    const uint32_t t = threadIdx.x;  // keys [64 t, 64 t + 64): words 2 t, 2 t + 1
+    const uint32_t nw = (K + 31u) / 32u;
+    const uint32_t w0 = 2u * t < nw ? bits[2u * t] : 0u, w1 = 2u * t + 1u < nw ? bits[2u * t + 1u] : 0u;
+    uint32_t total;
+    uint32_t r = block_excl_scan<1024>(static_cast<uint32_t>(__popc(w0) + __popc(w1)), lds, total);
+    if (64u * t >= K) return;
+    // The 64 entries as 32 packed pairs; a whole row goes out as eight
+    // 16-byte stores (key_index is 256-byte aligned), the last partial one
+    // entry by entry.
+    uint32_t pk[32];
+#pragma unroll
+    for (uint32_t j = 0; j < 64u; ++j) {
+        const bool present = ((j < 32u ? w0 >> j : w1 >> (j - 32u)) & 1u) != 0u;
+        const uint32_t v = present ? r : 0xFFFFu;
+        r += present ? 1u : 0u;
+        if (j & 1u)
+            pk[j >> 1] |= v << 16;
+        else
+            pk[j >> 1] = v;
+    }
+    if (64u * t + 64u <= K) {
+        uint4* dst = reinterpret_cast<uint4*>(key_index + 64u * t);
+#pragma unroll
+        for (uint32_t q = 0; q < 8u; ++q) dst[q] = make_uint4(pk[4 * q], pk[4 * q + 1], pk[4 * q + 2], pk[4 * q + 3]);
+    } else {
+#pragma unroll
+        for (uint32_t j = 0; j < 64u; ++j)
+            if (64u * t + j < K) key_index[64u * t + j] = static_cast<uint16_t>(pk[j >> 1] >> ((j & 1u) * 16u));
     }
 }
 
@@ -342,7 +390,9 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
                 }
             }
             if (pc != 0) {
-                const uint32_t slot = complement ? key_index[key] : key;
+                // the key's rank when a slot map is given (complement mode, or
+                // fewer ids than keys), else the key itself
+                const uint32_t slot = key_index != nullptr ? key_index[key] : key;
                 uint4* dst = reinterpret_cast<uint4*>(pool + static_cast<uint64_t>(slot) * 1024u);
 #pragma unroll
                 for (int q = 0; q < 8; ++q) st_stream(dst + lane + 64 * q, v[q]);
@@ -422,6 +472,7 @@ struct SmallPlan {
     uint32_t max_key;       // last stored key
     uint32_t vals[2 * SMALL_MAX];
     uint32_t cstart[2 * SMALL_MAX + 1];
+    uint32_t bslot[2 * SMALL_MAX];  // bitmap pool slot of a bitmap container (ids_small_write fills it)
 };
 
 __global__ __launch_bounds__(1024) void ids_small_plan(const uint32_t* ids, uint32_t n, uint32_t universe, uint32_t thr,
@@ -536,7 +587,7 @@ __global__ __launch_bounds__(1024) void ids_small_plan(const uint32_t* ids, uint
 
 // Single workgroup: containers are laid out in key order; bitmap containers
 // take consecutive 8 KiB slots, array containers consecutive ranges.
-__global__ __launch_bounds__(1024) void ids_small_write(const SmallPlan* plan, uint32_t thr, uint16_t* keys,
+__global__ __launch_bounds__(1024) void ids_small_write(SmallPlan* plan, uint32_t thr, uint16_t* keys,
                                                         uint8_t* types, uint32_t* offsets, uint16_t* cards,
                                                         uint64_t* bmp, uint16_t* arr, uint16_t* key_index,
                                                         uint32_t kidx_len)
@@ -572,8 +623,6 @@ __global__ __launch_bounds__(1024) void ids_small_write(const SmallPlan* plan, u
         }
     }
     for (uint32_t i = t; i < kidx_len; i += 1024) key_index[i] = 0xFFFFu;
-    const uint64_t bmp_words = static_cast<uint64_t>(plan->n_bitmap) * 1024u;
-    for (uint64_t i = t; i < bmp_words; i += 1024) bmp[i] = 0;
     __syncthreads();
     for (uint32_t c = t; c < nc; c += 1024) {
         const uint32_t s = plan->cstart[c], e = plan->cstart[c + 1], card = e - s;
@@ -584,23 +633,37 @@ __global__ __launch_bounds__(1024) void ids_small_write(const SmallPlan* plan, u
         if (card > thr) {
             types[c] = CR_BITMAP;
             offsets[c] = s_bslot[c] * 8192u;
+            plan->bslot[c] = s_bslot[c];
         } else {
             types[c] = CR_ARRAY;
             offsets[c] = s_aoff[c] * 2u;
             for (uint32_t i = s; i < e; ++i) arr[s_aoff[c] + (i - s)] = static_cast<uint16_t>(plan->vals[i]);
         }
     }
+}
+
+// The bitmap containers of the small path: one workgroup per container builds
+// its 8 KiB image in LDS from the container's values and writes it once with
+// 16-byte stores (containers that are arrays leave at once).
+__global__ __launch_bounds__(256) void ids_small_bitmaps(const SmallPlan* __restrict__ plan, uint32_t thr,
+                                                         uint64_t* __restrict__ bmp)
+{
+    __shared__ alignas(16) uint32_t img[2048];
+    const uint32_t c = blockIdx.x, t = threadIdx.x;
+    const uint32_t s = plan->cstart[c], e = plan->cstart[c + 1];
+    if (e - s <= thr) return;  // the same test for the whole workgroup
+    uint4* img4 = reinterpret_cast<uint4*>(img);
+    img4[t] = make_uint4(0, 0, 0, 0);
+    img4[t + 256] = make_uint4(0, 0, 0, 0);
     __syncthreads();
-    // bitmap bits: one lane per value (atomicOr: values of one container share words)
-    for (uint32_t c = 0; c < nc; ++c) {
-        const uint32_t s = plan->cstart[c], e = plan->cstart[c + 1];
-        if (e - s <= thr) continue;
-        uint64_t* dst = bmp + static_cast<uint64_t>(s_bslot[c]) * 1024u;
-        for (uint32_t i = s + t; i < e; i += 1024) {
-            const uint32_t low = plan->vals[i] & 0xFFFFu;
-            atomicOr(reinterpret_cast<unsigned long long*>(&dst[low >> 6]), 1ull << (low & 63u));
-        }
+    for (uint32_t i = s + t; i < e; i += 256u) {
+        const uint32_t low = plan->vals[i] & 0xFFFFu;
+        atomicOr(&img[low >> 5], 1u << (low & 31u));
     }
+    __syncthreads();
+    uint4* dst = reinterpret_cast<uint4*>(bmp + static_cast<uint64_t>(plan->bslot[c]) * 1024u);
+    dst[t] = img4[t];
+    dst[t + 256] = img4[t + 256];
 }
 
 static int small_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, uint32_t thr, hipStream_t s,
@@ -637,6 +700,11 @@ static int small_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, ui
                                            static_cast<uint32_t>(kidx_len));
     }
     CR_LAUNCH_CHECK();
+    if (n_bitmap) {
+        CR_TIMED("ids_small_bitmaps", s);
+        ids_small_bitmaps<<<nc, 256, 0, s>>>(plan, thr, out->bitmap_data);
+    }
+    CR_LAUNCH_CHECK();
     CR_RET(sync_stream(s));
     return CR_OK;
 }
@@ -667,6 +735,7 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     // the build's field groups read up to 7 words past a group's first: slack past the last tile
     const size_t o_part = c.add(sizeof(uint32_t) * (static_cast<uint64_t>(g.n_tiles) * TILE_WORDS + 8));
     const size_t o_wgc = c.add(sizeof(uint32_t) * static_cast<uint64_t>(g.G) * g.NB);
+    const size_t o_pres = c.add(sizeof(uint32_t) * 2048u);  // key presence bits (fewer ids than keys)
     Scratch sc;
     CR_RET(sc.alloc(c.total, s));
     uint32_t* gmax = sc.at<uint32_t>(o_gmax);
@@ -676,10 +745,14 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     uint32_t* part = sc.at<uint32_t>(o_part);
     uint32_t* wg_count = sc.at<uint32_t>(o_wgc);
 
-    // Containers <= min(keys, ids) bounds the metadata; the pool is addressed
-    // by key (slot k holds key k's container) until the ranks are known.
+    // Containers <= min(keys, ids) bounds the metadata.  With an id for every
+    // key possible (n >= K) the pool is addressed by key (slot k holds key
+    // k's container) until the ranks are known; with fewer ids than keys the
+    // ranks come first and the pool holds n slots (src/upload_ids.cu:243-262
+    // sizes it by the container count too).
     const uint64_t bound = std::min<uint64_t>(g.K, n);
-    const uint64_t pool_words = static_cast<uint64_t>(g.K) * 1024u;
+    const bool slotted = bound < g.K;
+    const uint64_t pool_words = bound * 1024u;
     const OutLayout L = plan_out(bound, g.K, pool_words, 0, 0);
     CR_RET(alloc_out(out, L, bound, g.K, pool_words, 0, 0, s));
     out->max_key = max_key32;
@@ -689,6 +762,20 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
         ids_tile_sort<false><<<g.G, TS_NT, 0, s>>>(d_ids, g, part, tab, gmax, tot, nullptr, wg_count);
     }
     CR_LAUNCH_CHECK();
+    if (slotted) {
+        uint32_t* pres = sc.at<uint32_t>(o_pres);
+        CR_RET(fill_u32(pres, 0u, 2048u, s));
+        {
+            CR_TIMED("ids_presence", s);
+            ids_presence<<<std::max(1u, std::min<uint32_t>((n + 255u) / 256u, 1024u)), 256, 0, s>>>(d_ids, n, g.K, pres);
+        }
+        CR_LAUNCH_CHECK();
+        {
+            CR_TIMED("ids_slots", s);
+            ids_slots<<<1, 1024, 0, s>>>(pres, g.K, out->key_index);
+        }
+        CR_LAUNCH_CHECK();
+    }
     HostSlotGuard hs;
     CR_RET(hs.acquire());
     {
@@ -697,13 +784,15 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
                                  ? BuildMeta{out->keys, out->types, out->offsets, out->cardinalities, out->key_index}
                                  : BuildMeta{};
         ids_build<<<build_grid_persistent(g.NB, num_cus()), BUILD_NT, 0, s>>>(
-            part, tab, g, wg_count, universe, false, nullptr, out->bitmap_data, nullptr, key_count, tot, bm);
+            part, tab, g, wg_count, universe, false, slotted ? out->key_index : nullptr, out->bitmap_data, nullptr,
+            key_count, tot, bm);
     }
     CR_LAUNCH_CHECK();
     {
         CR_TIMED("ids_rank", s);
         ids_rank<<<(g.K + 1023u) / 1024u, 1024, 0, s>>>(g, key_count, gmax, out->keys, out->types, out->offsets,
-                                                         out->cardinalities, out->key_index, tot, hs.dev<IdsTotals>());
+                                                         out->cardinalities, out->key_index, tot, hs.dev<IdsTotals>(),
+                                                         slotted);
     }
     CR_LAUNCH_CHECK();
     CR_RET(sync_stream(s));

@@ -13,9 +13,16 @@ static constexpr uint32_t PROMOTE_KEEP_DEFAULT = CR_PROMOTE_KEEP_DEFAULT;
 static constexpr uint32_t PROMOTE_ALL = CR_PROMOTE_ALL;
 static constexpr uint32_t PROMOTE_AUTO = CR_PROMOTE_AUTO;
 
-// PROMOTE_AUTO -> PROMOTE_ALL when the flat bitset of the universe would take
-// more than half of the device's L2 (as reported for one XCD), else
-// PROMOTE_KEEP_DEFAULT (promote.cuh:75, src/promote.cu:334-367).
+// PROMOTE_AUTO -> PROMOTE_ALL when the flat bitset of the universe, ceil(U/8)
+// bytes, is more than 1/32 of the device's L2 as reported for one XCD (4 MiB on
+// MI355X, so U > 2^20), else PROMOTE_KEEP_DEFAULT (promote.cuh:75; the
+// reference's rule is 2 ceil(U/8) > L2, src/promote.cu:334-367).  Measured on
+// gfx950, the all-bitmap layout answers point queries 1.8-5.4x faster from
+// U = 2^20 up, and 10^6 must stay compressed.  Where the container count is
+// known, upload() adds the reference's footprint term: under PROMOTE_AUTO it
+// keeps the layout when n_containers x 8 KiB x 2 >= ceil(U/8)
+// (src/upload.cpp:106-118).  promote_auto() has no such term, as in the
+// reference (src/promote.cu:369-385).
 uint32_t resolve_auto_threshold(uint32_t universe_size, int device_id = -1);
 
 // Every array and run container becomes an 8 KiB bitmap; returns a new

@@ -282,6 +282,33 @@ def test_resolve_auto_threshold_gfx950(gpu):
             assert orc.resolve_auto_threshold(1 << lg, gpu.device_l2_bytes()) == keep  # the reference's rule
 
 
+@pytest.mark.parametrize("n_keys", [8191, 8192])
+def test_upload_auto_footprint_guard(gpu, n_keys):
+    """The footprint term of PROMOTE_AUTO: upload() promotes under AUTO only while
+    n_containers x 8 KiB x 2 < ceil(U/8) (src/upload.cpp:106-118), so at U = 2^30
+    8191 sparse containers become bitmaps (64 MiB) and 8192 stay arrays (the
+    promoted layout would be as large as the flat bitset).  promote_auto has no
+    such guard (src/promote.cu:369-385): it promotes the 8192 arrays (and copies
+    the 8191 bitmaps)."""
+    _say("AUTO footprint guard", n_keys)
+    U = 1 << 30
+    keys = np.arange(n_keys, dtype=np.uint64) * 2  # every other key, 3 values each
+    ids = np.sort(((keys << np.uint64(16))[:, None] + np.array([5, 700, 40000], dtype=np.uint64)).ravel())
+    lite = orc.Lite.from_sorted_ids(ids.astype(np.uint32))
+    want = orc.upload_packed(lite, U, orc.PROMOTE_AUTO, auto_l2(gpu))
+    g = gpu.upload_containers(lite.containers(), U, False, lite.cardinality(), orc.PROMOTE_AUTO)
+    assert_same(gpu.download(g), want, strict=True, what=f"AUTO guard {n_keys}")
+    if gpu.resolve_auto_threshold(U) == orc.PROMOTE_ALL:
+        assert (g.n_bitmap_containers, g.n_array_containers) == ((n_keys, 0) if n_keys < 8192 else (0, n_keys))
+    p = gpu.promote_auto(g)
+    gpu.synchronize()
+    assert_same(gpu.download(p), orc.promote_auto(want, auto_l2(gpu)), strict=True, what=f"promote_auto {n_keys}")
+    if gpu.resolve_auto_threshold(U) == orc.PROMOTE_ALL:
+        assert p.n_bitmap_containers == n_keys  # 8191: already bitmaps (a copy); 8192: promoted
+    gpu.free(p)
+    gpu.free(g)
+
+
 # ---- bitset uploads ----------------------------------------------------------
 BITSET_CASES = [(100000, 0.1, 1), (100000, 0.9, 2), (200000, 1 / 3, 3), (5 * 65536 + 123, 0.001, 4),
                 (5 * 65536 + 123, 0.95, 5), (1 << 22, 0.5, 6), (1 << 22, 0.55, 7), (64, 1.0, 8), (96, 0.0, 9)]
