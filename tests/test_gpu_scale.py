@@ -11,6 +11,7 @@ multi_and configs over 2^30.
 import pytest
 
 import bench
+import orc
 
 pytestmark = pytest.mark.gpu
 
@@ -90,6 +91,24 @@ def test_upload_from_ids_full_size(gpu, torch, kind):
     assert torch.equal(_decoded(torch, gpu, g), want)
     assert g.total_cardinality == n_distinct
     gpu.free(g)
+
+
+def test_upload_from_ids_full_size_threshold_variants(gpu, torch):
+    """BASELINE configs[1] names AUTO, KEEP_DEFAULT and ALL: above 1024 ids the
+    reference builds all-bitmap whatever the threshold (src/upload_ids.cu:573-587),
+    so the KEEP and ALL uploads of the 100M headline ids equal the AUTO one
+    field by field, pools included."""
+    from helpers import assert_same
+    d_ids = bench.make_ids(torch)
+    _say("upload_from_ids full size AUTO")
+    g = gpu.upload_from_device_ids(d_ids, U)
+    want = gpu.download(g)
+    gpu.free(g)
+    for name, thr in (("KEEP_DEFAULT", orc.PROMOTE_KEEP_DEFAULT), ("ALL", orc.PROMOTE_ALL)):
+        _say("upload_from_ids full size", name)
+        g = gpu.upload_from_device_ids(d_ids, U, thr)
+        assert_same(gpu.download(g), want, strict=True, what=f"threshold {name}")
+        gpu.free(g)
 
 
 def test_upload_from_ids_full_size_complement(gpu, torch):
