@@ -68,9 +68,11 @@ _cpu_lib = None
 
 
 def lib():
+    """The checker; ORC_LIB_PATH, when set, names another build of it (the
+    sanitizer build, tests/test_sanitizers.py)."""
     global _lib
     if _lib is None:
-        _lib = _load(_LIB_PATH)
+        _lib = _load(os.environ.get("ORC_LIB_PATH") or _LIB_PATH)
     return _lib
 
 
@@ -91,7 +93,8 @@ def cpu_lib():
     AVX-512 (and that build exists), else the x86-64-v3 one."""
     global _cpu_lib
     if _cpu_lib is None:
-        _cpu_lib = _load(_LIB_V4_PATH) if host_supports_v4() and os.path.exists(_LIB_V4_PATH) else lib()
+        use_v4 = not os.environ.get("ORC_LIB_PATH") and host_supports_v4() and os.path.exists(_LIB_V4_PATH)
+        _cpu_lib = _load(_LIB_V4_PATH) if use_v4 else lib()
     return _cpu_lib
 
 

@@ -162,8 +162,10 @@ static int cmp_u32(const void* a, const void* b)
 rl_bitmap* rl_from_ids(const uint32_t* ids, uint64_t n)
 {
     uint32_t* v = (uint32_t*)malloc((size_t)(n ? n : 1) * 4u);
-    memcpy(v, ids, (size_t)n * 4u);
-    qsort(v, n, 4, cmp_u32);
+    if (n) { /* an empty input may come with a null pointer */
+        memcpy(v, ids, (size_t)n * 4u);
+        qsort(v, n, 4, cmp_u32);
+    }
     uint64_t w = 0;
     for (uint64_t i = 0; i < n; ++i)
         if (w == 0 || v[i] != v[w - 1]) v[w++] = v[i];
