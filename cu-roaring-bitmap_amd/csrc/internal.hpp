@@ -172,6 +172,15 @@ __device__ __forceinline__ void st_stream(uint2* p, uint2 v)
                                 reinterpret_cast<uint64_t*>(p));
 }
 
+// The wave's own LDS writes are visible to its later LDS reads (its LDS
+// operations retire in order); this keeps the compiler from moving them across.
+__device__ __forceinline__ void wave_lds_fence()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ uint32_t wave_sum(uint32_t v)
 {
 #pragma unroll

@@ -26,6 +26,7 @@ struct KeyRec {
     int32_t ai, bi;
     uint32_t size;        // array elements or run pairs reserved in the output pool
     uint32_t aoff, boff;  // byte offsets of the source containers
+    uint32_t ma, mb;      // (type << 16) | stored card of the source containers, 0 when absent
 };
 
 // One output container candidate, in key order (plan pass 2).
@@ -36,7 +37,22 @@ struct Item {
     int32_t ai, bi;
     uint32_t slot;        // bitmap slot, or u16 element offset into the array / run pool
     uint32_t aoff, boff;  // byte offsets of the source containers (0 when absent)
+    uint32_t ma, mb;      // (type << 16) | stored card of the source containers (0 when absent)
 };
+static_assert(sizeof(Item) == 32, "the plans write an item as two 16-byte words");
+
+// An item as the execution reads it (one scalar load): in execution order, with
+// its position in key order, where its card goes.
+struct ExecItem {
+    uint16_t pos;    // position in key order (< 65536: one item a key)
+    uint8_t cat;
+    uint8_t from_a;  // a one-sided item's side
+    uint32_t slot;
+    uint32_t aoff, boff;
+    uint32_t ma, mb;
+    uint32_t pad[2];
+};
+static_assert(sizeof(ExecItem) == 32, "one 32-byte scalar load");
 
 // Counters accumulated per 1024-key group and totalled over all groups.  The
 // last three check the key indexes when the classification reads them: the keys
@@ -151,21 +167,24 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_classify(Side A, Side B, uint
     rec.bi = bi;
     rec.aoff = ai >= 0 ? A.offsets[ai] : 0u;
     rec.boff = bi >= 0 ? B.offsets[bi] : 0u;
+    const uint32_t ta = ai >= 0 ? A.types[ai] : 0u, tb = bi >= 0 ? B.types[bi] : 0u;
+    const uint32_t ca = ai >= 0 ? A.cards[ai] : 0u, cb = bi >= 0 ? B.cards[bi] : 0u;
+    rec.ma = ai >= 0 ? (ta << 16) | ca : 0u;
+    rec.mb = bi >= 0 ? (tb << 16) | cb : 0u;
     const bool keep_a_only = op != CR_AND;                 // OR, XOR, ANDNOT copy A-only keys
     const bool keep_b_only = op == CR_OR || op == CR_XOR;  // OR, XOR copy B-only keys
     if (ai >= 0 && bi >= 0) {
-        const uint32_t ta = A.types[ai], tb = B.types[bi];
         if (ta == CR_BITMAP && tb == CR_BITMAP) {
             rec.cat = CAT_BB;
             cnt[C_BB] = 1;
         } else if (op == CR_AND && ((ta == CR_BITMAP && tb == CR_ARRAY) || (ta == CR_ARRAY && tb == CR_BITMAP))) {
             rec.cat = CAT_BA;
-            rec.size = ta == CR_ARRAY ? A.cards[ai] : B.cards[bi];
+            rec.size = ta == CR_ARRAY ? ca : cb;
             cnt[C_BAE] = rec.size;
             cnt[C_BA] = 1;
         } else if (op == CR_AND && ta == CR_ARRAY && tb == CR_ARRAY) {
             rec.cat = CAT_AA;
-            rec.size = min(static_cast<uint32_t>(A.cards[ai]), static_cast<uint32_t>(B.cards[bi]));
+            rec.size = min(ca, cb);
             cnt[C_AAE] = rec.size;
             cnt[C_AA] = 1;
         } else {
@@ -174,8 +193,8 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_classify(Side A, Side B, uint
         }
     } else if ((ai >= 0 && keep_a_only) || (bi >= 0 && keep_b_only)) {
         const bool from_a = ai >= 0;
-        const uint32_t ty = from_a ? A.types[ai] : B.types[bi];
-        const uint32_t c = from_a ? A.cards[ai] : B.cards[bi];
+        const uint32_t ty = from_a ? ta : tb;
+        const uint32_t c = from_a ? ca : cb;
         if (ty == CR_BITMAP) {
             rec.cat = CAT_COPY_BMP;
             cnt[C_CB] = 1;
@@ -212,7 +231,7 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_classify(Side A, Side B, uint
 
 // ---- plan pass 2: slot assignment in key order -----------------------------
 __global__ __launch_bounds__(PLAN_NT) void so_plan_assign(const KeyRec* recs, const uint32_t* group_counts,
-                                                          Item* items, Totals* totals, Caps caps)
+                                                          Item* items, ExecItem* xitems, Totals* totals, Caps caps)
 {
     __shared__ uint32_t gbase[C_N], gtot[C_N];
     __shared__ uint32_t scan_lds[2 * 8 * (PLAN_NT / 64) + 8];
@@ -271,8 +290,32 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_assign(const KeyRec* recs, co
     it.bi = rec.bi;
     it.aoff = rec.aoff;
     it.boff = rec.boff;
+    it.ma = rec.ma;
+    it.mb = rec.mb;
     it.slot = slot;
-    if (item_pos < caps.items) items[item_pos] = it;  // the item scratch holds caps.items
+    if (item_pos < caps.items) {  // the item scratch holds caps.items
+        items[item_pos] = it;
+        // The execution order: items that write a bitmap first (the longest
+        // start first), then those that write array or run values, each group
+        // in key order.
+        const uint32_t n_big = gtot[C_BB] + gtot[C_MX] + gtot[C_CB];
+        const uint32_t big_before = gbase[C_BB] + gbase[C_MX] + gbase[C_CB] + p_bb + p_mx + p_cb;
+        const bool big = cat == CAT_BB || cat == CAT_MIXED || cat == CAT_COPY_BMP;
+        const uint32_t e = big ? big_before : n_big + (item_pos - big_before);
+        if (e < caps.items) {  // (beyond it only when the plan overflows)
+            ExecItem x;
+            x.pos = static_cast<uint16_t>(item_pos);
+            x.cat = cat;
+            x.from_a = rec.ai >= 0 ? 1u : 0u;
+            x.slot = slot;
+            x.aoff = rec.aoff;
+            x.boff = rec.boff;
+            x.ma = rec.ma;
+            x.mb = rec.mb;
+            x.pad[0] = x.pad[1] = 0;
+            xitems[e] = x;
+        }
+    }
 }
 
 // ---- plan for two all-bitmap inputs with key indexes -------------------------
@@ -319,6 +362,8 @@ __global__ __launch_bounds__(KP_NT) void so_plan_bitmap(const uint16_t* __restri
                                                         const uint32_t* __restrict__ off_b,
                                                         const uint8_t* __restrict__ ty_a,
                                                         const uint8_t* __restrict__ ty_b,
+                                                        const uint16_t* __restrict__ cards_a,
+                                                        const uint16_t* __restrict__ cards_b,
                                                         const uint16_t* __restrict__ keys_a,
                                                         const uint16_t* __restrict__ keys_b, uint32_t na, uint32_t nb,
                                                         uint32_t op, Caps caps, Item* items, Totals* totals,
@@ -366,7 +411,10 @@ __global__ __launch_bounds__(KP_NT) void so_plan_bitmap(const uint16_t* __restri
         it.boff = inb ? off_b[xb] : 0u;
         // a container that is not a bitmap (counts that misdescribe the input)
         // makes the item invalid: the exec skips it and the compaction reports it
-        const bool bitmaps = (!ina || ty_a[xa] == CR_BITMAP) && (!inb || ty_b[xb] == CR_BITMAP);
+        const uint32_t ta = ina ? ty_a[xa] : 0u, tb = inb ? ty_b[xb] : 0u;
+        it.ma = ina ? (ta << 16) | cards_a[xa] : 0u;
+        it.mb = inb ? (tb << 16) | cards_b[xb] : 0u;
+        const bool bitmaps = (!ina || ta == CR_BITMAP) && (!inb || tb == CR_BITMAP);
         it.cat = !bitmaps ? CAT_NONE : (is_bb ? CAT_BB : CAT_COPY_BMP);
         it.slot = is_bb ? bb_before + r_bb : bb_total + (it_before - bb_before) + r_cb;
         items[pos] = it;
@@ -386,9 +434,21 @@ __global__ __launch_bounds__(KP_NT) void so_plan_bitmap(const uint16_t* __restri
     }
 }
 
-// ---- execution: one workgroup per item --------------------------------------
+// ---- execution: one wavefront per item --------------------------------------
+// Every work item is a chain of dependent loads, and most are small, so the time
+// follows the items in flight.  Each wave runs one item and exits, with no
+// workgroup barrier, 20 waves a CU (8 KiB of LDS each); the grid covers the
+// plan's bound and waves past the item count exit at once.  (A wave that went
+// on to a second item would first wait for its stores: a wave's loads and
+// stores retire in order.  Measured on the configs[2] pairs, that cost 5-15%.)
+// The plan puts the containers' types and cards in the item, and writes the
+// items in execution order -- bitmap-writing items first, the longest start
+// first -- so a wave reads its record with one scalar load and then issues all
+// its payload loads at once.  An 8 KiB bitmap is handled as eight 1 KiB pieces:
+// lane l holds the 128-bit chunks l + 64 j (j < 8) of a side.
 constexpr int EXEC_NT = 256;
-constexpr uint32_t LDS_ARRAY_CAP = 8192;  // u16 elements staged for array x array
+constexpr uint32_t EXEC_LDS_WORDS = 2048;   // 8 KiB of LDS a wave
+constexpr uint32_t EXEC_WAVES_PER_CU = 20;  // 160 KiB of LDS a CU
 
 template <uint32_t OP>
 __device__ __forceinline__ uint32_t apply32(uint32_t a, uint32_t b)
@@ -400,303 +460,451 @@ __device__ __forceinline__ uint32_t apply32(uint32_t a, uint32_t b)
 }
 
 template <uint32_t OP>
-__device__ __forceinline__ uint32_t bitmap_op_stream(const uint64_t* pa, const uint64_t* pb, uint64_t* po)
+__device__ __forceinline__ uint4 apply4(const uint4& a, const uint4& b)
 {
-    uint32_t pc = 0;
-    const uint32_t t = threadIdx.x;
-    if (((reinterpret_cast<uintptr_t>(pa) | reinterpret_cast<uintptr_t>(pb) | reinterpret_cast<uintptr_t>(po)) &
-         15u) == 0) {
-        const uint4* a = reinterpret_cast<const uint4*>(pa);
-        const uint4* b = reinterpret_cast<const uint4*>(pb);
-        uint4* o = reinterpret_cast<uint4*>(po);
-        const uint4 x0 = ld_stream(a + t), x1 = ld_stream(a + t + EXEC_NT), y0 = ld_stream(b + t),
-                    y1 = ld_stream(b + t + EXEC_NT);
-        uint4 r0, r1;
-        r0.x = apply32<OP>(x0.x, y0.x);
-        r0.y = apply32<OP>(x0.y, y0.y);
-        r0.z = apply32<OP>(x0.z, y0.z);
-        r0.w = apply32<OP>(x0.w, y0.w);
-        r1.x = apply32<OP>(x1.x, y1.x);
-        r1.y = apply32<OP>(x1.y, y1.y);
-        r1.z = apply32<OP>(x1.z, y1.z);
-        r1.w = apply32<OP>(x1.w, y1.w);
-        st_stream(o + t, r0);
-        st_stream(o + t + EXEC_NT, r1);
-        pc = __popc(r0.x) + __popc(r0.y) + __popc(r0.z) + __popc(r0.w) + __popc(r1.x) + __popc(r1.y) +
-             __popc(r1.z) + __popc(r1.w);
+    return make_uint4(apply32<OP>(a.x, b.x), apply32<OP>(a.y, b.y), apply32<OP>(a.z, b.z), apply32<OP>(a.w, b.w));
+}
+
+__device__ __forceinline__ uint32_t popc4(const uint4& r) { return __popc(r.x) + __popc(r.y) + __popc(r.z) + __popc(r.w); }
+
+__device__ __forceinline__ uint32_t uni(uint32_t v)
+{
+    return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+}
+
+// The wave's total of v (DPP scan, no LDS addresses held in registers).
+__device__ __forceinline__ uint32_t wave_total(uint32_t v)
+{
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(v)), 63));
+}
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask)
+{
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
+
+// A wave's record: the same for every lane, so it is read through the constant
+// address space, one scalar load into scalar registers.
+typedef uint32_t item_v8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ ExecItem load_xitem(const ExecItem* p)
+{
+    const item_v8 x = *reinterpret_cast<const __attribute__((address_space(4))) item_v8*>(reinterpret_cast<uintptr_t>(p));
+    ExecItem it;
+    it.pos = static_cast<uint16_t>(x[0]);
+    it.cat = static_cast<uint8_t>(x[0] >> 16);
+    it.from_a = static_cast<uint8_t>(x[0] >> 24);
+    it.slot = x[1];
+    it.aoff = x[2];
+    it.boff = x[3];
+    it.ma = x[4];
+    it.mb = x[5];
+    it.pad[0] = it.pad[1] = 0;
+    return it;
+}
+
+// A bitmap container's eight chunks of this lane.
+__device__ __forceinline__ void bitmap_side(const uint64_t* pool, uint32_t off, uint32_t lane, uint4 (&c)[8])
+{
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(pool) + (off >> 2);
+    if ((off & 15u) == 0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c[j] = ld_stream(reinterpret_cast<const uint4*>(src) + lane + 64u * j);
     } else {
-        for (uint32_t i = t; i < 1024u; i += EXEC_NT) {
-            const uint64_t a = pa[i], b = pb[i];
-            const uint64_t r = static_cast<uint64_t>(apply32<OP>(static_cast<uint32_t>(a), static_cast<uint32_t>(b))) |
-                               (static_cast<uint64_t>(apply32<OP>(static_cast<uint32_t>(a >> 32),
-                                                                  static_cast<uint32_t>(b >> 32)))
-                                << 32);
-            po[i] = r;
-            pc += __popcll(r);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t* p = src + 4u * (lane + 64u * j);
+            c[j] = make_uint4(p[0], p[1], p[2], p[3]);
         }
+    }
+}
+
+__device__ __forceinline__ void zero_image(uint32_t* img, uint32_t lane)
+{
+#pragma unroll
+    for (int j = 0; j < 8; ++j) reinterpret_cast<uint4*>(img)[lane + 64u * j] = make_uint4(0, 0, 0, 0);
+    wave_lds_fence();
+}
+
+__device__ __forceinline__ void read_image(const uint32_t* img, uint32_t lane, uint4 (&c)[8])
+{
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j] = reinterpret_cast<const uint4*>(img)[lane + 64u * j];
+}
+
+// The first payload words of a side, loaded for both sides as soon as the
+// record is in, so that both sides' loads are in flight together: an array's
+// values lane and lane + 64 (~0u past its end), or run `lane` as
+// start | length << 16 and the run before it (0 for lane 0 or past the end).
+// Bitmap and absent sides have none (a bitmap's 8 KiB are loaded whole).
+struct Pre {
+    uint32_t v0, v1;
+};
+
+__device__ __forceinline__ uint32_t run_word(const uint16_t* runs, uint32_t i, bool al4)
+{
+    if (al4) return reinterpret_cast<const uint32_t*>(runs)[i];
+    return static_cast<uint32_t>(runs[2 * i]) | (static_cast<uint32_t>(runs[2 * i + 1]) << 16);
+}
+
+__device__ __forceinline__ bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+__device__ __forceinline__ Pre preload(const Side& S, uint32_t meta, uint32_t off, uint32_t lane)
+{
+    const uint32_t ty = meta >> 16, n = meta & 0xFFFFu;
+    Pre p{~0u, ~0u};
+    if (ty == CR_ARRAY) {  // (an absent side: meta 0, no values)
+        const uint16_t* vals = S.arr + (off >> 1);
+        if (lane < n) p.v0 = vals[lane];
+        if (lane + 64u < n) p.v1 = vals[lane + 64u];
+    } else if (ty == CR_RUN) {
+        const uint16_t* runs = S.run + (off >> 1);
+        const bool al4 = aligned4(runs);
+        p.v0 = lane < n ? run_word(runs, lane, al4) : 0u;
+        p.v1 = lane > 0 && lane < n ? run_word(runs, lane - 1u, al4) : 0u;
+    }
+    return p;
+}
+
+// A side that is not a bitmap, set in the wave's 8 KiB image.  An array's
+// values become bits (LDS atomics).  A run container's runs become toggles:
+// each run flips its first bit and the bit after its last (XOR: a run that
+// starts where the previous one ends continues it), and image_chunk turns
+// them into bits.  Runs that are not sorted and disjoint (no well-formed
+// container has them) are ORed in as bits instead, as the reference's
+// expansion does (src/set_ops.cu:322-368), ends past 0xFFFF clamped.  The
+// first values come from `pre`.  Returns true when the image holds toggles.
+__device__ __forceinline__ bool build_image(const Side& S, uint32_t meta, uint32_t off, const Pre& pre,
+                                            uint32_t lane, uint32_t* img)
+{
+    const uint32_t ty = meta >> 16, n = meta & 0xFFFFu;
+    zero_image(img, lane);
+    if (ty == CR_ARRAY) {
+        if (pre.v0 != ~0u) atomicOr(&img[pre.v0 >> 5], 1u << (pre.v0 & 31u));
+        if (pre.v1 != ~0u) atomicOr(&img[pre.v1 >> 5], 1u << (pre.v1 & 31u));
+        const uint16_t* vals = S.arr + (off >> 1);
+        for (uint32_t i0 = lane + 128u; i0 < n; i0 += 4u * 64u) {  // four loads a lane in flight
+            uint32_t v[4];
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; ++k) v[k] = i0 + 64u * k < n ? static_cast<uint32_t>(vals[i0 + 64u * k]) : ~0u;
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; ++k)
+                if (v[k] != ~0u) atomicOr(&img[v[k] >> 5], 1u << (v[k] & 31u));
+        }
+        wave_lds_fence();
+        return false;
+    }
+    if (ty != CR_RUN) return false;  // an empty image
+    const uint16_t* runs = S.run + (off >> 1);
+    const bool al4 = aligned4(runs);
+    bool bad = false;
+    auto toggle = [&](uint32_t i, uint32_t cw, uint32_t pw) {
+        const uint32_t st = cw & 0xFFFFu, en = min(0xFFFFu, st + (cw >> 16));
+        bad |= i > 0 && st <= min(0xFFFFu, (pw & 0xFFFFu) + (pw >> 16));
+        atomicXor(&img[st >> 5], 1u << (st & 31u));
+        if (en < 0xFFFFu) atomicXor(&img[(en + 1u) >> 5], 1u << ((en + 1u) & 31u));
+    };
+    if (lane < n) toggle(lane, pre.v0, pre.v1);
+    for (uint32_t i0 = lane + 64u; i0 < n; i0 += 2u * 64u) {
+        uint32_t cw[2], pw[2];
+#pragma unroll
+        for (uint32_t k = 0; k < 2u; ++k) {
+            const uint32_t i = i0 + 64u * k;
+            cw[k] = i < n ? run_word(runs, i, al4) : 0u;
+            pw[k] = i < n ? run_word(runs, i - 1u, al4) : 0u;
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < 2u; ++k)
+            if (i0 + 64u * k < n) toggle(i0 + 64u * k, cw[k], pw[k]);
+    }
+    wave_lds_fence();
+    if (__ballot(bad) == 0ull) return true;
+    // Each run's words ORed in, the wave's lanes across its words: 64 runs
+    // loaded at a time, one lane each, then taken in turn.
+    zero_image(img, lane);
+    for (uint32_t r0 = 0; r0 < n; r0 += 64u) {
+        const uint32_t r = r0 + lane;
+        const uint32_t cw = r < n ? run_word(runs, r, al4) : 0u;
+        const uint32_t st = cw & 0xFFFFu, en = min(0xFFFFu, st + (cw >> 16));
+        const uint32_t m = min(64u, n - r0);
+        for (uint32_t k = 0; k < m; ++k) {
+            const uint32_t s0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(st), k));
+            const uint32_t e0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(en), k));
+            for (uint32_t w = (s0 >> 5) + lane; w <= (e0 >> 5); w += 64u)
+                atomicOr(&img[w], bit_span(w == (s0 >> 5) ? s0 & 31u : 0u, w == (e0 >> 5) ? e0 & 31u : 31u));
+        }
+    }
+    wave_lds_fence();
+    return false;
+}
+
+// Chunk l + 64 j of an image, read in the order j = 0..7.  With toggles each
+// 32-bit word is its own prefix XOR (five shifts) flipped by the parity of
+// every toggle before it: the words before it in the lane's chunk, the lanes
+// before it in group j (a ballot), and groups 0..j-1 (`carry`).
+__device__ __forceinline__ uint4 image_chunk(const uint32_t* img, uint32_t lane, uint32_t j, bool toggles,
+                                             uint32_t& carry)
+{
+    const uint4 x = reinterpret_cast<const uint4*>(img)[lane + 64u * j];
+    if (!toggles) return x;
+    uint32_t w[4] = {x.x, x.y, x.z, x.w};
+    uint32_t p = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        uint32_t y = w[q];
+        y ^= y << 1;
+        y ^= y << 2;
+        y ^= y << 4;
+        y ^= y << 8;
+        y ^= y << 16;
+        w[q] = y;
+        p ^= y >> 31;  // the word's parity
+    }
+    const uint64_t m = __ballot(p != 0u);
+    uint32_t in = (lanes_below(m) & 1u) ^ carry;  // parity before this lane's chunk
+    carry ^= static_cast<uint32_t>(__popcll(m)) & 1u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t pw = w[q] >> 31;
+        w[q] ^= 0u - in;
+        in ^= pw;
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Writes OP of the held chunks `x` (side A when X_IS_A) and the image's
+// chunks to the 8 KiB output slot; returns the lane's popcount.
+template <uint32_t OP, bool X_IS_A>
+__device__ __forceinline__ uint32_t store_with_image(const uint4 (&x)[8], const uint32_t* img, bool toggles,
+                                                     uint32_t lane, uint4* dst)
+{
+    uint32_t carry = 0, pc = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < 8u; ++j) {
+        const uint4 y = image_chunk(img, lane, j, toggles, carry);
+        const uint4 r = X_IS_A ? apply4<OP>(x[j], y) : apply4<OP>(y, x[j]);
+        st_stream(dst + lane + 64u * j, r);
+        pc += popc4(r);
     }
     return pc;
 }
 
-// Mixed pairs: thread t builds 128-bit chunks t and t + 256 of both sides' 8 KiB
-// images (words [4 t, 4 t + 4) and [1024 + 4 t, 1024 + 4 t + 4)) in registers,
-// so each of its two 16-byte stores is part of one contiguous 4 KiB store of
-// the workgroup.  A bitmap's chunks are loaded; a run container's come from
-// the runs that meet each chunk (a binary search for the last run starting at
-// or below its end, then back over the runs that reach into it; a run ending
-// past 0xFFFF is clamped, as expand_to_bitmap_kernel does,
-// src/set_ops.cu:355-359).  An array's values are scattered with LDS atomics
-// into an image that every thread then reads its chunks from -- the only case
-// that needs workgroup barriers.
-struct MixMeta {
-    uint32_t type, off, card;
-};
-
-__device__ __forceinline__ MixMeta mix_meta(const Side& S, int32_t idx)
+// n u16 values, four loads a lane in flight.
+__device__ __forceinline__ void wave_copy16(uint16_t* dst, const uint16_t* src, uint32_t n, uint32_t lane)
 {
-    return MixMeta{S.types[idx], S.offsets[idx], S.cards[idx]};
-}
-
-// The 4 words of bits [lo, lo + 128) of a run container.
-__device__ __forceinline__ uint4 run_chunk(const uint16_t* runs, uint32_t card, uint32_t lo)
-{
-    const uint32_t hi = lo + 127u;
-    uint32_t a = 0, b = card;  // first run starting past hi
-    while (a < b) {
-        const uint32_t mid = (a + b) >> 1;
-        if (runs[2 * mid] <= hi)
-            a = mid + 1;
-        else
-            b = mid;
-    }
-    // bits of word j (j = 0..3) inside [s, e], the chunk's bits 0..127
-    auto span = [](uint32_t s, uint32_t e, uint32_t j) {
-        const uint32_t wl = 32u * j, wh = wl + 31u;
-        return (e >= wl && s <= wh) ? bit_span(max(s, wl) - wl, min(e, wh) - wl) : 0u;
-    };
-    uint4 r = make_uint4(0, 0, 0, 0);
-    for (uint32_t k = a; k > 0; --k) {
-        const uint32_t s0 = runs[2 * (k - 1)];
-        const uint32_t e0 = min(0xFFFFu, s0 + runs[2 * (k - 1) + 1]);
-        if (e0 < lo) break;  // runs are sorted and disjoint: none before reaches the chunk
-        const uint32_t s = max(s0, lo) - lo, e = min(e0, hi) - lo;
-        r.x |= span(s, e, 0), r.y |= span(s, e, 1), r.z |= span(s, e, 2), r.w |= span(s, e, 3);
-    }
-    return r;
-}
-
-// A bitmap or run side's two chunks of this thread; for an array side zeroes
-// the thread's chunks of `img` and returns zeros (the caller syncs, scatters,
-// syncs and reads them back).
-struct Chunks2 {
-    uint4 c0, c1;
-};
-
-__device__ __forceinline__ Chunks2 mix_words(const Side& S, const MixMeta& m, uint32_t* img)
-{
-    const uint32_t t = threadIdx.x;
-    if (m.type == CR_BITMAP) {
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(S.bmp) + (m.off >> 2);
-        if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0)
-            return Chunks2{ld_stream(reinterpret_cast<const uint4*>(src) + t),
-                           ld_stream(reinterpret_cast<const uint4*>(src) + t + EXEC_NT)};
-        const uint32_t* p0 = src + 4u * t;
-        const uint32_t* p1 = p0 + 4u * EXEC_NT;
-        return Chunks2{make_uint4(p0[0], p0[1], p0[2], p0[3]), make_uint4(p1[0], p1[1], p1[2], p1[3])};
-    }
-    const uint4 z = make_uint4(0, 0, 0, 0);
-    if (m.type == CR_ARRAY) {
-        reinterpret_cast<uint4*>(img)[t] = z;
-        reinterpret_cast<uint4*>(img)[t + EXEC_NT] = z;
-        return Chunks2{z, z};
-    }
-    if (m.type != CR_RUN || m.card == 0) return Chunks2{z, z};
-    const uint16_t* runs = S.run + (m.off >> 1);
-    return Chunks2{run_chunk(runs, m.card, 128u * t), run_chunk(runs, m.card, 128u * (t + EXEC_NT))};
-}
-
-__device__ __forceinline__ void mix_scatter(const Side& S, const MixMeta& m, uint32_t* img)
-{
-    const uint16_t* vals = S.arr + (m.off >> 1);
-    for (uint32_t i0 = threadIdx.x; i0 < m.card; i0 += 8u * EXEC_NT) {  // eight values a thread in flight
-        uint32_t v[8];
+    for (uint32_t i0 = lane; i0 < n; i0 += 4u * 64u) {
+        uint16_t v[4];
 #pragma unroll
-        for (uint32_t k = 0; k < 8u; ++k) v[k] = i0 + EXEC_NT * k < m.card ? static_cast<uint32_t>(vals[i0 + EXEC_NT * k]) : ~0u;
+        for (uint32_t k = 0; k < 4u; ++k) v[k] = i0 + 64u * k < n ? src[i0 + 64u * k] : uint16_t(0);
 #pragma unroll
-        for (uint32_t k = 0; k < 8u; ++k)
-            if (v[k] != ~0u) atomicOr(&img[v[k] >> 5], 1u << (v[k] & 31u));
+        for (uint32_t k = 0; k < 4u; ++k)
+            if (i0 + 64u * k < n) dst[i0 + 64u * k] = v[k];
     }
 }
 
-// Eight workgroups a CU (at most 64 registers a lane): each item is a chain of
-// dependent loads, so the time follows the items in flight; against seven a
-// CU (69 registers) array pairs took 25-30% less, run pairs 10-15%.
+// AND of two sorted arrays: the values of `it_side` found in `srch` (LDS or
+// global), compacted in order with ballots; the first 128 values of
+// `it_side` come from `pit`.  Returns the count written to `out`.
+__device__ __forceinline__ uint32_t aa_probe(const uint16_t* it_side, uint32_t n_it, const Pre& pit,
+                                             const uint16_t* srch, uint32_t n_se, uint32_t lane, uint16_t* out)
+{
+    uint32_t card = 0;
+    for (uint32_t t0 = 0; t0 < n_it; t0 += 64u) {
+        const uint32_t i = t0 + lane;
+        bool p = false;
+        uint32_t v = 0;
+        if (i < n_it) {
+            v = t0 == 0 ? pit.v0 : (t0 == 64u ? pit.v1 : static_cast<uint32_t>(it_side[i]));
+            uint32_t lo = 0, hi = n_se;
+            while (lo < hi) {
+                const uint32_t mid = (lo + hi) >> 1;
+                if (srch[mid] < v)
+                    lo = mid + 1;
+                else
+                    hi = mid;
+            }
+            p = lo < n_se && srch[lo] == v;
+        }
+        const uint64_t mask = __ballot(p);
+        if (p) out[card + lanes_below(mask)] = static_cast<uint16_t>(v);
+        card += static_cast<uint32_t>(__popcll(mask));
+    }
+    return card;
+}
+
+// One item, run by one wave; returns its card | keep << 31.
 template <uint32_t OP>
-__global__ __launch_bounds__(EXEC_NT, 8) void so_exec(Side A, Side B, const Item* items, const Totals* totals,
-                                                   uint64_t* out_bmp, uint16_t* out_arr, uint16_t* out_run,
-                                                   uint32_t* item_card)
+__device__ __forceinline__ uint32_t run_item(const Side& A, const Side& B, const ExecItem& it, const Pre& pa,
+                                             const Pre& pb, uint32_t lane, uint32_t* img, uint64_t* out_bmp,
+                                             uint16_t* out_arr, uint16_t* out_run)
 {
-    __shared__ alignas(16) uint32_t lds[4096];  // 16 KiB: two array images, or a staged array
-    __shared__ uint32_t red[EXEC_NT / 64];
-    if (totals->overflow) return;  // the output was not allocated for this plan
-    const uint32_t n_items = totals->c[C_ITEM];
-    const uint32_t t = threadIdx.x;
-    for (uint32_t w = blockIdx.x; w < n_items; w += gridDim.x) {
-        const Item it = items[w];
-        uint32_t card = 0;
-        bool keep = true;
-        switch (it.cat) {
-        case CAT_BB: {
-            const uint64_t* pa = A.bmp + (it.aoff >> 3);
-            const uint64_t* pb = B.bmp + (it.boff >> 3);
-            const uint32_t pc = block_sum<EXEC_NT>(bitmap_op_stream<OP>(pa, pb, out_bmp + it.slot * 1024ull), red);
-            card = pc > 65535u ? 0u : pc;  // 65536 stored as 0 (src/set_ops.cu:179-180)
-            keep = card != 0 || OP == CR_OR;
-            break;
-        }
-        case CAT_MIXED: {
-            // both sides' metadata, then both sides' chunks, loaded together
-            const MixMeta ma = mix_meta(A, it.ai), mb = mix_meta(B, it.bi);
-            Chunks2 wa = mix_words(A, ma, lds);
-            Chunks2 wb = mix_words(B, mb, lds + 2048);
-            const bool arr_a = ma.type == CR_ARRAY, arr_b = mb.type == CR_ARRAY;  // the same in every thread
-            if (arr_a || arr_b) {
-                __syncthreads();  // the array images are zeroed
-                if (arr_a) mix_scatter(A, ma, lds);
-                if (arr_b) mix_scatter(B, mb, lds + 2048);
-                __syncthreads();
-                if (arr_a)
-                    wa = Chunks2{reinterpret_cast<const uint4*>(lds)[t], reinterpret_cast<const uint4*>(lds)[t + EXEC_NT]};
-                if (arr_b)
-                    wb = Chunks2{reinterpret_cast<const uint4*>(lds + 2048)[t],
-                                 reinterpret_cast<const uint4*>(lds + 2048)[t + EXEC_NT]};
+    const uint32_t ta = it.ma >> 16, tb = it.mb >> 16;
+    uint32_t card = 0;
+    bool keep = true;
+    switch (it.cat) {
+    case CAT_BB:
+    case CAT_MIXED: {
+        // A bitmap side is held in registers (its loads in flight while the
+        // other side's image is built); with two images, A's chunks are read
+        // into registers before B's image replaces them.
+        uint4* dst = reinterpret_cast<uint4*>(out_bmp + it.slot * 1024ull);  // 8 KiB slots: 16-byte aligned
+        uint32_t pc = 0;
+        uint4 x[8];
+        if (ta == CR_BITMAP && tb == CR_BITMAP) {
+            uint4 y[8];
+            bitmap_side(A.bmp, it.aoff, lane, x);
+            bitmap_side(B.bmp, it.boff, lane, y);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint4 r = apply4<OP>(x[j], y[j]);
+                st_stream(dst + lane + 64u * j, r);
+                pc += popc4(r);
             }
-            const uint4 r0 = make_uint4(apply32<OP>(wa.c0.x, wb.c0.x), apply32<OP>(wa.c0.y, wb.c0.y),
-                                        apply32<OP>(wa.c0.z, wb.c0.z), apply32<OP>(wa.c0.w, wb.c0.w));
-            const uint4 r1 = make_uint4(apply32<OP>(wa.c1.x, wb.c1.x), apply32<OP>(wa.c1.y, wb.c1.y),
-                                        apply32<OP>(wa.c1.z, wb.c1.z), apply32<OP>(wa.c1.w, wb.c1.w));
-            uint4* dst = reinterpret_cast<uint4*>(out_bmp + it.slot * 1024ull);  // 8 KiB slots: 16-byte aligned
-            st_stream(dst + t, r0);
-            st_stream(dst + t + EXEC_NT, r1);
-            uint32_t pc = __popc(r0.x) + __popc(r0.y) + __popc(r0.z) + __popc(r0.w) + __popc(r1.x) + __popc(r1.y) +
-                          __popc(r1.z) + __popc(r1.w);
-            pc = block_sum<EXEC_NT>(pc, red);
-            card = pc > 65535u ? 0u : pc;
-            keep = card != 0 || OP == CR_OR;
-            break;
+        } else if (ta == CR_BITMAP) {
+            bitmap_side(A.bmp, it.aoff, lane, x);
+            const bool tg = build_image(B, it.mb, it.boff, pb, lane, img);
+            pc = store_with_image<OP, true>(x, img, tg, lane, dst);
+        } else if (tb == CR_BITMAP) {
+            bitmap_side(B.bmp, it.boff, lane, x);
+            const bool tg = build_image(A, it.ma, it.aoff, pa, lane, img);
+            pc = store_with_image<OP, false>(x, img, tg, lane, dst);
+        } else {
+            bool tg = build_image(A, it.ma, it.aoff, pa, lane, img);
+            uint32_t carry = 0;
+#pragma unroll
+            for (uint32_t j = 0; j < 8u; ++j) x[j] = image_chunk(img, lane, j, tg, carry);
+            tg = build_image(B, it.mb, it.boff, pb, lane, img);  // its zeroing follows the reads above
+            pc = store_with_image<OP, true>(x, img, tg, lane, dst);
         }
-        case CAT_BA: {
-            const bool bmp_is_a = A.types[it.ai] == CR_BITMAP;
-            const uint64_t* bm = bmp_is_a ? A.bmp + (it.aoff >> 3) : B.bmp + (it.boff >> 3);
-            const uint16_t* arr = bmp_is_a ? B.arr + (it.boff >> 1) : A.arr + (it.aoff >> 1);
-            const uint32_t n = bmp_is_a ? B.cards[it.bi] : A.cards[it.ai];
-            uint16_t* out = out_arr + it.slot;
-            // Probe in array order and compact in order: output stays sorted.
-            for (uint32_t t0 = 0; t0 < n; t0 += EXEC_NT) {
-                const uint32_t i = t0 + t;
-                bool p = false;
-                uint32_t v = 0;
-                if (i < n) {
-                    v = arr[i];
-                    p = (bm[v >> 6] >> (v & 63u)) & 1u;
-                }
-                uint32_t tot;
-                const uint32_t r = block_flag_rank<EXEC_NT>(p, red, tot);
-                if (p) out[card + r] = static_cast<uint16_t>(v);
-                card += tot;
-            }
-            keep = card != 0;
-            break;
-        }
-        case CAT_AA: {
-            const uint16_t* x = A.arr + (it.aoff >> 1);
-            const uint16_t* y = B.arr + (it.boff >> 1);
-            uint32_t nx = A.cards[it.ai], ny = B.cards[it.bi];
-            // Iterate one side in order and binary-search the other, staged in LDS
-            // when it fits (sorted unique arrays: same result as a merge).
-            const uint16_t* it_side = x;
-            uint32_t n_it = nx;
-            const uint16_t* se_side = y;
-            uint32_t n_se = ny;
-            if (nx > ny) {
-                if (nx <= LDS_ARRAY_CAP) {
-                    it_side = y;
-                    n_it = ny;
-                    se_side = x;
-                    n_se = nx;
-                }
-            } else if (ny > LDS_ARRAY_CAP && nx <= LDS_ARRAY_CAP) {
-                it_side = y;
-                n_it = ny;
-                se_side = x;
-                n_se = nx;
-            }
-            const bool staged = n_se <= LDS_ARRAY_CAP;
-            uint16_t* lds16 = reinterpret_cast<uint16_t*>(lds);
-            if (staged) {
-                for (uint32_t i = t; i < n_se; i += EXEC_NT) lds16[i] = se_side[i];
-                __syncthreads();
-            }
-            const uint16_t* srch = staged ? lds16 : se_side;
-            uint16_t* out = out_arr + it.slot;
-            for (uint32_t t0 = 0; t0 < n_it; t0 += EXEC_NT) {
-                const uint32_t i = t0 + t;
-                bool p = false;
-                uint32_t v = 0;
-                if (i < n_it) {
-                    v = it_side[i];
-                    uint32_t lo = 0, hi = n_se;
-                    while (lo < hi) {
-                        const uint32_t mid = (lo + hi) >> 1;
-                        if (srch[mid] < v)
-                            lo = mid + 1;
-                        else
-                            hi = mid;
-                    }
-                    p = lo < n_se && srch[lo] == v;
-                }
-                uint32_t tot;
-                const uint32_t r = block_flag_rank<EXEC_NT>(p, red, tot);
-                if (p) out[card + r] = static_cast<uint16_t>(v);
-                card += tot;
-            }
-            keep = card != 0;
-            break;
-        }
-        case CAT_COPY_BMP: {
-            const bool from_a = it.ai >= 0;
-            const Side& S = from_a ? A : B;
-            const int32_t idx = from_a ? it.ai : it.bi;
-            const uint64_t* src = S.bmp + ((from_a ? it.aoff : it.boff) >> 3);
-            uint64_t* dst = out_bmp + it.slot * 1024ull;
-            if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
-                st_stream(reinterpret_cast<uint4*>(dst) + t, ld_stream(reinterpret_cast<const uint4*>(src) + t));
-                st_stream(reinterpret_cast<uint4*>(dst) + t + EXEC_NT,
-                          ld_stream(reinterpret_cast<const uint4*>(src) + t + EXEC_NT));
-            } else {
-                for (uint32_t i = t; i < 1024u; i += EXEC_NT) dst[i] = src[i];
-            }
-            card = S.cards[idx];
-            break;
-        }
-        case CAT_COPY_ARR:
-        case CAT_COPY_RUN: {
-            const bool from_a = it.ai >= 0;
-            const Side& S = from_a ? A : B;
-            const int32_t idx = from_a ? it.ai : it.bi;
-            card = S.cards[idx];
-            const bool is_arr = it.cat == CAT_COPY_ARR;
-            const uint16_t* src = (is_arr ? S.arr : S.run) + (S.offsets[idx] >> 1);
-            uint16_t* dst = (is_arr ? out_arr : out_run) + it.slot;
-            const uint32_t n = is_arr ? card : 2u * card;
-            for (uint32_t i = t; i < n; i += EXEC_NT) dst[i] = src[i];
-            break;
-        }
-        default: break;
-        }
-        if (t == 0) item_card[w] = card | (keep ? 0x80000000u : 0u);
-        __syncthreads();
+        pc = wave_total(pc);
+        card = pc > 65535u ? 0u : pc;  // 65536 stored as 0 (src/set_ops.cu:179-180)
+        keep = card != 0 || OP == CR_OR;
+        break;
     }
+    case CAT_BA: {
+        // AND of a bitmap and an array: the array's values whose bit is set,
+        // compacted in array order with ballots (the output is sorted).
+        const bool bmp_is_a = ta == CR_BITMAP;
+        const uint64_t* bm = bmp_is_a ? A.bmp + (it.aoff >> 3) : B.bmp + (it.boff >> 3);
+        const uint16_t* arr = bmp_is_a ? B.arr + (it.boff >> 1) : A.arr + (it.aoff >> 1);
+        const uint32_t n = (bmp_is_a ? it.mb : it.ma) & 0xFFFFu;
+        const Pre pv = bmp_is_a ? pb : pa;
+        uint16_t* out = out_arr + it.slot;
+        for (uint32_t t0 = 0; t0 < n; t0 += 4u * 64u) {  // four values a lane in flight
+            uint32_t v[4];
+            bool p[4];
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; ++k) {
+                const uint32_t i = t0 + 64u * k + lane;
+                const uint32_t x = (t0 == 0 && k < 2u) ? (k == 0 ? pv.v0 : pv.v1)
+                                                        : (i < n ? static_cast<uint32_t>(arr[i]) : 0u);
+                v[k] = i < n ? x : 0u;
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; ++k) {
+                const uint32_t i = t0 + 64u * k + lane;
+                p[k] = i < n && ((bm[v[k] >> 6] >> (v[k] & 63u)) & 1u) != 0u;
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; ++k) {
+                const uint64_t mask = __ballot(p[k]);
+                if (p[k]) out[card + lanes_below(mask)] = static_cast<uint16_t>(v[k]);
+                card += static_cast<uint32_t>(__popcll(mask));
+            }
+        }
+        keep = card != 0;
+        break;
+    }
+    case CAT_AA: {
+        // AND of two arrays: each value of one side is searched in the other,
+        // staged in the wave's LDS when it fits (sorted unique arrays: the same
+        // result as a merge), compacted with ballots.
+        const uint16_t* x = A.arr + (it.aoff >> 1);
+        const uint16_t* y = B.arr + (it.boff >> 1);
+        const uint32_t nx = it.ma & 0xFFFFu, ny = it.mb & 0xFFFFu;
+        constexpr uint32_t CAP = 2u * EXEC_LDS_WORDS;  // u16 values the wave's LDS holds
+        // iterate the shorter side unless only it fits the LDS
+        bool swap = nx > ny;
+        if (swap && nx > CAP && ny <= CAP) swap = false;
+        if (!swap && ny > CAP && nx <= CAP) swap = true;
+        const uint16_t* it_side = swap ? y : x;
+        const uint16_t* se_side = swap ? x : y;
+        const uint32_t n_it = swap ? ny : nx, n_se = swap ? nx : ny;
+        const Pre pit = swap ? pb : pa;
+        const Pre pse = swap ? pa : pb;
+        uint16_t* out = out_arr + it.slot;
+        if (n_se <= CAP) {
+            uint16_t* lds16 = reinterpret_cast<uint16_t*>(img);
+            if (lane < n_se) lds16[lane] = static_cast<uint16_t>(pse.v0);
+            if (lane + 64u < n_se) lds16[lane + 64u] = static_cast<uint16_t>(pse.v1);
+            if (n_se > 128u) wave_copy16(lds16 + 128, se_side + 128, n_se - 128u, lane);
+            wave_lds_fence();
+            card = aa_probe(it_side, n_it, pit, lds16, n_se, lane, out);
+            wave_lds_fence();  // the searches are done before the next item's LDS writes
+        } else {
+            card = aa_probe(it_side, n_it, pit, se_side, n_se, lane, out);
+        }
+        keep = card != 0;
+        break;
+    }
+    case CAT_COPY_BMP: {
+        const bool from_a = it.from_a != 0;
+        uint4 c[8];
+        bitmap_side(from_a ? A.bmp : B.bmp, from_a ? it.aoff : it.boff, lane, c);
+        uint4* dst = reinterpret_cast<uint4*>(out_bmp + it.slot * 1024ull);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) st_stream(dst + lane + 64u * j, c[j]);
+        card = (from_a ? it.ma : it.mb) & 0xFFFFu;
+        break;
+    }
+    case CAT_COPY_ARR:
+    case CAT_COPY_RUN: {
+        // the first 128 values (64 runs) from the preload, the rest copied
+        const bool from_a = it.from_a != 0;
+        const Pre pv = from_a ? pa : pb;
+        card = (from_a ? it.ma : it.mb) & 0xFFFFu;
+        const uint16_t* src;
+        uint16_t* dst;
+        uint32_t n;
+        if (it.cat == CAT_COPY_ARR) {
+            src = (from_a ? A.arr : B.arr) + ((from_a ? it.aoff : it.boff) >> 1);
+            dst = out_arr + it.slot;
+            n = card;
+            if (lane < n) dst[lane] = static_cast<uint16_t>(pv.v0);
+            if (lane + 64u < n) dst[lane + 64u] = static_cast<uint16_t>(pv.v1);
+        } else {
+            src = (from_a ? A.run : B.run) + ((from_a ? it.aoff : it.boff) >> 1);
+            dst = out_run + it.slot;
+            n = 2u * card;
+            if (lane < card) {
+                dst[2u * lane] = static_cast<uint16_t>(pv.v0);
+                dst[2u * lane + 1u] = static_cast<uint16_t>(pv.v0 >> 16);
+            }
+        }
+        if (n > 128u) wave_copy16(dst + 128, src + 128, n - 128u, lane);
+        break;
+    }
+    default: break;
+    }
+    return card | (keep ? 0x80000000u : 0u);
+}
+
+template <uint32_t OP>
+__global__ __launch_bounds__(EXEC_NT) __attribute__((amdgpu_waves_per_eu(EXEC_WAVES_PER_CU / 4u))) void so_exec(
+    Side A, Side B, const ExecItem* __restrict__ xitems, const Totals* totals, uint64_t* __restrict__ out_bmp,
+    uint16_t* __restrict__ out_arr, uint16_t* __restrict__ out_run, uint32_t* __restrict__ item_card)
+{
+    __shared__ alignas(16) uint32_t lds[(EXEC_NT / 64) * EXEC_LDS_WORDS];
+    if (totals->overflow) return;  // the output was not allocated for this plan
+    const uint32_t w = uni((blockIdx.x * EXEC_NT + threadIdx.x) >> 6);
+    if (w >= totals->c[C_ITEM]) return;
+    const uint32_t lane = __lane_id();
+    const ExecItem it = load_xitem(xitems + w);
+    const Pre pa = preload(A, it.ma, it.aoff, lane), pb = preload(B, it.mb, it.boff, lane);
+    const uint32_t r =
+        run_item<OP>(A, B, it, pa, pb, lane, lds + (threadIdx.x >> 6) * EXEC_LDS_WORDS, out_bmp, out_arr, out_run);
+    if (lane == 0) item_card[it.pos] = r;
 }
 
 // item_card: bit 31 = keep, bit 30 = an invalid item (the plan found a
@@ -713,8 +921,6 @@ constexpr int BB_NT = 256;
 
 template <uint32_t OP>
 __global__ __launch_bounds__(BB_NT) void so_exec_bb(const uint64_t* __restrict__ a_bmp, const uint64_t* __restrict__ b_bmp,
-                                                    const uint16_t* __restrict__ a_cards,
-                                                    const uint16_t* __restrict__ b_cards,
                                                     const Item* __restrict__ items, const Totals* totals,
                                                     uint64_t* __restrict__ out_bmp, uint32_t* __restrict__ item_card)
 {
@@ -748,7 +954,7 @@ __global__ __launch_bounds__(BB_NT) void so_exec_bb(const uint64_t* __restrict__
             } else {
                 for (uint32_t i = lane; i < 1024u; i += 64) po[i] = src[i];
             }
-            if (lane == 0) item_card[w] = static_cast<uint32_t>(from_a ? a_cards[cur.ai] : b_cards[cur.bi]) | 0x80000000u;
+            if (lane == 0) item_card[w] = ((from_a ? cur.ma : cur.mb) & 0xFFFFu) | 0x80000000u;
             continue;
         }
         if (((cur.aoff | cur.boff) & 15u) == 0) {
@@ -1098,6 +1304,7 @@ static Caps setop_caps(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_
 struct SetOpPlan {
     Scratch sc;
     Item* items;
+    ExecItem* xitems = nullptr;  // so_plan_assign: the items in execution order
     Totals* tot;
     uint32_t* icard;
     uint32_t n_tiles;
@@ -1113,12 +1320,14 @@ static int plan_set_operation(const Side& A, const Side& B, uint32_t op, uint32_
     const size_t o_recs = c.add(sizeof(KeyRec) * 65536);
     const size_t o_gc = c.add(sizeof(uint32_t) * PLAN_GROUPS * C_N);
     const size_t o_items = c.add(sizeof(Item) * bound);
+    const size_t o_xitems = c.add(sizeof(ExecItem) * bound);
     const size_t o_tot = c.add(sizeof(Totals));
     const size_t o_card = c.add(sizeof(uint32_t) * bound);
     CR_RET(P.sc.alloc(c.total, s));
     KeyRec* recs = P.sc.at<KeyRec>(o_recs);
     uint32_t* gc = P.sc.at<uint32_t>(o_gc);
     P.items = P.sc.at<Item>(o_items);
+    P.xitems = P.sc.at<ExecItem>(o_xitems);
     P.tot = P.sc.at<Totals>(o_tot);
     P.icard = P.sc.at<uint32_t>(o_card);
     {
@@ -1128,7 +1337,7 @@ static int plan_set_operation(const Side& A, const Side& B, uint32_t op, uint32_
     CR_LAUNCH_CHECK();
     {
         CR_TIMED("so_plan_assign", s);
-        so_plan_assign<<<PLAN_GROUPS, PLAN_NT, 0, s>>>(recs, gc, P.items, P.tot, caps);
+        so_plan_assign<<<PLAN_GROUPS, PLAN_NT, 0, s>>>(recs, gc, P.items, P.xitems, P.tot, caps);
     }
     CR_LAUNCH_CHECK();
     return CR_OK;
@@ -1155,7 +1364,8 @@ static int plan_bitmap_keyed(const cr_gpu_roaring* a, const cr_gpu_roaring* b, u
         const uint32_t groups = (std::max(len_a, len_b) + KP_NT - 1) / KP_NT;  // max_key <= 0xFFFF: <= 64
         P.n_kbad = groups;
         so_plan_bitmap<<<groups, KP_NT, 0, s>>>(a->key_index, len_a, b->key_index, len_b, a->offsets, b->offsets,
-                                                a->types, b->types, a->keys, b->keys, a->n_containers,
+                                                a->types, b->types, a->cardinalities, b->cardinalities,
+                                                a->keys, b->keys, a->n_containers,
                                                 b->n_containers, op, caps, P.items, P.tot, P.kbad);
     }
     CR_LAUNCH_CHECK();
@@ -1175,40 +1385,41 @@ static int exec_set_operation(const Side& A, const Side& B, uint32_t op, uint32_
         CR_TIMED("so_exec", s);
         switch (op) {
         case CR_AND:
-            so_exec_bb<CR_AND><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, A.cards, B.cards, P.items, P.tot, out->bitmap_data,
+            so_exec_bb<CR_AND><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, P.items, P.tot, out->bitmap_data,
                                                     P.icard);
             break;
         case CR_OR:
-            so_exec_bb<CR_OR><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, A.cards, B.cards, P.items, P.tot, out->bitmap_data,
+            so_exec_bb<CR_OR><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, P.items, P.tot, out->bitmap_data,
                                                    P.icard);
             break;
         case CR_ANDNOT:
-            so_exec_bb<CR_ANDNOT><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, A.cards, B.cards, P.items, P.tot,
+            so_exec_bb<CR_ANDNOT><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, P.items, P.tot,
                                                        out->bitmap_data, P.icard);
             break;
         default:
-            so_exec_bb<CR_XOR><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, A.cards, B.cards, P.items, P.tot, out->bitmap_data,
+            so_exec_bb<CR_XOR><<<gb, BB_NT, 0, s>>>(A.bmp, B.bmp, P.items, P.tot, out->bitmap_data,
                                                     P.icard);
             break;
         }
     } else {
-        const unsigned g = exec_grid(bound);
+        // one wave per item
+        const unsigned g = std::max(1u, (bound + 3u) / 4u);
         CR_TIMED("so_exec", s);
         switch (op) {
         case CR_AND:
-            so_exec<CR_AND><<<g, EXEC_NT, 0, s>>>(A, B, P.items, P.tot, out->bitmap_data, out->array_data,
+            so_exec<CR_AND><<<g, EXEC_NT, 0, s>>>(A, B, P.xitems, P.tot, out->bitmap_data, out->array_data,
                                                   out->run_data, P.icard);
             break;
         case CR_OR:
-            so_exec<CR_OR><<<g, EXEC_NT, 0, s>>>(A, B, P.items, P.tot, out->bitmap_data, out->array_data,
+            so_exec<CR_OR><<<g, EXEC_NT, 0, s>>>(A, B, P.xitems, P.tot, out->bitmap_data, out->array_data,
                                                  out->run_data, P.icard);
             break;
         case CR_ANDNOT:
-            so_exec<CR_ANDNOT><<<g, EXEC_NT, 0, s>>>(A, B, P.items, P.tot, out->bitmap_data, out->array_data,
-                                                     out->run_data, P.icard);
+            so_exec<CR_ANDNOT><<<g, EXEC_NT, 0, s>>>(A, B, P.xitems, P.tot, out->bitmap_data,
+                                                     out->array_data, out->run_data, P.icard);
             break;
         default:
-            so_exec<CR_XOR><<<g, EXEC_NT, 0, s>>>(A, B, P.items, P.tot, out->bitmap_data, out->array_data,
+            so_exec<CR_XOR><<<g, EXEC_NT, 0, s>>>(A, B, P.xitems, P.tot, out->bitmap_data, out->array_data,
                                                   out->run_data, P.icard);
             break;
         }

@@ -540,15 +540,6 @@ __device__ __forceinline__ void group_fields(const FieldGroup& q, uint32_t (&f)[
     f[7] = d4 >> 12;
 }
 
-// The wave's own LDS writes are visible to its later LDS reads (its LDS
-// operations retire in order); this keeps the compiler from moving them across.
-__device__ __forceinline__ void wave_lds_fence()
-{
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 template <class Prologue, class OnGroup>
 __device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, const uint16_t* __restrict__ tab,
                                             const IdsGeom& g, uint32_t b, uint32_t wave, uint32_t lane,

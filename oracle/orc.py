@@ -529,6 +529,25 @@ def upload_packed(bm: Lite, universe: Optional[int] = None, threshold: int = PRO
     return r
 
 
+def upload_containers(containers, universe: int = 0, complemented: bool = False, logical: int = 0,
+                      threshold: int = PROMOTE_AUTO, l2_bytes: int = DEFAULT_L2) -> HostRoaring:
+    """upload_packed of host containers given as [(key, typecode, card | n_runs,
+    payload)] sorted by key, taken as they are: the runs of a run container need
+    not be sorted, disjoint or merged (src/upload.cpp:215-221 copies them as
+    they are)."""
+    arr = (_OrcContainer * max(1, len(containers)))()
+    keep = []
+    for i, (key, tc, card, payload) in enumerate(containers):
+        p = np.ascontiguousarray(payload)
+        keep.append(p)
+        arr[i] = _OrcContainer(key, tc, card, p.ctypes.data if p.size else None)
+    c = _OrcRoaring()
+    _check(lib().orc_upload_packed(C.addressof(arr), len(containers), universe, 1 if complemented else 0, logical,
+                                   threshold, l2_bytes, C.byref(c)), "upload_containers")
+    del keep
+    return _from_c(c)
+
+
 # ---- generators ---------------------------------------------------------
 def mt_bernoulli_ids(seed: int, density: float, universe: int) -> np.ndarray:
     out = np.zeros(max(universe, 1), dtype=np.uint32)

@@ -559,6 +559,61 @@ def test_set_operation_dense_all_bitmap(gpu, op, case):
         gpu.free(x)
 
 
+def _irregular_run_operands():
+    """Run containers as the portable format allows but run_optimize never
+    writes: runs that touch (not merged), overlap, come out of order, or end past
+    0xFFFF, and runs on word and chunk edges; each against an array, a bitmap,
+    another run container, or nothing."""
+    rng = np.random.default_rng(91)
+
+    def run(*pairs):
+        return (orc.TC_RUN, len(pairs), np.array(pairs, dtype=np.uint16).ravel())
+
+    def arr(n):
+        v = np.unique(rng.integers(0, 65536, n)).astype(np.uint16)
+        return (orc.TC_ARRAY, v.size, v)
+
+    def bmp(p):
+        w = np.packbits(rng.random(65536) < p, bitorder="little").view(np.uint64)
+        return (orc.TC_BITSET, int(np.unpackbits(w.view(np.uint8)).sum()) % 65536, w)
+
+    many = [(2 * i * 7, i % 3) for i in range(3000)]  # 3000 short disjoint runs
+    a = {0: run((100, 49), (150, 9), (160, 0)),            # touching
+         1: run((1000, 500), (1200, 100), (1250, 3000)),   # overlapping
+         2: run((5000, 10), (100, 20)),                     # out of order
+         3: run((65000, 1000)),                             # ends past 0xFFFF
+         4: run(*many),
+         5: run((0, 0), (31, 1), (63, 64), (4095, 4097), (65535, 0)),
+         6: run((7, 3)),                                    # one-sided
+         8: run((31, 0), (32, 31), (64, 63), (127, 128))}   # touching on word edges
+    b = {0: arr(300), 1: bmp(0.4), 2: run((90, 5), (96, 3)), 3: run((0, 65535)), 4: arr(4000),
+         5: run((40000, 100), (30000, 5000)), 7: run((1, 1)), 8: bmp(0.02)}
+    to_list = lambda d: [(k,) + d[k] for k in sorted(d)]
+    return to_list(a), to_list(b)
+
+
+@pytest.mark.parametrize("op", [orc.AND, orc.OR, orc.ANDNOT, orc.XOR])
+@pytest.mark.parametrize("swap", [False, True])
+def test_set_operation_irregular_runs(gpu, op, swap):
+    """Runs are decoded as the reference's expansion does (each run's bits
+    ORed in, the end clamped to 0xFFFF; src/set_ops.cu:322-368) whatever their
+    order: the decode by toggles, and its fallback for runs that are not sorted
+    and disjoint."""
+    _say("set_operation irregular runs", op, swap)
+    ca, cb = _irregular_run_operands()
+    if swap:
+        ca, cb = cb, ca
+    thr = orc.PROMOTE_KEEP_DEFAULT
+    oa, ob = orc.upload_containers(ca, threshold=thr), orc.upload_containers(cb, threshold=thr)
+    ga, gb = gpu.upload_containers(ca, 0, False, 0, thr), gpu.upload_containers(cb, 0, False, 0, thr)
+    assert_same(gpu.download(ga), oa, strict=True, what="irregular upload a")
+    assert_same(gpu.download(gb), ob, strict=True, what="irregular upload b")
+    g = gpu.set_operation(ga, gb, op)
+    assert_same(gpu.download(g), orc.set_operation(oa, ob, op), strict=True, what=f"irregular runs {op}")
+    for x in (g, ga, gb):
+        gpu.free(x)
+
+
 def test_set_operation_empty_and_identical(gpu):
     _say("set_operation empty/identical")
     a = orc.Lite.from_sorted_ids(np.arange(1000, dtype=np.uint32))
