@@ -84,6 +84,9 @@ struct Caps {
     // only valid if they name exactly na and nb keys, each the key its
     // container holds (the reference matches on `keys`, src/set_ops.cu:76-122).
     uint32_t check_kidx, na, nb;
+    // Items that write array or run values, at most: the execution launches
+    // waves for this many (and for `bmp` bitmap-writing ones).
+    uint32_t small;
 };
 
 // The classification reads the key indexes instead of searching the keys.
@@ -252,6 +255,7 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_assign(const KeyRec* recs, co
         totals->overflow = gtot[C_ITEM] > caps.items || gtot[C_BB] + gtot[C_MX] + gtot[C_CB] > caps.bmp ||
                            gtot[C_BAE] + gtot[C_AAE] + gtot[C_CAE] > caps.arr || 2u * gtot[C_CRP] > caps.run_u16 ||
                            (caps.bb_only && gtot[C_BB] + gtot[C_CB] != gtot[C_ITEM]) ||
+                           gtot[C_ITEM] - (gtot[C_BB] + gtot[C_MX] + gtot[C_CB]) > caps.small ||
                            (caps.check_kidx && (gtot[C_KA] != caps.na || gtot[C_KB] != caps.nb || gtot[C_KBAD] != 0));
 
     const uint32_t key = blockIdx.x * PLAN_NT + t;
@@ -295,14 +299,13 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_assign(const KeyRec* recs, co
     it.slot = slot;
     if (item_pos < caps.items) {  // the item scratch holds caps.items
         items[item_pos] = it;
-        // The execution order: items that write a bitmap first (the longest
-        // start first), then those that write array or run values, each group
-        // in key order.
-        const uint32_t n_big = gtot[C_BB] + gtot[C_MX] + gtot[C_CB];
+        // The execution records: items that write a bitmap at [0, caps.items),
+        // those that write array or run values at caps.items + [0, caps.items),
+        // each in key order.
         const uint32_t big_before = gbase[C_BB] + gbase[C_MX] + gbase[C_CB] + p_bb + p_mx + p_cb;
         const bool big = cat == CAT_BB || cat == CAT_MIXED || cat == CAT_COPY_BMP;
-        const uint32_t e = big ? big_before : n_big + (item_pos - big_before);
-        if (e < caps.items) {  // (beyond it only when the plan overflows)
+        const uint32_t r = big ? big_before : item_pos - big_before;
+        if (r < caps.items) {  // (beyond it only when the plan overflows)
             ExecItem x;
             x.pos = static_cast<uint16_t>(item_pos);
             x.cat = cat;
@@ -313,7 +316,7 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_assign(const KeyRec* recs, co
             x.ma = rec.ma;
             x.mb = rec.mb;
             x.pad[0] = x.pad[1] = 0;
-            xitems[e] = x;
+            xitems[big ? r : caps.items + r] = x;
         }
     }
 }
@@ -642,12 +645,18 @@ __device__ __forceinline__ bool build_image(const Side& S, uint32_t meta, uint32
 // Chunk l + 64 j of an image, read in the order j = 0..7.  With toggles each
 // 32-bit word is its own prefix XOR (five shifts) flipped by the parity of
 // every toggle before it: the words before it in the lane's chunk, the lanes
-// before it in group j (a ballot), and groups 0..j-1 (`carry`).
+// before it in group j (a ballot), and groups 0..j-1 (`carry`).  A group with
+// no toggle (most of them: a run container holds a few runs) is all ones or
+// all zeros.
 __device__ __forceinline__ uint4 image_chunk(const uint32_t* img, uint32_t lane, uint32_t j, bool toggles,
                                              uint32_t& carry)
 {
     const uint4 x = reinterpret_cast<const uint4*>(img)[lane + 64u * j];
     if (!toggles) return x;
+    if (__ballot((x.x | x.y | x.z | x.w) != 0u) == 0ull) {  // no toggle in the group: all as before it
+        const uint32_t f = 0u - carry;
+        return make_uint4(f, f, f, f);
+    }
     uint32_t w[4] = {x.x, x.y, x.z, x.w};
     uint32_t p = 0;
 #pragma unroll
@@ -703,41 +712,11 @@ __device__ __forceinline__ void wave_copy16(uint16_t* dst, const uint16_t* src, 
     }
 }
 
-// AND of two sorted arrays: the values of `it_side` found in `srch` (LDS or
-// global), compacted in order with ballots; the first 128 values of
-// `it_side` come from `pit`.  Returns the count written to `out`.
-__device__ __forceinline__ uint32_t aa_probe(const uint16_t* it_side, uint32_t n_it, const Pre& pit,
-                                             const uint16_t* srch, uint32_t n_se, uint32_t lane, uint16_t* out)
-{
-    uint32_t card = 0;
-    for (uint32_t t0 = 0; t0 < n_it; t0 += 64u) {
-        const uint32_t i = t0 + lane;
-        bool p = false;
-        uint32_t v = 0;
-        if (i < n_it) {
-            v = t0 == 0 ? pit.v0 : (t0 == 64u ? pit.v1 : static_cast<uint32_t>(it_side[i]));
-            uint32_t lo = 0, hi = n_se;
-            while (lo < hi) {
-                const uint32_t mid = (lo + hi) >> 1;
-                if (srch[mid] < v)
-                    lo = mid + 1;
-                else
-                    hi = mid;
-            }
-            p = lo < n_se && srch[lo] == v;
-        }
-        const uint64_t mask = __ballot(p);
-        if (p) out[card + lanes_below(mask)] = static_cast<uint16_t>(v);
-        card += static_cast<uint32_t>(__popcll(mask));
-    }
-    return card;
-}
-
-// One item, run by one wave; returns its card | keep << 31.
+// An item that writes a bitmap (BB, MIXED, COPY_BMP), run by one wave;
+// returns its card | keep << 31.
 template <uint32_t OP>
-__device__ __forceinline__ uint32_t run_item(const Side& A, const Side& B, const ExecItem& it, const Pre& pa,
-                                             const Pre& pb, uint32_t lane, uint32_t* img, uint64_t* out_bmp,
-                                             uint16_t* out_arr, uint16_t* out_run)
+__device__ __forceinline__ uint32_t run_big(const Side& A, const Side& B, const ExecItem& it, const Pre& pa,
+                                            const Pre& pb, uint32_t lane, uint32_t* img, uint64_t* out_bmp)
 {
     const uint32_t ta = it.ma >> 16, tb = it.mb >> 16;
     uint32_t card = 0;
@@ -782,6 +761,32 @@ __device__ __forceinline__ uint32_t run_item(const Side& A, const Side& B, const
         keep = card != 0 || OP == CR_OR;
         break;
     }
+    case CAT_COPY_BMP: {
+        const bool from_a = it.from_a != 0;
+        uint4 c[8];
+        bitmap_side(from_a ? A.bmp : B.bmp, from_a ? it.aoff : it.boff, lane, c);
+        uint4* dst = reinterpret_cast<uint4*>(out_bmp + it.slot * 1024ull);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) st_stream(dst + lane + 64u * j, c[j]);
+        card = (from_a ? it.ma : it.mb) & 0xFFFFu;
+        break;
+    }
+    default: break;
+    }
+    return card | (keep ? 0x80000000u : 0u);
+}
+
+// An item that writes array or run values (BA, AA, COPY_ARR, COPY_RUN), run by
+// one wave; returns its card | keep << 31.
+template <uint32_t OP>
+__device__ __forceinline__ uint32_t run_small(const Side& A, const Side& B, const ExecItem& it, const Pre& pa,
+                                              const Pre& pb, uint32_t lane, uint32_t* img, uint16_t* out_arr,
+                                              uint16_t* out_run)
+{
+    const uint32_t ta = it.ma >> 16;
+    uint32_t card = 0;
+    bool keep = true;
+    switch (it.cat) {
     case CAT_BA: {
         // AND of a bitmap and an array: the array's values whose bit is set,
         // compacted in array order with ballots (the output is sorted).
@@ -817,45 +822,30 @@ __device__ __forceinline__ uint32_t run_item(const Side& A, const Side& B, const
         break;
     }
     case CAT_AA: {
-        // AND of two arrays: each value of one side is searched in the other,
-        // staged in the wave's LDS when it fits (sorted unique arrays: the same
-        // result as a merge), compacted with ballots.
-        const uint16_t* x = A.arr + (it.aoff >> 1);
-        const uint16_t* y = B.arr + (it.boff >> 1);
+        // AND of two arrays: one side's values set in the wave's image, the
+        // other side's probed against it in order and compacted with ballots
+        // (the output is sorted).  The longer side goes into the image.
         const uint32_t nx = it.ma & 0xFFFFu, ny = it.mb & 0xFFFFu;
-        constexpr uint32_t CAP = 2u * EXEC_LDS_WORDS;  // u16 values the wave's LDS holds
-        // iterate the shorter side unless only it fits the LDS
-        bool swap = nx > ny;
-        if (swap && nx > CAP && ny <= CAP) swap = false;
-        if (!swap && ny > CAP && nx <= CAP) swap = true;
-        const uint16_t* it_side = swap ? y : x;
-        const uint16_t* se_side = swap ? x : y;
-        const uint32_t n_it = swap ? ny : nx, n_se = swap ? nx : ny;
-        const Pre pit = swap ? pb : pa;
-        const Pre pse = swap ? pa : pb;
+        const bool img_a = nx > ny;
+        build_image(img_a ? A : B, img_a ? it.ma : it.mb, img_a ? it.aoff : it.boff, img_a ? pa : pb, lane, img);
+        const uint16_t* vals = img_a ? B.arr + (it.boff >> 1) : A.arr + (it.aoff >> 1);
+        const Pre pv = img_a ? pb : pa;
+        const uint32_t n = img_a ? ny : nx;
         uint16_t* out = out_arr + it.slot;
-        if (n_se <= CAP) {
-            uint16_t* lds16 = reinterpret_cast<uint16_t*>(img);
-            if (lane < n_se) lds16[lane] = static_cast<uint16_t>(pse.v0);
-            if (lane + 64u < n_se) lds16[lane + 64u] = static_cast<uint16_t>(pse.v1);
-            if (n_se > 128u) wave_copy16(lds16 + 128, se_side + 128, n_se - 128u, lane);
-            wave_lds_fence();
-            card = aa_probe(it_side, n_it, pit, lds16, n_se, lane, out);
-            wave_lds_fence();  // the searches are done before the next item's LDS writes
-        } else {
-            card = aa_probe(it_side, n_it, pit, se_side, n_se, lane, out);
+        for (uint32_t t0 = 0; t0 < n; t0 += 64u) {
+            const uint32_t i = t0 + lane;
+            bool p = false;
+            uint32_t v = 0;
+            if (i < n) {
+                v = t0 == 0 ? pv.v0 : (t0 == 64u ? pv.v1 : static_cast<uint32_t>(vals[i]));
+                p = ((img[v >> 5] >> (v & 31u)) & 1u) != 0u;
+            }
+            const uint64_t mask = __ballot(p);
+            if (p) out[card + lanes_below(mask)] = static_cast<uint16_t>(v);
+            card += static_cast<uint32_t>(__popcll(mask));
         }
+        wave_lds_fence();  // the probes are done before the next item's LDS writes
         keep = card != 0;
-        break;
-    }
-    case CAT_COPY_BMP: {
-        const bool from_a = it.from_a != 0;
-        uint4 c[8];
-        bitmap_side(from_a ? A.bmp : B.bmp, from_a ? it.aoff : it.boff, lane, c);
-        uint4* dst = reinterpret_cast<uint4*>(out_bmp + it.slot * 1024ull);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) st_stream(dst + lane + 64u * j, c[j]);
-        card = (from_a ? it.ma : it.mb) & 0xFFFFu;
         break;
     }
     case CAT_COPY_ARR:
@@ -890,21 +880,60 @@ __device__ __forceinline__ uint32_t run_item(const Side& A, const Side& B, const
     return card | (keep ? 0x80000000u : 0u);
 }
 
+// Waves [0, n_big_waves) run the bitmap-writing items, one each (those past
+// their count exit); the waves after them take SMALL_PER_WAVE of the other
+// items each.  The plan wrote the records of the first kind at xitems[0, stride)
+// and of the second at xitems[stride, 2 stride), so a wave's records sit at
+// offsets known at launch and load in the same scalar-load round as the
+// plan's totals.  A small-item wave loads
+// all its records and first payload words, then waits for all of them once:
+// from then on no item waits for an earlier one's stores (a wave's loads and
+// stores retire in order, and the compiler cannot count stores issued in
+// loops).
+constexpr uint32_t SMALL_PER_WAVE = 4;
+
 template <uint32_t OP>
 __global__ __launch_bounds__(EXEC_NT) __attribute__((amdgpu_waves_per_eu(EXEC_WAVES_PER_CU / 4u))) void so_exec(
-    Side A, Side B, const ExecItem* __restrict__ xitems, const Totals* totals, uint64_t* __restrict__ out_bmp,
-    uint16_t* __restrict__ out_arr, uint16_t* __restrict__ out_run, uint32_t* __restrict__ item_card)
+    Side A, Side B, const ExecItem* __restrict__ xitems, uint32_t stride, uint32_t n_big_waves, const Totals* totals,
+    uint64_t* __restrict__ out_bmp, uint16_t* __restrict__ out_arr, uint16_t* __restrict__ out_run,
+    uint32_t* __restrict__ item_card)
 {
     __shared__ alignas(16) uint32_t lds[(EXEC_NT / 64) * EXEC_LDS_WORDS];
-    if (totals->overflow) return;  // the output was not allocated for this plan
     const uint32_t w = uni((blockIdx.x * EXEC_NT + threadIdx.x) >> 6);
-    if (w >= totals->c[C_ITEM]) return;
     const uint32_t lane = __lane_id();
-    const ExecItem it = load_xitem(xitems + w);
-    const Pre pa = preload(A, it.ma, it.aoff, lane), pb = preload(B, it.mb, it.boff, lane);
-    const uint32_t r =
-        run_item<OP>(A, B, it, pa, pb, lane, lds + (threadIdx.x >> 6) * EXEC_LDS_WORDS, out_bmp, out_arr, out_run);
-    if (lane == 0) item_card[it.pos] = r;
+    uint32_t* img = lds + (threadIdx.x >> 6) * EXEC_LDS_WORDS;
+    if (w < n_big_waves) {
+        const ExecItem it = load_xitem(xitems + min(w, stride - 1u));
+        const uint32_t n_big = totals->c[C_BB] + totals->c[C_MX] + totals->c[C_CB];
+        // (the output was not allocated for an overflowed plan)
+        if (totals->overflow || w >= n_big) return;
+        const Pre pa = preload(A, it.ma, it.aoff, lane), pb = preload(B, it.mb, it.boff, lane);
+        const uint32_t r = run_big<OP>(A, B, it, pa, pb, lane, img, out_bmp);
+        if (lane == 0) item_card[it.pos] = r;
+        return;
+    }
+    const uint32_t first = SMALL_PER_WAVE * (w - n_big_waves);
+    ExecItem it[SMALL_PER_WAVE];
+#pragma unroll
+    for (uint32_t k = 0; k < SMALL_PER_WAVE; ++k)
+        if (first + k < stride) it[k] = load_xitem(xitems + stride + first + k);
+    const uint32_t n_small = totals->c[C_ITEM] - (totals->c[C_BB] + totals->c[C_MX] + totals->c[C_CB]);
+    if (totals->overflow || first >= n_small) return;
+    const uint32_t cnt = min(SMALL_PER_WAVE, n_small - first);
+    Pre pa[SMALL_PER_WAVE], pb[SMALL_PER_WAVE];
+#pragma unroll
+    for (uint32_t k = 0; k < SMALL_PER_WAVE; ++k)
+        if (k < cnt) {
+            pa[k] = preload(A, it[k].ma, it[k].aoff, lane);
+            pb[k] = preload(B, it[k].mb, it[k].boff, lane);
+        }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): every preload is in
+#pragma unroll
+    for (uint32_t k = 0; k < SMALL_PER_WAVE; ++k)
+        if (k < cnt) {
+            const uint32_t r = run_small<OP>(A, B, it[k], pa[k], pb[k], lane, img, out_arr, out_run);
+            if (lane == 0) item_card[it[k].pos] = r;
+        }
 }
 
 // item_card: bit 31 = keep, bit 30 = an invalid item (the plan found a
@@ -1297,14 +1326,18 @@ static Caps setop_caps(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_
         run = pa + pb;
     }
     auto c32 = [](uint64_t x) { return static_cast<uint32_t>(std::min<uint64_t>(x, 0xFFFFFFFFull)); };
-    return Caps{bound, c32(std::min<uint64_t>(bmp, bound)), c32(arr), c32(run), 0u};
+    Caps caps{bound, c32(std::min<uint64_t>(bmp, bound)), c32(arr), c32(run), 0u};
+    // each item that writes array or run values takes at least one array or run container
+    caps.small = c32(std::min<uint64_t>(bound, aa + ra + ab + rb));
+    return caps;
 }
 
 // The plan (classify + assign) for `bound` work items into fresh scratch.
 struct SetOpPlan {
     Scratch sc;
     Item* items;
-    ExecItem* xitems = nullptr;  // so_plan_assign: the items in execution order
+    ExecItem* xitems = nullptr;  // so_plan_assign: bitmap-writing items, then (from `xstride`) the others
+    uint32_t xstride = 0;       // the plan's bound
     Totals* tot;
     uint32_t* icard;
     uint32_t n_tiles;
@@ -1320,7 +1353,7 @@ static int plan_set_operation(const Side& A, const Side& B, uint32_t op, uint32_
     const size_t o_recs = c.add(sizeof(KeyRec) * 65536);
     const size_t o_gc = c.add(sizeof(uint32_t) * PLAN_GROUPS * C_N);
     const size_t o_items = c.add(sizeof(Item) * bound);
-    const size_t o_xitems = c.add(sizeof(ExecItem) * bound);
+    const size_t o_xitems = c.add(sizeof(ExecItem) * 2u * bound);
     const size_t o_tot = c.add(sizeof(Totals));
     const size_t o_card = c.add(sizeof(uint32_t) * bound);
     CR_RET(P.sc.alloc(c.total, s));
@@ -1328,6 +1361,7 @@ static int plan_set_operation(const Side& A, const Side& B, uint32_t op, uint32_
     uint32_t* gc = P.sc.at<uint32_t>(o_gc);
     P.items = P.sc.at<Item>(o_items);
     P.xitems = P.sc.at<ExecItem>(o_xitems);
+    P.xstride = bound;  // = caps.items, where so_plan_assign starts the second kind
     P.tot = P.sc.at<Totals>(o_tot);
     P.icard = P.sc.at<uint32_t>(o_card);
     {
@@ -1374,7 +1408,8 @@ static int plan_bitmap_keyed(const cr_gpu_roaring* a, const cr_gpu_roaring* b, u
 
 // Execution and compaction of a plan into `out` (allocated for at most
 // `bound` items); `host` (optional) receives the totals.
-static int exec_set_operation(const Side& A, const Side& B, uint32_t op, uint32_t bound, bool only_bb,
+static int exec_set_operation(const Side& A, const Side& B, uint32_t op, uint32_t bound, uint32_t big_max,
+                              uint32_t small_max, bool only_bb,
                               const SetOpPlan& P, cr_gpu_roaring* out, SetOpHost* host, hipStream_t s)
 {
     if (only_bb) {
@@ -1402,24 +1437,26 @@ static int exec_set_operation(const Side& A, const Side& B, uint32_t op, uint32_
             break;
         }
     } else {
-        // one wave per item
-        const unsigned g = std::max(1u, (bound + 3u) / 4u);
+        // a wave per bitmap-writing item, then one per SMALL_PER_WAVE others
+        // (at most big_max and small_max of them: the plan flags more)
+        const uint32_t waves = big_max + (small_max + SMALL_PER_WAVE - 1u) / SMALL_PER_WAVE;
+        const unsigned g = std::max(1u, (waves + 3u) / 4u);
         CR_TIMED("so_exec", s);
         switch (op) {
         case CR_AND:
-            so_exec<CR_AND><<<g, EXEC_NT, 0, s>>>(A, B, P.xitems, P.tot, out->bitmap_data, out->array_data,
+            so_exec<CR_AND><<<g, EXEC_NT, 0, s>>>(A, B, P.xitems, P.xstride, big_max, P.tot, out->bitmap_data, out->array_data,
                                                   out->run_data, P.icard);
             break;
         case CR_OR:
-            so_exec<CR_OR><<<g, EXEC_NT, 0, s>>>(A, B, P.xitems, P.tot, out->bitmap_data, out->array_data,
+            so_exec<CR_OR><<<g, EXEC_NT, 0, s>>>(A, B, P.xitems, P.xstride, big_max, P.tot, out->bitmap_data, out->array_data,
                                                  out->run_data, P.icard);
             break;
         case CR_ANDNOT:
-            so_exec<CR_ANDNOT><<<g, EXEC_NT, 0, s>>>(A, B, P.xitems, P.tot, out->bitmap_data,
+            so_exec<CR_ANDNOT><<<g, EXEC_NT, 0, s>>>(A, B, P.xitems, P.xstride, big_max, P.tot, out->bitmap_data,
                                                      out->array_data, out->run_data, P.icard);
             break;
         default:
-            so_exec<CR_XOR><<<g, EXEC_NT, 0, s>>>(A, B, P.xitems, P.tot, out->bitmap_data, out->array_data,
+            so_exec<CR_XOR><<<g, EXEC_NT, 0, s>>>(A, B, P.xitems, P.xstride, big_max, P.tot, out->bitmap_data, out->array_data,
                                                   out->run_data, P.icard);
             break;
         }
@@ -1461,7 +1498,7 @@ static int set_operation_exact(const cr_gpu_roaring* a, const cr_gpu_roaring* b,
     Side As = A, Bs = B;
     As.kidx = Bs.kidx = nullptr;
     As.kidx_n = Bs.kidx_n = 0;
-    const Caps unbounded{bound, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0u, 0u, 0u, 0u};
+    const Caps unbounded{bound, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0u, 0u, 0u, 0u, 0xFFFFFFFFu};
     CR_RET(plan_set_operation(As, Bs, op, bound, unbounded, s, P));
     Totals h{};
     CR_RET(read_back(&h, P.tot, sizeof(Totals), s));
@@ -1478,7 +1515,7 @@ static int set_operation_exact(const cr_gpu_roaring* a, const cr_gpu_roaring* b,
     CR_RET(alloc_out(out, L, n_items, 0, n_bmp * 1024, arr_elems, run_u16, s));
     set_counts(out, h.c);
     const bool only_bb = h.c[C_BB] + h.c[C_CB] == n_items && aligned_bitmaps(a, b);
-    CR_RET(exec_set_operation(As, Bs, op, n_items, only_bb, P, out, nullptr, s));
+    CR_RET(exec_set_operation(As, Bs, op, n_items, n_items, n_items, only_bb, P, out, nullptr, s));
     uint32_t n_out = 0;
     CR_RET(read_back(&n_out, &P.tot->n_out, sizeof(uint32_t), s));
     out->n_containers = n_out;
@@ -1579,7 +1616,8 @@ int set_operation_impl(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_
         } else {
             CR_RET(plan_set_operation(A, B, op, bound, caps, s, P));
         }
-        CR_RET(exec_set_operation(A, B, op, bound, only_bb, P, out, hs.dev<SetOpHost>(), s));
+        CR_RET(exec_set_operation(A, B, op, bound, std::min(caps.bmp, bound), std::min(caps.small, bound), only_bb, P,
+                                  out, hs.dev<SetOpHost>(), s));
         CR_RET(sync_stream(s));
     }
     const volatile SetOpHost* h = hs.host<SetOpHost>();
