@@ -570,6 +570,23 @@ __device__ __forceinline__ Pre preload(const Side& S, uint32_t meta, uint32_t of
     return p;
 }
 
+// An array's values set as bits in the wave's image (LDS atomics; the first
+// 128 from the preload, then four loads a lane in flight).
+__device__ __forceinline__ void set_array(const uint16_t* vals, uint32_t n, const Pre& pre, uint32_t lane, uint32_t* img)
+{
+    if (pre.v0 != ~0u) atomicOr(&img[pre.v0 >> 5], 1u << (pre.v0 & 31u));
+    if (pre.v1 != ~0u) atomicOr(&img[pre.v1 >> 5], 1u << (pre.v1 & 31u));
+    for (uint32_t i0 = lane + 128u; i0 < n; i0 += 4u * 64u) {
+        uint32_t v[4];
+#pragma unroll
+        for (uint32_t k = 0; k < 4u; ++k) v[k] = i0 + 64u * k < n ? static_cast<uint32_t>(vals[i0 + 64u * k]) : ~0u;
+#pragma unroll
+        for (uint32_t k = 0; k < 4u; ++k)
+            if (v[k] != ~0u) atomicOr(&img[v[k] >> 5], 1u << (v[k] & 31u));
+    }
+    wave_lds_fence();
+}
+
 // A side that is not a bitmap, set in the wave's 8 KiB image.  An array's
 // values become bits (LDS atomics).  A run container's runs become toggles:
 // each run flips its first bit and the bit after its last (XOR: a run that
@@ -584,18 +601,7 @@ __device__ __forceinline__ bool build_image(const Side& S, uint32_t meta, uint32
     const uint32_t ty = meta >> 16, n = meta & 0xFFFFu;
     zero_image(img, lane);
     if (ty == CR_ARRAY) {
-        if (pre.v0 != ~0u) atomicOr(&img[pre.v0 >> 5], 1u << (pre.v0 & 31u));
-        if (pre.v1 != ~0u) atomicOr(&img[pre.v1 >> 5], 1u << (pre.v1 & 31u));
-        const uint16_t* vals = S.arr + (off >> 1);
-        for (uint32_t i0 = lane + 128u; i0 < n; i0 += 4u * 64u) {  // four loads a lane in flight
-            uint32_t v[4];
-#pragma unroll
-            for (uint32_t k = 0; k < 4u; ++k) v[k] = i0 + 64u * k < n ? static_cast<uint32_t>(vals[i0 + 64u * k]) : ~0u;
-#pragma unroll
-            for (uint32_t k = 0; k < 4u; ++k)
-                if (v[k] != ~0u) atomicOr(&img[v[k] >> 5], 1u << (v[k] & 31u));
-        }
-        wave_lds_fence();
+        set_array(S.arr + (off >> 1), n, pre, lane, img);
         return false;
     }
     if (ty != CR_RUN) return false;  // an empty image
@@ -682,6 +688,57 @@ __device__ __forceinline__ uint4 image_chunk(const uint32_t* img, uint32_t lane,
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// A run container of at most RUN_DIRECT runs, decoded in registers from the
+// preload (run r in lane r).  For each run, the lane's chunks strictly inside
+// it are all ones, and its first and last chunk take masks computed once for
+// the wave; chunk groups the run does not reach are skipped.  Any order or
+// overlap of the runs gives the reference's expansion (src/set_ops.cu:322-368),
+// ends past 0xFFFF clamped.
+constexpr uint32_t RUN_DIRECT = 4;
+
+__device__ __forceinline__ uint4 chunk_span(uint32_t lo, uint32_t hi)  // bits lo..hi of a chunk, lo <= hi < 128
+{
+    uint32_t w[4];
+#pragma unroll
+    for (uint32_t q = 0; q < 4u; ++q) {
+        const uint32_t wl = 32u * q, wh = wl + 31u;
+        w[q] = (lo <= wh && hi >= wl) ? bit_span(max(lo, wl) - wl, min(hi, wh) - wl) : 0u;
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__device__ __forceinline__ void run_direct(const Pre& pre, uint32_t n, uint32_t lane, uint4 (&c)[8])
+{
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j] = make_uint4(0, 0, 0, 0);
+    for (uint32_t r = 0; r < n; ++r) {
+        const uint32_t wd = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(pre.v0), r));
+        const uint32_t st = wd & 0xFFFFu, en = min(0xFFFFu, st + (wd >> 16));
+        const uint32_t cs = st >> 7, ce = en >> 7;  // its first and last chunk
+        const uint4 ms = chunk_span(st & 127u, cs == ce ? en & 127u : 127u);
+        const uint4 me = chunk_span(0u, en & 127u);
+#pragma unroll
+        for (uint32_t j = 0; j < 8u; ++j) {
+            if (ce < 64u * j || cs > 64u * j + 63u) continue;  // the run misses chunk group j
+            const uint32_t ch = lane + 64u * j;
+            const uint32_t f = (ch > cs && ch < ce) ? ~0u : 0u;
+            const uint4 e = ch == cs ? ms : (ch == ce ? me : make_uint4(0, 0, 0, 0));
+            c[j].x |= f | e.x, c[j].y |= f | e.y, c[j].z |= f | e.z, c[j].w |= f | e.w;
+        }
+    }
+}
+
+// A side's registers without an image: a bitmap's chunks loaded, or a short
+// run container decoded.
+__device__ __forceinline__ void held_side(const Side& S, uint32_t meta, uint32_t off, const Pre& pre, uint32_t lane,
+                                          uint4 (&c)[8])
+{
+    if ((meta >> 16) == CR_BITMAP)
+        bitmap_side(S.bmp, off, lane, c);
+    else
+        run_direct(pre, meta & 0xFFFFu, lane, c);
+}
+
 // Writes OP of the held chunks `x` (side A when X_IS_A) and the image's
 // chunks to the 8 KiB output slot; returns the lane's popcount.
 template <uint32_t OP, bool X_IS_A>
@@ -724,28 +781,32 @@ __device__ __forceinline__ uint32_t run_big(const Side& A, const Side& B, const 
     switch (it.cat) {
     case CAT_BB:
     case CAT_MIXED: {
-        // A bitmap side is held in registers (its loads in flight while the
-        // other side's image is built); with two images, A's chunks are read
-        // into registers before B's image replaces them.
+        // A bitmap side, or a run container of a few runs, is held in
+        // registers (a bitmap's loads in flight while the other side's image
+        // is built); an array or a longer run container goes through the
+        // wave's image.  With two images, A's chunks are read into registers
+        // before B's image replaces them.
         uint4* dst = reinterpret_cast<uint4*>(out_bmp + it.slot * 1024ull);  // 8 KiB slots: 16-byte aligned
         uint32_t pc = 0;
+        const bool ha = ta == CR_BITMAP || (ta == CR_RUN && (it.ma & 0xFFFFu) <= RUN_DIRECT);
+        const bool hb = tb == CR_BITMAP || (tb == CR_RUN && (it.mb & 0xFFFFu) <= RUN_DIRECT);
         uint4 x[8];
-        if (ta == CR_BITMAP && tb == CR_BITMAP) {
+        if (ha && hb) {
             uint4 y[8];
-            bitmap_side(A.bmp, it.aoff, lane, x);
-            bitmap_side(B.bmp, it.boff, lane, y);
+            held_side(A, it.ma, it.aoff, pa, lane, x);
+            held_side(B, it.mb, it.boff, pb, lane, y);
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const uint4 r = apply4<OP>(x[j], y[j]);
                 st_stream(dst + lane + 64u * j, r);
                 pc += popc4(r);
             }
-        } else if (ta == CR_BITMAP) {
-            bitmap_side(A.bmp, it.aoff, lane, x);
+        } else if (ha) {
+            held_side(A, it.ma, it.aoff, pa, lane, x);
             const bool tg = build_image(B, it.mb, it.boff, pb, lane, img);
             pc = store_with_image<OP, true>(x, img, tg, lane, dst);
-        } else if (tb == CR_BITMAP) {
-            bitmap_side(B.bmp, it.boff, lane, x);
+        } else if (hb) {
+            held_side(B, it.mb, it.boff, pb, lane, x);
             const bool tg = build_image(A, it.ma, it.aoff, pa, lane, img);
             pc = store_with_image<OP, false>(x, img, tg, lane, dst);
         } else {
@@ -825,9 +886,14 @@ __device__ __forceinline__ uint32_t run_small(const Side& A, const Side& B, cons
         // AND of two arrays: one side's values set in the wave's image, the
         // other side's probed against it in order and compacted with ballots
         // (the output is sorted).  The longer side goes into the image.
+        // The image is clear on entry (the wave clears it before its first
+        // item) and is cleared again on exit: the words this item set, or
+        // the whole image after more than 128 values.
         const uint32_t nx = it.ma & 0xFFFFu, ny = it.mb & 0xFFFFu;
         const bool img_a = nx > ny;
-        build_image(img_a ? A : B, img_a ? it.ma : it.mb, img_a ? it.aoff : it.boff, img_a ? pa : pb, lane, img);
+        const Pre pi = img_a ? pa : pb;
+        const uint32_t ni = img_a ? nx : ny;
+        set_array(img_a ? A.arr + (it.aoff >> 1) : B.arr + (it.boff >> 1), ni, pi, lane, img);
         const uint16_t* vals = img_a ? B.arr + (it.boff >> 1) : A.arr + (it.aoff >> 1);
         const Pre pv = img_a ? pb : pa;
         const uint32_t n = img_a ? ny : nx;
@@ -844,7 +910,14 @@ __device__ __forceinline__ uint32_t run_small(const Side& A, const Side& B, cons
             if (p) out[card + lanes_below(mask)] = static_cast<uint16_t>(v);
             card += static_cast<uint32_t>(__popcll(mask));
         }
-        wave_lds_fence();  // the probes are done before the next item's LDS writes
+        wave_lds_fence();  // the probes are done before the image is cleared
+        if (ni > 128u) {
+            zero_image(img, lane);
+        } else {
+            if (pi.v0 != ~0u) img[pi.v0 >> 5] = 0u;
+            if (pi.v1 != ~0u) img[pi.v1 >> 5] = 0u;
+            wave_lds_fence();
+        }
         keep = card != 0;
         break;
     }
@@ -927,6 +1000,7 @@ __global__ __launch_bounds__(EXEC_NT) __attribute__((amdgpu_waves_per_eu(EXEC_WA
             pa[k] = preload(A, it[k].ma, it[k].aoff, lane);
             pb[k] = preload(B, it[k].mb, it[k].boff, lane);
         }
+    zero_image(img, lane);  // array x array items keep it clear between them
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): every preload is in
 #pragma unroll
     for (uint32_t k = 0; k < SMALL_PER_WAVE; ++k)

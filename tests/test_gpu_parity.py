@@ -585,9 +585,12 @@ def _irregular_run_operands():
          4: run(*many),
          5: run((0, 0), (31, 1), (63, 64), (4095, 4097), (65535, 0)),
          6: run((7, 3)),                                    # one-sided
-         8: run((31, 0), (32, 31), (64, 63), (127, 128))}   # touching on word edges
+         8: run((31, 0), (32, 31), (64, 63), (127, 128)),   # touching on word edges
+         9: run((9000, 10), (100, 20), (50, 70), (3000, 5), (2990, 20), (65000, 900)),  # > 4, unordered
+         10: run(*[(i * 300, 299) for i in range(6)])}       # > 4, each touching the next
     b = {0: arr(300), 1: bmp(0.4), 2: run((90, 5), (96, 3)), 3: run((0, 65535)), 4: arr(4000),
-         5: run((40000, 100), (30000, 5000)), 7: run((1, 1)), 8: bmp(0.02)}
+         5: run((40000, 100), (30000, 5000)), 7: run((1, 1)), 8: bmp(0.02), 9: bmp(0.3),
+         10: run((5, 1), (1000, 2), (4000, 3), (7000, 4), (9000, 5), (20000, 6))}
     to_list = lambda d: [(k,) + d[k] for k in sorted(d)]
     return to_list(a), to_list(b)
 
