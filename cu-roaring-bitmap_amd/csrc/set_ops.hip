@@ -717,13 +717,21 @@ __device__ __forceinline__ void run_direct(const Pre& pre, uint32_t n, uint32_t 
         const uint32_t cs = st >> 7, ce = en >> 7;  // its first and last chunk
         const uint4 ms = chunk_span(st & 127u, cs == ce ? en & 127u : 127u);
         const uint4 me = chunk_span(0u, en & 127u);
+        const uint32_t js = cs >> 6, je = ce >> 6;  // the chunk groups of its ends
 #pragma unroll
         for (uint32_t j = 0; j < 8u; ++j) {
-            if (ce < 64u * j || cs > 64u * j + 63u) continue;  // the run misses chunk group j
+            if (j < js || j > je) continue;  // the run misses chunk group j
             const uint32_t ch = lane + 64u * j;
             const uint32_t f = (ch > cs && ch < ce) ? ~0u : 0u;
-            const uint4 e = ch == cs ? ms : (ch == ce ? me : make_uint4(0, 0, 0, 0));
-            c[j].x |= f | e.x, c[j].y |= f | e.y, c[j].z |= f | e.z, c[j].w |= f | e.w;
+            c[j].x |= f, c[j].y |= f, c[j].z |= f, c[j].w |= f;
+            if (j == js) {
+                const bool at = lane == (cs & 63u);
+                c[j].x |= at ? ms.x : 0u, c[j].y |= at ? ms.y : 0u, c[j].z |= at ? ms.z : 0u, c[j].w |= at ? ms.w : 0u;
+            }
+            if (j == je && ce != cs) {
+                const bool at = lane == (ce & 63u);
+                c[j].x |= at ? me.x : 0u, c[j].y |= at ? me.y : 0u, c[j].z |= at ? me.z : 0u, c[j].w |= at ? me.w : 0u;
+            }
         }
     }
 }
