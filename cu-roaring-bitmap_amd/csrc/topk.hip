@@ -178,6 +178,7 @@ struct TkArgs {
     uint32_t k;
     uint32_t n_chunks;  // multiple of 8
     uint32_t vec;       // rows are 16-B aligned with dim % 4 == 0
+    uint32_t qvec;      // so are the queries
     float* list_d;      // two planes of [n_chunks][n_q][k]: a merge reads one, writes the other
     uint32_t* list_id;  // the same two planes
     size_t plane;       // elements per plane
@@ -464,6 +465,34 @@ __device__ __forceinline__ void tk_store_rows(Lds& L, int buf, const float4 (&pr
     }
 }
 
+// This lane's query dimensions [h DP/2, h DP/2 + DP/2) into qreg (zeros past
+// dim or for a lane without a query): 16-byte loads when the queries allow
+// them, each a contiguous 16 bytes of the lane's row, else one float at a
+// time.  Returns the sum of their squares.
+template <int DP>
+__device__ __forceinline__ float tk_load_query(const TkArgs& a, bool qok, uint32_t q, uint32_t h, float (&qreg)[DP / 2])
+{
+    const float* src = a.queries + static_cast<size_t>(q) * a.dim + h * (DP / 2);
+    if (a.qvec) {
+#pragma unroll
+        for (int s = 0; s < DP / 2; s += 4) {
+            const uint32_t c = h * (DP / 2) + s;
+            const float4 v = (qok && c < a.dim) ? *reinterpret_cast<const float4*>(src + s) : make_float4(0.f, 0.f, 0.f, 0.f);
+            qreg[s] = v.x, qreg[s + 1] = v.y, qreg[s + 2] = v.z, qreg[s + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < DP / 2; ++s) {
+            const uint32_t c = h * (DP / 2) + s;
+            qreg[s] = (qok && c < a.dim) ? src[s] : 0.f;
+        }
+    }
+    float part = 0.f;
+#pragma unroll
+    for (int s = 0; s < DP / 2; ++s) part += qreg[s] * qreg[s];
+    return part;
+}
+
 // Base row held by accumulator register rr (0..31: block rr/16, register
 // rr%16) of the lane half hh.
 __device__ __forceinline__ int tk_row(int rr, int hh)
@@ -515,13 +544,7 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
 
     // B operand: this lane's query, dimensions [h*DP/2, h*DP/2 + DP/2).
     float qreg[DP / 2];
-    float qpart = 0.f;
-#pragma unroll
-    for (int s = 0; s < DP / 2; ++s) {
-        const uint32_t c = h * (DP / 2) + s;
-        qreg[s] = (qok && c < a.dim) ? a.queries[static_cast<size_t>(q0 + j) * a.dim + c] : 0.f;
-        qpart += qreg[s] * qreg[s];
-    }
+    const float qpart = tk_load_query<DP>(a, qok, q0 + j, h, qreg);
     const float qg = (1.f - TK_GATE_ERR) * (qpart + __shfl_xor(qpart, 32, 64));
 
     float4 pre[DP / 32];
@@ -813,33 +836,30 @@ __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t h = lane >> 5;
     const uint32_t j = lane & 31u;
+    // The workgroups of a query block take its tiles in turn: tile c, c + n_cw,
+    // ... (the grid is n_cw x n_qb, balanced however many rows there are).
     const uint32_t n_qb = (a.n_q + TK_QB - 1) / TK_QB;
+    const uint32_t n_cw = gridDim.x / n_qb;
     const uint32_t chunk = blockIdx.x / n_qb;
     const uint32_t qb = blockIdx.x % n_qb;
-    const uint64_t rpc = ((n_rows + a.n_chunks - 1) / a.n_chunks + TK_ROWS - 1) / TK_ROWS * TK_ROWS;
-    const uint64_t r0 = std::min<uint64_t>(n_rows, static_cast<uint64_t>(chunk) * rpc);
-    const uint64_t r1 = std::min<uint64_t>(n_rows, r0 + rpc);
-    const uint32_t n_tiles = static_cast<uint32_t>((r1 - r0 + TK_ROWS - 1) / TK_ROWS);
+    const uint64_t n_all = (n_rows + TK_ROWS - 1) / TK_ROWS;
+    const uint32_t n_tiles = chunk < n_all ? static_cast<uint32_t>((n_all - chunk + n_cw - 1) / n_cw) : 0u;
+    auto tile_r0 = [&](uint32_t i) { return (static_cast<uint64_t>(chunk) + static_cast<uint64_t>(i) * n_cw) * TK_ROWS; };
+    auto tile_r1 = [&](uint32_t i) { return std::min<uint64_t>(n_rows, tile_r0(i) + TK_ROWS); };
     const uint32_t q0 = qb * TK_QB + wave * TK_QW;
     const uint32_t nq_wave = q0 < a.n_q ? std::min<uint32_t>(TK_QW, a.n_q - q0) : 0u;
     const bool qok = j < nq_wave;
     float qreg[DP / 2];
-    float qpart = 0.f;
-#pragma unroll
-    for (int s = 0; s < DP / 2; ++s) {
-        const uint32_t c = h * (DP / 2) + s;
-        qreg[s] = (qok && c < a.dim) ? a.queries[static_cast<size_t>(q0 + j) * a.dim + c] : 0.f;
-        qpart += qreg[s] * qreg[s];
-    }
+    const float qpart = tk_load_query<DP>(a, qok, q0 + j, h, qreg);
     const float qg = (1.f - TK_GATE_ERR) * (qpart + __shfl_xor(qpart, 32, 64));
     if (chunk == 0 && h == 0 && qok) a.pq[q0 + j] = qg;
     float4 pre[DP / 32];
     uint32_t pid[DP / 32], nid[DP / 32];  // ids of the next tile, and of the one after it
     if (n_tiles > 0) {
-        tk_load_rows<DP>(a, r0, r1, pre, pid);
+        tk_load_rows<DP>(a, tile_r0(0), tile_r1(0), pre, pid);
         tk_store_rows<DP>(L, 0, pre, pid);
     }
-    tk_load_ids<DP>(a, r0 + TK_ROWS, r1, nid);
+    tk_load_ids<DP>(a, tile_r0(1), n_tiles > 1 ? tile_r1(1) : 0, nid);
     __syncthreads();
     float ulo = __builtin_inff(), uhi = -__builtin_inff();  // range of the upper bounds of this lane's rows
     for (uint32_t t = 0; t < n_tiles; ++t) {
@@ -848,7 +868,7 @@ __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
 #pragma unroll
             for (int p = 0; p < DP / 32; ++p) pid[p] = nid[p];
             tk_load_rows_of<DP>(a, pid, pre);
-            tk_load_ids<DP>(a, r0 + static_cast<uint64_t>(t + 2) * TK_ROWS, r1, nid);
+            tk_load_ids<DP>(a, tile_r0(t + 2), t + 2 < n_tiles ? tile_r1(t + 2) : 0, nid);
         }
         if (nq_wave > 0) {
             f32x16 acc0 = {}, acc1 = {};
@@ -869,8 +889,8 @@ __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
             }
             // Through LDS, so each store writes 64 consecutive rows of one query.
             float* E = L.est[wave];
-            const uint64_t tr0 = r0 + static_cast<uint64_t>(t) * TK_ROWS;
-            const int rows = static_cast<int>(std::min<uint64_t>(TK_ROWS, r1 - tr0));  // rows of this tile
+            const uint64_t tr0 = tile_r0(t);
+            const int rows = static_cast<int>(tile_r1(t) - tr0);  // rows of this tile
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row0 = tk_row(r, static_cast<int>(h)), row1 = tk_row(16 + r, static_cast<int>(h));
@@ -898,8 +918,8 @@ __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
             __builtin_amdgcn_wave_barrier();
         }
         if (qb == 0 && wave == 0) {
-            const uint64_t gr = r0 + static_cast<uint64_t>(t) * TK_ROWS + lane;
-            if (gr < r1) a.px[gr] = L.xg[b][lane];
+            const uint64_t gr = tile_r0(t) + lane;
+            if (gr < tile_r1(t)) a.px[gr] = L.xg[b][lane];
         }
         if (t + 1 < n_tiles) tk_store_rows<DP>(L, b ^ 1, pre, pid);
         __syncthreads();
@@ -1136,13 +1156,29 @@ __global__ __launch_bounds__(TK_SEL_NT) void tk_select(TkArgs a, float* out_d, i
     }
 }
 
+// The call's state in one launch: every query's bound (tau) and each chunk's
+// m_rank-th distance (tau_m) at +inf, and for the small-set path the range of
+// the upper bounds (qlo at the largest value, qhi at the smallest).
+__global__ __launch_bounds__(256) void tk_init(TkArgs a)
+{
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
+    if (i < static_cast<uint64_t>(a.n_chunks) * a.n_q) a.tau_m[i] = 0x7F800000u;
+    if (i < a.n_q) {
+        a.tau[i] = 0x7F800000u;
+        if (a.small_max) {
+            a.qlo[i] = 0xFFFFFFFFu;
+            a.qhi[i] = 0u;
+        }
+    }
+}
+
 template <int DP>
-int launch_dist(const TkArgs& a, uint32_t grid, hipStream_t s)
+int launch_dist(const TkArgs& a, uint32_t grid, uint32_t pairs_grid, hipStream_t s)
 {
     if (a.small_max) {  // estimates of a small set, or the seed rows of a larger one, and the seed bound
         {
             CR_TIMED("tk_pairs", s);
-            tk_pairs<DP><<<grid, TK_NT, 0, s>>>(a);
+            tk_pairs<DP><<<pairs_grid, TK_NT, 0, s>>>(a);
         }
         CR_LAUNCH_CHECK();
         {
@@ -1217,6 +1253,7 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     a.k = k;
     a.n_chunks = n_chunks;
     a.vec = (dim % 4 == 0) && (reinterpret_cast<uintptr_t>(d_base) % 16 == 0);
+    a.qvec = (dim % 4 == 0) && (reinterpret_cast<uintptr_t>(d_queries) % 16 == 0);
     a.list_d = sc.at<float>(o_ld);
     a.list_id = sc.at<uint32_t>(o_li);
     a.list_n = sc.at<uint32_t>(o_ln);
@@ -1230,12 +1267,8 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     a.px = small_max ? sc.at<float>(o_px) : nullptr;
     a.qlo = small_max ? sc.at<uint32_t>(o_qlo) : nullptr;
     a.qhi = small_max ? sc.at<uint32_t>(o_qhi) : nullptr;
-    if (small_max) {
-        CR_RET(fill_u32(a.qlo, 0xFFFFFFFFu, n_q, s));
-        CR_RET(fill_u32(a.qhi, 0u, n_q, s));
-    }
-    CR_RET(fill_u32(a.tau, 0x7F800000u, n_q, s));  // +inf
-    CR_RET(fill_u32(a.tau_m, 0x7F800000u, static_cast<uint64_t>(n_chunks) * n_q, s));
+    tk_init<<<static_cast<unsigned>((static_cast<uint64_t>(n_chunks) * n_q + 255) / 256), 256, 0, s>>>(a);
+    CR_LAUNCH_CHECK();
     if (filter) {
         cr_gpu_roaring_view cv_view;
         CR_RET(cr_make_view(filter, &cv_view));
@@ -1255,12 +1288,15 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
         CR_LAUNCH_CHECK();
     }
     const uint32_t grid = n_chunks * n_qb;
+    // tk_pairs: one workgroup a CU (two waves a SIMD fill it), each query
+    // block's tiles dealt out among its workgroups
+    const uint32_t pairs_grid = std::max<uint32_t>(1, (cus + n_qb - 1) / n_qb) * n_qb;
     if (dim <= 32) {
-        CR_RET(launch_dist<32>(a, grid, s));
+        CR_RET(launch_dist<32>(a, grid, pairs_grid, s));
     } else if (dim <= 64) {
-        CR_RET(launch_dist<64>(a, grid, s));
+        CR_RET(launch_dist<64>(a, grid, pairs_grid, s));
     } else {
-        CR_RET(launch_dist<128>(a, grid, s));
+        CR_RET(launch_dist<128>(a, grid, pairs_grid, s));
     }
     {
         CR_TIMED("tk_merge", s);
