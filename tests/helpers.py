@@ -98,6 +98,26 @@ def assert_same(got, want, strict: bool = False, what: str = ""):
 
 
 # ---- reference-test input generators (std::mt19937 based) ---------------
+def assert_packed_offsets(h, what: str = ""):
+    """The packed layout's offsets, checked against what the layout itself fixes:
+    containers go into their type's pool in key order, back to back, so each
+    offset is the sum of the sizes of the earlier containers of its type --
+    8192 bytes a bitmap, 2 bytes a value of an array, 4 bytes a run
+    (src/upload.cpp:89-287) -- and each pool holds exactly its containers."""
+    n = h.n_containers
+    types, cards, offs = np.asarray(h.types[:n]), np.asarray(h.cards[:n]).astype(np.int64), np.asarray(h.offsets[:n])
+    keys = np.asarray(h.keys[:n]).astype(np.int64)
+    assert np.all(np.diff(keys) > 0), f"{what}: keys not ascending"
+    size = np.where(types == 1, 8192, np.where(types == 0, 2 * cards, 4 * cards))
+    for ty, pool in ((1, "bitmap"), (0, "array"), (2, "run")):
+        m = types == ty
+        want = np.concatenate([[0], np.cumsum(size[m])[:-1]]) if m.any() else np.zeros(0, np.int64)
+        assert np.array_equal(offs[m].astype(np.int64), want), f"{what}: {pool} offsets are not the prefix sums"
+    assert 8192 * int((types == 1).sum()) == 8192 * h.n_bitmap_containers
+    assert int(size[types == 0].sum()) == h.array_pool_bytes, f"{what}: array pool size"
+    assert int(size[types == 2].sum()) == h.run_pool_bytes, f"{what}: run pool size"
+
+
 def mt_bernoulli(seed: int, density: float, universe: int) -> np.ndarray:
     """ids i < universe with uniform_real_distribution<double>(0,1)(mt19937(seed)) < density."""
     return orc.mt_bernoulli_ids(seed, density, universe)

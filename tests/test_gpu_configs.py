@@ -21,7 +21,7 @@ import pytest
 
 import bench
 import orc
-from helpers import assert_same
+from helpers import assert_packed_offsets, assert_same
 
 pytestmark = pytest.mark.gpu
 
@@ -83,7 +83,9 @@ def operands(gpu, torch):
             lite.run_optimize()
         g = bench.keep_upload(gpu, lite)
         want = orc.upload_packed(lite, None, orc.PROMOTE_KEEP_DEFAULT)
-        assert_same(gpu.download(g), want, strict=True, what=f"operand {name}")
+        got = gpu.download(g)
+        assert_same(got, want, strict=True, what=f"operand {name}")
+        assert_packed_offsets(got, what=f"operand {name}")
         out[name] = (want, g)
     types = {k: (v[1].n_array_containers, v[1].n_bitmap_containers, v[1].n_run_containers) for k, v in out.items()}
     assert types["A"][0] > 0 and types["B"][1] > 0 and types["C"][2] > 0, types
@@ -180,10 +182,65 @@ def topk_data(gpu, torch):
             gpu.free(f)
 
 
+def _torch_topk_fp64(torch, base, queries, k, passing):
+    """Every query's k smallest squared L2 distances over the passing rows, in
+    fp64 by torch on the device (an fp64 GEMM per 1M-row chunk,
+    |q|^2 + |x|^2 - 2 q.x, then a top-k per chunk and one over the chunks'
+    candidates): (distances, ids), ascending."""
+    q64 = queries.to(torch.float64)
+    qn = (q64 * q64).sum(dim=1, keepdim=True)
+    cand_d, cand_i = [], []
+    step = 1 << 20
+    for r0 in range(0, base.shape[0], step):
+        x = base[r0:r0 + step].to(torch.float64)
+        d = qn + (x * x).sum(dim=1)[None, :] - 2.0 * (q64 @ x.T)
+        if passing is not None:
+            d.masked_fill_(~passing[r0:r0 + step][None, :], float("inf"))
+        kk = min(k, d.shape[1])
+        v, i = torch.topk(d, kk, dim=1, largest=False)
+        cand_d.append(v)
+        cand_i.append(i + r0)
+        del x, d
+    d = torch.cat(cand_d, dim=1)
+    i = torch.cat(cand_i, dim=1)
+    v, j = torch.topk(d, k, dim=1, largest=False)
+    return v, torch.gather(i, 1, j)
+
+
+def _check_all_queries(torch, base, queries, k, passing, got_d, got_i):
+    """All queries against the fp64 device reference: padding past the passing
+    count, ids in range, unique and inside the filter, distances within 1e-4
+    relative of their exact fp64 values and ascending, and every id that differs
+    from the reference's a tie at the k-th distance (the unit tests' rule)."""
+    from test_gpu_topk import RTOL
+    n_pass = base.shape[0] if passing is None else int(passing.sum().item())
+    valid = min(k, n_pass)
+    assert bool((got_i[:, valid:] == -1).all()) and bool(torch.isinf(got_d[:, valid:]).all())
+    gi, gd = got_i[:, :valid], got_d[:, :valid].to(torch.float64)
+    assert bool(((gi >= 0) & (gi < base.shape[0])).all())
+    srt = torch.sort(gi, dim=1).values
+    assert bool((srt[:, 1:] != srt[:, :-1]).all()), "duplicate ids"
+    if passing is not None:
+        assert bool(passing[gi].all()), "an id outside the filter"
+    exact = ((base[gi].to(torch.float64) - queries[:, None, :].to(torch.float64)) ** 2).sum(dim=2)
+    assert bool(((gd - exact).abs() <= RTOL * exact.abs()).all()), "a distance off by more than 1e-4 relative"
+    assert bool((gd[:, 1:] >= gd[:, :-1]).all()), "not ascending"
+    want_d, want_i = _torch_topk_fp64(torch, base, queries, valid, passing)
+    kth = want_d[:, -1:]
+    # an id the kernel returned that the reference did not, or the reverse, must tie at the k-th distance
+    in_want = (gi[:, :, None] == want_i[:, None, :]).any(dim=2)
+    in_got = (want_i[:, :, None] == gi[:, None, :]).any(dim=2)
+    tol = RTOL * kth.abs().clamp_min(1e-30)
+    assert bool(((exact - kth).abs()[~in_want] <= tol.expand_as(exact)[~in_want]).all()), "an extra id is not a tie"
+    assert bool(((want_d - kth).abs()[~in_got] <= tol.expand_as(want_d)[~in_got]).all()), "a missing id is not a tie"
+
+
 @pytest.mark.parametrize("k", [10, 100])
 @pytest.mark.parametrize("sel", ["unfiltered", "sel_0.001", "sel_0.01", "sel_0.1", "sel_0.5"])
 def test_config4_topk_full_size(gpu, torch, topk_data, k, sel):
-    """All 1024 queries run; 8 of them (spread over the batch) are checked."""
+    """All 1024 queries run and all are checked against an fp64 top-k that torch
+    computes on the device; 8 of them (spread over the batch) also against the
+    oracle's fp64 brute force."""
     from test_gpu_topk import check_topk
     _say("configs[4] top-k", k, sel)
     base, queries, hbase, filters = topk_data
@@ -192,6 +249,8 @@ def test_config4_topk_full_size(gpu, torch, topk_data, k, sel):
     ids = torch.empty((bench.TK_Q, k), device="cuda", dtype=torch.int64)
     gpu.topk_filtered(base, queries, k, f, dist, ids)
     torch.cuda.synchronize()
+    dev_pass = None if passing is None else torch.from_numpy(passing.astype(bool)).cuda()
+    _check_all_queries(torch, base, queries, k, dev_pass, dist, ids)
     sample = np.array([0, 129, 258, 387, 516, 645, 774, 1023])
     hq = queries.cpu().numpy()[sample]
     check_topk(hbase, hq, k, passing, dist.cpu().numpy()[sample], ids.cpu().numpy()[sample])

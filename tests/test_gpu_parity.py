@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import orc
-from helpers import assert_same, flat_from_ids, mt_bernoulli, mt_mod_filter, words_mask, auto_l2
+from helpers import assert_packed_offsets, assert_same, flat_from_ids, mt_bernoulli, mt_mod_filter, words_mask, auto_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -387,7 +387,9 @@ def test_upload_containers_parity(gpu, name, thr, with_u):
     else:
         src, comp = lite, False
     g = gpu.upload_containers(src.containers(), U if with_u else 0, comp, lite.cardinality(), thr)
-    assert_same(gpu.download(g), want, strict=True, what="upload_containers")
+    got = gpu.download(g)
+    assert_same(got, want, strict=True, what="upload_containers")
+    assert_packed_offsets(got, what="upload_containers")
     gpu.free(g)
 
 

@@ -495,3 +495,45 @@ def test_deep_copy_and_promote_auto():
     big = orc.upload_packed(orc.Lite.from_sorted_ids(ids), 1 << 30, orc.PROMOTE_KEEP_DEFAULT)
     p = orc.promote_auto(big)
     assert p.n_array_containers == 0 and p.n_bitmap_containers == p.n_containers
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_packed_upload_offsets_are_prefix_sums(seed):
+    """The oracle's packed layout (src/upload.cpp:89-287) against what the layout
+    itself fixes: each type's pool holds its containers in key order, back to
+    back (helpers.assert_packed_offsets), for random mixes of array, bitmap and
+    run containers, thresholds and complements; and the decoded set is the input's."""
+    from helpers import assert_packed_offsets
+    rng = np.random.default_rng(500 + seed)
+    parts = []
+    for key in range(int(rng.integers(1, 40))):
+        base = int(rng.integers(0, 4096)) * 65536
+        kind = int(rng.integers(0, 3))
+        if kind == 0:
+            parts.append(base + np.unique(rng.integers(0, 65536, int(rng.integers(1, 4000)))))
+        elif kind == 1:
+            parts.append(base + np.nonzero(rng.random(65536) < rng.uniform(0.1, 0.9))[0])
+        else:
+            s = int(rng.integers(0, 60000))
+            parts.append(base + np.arange(s, s + int(rng.integers(1, 5000))))
+    ids = np.unique(np.concatenate(parts)).astype(np.uint32)
+    lite = orc.Lite.from_sorted_ids(ids).run_optimize()
+    for thr in (orc.PROMOTE_KEEP_DEFAULT, orc.PROMOTE_ALL, 100):
+        h = orc.upload_packed(lite, None, thr)
+        assert_packed_offsets(h, what=f"seed {seed} thr {thr}")
+        assert np.array_equal(orc.enumerate_ids(h), ids.astype(np.int64))
+    U = int(ids.max()) + 1
+    h = orc.upload_packed(lite, U, orc.PROMOTE_KEEP_DEFAULT)  # the complement when more than U/2
+    assert_packed_offsets(h, what=f"seed {seed} with U")
+    stored = orc.enumerate_ids(h)
+    if h.negated:
+        stored = np.setdiff1d(np.arange(U, dtype=np.int64), stored)
+    assert np.array_equal(stored, ids.astype(np.int64))
+    # a dense set: stored as its complement, whose pools obey the same rule
+    U2 = 3 * 65536 + 777 + seed
+    dense = np.setdiff1d(np.arange(U2), rng.integers(0, U2, 20000)).astype(np.uint32)
+    h = orc.upload_packed(orc.Lite.from_sorted_ids(dense).run_optimize(), U2, orc.PROMOTE_KEEP_DEFAULT)
+    assert h.negated
+    assert_packed_offsets(h, what=f"seed {seed} complement")
+    stored = np.setdiff1d(np.arange(U2, dtype=np.int64), orc.enumerate_ids(h))
+    assert np.array_equal(stored, dense.astype(np.int64))
