@@ -190,7 +190,7 @@ struct TkArgs {
     // estimate (pd[q][row], lower bounds of the fp32 distances) with the scaled
     // norms (pq[q], px[row]), and tk_select picks each query's k from them.
     uint32_t small_max;  // 0: never
-    float* pd;           // [n_q][small_max]
+    float* pd;           // [n_qb * TK_QB][small_max] (rows past n_q unused)
     float* pq;           // [n_q]
     float* px;           // [small_max]
     uint32_t* qlo;       // [n_q] order-preserving bits of the smallest upper bound of the query's rows
@@ -405,39 +405,53 @@ __device__ __forceinline__ void tk_load_rows(const TkArgs& a, uint64_t row0, uin
     }
 }
 
-// The ids of a tile's rows (the passing-id list, or the row numbers), one per
-// (thread, pass) as tk_load_rows assigns them: loaded a tile earlier, so the
-// dependent row loads do not wait for them.
-template <int DP>
-__device__ __forceinline__ void tk_load_ids(const TkArgs& a, uint64_t row0, uint64_t row_end, uint32_t (&pid)[DP / 32])
+// The prefetch of a persistent loop, without branches or selects on loaded
+// values (either makes the compiler wait for the loads where they are issued):
+// the raw ids of a tile's rows, sel[min(r, last)] (or r without a filter),
+// loaded a tile ahead of their use; tk_ids_valid then marks the rows past the
+// tile as TK_NOID, and tk_load_rows_nb loads a row for every id (row 0 stands
+// in for TK_NOID; tk_store_rows stores zeros for it).
+template <int DP, bool SEL>
+__device__ __forceinline__ void tk_ids_raw(const TkArgs& a, uint64_t row0, uint64_t last, uint32_t (&raw)[DP / 32])
 {
     constexpr int TPR = DP / 4;
     constexpr int RPP = TK_NT / TPR;
 #pragma unroll
     for (int p = 0; p < DP / 32; ++p) {
         const uint64_t r = row0 + static_cast<uint64_t>(p * RPP + threadIdx.x / TPR);
-        pid[p] = r < row_end ? (a.sel ? a.sel[r] : static_cast<uint32_t>(r)) : TK_NOID;
+        raw[p] = SEL ? a.sel[std::min<uint64_t>(r, last)] : static_cast<uint32_t>(r);
     }
 }
 
 template <int DP>
-__device__ __forceinline__ void tk_load_rows_of(const TkArgs& a, const uint32_t (&pid)[DP / 32], float4 (&pre)[DP / 32])
+__device__ __forceinline__ void tk_ids_valid(uint64_t row0, uint64_t row_end, uint32_t (&pid)[DP / 32])
+{
+    constexpr int TPR = DP / 4;
+    constexpr int RPP = TK_NT / TPR;
+#pragma unroll
+    for (int p = 0; p < DP / 32; ++p) {
+        const uint64_t r = row0 + static_cast<uint64_t>(p * RPP + threadIdx.x / TPR);
+        if (r >= row_end) pid[p] = TK_NOID;
+    }
+}
+
+template <int DP>
+__device__ __forceinline__ void tk_load_rows_nb(const TkArgs& a, const uint32_t (&pid)[DP / 32], float4 (&pre)[DP / 32])
 {
     constexpr int TPR = DP / 4;
     const uint32_t c = (threadIdx.x % TPR) * 4;
 #pragma unroll
     for (int p = 0; p < DP / 32; ++p) {
+        const uint32_t id = pid[p] != TK_NOID ? pid[p] : 0u;
+        const float* src = a.base + static_cast<size_t>(id) * a.dim;
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (pid[p] != TK_NOID) {
-            const float* src = a.base + static_cast<size_t>(pid[p]) * a.dim;
-            if (a.vec) {
-                if (c < a.dim) v = *reinterpret_cast<const float4*>(src + c);
-            } else {
-                if (c + 0 < a.dim) v.x = src[c + 0];
-                if (c + 1 < a.dim) v.y = src[c + 1];
-                if (c + 2 < a.dim) v.z = src[c + 2];
-                if (c + 3 < a.dim) v.w = src[c + 3];
-            }
+        if (a.vec) {
+            if (c < a.dim) v = *reinterpret_cast<const float4*>(src + c);
+        } else {
+            if (c + 0 < a.dim) v.x = src[c + 0];
+            if (c + 1 < a.dim) v.y = src[c + 1];
+            if (c + 2 < a.dim) v.z = src[c + 2];
+            if (c + 3 < a.dim) v.w = src[c + 3];
         }
         pre[p] = v;
     }
@@ -454,8 +468,9 @@ __device__ __forceinline__ void tk_store_rows(Lds& L, int buf, const float4 (&pr
     for (int p = 0; p < DP / 32; ++p) {
         const int row = p * RPP + static_cast<int>(t / TPR);
         const int c = static_cast<int>(t % TPR) * 4;
-        *reinterpret_cast<float4*>(&L.tile[buf][row * (DP + 4) + c]) = pre[p];
-        float ss = pre[p].x * pre[p].x + pre[p].y * pre[p].y + pre[p].z * pre[p].z + pre[p].w * pre[p].w;
+        const float4 v = pid[p] != TK_NOID ? pre[p] : make_float4(0.f, 0.f, 0.f, 0.f);
+        *reinterpret_cast<float4*>(&L.tile[buf][row * (DP + 4) + c]) = v;
+        float ss = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
 #pragma unroll
         for (int o = TPR / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
         if (c == 0) {
@@ -816,15 +831,28 @@ __global__ __launch_bounds__(TK_MERGE_NT) void tk_merge(TkArgs a, const float* l
 // queries -- (1 - TK_GATE_ERR)(|q|^2 + |x|^2) - 2 q.x, at most the fp32
 // distance -- to pd[q][row], the scaled query norms to pq (chunk 0) and the
 // scaled row norms to px (query block 0).
+// Rows whose upper bounds set the first bound: a larger sample costs reads, a
+// smaller one admits about k * rows / sample candidates, each a gathered row.
+constexpr uint32_t TK_SEL_SAMPLE = 16384;
+constexpr uint32_t TK_SEL_SAMPLE_PER_K = 1024;
+// The upper bounds' range matters only over the rows a histogram reads: the
+// selection's sample, which includes every seed row (at most 256 k of them).
+__device__ __forceinline__ uint64_t tk_hist_rows(const TkArgs& a)
+{
+    return max(TK_SEL_SAMPLE, TK_SEL_SAMPLE_PER_K * a.k);
+}
+
+constexpr int TK_ES = TK_ROWS + 4;  // estimate staging: a query's 64 rows, 16-byte aligned
+
 template <int DP>
 struct TkPairsLds {
     float tile[2][TK_ROWS * (DP + 4)];
     float xg[2][TK_ROWS];
     uint32_t id[2][TK_ROWS];
-    float est[TK_WAVES][TK_QW * (TK_ROWS + 1)];  // a wave's 32 x 64 estimates, rows padded by one
+    float est[TK_WAVES][TK_QW * TK_ES];  // a wave's 32 x 64 estimates
 };
 
-template <int DP>
+template <int DP, bool SEL>
 __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
 {
     // Every row of a small set, or the seed rows of a larger one.
@@ -847,6 +875,7 @@ __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
     auto tile_r0 = [&](uint32_t i) { return (static_cast<uint64_t>(chunk) + static_cast<uint64_t>(i) * n_cw) * TK_ROWS; };
     auto tile_r1 = [&](uint32_t i) { return std::min<uint64_t>(n_rows, tile_r0(i) + TK_ROWS); };
     const uint32_t q0 = qb * TK_QB + wave * TK_QW;
+    const uint32_t uq0 = __builtin_amdgcn_readfirstlane(q0);  // the same, known to be wave-uniform
     const uint32_t nq_wave = q0 < a.n_q ? std::min<uint32_t>(TK_QW, a.n_q - q0) : 0u;
     const bool qok = j < nq_wave;
     float qreg[DP / 2];
@@ -854,22 +883,27 @@ __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
     const float qg = (1.f - TK_GATE_ERR) * (qpart + __shfl_xor(qpart, 32, 64));
     if (chunk == 0 && h == 0 && qok) a.pq[q0 + j] = qg;
     float4 pre[DP / 32];
-    uint32_t pid[DP / 32], nid[DP / 32];  // ids of the next tile, and of the one after it
+    uint32_t pid[DP / 32], nid[DP / 32];  // ids of the next tile, and (raw) of the one after it
+    const uint64_t last = n_rows - 1;
+    // A tile's loads are all issued before the previous tile's MFMA and
+    // waited for after it: the rows of tile t + 1 (their ids known since
+    // tile t - 1) and the ids of tile t + 2.  Every iteration prefetches (a tile
+    // past the last has no valid rows and is never read), so no branch skips
+    // a load and the one wait of an iteration comes after its MFMA.
+    tk_ids_raw<DP, SEL>(a, tile_r0(1), last, nid);
     if (n_tiles > 0) {
         tk_load_rows<DP>(a, tile_r0(0), tile_r1(0), pre, pid);
         tk_store_rows<DP>(L, 0, pre, pid);
     }
-    tk_load_ids<DP>(a, tile_r0(1), n_tiles > 1 ? tile_r1(1) : 0, nid);
+#pragma unroll
+    for (int p = 0; p < DP / 32; ++p) pid[p] = nid[p];
+    tk_ids_valid<DP>(tile_r0(1), tile_r1(1), pid);
     __syncthreads();
     float ulo = __builtin_inff(), uhi = -__builtin_inff();  // range of the upper bounds of this lane's rows
     for (uint32_t t = 0; t < n_tiles; ++t) {
         const int b = static_cast<int>(t & 1u);
-        if (t + 1 < n_tiles) {
-#pragma unroll
-            for (int p = 0; p < DP / 32; ++p) pid[p] = nid[p];
-            tk_load_rows_of<DP>(a, pid, pre);
-            tk_load_ids<DP>(a, tile_r0(t + 2), t + 2 < n_tiles ? tile_r1(t + 2) : 0, nid);
-        }
+        tk_load_rows_nb<DP>(a, pid, pre);
+        tk_ids_raw<DP, SEL>(a, tile_r0(t + 2), last, nid);
         if (nq_wave > 0) {
             f32x16 acc0 = {}, acc1 = {};
             const float* A0 = &L.tile[b][j * (DP + 4) + h * (DP / 2)];
@@ -887,41 +921,62 @@ __global__ __launch_bounds__(TK_NT) void tk_pairs(TkArgs a)
                 acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.w, qreg[s + 3], acc0, 0, 0, 0);
                 acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.w, qreg[s + 3], acc1, 0, 0, 0);
             }
-            // Through LDS, so each store writes 64 consecutive rows of one query.
+            // Through LDS, so each store writes 64 consecutive rows of four
+            // queries.  Accumulator registers 4m .. 4m + 3 of a block hold four
+            // consecutive rows (tk_row), one 16-byte LDS access.
             float* E = L.est[wave];
-            const uint64_t tr0 = tile_r0(t);
-            const int rows = static_cast<int>(tile_r1(t) - tr0);  // rows of this tile
+            const int rows = static_cast<int>(tile_r1(t) - tile_r0(t));  // rows of this tile
+            const bool track = tile_r0(t) < tk_hist_rows(a);  // uniform
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row0 = tk_row(r, static_cast<int>(h)), row1 = tk_row(16 + r, static_cast<int>(h));
-                const float xg0 = L.xg[b][row0], xg1 = L.xg[b][row1];
-                const float e0 = qg + xg0 - 2.f * acc0[r], e1 = qg + xg1 - 2.f * acc1[r];
-                E[j * (TK_ROWS + 1) + row0] = e0;
-                E[j * (TK_ROWS + 1) + row1] = e1;
-                if (row0 < rows) {
-                    const float u = tk_upper(e0, qg, xg0);
-                    ulo = fminf(ulo, u);
-                    uhi = fmaxf(uhi, u);
-                }
-                if (row1 < rows) {
-                    const float u = tk_upper(e1, qg, xg1);
-                    ulo = fminf(ulo, u);
-                    uhi = fmaxf(uhi, u);
+            for (int m = 0; m < 4; ++m) {
+                const int ra = tk_row(4 * m, static_cast<int>(h)), rb = tk_row(16 + 4 * m, static_cast<int>(h));
+                const float4 ga = *reinterpret_cast<const float4*>(&L.xg[b][ra]);
+                const float4 gb = *reinterpret_cast<const float4*>(&L.xg[b][rb]);
+                const float4 ea = make_float4(qg + ga.x - 2.f * acc0[4 * m + 0], qg + ga.y - 2.f * acc0[4 * m + 1],
+                                              qg + ga.z - 2.f * acc0[4 * m + 2], qg + ga.w - 2.f * acc0[4 * m + 3]);
+                const float4 eb = make_float4(qg + gb.x - 2.f * acc1[4 * m + 0], qg + gb.y - 2.f * acc1[4 * m + 1],
+                                              qg + gb.z - 2.f * acc1[4 * m + 2], qg + gb.w - 2.f * acc1[4 * m + 3]);
+                *reinterpret_cast<float4*>(&E[j * TK_ES + ra]) = ea;
+                *reinterpret_cast<float4*>(&E[j * TK_ES + rb]) = eb;
+                if (track) {
+                    const float e8[8] = {ea.x, ea.y, ea.z, ea.w, eb.x, eb.y, eb.z, eb.w};
+                    const float g8[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) {
+                        const bool in = (c < 4 ? ra : rb - 4) + c < rows;  // a row of the tile
+                        const float u = tk_upper(e8[c], qg, g8[c]);
+                        ulo = fminf(ulo, in ? u : __builtin_inff());
+                        uhi = fmaxf(uhi, in ? u : -__builtin_inff());
+                    }
                 }
             }
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            if (static_cast<int>(lane) < rows) {
-                float* dst = a.pd + static_cast<size_t>(q0) * a.small_max + tr0 + lane;
-                for (uint32_t qq = 0; qq < nq_wave; ++qq, dst += a.small_max) *dst = E[qq * (TK_ROWS + 1) + lane];
+        }
+        // Tile t + 1 into the other buffer, and tile t + 2's valid ids.
+        tk_store_rows<DP>(L, b ^ 1, pre, pid);
+#pragma unroll
+        for (int p = 0; p < DP / 32; ++p) pid[p] = nid[p];
+        tk_ids_valid<DP>(tile_r0(t + 2), tile_r1(t + 2), pid);
+        // Every wave stores all 32 of its queries' rows and every lane its row
+        // (the estimate rows are allocated for whole query blocks and whole
+        // tiles; a query past n_q, or a row past the tile's last, receives a
+        // value nothing reads), after the iteration's wait: nothing waits for
+        // these stores before the next tile's MFMA has run.
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        {
+            // lane l stores rows 4 (l % 16) .. + 3 of query 4 i + l / 16
+            const float* E = L.est[wave];
+            const uint32_t ql = lane >> 4, cl = 4u * (lane & 15u);
+            float* dst = a.pd + static_cast<size_t>(uq0) * a.small_max + tile_r0(t);  // uniform
+#pragma unroll
+            for (uint32_t i = 0; i < TK_QW / 4; ++i) {
+                const float4 v = *reinterpret_cast<const float4*>(&E[(4u * i + ql) * TK_ES + cl]);
+                *reinterpret_cast<float4*>(dst + static_cast<size_t>(4u * i + ql) * a.small_max + cl) = v;
             }
-            __builtin_amdgcn_wave_barrier();
+            // the scaled norms, from every wave (the same values)
+            a.px[tile_r0(t) + lane] = L.xg[b][lane];
         }
-        if (qb == 0 && wave == 0) {
-            const uint64_t gr = tile_r0(t) + lane;
-            if (gr < tile_r1(t)) a.px[gr] = L.xg[b][lane];
-        }
-        if (t + 1 < n_tiles) tk_store_rows<DP>(L, b ^ 1, pre, pid);
+        __builtin_amdgcn_wave_barrier();
         __syncthreads();
     }
     ulo = fminf(ulo, __shfl_xor(ulo, 32, 64));
@@ -944,10 +999,6 @@ constexpr int TK_SEL_NT = 1024;
 constexpr uint32_t TK_SEL_BINS = TK_SEL_NT;  // one histogram bin per thread
 constexpr uint32_t TK_SEL_CB = 8192;         // candidates per batch
 constexpr uint32_t TK_SEL_RPT = 4;           // rows per thread per candidate chunk
-// Rows whose upper bounds set the first bound: a larger sample costs reads, a
-// smaller one admits about k * rows / sample candidates, each a gathered row.
-constexpr uint32_t TK_SEL_SAMPLE = 16384;
-constexpr uint32_t TK_SEL_SAMPLE_PER_K = 1024;
 // Process-wide limit of the small-set path (cr_topk_set_small_limit).
 std::atomic<uint32_t> g_topk_small{TK_SMALL};
 
@@ -969,13 +1020,24 @@ __device__ __forceinline__ float tk_hist_bound(const TkArgs& a, uint32_t q, cons
     bmax[t] = 0;
     if (t == 0) s_bound = 0;
     __syncthreads();
-    for (uint32_t r0 = t; r0 < Sn; r0 += 8 * TK_SEL_NT) {  // eight rows' loads in flight
-        float l8[8], x8[8];
+    // Eight rows a thread per step, the next step's loads issued before this
+    // step's are binned (clamped to the last row, tested against Sn only where
+    // used, so nothing waits for them early).
+    const uint32_t last = Sn - 1;  // Sn > k >= 1
+    float l8[8], x8[8];
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+        const uint32_t r = min(t + i * TK_SEL_NT, last);
+        l8[i] = lrow[r];
+        x8[i] = a.px[r];
+    }
+    for (uint32_t r0 = t; r0 < Sn; r0 += 8 * TK_SEL_NT) {
+        float nl8[8], nx8[8];
 #pragma unroll
         for (uint32_t i = 0; i < 8; ++i) {
-            const uint32_t r = r0 + i * TK_SEL_NT;
-            l8[i] = r < Sn ? lrow[r] : 0.f;
-            x8[i] = r < Sn ? a.px[r] : 0.f;
+            const uint32_t r = min(r0 + (8 + i) * TK_SEL_NT, last);
+            nl8[i] = lrow[r];
+            nx8[i] = a.px[r];
         }
 #pragma unroll
         for (uint32_t i = 0; i < 8; ++i) {
@@ -987,6 +1049,8 @@ __device__ __forceinline__ float tk_hist_bound(const TkArgs& a, uint32_t q, cons
             atomicAdd(&hist[bin], 1u);
             atomicMax(&bmax[bin], tk_ordered(u));
         }
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) l8[i] = nl8[i], x8[i] = nx8[i];
     }
     __syncthreads();
     uint32_t total;
@@ -1019,7 +1083,7 @@ __global__ __launch_bounds__(TK_SEL_NT) void tk_seed_bound(TkArgs a)
     if (threadIdx.x == 0) atomicMin(a.tau + q, __float_as_uint(fmaxf(bound, 0.f)));
 }
 
-__global__ __launch_bounds__(TK_SEL_NT) void tk_select(TkArgs a, float* out_d, int64_t* out_id)
+__global__ __launch_bounds__(TK_SEL_NT) __attribute__((amdgpu_waves_per_eu(8))) void tk_select(TkArgs a, float* out_d, int64_t* out_id)
 {
     __shared__ float bd[2][TK_KMAX];  // the running best, ascending (two planes)
     __shared__ uint32_t bi[2][TK_KMAX];
@@ -1035,7 +1099,7 @@ __global__ __launch_bounds__(TK_SEL_NT) void tk_select(TkArgs a, float* out_d, i
     const uint32_t q = blockIdx.x;
     const uint32_t t = threadIdx.x;
     const float* lrow = a.pd + static_cast<size_t>(q) * a.small_max;
-    for (uint32_t c = t; c < a.dim; c += TK_SEL_NT) qv[c] = a.queries[static_cast<size_t>(q) * a.dim + c];
+    for (uint32_t c = t; c < 128; c += TK_SEL_NT) qv[c] = c < a.dim ? a.queries[static_cast<size_t>(q) * a.dim + c] : 0.f;
     float bound = __builtin_inff();
     if (S > a.k) {
         // The first bound from the upper bounds of the first rows (a sample
@@ -1056,14 +1120,25 @@ __global__ __launch_bounds__(TK_SEL_NT) void tk_select(TkArgs a, float* out_d, i
             if (c < nbatch) {
                 const uint32_t r = ci[c];
                 id = a.sel ? a.sel[r] : r;
-                const float* x = a.base + static_cast<size_t>(id) * a.dim;
+                // the part's 16 dimensions, all loaded before any is used (zeros
+                // past dim, where qv is zero too, add nothing)
+                const float* x = a.base + static_cast<size_t>(id) * a.dim + part * 16;
+                float xv[16];
+                if (a.vec) {  // dim % 4 == 0, 16-byte aligned rows
+#pragma unroll
+                    for (uint32_t q4 = 0; q4 < 4; ++q4) {
+                        const float4 v = part * 16 + 4 * q4 < a.dim ? *reinterpret_cast<const float4*>(x + 4 * q4)
+                                                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+                        xv[4 * q4] = v.x, xv[4 * q4 + 1] = v.y, xv[4 * q4 + 2] = v.z, xv[4 * q4 + 3] = v.w;
+                    }
+                } else {
+#pragma unroll
+                    for (uint32_t s2 = 0; s2 < 16; ++s2) xv[s2] = part * 16 + s2 < a.dim ? x[s2] : 0.f;
+                }
 #pragma unroll
                 for (uint32_t s2 = 0; s2 < 16; ++s2) {
-                    const uint32_t d = part * 16 + s2;
-                    if (d < a.dim) {
-                        const float e = qv[d] - x[d];
-                        e2 = fmaf(e, e, e2);
-                    }
+                    const float e = qv[part * 16 + s2] - xv[s2];
+                    e2 = fmaf(e, e, e2);
                 }
             }
             e2 += __shfl_xor(e2, 1, 64);
@@ -1126,25 +1201,31 @@ __global__ __launch_bounds__(TK_SEL_NT) void tk_select(TkArgs a, float* out_d, i
         if (nb == a.k) bound = fminf(bound, bd[cur][a.k - 1]);  // the k-th best so far bounds the answer
     };
     // Candidates are few: a thread that finds one takes a batch slot with an
-    // LDS atomic.  Chunks of TK_SEL_RPT rows per thread (loads in flight); a
-    // batch that could overflow in the next chunk is flushed first.
+    // LDS atomic.  Chunks of TK_SEL_RPT rows per thread, the next chunk's
+    // loads issued before the current one is tested (clamped to the last row,
+    // and tested against S only where used, so nothing waits for them early);
+    // a batch that could overflow in the next chunk is flushed first.
+    constexpr uint32_t CH = TK_SEL_RPT * TK_SEL_NT;
     if (t == 0) s_nbatch = 0;
-    for (uint32_t r0 = 0; r0 < S; r0 += TK_SEL_RPT * TK_SEL_NT) {
+    float l4[TK_SEL_RPT];
+    const uint32_t last = S > 0 ? S - 1 : 0;
+#pragma unroll
+    for (uint32_t i = 0; i < TK_SEL_RPT; ++i) l4[i] = lrow[min(i * TK_SEL_NT + t, last)];
+    for (uint32_t r0 = 0; r0 < S; r0 += CH) {
+        float n4[TK_SEL_RPT];
+#pragma unroll
+        for (uint32_t i = 0; i < TK_SEL_RPT; ++i) n4[i] = lrow[min(r0 + CH + i * TK_SEL_NT + t, last)];
         __syncthreads();  // the previous chunk's slots are taken
         nbatch = s_nbatch;
         __syncthreads();  // every thread has read the count before the next slots are taken
-        if (nbatch > TK_SEL_CB - TK_SEL_RPT * TK_SEL_NT) flush();
-        float l4[TK_SEL_RPT];
-#pragma unroll
-        for (uint32_t i = 0; i < TK_SEL_RPT; ++i) {
-            const uint32_t r = r0 + i * TK_SEL_NT + t;
-            l4[i] = r < S ? lrow[r] : __builtin_inff();
-        }
+        if (nbatch > TK_SEL_CB - CH) flush();
 #pragma unroll
         for (uint32_t i = 0; i < TK_SEL_RPT; ++i) {
             const uint32_t r = r0 + i * TK_SEL_NT + t;
             if (r < S && l4[i] <= bound) ci[atomicAdd(&s_nbatch, 1u)] = r;
         }
+#pragma unroll
+        for (uint32_t i = 0; i < TK_SEL_RPT; ++i) l4[i] = n4[i];
     }
     __syncthreads();
     nbatch = s_nbatch;
@@ -1178,7 +1259,10 @@ int launch_dist(const TkArgs& a, uint32_t grid, uint32_t pairs_grid, hipStream_t
     if (a.small_max) {  // estimates of a small set, or the seed rows of a larger one, and the seed bound
         {
             CR_TIMED("tk_pairs", s);
-            tk_pairs<DP><<<pairs_grid, TK_NT, 0, s>>>(a);
+            if (a.sel)
+                tk_pairs<DP, true><<<pairs_grid, TK_NT, 0, s>>>(a);
+            else
+                tk_pairs<DP, false><<<pairs_grid, TK_NT, 0, s>>>(a);
         }
         CR_LAUNCH_CHECK();
         {
@@ -1232,11 +1316,12 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     const size_t o_ln = cv.add(static_cast<size_t>(n_chunks) * n_q * 4);
     const size_t o_tau = cv.add(static_cast<size_t>(n_q) * 4);
     const size_t o_taum = cv.add(static_cast<size_t>(n_chunks) * n_q * 4);
-    // The small-set path keeps every estimate, n_q x small_max floats, within
-    // TK_SMALL_BYTES.
+    // The small-set path keeps every estimate, small_max floats for each query
+    // of every whole query block, within TK_SMALL_BYTES.
+    const uint64_t q_rows = static_cast<uint64_t>(n_qb) * TK_QB;
     const uint32_t small_max = static_cast<uint32_t>(std::min<uint64_t>(
-        g_topk_small.load(), TK_SMALL_BYTES / (4ull * n_q) / TK_ROWS * TK_ROWS));
-    const size_t o_pd = cv.add(static_cast<size_t>(n_q) * small_max * 4);
+        g_topk_small.load(), TK_SMALL_BYTES / (4ull * q_rows) / TK_ROWS * TK_ROWS));
+    const size_t o_pd = cv.add(q_rows * small_max * 4);
     const size_t o_pq = cv.add(small_max ? static_cast<size_t>(n_q) * 4 : 0);
     const size_t o_px = cv.add(static_cast<size_t>(small_max) * 4);
     const size_t o_qlo = cv.add(small_max ? static_cast<size_t>(n_q) * 4 : 0);
