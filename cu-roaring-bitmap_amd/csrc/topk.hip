@@ -1066,23 +1066,11 @@ __device__ __forceinline__ float tk_hist_bound(const TkArgs& a, uint32_t q, cons
     return tk_unordered(s_bound);
 }
 
-// Larger sets: query q's bound from the upper bounds of its seed rows (more
-// than k of them), into tau for the list path.  At least k rows have an fp32
-// distance at or below it, so the k-th best does; tau holds the bits of
-// non-negative distances.
-__global__ __launch_bounds__(TK_SEL_NT) void tk_seed_bound(TkArgs a)
-{
-    __shared__ uint32_t hist[TK_SEL_BINS], bmax[TK_SEL_BINS];
-    __shared__ uint32_t lds[TK_SEL_NT / 64];
-    __shared__ uint32_t s_bin, s_bound;
-    const uint32_t S = tk_seed_rows(a, tk_rows(a));
-    if (S <= a.k) return;
-    const uint32_t q = blockIdx.x;
-    const float bound = tk_hist_bound(a, q, a.pd + static_cast<size_t>(q) * a.small_max, S, hist, bmax, lds, s_bin,
-                                      s_bound);
-    if (threadIdx.x == 0) atomicMin(a.tau + q, __float_as_uint(fmaxf(bound, 0.f)));
-}
-
+// One workgroup per query, right after tk_pairs, on both paths.  A small set
+// is answered here (below).  A larger one gets query q's bound from the upper
+// bounds of its seed rows (more than k of them), into tau for the list path:
+// at least k rows have an fp32 distance at or below it, so the k-th best does
+// (tau holds the bits of non-negative distances).
 __global__ __launch_bounds__(TK_SEL_NT) __attribute__((amdgpu_waves_per_eu(8))) void tk_select(TkArgs a, float* out_d, int64_t* out_id)
 {
     __shared__ float bd[2][TK_KMAX];  // the running best, ascending (two planes)
@@ -1094,7 +1082,15 @@ __global__ __launch_bounds__(TK_SEL_NT) __attribute__((amdgpu_waves_per_eu(8))) 
     __shared__ uint32_t lds[TK_SEL_NT / 64];
     __shared__ uint32_t s_bin, s_bound, s_nbatch;
     const uint64_t n_rows = tk_rows(a);
-    if (!tk_small(a, n_rows)) return;  // the list path answers
+    if (!tk_small(a, n_rows)) {  // the list path answers; its seed bound
+        const uint32_t Sd = tk_seed_rows(a, n_rows);
+        if (Sd <= a.k) return;
+        const uint32_t qs = blockIdx.x;
+        const float sb = tk_hist_bound(a, qs, a.pd + static_cast<size_t>(qs) * a.small_max, Sd, hist, bmax, lds,
+                                       s_bin, s_bound);
+        if (threadIdx.x == 0) atomicMin(a.tau + qs, __float_as_uint(fmaxf(sb, 0.f)));
+        return;
+    }
     const uint32_t S = static_cast<uint32_t>(n_rows);
     const uint32_t q = blockIdx.x;
     const uint32_t t = threadIdx.x;
@@ -1123,22 +1119,26 @@ __global__ __launch_bounds__(TK_SEL_NT) __attribute__((amdgpu_waves_per_eu(8))) 
                 // the part's 16 dimensions, all loaded before any is used (zeros
                 // past dim, where qv is zero too, add nothing)
                 const float* x = a.base + static_cast<size_t>(id) * a.dim + part * 16;
-                float xv[16];
-                if (a.vec) {  // dim % 4 == 0, 16-byte aligned rows
 #pragma unroll
-                    for (uint32_t q4 = 0; q4 < 4; ++q4) {
-                        const float4 v = part * 16 + 4 * q4 < a.dim ? *reinterpret_cast<const float4*>(x + 4 * q4)
-                                                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-                        xv[4 * q4] = v.x, xv[4 * q4 + 1] = v.y, xv[4 * q4 + 2] = v.z, xv[4 * q4 + 3] = v.w;
+                for (uint32_t hh = 0; hh < 16; hh += 8) {  // two halves of 8
+                    float xv[8];
+                    if (a.vec) {  // dim % 4 == 0, 16-byte aligned rows
+#pragma unroll
+                        for (uint32_t q4 = 0; q4 < 8; q4 += 4) {
+                            const float4 v = part * 16 + hh + q4 < a.dim
+                                                 ? *reinterpret_cast<const float4*>(x + hh + q4)
+                                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+                            xv[q4] = v.x, xv[q4 + 1] = v.y, xv[q4 + 2] = v.z, xv[q4 + 3] = v.w;
+                        }
+                    } else {
+#pragma unroll
+                        for (uint32_t s2 = 0; s2 < 8; ++s2) xv[s2] = part * 16 + hh + s2 < a.dim ? x[hh + s2] : 0.f;
                     }
-                } else {
 #pragma unroll
-                    for (uint32_t s2 = 0; s2 < 16; ++s2) xv[s2] = part * 16 + s2 < a.dim ? x[s2] : 0.f;
-                }
-#pragma unroll
-                for (uint32_t s2 = 0; s2 < 16; ++s2) {
-                    const float e = qv[part * 16 + s2] - xv[s2];
-                    e2 = fmaf(e, e, e2);
+                    for (uint32_t s2 = 0; s2 < 8; ++s2) {
+                        const float e = qv[part * 16 + hh + s2] - xv[s2];
+                        e2 = fmaf(e, e, e2);
+                    }
                 }
             }
             e2 += __shfl_xor(e2, 1, 64);
@@ -1201,31 +1201,32 @@ __global__ __launch_bounds__(TK_SEL_NT) __attribute__((amdgpu_waves_per_eu(8))) 
         if (nb == a.k) bound = fminf(bound, bd[cur][a.k - 1]);  // the k-th best so far bounds the answer
     };
     // Candidates are few: a thread that finds one takes a batch slot with an
-    // LDS atomic.  Chunks of TK_SEL_RPT rows per thread, the next chunk's
-    // loads issued before the current one is tested (clamped to the last row,
-    // and tested against S only where used, so nothing waits for them early);
-    // a batch that could overflow in the next chunk is flushed first.
+    // LDS atomic.  Chunks of TK_SEL_RPT consecutive rows per thread (one
+    // 16-byte load), the loads of the next two chunks in flight while one is
+    // tested (clamped to the last whole vector of the row, which the estimate
+    // row holds, and tested against S only where used, so nothing waits for
+    // them early); a batch that could overflow in the next chunk is flushed
+    // first.
+    static_assert(TK_SEL_RPT == 4, "one float4 a thread per chunk");
     constexpr uint32_t CH = TK_SEL_RPT * TK_SEL_NT;
     if (t == 0) s_nbatch = 0;
-    float l4[TK_SEL_RPT];
-    const uint32_t last = S > 0 ? S - 1 : 0;
-#pragma unroll
-    for (uint32_t i = 0; i < TK_SEL_RPT; ++i) l4[i] = lrow[min(i * TK_SEL_NT + t, last)];
+    const uint32_t last4 = S > 0 ? (S - 1) & ~3u : 0;
+    auto ld4 = [&](uint32_t r) { return *reinterpret_cast<const float4*>(lrow + min(r, last4)); };
+    float4 l4 = ld4(4 * t), n4 = ld4(CH + 4 * t);
     for (uint32_t r0 = 0; r0 < S; r0 += CH) {
-        float n4[TK_SEL_RPT];
-#pragma unroll
-        for (uint32_t i = 0; i < TK_SEL_RPT; ++i) n4[i] = lrow[min(r0 + CH + i * TK_SEL_NT + t, last)];
+        const float4 m4 = ld4(r0 + 2 * CH + 4 * t);
         __syncthreads();  // the previous chunk's slots are taken
         nbatch = s_nbatch;
         __syncthreads();  // every thread has read the count before the next slots are taken
         if (nbatch > TK_SEL_CB - CH) flush();
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
 #pragma unroll
-        for (uint32_t i = 0; i < TK_SEL_RPT; ++i) {
-            const uint32_t r = r0 + i * TK_SEL_NT + t;
-            if (r < S && l4[i] <= bound) ci[atomicAdd(&s_nbatch, 1u)] = r;
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t r = r0 + 4 * t + i;
+            if (r < S && lv[i] <= bound) ci[atomicAdd(&s_nbatch, 1u)] = r;
         }
-#pragma unroll
-        for (uint32_t i = 0; i < TK_SEL_RPT; ++i) l4[i] = n4[i];
+        l4 = n4;
+        n4 = m4;
     }
     __syncthreads();
     nbatch = s_nbatch;
@@ -1254,9 +1255,9 @@ __global__ __launch_bounds__(256) void tk_init(TkArgs a)
 }
 
 template <int DP>
-int launch_dist(const TkArgs& a, uint32_t grid, uint32_t pairs_grid, hipStream_t s)
+int launch_dist(const TkArgs& a, uint32_t grid, uint32_t pairs_grid, float* out_d, int64_t* out_ids, hipStream_t s)
 {
-    if (a.small_max) {  // estimates of a small set, or the seed rows of a larger one, and the seed bound
+    if (a.small_max) {  // estimates of a small set (and its answer), or the seed rows of a larger one and their bound
         {
             CR_TIMED("tk_pairs", s);
             if (a.sel)
@@ -1266,8 +1267,8 @@ int launch_dist(const TkArgs& a, uint32_t grid, uint32_t pairs_grid, hipStream_t
         }
         CR_LAUNCH_CHECK();
         {
-            CR_TIMED("tk_seed", s);
-            tk_seed_bound<<<a.n_q, TK_SEL_NT, 0, s>>>(a);
+            CR_TIMED("tk_select", s);
+            tk_select<<<a.n_q, TK_SEL_NT, 0, s>>>(a, out_d, out_ids);
         }
         CR_LAUNCH_CHECK();
     }
@@ -1377,21 +1378,16 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     // block's tiles dealt out among its workgroups
     const uint32_t pairs_grid = std::max<uint32_t>(1, (cus + n_qb - 1) / n_qb) * n_qb;
     if (dim <= 32) {
-        CR_RET(launch_dist<32>(a, grid, pairs_grid, s));
+        CR_RET(launch_dist<32>(a, grid, pairs_grid, d_out_dist, d_out_ids, s));
     } else if (dim <= 64) {
-        CR_RET(launch_dist<64>(a, grid, pairs_grid, s));
+        CR_RET(launch_dist<64>(a, grid, pairs_grid, d_out_dist, d_out_ids, s));
     } else {
-        CR_RET(launch_dist<128>(a, grid, pairs_grid, s));
+        CR_RET(launch_dist<128>(a, grid, pairs_grid, d_out_dist, d_out_ids, s));
     }
     {
         CR_TIMED("tk_merge", s);
         tk_merge<<<(n_q + 3) / 4, TK_MERGE_NT, 0, s>>>(a, a.list_d, a.list_id, a.plane, a.list_n, n_chunks, n_q, k,
                                                         d_out_dist, d_out_ids);
-    }
-    CR_LAUNCH_CHECK();
-    if (small_max) {
-        CR_TIMED("tk_select", s);
-        tk_select<<<n_q, TK_SEL_NT, 0, s>>>(a, d_out_dist, d_out_ids);
     }
     CR_LAUNCH_CHECK();
     return CR_OK;
