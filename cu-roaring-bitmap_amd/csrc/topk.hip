@@ -457,6 +457,28 @@ __device__ __forceinline__ void tk_load_rows_nb(const TkArgs& a, const uint32_t 
     }
 }
 
+// Sum over aligned groups of W lanes (8, 16 or 32) with DPP moves, no LDS
+// round trips: quad swaps, the half-row and row mirrors, then (W = 32) row
+// 15's value broadcast into the next row.  Every lane of a group holds the
+// total for W <= 16, the group's upper 16 lanes for W = 32.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float tk_dpp(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+
+template <int W>
+__device__ __forceinline__ float tk_group_sum(float x)
+{
+    static_assert(W == 8 || W == 16 || W == 32, "lane groups of 8, 16 or 32");
+    x += tk_dpp<0xB1, 0xF>(x);   // quad_perm [1, 0, 3, 2]
+    x += tk_dpp<0x4E, 0xF>(x);   // quad_perm [2, 3, 0, 1]
+    x += tk_dpp<0x141, 0xF>(x);  // row_half_mirror
+    if constexpr (W >= 16) x += tk_dpp<0x140, 0xF>(x);  // row_mirror
+    if constexpr (W == 32) x += tk_dpp<0x142, 0xA>(x);  // row_bcast:15 into rows 1 and 3 (rows 0 and 2 add 0)
+    return x;
+}
+
 template <int DP, class Lds>
 __device__ __forceinline__ void tk_store_rows(Lds& L, int buf, const float4 (&pre)[DP / 32],
                                               const uint32_t (&pid)[DP / 32])
@@ -470,10 +492,8 @@ __device__ __forceinline__ void tk_store_rows(Lds& L, int buf, const float4 (&pr
         const int c = static_cast<int>(t % TPR) * 4;
         const float4 v = pid[p] != TK_NOID ? pre[p] : make_float4(0.f, 0.f, 0.f, 0.f);
         *reinterpret_cast<float4*>(&L.tile[buf][row * (DP + 4) + c]) = v;
-        float ss = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-#pragma unroll
-        for (int o = TPR / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-        if (c == 0) {
+        const float ss = tk_group_sum<TPR>(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
+        if (static_cast<int>(t % TPR) == (TPR == 32 ? TPR - 1 : 0)) {  // a lane holding the row's total
             L.xg[buf][row] = pid[p] != TK_NOID ? (1.f - TK_GATE_ERR) * ss : __builtin_nanf("");
             L.id[buf][row] = pid[p];
         }
