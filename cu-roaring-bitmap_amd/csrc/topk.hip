@@ -535,7 +535,7 @@ __device__ __forceinline__ int tk_row(int rr, int hh)
     return (rr >> 4) * 32 + 8 * ((rr & 15) >> 2) + 4 * hh + (rr & 3);
 }
 
-template <int DP>
+template <int DP, bool SEL>
 __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
 {
     __shared__ TkLds<DP> L;
@@ -582,11 +582,25 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
     const float qpart = tk_load_query<DP>(a, qok, q0 + j, h, qreg);
     const float qg = (1.f - TK_GATE_ERR) * (qpart + __shfl_xor(qpart, 32, 64));
 
+    // The prefetch as in tk_pairs: tile t + 1's rows (ids known since tile
+    // t - 1) and tile t + 2's raw ids are issued before tile t's MFMA and
+    // waited for after it.
+    auto tile_r0 = [&](uint32_t i) { return r0 + static_cast<uint64_t>(i) * TK_ROWS; };
+    auto tile_r1 = [&](uint32_t i) { return std::min<uint64_t>(r1, tile_r0(i) + TK_ROWS); };
+    const uint64_t last = n_rows > 0 ? n_rows - 1 : 0;
     float4 pre[DP / 32];
-    uint32_t pid[DP / 32];
+    uint32_t pid[DP / 32], nid[DP / 32];
+    if constexpr (SEL) {
+        if (n_rows > 0) tk_ids_raw<DP, SEL>(a, tile_r0(1), last, nid);
+    }
     if (n_tiles > 0) {
         tk_load_rows<DP>(a, r0, r1, pre, pid);
         tk_store_rows<DP>(L, 0, pre, pid);
+    }
+    if constexpr (SEL) {
+#pragma unroll
+        for (int p = 0; p < DP / 32; ++p) pid[p] = n_rows > 0 ? nid[p] : TK_NOID;
+        tk_ids_valid<DP>(tile_r0(1), tile_r1(1), pid);
     }
     __syncthreads();
 
@@ -600,7 +614,12 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
     uint32_t cnt = 0;  // wave-uniform fill of the candidate buffer
     for (uint32_t t = 0; t < n_tiles; ++t) {
         const int b = static_cast<int>(t & 1u);
-        if (t + 1 < n_tiles) tk_load_rows<DP>(a, r0 + static_cast<uint64_t>(t + 1) * TK_ROWS, r1, pre, pid);
+        if constexpr (SEL) {
+            tk_load_rows_nb<DP>(a, pid, pre);
+            tk_ids_raw<DP, SEL>(a, tile_r0(t + 2), last, nid);
+        } else if (t + 1 < n_tiles) {  // the row numbers are the ids
+            tk_load_rows<DP>(a, tile_r0(t + 1), r1, pre, pid);
+        }
         const float tsh_new = qok ? tk_atomic_load(tau_q0 + j) : __builtin_inff();
 
         if (nq_wave > 0) {
@@ -749,7 +768,14 @@ __global__ __launch_bounds__(TK_NT) void tk_dist(TkArgs a)
         // every wave to merge after the barrier, so the waves of the block
         // stall for one merge at a time rather than one after another.
         if (cnt > TK_CB * 3 / 4 && lane == 0) L.flush_req = t;
-        if (t + 1 < n_tiles) tk_store_rows<DP>(L, b ^ 1, pre, pid);
+        if constexpr (SEL) {
+            tk_store_rows<DP>(L, b ^ 1, pre, pid);
+#pragma unroll
+            for (int p = 0; p < DP / 32; ++p) pid[p] = nid[p];
+            tk_ids_valid<DP>(tile_r0(t + 2), tile_r1(t + 2), pid);
+        } else if (t + 1 < n_tiles) {
+            tk_store_rows<DP>(L, b ^ 1, pre, pid);
+        }
         __syncthreads();
         if (L.flush_req == t && cnt > 0) {
             tk_flush(W, cnt, a.k, a.m_rank, nq_wave, a.list_d + list_row, a.list_id + list_row, a.plane, tau_q0, tau_m_q0);
@@ -1294,7 +1320,10 @@ int launch_dist(const TkArgs& a, uint32_t grid, uint32_t pairs_grid, float* out_
     }
     {
         CR_TIMED("tk_dist", s);
-        tk_dist<DP><<<grid, TK_NT, 0, s>>>(a);
+        if (a.sel)
+            tk_dist<DP, true><<<grid, TK_NT, 0, s>>>(a);
+        else
+            tk_dist<DP, false><<<grid, TK_NT, 0, s>>>(a);
     }
     CR_LAUNCH_CHECK();
     return CR_OK;
