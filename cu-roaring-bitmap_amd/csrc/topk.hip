@@ -93,80 +93,6 @@ __device__ __forceinline__ uint32_t tk_lower_bound(const float* d, const uint32_
 
 __device__ __forceinline__ uint64_t lanemask_lt() { return (1ull << __lane_id()) - 1ull; }
 
-// ---- 1. passing ids ---------------------------------------------------------
-
-// A workgroup covers 8192 consecutive ids, a 256-word slice of one key's
-// container: the container is looked up once, and thread t takes word t of the
-// slice -- from the bitmap, or from the container's image built in LDS for an
-// array or run container -- complemented for a negated filter (contains()
-// answers `negated` for absent keys) and cut at n_base.
-static_assert(TK_ENUM_IDS == 32u * TK_ENUM_NT && 65536u % TK_ENUM_IDS == 0, "one word per thread, one key per block");
-
-__device__ uint32_t tk_enum_word(const GpuRoaringView& v, uint64_t n_base, uint32_t* img, int32_t* cover, int32_t* s_c)
-{
-    const uint32_t t = threadIdx.x;
-    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * TK_ENUM_IDS;
-    const uint32_t key = static_cast<uint32_t>(base >> 16);
-    if (v.key_index && key <= v.max_key) {
-        if (t == 0) {
-            const uint16_t e = v.key_index[key];
-            *s_c = e == 0xFFFFu ? -1 : static_cast<int32_t>(e);
-        }
-    } else if (key > v.max_key && v.key_index) {
-        if (t == 0) *s_c = -1;
-    } else if (t < 64) {
-        const uint32_t pos = wave_lower_bound_u16(v.keys, v.n_containers, key);
-        if (t == 0) *s_c = (pos < v.n_containers && v.keys[pos] == key) ? static_cast<int32_t>(pos) : -1;
-    }
-    __syncthreads();
-    const int32_t c = *s_c;
-    const uint32_t w0 = static_cast<uint32_t>(base & 0xFFFFu) >> 5;  // first word of the slice in the container
-    uint32_t word = 0;
-    const uint8_t type = c >= 0 ? static_cast<uint8_t>(v.types[c]) : uint8_t(0xFF);  // block-uniform
-    if (type == CR_BITMAP) {
-        word = reinterpret_cast<const uint32_t*>(v.bitmap_data + v.offsets[c] / 8u)[w0 + t];
-    } else if (type == CR_ARRAY || type == CR_RUN) {
-        expand_img<TK_ENUM_NT>(type, (type == CR_ARRAY ? v.array_data : v.run_data) + v.offsets[c] / 2u,
-                               v.cardinalities[c], img, cover);
-        word = img[w0 + t];
-    }
-    if (v.negated) word = ~word;
-    const uint64_t id0 = base + 32u * t;
-    if (id0 >= n_base) word = 0;
-    else if (n_base - id0 < 32u) word &= (1u << (n_base - id0)) - 1u;
-    return word;
-}
-
-__global__ __launch_bounds__(TK_ENUM_NT) void tk_enum_count(GpuRoaringView v, uint64_t n_base, uint32_t* counts)
-{
-    __shared__ alignas(16) uint32_t img[2048];
-    __shared__ int32_t cover[2048];
-    __shared__ int32_t s_c;
-    __shared__ uint32_t red[TK_ENUM_NT / 64];
-    const uint32_t c = block_sum<TK_ENUM_NT>(__popc(tk_enum_word(v, n_base, img, cover, &s_c)), red);
-    if (threadIdx.x == 0) counts[blockIdx.x] = c;
-}
-
-__global__ __launch_bounds__(TK_ENUM_NT) void tk_enum_write(GpuRoaringView v, uint64_t n_base, const uint32_t* counts,
-                                                            uint32_t* sel, uint32_t* n_sel)
-{
-    __shared__ alignas(16) uint32_t img[2048];
-    __shared__ int32_t cover[2048];
-    __shared__ int32_t s_c;
-    __shared__ uint32_t red[TK_ENUM_NT / 64];
-    uint32_t pre = 0;
-    for (uint32_t i = threadIdx.x; i < blockIdx.x; i += TK_ENUM_NT) pre += counts[i];
-    const uint32_t run = block_sum<TK_ENUM_NT>(pre, red);
-    const uint32_t word = tk_enum_word(v, n_base, img, cover, &s_c);
-    uint32_t tot;
-    uint32_t pos = run + block_excl_scan<TK_ENUM_NT>(__popc(word), red, tot);
-    const uint32_t id0 = static_cast<uint32_t>(static_cast<uint64_t>(blockIdx.x) * TK_ENUM_IDS) + 32u * threadIdx.x;
-    for (uint32_t x = word; x; x &= x - 1) sel[pos++] = id0 + static_cast<uint32_t>(__builtin_ctz(x));
-    if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) *n_sel = run + tot;
-}
-
-// ---- 2. distances and per-chunk selection ----------------------------------
-
 struct TkArgs {
     const float* base;
     const float* queries;
@@ -214,6 +140,102 @@ __device__ __forceinline__ uint32_t tk_seed_rows(const TkArgs& a, uint64_t n_row
     const uint64_t want = std::max<uint64_t>(TK_SEED_ROWS, static_cast<uint64_t>(TK_SEED_ROWS_PER_K) * a.k);
     return static_cast<uint32_t>(std::min<uint64_t>(std::min<uint64_t>(n_rows, a.small_max), want));
 }
+
+// The call's state: every query's bound (tau) and each chunk's m_rank-th
+// distance (tau_m) at +inf, and for the small-set path the range of the upper
+// bounds (qlo at the largest value, qhi at the smallest); thread i of `stride`.
+__device__ __forceinline__ void tk_init_from(const TkArgs& a, uint64_t i, uint64_t stride)
+{
+    const uint64_t n = std::max<uint64_t>(static_cast<uint64_t>(a.n_chunks) * a.n_q, a.n_q);
+    for (; i < n; i += stride) {
+        if (i < static_cast<uint64_t>(a.n_chunks) * a.n_q) a.tau_m[i] = 0x7F800000u;
+        if (i < a.n_q) {
+            a.tau[i] = 0x7F800000u;
+            if (a.small_max) {
+                a.qlo[i] = 0xFFFFFFFFu;
+                a.qhi[i] = 0u;
+            }
+        }
+    }
+}
+
+// ---- 1. passing ids ---------------------------------------------------------
+
+// A workgroup covers 8192 consecutive ids, a 256-word slice of one key's
+// container: the container is looked up once, and thread t takes word t of the
+// slice -- from the bitmap, or from the container's image built in LDS for an
+// array or run container -- complemented for a negated filter (contains()
+// answers `negated` for absent keys) and cut at n_base.
+static_assert(TK_ENUM_IDS == 32u * TK_ENUM_NT && 65536u % TK_ENUM_IDS == 0, "one word per thread, one key per block");
+
+__device__ uint32_t tk_enum_word(const GpuRoaringView& v, uint64_t n_base, uint32_t* img, int32_t* cover, int32_t* s_c)
+{
+    const uint32_t t = threadIdx.x;
+    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * TK_ENUM_IDS;
+    const uint32_t key = static_cast<uint32_t>(base >> 16);
+    if (v.key_index && key <= v.max_key) {
+        if (t == 0) {
+            const uint16_t e = v.key_index[key];
+            *s_c = e == 0xFFFFu ? -1 : static_cast<int32_t>(e);
+        }
+    } else if (key > v.max_key && v.key_index) {
+        if (t == 0) *s_c = -1;
+    } else if (t < 64) {
+        const uint32_t pos = wave_lower_bound_u16(v.keys, v.n_containers, key);
+        if (t == 0) *s_c = (pos < v.n_containers && v.keys[pos] == key) ? static_cast<int32_t>(pos) : -1;
+    }
+    __syncthreads();
+    const int32_t c = *s_c;
+    const uint32_t w0 = static_cast<uint32_t>(base & 0xFFFFu) >> 5;  // first word of the slice in the container
+    uint32_t word = 0;
+    const uint8_t type = c >= 0 ? static_cast<uint8_t>(v.types[c]) : uint8_t(0xFF);  // block-uniform
+    if (type == CR_BITMAP) {
+        word = reinterpret_cast<const uint32_t*>(v.bitmap_data + v.offsets[c] / 8u)[w0 + t];
+    } else if (type == CR_ARRAY || type == CR_RUN) {
+        expand_img<TK_ENUM_NT>(type, (type == CR_ARRAY ? v.array_data : v.run_data) + v.offsets[c] / 2u,
+                               v.cardinalities[c], img, cover);
+        word = img[w0 + t];
+    }
+    if (v.negated) word = ~word;
+    const uint64_t id0 = base + 32u * t;
+    if (id0 >= n_base) word = 0;
+    else if (n_base - id0 < 32u) word &= (1u << (n_base - id0)) - 1u;
+    return word;
+}
+
+// Also initialises the call's state (tk_init_from), which saves a launch.
+__global__ __launch_bounds__(TK_ENUM_NT) void tk_enum_count(GpuRoaringView v, uint64_t n_base, uint32_t* counts,
+                                                            TkArgs a)
+{
+    tk_init_from(a, static_cast<uint64_t>(blockIdx.x) * TK_ENUM_NT + threadIdx.x,
+                 static_cast<uint64_t>(gridDim.x) * TK_ENUM_NT);
+    __shared__ alignas(16) uint32_t img[2048];
+    __shared__ int32_t cover[2048];
+    __shared__ int32_t s_c;
+    __shared__ uint32_t red[TK_ENUM_NT / 64];
+    const uint32_t c = block_sum<TK_ENUM_NT>(__popc(tk_enum_word(v, n_base, img, cover, &s_c)), red);
+    if (threadIdx.x == 0) counts[blockIdx.x] = c;
+}
+
+__global__ __launch_bounds__(TK_ENUM_NT) void tk_enum_write(GpuRoaringView v, uint64_t n_base, const uint32_t* counts,
+                                                            uint32_t* sel, uint32_t* n_sel)
+{
+    __shared__ alignas(16) uint32_t img[2048];
+    __shared__ int32_t cover[2048];
+    __shared__ int32_t s_c;
+    __shared__ uint32_t red[TK_ENUM_NT / 64];
+    uint32_t pre = 0;
+    for (uint32_t i = threadIdx.x; i < blockIdx.x; i += TK_ENUM_NT) pre += counts[i];
+    const uint32_t run = block_sum<TK_ENUM_NT>(pre, red);
+    const uint32_t word = tk_enum_word(v, n_base, img, cover, &s_c);
+    uint32_t tot;
+    uint32_t pos = run + block_excl_scan<TK_ENUM_NT>(__popc(word), red, tot);
+    const uint32_t id0 = static_cast<uint32_t>(static_cast<uint64_t>(blockIdx.x) * TK_ENUM_IDS) + 32u * threadIdx.x;
+    for (uint32_t x = word; x; x &= x - 1) sel[pos++] = id0 + static_cast<uint32_t>(__builtin_ctz(x));
+    if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) *n_sel = run + tot;
+}
+
+// ---- 2. distances and per-chunk selection ----------------------------------
 
 // Per-wave selection state in LDS.
 struct TkWave {
@@ -1284,20 +1306,10 @@ __global__ __launch_bounds__(TK_SEL_NT) __attribute__((amdgpu_waves_per_eu(8))) 
     }
 }
 
-// The call's state in one launch: every query's bound (tau) and each chunk's
-// m_rank-th distance (tau_m) at +inf, and for the small-set path the range of
-// the upper bounds (qlo at the largest value, qhi at the smallest).
+// The call's state (tk_init_from), when no enumeration kernel sets it.
 __global__ __launch_bounds__(256) void tk_init(TkArgs a)
 {
-    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
-    if (i < static_cast<uint64_t>(a.n_chunks) * a.n_q) a.tau_m[i] = 0x7F800000u;
-    if (i < a.n_q) {
-        a.tau[i] = 0x7F800000u;
-        if (a.small_max) {
-            a.qlo[i] = 0xFFFFFFFFu;
-            a.qhi[i] = 0u;
-        }
-    }
+    tk_init_from(a, static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x, static_cast<uint64_t>(gridDim.x) * 256u);
 }
 
 template <int DP>
@@ -1402,8 +1414,10 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     a.px = small_max ? sc.at<float>(o_px) : nullptr;
     a.qlo = small_max ? sc.at<uint32_t>(o_qlo) : nullptr;
     a.qhi = small_max ? sc.at<uint32_t>(o_qhi) : nullptr;
-    tk_init<<<static_cast<unsigned>((static_cast<uint64_t>(n_chunks) * n_q + 255) / 256), 256, 0, s>>>(a);
-    CR_LAUNCH_CHECK();
+    if (!filter || nb == 0) {
+        tk_init<<<static_cast<unsigned>((static_cast<uint64_t>(n_chunks) * n_q + 255) / 256), 256, 0, s>>>(a);
+        CR_LAUNCH_CHECK();
+    }
     if (filter) {
         cr_gpu_roaring_view cv_view;
         CR_RET(cr_make_view(filter, &cv_view));
@@ -1416,7 +1430,7 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
             CR_RET(fill_u32(sc.at<uint32_t>(o_nsel), 0u, 1, s));
         } else {
             CR_TIMED("tk_enum", s);
-            tk_enum_count<<<static_cast<unsigned>(nb), TK_ENUM_NT, 0, s>>>(v, n_base, sc.at<uint32_t>(o_counts));
+            tk_enum_count<<<static_cast<unsigned>(nb), TK_ENUM_NT, 0, s>>>(v, n_base, sc.at<uint32_t>(o_counts), a);
             tk_enum_write<<<static_cast<unsigned>(nb), TK_ENUM_NT, 0, s>>>(v, n_base, sc.at<uint32_t>(o_counts),
                                                                            sc.at<uint32_t>(o_sel), sc.at<uint32_t>(o_nsel));
         }
