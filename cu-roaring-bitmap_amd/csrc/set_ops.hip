@@ -50,7 +50,9 @@ struct ExecItem {
     uint32_t slot;
     uint32_t aoff, boff;
     uint32_t ma, mb;
-    uint32_t pad[2];
+    // A side that is a run container of one run: that run's word (start |
+    // length - 1 << 16), so the execution needs no load of its payload; else 0.
+    uint32_t run0_a, run0_b;
 };
 static_assert(sizeof(ExecItem) == 32, "one 32-byte scalar load");
 
@@ -234,7 +236,8 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_classify(Side A, Side B, uint
 
 // ---- plan pass 2: slot assignment in key order -----------------------------
 __global__ __launch_bounds__(PLAN_NT) void so_plan_assign(const KeyRec* recs, const uint32_t* group_counts,
-                                                          Item* items, ExecItem* xitems, Totals* totals, Caps caps)
+                                                          Item* items, ExecItem* xitems, Totals* totals, Caps caps,
+                                                          const uint16_t* run_a, const uint16_t* run_b)
 {
     __shared__ uint32_t gbase[C_N], gtot[C_N];
     __shared__ uint32_t scan_lds[2 * 8 * (PLAN_NT / 64) + 8];
@@ -315,7 +318,13 @@ __global__ __launch_bounds__(PLAN_NT) void so_plan_assign(const KeyRec* recs, co
             x.boff = rec.boff;
             x.ma = rec.ma;
             x.mb = rec.mb;
-            x.pad[0] = x.pad[1] = 0;
+            auto run0 = [](const uint16_t* runs, uint32_t meta, uint32_t off) -> uint32_t {
+                if ((meta >> 16) != CR_RUN || (meta & 0xFFFFu) != 1u) return 0u;
+                const uint16_t* r = runs + (off >> 1);
+                return static_cast<uint32_t>(r[0]) | (static_cast<uint32_t>(r[1]) << 16);
+            };
+            x.run0_a = rec.ai >= 0 ? run0(run_a, rec.ma, rec.aoff) : 0u;
+            x.run0_b = rec.bi >= 0 ? run0(run_b, rec.mb, rec.boff) : 0u;
             xitems[big ? r : caps.items + r] = x;
         }
     }
@@ -503,7 +512,8 @@ __device__ __forceinline__ ExecItem load_xitem(const ExecItem* p)
     it.boff = x[3];
     it.ma = x[4];
     it.mb = x[5];
-    it.pad[0] = it.pad[1] = 0;
+    it.run0_a = x[6];
+    it.run0_b = x[7];
     return it;
 }
 
@@ -553,10 +563,15 @@ __device__ __forceinline__ uint32_t run_word(const uint16_t* runs, uint32_t i, b
 
 __device__ __forceinline__ bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
-__device__ __forceinline__ Pre preload(const Side& S, uint32_t meta, uint32_t off, uint32_t lane)
+__device__ __forceinline__ Pre preload(const Side& S, uint32_t meta, uint32_t off, uint32_t lane, uint32_t run0)
 {
     const uint32_t ty = meta >> 16, n = meta & 0xFFFFu;
     Pre p{~0u, ~0u};
+    if (ty == CR_RUN && n == 1u) {  // the record holds the run: no load
+        p.v0 = lane == 0 ? run0 : 0u;
+        p.v1 = 0u;
+        return p;
+    }
     if (ty == CR_ARRAY) {  // (an absent side: meta 0, no values)
         const uint16_t* vals = S.arr + (off >> 1);
         if (lane < n) p.v0 = vals[lane];
@@ -988,7 +1003,7 @@ __global__ __launch_bounds__(EXEC_NT) __attribute__((amdgpu_waves_per_eu(EXEC_WA
         const uint32_t n_big = totals->c[C_BB] + totals->c[C_MX] + totals->c[C_CB];
         // (the output was not allocated for an overflowed plan)
         if (totals->overflow || w >= n_big) return;
-        const Pre pa = preload(A, it.ma, it.aoff, lane), pb = preload(B, it.mb, it.boff, lane);
+        const Pre pa = preload(A, it.ma, it.aoff, lane, it.run0_a), pb = preload(B, it.mb, it.boff, lane, it.run0_b);
         const uint32_t r = run_big<OP>(A, B, it, pa, pb, lane, img, out_bmp);
         if (lane == 0) item_card[it.pos] = r;
         return;
@@ -1005,8 +1020,8 @@ __global__ __launch_bounds__(EXEC_NT) __attribute__((amdgpu_waves_per_eu(EXEC_WA
 #pragma unroll
     for (uint32_t k = 0; k < SMALL_PER_WAVE; ++k)
         if (k < cnt) {
-            pa[k] = preload(A, it[k].ma, it[k].aoff, lane);
-            pb[k] = preload(B, it[k].mb, it[k].boff, lane);
+            pa[k] = preload(A, it[k].ma, it[k].aoff, lane, it[k].run0_a);
+            pb[k] = preload(B, it[k].mb, it[k].boff, lane, it[k].run0_b);
         }
     zero_image(img, lane);  // array x array items keep it clear between them
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): every preload is in
@@ -1409,8 +1424,11 @@ static Caps setop_caps(const cr_gpu_roaring* a, const cr_gpu_roaring* b, uint32_
     }
     auto c32 = [](uint64_t x) { return static_cast<uint32_t>(std::min<uint64_t>(x, 0xFFFFFFFFull)); };
     Caps caps{bound, c32(std::min<uint64_t>(bmp, bound)), c32(arr), c32(run), 0u};
-    // each item that writes array or run values takes at least one array or run container
-    caps.small = c32(std::min<uint64_t>(bound, aa + ra + ab + rb));
+    // Each item that writes array or run values takes at least one array or run
+    // container: for AND only an array (bitmap x array or array x array), for
+    // ANDNOT one of A's (a copy of an A-only key, or an A array against B).
+    const uint64_t small = op == CR_AND ? aa + ab : (op == CR_ANDNOT ? aa + ra : aa + ra + ab + rb);
+    caps.small = c32(std::min<uint64_t>(bound, small));
     return caps;
 }
 
@@ -1453,7 +1471,7 @@ static int plan_set_operation(const Side& A, const Side& B, uint32_t op, uint32_
     CR_LAUNCH_CHECK();
     {
         CR_TIMED("so_plan_assign", s);
-        so_plan_assign<<<PLAN_GROUPS, PLAN_NT, 0, s>>>(recs, gc, P.items, P.xitems, P.tot, caps);
+        so_plan_assign<<<PLAN_GROUPS, PLAN_NT, 0, s>>>(recs, gc, P.items, P.xitems, P.tot, caps, A.run, B.run);
     }
     CR_LAUNCH_CHECK();
     return CR_OK;
