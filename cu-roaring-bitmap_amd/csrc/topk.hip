@@ -121,6 +121,10 @@ struct TkArgs {
     float* px;           // [small_max]
     uint32_t* qlo;       // [n_q] order-preserving bits of the smallest upper bound of the query's rows
     uint32_t* qhi;       // [n_q] ... and of the largest
+    // The host knew the passing count to be within small_max (no filter and a
+    // small base, or a filter's recorded cardinality) and launched no list
+    // path; tk_select then answers any count (every row a candidate past it).
+    uint32_t list_off;
 };
 
 // Rows the distance kernel covers, and whether the small-set path takes them.
@@ -1150,7 +1154,11 @@ __global__ __launch_bounds__(TK_SEL_NT) __attribute__((amdgpu_waves_per_eu(8))) 
     __shared__ uint32_t lds[TK_SEL_NT / 64];
     __shared__ uint32_t s_bin, s_bound, s_nbatch;
     const uint64_t n_rows = tk_rows(a);
-    if (!tk_small(a, n_rows)) {  // the list path answers; its seed bound
+    // More rows than the small-set limit with no list path launched: only a
+    // filter whose recorded cardinality understates its set does that, and
+    // every row is then a candidate (exact, slower; no estimate is read).
+    const bool all_rows = a.list_off && !tk_small(a, n_rows);
+    if (!tk_small(a, n_rows) && !all_rows) {  // the list path answers; its seed bound
         const uint32_t Sd = tk_seed_rows(a, n_rows);
         if (Sd <= a.k) return;
         const uint32_t qs = blockIdx.x;
@@ -1165,7 +1173,7 @@ __global__ __launch_bounds__(TK_SEL_NT) __attribute__((amdgpu_waves_per_eu(8))) 
     const float* lrow = a.pd + static_cast<size_t>(q) * a.small_max;
     for (uint32_t c = t; c < 128; c += TK_SEL_NT) qv[c] = c < a.dim ? a.queries[static_cast<size_t>(q) * a.dim + c] : 0.f;
     float bound = __builtin_inff();
-    if (S > a.k) {
+    if (S > a.k && !all_rows) {
         // The first bound from the upper bounds of the first rows (a sample
         // only loosens it).
         const uint32_t Sn = min(S, max(TK_SEL_SAMPLE, TK_SEL_SAMPLE_PER_K * a.k));
@@ -1278,10 +1286,23 @@ __global__ __launch_bounds__(TK_SEL_NT) __attribute__((amdgpu_waves_per_eu(8))) 
     static_assert(TK_SEL_RPT == 4, "one float4 a thread per chunk");
     constexpr uint32_t CH = TK_SEL_RPT * TK_SEL_NT;
     if (t == 0) s_nbatch = 0;
-    const uint32_t last4 = S > 0 ? (S - 1) & ~3u : 0;
+    if (all_rows) {
+        for (uint32_t r0 = 0; r0 < S; r0 += CH) {
+            __syncthreads();  // the previous chunk's slots are taken
+            nbatch = s_nbatch;
+            __syncthreads();
+            if (nbatch > TK_SEL_CB - CH) flush();
+#pragma unroll
+            for (uint32_t i = 0; i < TK_SEL_RPT; ++i) {
+                const uint32_t r = r0 + i * TK_SEL_NT + t;
+                if (r < S) ci[atomicAdd(&s_nbatch, 1u)] = r;
+            }
+        }
+    }
+    const uint32_t last4 = S > 0 && !all_rows ? (S - 1) & ~3u : 0;
     auto ld4 = [&](uint32_t r) { return *reinterpret_cast<const float4*>(lrow + min(r, last4)); };
     float4 l4 = ld4(4 * t), n4 = ld4(CH + 4 * t);
-    for (uint32_t r0 = 0; r0 < S; r0 += CH) {
+    for (uint32_t r0 = 0; r0 < (all_rows ? 0u : S); r0 += CH) {
         const float4 m4 = ld4(r0 + 2 * CH + 4 * t);
         __syncthreads();  // the previous chunk's slots are taken
         nbatch = s_nbatch;
@@ -1330,7 +1351,7 @@ int launch_dist(const TkArgs& a, uint32_t grid, uint32_t pairs_grid, float* out_
         }
         CR_LAUNCH_CHECK();
     }
-    {
+    if (!a.list_off) {
         CR_TIMED("tk_dist", s);
         if (a.sel)
             tk_dist<DP, true><<<grid, TK_NT, 0, s>>>(a);
@@ -1414,6 +1435,18 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     a.px = small_max ? sc.at<float>(o_px) : nullptr;
     a.qlo = small_max ? sc.at<uint32_t>(o_qlo) : nullptr;
     a.qhi = small_max ? sc.at<uint32_t>(o_qhi) : nullptr;
+    // The list path is not launched when the passing count is known to fit the
+    // small-set path: no filter and a small base, or a filter's recorded
+    // cardinality (the library's uploads and fused multi_and record it, and the
+    // reference's conversions rely on it too, src/to_csr.cu:212-216), plus one
+    // per container for a multi_and's full containers stored as 65535.
+    if (small_max) {
+        const uint64_t bound = !filter ? n_base
+                                       : (filter->total_cardinality > 0
+                                              ? std::min<uint64_t>(n_base, filter->total_cardinality + filter->n_containers)
+                                              : UINT64_MAX);
+        a.list_off = bound <= small_max ? 1u : 0u;
+    }
     if (!filter || nb == 0) {
         tk_init<<<static_cast<unsigned>((static_cast<uint64_t>(n_chunks) * n_q + 255) / 256), 256, 0, s>>>(a);
         CR_LAUNCH_CHECK();
@@ -1447,7 +1480,7 @@ extern "C" int cr_topk_filtered(const float* d_base, uint64_t n_base, const floa
     } else {
         CR_RET(launch_dist<128>(a, grid, pairs_grid, d_out_dist, d_out_ids, s));
     }
-    {
+    if (!a.list_off) {
         CR_TIMED("tk_merge", s);
         tk_merge<<<(n_q + 3) / 4, TK_MERGE_NT, 0, s>>>(a, a.list_d, a.list_id, a.plane, a.list_n, n_chunks, n_q, k,
                                                         d_out_dist, d_out_ids);

@@ -193,6 +193,32 @@ def test_topk_multi_and_filter(gpu, path):
         gpu.free(g)
 
 
+def test_topk_understated_cardinality(gpu):
+    """The host leaves the list path out when a filter's recorded cardinality
+    fits the small-set limit.  A caller-built struct whose total_cardinality
+    understates its set (the library's own results record the exact count) then
+    reaches tk_select with more rows than the limit, which takes every passing
+    row as a candidate: the answer is still exact."""
+    _say("topk understated cardinality")
+    prev = gpu.topk_set_small_limit(16384)
+    try:
+        n_base = 60000
+        ids = mt_bernoulli(71, 0.5, n_base)  # ~30000 passing rows, past the limit
+        g = gpu.upload_from_ids(ids, n_base)
+        true_card = g.total_cardinality
+        assert true_card > 16384
+        g.total_cardinality = 100
+        mask = np.zeros(n_base, np.uint8)
+        mask[ids] = 1
+        base, queries = _data(n_base, 12, 64, 72)
+        got_d, got_i = _run(gpu, base, queries, 20, g)
+        check_topk(base, queries, 20, mask, got_d, got_i)
+        g.total_cardinality = true_card
+        gpu.free(g)
+    finally:
+        gpu.topk_set_small_limit(prev)
+
+
 def test_topk_rejects_unsupported(gpu):
     _say("topk unsupported")
     torch = _torch()
