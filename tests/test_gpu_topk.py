@@ -129,6 +129,9 @@ CASES = [
     (16385, 40, 128, 100, "none", 1.0, 15),  # one row past it
     (3000, 9, 64, 10, "keep", 0.0, 16),  # no passing row: every slot is (+inf, -1)
     (60000, 20, 64, 10, "setop", 0.3, 17),
+    (5000, 20, 17, 10, "keep", 0.3, 18),  # a filter with scalar row loads (dim % 4 != 0)
+    (50000, 20, 72, 10, "ids", 0.4, 19),  # a filter, dim 72 of the 128-wide tiles
+    (41000, 30, 128, 40, "setop", 0.5, 20),  # a filtered list path with a partial last tile in every chunk
 ]
 
 
