@@ -17,6 +17,12 @@
 //      if it does.  A full buffer is merged into per-(chunk, query) sorted
 //      top-k lists; every stored and returned distance is the direct one.
 //   3. tk_merge: one wave per query merges its chunk lists into the answer.
+// Before tk_dist, tk_pairs and tk_select run on both paths: for a small set
+// (at most the small-set limit of passing rows) tk_pairs writes every row's
+// distance estimate and tk_select picks each query's k from them, and the list
+// path's kernels exit (or are not launched when the host knows the count);
+// for a larger set they bound each query's k-th distance from the first rows,
+// the bound tk_dist starts from.
 #include <algorithm>
 #include <atomic>
 #include <cstring>
