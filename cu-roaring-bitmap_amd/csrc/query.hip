@@ -340,7 +340,7 @@ __global__ __launch_bounds__(BUILD_NT) void qp_answer(const uint32_t* __restrict
     // All 8 answers of a group go into one byte that only this lane writes:
     // fields past the run answer into b's padding, and any 20-bit value
     // indexes the LDS image.
-    walk_groups(part, tab, g, b, wave, lane, queue, desc,
+    walk_groups<false>(part, tab, g, b, wave, lane, queue, desc,
                 [&] {  // wave w loads container w of the bucket (zeros past the last key)
                     if (key < g.K) {
                         qp_load_container(v, key, bits + wave * 2048u, lane);
@@ -415,7 +415,7 @@ int contains_partitioned(const GpuRoaringView& v, const uint32_t* d_ids, uint64_
     g.G = std::max<uint32_t>(1, std::min<uint32_t>(num_cus(), (g.n_tiles + TB - 1) / TB));
     g.vec = (reinterpret_cast<uintptr_t>(d_ids) & 15u) == 0;
     Carver c;
-    // qp_answer reads up to 7 words past a field group's first: slack past the last tile
+    // qp_answer reads up to 5 words past a field group's first: slack past the last tile
     const size_t o_part = c.add(sizeof(uint32_t) * (static_cast<uint64_t>(g.n_tiles) * TILE_WORDS + 8));
     const size_t o_tab = c.add(sizeof(uint16_t) * static_cast<uint64_t>((g.n_tiles + TB - 1) / TB) * TB * (g.NB + 1));
     const size_t o_perm = c.add(sizeof(uint16_t) * static_cast<uint64_t>(g.n_tiles) * TILE);

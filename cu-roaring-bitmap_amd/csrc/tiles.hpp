@@ -458,8 +458,8 @@ inline uint32_t build_grid_persistent(uint32_t nb, uint32_t cus)
 // thread, once the first run bounds are requested: the caller's LDS set-up,
 // published by a workgroup barrier before the first on_group.  Every thread of
 // the BUILD_NT-thread workgroup calls it (wave = t >> 6, lane = its lane).
-// Reads reach 8 words past a group's first word, rounded down to an even word:
-// `part` needs 8 words of slack past the last tile.
+// A group's reads are the 6 words from its first word on: `part` needs 8
+// words of slack past the last tile.
 //
 // Wave w owns tile blocks w, w + 16, ...; a step covers 2 x 64 / TB of them,
 // two tiles per lane, whose run bounds are loaded a step ahead.  The step's
@@ -470,11 +470,13 @@ inline uint32_t build_grid_persistent(uint32_t nb, uint32_t cus)
 // neighbouring lanes read neighbouring words of one run (their loads share
 // cache lines); eight rounds are loaded before any is handed on.  A descriptor
 // is the owner lane (6 bits), which of its two tiles (1), the group's first
-// sorted position p (15: p < TILE) and n - 1 (3).  A run of more than
-// GROUP_LONG groups (sorted or clustered ids: a bucket's fields in a few tiles,
-// all in one wave's blocks) is queued in LDS and its groups dealt to all
-// sixteen waves after the walk; one that finds the queue full is dealt with its
-// wave's other runs.  `queue` is the workgroup's LDS queue.
+// sorted position p (15: p < TILE), n - 1 (3) and the first field's bit in its
+// word, 20 p mod 32 (5: the same for every group of a run, 8 fields being 5
+// words).  A run of more than GROUP_LONG groups (sorted or clustered ids: a
+// bucket's fields in a few tiles, all in one wave's blocks) is queued in LDS
+// and its groups dealt to all sixteen waves after the walk; one that finds the
+// queue full is dealt with its wave's other runs.  `queue` is the workgroup's
+// LDS queue.
 constexpr uint32_t GROUP_LONG = 64;
 constexpr uint32_t GROUP_QCAP = 1024;  // 8 KiB of LDS beside the callers' 128 KiB image
 constexpr uint32_t DESC_CAP = 256;     // descriptors per wave: 16 KiB for sixteen waves
@@ -495,30 +497,38 @@ struct FieldGroup {
     uint32_t o;     // the first field's bit within word w0
 };
 
+// Two words at any 4-byte boundary: the hardware takes a multi-dword global
+// load at dword alignment, so a group is read from its own first word.
+typedef uint32_t u32x2_dw __attribute__((ext_vector_type(2), aligned(4)));
+
 // The words of the group whose first field sits at sorted position p of
-// `tile`: four 8-byte loads from the even word at or below w0.
+// `tile`: three 8-byte loads from w0, the word holding the first field.
 struct GroupWords {
-    uint2 p[4];
-    uint32_t odd, o;
+    u32x2_dw p[3];
+    uint32_t o;
 };
+
+// The word of `part` holding the first field of the group at sorted position p
+// of `tile`: tile * TILE_WORDS + 20 p / 32, below 2^32 since the callers take
+// at most 0xFFFFFFFF / TILE_WORDS tiles (24-bit multiplies: full rate).
+__device__ __forceinline__ uint32_t group_word(uint32_t tile, uint32_t p)
+{
+    return __umul24(tile, TILE_WORDS) + (__umul24(FIELD_BITS, p) >> 5);
+}
 
 __device__ __forceinline__ void group_issue(const uint32_t* __restrict__ part, uint32_t tile, uint32_t p,
                                             GroupWords& q)
 {
-    const uint32_t bit = FIELD_BITS * p;
-    const uint32_t w0 = bit >> 5;
-    q.o = bit & 31u;
-    q.odd = w0 & 1u;
-    const uint2* src = reinterpret_cast<const uint2*>(part + static_cast<uint64_t>(tile) * TILE_WORDS + (w0 & ~1u));
+    q.o = __umul24(FIELD_BITS, p) & 31u;
+    const u32x2_dw* src = reinterpret_cast<const u32x2_dw*>(part + group_word(tile, p));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) q.p[i] = src[i];
+    for (int i = 0; i < 3; ++i) q.p[i] = src[i];
 }
 
 __device__ __forceinline__ void group_words(const GroupWords& w, FieldGroup& q)
 {
-    const bool odd = w.odd != 0u;
-    q.x[0] = odd ? w.p[0].y : w.p[0].x, q.x[1] = odd ? w.p[1].x : w.p[0].y, q.x[2] = odd ? w.p[1].y : w.p[1].x;
-    q.x[3] = odd ? w.p[2].x : w.p[1].y, q.x[4] = odd ? w.p[2].y : w.p[2].x, q.x[5] = odd ? w.p[3].x : w.p[2].y;
+    q.x[0] = w.p[0].x, q.x[1] = w.p[0].y, q.x[2] = w.p[1].x;
+    q.x[3] = w.p[1].y, q.x[4] = w.p[2].x, q.x[5] = w.p[2].y;
     q.o = w.o;
 }
 
@@ -540,7 +550,11 @@ __device__ __forceinline__ void group_fields(const FieldGroup& q, uint32_t (&f)[
     f[7] = d4 >> 12;
 }
 
-template <class Prologue, class OnGroup>
+// WHOLE_TAIL (an on_group for which a field seen twice is the same as once,
+// such as setting its bit): a run of at least 8 fields ends in a whole group,
+// fields E - 8 .. E - 1, which repeats some of the group before it, so only
+// runs shorter than 8 fields hand on_group a partial group.
+template <bool WHOLE_TAIL, class Prologue, class OnGroup>
 __device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, const uint16_t* __restrict__ tab,
                                             const IdsGeom& g, uint32_t b, uint32_t wave, uint32_t lane,
                                             GroupQueue& queue, uint32_t* desc, Prologue prologue, OnGroup on_group)
@@ -558,6 +572,12 @@ __device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, c
     const uint32_t n_blk = (g.n_tiles + TB - 1) / TB;
     const uint32_t per_wave = n_blk > wave ? (n_blk - wave + BUILD_WAVES - 1) / BUILD_WAVES : 0u;
     auto tile_of = [&](uint32_t st, uint32_t l) { return (wave + BUILD_WAVES * (st * BPS + l / TB)) * TB + l % TB; };
+    // tile_of(2 st + a, l) for a descriptor's owner lane l (bits 0-5) and tile a
+    // (bit 6): with TB = BPS = 8, (2 st + a) BPS + l / TB = 16 st + bits 3-6.
+    static_assert(TB == 8 && BPS == 8, "desc_tile's bit fields");
+    auto desc_tile = [&](uint32_t st, uint32_t d) {
+        return wave * TB + BUILD_WAVES * TB * (16u * st + ((d >> 3) & 15u)) + (d & 7u);
+    };
     auto tab_load = [&](uint32_t st, uint32_t& r0, uint32_t& r1) {
         r0 = r1 = 0;
         const uint32_t jb = st * BPS + lane / TB;
@@ -594,6 +614,25 @@ __device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, c
         uint32_t P = wave_incl_scan(G);  // then exclusive: the lane's first group
         const uint32_t T = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(P), 63));
         P -= G;
+        // Writes the descriptors of a run's groups that fall in the list's
+        // window [w0, w0 + DESC_CAP): group j (numbered `first` + j) of a run
+        // at [S, E) starts at p = S + 8 j, so a whole group's descriptor is
+        // the first one's plus 1024 j; the last group's n, and with
+        // WHOLE_TAIL its p and bit, are written over it afterwards (the same
+        // lane's LDS writes land in order).
+        auto put_run = [&](uint32_t w0, uint32_t first, uint32_t Gr, uint32_t S, uint32_t E, uint32_t which) {
+            if (Gr == 0u) return;
+            const uint32_t d0 = lane | which | (S << 7) | (7u << 22) | ((__umul24(FIELD_BITS, S) & 31u) << 25);
+            const uint32_t hi = min(first + Gr, w0 + DESC_CAP);
+            for (uint32_t u = max(first, w0); u < hi; ++u) wdesc[u - w0] = d0 + ((u - first) << 10);
+            const uint32_t ul = first + Gr - 1u;
+            if (ul - w0 < DESC_CAP) {
+                uint32_t p = S + 8u * (Gr - 1u), n = E - p;  // 1 .. 8
+                // the whole tail's bit: 20 (E - 8) mod 32 = 20 E mod 32
+                if (WHOLE_TAIL && n < 8u && E - S >= 8u) p = E - 8u, n = 8u;
+                wdesc[ul - w0] = lane | which | (p << 7) | ((n - 1u) << 22) | ((__umul24(FIELD_BITS, p) & 31u) << 25);
+            }
+        };
         // Batches of WALK_ROUNDS rounds (64 groups a round): the descriptor
         // list holds DESC_ROUNDS rounds, so it is filled and read into
         // registers WALK_ROUNDS / DESC_ROUNDS times per batch before any load.
@@ -604,14 +643,8 @@ __device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, c
                 const uint32_t w0 = c0 + h * DESC_CAP;  // wave-uniform
                 if (w0 < T) {
                     // This lane's groups numbered [w0, w0 + DESC_CAP): their descriptors.
-                    const uint32_t u_hi = min(P + G, w0 + DESC_CAP);
-                    for (uint32_t u = max(P, w0); u < u_hi; ++u) {
-                        const uint32_t j = u - P;
-                        const bool in_a = j < Ga;
-                        const uint32_t p = in_a ? Sa + 8u * j : Sb + 8u * (j - Ga);
-                        const uint32_t n = min((in_a ? Ea : Eb) - p, 8u);
-                        wdesc[u - w0] = lane | (in_a ? 0u : 64u) | (p << 7) | ((n - 1u) << 22);
-                    }
+                    put_run(w0, P, Ga, Sa, Ea, 0u);
+                    put_run(w0, P + Ga, Gb, Sb, Eb, 64u);
                     wave_lds_fence();
 #pragma unroll
                     for (uint32_t k = 0; k < DESC_ROUNDS; ++k) {
@@ -627,25 +660,20 @@ __device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, c
             }
             // All the batch's addresses, then all its loads, then the groups:
             // no branch between, so the loads are in flight together.
-            const uint2* src[WALK_ROUNDS];
+            const u32x2_dw* src[WALK_ROUNDS];
 #pragma unroll
-            for (uint32_t k = 0; k < WALK_ROUNDS; ++k) {
-                const uint32_t tile = tile_of(2u * st + ((dd[k] >> 6) & 1u), dd[k] & 63u);
-                const uint32_t w0 = (FIELD_BITS * ((dd[k] >> 7) & 0x7FFFu)) >> 5;
-                src[k] = reinterpret_cast<const uint2*>(part + static_cast<uint64_t>(tile) * TILE_WORDS + (w0 & ~1u));
-            }
+            for (uint32_t k = 0; k < WALK_ROUNDS; ++k)
+                src[k] = reinterpret_cast<const u32x2_dw*>(part + group_word(desc_tile(st, dd[k]), (dd[k] >> 7) & 0x7FFFu));
             GroupWords w[WALK_ROUNDS];
 #pragma unroll
             for (uint32_t k = 0; k < WALK_ROUNDS; ++k)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) w[k].p[i] = src[k][i];
+                for (int i = 0; i < 3; ++i) w[k].p[i] = src[k][i];
 #pragma unroll
             for (uint32_t k = 0; k < WALK_ROUNDS; ++k) {
                 const uint32_t p = (dd[k] >> 7) & 0x7FFFu;
-                const uint32_t bit = FIELD_BITS * p;
-                w[k].o = bit & 31u;
-                w[k].odd = (bit >> 5) & 1u;
-                const uint32_t tile = tile_of(2u * st + ((dd[k] >> 6) & 1u), dd[k] & 63u);
+                w[k].o = (dd[k] >> 25) & 31u;
+                const uint32_t tile = desc_tile(st, dd[k]);
                 handle(tile, p, (dd[k] & DESC_EMPTY) ? 0u : ((dd[k] >> 22) & 7u) + 1u, w[k]);
             }
         }
@@ -663,9 +691,11 @@ __device__ __forceinline__ void walk_groups(const uint32_t* __restrict__ part, c
         for (uint32_t c = (wave + BUILD_WAVES - off % BUILD_WAVES) % BUILD_WAVES; c < nch; c += BUILD_WAVES) {
             const uint32_t j = 64u * c + lane;
             if (j < G) {
+                uint32_t p = S + 8u * j, n = min(E - p, 8u);
+                if (WHOLE_TAIL && n < 8u && E - S >= 8u) p = E - 8u, n = 8u;
                 GroupWords w;
-                group_issue(part, ent.x, S + 8u * j, w);
-                handle(ent.x, S + 8u * j, min(E - S - 8u * j, 8u), w);
+                group_issue(part, ent.x, p, w);
+                handle(ent.x, p, n, w);
             }
         }
         off += nch;

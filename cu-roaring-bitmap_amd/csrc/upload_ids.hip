@@ -331,20 +331,33 @@ __global__ __launch_bounds__(BUILD_NT) void ids_build(const uint32_t* __restrict
         // registers across the whole loop.
         uint32_t lane = __lane_id();
         asm volatile("" : "+v"(lane));
-        walk_groups(part, tab, g, b, wave, lane, queue, desc,
+        walk_groups<true>(part, tab, g, b, wave, lane, queue, desc,
                     [&] {
                         for (uint32_t i = t; i < BK_KEYS * 512u; i += BUILD_NT)
                             reinterpret_cast<uint4*>(bits)[i] = make_uint4(0, 0, 0, 0);
                         if constexpr (decltype(first)::value) compute_order();
                     },
                     [&](uint32_t, uint32_t, uint32_t n, const uint32_t (&f)[8]) {
-                        // Fields past the run OR in nothing (no branch per field); an
-                        // empty slot sets nothing (its lanes would all hit one group's words).
+                        // An empty slot sets nothing (its lanes would all hit one
+                        // group's words).  When no lane of the wave holds a partial
+                        // group (only runs of fewer than 8 fields make one), every
+                        // field is set; otherwise the fields past a run OR in
+                        // nothing (no branch per field).
+                        const bool whole = __ballot(n - 1u < 7u) == 0ull;  // wave-uniform
                         if (n == 0u) return;
+                        if (whole) {
 #pragma unroll
-                        for (uint32_t k = 0; k < 8u; ++k) {
-                            const uint32_t F = f[k] & FIELD_MASK;  // key-in-bucket << 16 | low 16 bits
-                            atomicOr(&bits[F >> 5], k < n ? 1u << (F & 31u) : 0u);
+                            for (uint32_t k = 0; k < 8u; ++k) {
+                                const uint32_t F = f[k] & FIELD_MASK;  // key-in-bucket << 16 | low 16 bits
+                                atomicOr(&bits[F >> 5], 1u << (F & 31u));
+                            }
+                        } else {
+                            const uint32_t live = (1u << n) - 1u;  // bit k: field k is the run's
+#pragma unroll
+                            for (uint32_t k = 0; k < 8u; ++k) {
+                                const uint32_t F = f[k] & FIELD_MASK;
+                                atomicOr(&bits[F >> 5], ((live >> k) & 1u) << (F & 31u));
+                            }
                         }
                     });
         __syncthreads();
@@ -709,6 +722,9 @@ static int small_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, ui
     return CR_OK;
 }
 
+// u32 id counts: the tiles' word offsets (group_word) stay below 2^32.
+static_assert((0xFFFFFFFFull + TILE - 1) / TILE <= 0xFFFFFFFFull / TILE_WORDS, "tile count bound");
+
 static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hipStream_t s, cr_gpu_roaring* out)
 {
     if (universe == 0) {
@@ -732,7 +748,7 @@ static int large_upload(const uint32_t* d_ids, uint32_t n, uint32_t universe, hi
     const size_t o_tab =
         c.add(sizeof(uint16_t) * static_cast<uint64_t>((g.n_tiles + TB - 1) / TB) * TB * (g.NB + 1));
     // Whole tiles (a partial last tile is padded) + the build's window overrun.
-    // the build's field groups read up to 7 words past a group's first: slack past the last tile
+    // the build's field groups read up to 5 words past a group's first: slack past the last tile
     const size_t o_part = c.add(sizeof(uint32_t) * (static_cast<uint64_t>(g.n_tiles) * TILE_WORDS + 8));
     const size_t o_wgc = c.add(sizeof(uint32_t) * static_cast<uint64_t>(g.G) * g.NB);
     const size_t o_pres = c.add(sizeof(uint32_t) * 2048u);  // key presence bits (fewer ids than keys)

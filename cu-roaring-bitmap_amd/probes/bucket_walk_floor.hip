@@ -33,7 +33,7 @@ __global__ __launch_bounds__(BUILD_NT) void walk_kernel(const uint32_t* __restri
     if (b >= g.NB) return;
     const uint32_t wave = t >> 6, lane = __lane_id();
     uint32_t acc = 0;
-    walk_groups(part, tab, g, b, wave, lane, queue, desc,
+    walk_groups<true>(part, tab, g, b, wave, lane, queue, desc,  // the groups the build walks
         [&] { if (BITS) for (uint32_t i = t; i < BK_KEYS * 512u; i += BUILD_NT) reinterpret_cast<uint4*>(bits)[i] = make_uint4(0,0,0,0); },
         [&](uint32_t, uint32_t, uint32_t n, const uint32_t (&f)[8]) {
             if (n == 0u) return;
