@@ -160,6 +160,10 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
     }
     for (uint32_t i = t; i <= NB; i += TS_NT) cnt[i] = 0;  // the first tile's counts; each tile zeroes the next's
     __syncthreads();
+    // The first tile's ids are in before the loop (vmcnt(0)), and every tile
+    // ends with the next one's in (below), so the loop's top needs no wait of
+    // its own, which would otherwise also wait for the write-out's stores.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     for (uint32_t tile = first; tile < g.n_tiles; tile = next(tile)) {
         // The thread index, opaque to the compiler here, so per-lane addresses
         // are formed inside the loop rather than hoisted out of it and
@@ -421,8 +425,22 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
         // Ordinary stores, so the packed tiles are kept in the Infinity Cache
         // for the kernel that reads them next; the ids come in through
         // nontemporal loads, which do not displace them.  The next tile's
-        // scatter overwrites buf only after two more barriers.
-        for (uint32_t u = t; u < n4; u += TS_NT) dst[u] = reinterpret_cast<const uint4*>(buf)[u];
+        // scatter overwrites buf only after two more barriers.  Every lane
+        // makes the same number of stores (one past the last vector stores
+        // that vector again, the same bytes; a tile without real ids writes
+        // its slot's first vector, which no run covers): the memory counter
+        // counts stores with loads, in order, so with a fixed count the next
+        // tile waits for its ids alone and leaves these stores in flight.
+        constexpr uint32_t WO = (TILE_WORDS / 4 + TS_NT - 1) / TS_NT;  // 16-byte vectors a lane
+        const uint32_t last = max(n4, 1u) - 1u;
+        uint4 wv[WO];
+#pragma unroll
+        for (uint32_t k = 0; k < WO; ++k) wv[k] = reinterpret_cast<const uint4*>(buf)[min(t + k * TS_NT, last)];
+#pragma unroll
+        for (uint32_t k = 0; k < WO; ++k) dst[min(t + k * TS_NT, last)] = wv[k];
+        // vmcnt(WO): the next tile's ids, loaded before these WO stores, are in.
+        static_assert(WO == 4, "the wait below counts WO stores");
+        __builtin_amdgcn_s_waitcnt(0x0F74);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(mx, o, 64)));
