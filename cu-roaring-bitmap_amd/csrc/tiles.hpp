@@ -9,6 +9,8 @@
 // bucket's 16 containers in 128 KiB of LDS -- then reads the bucket's run in
 // every tile (~24 fields, 60 bytes, at 2^30).
 #pragma once
+#include <type_traits>
+
 #include "internal.hpp"
 
 namespace crimpl {
@@ -253,15 +255,33 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
             const uint32_t wave = t >> 6;
             const uint32_t b0 = 16u * t;  // = 1024 wave + 16 lane
             uint4* c4 = reinterpret_cast<uint4*>(cnt + b0);
-            auto real = [&](uint32_t c, uint32_t b) { return b < NB ? c : 0u; };
-            uint32_t s = 0, incl = 0, seg = 0;
-            if (wave < W) {
+            // The counts of the sentinel bucket and past it are left out.  A
+            // wave whose buckets are all real (every wave when NB is a multiple
+            // of 1024) takes the count as it is: a wave-uniform branch between
+            // two copies of each pass, instead of a compare and a select per
+            // count on the one wave that the other fifteen wait for.
+            const bool whole = __ballot(b0 + 16u > NB) == 0ull;
+            auto real = [&](auto masked, uint32_t c, uint32_t b) {
+                if constexpr (decltype(masked)::value) return b < NB ? c : 0u;
+                else return c;
+            };
+            auto sum16 = [&](auto masked) {
+                uint32_t sum = 0;
 #pragma unroll
                 for (uint32_t q = 0; q < 4; ++q) {
                     const uint4 c = c4[q];
                     const uint32_t b = b0 + 4u * q;
-                    s += real(c.x, b) + real(c.y, b + 1u) + real(c.z, b + 2u) + real(c.w, b + 3u);
+                    sum += real(masked, c.x, b) + real(masked, c.y, b + 1u) + real(masked, c.z, b + 2u) +
+                           real(masked, c.w, b + 3u);
                 }
+                return sum;
+            };
+            uint32_t s = 0, incl = 0, seg = 0;
+            if (wave < W) {
+                if (whole)
+                    s = sum16(std::false_type{});
+                else
+                    s = sum16(std::true_type{});
                 incl = wave_incl_scan(s);
                 seg = __builtin_amdgcn_readlane(incl, 63);
                 if (W > 1u && lane == 63) lds[wave] = seg;
@@ -282,29 +302,36 @@ __global__ __launch_bounds__(TS_NT) void ids_tile_sort(const uint32_t* __restric
                     return PERM ? st | (((st + 7u * b + 7u) & ~7u) << 16) : st;
                 };
                 uint32_t st[8];  // the lane's 16 starts as u16 pairs
+                auto starts16 = [&](auto masked) {
 #pragma unroll
-                for (uint32_t q = 0; q < 4; ++q) {
-                    const uint4 c = c4[q];
-                    const uint32_t b = b0 + 4u * q;
-                    const uint32_t cx = real(c.x, b), cy = real(c.y, b + 1u), cz = real(c.z, b + 2u), cw = real(c.w, b + 3u);
-                    const uint32_t s0 = run, s1 = s0 + cx, s2 = s1 + cy, s3 = s2 + cz;
-                    run = s3 + cw;
-                    c4[q] = make_uint4(start(s0, b), start(s1, b + 1u), start(s2, b + 2u), start(s3, b + 3u));
-                    st[2 * q] = s0 | (s1 << 16);
-                    st[2 * q + 1] = s2 | (s3 << 16);
-                    if (!staged) {  // straight into the table (entries b <= NB), and the totals
-                        uint16_t* rp = tab + (static_cast<uint64_t>(tile / TB) * (NB + 1) + b) * TB + tile % TB;
-                        if (b <= NB) rp[0] = static_cast<uint16_t>(s0);
-                        if (b + 1u <= NB) rp[TB] = static_cast<uint16_t>(s1);
-                        if (b + 2u <= NB) rp[2 * TB] = static_cast<uint16_t>(s2);
-                        if (b + 3u <= NB) rp[3 * TB] = static_cast<uint16_t>(s3);
-                        if constexpr (!PERM) {
-                            uint4* a4 = reinterpret_cast<uint4*>(acc + b);
-                            const uint4 a = *a4;
-                            *a4 = make_uint4(a.x + cx, a.y + cy, a.z + cz, a.w + cw);
+                    for (uint32_t q = 0; q < 4; ++q) {
+                        const uint4 c = c4[q];
+                        const uint32_t b = b0 + 4u * q;
+                        const uint32_t cx = real(masked, c.x, b), cy = real(masked, c.y, b + 1u),
+                                       cz = real(masked, c.z, b + 2u), cw = real(masked, c.w, b + 3u);
+                        const uint32_t s0 = run, s1 = s0 + cx, s2 = s1 + cy, s3 = s2 + cz;
+                        run = s3 + cw;
+                        c4[q] = make_uint4(start(s0, b), start(s1, b + 1u), start(s2, b + 2u), start(s3, b + 3u));
+                        st[2 * q] = s0 | (s1 << 16);
+                        st[2 * q + 1] = s2 | (s3 << 16);
+                        if (!staged) {  // straight into the table (entries b <= NB), and the totals
+                            uint16_t* rp = tab + (static_cast<uint64_t>(tile / TB) * (NB + 1) + b) * TB + tile % TB;
+                            if (b <= NB) rp[0] = static_cast<uint16_t>(s0);
+                            if (b + 1u <= NB) rp[TB] = static_cast<uint16_t>(s1);
+                            if (b + 2u <= NB) rp[2 * TB] = static_cast<uint16_t>(s2);
+                            if (b + 3u <= NB) rp[3 * TB] = static_cast<uint16_t>(s3);
+                            if constexpr (!PERM) {
+                                uint4* a4 = reinterpret_cast<uint4*>(acc + b);
+                                const uint4 a = *a4;
+                                *a4 = make_uint4(a.x + cx, a.y + cy, a.z + cz, a.w + cw);
+                            }
                         }
                     }
-                }
+                };
+                if (whole)
+                    starts16(std::false_type{});
+                else
+                    starts16(std::true_type{});
                 if (staged) {  // W = 1: buckets 16 t .. 16 t + 15 < STAGE_W
                     uint4* sp = reinterpret_cast<uint4*>(stage + (tile % TB) * STAGE_W + b0);
                     sp[0] = make_uint4(st[0], st[1], st[2], st[3]);
