@@ -210,6 +210,31 @@ def test_contains_partitioned_many_buckets(gpu, universe):
     gpu.free(g)
 
 
+@pytest.mark.parametrize("density", [0.05, 0.6])
+def test_contains_partitioned_sentinel_tiles(gpu, density):
+    """Mode 4 with whole tiles of queries past the bitmap's last bucket (the tile
+    sort's sentinel bucket): such a tile has no field of a real bucket to write
+    out, and its answers are all `negated` (a density above 1/2 uploads as a
+    negated complement); a mixed tile, an ordinary one and a partial one follow."""
+    _say("contains partitioned sentinel tiles", density)
+    torch = _torch()
+    rng = np.random.default_rng(97)
+    U = 1 << 24
+    ids = np.nonzero(rng.random(U) < density)[0].astype(np.uint32)
+    g, want = gpu.upload_from_ids(ids, U), orc.upload_from_ids(ids, U)
+    assert bool(g.negated) == (density > 0.5)
+    q = np.concatenate([rng.integers(1 << 28, 1 << 32, 24576 * 2, dtype=np.uint64),
+                        rng.integers(0, 1 << 32, 24576, dtype=np.uint64),
+                        rng.integers(0, U, 24576 + 5, dtype=np.uint64)]).astype(np.uint32)
+    out = torch.empty(q.size, dtype=torch.int32, device="cuda")
+    gpu.contains_batch(g, _dev_u32(q), out, 4)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint32)
+    assert np.array_equal(got, orc.contains_many(want, q))
+    assert np.all(got[:24576 * 2] == (1 if g.negated else 0))
+    gpu.free(g)
+
+
 def _skewed_ids(case, rng):
     """Inputs whose tiles each fall in a few key buckets (16 keys a bucket):
     long runs per (bucket, tile), shared by the whole build workgroup.
