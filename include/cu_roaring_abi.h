@@ -232,14 +232,14 @@ int cr_make_view(const cr_gpu_roaring* bm, cr_gpu_roaring_view* out);
  * benches and tests write around them (bench/bench_point_query.cu:123-144). */
 int cr_contains_batch(const cr_gpu_roaring_view* view, const uint32_t* d_ids, uint64_t n, uint32_t* d_out,
                       uint32_t mode, cr_stream_t stream);
-/* Filtered brute-force top-k (no reference implementation; BASELINE.json's
- * fused filtered top-k).  base: n_base x dim fp32 row-major (device),
- * queries: n_q x dim fp32 (device), filter: a GpuRoaring over [0, n_base)
- * (NULL = no filter).  Writes, per query, the k smallest squared L2 distances
- * ascending (ties: smaller id first) and their ids; slots beyond the number of
- * passing vectors hold +inf and -1.  A filter's total_cardinality, when
- * non-zero, tells the call which path to launch (an understated one costs time,
- * never the answer). */
+/* Filtered brute-force top-k (no reference implementation; the reference
+ * motivates a fused filtered search in README.md:265).  base: n_base x dim
+ * fp32 row-major (device), queries: n_q x dim fp32 (device), filter: a
+ * GpuRoaring over [0, n_base) (NULL = no filter).  Writes, per query, the k
+ * smallest squared L2 distances ascending (ties: smaller id first) and their
+ * ids; slots beyond the number of passing vectors hold +inf and -1.  A
+ * filter's total_cardinality, when non-zero, tells the call which path to
+ * launch (an understated one costs time, never the answer). */
 int cr_topk_filtered(const float* d_base, uint64_t n_base, const float* d_queries, uint32_t n_q, uint32_t dim,
                      const cr_gpu_roaring* filter, uint32_t k, float* d_out_dist, int64_t* d_out_ids,
                      cr_stream_t stream);
